@@ -1,0 +1,149 @@
+/*
+ * rt_hip.h -- C ABI of the MI355X (gfx950) quantized-linear library.
+ *
+ * Drop-in boundary for rich-triplet's quantized-weight linear path.  Every
+ * entry point takes plain device pointers and sizes; nothing here carries a
+ * C++ or torch type.  Weights are [N, K] row-major (out_features x
+ * in_features), activations [M, K] row-major f32, outputs [M, N] f32:
+ * y = x * W^T, exactly the reference's `Mat` / `Q4KMat` / `MatBf16`
+ * convention (include/rt/quant.hpp:119-199, include/rt/mat.hpp:157-207).
+ *
+ * Errors: every function returns an rt_hip_status; 0 is success.  The
+ * message for the last failure on the calling thread is rt_hip_last_error().
+ * (The reference aborts in its GPU ops, metal_ops.mm:312-315, and asserts
+ * on the CPU; a C ABI reports instead.)  Kernels run asynchronously on the
+ * given stream (NULL = the legacy default stream); a status of 0 means the
+ * launch was accepted.  Calls on different streams may run concurrently;
+ * calls that share a workspace (argmax, GEMM) are serialised per stream by
+ * the caller's stream order.
+ *
+ * Weight byte formats (verbatim, as the reference holds them in memory):
+ *   RT_HIP_Q4K   144-byte GGUF Q4_K super-blocks, K/256 per row
+ *                (d:f16 | dmin:f16 | scales[12] | qs[128]); quant.hpp:119-137
+ *   RT_HIP_Q4_0  18-byte GGUF Q4_0 blocks, K/32 per row (d:f16 | qs[16]);
+ *                gguf.cpp:495-529 -- the form Q4Mat decodes from
+ *   RT_HIP_BF16  uint16 bf16 bits; mat.hpp:157-207
+ */
+#ifndef RT_HIP_H
+#define RT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* rt_hip_stream; /* a hipStream_t */
+
+typedef enum {
+    RT_HIP_OK = 0,
+    RT_HIP_E_ARG = 1,          /* null pointer, negative size, bad enum */
+    RT_HIP_E_SHAPE = 2,        /* M/N/K outside what the kernel supports */
+    RT_HIP_E_ALIGN = 3,        /* K not a multiple of the block size, or a
+                                  pointer not 16-byte aligned */
+    RT_HIP_E_OOM = 4,          /* device allocation failed */
+    RT_HIP_E_HIP = 5,          /* a HIP runtime call failed */
+    RT_HIP_E_UNSUPPORTED = 6   /* no gfx950 device, or format not handled */
+} rt_hip_status;
+
+typedef enum {
+    RT_HIP_F32 = 0,
+    RT_HIP_BF16 = 1,
+    RT_HIP_Q4K = 2,
+    RT_HIP_Q4_0 = 3
+} rt_hip_format;
+
+/* Largest activation batch the GEMV kernels take; the reference's
+ * speculative-verify batch is MAX_BATCH 8 (shaders/decode_gemma3.msl:418). */
+#define RT_HIP_GEMV_MAX_M 8
+
+/* ---- library ----------------------------------------------------------- */
+
+/* Thread-local message of the last failed call ("" if none). */
+const char* rt_hip_last_error(void);
+/* Library version string. */
+const char* rt_hip_version(void);
+/* Checks that device `ordinal` exists and is gfx950; makes it current. */
+int rt_hip_init(int ordinal);
+
+/* ---- GEMV: M <= 8 activation rows ---------------------------------------
+ * Replace: Q4KMat::matmul_q4k_t / _blas for M == 1 (gemv_mt) and the M > 1
+ * scalar loop for small M (src/quant_q4k.cpp:564-634); the Metal
+ * metal_gemv_q4k_t (include/rt/metal_ops.hpp:57-62, src/metal_ops.mm:663-669)
+ * and the engine kernels gemv_q4k_t / gemv_q4k_t_batch
+ * (src/shaders/decode_gemma3.msl:328-470).
+ * Requires K % 256 == 0 (the reference's Q4_K precondition, quant.hpp:139,
+ * which its Release build does not check -- here it is an error). */
+int rt_hip_gemv_q4k(const void* blocks, const float* x, float* y, int64_t n, int64_t k,
+                    int32_t m, rt_hip_stream stream);
+
+/* Replace: MatBf16::matmul_by_t for M <= 8 (src/mat.cpp:318-414); Metal
+ * metal_gemv_bf16_t (metal_ops.hpp:64-65) and gemv_bf16_t / _batch
+ * (decode_gemma3.msl:390-518).  Requires K % 8 == 0. */
+int rt_hip_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
+                     int32_t m, rt_hip_stream stream);
+
+/* GGUF Q4_0 weights streamed as 18-byte blocks.
+ * Replace: Q4Mat::matmul_q4_t on GgufFile::decode_q4_0_to_q4mat output
+ * (src/quant_q4.cpp:92-114, src/gguf.cpp:392-450) and metal_matmul_q4_t
+ * (metal_ops.hpp:54-55).  Requires K % 256 == 0. */
+int rt_hip_gemv_q4_0(const void* blocks, const float* x, float* y, int64_t n, int64_t k,
+                     int32_t m, rt_hip_stream stream);
+
+/* ---- argmax ---------------------------------------------------------------
+ * Replace: greedy sampling, src/transformer5.cpp:382-391 -- the first index
+ * of the strict maximum of each row; NaN never wins; a row with no value
+ * above -inf gives 0.  idx[rows] (int64) and val[rows] (f32, may be NULL) are
+ * device pointers.  Uses a library-owned device workspace. */
+int rt_hip_argmax(const float* logits, int64_t rows, int64_t cols, int64_t* idx, float* val,
+                  rt_hip_stream stream);
+
+/* BF16 GEMV (M == 1) with the argmax of y fused into the same pass: y as
+ * rt_hip_gemv_bf16, plus idx[0]/val[0] as rt_hip_argmax over y.  The
+ * lm_head + greedy step of transformer5.cpp:262-266 and :382-391. */
+int rt_hip_gemv_bf16_argmax(const uint16_t* w, const float* x, float* y, int64_t n,
+                            int64_t k, int64_t* idx, float* val, rt_hip_stream stream);
+
+/* ---- dequantization and quantization ---------------------------------- */
+
+/* Q4_K -> f32, [N, K]: Q4KMat::dequantize_row_into for every row
+ * (src/quant_q4k.cpp:280-317).  Bit-exact. */
+int rt_hip_dequant_q4k_f32(const void* blocks, float* out, int64_t n, int64_t k,
+                           rt_hip_stream stream);
+/* Q4_K -> bf16 (RNE), [N, K]: flux_dequant_q4k (src/shaders/flux.msl:51-82). */
+int rt_hip_dequant_q4k_bf16(const void* blocks, uint16_t* out, int64_t n, int64_t k,
+                            rt_hip_stream stream);
+/* f32 [N, K] -> Q4_K blocks, byte-identical to Q4KMat::quantize
+ * (src/quant_q4k.cpp:71-205).  Requires K % 256 == 0. */
+int rt_hip_quantize_q4k(const float* w, void* blocks, int64_t n, int64_t k,
+                        rt_hip_stream stream);
+
+/* ---- GEMM: any M ----------------------------------------------------------
+ * C[M,N] = A[M,K] * W^T (+ bias[N]).  A is f32 (a_dtype RT_HIP_F32) or bf16
+ * bits (RT_HIP_BF16).  Operands are rounded to bf16 (RNE) and contracted on
+ * bf16 MFMA with f32 accumulation.
+ * Replace: Q4KMat::matmul_q4k_t_exact (src/quant_q4k.cpp:636-710) and
+ * QLinear::forward (src/qlinear.cpp:55-80); the FLUX gemm_into sequence
+ * flux_dequant_q4k + flux_gemm_bt + flux_add_bias (src/metal_flux.mm:155-185,
+ * src/shaders/flux.msl:51-143).  The Q4_K weight is dequantized into LDS tile
+ * by tile; no dequantized copy is ever written to HBM.  K % 256 == 0. */
+int rt_hip_gemm_q4k(const void* a, int32_t a_dtype, const void* blocks, const float* bias,
+                    float* c, int64_t m, int64_t n, int64_t k, rt_hip_stream stream);
+/* Replace: MatBf16::matmul_by_t for M > 1 (src/mat.cpp:351-414).  K % 64 == 0. */
+int rt_hip_gemm_bf16(const void* a, int32_t a_dtype, const uint16_t* w, const float* bias,
+                     float* c, int64_t m, int64_t n, int64_t k, rt_hip_stream stream);
+
+/* ---- linear dispatch ------------------------------------------------------
+ * The QLinear / Linear2::fused_linear dispatch over whichever weight format
+ * is loaded (src/qlinear.cpp:55-80, src/nn2.cpp:143-203): M <= 8 takes the
+ * GEMV kernels, larger M the MFMA GEMM; the bias (may be NULL) is added to
+ * every row (qlinear.cpp:42-53).  x is f32. */
+int rt_hip_linear_forward(int32_t format, const void* w, const float* bias, const float* x,
+                          float* y, int64_t m, int64_t n, int64_t k, rt_hip_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RT_HIP_H */

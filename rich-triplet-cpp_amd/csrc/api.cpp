@@ -1,0 +1,331 @@
+// api.cpp -- the C ABI (include/rt_hip.h): argument validation, device
+// bookkeeping, workspaces and dispatch to the kernel launchers.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "rt_hip.h"
+#include "rt_launch.hpp"
+
+namespace rt_hip {
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(RT_HIP_E_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+struct DeviceState {
+    DeviceInfo info;
+    bool ok = false;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+};
+
+std::mutex g_mu;
+std::vector<DeviceState> g_dev;
+
+DeviceState* state_for_current(hipError_t* err) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        *err = e;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (static_cast<int>(g_dev.size()) <= dev) g_dev.resize(dev + 1);
+    DeviceState& st = g_dev[dev];
+    if (!st.ok) {
+        hipDeviceProp_t prop;
+        e = hipGetDeviceProperties(&prop, dev);
+        if (e != hipSuccess) {
+            *err = e;
+            return nullptr;
+        }
+        st.info.ordinal = dev;
+        st.info.cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+        st.info.lds_per_block = prop.sharedMemPerBlock;
+        st.ok = true;
+    }
+    *err = hipSuccess;
+    return &st;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_stream_launch(hipError_t e, const char* what) {
+    if (e != hipSuccess) return hip_fail(e, what);
+    return RT_HIP_OK;
+}
+
+// Common GEMV argument checks.  Returns 0 or an error code.
+int gemv_args(const char* fn, const void* w, const float* x, const float* y, int64_t n,
+              int64_t k, int32_t m, int64_t k_multiple) {
+    if (!w || !x || !y) return fail(RT_HIP_E_ARG, std::string(fn) + ": null pointer");
+    if (n <= 0 || k <= 0) return fail(RT_HIP_E_ARG, std::string(fn) + ": n and k must be > 0");
+    if (m < 1 || m > RT_HIP_GEMV_MAX_M)
+        return fail(RT_HIP_E_SHAPE, std::string(fn) + ": m must be in [1, 8]");
+    if (k % k_multiple != 0)
+        return fail(RT_HIP_E_ALIGN,
+                    std::string(fn) + ": k must be a multiple of " + std::to_string(k_multiple));
+    if (n > 0x7fffffffLL || k > 0x7fffffffLL)
+        return fail(RT_HIP_E_SHAPE, std::string(fn) + ": n and k must fit in int32");
+    if (!aligned16(w) || !aligned16(x))
+        return fail(RT_HIP_E_ALIGN, std::string(fn) + ": w and x must be 16-byte aligned");
+    return RT_HIP_OK;
+}
+
+// Runs a GEMV in batches of activation rows that fit the LDS budget.
+template <typename F>
+int gemv_batched(const char* fn, int fmt, const float* x, float* y, int64_t n, int64_t k,
+                 int32_t m, F&& launch) {
+    hipError_t e;
+    DeviceState* st = state_for_current(&e);
+    if (!st) return hip_fail(e, fn);
+    const size_t cap = st->info.lds_per_block < 65536 ? st->info.lds_per_block : 65536;
+    int mb = m;
+    while (mb > 1 && gemv_lds_bytes(fmt, mb, k) > cap) --mb;
+    if (gemv_lds_bytes(fmt, mb, k) > cap)
+        return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k too large for the LDS-staged GEMV");
+    for (int32_t m0 = 0; m0 < m; m0 += mb) {
+        const int32_t mm = (m - m0) < mb ? (m - m0) : mb;
+        e = launch(x + static_cast<size_t>(m0) * k, y + static_cast<size_t>(m0) * n, mm);
+        if (e != hipSuccess) return hip_fail(e, fn);
+    }
+    return RT_HIP_OK;
+}
+
+}  // namespace
+
+const DeviceInfo& device_info() {
+    hipError_t e;
+    DeviceState* st = state_for_current(&e);
+    static DeviceInfo fallback;
+    return st ? st->info : fallback;
+}
+
+void* workspace(size_t bytes, hipError_t* err) {
+    DeviceState* st = state_for_current(err);
+    if (!st) return nullptr;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (st->ws_bytes < bytes) {
+        if (st->ws) {
+            *err = hipFree(st->ws);
+            if (*err != hipSuccess) return nullptr;
+            st->ws = nullptr;
+            st->ws_bytes = 0;
+        }
+        size_t sz = bytes < (1u << 20) ? (1u << 20) : bytes;
+        *err = hipMalloc(&st->ws, sz);
+        if (*err != hipSuccess) return nullptr;
+        st->ws_bytes = sz;
+    }
+    *err = hipSuccess;
+    return st->ws;
+}
+
+}  // namespace rt_hip
+
+using namespace rt_hip;
+
+extern "C" {
+
+const char* rt_hip_last_error(void) { return g_last_error.c_str(); }
+
+const char* rt_hip_version(void) { return "rt_hip 0.1 gfx950"; }
+
+int rt_hip_init(int ordinal) {
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return hip_fail(e, "rt_hip_init");
+    if (ordinal < 0 || ordinal >= count)
+        return fail(RT_HIP_E_ARG, "rt_hip_init: no device " + std::to_string(ordinal));
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, ordinal);
+    if (e != hipSuccess) return hip_fail(e, "rt_hip_init");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(RT_HIP_E_UNSUPPORTED,
+                    std::string("rt_hip_init: device is ") + prop.gcnArchName + ", not gfx950");
+    e = hipSetDevice(ordinal);
+    if (e != hipSuccess) return hip_fail(e, "rt_hip_init");
+    DeviceState* st = state_for_current(&e);
+    if (!st) return hip_fail(e, "rt_hip_init");
+    return RT_HIP_OK;
+}
+
+int rt_hip_gemv_q4k(const void* blocks, const float* x, float* y, int64_t n, int64_t k,
+                    int32_t m, rt_hip_stream stream) {
+    int rc = gemv_args("rt_hip_gemv_q4k", blocks, x, y, n, k, m, 256);
+    if (rc) return rc;
+    return gemv_batched("rt_hip_gemv_q4k", RT_HIP_Q4K, x, y, n, k, m,
+                        [&](const float* xx, float* yy, int mm) {
+                            return launch_gemv_q4k(blocks, xx, yy, n, k, mm,
+                                                   static_cast<hipStream_t>(stream));
+                        });
+}
+
+int rt_hip_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
+                     int32_t m, rt_hip_stream stream) {
+    int rc = gemv_args("rt_hip_gemv_bf16", w, x, y, n, k, m, 8);
+    if (rc) return rc;
+    return gemv_batched("rt_hip_gemv_bf16", RT_HIP_BF16, x, y, n, k, m,
+                        [&](const float* xx, float* yy, int mm) {
+                            return launch_gemv_bf16(w, xx, yy, n, k, mm, nullptr,
+                                                    static_cast<hipStream_t>(stream));
+                        });
+}
+
+int rt_hip_gemv_q4_0(const void* blocks, const float* x, float* y, int64_t n, int64_t k,
+                     int32_t m, rt_hip_stream stream) {
+    int rc = gemv_args("rt_hip_gemv_q4_0", blocks, x, y, n, k, m, 256);
+    if (rc) return rc;
+    return gemv_batched("rt_hip_gemv_q4_0", RT_HIP_Q4_0, x, y, n, k, m,
+                        [&](const float* xx, float* yy, int mm) {
+                            return launch_gemv_q4_0(blocks, xx, yy, n, k, mm,
+                                                    static_cast<hipStream_t>(stream));
+                        });
+}
+
+int rt_hip_argmax(const float* logits, int64_t rows, int64_t cols, int64_t* idx, float* val,
+                  rt_hip_stream stream) {
+    if (!logits || !idx) return fail(RT_HIP_E_ARG, "rt_hip_argmax: null pointer");
+    if (rows <= 0 || cols <= 0) return fail(RT_HIP_E_ARG, "rt_hip_argmax: rows, cols must be > 0");
+    if (cols > 0xffffffffLL || rows > 65535)
+        return fail(RT_HIP_E_SHAPE, "rt_hip_argmax: cols < 2^32 and rows <= 65535 required");
+    hipError_t e;
+    uint64_t* keys = static_cast<uint64_t*>(workspace(static_cast<size_t>(rows) * 8, &e));
+    if (!keys) return hip_fail(e, "rt_hip_argmax: workspace");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if ((e = launch_argmax_init(keys, rows, s)) != hipSuccess) return hip_fail(e, "rt_hip_argmax");
+    if ((e = launch_argmax_scan(logits, rows, cols, keys, s)) != hipSuccess)
+        return hip_fail(e, "rt_hip_argmax");
+    if ((e = launch_argmax_finalize(keys, rows, idx, val, s)) != hipSuccess)
+        return hip_fail(e, "rt_hip_argmax");
+    return RT_HIP_OK;
+}
+
+int rt_hip_gemv_bf16_argmax(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
+                            int64_t* idx, float* val, rt_hip_stream stream) {
+    int rc = gemv_args("rt_hip_gemv_bf16_argmax", w, x, y, n, k, 1, 8);
+    if (rc) return rc;
+    if (!idx) return fail(RT_HIP_E_ARG, "rt_hip_gemv_bf16_argmax: null idx");
+    hipError_t e;
+    if (gemv_lds_bytes(RT_HIP_BF16, 1, k) > 65536)
+        return fail(RT_HIP_E_SHAPE, "rt_hip_gemv_bf16_argmax: k too large");
+    uint64_t* key = static_cast<uint64_t*>(workspace(8, &e));
+    if (!key) return hip_fail(e, "rt_hip_gemv_bf16_argmax: workspace");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if ((e = launch_argmax_init(key, 1, s)) != hipSuccess)
+        return hip_fail(e, "rt_hip_gemv_bf16_argmax");
+    if ((e = launch_gemv_bf16(w, x, y, n, k, 1, key, s)) != hipSuccess)
+        return hip_fail(e, "rt_hip_gemv_bf16_argmax");
+    if ((e = launch_argmax_finalize(key, 1, idx, val, s)) != hipSuccess)
+        return hip_fail(e, "rt_hip_gemv_bf16_argmax");
+    return RT_HIP_OK;
+}
+
+int rt_hip_dequant_q4k_f32(const void* blocks, float* out, int64_t n, int64_t k,
+                           rt_hip_stream stream) {
+    if (!blocks || !out) return fail(RT_HIP_E_ARG, "rt_hip_dequant_q4k_f32: null pointer");
+    if (n <= 0 || k <= 0) return fail(RT_HIP_E_ARG, "rt_hip_dequant_q4k_f32: n, k must be > 0");
+    if (k % 256) return fail(RT_HIP_E_ALIGN, "rt_hip_dequant_q4k_f32: k must be a multiple of 256");
+    if (!aligned16(blocks) || !aligned16(out))
+        return fail(RT_HIP_E_ALIGN, "rt_hip_dequant_q4k_f32: pointers must be 16-byte aligned");
+    return check_stream_launch(
+        launch_dequant_q4k(blocks, out, false, n, k, static_cast<hipStream_t>(stream)),
+        "rt_hip_dequant_q4k_f32");
+}
+
+int rt_hip_dequant_q4k_bf16(const void* blocks, uint16_t* out, int64_t n, int64_t k,
+                            rt_hip_stream stream) {
+    if (!blocks || !out) return fail(RT_HIP_E_ARG, "rt_hip_dequant_q4k_bf16: null pointer");
+    if (n <= 0 || k <= 0) return fail(RT_HIP_E_ARG, "rt_hip_dequant_q4k_bf16: n, k must be > 0");
+    if (k % 256) return fail(RT_HIP_E_ALIGN, "rt_hip_dequant_q4k_bf16: k must be a multiple of 256");
+    if (!aligned16(blocks) || !aligned16(out))
+        return fail(RT_HIP_E_ALIGN, "rt_hip_dequant_q4k_bf16: pointers must be 16-byte aligned");
+    return check_stream_launch(
+        launch_dequant_q4k(blocks, out, true, n, k, static_cast<hipStream_t>(stream)),
+        "rt_hip_dequant_q4k_bf16");
+}
+
+int rt_hip_quantize_q4k(const float* w, void* blocks, int64_t n, int64_t k,
+                        rt_hip_stream stream) {
+    if (!w || !blocks) return fail(RT_HIP_E_ARG, "rt_hip_quantize_q4k: null pointer");
+    if (n <= 0 || k <= 0) return fail(RT_HIP_E_ARG, "rt_hip_quantize_q4k: n, k must be > 0");
+    if (k % 256) return fail(RT_HIP_E_ALIGN, "rt_hip_quantize_q4k: k must be a multiple of 256");
+    if (!aligned16(w) || !aligned16(blocks))
+        return fail(RT_HIP_E_ALIGN, "rt_hip_quantize_q4k: pointers must be 16-byte aligned");
+    return check_stream_launch(
+        launch_quantize_q4k(w, blocks, n, k, static_cast<hipStream_t>(stream)),
+        "rt_hip_quantize_q4k");
+}
+
+static int gemm_common(const char* fn, int w_fmt, const void* a, int32_t a_dtype, const void* w,
+                       const float* bias, float* c, int64_t m, int64_t n, int64_t k,
+                       int64_t k_multiple, rt_hip_stream stream) {
+    if (!a || !w || !c) return fail(RT_HIP_E_ARG, std::string(fn) + ": null pointer");
+    if (m <= 0 || n <= 0 || k <= 0) return fail(RT_HIP_E_ARG, std::string(fn) + ": sizes must be > 0");
+    if (a_dtype != RT_HIP_F32 && a_dtype != RT_HIP_BF16)
+        return fail(RT_HIP_E_ARG, std::string(fn) + ": a_dtype must be RT_HIP_F32 or RT_HIP_BF16");
+    if (k % k_multiple)
+        return fail(RT_HIP_E_ALIGN,
+                    std::string(fn) + ": k must be a multiple of " + std::to_string(k_multiple));
+    if (m > 0x7fffffffLL || n > 0x7fffffffLL || k > 0x7fffffffLL)
+        return fail(RT_HIP_E_SHAPE, std::string(fn) + ": sizes must fit in int32");
+    if (!aligned16(a) || !aligned16(w) || !aligned16(c))
+        return fail(RT_HIP_E_ALIGN, std::string(fn) + ": a, w, c must be 16-byte aligned");
+    if (n % 4) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": n must be a multiple of 4");
+    return check_stream_launch(launch_gemm(w_fmt, a, a_dtype == RT_HIP_BF16, w, bias, c, m, n, k,
+                                           static_cast<hipStream_t>(stream)),
+                               fn);
+}
+
+int rt_hip_gemm_q4k(const void* a, int32_t a_dtype, const void* blocks, const float* bias,
+                    float* c, int64_t m, int64_t n, int64_t k, rt_hip_stream stream) {
+    return gemm_common("rt_hip_gemm_q4k", RT_HIP_Q4K, a, a_dtype, blocks, bias, c, m, n, k, 256,
+                       stream);
+}
+
+int rt_hip_gemm_bf16(const void* a, int32_t a_dtype, const uint16_t* w, const float* bias,
+                     float* c, int64_t m, int64_t n, int64_t k, rt_hip_stream stream) {
+    return gemm_common("rt_hip_gemm_bf16", RT_HIP_BF16, a, a_dtype, w, bias, c, m, n, k, 64,
+                       stream);
+}
+
+int rt_hip_linear_forward(int32_t format, const void* w, const float* bias, const float* x,
+                          float* y, int64_t m, int64_t n, int64_t k, rt_hip_stream stream) {
+    int rc;
+    if (m <= RT_HIP_GEMV_MAX_M) {
+        switch (format) {
+            case RT_HIP_Q4K: rc = rt_hip_gemv_q4k(w, x, y, n, k, static_cast<int32_t>(m), stream); break;
+            case RT_HIP_BF16:
+                rc = rt_hip_gemv_bf16(static_cast<const uint16_t*>(w), x, y, n, k,
+                                      static_cast<int32_t>(m), stream);
+                break;
+            case RT_HIP_Q4_0: rc = rt_hip_gemv_q4_0(w, x, y, n, k, static_cast<int32_t>(m), stream); break;
+            default: return fail(RT_HIP_E_UNSUPPORTED, "rt_hip_linear_forward: unsupported format");
+        }
+        if (rc || !bias) return rc;
+        return check_stream_launch(launch_add_bias(y, bias, m, n, static_cast<hipStream_t>(stream)),
+                                   "rt_hip_linear_forward");
+    }
+    switch (format) {
+        case RT_HIP_Q4K: return rt_hip_gemm_q4k(x, RT_HIP_F32, w, bias, y, m, n, k, stream);
+        case RT_HIP_BF16:
+            return rt_hip_gemm_bf16(x, RT_HIP_F32, static_cast<const uint16_t*>(w), bias, y, m, n,
+                                    k, stream);
+        default: return fail(RT_HIP_E_UNSUPPORTED, "rt_hip_linear_forward: unsupported format for M > 8");
+    }
+}
+
+}  // extern "C"

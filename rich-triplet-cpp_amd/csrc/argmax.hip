@@ -1,0 +1,97 @@
+// argmax.hip -- greedy token selection over logits rows.
+//
+// Semantics of the reference's greedy branch (src/transformer5.cpp:382-391):
+// the first index of the strict maximum; NaN is never selected; a row with
+// nothing above -inf yields index 0.
+//
+// Each (value, index) pair is packed into one u64 key: an order-preserving
+// map of the f32 (with -0 folded onto +0, since -0 > +0 is false in the
+// reference's comparison) in the high half and (0xffffffff - index) in the
+// low half.  The maximum key is then the largest value with the lowest
+// index.  Keys start at (-inf, index 0), which every finite value beats and
+// no -inf beats, so an all -inf/NaN row keeps index 0.  Blocks combine with
+// atomicMax (order-independent, so the result is deterministic).
+#include "rt_common.hpp"
+#include "rt_launch.hpp"
+
+namespace rt_hip {
+namespace {
+
+constexpr uint32_t kNegInfOrdered = ~0xff800000u;  // order map of -inf
+constexpr uint64_t kInitKey = (static_cast<uint64_t>(kNegInfOrdered) << 32) | 0xffffffffull;
+
+__device__ __forceinline__ uint64_t key_of(float v, uint32_t idx) {
+    uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (static_cast<uint64_t>(u) << 32) | (0xffffffffu - idx);
+}
+
+__global__ void k_argmax_init(uint64_t* keys, int64_t rows) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < rows) keys[i] = kInitKey;
+}
+
+// grid = (chunks, rows): block (c, r) scans a chunk of row r.
+__global__ __launch_bounds__(256) void k_argmax_scan(const float* __restrict__ v, int64_t cols,
+                                                     int64_t chunk, uint64_t* keys) {
+    const int64_t r = blockIdx.y;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * chunk;
+    int64_t c1 = c0 + chunk;
+    if (c1 > cols) c1 = cols;
+    const float* row = v + r * cols;
+    uint64_t best = 0;
+    for (int64_t c = c0 + threadIdx.x; c < c1; c += 256) {
+        const float x = row[c];
+        if (x == x) {
+            const uint64_t k = key_of(x, static_cast<uint32_t>(c));
+            best = k > best ? k : best;
+        }
+    }
+#pragma unroll
+    for (int off = kWave / 2; off >= 1; off >>= 1) {
+        const uint64_t o = __shfl_xor(best, off, kWave);
+        best = o > best ? o : best;
+    }
+    if ((threadIdx.x & (kWave - 1)) == 0 && best != 0)
+        atomicMax(reinterpret_cast<unsigned long long*>(keys + r),
+                  static_cast<unsigned long long>(best));
+}
+
+__global__ void k_argmax_finalize(const uint64_t* keys, int64_t rows, int64_t* idx, float* val) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= rows) return;
+    const uint64_t k = keys[i];
+    const uint32_t u = static_cast<uint32_t>(k >> 32);
+    const uint32_t bits = (u & 0x80000000u) ? (u & 0x7fffffffu) : ~u;
+    idx[i] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(k));
+    if (val) val[i] = __uint_as_float(bits);
+}
+
+}  // namespace
+
+hipError_t launch_argmax_init(uint64_t* keys, int64_t rows, hipStream_t s) {
+    const unsigned blocks = static_cast<unsigned>((rows + 255) / 256);
+    hipLaunchKernelGGL(k_argmax_init, dim3(blocks), dim3(256), 0, s, keys, rows);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_scan(const float* v, int64_t rows, int64_t cols, uint64_t* keys,
+                              hipStream_t s) {
+    // About 16 K values per block; enough blocks to cover the chip for one row.
+    int64_t chunk = 16384;
+    int64_t chunks = (cols + chunk - 1) / chunk;
+    if (chunks < 1) chunks = 1;
+    hipLaunchKernelGGL(k_argmax_scan, dim3(static_cast<unsigned>(chunks),
+                                           static_cast<unsigned>(rows)),
+                       dim3(256), 0, s, v, cols, chunk, keys);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_finalize(uint64_t* keys, int64_t rows, int64_t* idx, float* val,
+                                  hipStream_t s) {
+    const unsigned blocks = static_cast<unsigned>((rows + 255) / 256);
+    hipLaunchKernelGGL(k_argmax_finalize, dim3(blocks), dim3(256), 0, s, keys, rows, idx, val);
+    return hipGetLastError();
+}
+
+}  // namespace rt_hip

@@ -1,0 +1,99 @@
+// rt_common.hpp -- device helpers shared by the gfx950 kernels.
+//
+// Numeric contracts (these are what make the kernels bit-exact where the
+// reference is exact):
+//  * f16 -> f32 is exact (v_cvt_f32_f16; f16 denormals are kept, the
+//    kernels never change the MODE register).  include/rt/bf16.hpp:66-93.
+//  * bf16 -> f32 is a 16-bit shift.  bf16.hpp:42-44.
+//  * Q4_K dequant w = (d*sv)*q - dmin*mv: both products are exact in f32
+//    (at most 11+6+4 significant bits), so only the subtraction rounds and
+//    the value cannot depend on FMA contraction.  quant_q4k.cpp:301-312.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rt_hip {
+
+constexpr int kWave = 64;
+constexpr int kQ4kBlockBytes = 144;
+constexpr int kQ4kBlockElems = 256;
+constexpr int kQ40BlockBytes = 18;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+}
+
+__device__ __forceinline__ float bf16_lo_to_f32(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi_to_f32(uint32_t w) {
+    return __uint_as_float(w & 0xffff0000u);
+}
+
+// Byte k (0..3) of a dword as f32: v_cvt_f32_ubyte{k}.
+__device__ __forceinline__ float ubyte_f32(uint32_t w, int k) {
+    return static_cast<float>((w >> (8 * k)) & 0xffu);
+}
+
+// 16-byte load through the vector memory path.
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+
+// Non-temporal 16-byte load for weights that are streamed exactly once.
+__device__ __forceinline__ u32x4 ld16_stream(const void* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// f32 -> bf16 round-to-nearest-even with NaN quieting (bf16.hpp:50-60).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float v) {
+    const uint32_t bits = __float_as_uint(v);
+    if ((bits & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((bits >> 16) | 0x40u);
+    return static_cast<uint16_t>((bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16);
+}
+
+// Sum over the `L` lanes of an aligned lane segment (L = 8..64), by xor
+// butterflies; every lane of the segment ends with the same value.
+template <int L>
+__device__ __forceinline__ float segment_sum(float v) {
+#pragma unroll
+    for (int off = L / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Q4_K 6-bit scale/min of sub-block j of a super-block, from the three
+// scale dwords s0 = sc[0..3], s1 = sc[4..7], s2 = sc[8..11]
+// (Q4KMat::scale_min, quant_q4k.cpp:58-69):
+//   j < 4 : sv = sc[j] & 63,            mv = sc[j+4] & 63
+//   j >= 4: sv = (sc[j+4] & 15) | ((sc[j-4] >> 6) << 4)
+//           mv = (sc[j+4] >> 4) | ((sc[j]   >> 6) << 4)
+// Lanes carry a per-lane j, so the selection is written branch-free from
+// precomputed bit offsets (ScaleSel).
+struct ScaleSel {
+    uint32_t lo_s_off;  // offset of the low 4 bits of sv
+    uint32_t lo_m_off;  // offset of the low 4 bits of mv
+    uint32_t hi_off;    // offset of the top 2 bits (sv in s0, mv in s1)
+    bool high;          // j >= 4: low bits come from s2
+};
+
+__device__ __forceinline__ ScaleSel make_scale_sel(int j) {
+    ScaleSel s;
+    const uint32_t t = static_cast<uint32_t>(j & 3) * 8u;
+    s.high = j >= 4;
+    s.lo_s_off = t;
+    s.lo_m_off = s.high ? t + 4u : t;
+    s.hi_off = s.high ? t + 6u : t + 4u;
+    return s;
+}
+
+__device__ __forceinline__ void decode_scale_min(const ScaleSel& s, uint32_t s0, uint32_t s1,
+                                                 uint32_t s2, uint32_t& sv, uint32_t& mv) {
+    const uint32_t src_s = s.high ? s2 : s0;
+    const uint32_t src_m = s.high ? s2 : s1;
+    sv = __builtin_amdgcn_ubfe(src_s, s.lo_s_off, 4) | (__builtin_amdgcn_ubfe(s0, s.hi_off, 2) << 4);
+    mv = __builtin_amdgcn_ubfe(src_m, s.lo_m_off, 4) | (__builtin_amdgcn_ubfe(s1, s.hi_off, 2) << 4);
+}
+
+}  // namespace rt_hip

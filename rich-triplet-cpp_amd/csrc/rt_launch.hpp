@@ -1,0 +1,48 @@
+// rt_launch.hpp -- internal launcher declarations (host side of each .hip
+// file); the C ABI in api.cpp validates arguments and calls these.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rt_hip.h"
+
+namespace rt_hip {
+
+// Device facts used for launch sizing (filled once per device by api.cpp).
+struct DeviceInfo {
+    int ordinal = -1;
+    int cus = 256;
+    size_t lds_per_block = 65536;
+};
+const DeviceInfo& device_info();
+
+// Library-owned device workspace, grown on demand, one per device.
+void* workspace(size_t bytes, hipError_t* err);
+
+// Largest M*K the GEMV kernels stage in LDS (f32 activations + 16-value sums).
+size_t gemv_lds_bytes(int fmt, int m, int64_t k);
+
+hipError_t launch_gemv_q4k(const void* w, const float* x, float* y, int64_t n, int64_t k,
+                           int m, hipStream_t s);
+hipError_t launch_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
+                            int m, uint64_t* argmax_key, hipStream_t s);
+hipError_t launch_gemv_q4_0(const void* w, const float* x, float* y, int64_t n, int64_t k,
+                            int m, hipStream_t s);
+
+hipError_t launch_argmax_init(uint64_t* keys, int64_t rows, hipStream_t s);
+hipError_t launch_argmax_scan(const float* v, int64_t rows, int64_t cols, uint64_t* keys,
+                              hipStream_t s);
+hipError_t launch_argmax_finalize(uint64_t* keys, int64_t rows, int64_t* idx, float* val,
+                                  hipStream_t s);
+
+hipError_t launch_dequant_q4k(const void* w, void* out, bool bf16, int64_t n, int64_t k,
+                              hipStream_t s);
+hipError_t launch_quantize_q4k(const float* w, void* blocks, int64_t n, int64_t k,
+                               hipStream_t s);
+
+hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, const float* bias,
+                       float* c, int64_t m, int64_t n, int64_t k, hipStream_t s);
+hipError_t launch_add_bias(float* y, const float* bias, int64_t m, int64_t n, hipStream_t s);
+
+}  // namespace rt_hip

@@ -1,0 +1,198 @@
+"""ctypes binding of the C ABI in include/rt_hip.h (lib/librt_hip.so).
+
+torch is only the device-memory and stream plumbing here: every call passes
+``tensor.data_ptr()`` and the current HIP stream to the native library, which
+runs the gfx950 kernels.  There is no fallback: if the library is missing or
+a call fails, an exception is raised.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIB_PATH = os.path.join(HERE, "lib", "librt_hip.so")
+HEADER_PATH = os.path.join(ROOT, "include", "rt_hip.h")
+
+F32, BF16, Q4K, Q4_0 = 0, 1, 2, 3
+GEMV_MAX_M = 8
+
+_vp, _i64, _i32 = C.c_void_p, C.c_int64, C.c_int32
+
+# name -> argtypes (restype is int unless noted)
+_SIGNATURES = {
+    "rt_hip_init": [C.c_int],
+    "rt_hip_gemv_q4k": [_vp, _vp, _vp, _i64, _i64, _i32, _vp],
+    "rt_hip_gemv_bf16": [_vp, _vp, _vp, _i64, _i64, _i32, _vp],
+    "rt_hip_gemv_q4_0": [_vp, _vp, _vp, _i64, _i64, _i32, _vp],
+    "rt_hip_argmax": [_vp, _i64, _i64, _vp, _vp, _vp],
+    "rt_hip_gemv_bf16_argmax": [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp],
+    "rt_hip_dequant_q4k_f32": [_vp, _vp, _i64, _i64, _vp],
+    "rt_hip_dequant_q4k_bf16": [_vp, _vp, _i64, _i64, _vp],
+    "rt_hip_quantize_q4k": [_vp, _vp, _i64, _i64, _vp],
+    "rt_hip_gemm_q4k": [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "rt_hip_gemm_bf16": [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "rt_hip_linear_forward": [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
+}
+
+
+class RtHipError(RuntimeError):
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed with status {code}: {msg}")
+        self.code = code
+
+
+def header_functions(path: str = HEADER_PATH) -> list[str]:
+    """Names of the functions include/rt_hip.h declares."""
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rt_hip_\w+)\s*\(", text)))
+
+
+class Library:
+    """The loaded native library (no compute happens at load time)."""
+
+    def __init__(self, path: str = LIB_PATH):
+        if not os.path.exists(path):
+            raise FileNotFoundError(
+                f"{path} is missing: build it with `make -C rich-triplet-cpp_amd` "
+                "(or __graft_entry__.build())")
+        self.path = path
+        self.lib = C.CDLL(path)
+        self.lib.rt_hip_last_error.restype = C.c_char_p
+        self.lib.rt_hip_version.restype = C.c_char_p
+        for name, args in _SIGNATURES.items():
+            fn = getattr(self.lib, name)
+            fn.restype = C.c_int
+            fn.argtypes = args
+
+    def version(self) -> str:
+        return self.lib.rt_hip_version().decode()
+
+    def call(self, name: str, *args) -> None:
+        rc = getattr(self.lib, name)(*args)
+        if rc != 0:
+            raise RtHipError(name, rc, self.lib.rt_hip_last_error().decode())
+
+    def status(self, name: str, *args) -> int:
+        """Call and return the status code without raising (for error tests)."""
+        return getattr(self.lib, name)(*args)
+
+
+_LIB: Library | None = None
+
+
+def library() -> Library:
+    global _LIB
+    if _LIB is None:
+        _LIB = Library()
+    return _LIB
+
+
+# ---------------------------------------------------------------- torch API --
+
+def _torch():
+    import torch  # noqa: PLC0415  (plumbing only)
+    return torch
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream=None) -> int:
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def init(ordinal: int = 0) -> None:
+    library().call("rt_hip_init", ordinal)
+
+
+def _dev_check(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("rt_hip: tensors must live on the GPU")
+        if t is not None and not t.is_contiguous():
+            raise ValueError("rt_hip: tensors must be contiguous")
+
+
+def gemv(fmt: int, w, x, n: int, k: int, y=None, stream=None):
+    """y[M, N] = x[M, K] @ W^T for M <= 8; W in `fmt` bytes on the device."""
+    torch = _torch()
+    x = x.reshape(-1, k)
+    m = x.shape[0]
+    if y is None:
+        y = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    _dev_check(w, x, y)
+    name = {Q4K: "rt_hip_gemv_q4k", BF16: "rt_hip_gemv_bf16", Q4_0: "rt_hip_gemv_q4_0"}[fmt]
+    library().call(name, _ptr(w), _ptr(x), _ptr(y), n, k, m, _stream(stream))
+    return y
+
+
+def gemv_bf16_argmax(w, x, n: int, k: int, y=None, stream=None):
+    torch = _torch()
+    if y is None:
+        y = torch.empty((1, n), dtype=torch.float32, device=x.device)
+    idx = torch.empty(1, dtype=torch.int64, device=x.device)
+    val = torch.empty(1, dtype=torch.float32, device=x.device)
+    _dev_check(w, x, y)
+    library().call("rt_hip_gemv_bf16_argmax", _ptr(w), _ptr(x), _ptr(y), n, k, _ptr(idx),
+                   _ptr(val), _stream(stream))
+    return y, idx, val
+
+
+def argmax(logits, stream=None):
+    torch = _torch()
+    rows, cols = logits.shape
+    idx = torch.empty(rows, dtype=torch.int64, device=logits.device)
+    val = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    _dev_check(logits)
+    library().call("rt_hip_argmax", _ptr(logits), rows, cols, _ptr(idx), _ptr(val),
+                   _stream(stream))
+    return idx, val
+
+
+def dequant_q4k(blocks, n: int, k: int, bf16: bool = False, stream=None):
+    torch = _torch()
+    out = torch.empty((n, k), dtype=torch.int16 if bf16 else torch.float32, device=blocks.device)
+    _dev_check(blocks)
+    name = "rt_hip_dequant_q4k_bf16" if bf16 else "rt_hip_dequant_q4k_f32"
+    library().call(name, _ptr(blocks), _ptr(out), n, k, _stream(stream))
+    return out
+
+
+def quantize_q4k(w, stream=None):
+    torch = _torch()
+    n, k = w.shape
+    blocks = torch.empty(n * (k // 256) * 144, dtype=torch.uint8, device=w.device)
+    _dev_check(w)
+    library().call("rt_hip_quantize_q4k", _ptr(w), _ptr(blocks), n, k, _stream(stream))
+    return blocks
+
+
+def gemm(fmt: int, a, w, n: int, k: int, bias=None, c=None, stream=None):
+    """C[M, N] = A[M, K] @ W^T (+ bias); A f32 or bf16 (torch.bfloat16)."""
+    torch = _torch()
+    m = a.shape[0]
+    if c is None:
+        c = torch.empty((m, n), dtype=torch.float32, device=a.device)
+    a_dtype = BF16 if a.dtype == torch.bfloat16 else F32
+    _dev_check(a, w, c, bias)
+    name = {Q4K: "rt_hip_gemm_q4k", BF16: "rt_hip_gemm_bf16"}[fmt]
+    library().call(name, _ptr(a), a_dtype, _ptr(w), _ptr(bias), _ptr(c), m, n, k, _stream(stream))
+    return c
+
+
+def linear_forward(fmt: int, w, x, n: int, k: int, bias=None, y=None, stream=None):
+    torch = _torch()
+    m = x.shape[0]
+    if y is None:
+        y = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    _dev_check(w, x, y, bias)
+    library().call("rt_hip_linear_forward", fmt, _ptr(w), _ptr(bias), _ptr(x), _ptr(y), m, n, k,
+                   _stream(stream))
+    return y

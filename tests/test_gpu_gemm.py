@@ -1,0 +1,82 @@
+"""GPU parity for the bf16-MFMA GEMM (prefill / FLUX linears).
+
+Two stated tolerances:
+ (i)  against the f32-accumulated product of the same bf16-rounded operands
+      (fp64 reference): normwise <= 1e-5;
+ (ii) against the reference's f32 CPU path (Q4KMat::matmul_q4k_t's scalar
+      loop / MatBf16::matmul_by_t): relative RMS <= 1e-2 -- the bf16 operand
+      rounding, the same philosophy as the reference's Metal GEMM test bound
+      (tests/test_metal_flux.cpp:140-145).
+"""
+import numpy as np
+import pytest
+
+from helpers import (GEMM_TOL_SAME_OPERANDS, GEMM_TOL_VS_F32_RMS, bf16_bits_to_f32,
+                     f32_to_bf16_rne, from_dev, normwise_err, rel_rms, say, to_dev)
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # (M, N, K, a_bf16)
+    (128, 128, 256, False),
+    (200, 300, 512, False),
+    (64, 1000, 768, True),
+    (513, 260, 1024, False),
+    (9, 64, 256, False),
+]
+
+
+@pytest.mark.parametrize("m,n,k,a_bf16", CASES)
+def test_gemm_q4k(rt, orc, m, n, k, a_bf16):
+    say(f"[gemm q4k] M={m} N={n} K={k} a_bf16={a_bf16}")
+    import torch
+    rng = np.random.default_rng(m + n + k)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    blocks = orc.q4k_quantize(w)
+    deq = orc.q4k_dequant(blocks, n, k)
+    a_bits = f32_to_bf16_rne(a)
+    a_r = bf16_bits_to_f32(a_bits).astype(np.float64)
+    w_r = bf16_bits_to_f32(f32_to_bf16_rne(deq)).astype(np.float64)
+    same = a_r @ w_r.T + bias
+    d_a = to_dev(a_bits).view(torch.bfloat16) if a_bf16 else to_dev(a)
+    c = from_dev(rt.gemm(rt.Q4K, d_a, to_dev(blocks), n, k, bias=to_dev(bias)))
+    assert normwise_err(c, same) <= GEMM_TOL_SAME_OPERANDS
+    if m * n * k <= 64 * 1024 * 1024:
+        ref = orc.q4k_matmul_t(blocks, n, k, a if not a_bf16 else bf16_bits_to_f32(a_bits)) + bias
+        assert rel_rms(c, ref) <= GEMM_TOL_VS_F32_RMS
+
+
+@pytest.mark.parametrize("m,n,k,a_bf16", [(128, 128, 128, False), (300, 200, 576, True),
+                                         (17, 520, 192, False)])
+def test_gemm_bf16(rt, orc, m, n, k, a_bf16):
+    say(f"[gemm bf16] M={m} N={n} K={k}")
+    import torch
+    rng = np.random.default_rng(m * n + k)
+    wb = orc.f32_to_bf16_n((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    a_bits = f32_to_bf16_rne(a)
+    same = bf16_bits_to_f32(a_bits).astype(np.float64) @ bf16_bits_to_f32(wb).astype(np.float64).T
+    d_a = to_dev(a_bits).view(torch.bfloat16) if a_bf16 else to_dev(a)
+    c = from_dev(rt.gemm(rt.BF16, d_a, to_dev(wb), n, k))
+    assert normwise_err(c, same) <= GEMM_TOL_SAME_OPERANDS
+    ref = orc.bf16_matmul_t(wb, a)
+    assert rel_rms(c, ref) <= GEMM_TOL_VS_F32_RMS
+
+
+def test_gemm_prefill_shape_properties(rt):
+    """BASELINE config 4 gate shape (M=512, N=8192, K=3072) at full size:
+    GEMM of the GPU-quantized weight equals the product with its bf16
+    dequantization computed by torch in f32 (tolerance (i))."""
+    import torch
+    m, n, k = 512, 8192, 3072
+    g = torch.Generator(device="cuda").manual_seed(1)
+    w = torch.randn((n, k), generator=g, device="cuda") * 0.02
+    a = torch.randn((m, k), generator=g, device="cuda")
+    blocks = rt.quantize_q4k(w)
+    wd = rt.dequant_q4k(blocks, n, k, bf16=True).view(torch.bfloat16).float()
+    ref = a.bfloat16().float() @ wd.T
+    c = rt.gemm(rt.Q4K, a, blocks, n, k)
+    err = ((c - ref).abs().max() / ref.abs().max()).item()
+    assert err <= 1e-5 * 4  # f32 torch reference itself rounds differently
