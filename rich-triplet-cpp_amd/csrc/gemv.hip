@@ -3,26 +3,29 @@
 //
 // y[m, n] = sum_k x[m, k] * W[n, k]
 //
-// Work decomposition (all three formats):
-//  * A "piece" is the unit one lane loads per weight row: 16 bytes of Q4_K
-//    qs (32 nibbles) plus its block header, 144 bytes of Q4_0 (8 blocks), or
-//    16 bytes of BF16 (8 values).
+// Work decomposition (all three formats share one pipelined driver):
+//  * A "piece" is what one lane loads per weight row per step: 16 bytes of
+//    Q4_K qs (32 nibbles) plus the 16-byte header of its super-block, 144
+//    bytes of GGUF Q4_0 (8 blocks, 256 values), or 16 bytes of BF16 (8
+//    values).
 //  * A row is split over L lanes (L = the largest power of two <= 64 that
-//    divides the row's piece count), so each lane owns a fixed set of piece
+//    divides the row's piece count), so each lane owns fixed piece
 //    positions for the whole kernel: its Q4_K sub-block selector and its
 //    activation offsets are lane constants.  A wave covers R = 64/L row
-//    segments, and each lane carries P rows (P independent accumulators),
-//    so one activation read from LDS feeds P rows.
-//  * x[M, K] is staged in LDS once per workgroup (with the sum of every
-//    16-value group, which the Q4_K/Q4_0 min/offset terms need).  The first
-//    piece's weight loads are issued before staging, and every iteration
-//    issues the next piece's loads before computing the current one (two
-//    register sets used alternately), so HBM requests stay in flight.
+//    segments and each lane carries P rows, so one activation read from LDS
+//    feeds P rows.  A "row group" is the R*P rows a wave computes together.
+//  * Software pipeline: a ring of D register slots, each holding one piece
+//    for P rows.  The loads for the first D pieces are issued before x is
+//    staged, and every computed slot is immediately refilled with the piece
+//    D steps ahead (walking row groups g = wave, wave + nwaves, ...), so each
+//    wave keeps D*P pieces of HBM traffic in flight at all times.
+//  * x[M, K] is staged in LDS once per workgroup, with the sum of every
+//    16-value group (the Q4_K min term and the Q4_0 offset term need it).
 //  * Rows are reduced across their L lanes with xor butterflies.
 //
-// Numerics: f32 FMA accumulation; the reduction order differs from the
-// reference's sequential dot_row (quant_q4k.cpp:489-522, mat.cpp:310-314),
-// so results agree to f32 rounding, not bit-for-bit.
+// Numerics: f32 FMA accumulation; the order differs from the reference's
+// sequential dot_row (quant_q4k.cpp:489-522, mat.cpp:310-314), so results
+// agree to f32 rounding, not bit-for-bit.
 #include "rt_common.hpp"
 #include "rt_launch.hpp"
 
@@ -32,27 +35,6 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
 
-// x[M*K] into LDS; then sums of each 16-value group (M*K/16 of them).
-template <int M, bool SUMS>
-__device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ X, int K) {
-    const int n4 = M * K / 4;
-    for (int i = threadIdx.x; i < n4; i += kBlock)
-        reinterpret_cast<f32x4*>(xs)[i] = reinterpret_cast<const f32x4*>(X)[i];
-    __syncthreads();
-    if constexpr (SUMS) {
-        float* xsum = xs + M * K;
-        const int ng = M * K / 16;
-        for (int i = threadIdx.x; i < ng; i += kBlock) {
-            const float* p = xs + 16 * i;
-            float s = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) s += p[j];
-            xsum[i] = s;
-        }
-        __syncthreads();
-    }
-}
-
 __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
     // Order-preserving map of f32 to u32 (with -0 folded onto +0), index in
     // the low half inverted so the lowest index wins ties under max.
@@ -61,83 +43,85 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
     return (static_cast<uint64_t>(u) << 32) | (0xffffffffu - idx);
 }
 
-// ---------------------------------------------------------------- Q4_K --
+// ------------------------------------------------------------ formats --
 
-template <int P>
-struct Q4kRegs {
-    u32x4 q[P];
-    u32x4 h[P];
-};
-
-template <int L, int P, int M>
-__global__ __launch_bounds__(kBlock) void k_gemv_q4k(const uint8_t* __restrict__ W,
-                                                     const float* __restrict__ X,
-                                                     float* __restrict__ Y, int N, int K) {
-    extern __shared__ float lds[];
-    constexpr int R = kWave / L;
-    constexpr int RG = R * P;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int li = lane & (L - 1);
-    const int seg = lane / L;
-    const int nb = K >> 8;
-    const int S = (nb * 8) / L;
-    const int G = (N + RG - 1) / RG;
-    const int nwaves = gridDim.x * kWavesPerBlock;
-    int g = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-
-    // Lane constants: piece p of every block it visits (L is a multiple of 8).
-    const int p = li & 7, c = p >> 1, h = p & 1;
-    const size_t row_bytes = static_cast<size_t>(nb) * kQ4kBlockBytes;
-    const uint8_t* Wl = W + static_cast<size_t>(li >> 3) * kQ4kBlockBytes;
-    const size_t t_stride = static_cast<size_t>(L / 8) * kQ4kBlockBytes;
-    const int qoff = 16 + 16 * p;
-
-    auto issue = [&](int gg, int tt, Q4kRegs<P>& r) {
-        const uint8_t* base = Wl + static_cast<size_t>(tt) * t_stride;
-#pragma unroll
-        for (int i = 0; i < P; ++i) {
-            int row = gg * RG + i * R + seg;
-            row = row < N ? row : N - 1;
-            const uint8_t* bp = base + static_cast<size_t>(row) * row_bytes;
-            r.h[i] = ld16(bp);
-            r.q[i] = ld16(bp + qoff);
-        }
+// Q4_K: piece = (block b, 16-byte qs half-chunk p); regs = {header, qs}.
+struct Q4kFmt {
+    static constexpr int kRegs = 2;
+    static constexpr bool kSums = true;
+    __host__ __device__ static int pieces_per_row(int K) { return (K >> 8) * 8; }
+    __host__ __device__ static size_t row_bytes(int K) {
+        return static_cast<size_t>(K >> 8) * kQ4kBlockBytes;
+    }
+    struct Lane {
+        int p, c, h;
+        ScaleSel s1, s2;
     };
-
-    Q4kRegs<P> A, B;
-    if (g < G) issue(g, 0, A);
-    stage_x<M, true>(lds, X, K);
-    if (g >= G) return;
-    const float* xs = lds;
-    const float* xsum = lds + M * K;
-
-    const ScaleSel sel1 = make_scale_sel(2 * c), sel2 = make_scale_sel(2 * c + 1);
-    float acc[P][M];
-#pragma unroll
-    for (int i = 0; i < P; ++i)
-#pragma unroll
-        for (int m = 0; m < M; ++m) acc[i][m] = 0.0f;
-
-    int t = 0;
-    // One piece: compute from `cur`, prefetch into `nxt`.  Returns false when
-    // the wave has no further piece.
-    auto step = [&](Q4kRegs<P>& cur, Q4kRegs<P>& nxt) -> bool {
-        int gn = g, tn = t + 1;
-        if (tn == S) {
-            tn = 0;
-            gn = g + nwaves;
+    __device__ static Lane lane(int li) {
+        Lane ln;
+        ln.p = li & 7;
+        ln.c = ln.p >> 1;
+        ln.h = ln.p & 1;
+        ln.s1 = make_scale_sel(2 * ln.c);
+        ln.s2 = make_scale_sel(2 * ln.c + 1);
+        return ln;
+    }
+    // LDS layout, piece-major so that consecutive lanes read consecutive
+    // 16-byte chunks (no bank conflicts): piece s = 8*b + 2*c + h covers the
+    // low-nibble values b*256 + 64c + 16h + [0,16) and the high-nibble
+    // values 32 later; f32x4 number j (0-3 low, 4-7 high) of piece s of
+    // activation row m sits at xs4[(m*8 + j)*NP + s], NP = K/32 pieces.
+    // The two 16-value sums of piece s sit at sums2[m*NP + s].
+    static size_t lds_floats(int M, int K) {
+        return static_cast<size_t>(M) * K + static_cast<size_t>(M) * (K / 16);
+    }
+    template <int M>
+    __device__ static void stage(float* lds, const float* __restrict__ X, int K, int tid, int nthr) {
+        const int np = K >> 5;
+        f32x4* xs4 = reinterpret_cast<f32x4*>(lds);
+        for (int f = tid; f < M * K / 4; f += nthr) {
+            const int m = f / (K >> 2), k = 4 * (f - m * (K >> 2));
+            const int b = k >> 8, w = k & 255, c = w >> 6, r = w & 63;
+            const int hi = r >> 5, h = (r >> 4) & 1, q = (r & 15) >> 2;
+            xs4[(m * 8 + 4 * hi + q) * np + 8 * b + 2 * c + h] =
+                reinterpret_cast<const f32x4*>(X)[f];
         }
-        const bool more = gn < G;
-        if (more) issue(gn, tn, nxt);
-
+        __syncthreads();
+        f32x2* sums = reinterpret_cast<f32x2*>(lds + static_cast<size_t>(M) * K);
+        for (int e = tid; e < M * np; e += nthr) {
+            const int m = e / np, sp = e - m * np;
+            float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f32x4 a = xs4[(m * 8 + j) * np + sp];
+                const f32x4 b = xs4[(m * 8 + 4 + j) * np + sp];
+                lo += a[0]; lo += a[1]; lo += a[2]; lo += a[3];
+                hi += b[0]; hi += b[1]; hi += b[2]; hi += b[3];
+            }
+            sums[e] = f32x2{lo, hi};
+        }
+        __syncthreads();
+    }
+    template <int L>
+    __device__ static int block_of(int li, int t) { return (li >> 3) + (L / 8) * t; }
+    template <int L>
+    __device__ static void load(const uint8_t* row, int li, int t, const Lane& ln, u32x4* r) {
+        const uint8_t* bp = row + static_cast<size_t>(block_of<L>(li, t)) * kQ4kBlockBytes;
+        r[0] = ld16(bp);
+        r[1] = ld16(bp + 16 + 16 * ln.p);
+    }
+    template <int L, int P, int M>
+    __device__ static void compute(const u32x4 (&v)[P][kRegs], int li, int t, const Lane& ln,
+                                   const float* xs, const float* xsum, int K, float (&acc)[P][M]) {
         float s1[P], n1[P], s2[P], n2[P];
 #pragma unroll
         for (int i = 0; i < P; ++i) {
-            const float d = f16_bits_to_f32(cur.h[i][0] & 0xffffu);
-            const float dm = f16_bits_to_f32(cur.h[i][0] >> 16);
+            const u32x4 hd = v[i][0];
+            const float d = f16_bits_to_f32(hd[0] & 0xffffu);
+            const float dm = f16_bits_to_f32(hd[0] >> 16);
             uint32_t sv1, mv1, sv2, mv2;
-            decode_scale_min(sel1, cur.h[i][1], cur.h[i][2], cur.h[i][3], sv1, mv1);
-            decode_scale_min(sel2, cur.h[i][1], cur.h[i][2], cur.h[i][3], sv2, mv2);
+            decode_scale_min(ln.s1, hd[1], hd[2], hd[3], sv1, mv1);
+            decode_scale_min(ln.s2, hd[1], hd[2], hd[3], sv2, mv2);
             s1[i] = d * static_cast<float>(sv1);
             n1[i] = dm * static_cast<float>(mv1);
             // High nibbles are converted as 16*q (mask 0xF0): fold the exact
@@ -145,27 +129,26 @@ __global__ __launch_bounds__(kBlock) void k_gemv_q4k(const uint8_t* __restrict__
             s2[i] = (d * static_cast<float>(sv2)) * 0.0625f;
             n2[i] = dm * static_cast<float>(mv2);
         }
-        const int b = (li >> 3) + (L / 8) * t;
-        const int xo = b * 256 + c * 64 + h * 16;
-        const int go = xo >> 4;
+        const int np = K >> 5;
+        const int sp = li + L * t;  // this lane's piece index within the row
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            const float* xm = xs + m * K + xo;
+            const f32x4* xm = reinterpret_cast<const f32x4*>(xs) + m * 8 * np + sp;
             f32x4 xl[4], xh[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                xl[j] = reinterpret_cast<const f32x4*>(xm)[j];
-                xh[j] = reinterpret_cast<const f32x4*>(xm + 32)[j];
+                xl[j] = xm[j * np];
+                xh[j] = xm[(j + 4) * np];
             }
-            const float sl = xsum[m * (K >> 4) + go];
-            const float sh = xsum[m * (K >> 4) + go + 2];
+            const f32x2 ss = reinterpret_cast<const f32x2*>(xsum)[m * np + sp];
+            const float sl = ss[0], sh = ss[1];
 #pragma unroll
             for (int i = 0; i < P; ++i) {
                 float dl = 0.0f, dh = 0.0f;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const uint32_t wl = cur.q[i][j] & 0x0f0f0f0fu;
-                    const uint32_t wh = cur.q[i][j] & 0xf0f0f0f0u;
+                    const uint32_t wl = v[i][1][j] & 0x0f0f0f0fu;
+                    const uint32_t wh = v[i][1][j] & 0xf0f0f0f0u;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         dl = __builtin_fmaf(ubyte_f32(wl, e), xl[j][e], dl);
@@ -180,235 +163,141 @@ __global__ __launch_bounds__(kBlock) void k_gemv_q4k(const uint8_t* __restrict__
                 acc[i][m] = a;
             }
         }
-        if (tn == 0) {
+    }
+};
+
+// BF16: piece = 8 consecutive values.
+struct Bf16Fmt {
+    static constexpr int kRegs = 1;
+    static constexpr bool kSums = false;
+    __host__ __device__ static int pieces_per_row(int K) { return K / 8; }
+    __host__ __device__ static size_t row_bytes(int K) { return static_cast<size_t>(K) * 2; }
+    // LDS layout: piece s (values 8s..8s+7) of activation row m as two
+    // f32x4 at xs4[(m*2 + j)*NP + s], NP = K/8 (consecutive lanes read
+    // consecutive 16-byte chunks).
+    static size_t lds_floats(int M, int K) { return static_cast<size_t>(M) * K; }
+    template <int M>
+    __device__ static void stage(float* lds, const float* __restrict__ X, int K, int tid, int nthr) {
+        const int np = K >> 3;
+        f32x4* xs4 = reinterpret_cast<f32x4*>(lds);
+        for (int f = tid; f < M * K / 4; f += nthr) {
+            const int m = f / (K >> 2), k4 = f - m * (K >> 2);
+            xs4[(m * 2 + (k4 & 1)) * np + (k4 >> 1)] = reinterpret_cast<const f32x4*>(X)[f];
+        }
+        __syncthreads();
+    }
+    struct Lane {};
+    __device__ static Lane lane(int) { return Lane{}; }
+    template <int L>
+    __device__ static void load(const uint8_t* row, int li, int t, const Lane&, u32x4* r) {
+        r[0] = ld16(row + 16 * static_cast<size_t>(li + L * t));
+    }
+    template <int L, int P, int M>
+    __device__ static void compute(const u32x4 (&v)[P][kRegs], int li, int t, const Lane&,
+                                   const float* xs, const float*, int K, float (&acc)[P][M]) {
+        const int np = K >> 3;
+        const int sp = li + L * t;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const f32x4* xm = reinterpret_cast<const f32x4*>(xs) + m * 2 * np + sp;
+            const f32x4 x0 = xm[0];
+            const f32x4 x1 = xm[np];
 #pragma unroll
             for (int i = 0; i < P; ++i) {
-                const int row = g * RG + i * R + seg;
-#pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    const float v = segment_sum<L>(acc[i][m]);
-                    if (li == 0 && row < N) Y[static_cast<size_t>(m) * N + row] = v;
-                    acc[i][m] = 0.0f;
-                }
+                const u32x4 w = v[i][0];
+                float a = acc[i][m];
+                a = __builtin_fmaf(bf16_lo_to_f32(w[0]), x0[0], a);
+                a = __builtin_fmaf(bf16_hi_to_f32(w[0]), x0[1], a);
+                a = __builtin_fmaf(bf16_lo_to_f32(w[1]), x0[2], a);
+                a = __builtin_fmaf(bf16_hi_to_f32(w[1]), x0[3], a);
+                a = __builtin_fmaf(bf16_lo_to_f32(w[2]), x1[0], a);
+                a = __builtin_fmaf(bf16_hi_to_f32(w[2]), x1[1], a);
+                a = __builtin_fmaf(bf16_lo_to_f32(w[3]), x1[2], a);
+                a = __builtin_fmaf(bf16_hi_to_f32(w[3]), x1[3], a);
+                acc[i][m] = a;
             }
         }
-        g = gn;
-        t = tn;
-        return more;
-    };
-
-    for (;;) {
-        if (!step(A, B)) break;
-        if (!step(B, A)) break;
     }
-}
-
-// ---------------------------------------------------------------- BF16 --
-
-template <int P>
-struct Bf16Regs {
-    u32x4 w[P];
 };
 
-template <int L, int P, int M, bool ARGMAX>
-__global__ __launch_bounds__(kBlock) void k_gemv_bf16(const uint16_t* __restrict__ W,
-                                                      const float* __restrict__ X,
-                                                      float* __restrict__ Y, int N, int K,
-                                                      uint64_t* __restrict__ key_out) {
-    extern __shared__ float lds[];
-    constexpr int R = kWave / L;
-    constexpr int RG = R * P;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int li = lane & (L - 1);
-    const int seg = lane / L;
-    const int S = (K / 8) / L;
-    const int G = (N + RG - 1) / RG;
-    const int nwaves = gridDim.x * kWavesPerBlock;
-    int g = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-    const uint16_t* Wl = W + 8 * li;
-
-    auto issue = [&](int gg, int tt, Bf16Regs<P>& r) {
-        const uint16_t* base = Wl + static_cast<size_t>(tt) * (8 * L);
-#pragma unroll
-        for (int i = 0; i < P; ++i) {
-            int row = gg * RG + i * R + seg;
-            row = row < N ? row : N - 1;
-            r.w[i] = ld16(base + static_cast<size_t>(row) * K);
+// GGUF Q4_0: piece = 8 blocks = 144 bytes = 256 values, 9 x 16-byte loads.
+struct Q40Fmt {
+    static constexpr int kRegs = 9;
+    static constexpr bool kSums = true;
+    __host__ __device__ static int pieces_per_row(int K) { return K >> 8; }
+    __host__ __device__ static size_t row_bytes(int K) { return static_cast<size_t>(K >> 8) * 144; }
+    // LDS layout: piece s (values 256s..256s+255) of activation row m as 64
+    // f32x4 at xs4[(m*64 + j)*NP + s], NP = K/256; the sum of each 32-value
+    // block blk of piece s at sums[(m*8 + blk)*NP + s].
+    static size_t lds_floats(int M, int K) { return static_cast<size_t>(M) * K * 33 / 32; }
+    template <int M>
+    __device__ static void stage(float* lds, const float* __restrict__ X, int K, int tid, int nthr) {
+        const int np = K >> 8;
+        f32x4* xs4 = reinterpret_cast<f32x4*>(lds);
+        for (int f = tid; f < M * K / 4; f += nthr) {
+            const int m = f / (K >> 2), k4 = f - m * (K >> 2);
+            xs4[(m * 64 + (k4 & 63)) * np + (k4 >> 6)] = reinterpret_cast<const f32x4*>(X)[f];
         }
-    };
-
-    Bf16Regs<P> A, B;
-    if (g < G) issue(g, 0, A);
-    stage_x<M, false>(lds, X, K);
-    uint64_t best = 0;
-    if (g < G) {
-        const float* xs = lds;
-        float acc[P][M];
+        __syncthreads();
+        float* sums = lds + static_cast<size_t>(M) * K;
+        for (int e = tid; e < M * 8 * np; e += nthr) {
+            const int m = e / (8 * np), r = e - m * 8 * np, blk = r / np, sp = r - blk * np;
+            float acc = 0.0f;
 #pragma unroll
-        for (int i = 0; i < P; ++i)
-#pragma unroll
-            for (int m = 0; m < M; ++m) acc[i][m] = 0.0f;
-        int t = 0;
-        auto step = [&](Bf16Regs<P>& cur, Bf16Regs<P>& nxt) -> bool {
-            int gn = g, tn = t + 1;
-            if (tn == S) {
-                tn = 0;
-                gn = g + nwaves;
+            for (int j = 0; j < 8; ++j) {
+                const f32x4 a = xs4[(m * 64 + 8 * blk + j) * np + sp];
+                acc += a[0]; acc += a[1]; acc += a[2]; acc += a[3];
             }
-            const bool more = gn < G;
-            if (more) issue(gn, tn, nxt);
-            const int xo = 8 * (li + L * t);
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                const f32x4 x0 = reinterpret_cast<const f32x4*>(xs + m * K + xo)[0];
-                const f32x4 x1 = reinterpret_cast<const f32x4*>(xs + m * K + xo)[1];
-#pragma unroll
-                for (int i = 0; i < P; ++i) {
-                    float a = acc[i][m];
-                    a = __builtin_fmaf(bf16_lo_to_f32(cur.w[i][0]), x0[0], a);
-                    a = __builtin_fmaf(bf16_hi_to_f32(cur.w[i][0]), x0[1], a);
-                    a = __builtin_fmaf(bf16_lo_to_f32(cur.w[i][1]), x0[2], a);
-                    a = __builtin_fmaf(bf16_hi_to_f32(cur.w[i][1]), x0[3], a);
-                    a = __builtin_fmaf(bf16_lo_to_f32(cur.w[i][2]), x1[0], a);
-                    a = __builtin_fmaf(bf16_hi_to_f32(cur.w[i][2]), x1[1], a);
-                    a = __builtin_fmaf(bf16_lo_to_f32(cur.w[i][3]), x1[2], a);
-                    a = __builtin_fmaf(bf16_hi_to_f32(cur.w[i][3]), x1[3], a);
-                    acc[i][m] = a;
-                }
-            }
-            if (tn == 0) {
-#pragma unroll
-                for (int i = 0; i < P; ++i) {
-                    const int row = g * RG + i * R + seg;
-#pragma unroll
-                    for (int m = 0; m < M; ++m) {
-                        const float v = segment_sum<L>(acc[i][m]);
-                        if (li == 0 && row < N) {
-                            Y[static_cast<size_t>(m) * N + row] = v;
-                            if constexpr (ARGMAX) {
-                                if (v == v) {
-                                    const uint64_t kk = argmax_key(v, static_cast<uint32_t>(row));
-                                    best = kk > best ? kk : best;
-                                }
-                            }
-                        }
-                        acc[i][m] = 0.0f;
-                    }
-                }
-            }
-            g = gn;
-            t = tn;
-            return more;
-        };
-        for (;;) {
-            if (!step(A, B)) break;
-            if (!step(B, A)) break;
+            sums[e] = acc;
         }
+        __syncthreads();
     }
-    if constexpr (ARGMAX) {
+    struct Lane {};
+    __device__ static Lane lane(int) { return Lane{}; }
+    template <int L>
+    __device__ static void load(const uint8_t* row, int li, int t, const Lane&, u32x4* r) {
+        const uint8_t* bp = row + 144 * static_cast<size_t>(li + L * t);
 #pragma unroll
-        for (int off = kWave / 2; off >= 1; off >>= 1) {
-            const uint64_t o = __shfl_xor(best, off, kWave);
-            best = o > best ? o : best;
-        }
-        if (lane == 0 && best != 0) atomicMax(reinterpret_cast<unsigned long long*>(key_out),
-                                              static_cast<unsigned long long>(best));
+        for (int j = 0; j < 9; ++j) r[j] = ld16(bp + 16 * j);
     }
-}
-
-// ---------------------------------------------------------------- Q4_0 --
-// Piece = 8 GGUF blocks = 144 bytes = 256 values, loaded as 9 x 16 bytes.
-
-template <int P>
-struct Q40Regs {
-    u32x4 w[P][9];
-};
-
-template <int L, int P, int M>
-__global__ __launch_bounds__(kBlock) void k_gemv_q4_0(const uint8_t* __restrict__ W,
-                                                      const float* __restrict__ X,
-                                                      float* __restrict__ Y, int N, int K) {
-    extern __shared__ float lds[];
-    constexpr int R = kWave / L;
-    constexpr int RG = R * P;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int li = lane & (L - 1);
-    const int seg = lane / L;
-    const int nb = K >> 8;  // pieces per row
-    const int S = nb / L;
-    const int G = (N + RG - 1) / RG;
-    const int nwaves = gridDim.x * kWavesPerBlock;
-    int g = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-    const size_t row_bytes = static_cast<size_t>(nb) * 144;
-    const uint8_t* Wl = W + static_cast<size_t>(li) * 144;
-
-    auto issue = [&](int gg, int tt, Q40Regs<P>& r) {
-        const uint8_t* base = Wl + static_cast<size_t>(tt) * (144 * L);
-#pragma unroll
-        for (int i = 0; i < P; ++i) {
-            int row = gg * RG + i * R + seg;
-            row = row < N ? row : N - 1;
-            const uint8_t* bp = base + static_cast<size_t>(row) * row_bytes;
-#pragma unroll
-            for (int j = 0; j < 9; ++j) r.w[i][j] = ld16(bp + 16 * j);
-        }
-    };
-
-    Q40Regs<P> A, B;
-    if (g < G) issue(g, 0, A);
-    stage_x<M, true>(lds, X, K);
-    if (g >= G) return;
-    const float* xs = lds;
-    const float* xsum = lds + M * K;
-    float acc[P][M];
-#pragma unroll
-    for (int i = 0; i < P; ++i)
-#pragma unroll
-        for (int m = 0; m < M; ++m) acc[i][m] = 0.0f;
-    int t = 0;
-
-    auto dw = [](const Q40Regs<P>& r, int i, int d) -> uint32_t { return r.w[i][d >> 2][d & 3]; };
-
-    auto step = [&](Q40Regs<P>& cur, Q40Regs<P>& nxt) -> bool {
-        int gn = g, tn = t + 1;
-        if (tn == S) {
-            tn = 0;
-            gn = g + nwaves;
-        }
-        const bool more = gn < G;
-        if (more) issue(gn, tn, nxt);
-        const int kb = 256 * (li + L * t);
+    template <int P>
+    __device__ static uint32_t dw(const u32x4 (&v)[P][kRegs], int i, int d) {
+        return v[i][d >> 2][d & 3];
+    }
+    template <int L, int P, int M>
+    __device__ static void compute(const u32x4 (&v)[P][kRegs], int li, int t, const Lane&,
+                                   const float* xs, const float* xsum, int K, float (&acc)[P][M]) {
+        const int np = K >> 8;
+        const int sp = li + L * t;
 #pragma unroll
         for (int blk = 0; blk < 8; ++blk) {
-            // Block blk: d at byte 18*blk, qs at byte 18*blk + 2.
+            // Block blk: d (f16) at byte 18*blk, qs[16] at byte 18*blk + 2.
             const int ob = 18 * blk;
+            const int oq = ob + 2;
             float d[P];
             uint32_t q[P][4];
 #pragma unroll
             for (int i = 0; i < P; ++i) {
-                d[i] = f16_bits_to_f32((dw(cur, i, ob >> 2) >> (8 * (ob & 3))) & 0xffffu);
-                const int oq = ob + 2;
-                if ((oq & 3) == 0) {
+                d[i] = f16_bits_to_f32((dw<P>(v, i, ob >> 2) >> (8 * (ob & 3))) & 0xffffu);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) q[i][j] = dw(cur, i, (oq >> 2) + j);
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        q[i][j] = __builtin_amdgcn_alignbyte(dw(cur, i, (oq >> 2) + j + 1),
-                                                             dw(cur, i, (oq >> 2) + j), 2);
+                for (int j = 0; j < 4; ++j) {
+                    if ((oq & 3) == 0)
+                        q[i][j] = dw<P>(v, i, (oq >> 2) + j);
+                    else
+                        q[i][j] = __builtin_amdgcn_alignbyte(dw<P>(v, i, (oq >> 2) + j + 1),
+                                                             dw<P>(v, i, (oq >> 2) + j), 2);
                 }
             }
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const float* xm = xs + m * K + kb + 32 * blk;
+                const f32x4* xm = reinterpret_cast<const f32x4*>(xs) + (m * 64 + 8 * blk) * np + sp;
                 f32x4 xl[4], xh[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    xl[j] = reinterpret_cast<const f32x4*>(xm)[j];
-                    xh[j] = reinterpret_cast<const f32x4*>(xm + 16)[j];
+                    xl[j] = xm[j * np];
+                    xh[j] = xm[(j + 4) * np];
                 }
-                const int go = m * (K >> 4) + ((kb + 32 * blk) >> 4);
-                const float s32 = xsum[go] + xsum[go + 1];
+                const float s32 = xsum[(m * 8 + blk) * np + sp];
 #pragma unroll
                 for (int i = 0; i < P; ++i) {
                     float dot = 0.0f;
@@ -427,25 +316,104 @@ __global__ __launch_bounds__(kBlock) void k_gemv_q4_0(const uint8_t* __restrict_
                 }
             }
         }
-        if (tn == 0) {
+    }
+};
+
+// ------------------------------------------------------------- driver --
+
+template <class F, int L, int P, int M, int D, bool ARGMAX>
+__global__ __launch_bounds__(kBlock) void k_gemv(const uint8_t* __restrict__ W,
+                                                 const float* __restrict__ X,
+                                                 float* __restrict__ Y, int N, int K,
+                                                 uint64_t* __restrict__ key_out) {
+    extern __shared__ float lds[];
+    constexpr int R = kWave / L;
+    constexpr int RG = R * P;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int li = lane & (L - 1);
+    const int seg = lane / L;
+    const int S = F::pieces_per_row(K) / L;
+    const int G = (N + RG - 1) / RG;
+    const int nwaves = gridDim.x * kWavesPerBlock;
+    const int g0 = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const size_t rb = F::row_bytes(K);
+    const typename F::Lane ln = F::lane(li);
+
+    u32x4 ring[D][P][F::kRegs];
+
+    // Issue cursor: the next (row group, piece) whose loads go out.
+    int ig = g0, it = 0;
+    // Loads are unconditional (a finished wave re-reads row N-1, in
+    // bounds): a conditional load would make the compiler merge register
+    // versions at every branch and drain the pipeline there.
+    auto issue = [&](u32x4 (&slot)[P][F::kRegs]) {
 #pragma unroll
-            for (int i = 0; i < P; ++i) {
-                const int row = g * RG + i * R + seg;
+        for (int i = 0; i < P; ++i) {
+            int row = ig * RG + i * R + seg;
+            row = row < N ? row : N - 1;
+            F::template load<L>(W + static_cast<size_t>(row) * rb, li, it, ln, slot[i]);
+        }
+        if (++it == S) {
+            it = 0;
+            ig += nwaves;
+        }
+    };
+
 #pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    const float v = segment_sum<L>(acc[i][m]);
-                    if (li == 0 && row < N) Y[static_cast<size_t>(m) * N + row] = v;
-                    acc[i][m] = 0.0f;
+    for (int j = 0; j < D; ++j) issue(ring[j]);
+    F::template stage<M>(lds, X, K, threadIdx.x, kBlock);
+
+    uint64_t best = 0;
+    if (g0 < G) {
+        const float* xs = lds;
+        const float* xsum = lds + static_cast<size_t>(M) * K;
+        float acc[P][M];
+#pragma unroll
+        for (int i = 0; i < P; ++i)
+#pragma unroll
+            for (int m = 0; m < M; ++m) acc[i][m] = 0.0f;
+        int cg = g0, ct = 0;
+        for (;;) {
+#pragma unroll
+            for (int j = 0; j < D; ++j) {
+                F::template compute<L, P, M>(ring[j], li, ct, ln, xs, xsum, K, acc);
+                issue(ring[j]);
+                if (++ct == S) {
+#pragma unroll
+                    for (int i = 0; i < P; ++i) {
+                        const int row = cg * RG + i * R + seg;
+#pragma unroll
+                        for (int m = 0; m < M; ++m) {
+                            const float val = segment_sum<L>(acc[i][m]);
+                            acc[i][m] = 0.0f;
+                            if (li == 0 && row < N) {
+                                Y[static_cast<size_t>(m) * N + row] = val;
+                                if constexpr (ARGMAX) {
+                                    if (val == val) {
+                                        const uint64_t kk = argmax_key(val, static_cast<uint32_t>(row));
+                                        best = kk > best ? kk : best;
+                                    }
+                                }
+                            }
+                        }
+                    }
+                    ct = 0;
+                    cg += nwaves;
+                    if (cg >= G) goto done;
                 }
             }
         }
-        g = gn;
-        t = tn;
-        return more;
-    };
-    for (;;) {
-        if (!step(A, B)) break;
-        if (!step(B, A)) break;
+    }
+done:
+    if constexpr (ARGMAX) {
+#pragma unroll
+        for (int off = kWave / 2; off >= 1; off >>= 1) {
+            const uint64_t o = __shfl_xor(best, off, kWave);
+            best = o > best ? o : best;
+        }
+        if (lane == 0 && best != 0)
+            atomicMax(reinterpret_cast<unsigned long long*>(key_out),
+                      static_cast<unsigned long long>(best));
     }
 }
 
@@ -457,6 +425,8 @@ int lowbit_pow2_capped(int64_t v, int cap) {
     return l;
 }
 
+// Rows per lane: more rows per lane shares activation reads and deepens the
+// pipeline, but needs enough row groups to occupy every SIMD.
 int pick_p(int64_t n, int R, int cus, int pmax) {
     const int64_t target = static_cast<int64_t>(cus) * 8;
     if (pmax >= 4 && (n + 4 * R - 1) / (4 * R) >= target) return 4;
@@ -464,155 +434,100 @@ int pick_p(int64_t n, int R, int cus, int pmax) {
     return 1;
 }
 
-dim3 grid_for(int64_t n, int rows_per_wave, int cus) {
-    const int64_t waves = (n + rows_per_wave - 1) / rows_per_wave;
-    int64_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int64_t cap = static_cast<int64_t>(cus) * 8;
+template <class F, int L, int P, int M, int D, bool AM>
+hipError_t run(const void* w, const float* x, float* y, int64_t n, int64_t k, uint64_t* key,
+               hipStream_t s, int fmt) {
+    constexpr int RG = (kWave / L) * P;
+    const size_t lds = gemv_lds_bytes(fmt, M, k);
+    const int64_t groups = (n + RG - 1) / RG;
+    int64_t blocks = (groups + kWavesPerBlock - 1) / kWavesPerBlock;
+    const int64_t cap = static_cast<int64_t>(device_info().cus) * 4;
     if (blocks > cap) blocks = cap;
-    return dim3(static_cast<unsigned>(blocks));
-}
-
-template <int L, int P, int M>
-hipError_t run_q4k(const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t s) {
-    const size_t lds = gemv_lds_bytes(RT_HIP_Q4K, M, k);
-    const dim3 grid = grid_for(n, (kWave / L) * P, device_info().cus);
-    hipLaunchKernelGGL((k_gemv_q4k<L, P, M>), grid, dim3(kBlock), lds, s,
-                       static_cast<const uint8_t*>(w), x, y, static_cast<int>(n),
-                       static_cast<int>(k));
-    return hipGetLastError();
-}
-
-template <int L, int P, int M, bool AM>
-hipError_t run_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
-                    uint64_t* key, hipStream_t s) {
-    const size_t lds = gemv_lds_bytes(RT_HIP_BF16, M, k);
-    const dim3 grid = grid_for(n, (kWave / L) * P, device_info().cus);
-    hipLaunchKernelGGL((k_gemv_bf16<L, P, M, AM>), grid, dim3(kBlock), lds, s, w, x, y,
+    hipLaunchKernelGGL((k_gemv<F, L, P, M, D, AM>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kBlock), lds, s, static_cast<const uint8_t*>(w), x, y,
                        static_cast<int>(n), static_cast<int>(k), key);
     return hipGetLastError();
 }
 
-template <int L, int P, int M>
-hipError_t run_q40(const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t s) {
-    const size_t lds = gemv_lds_bytes(RT_HIP_Q4_0, M, k);
-    const dim3 grid = grid_for(n, (kWave / L) * P, device_info().cus);
-    hipLaunchKernelGGL((k_gemv_q4_0<L, P, M>), grid, dim3(kBlock), lds, s,
-                       static_cast<const uint8_t*>(w), x, y, static_cast<int>(n),
-                       static_cast<int>(k));
-    return hipGetLastError();
-}
+// Per-format pipeline depth (pieces in flight per slot ring) for M == 1.
+template <class F> struct Depth;
+template <> struct Depth<Q4kFmt> { static constexpr int D = 4; };
+template <> struct Depth<Bf16Fmt> { static constexpr int D = 8; };
+template <> struct Depth<Q40Fmt> { static constexpr int D = 2; };
 
-template <int L>
-hipError_t q4k_for_l(const void* w, const float* x, float* y, int64_t n, int64_t k, int m,
-                     hipStream_t s) {
+template <class F, int L, bool AM>
+hipError_t for_l(const void* w, const float* x, float* y, int64_t n, int64_t k, int m,
+                 uint64_t* key, hipStream_t s, int fmt) {
+    constexpr int D = Depth<F>::D;
+    constexpr int DB = D > 2 ? D / 2 : D;  // batched rows carry M accumulators
+    constexpr int PMAX = F::kRegs > 2 ? 1 : (F::kRegs == 2 ? 2 : 4);
     if (m == 1) {
-        const int p = pick_p(n, kWave / L, device_info().cus, 4);
-        if (p == 4) return run_q4k<L, 4, 1>(w, x, y, n, k, s);
-        if (p == 2) return run_q4k<L, 2, 1>(w, x, y, n, k, s);
-        return run_q4k<L, 1, 1>(w, x, y, n, k, s);
-    }
-    switch (m) {
-        case 2: return run_q4k<L, 1, 2>(w, x, y, n, k, s);
-        case 3: return run_q4k<L, 1, 3>(w, x, y, n, k, s);
-        case 4: return run_q4k<L, 1, 4>(w, x, y, n, k, s);
-        case 5: return run_q4k<L, 1, 5>(w, x, y, n, k, s);
-        case 6: return run_q4k<L, 1, 6>(w, x, y, n, k, s);
-        case 7: return run_q4k<L, 1, 7>(w, x, y, n, k, s);
-        case 8: return run_q4k<L, 1, 8>(w, x, y, n, k, s);
-        default: return hipErrorInvalidValue;
-    }
-}
-
-template <int L>
-hipError_t bf16_for_l(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k, int m,
-                      uint64_t* key, hipStream_t s) {
-    if (m == 1) {
-        const int p = pick_p(n, kWave / L, device_info().cus, 4);
-        if (key) {
-            if (p == 4) return run_bf16<L, 4, 1, true>(w, x, y, n, k, key, s);
-            if (p == 2) return run_bf16<L, 2, 1, true>(w, x, y, n, k, key, s);
-            return run_bf16<L, 1, 1, true>(w, x, y, n, k, key, s);
+        const int p = pick_p(n, kWave / L, device_info().cus, PMAX);
+        if constexpr (AM) {
+            if (key) {
+                if (p == 4) return run<F, L, 4, 1, D, true>(w, x, y, n, k, key, s, fmt);
+                if (p == 2) return run<F, L, 2, 1, D, true>(w, x, y, n, k, key, s, fmt);
+                return run<F, L, 1, 1, D, true>(w, x, y, n, k, key, s, fmt);
+            }
         }
-        if (p == 4) return run_bf16<L, 4, 1, false>(w, x, y, n, k, nullptr, s);
-        if (p == 2) return run_bf16<L, 2, 1, false>(w, x, y, n, k, nullptr, s);
-        return run_bf16<L, 1, 1, false>(w, x, y, n, k, nullptr, s);
+        if constexpr (PMAX >= 4)
+            if (p == 4) return run<F, L, 4, 1, D, false>(w, x, y, n, k, key, s, fmt);
+        if constexpr (PMAX >= 2)
+            if (p == 2) return run<F, L, 2, 1, D, false>(w, x, y, n, k, key, s, fmt);
+        return run<F, L, 1, 1, D, false>(w, x, y, n, k, key, s, fmt);
     }
     switch (m) {
-        case 2: return run_bf16<L, 1, 2, false>(w, x, y, n, k, nullptr, s);
-        case 3: return run_bf16<L, 1, 3, false>(w, x, y, n, k, nullptr, s);
-        case 4: return run_bf16<L, 1, 4, false>(w, x, y, n, k, nullptr, s);
-        case 5: return run_bf16<L, 1, 5, false>(w, x, y, n, k, nullptr, s);
-        case 6: return run_bf16<L, 1, 6, false>(w, x, y, n, k, nullptr, s);
-        case 7: return run_bf16<L, 1, 7, false>(w, x, y, n, k, nullptr, s);
-        case 8: return run_bf16<L, 1, 8, false>(w, x, y, n, k, nullptr, s);
+        case 2: return run<F, L, 1, 2, DB, false>(w, x, y, n, k, nullptr, s, fmt);
+        case 3: return run<F, L, 1, 3, DB, false>(w, x, y, n, k, nullptr, s, fmt);
+        case 4: return run<F, L, 1, 4, DB, false>(w, x, y, n, k, nullptr, s, fmt);
+        case 5: return run<F, L, 1, 5, DB, false>(w, x, y, n, k, nullptr, s, fmt);
+        case 6: return run<F, L, 1, 6, DB, false>(w, x, y, n, k, nullptr, s, fmt);
+        case 7: return run<F, L, 1, 7, DB, false>(w, x, y, n, k, nullptr, s, fmt);
+        case 8: return run<F, L, 1, 8, DB, false>(w, x, y, n, k, nullptr, s, fmt);
         default: return hipErrorInvalidValue;
     }
 }
 
-template <int L>
-hipError_t q40_for_l(const void* w, const float* x, float* y, int64_t n, int64_t k, int m,
-                     hipStream_t s) {
-    if (m == 1) {
-        const int p = pick_p(n, kWave / L, device_info().cus, 2);
-        if (p >= 2) return run_q40<L, 2, 1>(w, x, y, n, k, s);
-        return run_q40<L, 1, 1>(w, x, y, n, k, s);
+template <class F, int LMIN, bool AM>
+hipError_t dispatch(const void* w, const float* x, float* y, int64_t n, int64_t k, int m,
+                    uint64_t* key, hipStream_t s, int fmt) {
+    switch (lowbit_pow2_capped(F::pieces_per_row(static_cast<int>(k)), kWave)) {
+        case 1: if constexpr (LMIN <= 1) return for_l<F, 1, AM>(w, x, y, n, k, m, key, s, fmt); break;
+        case 2: if constexpr (LMIN <= 2) return for_l<F, 2, AM>(w, x, y, n, k, m, key, s, fmt); break;
+        case 4: if constexpr (LMIN <= 4) return for_l<F, 4, AM>(w, x, y, n, k, m, key, s, fmt); break;
+        case 8: return for_l<F, 8, AM>(w, x, y, n, k, m, key, s, fmt);
+        case 16: return for_l<F, 16, AM>(w, x, y, n, k, m, key, s, fmt);
+        case 32: return for_l<F, 32, AM>(w, x, y, n, k, m, key, s, fmt);
+        default: return for_l<F, 64, AM>(w, x, y, n, k, m, key, s, fmt);
     }
-    switch (m) {
-        case 2: return run_q40<L, 1, 2>(w, x, y, n, k, s);
-        case 3: return run_q40<L, 1, 3>(w, x, y, n, k, s);
-        case 4: return run_q40<L, 1, 4>(w, x, y, n, k, s);
-        case 5: return run_q40<L, 1, 5>(w, x, y, n, k, s);
-        case 6: return run_q40<L, 1, 6>(w, x, y, n, k, s);
-        case 7: return run_q40<L, 1, 7>(w, x, y, n, k, s);
-        case 8: return run_q40<L, 1, 8>(w, x, y, n, k, s);
-        default: return hipErrorInvalidValue;
-    }
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
 
 size_t gemv_lds_bytes(int fmt, int m, int64_t k) {
-    const size_t xs = static_cast<size_t>(m) * static_cast<size_t>(k) * 4;
-    return fmt == RT_HIP_BF16 ? xs : xs + xs / 16;
+    const int kk = static_cast<int>(k);
+    switch (fmt) {
+        case RT_HIP_Q4K: return 4 * Q4kFmt::lds_floats(m, kk);
+        case RT_HIP_BF16: return 4 * Bf16Fmt::lds_floats(m, kk);
+        default: return 4 * Q40Fmt::lds_floats(m, kk);
+    }
 }
 
 hipError_t launch_gemv_q4k(const void* w, const float* x, float* y, int64_t n, int64_t k, int m,
                            hipStream_t s) {
-    const int l = lowbit_pow2_capped((k / 256) * 8, kWave);
-    switch (l) {
-        case 8: return q4k_for_l<8>(w, x, y, n, k, m, s);
-        case 16: return q4k_for_l<16>(w, x, y, n, k, m, s);
-        case 32: return q4k_for_l<32>(w, x, y, n, k, m, s);
-        default: return q4k_for_l<64>(w, x, y, n, k, m, s);
-    }
+    // Q4_K pieces per row = 8 * K/256, so L >= 8 always.
+    return dispatch<Q4kFmt, 8, false>(w, x, y, n, k, m, nullptr, s, RT_HIP_Q4K);
 }
 
 hipError_t launch_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
                             int m, uint64_t* key, hipStream_t s) {
-    const int l = lowbit_pow2_capped(k / 8, kWave);
-    switch (l) {
-        case 1: return bf16_for_l<1>(w, x, y, n, k, m, key, s);
-        case 2: return bf16_for_l<2>(w, x, y, n, k, m, key, s);
-        case 4: return bf16_for_l<4>(w, x, y, n, k, m, key, s);
-        case 8: return bf16_for_l<8>(w, x, y, n, k, m, key, s);
-        case 16: return bf16_for_l<16>(w, x, y, n, k, m, key, s);
-        case 32: return bf16_for_l<32>(w, x, y, n, k, m, key, s);
-        default: return bf16_for_l<64>(w, x, y, n, k, m, key, s);
-    }
+    return dispatch<Bf16Fmt, 1, true>(w, x, y, n, k, m, key, s, RT_HIP_BF16);
 }
 
 hipError_t launch_gemv_q4_0(const void* w, const float* x, float* y, int64_t n, int64_t k, int m,
                             hipStream_t s) {
-    const int l = lowbit_pow2_capped(k / 256, kWave);
-    switch (l) {
-        case 1: return q40_for_l<1>(w, x, y, n, k, m, s);
-        case 2: return q40_for_l<2>(w, x, y, n, k, m, s);
-        case 4: return q40_for_l<4>(w, x, y, n, k, m, s);
-        case 8: return q40_for_l<8>(w, x, y, n, k, m, s);
-        case 16: return q40_for_l<16>(w, x, y, n, k, m, s);
-        case 32: return q40_for_l<32>(w, x, y, n, k, m, s);
-        default: return q40_for_l<64>(w, x, y, n, k, m, s);
-    }
+    return dispatch<Q40Fmt, 1, false>(w, x, y, n, k, m, nullptr, s, RT_HIP_Q4_0);
 }
 
 }  // namespace rt_hip
