@@ -78,6 +78,16 @@ int rt_hip_init(int ordinal);
 int rt_hip_gemv_q4k(const void* blocks, const float* x, float* y, int64_t n, int64_t k,
                     int32_t m, rt_hip_stream stream);
 
+/* Up to RT_HIP_MULTI_MAX Q4_K GEMVs (M == 1) that read the same x and K, in
+ * one launch: y[j] = x * W[j]^T for j < count.  A layer's q/k/v or gate/up.
+ * blocks, y and n are host arrays of device pointers / row counts.
+ * Replace: the engine's back-to-back dispatch_gemv calls on one activation
+ * (src/metal_decode.mm:448-450, 472-473), which the reference issues as
+ * separate dispatches inside one command buffer. */
+#define RT_HIP_MULTI_MAX 4
+int rt_hip_gemv_q4k_multi(int32_t count, const void* const* blocks, float* const* y,
+                          const int64_t* n, const float* x, int64_t k, rt_hip_stream stream);
+
 /* Replace: MatBf16::matmul_by_t for M <= 8 (src/mat.cpp:318-414); Metal
  * metal_gemv_bf16_t (metal_ops.hpp:64-65) and gemv_bf16_t / _batch
  * (decode_gemma3.msl:390-518).  Requires K % 8 == 0. */

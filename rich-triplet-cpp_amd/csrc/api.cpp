@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -114,6 +115,19 @@ const DeviceInfo& device_info() {
     return st ? st->info : fallback;
 }
 
+int tune_param(const char* name, int fallback) {
+    static std::mutex mu;
+    static std::vector<std::pair<std::string, int>> cache;
+    std::lock_guard<std::mutex> lk(mu);
+    for (const auto& kv : cache)
+        if (kv.first == name) return kv.second;
+    int v = fallback;
+    const std::string env = std::string("RT_HIP_") + name;
+    if (const char* s = std::getenv(env.c_str())) v = std::atoi(s);
+    cache.emplace_back(name, v);
+    return v;
+}
+
 void* workspace(size_t bytes, hipError_t* err) {
     DeviceState* st = state_for_current(err);
     if (!st) return nullptr;
@@ -172,6 +186,21 @@ int rt_hip_gemv_q4k(const void* blocks, const float* x, float* y, int64_t n, int
                             return launch_gemv_q4k(blocks, xx, yy, n, k, mm,
                                                    static_cast<hipStream_t>(stream));
                         });
+}
+
+int rt_hip_gemv_q4k_multi(int32_t count, const void* const* blocks, float* const* y,
+                          const int64_t* n, const float* x, int64_t k, rt_hip_stream stream) {
+    if (count < 1 || count > RT_HIP_MULTI_MAX || !blocks || !y || !n)
+        return fail(RT_HIP_E_ARG, "rt_hip_gemv_q4k_multi: count must be in [1, 4] with arrays");
+    for (int32_t j = 0; j < count; ++j) {
+        int rc = gemv_args("rt_hip_gemv_q4k_multi", blocks[j], x, y[j], n[j], k, 1, 256);
+        if (rc) return rc;
+    }
+    if (gemv_lds_bytes(RT_HIP_Q4K, 1, k) > 65536)
+        return fail(RT_HIP_E_SHAPE, "rt_hip_gemv_q4k_multi: k too large");
+    return check_stream_launch(launch_gemv_q4k_mfma_multi(count, blocks, y, n, x, k,
+                                                          static_cast<hipStream_t>(stream)),
+                               "rt_hip_gemv_q4k_multi");
 }
 
 int rt_hip_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,

@@ -1,0 +1,167 @@
+// q4k_mfma.hpp -- Q4_K x f32 dot products on gfx950 int8 MFMA.
+//
+// The f32 activation is represented exactly enough to stand in for f32: per
+// 32-value sub-block (the Q4_K sub-block size), a power-of-two scale s
+// (2^(E-5) for the sub-block's absmax exponent E) and three int8 limbs
+//     a = s * (A0 + A1/254 + A2/254^2) + e,   |A0| <= 64, |A1|,|A2| <= 127,
+//     |e| <= 0.5 * s / 254^2 <= 2.5e-7 * absmax.
+// A power-of-two s keeps the one-hot case exact: x = e_k gives A0 = 1/s,
+// A1 = A2 = 0, and the result is the dequantized weight bit-for-bit.
+//
+// v_mfma_i32_16x16x64_i8 computes C[16x16] += A[16x64] * B[64x16] exactly in
+// int32.  For a 16-row weight tile, lane l = (n = l%16, g = l/16) supplies
+// column n of B: 16 nibble bytes of chunk g of row n's super-block (sub-block
+// 2g from the low nibbles, 2g+1 from the high ones).  Row m = 4*gm + lambda
+// of A is nonzero only in the K-slots of lane group gm, where it holds limb
+// lambda of the matching activations.  The hardware leaves lane l holding
+// C[4g + r][n], r = 0..3, i.e. exactly the three limb dots of its own
+// sub-block for its own row -- no cross-lane traffic before the epilogue.
+//
+// Exactness of the integer part: |C| <= 32 * 15 * 127 < 2^24, so the int32
+// sums and their f32 conversions are exact; the only roundings are the
+// epilogue's f32 operations.
+#pragma once
+
+#include "rt_common.hpp"
+
+namespace rt_hip {
+namespace q4k_mfma {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// LDS layout of one staged activation vector of length K (K % 256 == 0):
+//   [0, 3K)            limb planes lambda = 0, 1, 2 (int8, K bytes each)
+//   [3K, 3K + 64)      zeros (the A operand of inactive lanes)
+//   [3K + 64, ...)     per sub-block f32x4 {s, s/254, s/254^2, sum}
+__host__ __device__ inline size_t lds_bytes(int K) {
+    return 3 * static_cast<size_t>(K) + 64 + static_cast<size_t>(K / 32) * 16;
+}
+
+// Limbs of 4 activations (one f32x4) of a sub-block whose 8 holders are the
+// aligned 8-lane group of the calling lane.  Writes the limb bytes and, from
+// the group's first lane, the sub-block constants.
+__device__ __forceinline__ void limbs_of(const f32x4 v, uint8_t* lds, int K, int f) {
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    float sum = (v[0] + v[1]) + (v[2] + v[3]);
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+        sum += __shfl_xor(sum, off, kWave);
+    }
+    // s = 2^(E-5), E = unbiased exponent of amax; zero (or subnormal-range)
+    // sub-blocks get s = 0 and zero limbs.
+    // An Inf/NaN activation makes s non-finite so the output is NaN/Inf,
+    // as the reference's f32 arithmetic would make it.
+    const uint32_t eb = (__float_as_uint(amax) >> 23) & 0xffu;
+    const bool live = eb > 6 && eb < 0xff;
+    const float s = live ? __uint_as_float((eb - 5u) << 23) : (eb == 0xff ? amax : 0.0f);
+    const float inv = live ? __uint_as_float((254u - (eb - 5u)) << 23) : 0.0f;
+    uint32_t w0 = 0, w1 = 0, w2 = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float r = v[e] * inv;  // exact: power-of-two scaling
+        const float a0 = __builtin_rintf(r);
+        const float r1 = (r - a0) * 254.0f;
+        const float a1 = __builtin_rintf(r1);
+        const float a2 = __builtin_rintf((r1 - a1) * 254.0f);
+        w0 |= (static_cast<uint32_t>(static_cast<int>(a0)) & 0xffu) << (8 * e);
+        w1 |= (static_cast<uint32_t>(static_cast<int>(a1)) & 0xffu) << (8 * e);
+        w2 |= (static_cast<uint32_t>(static_cast<int>(a2)) & 0xffu) << (8 * e);
+    }
+    uint32_t* l32 = reinterpret_cast<uint32_t*>(lds);
+    l32[f] = w0;
+    l32[(K >> 2) + f] = w1;
+    l32[(K >> 1) + f] = w2;
+    if ((f & 7) == 0) {
+        f32x4* cst = reinterpret_cast<f32x4*>(lds + 3 * static_cast<size_t>(K) + 64);
+        cst[f >> 3] = f32x4{s, s * (1.0f / 254.0f), s * (1.0f / 64516.0f), sum};
+    }
+}
+
+// Per-lane constants of the tile layout.
+struct Lane {
+    int n, g;          // weight row within the tile, chunk / C row group
+    uint32_t a_base;   // LDS byte offset of this lane's A operand (block 0)
+    uint32_t a_mask;   // 0 for inactive A lanes (they read the zero area)
+    uint32_t cst_base; // LDS byte offset of the constants of sub-block 2g
+    uint32_t hmask;    // ~0 when g >= 2: sub-blocks 4..7 (split 6-bit scale layout)
+};
+
+__device__ __forceinline__ Lane make_lane(int lane, int K) {
+    Lane ln;
+    ln.n = lane & 15;
+    ln.g = lane >> 4;
+    const int m = lane & 15, gm = m >> 2, lambda = m & 3;
+    const bool active = gm == ln.g && lambda < 3;
+    ln.a_base = active ? static_cast<uint32_t>(lambda * K + 64 * ln.g) : static_cast<uint32_t>(3 * K);
+    ln.a_mask = active ? 0xffffffffu : 0u;
+    ln.cst_base = static_cast<uint32_t>(3 * K + 64 + 32 * ln.g);
+    ln.hmask = ln.g >= 2 ? 0xffffffffu : 0u;
+    return ln;
+}
+
+// Registers one lane holds per super-block: its header and its 32-byte chunk.
+struct Blk {
+    u32x4 h, q0, q1;
+};
+
+__device__ __forceinline__ void load_blk(const uint8_t* row, int b, const Lane& ln, Blk& r) {
+    const uint8_t* bp = row + static_cast<size_t>(b) * kQ4kBlockBytes;
+    r.h = ld16(bp);
+    r.q0 = ld16(bp + 16 + 32 * ln.g);
+    r.q1 = ld16(bp + 32 + 32 * ln.g);
+}
+
+// acc += this lane's share (chunk g of block b) of row n's dot product;
+// `lds` is the staged activation (layout above).
+__device__ __forceinline__ float block_dot(const Blk& r, int b, const Lane& ln,
+                                           const uint8_t* lds, float acc) {
+    auto lds_a = [&](uint32_t off) { return *reinterpret_cast<const i32x4*>(lds + off); };
+    auto lds_f4 = [&](uint32_t off) { return *reinterpret_cast<const f32x4*>(lds + off); };
+    // Scales: bytes 2g and 2g+1 of the 6-bit scale/min arrays
+    // (Q4KMat::scale_min, quant_q4k.cpp:58-69), both decoded at once.
+    const uint32_t off = 16u * static_cast<uint32_t>(ln.g & 1);
+    const uint32_t a0 = __builtin_amdgcn_ubfe(r.h[1], off, 16);
+    const uint32_t a1 = __builtin_amdgcn_ubfe(r.h[2], off, 16);
+    const uint32_t a2 = __builtin_amdgcn_ubfe(r.h[3], off, 16);
+    // Both layouts computed, then selected with the lane mask (no branch).
+    const uint32_t sv_lo = a0 & 0x3f3fu, mv_lo = a1 & 0x3f3fu;
+    const uint32_t sv_hi = (a2 & 0x0f0fu) | ((a0 >> 2) & 0x3030u);
+    const uint32_t mv_hi = ((a2 >> 4) & 0x0f0fu) | ((a1 >> 2) & 0x3030u);
+    const uint32_t svp = sv_lo ^ ((sv_lo ^ sv_hi) & ln.hmask);
+    const uint32_t mvp = mv_lo ^ ((mv_lo ^ mv_hi) & ln.hmask);
+    const float d = f16_bits_to_f32(r.h[0] & 0xffffu);
+    const float dm = f16_bits_to_f32(r.h[0] >> 16);
+
+    const uint32_t a_addr = ln.a_base + ((static_cast<uint32_t>(b) << 8) & ln.a_mask);
+    const i32x4 A0 = lds_a(a_addr), A1 = lds_a(a_addr + 16), A2 = lds_a(a_addr + 32),
+                A3 = lds_a(a_addr + 48);
+    const i32x4 B0 = __builtin_bit_cast(i32x4, r.q0 & 0x0f0f0f0fu);
+    const i32x4 B1 = __builtin_bit_cast(i32x4, r.q1 & 0x0f0f0f0fu);
+    const i32x4 B2 = __builtin_bit_cast(i32x4, (r.q0 >> 4) & 0x0f0f0f0fu);
+    const i32x4 B3 = __builtin_bit_cast(i32x4, (r.q1 >> 4) & 0x0f0f0f0fu);
+    const i32x4 z = {0, 0, 0, 0};
+    i32x4 clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, z, 0, 0, 0);
+    clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, clo, 0, 0, 0);
+    i32x4 chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, B2, z, 0, 0, 0);
+    chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A3, B3, chi, 0, 0, 0);
+
+    const uint32_t c_addr = ln.cst_base + (static_cast<uint32_t>(b) << 7);
+    const f32x4 kl = lds_f4(c_addr), kh = lds_f4(c_addr + 16);
+    // dot of the sub-block in activation units: s*C0 + s/254*C1 + s/254^2*C2
+    float dl = static_cast<float>(clo[0]) * kl[0];
+    dl = __builtin_fmaf(static_cast<float>(clo[1]), kl[1], dl);
+    dl = __builtin_fmaf(static_cast<float>(clo[2]), kl[2], dl);
+    float dh = static_cast<float>(chi[0]) * kh[0];
+    dh = __builtin_fmaf(static_cast<float>(chi[1]), kh[1], dh);
+    dh = __builtin_fmaf(static_cast<float>(chi[2]), kh[2], dh);
+    // sum_w x = (d*sv) * dot - (dmin*mv) * sum(x), per sub-block
+    acc = __builtin_fmaf(d * ubyte_f32(svp, 0), dl, acc);
+    acc = __builtin_fmaf(-(dm * ubyte_f32(mvp, 0)), kl[3], acc);
+    acc = __builtin_fmaf(d * ubyte_f32(svp, 1), dh, acc);
+    acc = __builtin_fmaf(-(dm * ubyte_f32(mvp, 1)), kh[3], acc);
+    return acc;
+}
+
+}  // namespace q4k_mfma
+}  // namespace rt_hip

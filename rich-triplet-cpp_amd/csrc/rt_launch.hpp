@@ -17,6 +17,10 @@ struct DeviceInfo {
 };
 const DeviceInfo& device_info();
 
+// Integer tuning knob read once from the environment (RT_HIP_<name>), else
+// `fallback`.  Used for launch-shape sweeps; defaults are the measured best.
+int tune_param(const char* name, int fallback);
+
 // Library-owned device workspace, grown on demand, one per device.
 void* workspace(size_t bytes, hipError_t* err);
 
@@ -25,6 +29,10 @@ size_t gemv_lds_bytes(int fmt, int m, int64_t k);
 
 hipError_t launch_gemv_q4k(const void* w, const float* x, float* y, int64_t n, int64_t k,
                            int m, hipStream_t s);
+hipError_t launch_gemv_q4k_mfma(const void* w, const float* x, float* y, int64_t n, int64_t k,
+                                hipStream_t s);
+hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* const* y,
+                                      const int64_t* n, const float* x, int64_t k, hipStream_t s);
 hipError_t launch_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
                             int m, uint64_t* argmax_key, hipStream_t s);
 hipError_t launch_gemv_q4_0(const void* w, const float* x, float* y, int64_t n, int64_t k,

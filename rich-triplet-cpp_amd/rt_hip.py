@@ -26,6 +26,7 @@ _SIGNATURES = {
     "rt_hip_init": [C.c_int],
     "rt_hip_gemv_q4k": [_vp, _vp, _vp, _i64, _i64, _i32, _vp],
     "rt_hip_gemv_bf16": [_vp, _vp, _vp, _i64, _i64, _i32, _vp],
+    "rt_hip_gemv_q4k_multi": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _i64, _vp],
     "rt_hip_gemv_q4_0": [_vp, _vp, _vp, _i64, _i64, _i32, _vp],
     "rt_hip_argmax": [_vp, _i64, _i64, _vp, _vp, _vp],
     "rt_hip_gemv_bf16_argmax": [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp],
@@ -131,6 +132,20 @@ def gemv(fmt: int, w, x, n: int, k: int, y=None, stream=None):
     name = {Q4K: "rt_hip_gemv_q4k", BF16: "rt_hip_gemv_bf16", Q4_0: "rt_hip_gemv_q4_0"}[fmt]
     library().call(name, _ptr(w), _ptr(x), _ptr(y), n, k, m, _stream(stream))
     return y
+
+
+def gemv_q4k_multi(ws, x, ns, k: int, ys=None, stream=None):
+    """y[j] = x @ W[j]^T for up to 4 Q4_K weights sharing x (one launch)."""
+    torch = _torch()
+    count = len(ws)
+    if ys is None:
+        ys = [torch.empty((1, n), dtype=torch.float32, device=x.device) for n in ns]
+    _dev_check(x, *ws, *ys)
+    wp = (_vp * count)(*[w.data_ptr() for w in ws])
+    yp = (_vp * count)(*[y.data_ptr() for y in ys])
+    npp = (_i64 * count)(*ns)
+    library().call("rt_hip_gemv_q4k_multi", count, wp, yp, npp, _ptr(x), k, _stream(stream))
+    return ys
 
 
 def gemv_bf16_argmax(w, x, n: int, k: int, y=None, stream=None):

@@ -96,6 +96,27 @@ def test_q4k_gemv_linearity_full_size(rt, orc):
     assert normwise_err(from_dev(y12), from_dev(0.5 * y1 + y2)) <= 2 * GEMV_TOL
 
 
+def test_q4k_gemv_multi_matches_single(rt, orc):
+    """q/k/v-style fused launch: each job bit-identical to its single launch
+    (same kernel arithmetic per row) and within tolerance of the oracle."""
+    rng = np.random.default_rng(21)
+    k = 3072
+    ns = [3072, 1024, 1024, 8]
+    blocks = [orc.q4k_quantize((rng.standard_normal((n, k)) * 0.02).astype(np.float32)) for n in ns]
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    dw = [to_dev(b) for b in blocks]
+    dx = to_dev(x)
+    ys = rt.gemv_q4k_multi(dw, dx, ns, k)
+    for j, n in enumerate(ns):
+        y = from_dev(ys[j])
+        y_ref = orc.q4k_matmul_t(blocks[j], n, k, x)
+        assert normwise_err(y, y_ref) <= GEMV_TOL, j
+    ys2 = rt.gemv_q4k_multi(dw[:2], dx, ns[:2], k)
+    for j in range(2):
+        single = from_dev(rt.gemv(rt.Q4K, dw[j], dx, ns[j], k))
+        assert normwise_err(from_dev(ys2[j]), single) <= GEMV_TOL
+
+
 BF16_CASES = [
     (4096, 1152, 1, "lm_head slice (K=1152, 16 lanes per row)"),
     (1024, 3072, 1, "llama v widened to BF16"),
