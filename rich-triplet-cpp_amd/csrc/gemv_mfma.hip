@@ -23,7 +23,6 @@ using namespace q4k_mfma;
 
 constexpr int kThreads = 256;
 constexpr int kMaxJobs = 4;
-constexpr int kXPre = 4;  // f32x4 of x per thread loaded before the weight prologue
 
 // LDS-only workgroup barrier: waits for this wave's LDS traffic, not for its
 // global loads, so the weight pipeline keeps running across it.
@@ -31,139 +30,180 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Job table passed by value: job j owns tiles [tile0[j], tile0[j + 1]).
+// Job table passed by value: job j owns tiles [tile0[j], tile0[j + 1]), the
+// last one up to `total`; unused entries hold `total`.
 struct Jobs {
     const uint8_t* w[kMaxJobs];
     float* y[kMaxJobs];
     int n[kMaxJobs];
-    int tile0[kMaxJobs + 1];
+    int tile0[kMaxJobs];
+    int total;
     int count;
 };
 
-template <int D, int KS>
+// The job table held in scalar registers.  Each field goes through
+// readfirstlane once and is kept as four named values, so that selecting a
+// job is a chain of scalar selects: read from the kernel arguments (or from
+// an array), a job lookup becomes an indexed load and a wait in the middle
+// of the pipeline.
+template <typename T>
+struct Four {
+    T a, b, c, d;
+    __device__ __forceinline__ T operator[](int j) const { return j == 3 ? d : (j == 2 ? c : (j == 1 ? b : a)); }
+};
+
+__device__ __forceinline__ int sreg(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ uint64_t sreg(const void* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v >> 32)));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+struct SJobs {
+    Four<uint64_t> w, y;
+    Four<int> n, tile0;
+    int count;
+};
+
+__device__ __forceinline__ SJobs to_sregs(const Jobs& j) {
+    static_assert(kMaxJobs == 4, "SJobs holds four jobs");
+    SJobs s;
+    s.w = {sreg(j.w[0]), sreg(j.w[1]), sreg(j.w[2]), sreg(j.w[3])};
+    s.y = {sreg(j.y[0]), sreg(j.y[1]), sreg(j.y[2]), sreg(j.y[3])};
+    s.n = {sreg(j.n[0]), sreg(j.n[1]), sreg(j.n[2]), sreg(j.n[3])};
+    s.tile0 = {sreg(j.tile0[0]), sreg(j.tile0[1]), sreg(j.tile0[2]), sreg(j.tile0[3])};
+    s.count = sreg(j.count);
+    return s;
+}
+
+template <int D, int KS, int XP>
 __global__ __launch_bounds__(kThreads) void k_gemv_q4k_mfma(const Jobs jobs,
                                                             const float* __restrict__ X, int K) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    constexpr int TPW = 4 / KS;  // tiles per workgroup pass
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int TPW = 4 / KS;  // tiles per workgroup
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nb = K >> 8;
-    const int T = jobs.tile0[jobs.count];
     const int ks = wave % KS, tslot = wave / KS;
     const int bpw = (nb + KS - 1) / KS;
     const int b0 = ks * bpw;
     const int nbw = min(nb, b0 + bpw) - b0;  // >= 1: the host picks KS so every split is non-empty
-    const int passes = (T + TPW * static_cast<int>(gridDim.x) - 1) / (TPW * static_cast<int>(gridDim.x));
     const Lane ln = make_lane(lane, K);
-    const size_t rb = static_cast<size_t>(nb) * kQ4kBlockBytes;
+    const int64_t rb = static_cast<int64_t>(nb) * kQ4kBlockBytes;
+    const uint32_t roff = static_cast<uint32_t>(ln.n * rb);
     const int nx = K >> 2;
     const f32x4* X4 = reinterpret_cast<const f32x4*>(X);
 
-    f32x4 xv[kXPre];
+    // x first: its loads complete before the weight prologue's.
+    f32x4 xv[XP];
 #pragma unroll
-    for (int i = 0; i < kXPre; ++i) {
+    for (int i = 0; i < XP; ++i) {
         const int f = tid + kThreads * i;
         xv[i] = X4[f < nx ? f : 0];
     }
+    __builtin_amdgcn_sched_barrier(0);
 
-    // Tile t -> (job, first row); tiles past the end repeat the last one, so
-    // that the pipeline's look-ahead loads stay in bounds.
-    auto locate = [&](int pass, int& job, int& row0) {
-        int t = (static_cast<int>(blockIdx.x) + pass * static_cast<int>(gridDim.x)) * TPW + tslot;
-        t = t < T ? t : T - 1;
-        job = 0;
-#pragma unroll
-        for (int j = 1; j < kMaxJobs; ++j) job += (j < jobs.count && t >= jobs.tile0[j]) ? 1 : 0;
-        row0 = 16 * (t - jobs.tile0[job]);
-    };
-    auto row_ptr = [&](int pass) {
-        int job, row0;
-        locate(pass, job, row0);
-        int row = row0 + ln.n;
-        row = row < jobs.n[job] ? row : jobs.n[job] - 1;
-        return jobs.w[job] + static_cast<size_t>(row) * rb;
-    };
-    int ip = 0, ib = 0;  // issue cursor: pass, block within this wave's range
-    const uint8_t* iw = row_ptr(0);
-    auto issue = [&](Blk& slot) {
-        load_blk(iw, b0 + ib, ln, slot);
-        if (++ib == nbw) {
-            ib = 0;
-            iw = row_ptr(++ip);
-        }
+    // This wave's tile: job and first row (wave-uniform).  A tile slot past
+    // the last tile belongs to the last job with rows past its end, so its
+    // loads read zeros and it stores nothing.
+    const SJobs sj = to_sregs(jobs);
+    const int t = static_cast<int>(blockIdx.x) * TPW + tslot;
+    const int job = (sj.count > 1 && t >= sj.tile0.b ? 1 : 0) + (sj.count > 2 && t >= sj.tile0.c ? 1 : 0) +
+                    (sj.count > 3 && t >= sj.tile0.d ? 1 : 0);
+    const int row0 = 16 * (t - sj.tile0[job]);
+    const int n_job = sj.n[job];
+    const int64_t off0 = static_cast<int64_t>(row0) * rb + static_cast<int64_t>(b0) * kQ4kBlockBytes;
+    const uint8_t* const tbase = reinterpret_cast<const uint8_t*>(sj.w[job]) + off0;
+    const int64_t tleft = static_cast<int64_t>(n_job) * rb - off0;
+
+    // Block i of the wave's range through a resource based at that block of
+    // the tile's first row; past the range the resource is empty (zeros,
+    // no memory traffic).
+    auto issue = [&](Blk& slot, int i) {
+        const int64_t o = static_cast<int64_t>(i) * kQ4kBlockBytes;
+        load_blk(make_rsrc(tbase + o, i < nbw ? tleft - o : 0), roff, ln, slot);
     };
 
     // The scheduling barriers keep the ring's loads in slot order, so that
     // slot j's data is always the oldest in flight when it is consumed and
-    // the waits stay partial (s_waitcnt vmcnt(3*(D-1))).
+    // the waits stay partial (s_waitcnt vmcnt(3*(D-1))); in the main loop
+    // the barrier sits between decoding a slot and refilling it.
     Blk ring[D];
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-        issue(ring[j]);
+        issue(ring[j], j);
         __builtin_amdgcn_sched_barrier(0);
     }
 
+    // Every lane converts its prefetched values (past the end: a dummy that
+    // is not stored), so the loads are consumed where they were issued.
 #pragma unroll
-    for (int i = 0; i < kXPre; ++i) {
+    for (int i = 0; i < XP; ++i) {
         const int f = tid + kThreads * i;
-        if (f < nx) limbs_of(xv[i], lds, K, f);
+        limbs_of(xv[i], lds, K, f, f < nx);
     }
-    for (int f = tid + kThreads * kXPre; f < nx; f += kThreads) limbs_of(X4[f], lds, K, f);
+    for (int f = tid + kThreads * XP; f < nx; f += kThreads) limbs_of(X4[f], lds, K, f);
     if (tid < 4) reinterpret_cast<u32x4*>(lds + 3 * static_cast<size_t>(K))[tid] = u32x4{0u, 0u, 0u, 0u};
-    float* red = reinterpret_cast<float*>(lds + lds_bytes(K));  // [2][TPW][KS][16]
     lds_barrier();
 
+    // Steady rounds: straight-line, no branch around the ring's loads (a
+    // branch there makes the compiler merge register versions and drain
+    // the pipeline).  Decode slot j, refill it with block i + D + j, then
+    // compute: once decoded its registers are free, so the refill needs no
+    // copy.  The tail consumes the last <= D blocks and issues nothing.
     float acc = 0.0f;
-    int pc = 0, bc = 0;  // compute cursor
-    for (;;) {
+    int i = 0;
+    for (; i + D < nbw; i += D) {
 #pragma unroll
         for (int j = 0; j < D; ++j) {
-            acc = block_dot(ring[j], b0 + bc, ln, lds, acc);
-            issue(ring[j]);
+            const Dec dc = decode(ring[j], ln);
             __builtin_amdgcn_sched_barrier(0);
-            if (++bc == nbw) {
-                // Row n's partial: sum the four chunk lanes g.
-                float v = acc;
-                v += __shfl_xor(v, 16, kWave);
-                v += __shfl_xor(v, 32, kWave);
-                acc = 0.0f;
-                const int t = (static_cast<int>(blockIdx.x) + pc * static_cast<int>(gridDim.x)) * TPW + tslot;
-                int job, row0;
-                locate(pc, job, row0);
-                const int row = row0 + ln.n;
-                const bool keep = t < T && row < jobs.n[job];
-                if constexpr (KS == 1) {
-                    if (lane < 16 && keep) jobs.y[job][row] = v;
-                } else {
-                    float* rp = red + ((pc & 1) * TPW + tslot) * KS * 16;
-                    if (lane < 16) rp[ks * 16 + lane] = v;
-                    lds_barrier();
-                    if (ks == 0 && lane < 16 && keep) {
-                        float s = rp[lane];
-#pragma unroll
-                        for (int q = 1; q < KS; ++q) s += rp[q * 16 + lane];
-                        jobs.y[job][row] = s;
-                    }
-                }
-                bc = 0;
-                if (++pc == passes) goto done;
-            }
+            issue(ring[j], i + D + j);
+            acc = dot(dc, b0 + i + j, ln, lds, acc);
         }
     }
-done:
-    return;
+#pragma unroll
+    for (int j = 0; j < D; ++j)
+        if (i + j < nbw) acc = dot(decode(ring[j], ln), b0 + i + j, ln, lds, acc);
+
+    // Row n's partial: sum the four chunk lanes g.
+    float v = acc;
+    v += __shfl_xor(v, 16, kWave);
+    v += __shfl_xor(v, 32, kWave);
+    const int row = row0 + ln.n;
+    const bool keep = row < n_job;  // false for tile slots past the last tile
+    float* const yj = reinterpret_cast<float*>(sj.y[job]);
+    if constexpr (KS == 1) {
+        if (lane < 16 && keep) yj[row] = v;
+    } else {
+        float* red = reinterpret_cast<float*>(lds + lds_bytes(K));  // [TPW][KS][16]
+        float* rp = red + tslot * KS * 16;
+        if (lane < 16) rp[ks * 16 + lane] = v;
+        lds_barrier();
+        if (ks == 0 && lane < 16 && keep) {
+            float s = rp[lane];
+#pragma unroll
+            for (int q = 1; q < KS; ++q) s += rp[q * 16 + lane];
+            yj[row] = s;
+        }
+    }
 }
 
-template <int D, int KS>
+template <int D, int KS, int XP>
 hipError_t run(const Jobs& jobs, const float* x, int64_t k, hipStream_t s) {
     constexpr int TPW = 4 / KS;
-    const int64_t tiles = jobs.tile0[jobs.count];
-    int64_t wgs = (tiles + TPW - 1) / TPW;
-    const int64_t cap = static_cast<int64_t>(device_info().cus) * tune_param("Q4K_WGS_PER_CU", 8);
-    if (wgs > cap) wgs = cap;
-    const size_t lds = lds_bytes(static_cast<int>(k)) + 2 * TPW * KS * 16 * sizeof(float);
-    hipLaunchKernelGGL((k_gemv_q4k_mfma<D, KS>), dim3(static_cast<unsigned>(wgs)), dim3(kThreads),
+    const int64_t wgs = (static_cast<int64_t>(jobs.total) + TPW - 1) / TPW;
+    const size_t lds = lds_bytes(static_cast<int>(k)) + TPW * KS * 16 * sizeof(float);
+    hipLaunchKernelGGL((k_gemv_q4k_mfma<D, KS, XP>), dim3(static_cast<unsigned>(wgs)), dim3(kThreads),
                        lds, s, jobs, x, static_cast<int>(k));
     return hipGetLastError();
+}
+
+// x prefetch depth: all of x (up to K = 8192) before the weight prologue.
+template <int D, int KS>
+hipError_t run_xp(const Jobs& jobs, const float* x, int64_t k, hipStream_t s) {
+    return k > 4 * kThreads * 4 ? run<D, KS, 8>(jobs, x, k, s) : run<D, KS, 4>(jobs, x, k, s);
 }
 
 }  // namespace
@@ -175,25 +215,31 @@ hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* co
     if (count < 1 || count > kMaxJobs) return hipErrorInvalidValue;
     Jobs jobs{};
     jobs.count = count;
-    jobs.tile0[0] = 0;
+    int64_t tiles = 0;
     for (int j = 0; j < count; ++j) {
         jobs.w[j] = static_cast<const uint8_t*>(w[j]);
         jobs.y[j] = y[j];
         jobs.n[j] = static_cast<int>(n[j]);
-        jobs.tile0[j + 1] = jobs.tile0[j] + static_cast<int>((n[j] + 15) / 16);
+        jobs.tile0[j] = static_cast<int>(tiles);
+        tiles += (n[j] + 15) / 16;
     }
-    for (int j = count; j < kMaxJobs; ++j) jobs.tile0[j + 1] = jobs.tile0[count];
-    const int64_t tiles = jobs.tile0[count];
+    for (int j = count; j < kMaxJobs; ++j) {
+        jobs.w[j] = jobs.w[0];
+        jobs.y[j] = jobs.y[0];
+        jobs.n[j] = jobs.n[0];
+        jobs.tile0[j] = static_cast<int>(tiles);
+    }
+    jobs.total = static_cast<int>(tiles);
     const int64_t nb = k / 256;
     const int64_t want = static_cast<int64_t>(device_info().cus) * tune_param("Q4K_WANT_WAVES_PER_CU", 8);
     // every wave of a split must own at least one super-block
     auto splits_ok = [&](int64_t ks) { return (ks - 1) * ((nb + ks - 1) / ks) < nb; };
     const int d = tune_param("Q4K_RING", 4);
     if (tiles >= want || !splits_ok(2))
-        return d == 8 ? run<8, 1>(jobs, x, k, s) : run<4, 1>(jobs, x, k, s);
+        return d == 8 ? run_xp<8, 1>(jobs, x, k, s) : run_xp<4, 1>(jobs, x, k, s);
     if (tiles * 2 >= want || !splits_ok(4))
-        return d == 8 ? run<8, 2>(jobs, x, k, s) : run<4, 2>(jobs, x, k, s);
-    return d == 8 ? run<8, 4>(jobs, x, k, s) : run<4, 4>(jobs, x, k, s);
+        return d == 8 ? run_xp<8, 2>(jobs, x, k, s) : run_xp<4, 2>(jobs, x, k, s);
+    return d == 8 ? run_xp<8, 4>(jobs, x, k, s) : run_xp<4, 4>(jobs, x, k, s);
 }
 
 hipError_t launch_gemv_q4k_mfma(const void* w, const float* x, float* y, int64_t n, int64_t k,

@@ -37,17 +37,35 @@ __host__ __device__ inline size_t lds_bytes(int K) {
     return 3 * static_cast<size_t>(K) + 64 + static_cast<size_t>(K / 32) * 16;
 }
 
+// DPP lane swizzles within a row of 16 lanes (VALU, no LDS round trip).
+constexpr int kDppQuadSwap1 = 0xb1;    // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kDppQuadSwap2 = 0x4e;    // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror: lane i <-> 7 - i in each 8
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum and max over the aligned 8-lane group.  The pairing tree is
+// ((l, l^1), (l^2 pair)), (other quad): every lane of the group ends with
+// the same bits, since each step adds two values in either order.
+__device__ __forceinline__ void group8_sum_max(float& sum, float& amax) {
+    sum += dpp<kDppQuadSwap1>(sum);
+    amax = fmaxf(amax, dpp<kDppQuadSwap1>(amax));
+    sum += dpp<kDppQuadSwap2>(sum);
+    amax = fmaxf(amax, dpp<kDppQuadSwap2>(amax));
+    sum += dpp<kDppHalfMirror>(sum);
+    amax = fmaxf(amax, dpp<kDppHalfMirror>(amax));
+}
+
 // Limbs of 4 activations (one f32x4) of a sub-block whose 8 holders are the
 // aligned 8-lane group of the calling lane.  Writes the limb bytes and, from
-// the group's first lane, the sub-block constants.
-__device__ __forceinline__ void limbs_of(const f32x4 v, uint8_t* lds, int K, int f) {
+// the group's first lane, the sub-block constants; with store == false it
+// only takes part in the group reductions (lanes past the end of x).
+__device__ __forceinline__ void limbs_of(const f32x4 v, uint8_t* lds, int K, int f, bool store = true) {
     float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     float sum = (v[0] + v[1]) + (v[2] + v[3]);
-#pragma unroll
-    for (int off = 1; off < 8; off <<= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
-        sum += __shfl_xor(sum, off, kWave);
-    }
+    group8_sum_max(sum, amax);
     // s = 2^(E-5), E = unbiased exponent of amax; zero (or subnormal-range)
     // sub-blocks get s = 0 and zero limbs.
     // An Inf/NaN activation makes s non-finite so the output is NaN/Inf,
@@ -68,6 +86,7 @@ __device__ __forceinline__ void limbs_of(const f32x4 v, uint8_t* lds, int K, int
         w1 |= (static_cast<uint32_t>(static_cast<int>(a1)) & 0xffu) << (8 * e);
         w2 |= (static_cast<uint32_t>(static_cast<int>(a2)) & 0xffu) << (8 * e);
     }
+    if (!store) return;
     uint32_t* l32 = reinterpret_cast<uint32_t*>(lds);
     l32[f] = w0;
     l32[(K >> 2) + f] = w1;
@@ -112,12 +131,26 @@ __device__ __forceinline__ void load_blk(const uint8_t* row, int b, const Lane& 
     r.q1 = ld16(bp + 32 + 32 * ln.g);
 }
 
-// acc += this lane's share (chunk g of block b) of row n's dot product;
-// `lds` is the staged activation (layout above).
-__device__ __forceinline__ float block_dot(const Blk& r, int b, const Lane& ln,
-                                           const uint8_t* lds, float acc) {
-    auto lds_a = [&](uint32_t off) { return *reinterpret_cast<const i32x4*>(lds + off); };
-    auto lds_f4 = [&](uint32_t off) { return *reinterpret_cast<const f32x4*>(lds + off); };
+// Same, through a buffer resource whose base is super-block b of the tile's
+// first row: `roff` = n * row_bytes, lane's row; rows past the resource's end
+// read as zeros.
+__device__ __forceinline__ void load_blk(BufRsrc rs, uint32_t roff, const Lane& ln, Blk& r) {
+    r.h = ld16(rs, roff);
+    r.q0 = ld16(rs, roff + 16 + 32 * ln.g);
+    r.q1 = ld16(rs, roff + 32 + 32 * ln.g);
+}
+
+// A super-block with its loaded registers already taken apart: the nibble
+// planes as MFMA B operands and this lane's two scales and mins.  Once a
+// block is decoded its load registers are free for the next load.
+struct Dec {
+    i32x4 B0, B1, B2, B3;
+    uint32_t svp, mvp;  // (scale, min) 6-bit values of sub-blocks 2g, 2g+1
+    float d, dm;
+};
+
+__device__ __forceinline__ Dec decode(const Blk& r, const Lane& ln) {
+    Dec o;
     // Scales: bytes 2g and 2g+1 of the 6-bit scale/min arrays
     // (Q4KMat::scale_min, quant_q4k.cpp:58-69), both decoded at once.
     const uint32_t off = 16u * static_cast<uint32_t>(ln.g & 1);
@@ -128,23 +161,33 @@ __device__ __forceinline__ float block_dot(const Blk& r, int b, const Lane& ln,
     const uint32_t sv_lo = a0 & 0x3f3fu, mv_lo = a1 & 0x3f3fu;
     const uint32_t sv_hi = (a2 & 0x0f0fu) | ((a0 >> 2) & 0x3030u);
     const uint32_t mv_hi = ((a2 >> 4) & 0x0f0fu) | ((a1 >> 2) & 0x3030u);
-    const uint32_t svp = sv_lo ^ ((sv_lo ^ sv_hi) & ln.hmask);
-    const uint32_t mvp = mv_lo ^ ((mv_lo ^ mv_hi) & ln.hmask);
-    const float d = f16_bits_to_f32(r.h[0] & 0xffffu);
-    const float dm = f16_bits_to_f32(r.h[0] >> 16);
+    o.svp = sv_lo ^ ((sv_lo ^ sv_hi) & ln.hmask);
+    o.mvp = mv_lo ^ ((mv_lo ^ mv_hi) & ln.hmask);
+    o.d = f16_bits_to_f32(r.h[0] & 0xffffu);
+    o.dm = f16_bits_to_f32(r.h[0] >> 16);
+    o.B0 = __builtin_bit_cast(i32x4, r.q0 & 0x0f0f0f0fu);
+    o.B1 = __builtin_bit_cast(i32x4, r.q1 & 0x0f0f0f0fu);
+    o.B2 = __builtin_bit_cast(i32x4, (r.q0 >> 4) & 0x0f0f0f0fu);
+    o.B3 = __builtin_bit_cast(i32x4, (r.q1 >> 4) & 0x0f0f0f0fu);
+    return o;
+}
 
+// acc += this lane's share (chunk g of block b) of row n's dot product;
+// `lds` is the staged activation (layout above).
+__device__ __forceinline__ float dot(const Dec& r, int b, const Lane& ln, const uint8_t* lds,
+                                     float acc) {
+    auto lds_a = [&](uint32_t off) { return *reinterpret_cast<const i32x4*>(lds + off); };
+    auto lds_f4 = [&](uint32_t off) { return *reinterpret_cast<const f32x4*>(lds + off); };
     const uint32_t a_addr = ln.a_base + ((static_cast<uint32_t>(b) << 8) & ln.a_mask);
     const i32x4 A0 = lds_a(a_addr), A1 = lds_a(a_addr + 16), A2 = lds_a(a_addr + 32),
                 A3 = lds_a(a_addr + 48);
-    const i32x4 B0 = __builtin_bit_cast(i32x4, r.q0 & 0x0f0f0f0fu);
-    const i32x4 B1 = __builtin_bit_cast(i32x4, r.q1 & 0x0f0f0f0fu);
-    const i32x4 B2 = __builtin_bit_cast(i32x4, (r.q0 >> 4) & 0x0f0f0f0fu);
-    const i32x4 B3 = __builtin_bit_cast(i32x4, (r.q1 >> 4) & 0x0f0f0f0fu);
     const i32x4 z = {0, 0, 0, 0};
-    i32x4 clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, z, 0, 0, 0);
-    clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, clo, 0, 0, 0);
-    i32x4 chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, B2, z, 0, 0, 0);
-    chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A3, B3, chi, 0, 0, 0);
+    i32x4 clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, r.B0, z, 0, 0, 0);
+    clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, r.B1, clo, 0, 0, 0);
+    i32x4 chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, r.B2, z, 0, 0, 0);
+    chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A3, r.B3, chi, 0, 0, 0);
+    const float d = r.d, dm = r.dm;
+    const uint32_t svp = r.svp, mvp = r.mvp;
 
     const uint32_t c_addr = ln.cst_base + (static_cast<uint32_t>(b) << 7);
     const f32x4 kl = lds_f4(c_addr), kh = lds_f4(c_addr + 16);

@@ -43,6 +43,21 @@ __device__ __forceinline__ u32x4 ld16(const void* p) {
     return *reinterpret_cast<const u32x4*>(p);
 }
 
+// Raw buffer resource over [base, base + bytes): loads at byte offsets
+// >= bytes return zeros without touching memory.  Word 3 is the gfx9-family
+// raw-buffer format (stride 0, no swizzle).  The range check covers the
+// per-lane offset and the instruction offset, not soffset, so callers move
+// the base rather than pass soffset.
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+__device__ __forceinline__ BufRsrc make_rsrc(const void* base, int64_t bytes) {
+    const uint32_t n = bytes <= 0 ? 0u : (bytes >= 0xffffffffll ? 0xffffffffu : static_cast<uint32_t>(bytes));
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                             static_cast<int>(n), 0x00020000);
+}
+__device__ __forceinline__ u32x4 ld16(BufRsrc r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0));
+}
+
 // Non-temporal 16-byte load for weights that are streamed exactly once.
 __device__ __forceinline__ u32x4 ld16_stream(const void* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
