@@ -60,8 +60,9 @@ def weight_bytes(fmt, n, k, rt):
 class DecodeModel:
     """Synthetic Llama-3.2-3B linear weights and per-GEMV inputs on the GPU."""
 
-    def __init__(self, rt, torch, mix: str, seed: int = 0):
+    def __init__(self, rt, torch, mix: str, layout: str = "tiled", seed: int = 0):
         self.rt, self.torch = rt, torch
+        self.layout = layout
         g = torch.Generator(device="cuda").manual_seed(seed)
         self.gemvs = []  # (name, fmt, w, x, y, n, k)
         dev = "cuda"
@@ -95,8 +96,31 @@ class DecodeModel:
         x_f = torch.randn((1, HIDDEN), generator=g, device=dev)
         self.gemvs.append(("lm_head", rt.Q4K, make(VOCAB, HIDDEN, rt.Q4K), x_f,
                            torch.empty((1, VOCAB), device=dev), VOCAB, HIDDEN))
+        # Tiled copies of the Q4_K weights (a one-time load-time repack; the
+        # row-major blocks stay for the CPU baseline, which needs the
+        # reference's layout).  Only the copies the plan uses are read per token.
+        self.tiled = {}
+        if layout == "tiled":
+            for name, fmt, w, _, _, n, k in self.gemvs:
+                if fmt == rt.Q4K:
+                    self.tiled[name] = rt.q4k_tile(w, n, k)
         self.plan = self.launches()
         torch.cuda.synchronize()
+
+    def q4k_multi(self, item):
+        if self.layout == "tiled":
+            self.rt.gemv_q4k_tiled_multi([self.tiled[gv[0]] for gv in item], item[0][3],
+                                         [gv[5] for gv in item], item[0][6], ys=[gv[4] for gv in item])
+        else:
+            self.rt.gemv_q4k_multi([gv[2] for gv in item], item[0][3], [gv[5] for gv in item],
+                                   item[0][6], ys=[gv[4] for gv in item])
+
+    def one(self, gv):
+        name, fmt, w, x, y, n, k = gv
+        if fmt == self.rt.Q4K and self.layout == "tiled":
+            self.rt.gemv_q4k_tiled(self.tiled[name], x, n, k, y=y)
+        else:
+            self.rt.gemv(fmt, w, x, n, k, y=y)
 
     def bytes_per_token(self) -> int:
         return sum(weight_bytes(f, n, k, self.rt) + 4 * k + 4 * n
@@ -126,15 +150,13 @@ class DecodeModel:
     def step(self):
         for kind, item in self.plan:
             if kind == "multi":
-                self.rt.gemv_q4k_multi([gv[2] for gv in item], item[0][3], [gv[5] for gv in item],
-                                       item[0][6], ys=[gv[4] for gv in item])
+                self.q4k_multi(item)
             else:
-                _, fmt, w, x, y, n, k = item
-                self.rt.gemv(fmt, w, x, n, k, y=y)
+                self.one(item)
 
     def step_unfused(self):
-        for _, fmt, w, x, y, n, k in self.gemvs:
-            self.rt.gemv(fmt, w, x, n, k, y=y)
+        for gv in self.gemvs:
+            self.one(gv)
 
 
 def time_graph(torch, fn, warmup: int, steps: int):
@@ -171,14 +193,13 @@ def dominant_kernel_roofline(rt, torch, model, reps: int = 5):
 
     def run():
         for item in sel:
-            rt.gemv_q4k_multi([gv[2] for gv in item], item[0][3], [gv[5] for gv in item],
-                              item[0][6], ys=[gv[4] for gv in item])
+            model.q4k_multi(item)
 
     ms, _ = time_graph(torch, run, 2, reps)
     per_launch_us = ms * 1e3 / len(sel)
     algo = 2 * q4k_bytes(FFN, HIDDEN) + 4 * HIDDEN + 4 * 2 * FFN
     achieved = algo / (per_launch_us * 1e-6) / 1e9
-    return {"kernel": "k_gemv_q4k_mfma (fused gate+up Q4_K GEMV, 2 x 8192 x 3072)",
+    return {"kernel": f"k_gemv_q4k_mfma (fused gate+up Q4_K GEMV, 2 x 8192 x 3072, {model.layout})",
             "bytes_per_launch": algo, "us_per_launch": per_launch_us,
             "achieved_gbs": achieved}
 
@@ -243,7 +264,7 @@ def cpu_baseline(rt, torch, model, budget_s: float = 12.0):
 
 
 def bench_decode(args, rt, torch):
-    model = DecodeModel(rt, torch, args.mix)
+    model = DecodeModel(rt, torch, args.mix, args.layout)
     nbytes = model.bytes_per_token()
     log(f"[bench] {len(model.gemvs)} GEMVs in {len(model.plan)} launches, "
         f"{nbytes / 1e9:.3f} GB/token ({args.mix})")
@@ -275,7 +296,9 @@ def bench_decode(args, rt, torch):
                    "gemvs_per_token": len(model.gemvs), "bytes_per_token": nbytes,
                    "us_per_token": round(us, 2), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
                    "launches_per_token": len(model.plan),
-                   "launch": "one hipGraph per token; q/k/v and gate/up fused per layer"},
+                   "launch": "one hipGraph per token; q/k/v and gate/up fused per layer",
+                   "q4k_layout": ("tiled (rt_hip_q4k_tile once at load; bit-identical results)"
+                                  if args.layout == "tiled" else "reference row-major blocks")},
         "roofline": roof, "cpu_baseline": cpu,
     }
 
@@ -350,6 +373,9 @@ def main() -> int:
                              "flux"])
     ap.add_argument("--mix", default="q4km", choices=["q4km", "q4k"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--layout", default="tiled", choices=["tiled", "rows"],
+                    help="Q4_K weights tiled once at load (default) or the reference's row-major "
+                         "blocks through rt_hip_gemv_q4k*")
     ap.add_argument("--unfused", action="store_true",
                     help="also time the one-launch-per-GEMV step (stderr)")
     ap.add_argument("--traffic-bytes", type=float, default=None,

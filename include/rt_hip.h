@@ -88,6 +88,29 @@ int rt_hip_gemv_q4k(const void* blocks, const float* x, float* y, int64_t n, int
 int rt_hip_gemv_q4k_multi(int32_t count, const void* const* blocks, float* const* y,
                           const int64_t* n, const float* x, int64_t k, rt_hip_stream stream);
 
+/* Tiled Q4_K layout.  No counterpart in the reference: a one-time,
+ * size-preserving rearrangement of Q4KMat's row-major blocks, made once
+ * when a weight is uploaded to the GPU (where the reference's GPU path
+ * copies the blocks unchanged: upload_linear_detect_type,
+ * src/metal_decode.mm:157-175), so that every load of the M == 1 GEMV reads
+ * contiguous memory.  Each 16-row tile's super-block becomes 2304 bytes in
+ * the GEMV's lane order; the scale/min bytes are re-encoded per lane, the
+ * values are not changed, and GEMV results are bit-identical to
+ * rt_hip_gemv_q4k on the same blocks.
+ * rt_hip_q4k_tiled_bytes: size of the tiled copy (rows rounded up to a
+ * multiple of 16), or -1 for invalid n, k (K % 256 == 0 required).
+ * rt_hip_q4k_tile: device blocks -> device tiled copy (not in place). */
+int64_t rt_hip_q4k_tiled_bytes(int64_t n, int64_t k);
+int rt_hip_q4k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, rt_hip_stream stream);
+
+/* M == 1 Q4_K GEMV on a tiled copy: same contract and results as
+ * rt_hip_gemv_q4k (m == 1) / rt_hip_gemv_q4k_multi.
+ * Replace: as rt_hip_gemv_q4k, for callers that keep weights tiled. */
+int rt_hip_gemv_q4k_tiled(const void* tiled, const float* x, float* y, int64_t n, int64_t k,
+                          rt_hip_stream stream);
+int rt_hip_gemv_q4k_tiled_multi(int32_t count, const void* const* tiled, float* const* y,
+                                const int64_t* n, const float* x, int64_t k, rt_hip_stream stream);
+
 /* Replace: MatBf16::matmul_by_t for M <= 8 (src/mat.cpp:318-414); Metal
  * metal_gemv_bf16_t (metal_ops.hpp:64-65) and gemv_bf16_t / _batch
  * (decode_gemma3.msl:390-518).  Requires K % 8 == 0. */

@@ -199,8 +199,46 @@ int rt_hip_gemv_q4k_multi(int32_t count, const void* const* blocks, float* const
     if (gemv_lds_bytes(RT_HIP_Q4K, 1, k) > 65536)
         return fail(RT_HIP_E_SHAPE, "rt_hip_gemv_q4k_multi: k too large");
     return check_stream_launch(launch_gemv_q4k_mfma_multi(count, blocks, y, n, x, k,
-                                                          static_cast<hipStream_t>(stream)),
+                                                          static_cast<hipStream_t>(stream), false),
                                "rt_hip_gemv_q4k_multi");
+}
+
+int64_t rt_hip_q4k_tiled_bytes(int64_t n, int64_t k) {
+    if (n <= 0 || k <= 0 || k % 256 != 0 || n > 0x7fffffffLL || k > 0x7fffffffLL) return -1;
+    return (n + 15) / 16 * 16 * (k / 256) * 144;
+}
+
+int rt_hip_q4k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, rt_hip_stream stream) {
+    if (!blocks || !tiled) return fail(RT_HIP_E_ARG, "rt_hip_q4k_tile: null pointer");
+    if (rt_hip_q4k_tiled_bytes(n, k) < 0)
+        return fail(RT_HIP_E_SHAPE, "rt_hip_q4k_tile: need n > 0, k > 0, k % 256 == 0, int32 sizes");
+    if (!aligned16(blocks) || !aligned16(tiled))
+        return fail(RT_HIP_E_ALIGN, "rt_hip_q4k_tile: blocks and tiled must be 16-byte aligned");
+    if (blocks == tiled) return fail(RT_HIP_E_ARG, "rt_hip_q4k_tile: in-place tiling is not supported");
+    hipError_t e;
+    if (!state_for_current(&e)) return hip_fail(e, "rt_hip_q4k_tile");
+    return check_stream_launch(launch_q4k_tile(blocks, tiled, n, k, static_cast<hipStream_t>(stream)),
+                               "rt_hip_q4k_tile");
+}
+
+int rt_hip_gemv_q4k_tiled_multi(int32_t count, const void* const* tiled, float* const* y,
+                                const int64_t* n, const float* x, int64_t k, rt_hip_stream stream) {
+    if (count < 1 || count > RT_HIP_MULTI_MAX || !tiled || !y || !n)
+        return fail(RT_HIP_E_ARG, "rt_hip_gemv_q4k_tiled_multi: count must be in [1, 4] with arrays");
+    for (int32_t j = 0; j < count; ++j) {
+        int rc = gemv_args("rt_hip_gemv_q4k_tiled_multi", tiled[j], x, y[j], n[j], k, 1, 256);
+        if (rc) return rc;
+    }
+    if (gemv_lds_bytes(RT_HIP_Q4K, 1, k) > 65536)
+        return fail(RT_HIP_E_SHAPE, "rt_hip_gemv_q4k_tiled_multi: k too large");
+    return check_stream_launch(launch_gemv_q4k_mfma_multi(count, tiled, y, n, x, k,
+                                                          static_cast<hipStream_t>(stream), true),
+                               "rt_hip_gemv_q4k_tiled_multi");
+}
+
+int rt_hip_gemv_q4k_tiled(const void* tiled, const float* x, float* y, int64_t n, int64_t k,
+                          rt_hip_stream stream) {
+    return rt_hip_gemv_q4k_tiled_multi(1, &tiled, &y, &n, x, k, stream);
 }
 
 int rt_hip_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,

@@ -20,12 +20,6 @@ namespace {
 constexpr uint32_t kNegInfOrdered = ~0xff800000u;  // order map of -inf
 constexpr uint64_t kInitKey = (static_cast<uint64_t>(kNegInfOrdered) << 32) | 0xffffffffull;
 
-__device__ __forceinline__ uint64_t key_of(float v, uint32_t idx) {
-    uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return (static_cast<uint64_t>(u) << 32) | (0xffffffffu - idx);
-}
-
 __global__ void k_argmax_init(uint64_t* keys, int64_t rows) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < rows) keys[i] = kInitKey;
@@ -43,7 +37,7 @@ __global__ __launch_bounds__(256) void k_argmax_scan(const float* __restrict__ v
     for (int64_t c = c0 + threadIdx.x; c < c1; c += 256) {
         const float x = row[c];
         if (x == x) {
-            const uint64_t k = key_of(x, static_cast<uint32_t>(c));
+            const uint64_t k = argmax_key(x, static_cast<uint32_t>(c));
             best = k > best ? k : best;
         }
     }

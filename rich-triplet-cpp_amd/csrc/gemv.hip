@@ -35,14 +35,6 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
 
-__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
-    // Order-preserving map of f32 to u32 (with -0 folded onto +0), index in
-    // the low half inverted so the lowest index wins ties under max.
-    uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return (static_cast<uint64_t>(u) << 32) | (0xffffffffu - idx);
-}
-
 // ------------------------------------------------------------ formats --
 
 // Q4_K: piece = (block b, 16-byte qs half-chunk p); regs = {header, qs}.
@@ -524,6 +516,8 @@ hipError_t launch_gemv_q4k(const void* w, const float* x, float* y, int64_t n, i
 
 hipError_t launch_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
                             int m, uint64_t* key, hipStream_t s) {
+    // M == 1 (decode, and the fused-argmax lm_head) has its own kernel.
+    if (m == 1 && bf16_m1_lds_bytes(k) <= 65536) return launch_gemv_bf16_m1(w, x, y, n, k, key, s);
     return dispatch<Bf16Fmt, 1, true>(w, x, y, n, k, m, key, s, RT_HIP_BF16);
 }
 

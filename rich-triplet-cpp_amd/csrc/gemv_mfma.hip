@@ -13,6 +13,8 @@
 // The activation is staged once per workgroup as int8 limbs in LDS; its
 // global loads are issued before the weight prologue so that waiting for
 // them does not drain the weight loads (vmcnt completes in order).
+#include <type_traits>
+
 #include "q4k_mfma.hpp"
 #include "rt_launch.hpp"
 
@@ -77,7 +79,7 @@ __device__ __forceinline__ SJobs to_sregs(const Jobs& j) {
     return s;
 }
 
-template <int D, int KS, int XP>
+template <int D, int KS, int XP, bool TILED>
 __global__ __launch_bounds__(kThreads) void k_gemv_q4k_mfma(const Jobs jobs,
                                                             const float* __restrict__ X, int K) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -113,23 +115,42 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q4k_mfma(const Jobs jobs,
                     (sj.count > 3 && t >= sj.tile0.d ? 1 : 0);
     const int row0 = 16 * (t - sj.tile0[job]);
     const int n_job = sj.n[job];
-    const int64_t off0 = static_cast<int64_t>(row0) * rb + static_cast<int64_t>(b0) * kQ4kBlockBytes;
+    // Row-major blocks: the tile's rows are rb apart and block b sits at
+    // b * 144 in its row.  Tiled: the tile's block b is 2304 contiguous bytes
+    // at (tile * nb + b) * 2304, rows past N stored as zeros.
+    constexpr int64_t kStride = TILED ? kTiledBlockBytes : kQ4kBlockBytes;
+    const int64_t off0 = TILED ? (static_cast<int64_t>(row0 >> 4) * nb + b0) * kTiledBlockBytes
+                               : static_cast<int64_t>(row0) * rb + static_cast<int64_t>(b0) * kQ4kBlockBytes;
+    const int64_t job_bytes = TILED ? static_cast<int64_t>((n_job + 15) >> 4) * 16 * rb
+                                    : static_cast<int64_t>(n_job) * rb;
     const uint8_t* const tbase = reinterpret_cast<const uint8_t*>(sj.w[job]) + off0;
-    const int64_t tleft = static_cast<int64_t>(n_job) * rb - off0;
+    const int64_t tleft = job_bytes - off0;
+    const TLane tl = make_tlane(lane);
 
     // Block i of the wave's range through a resource based at that block of
-    // the tile's first row; past the range the resource is empty (zeros,
-    // no memory traffic).
-    auto issue = [&](Blk& slot, int i) {
-        const int64_t o = static_cast<int64_t>(i) * kQ4kBlockBytes;
-        load_blk(make_rsrc(tbase + o, i < nbw ? tleft - o : 0), roff, ln, slot);
+    // the tile; past the range (or past the job) the resource is empty:
+    // zeros, no memory traffic.
+    using B = typename std::conditional<TILED, BlkT, Blk>::type;
+    auto issue = [&](B& slot, int i) {
+        const int64_t o = static_cast<int64_t>(i) * kStride;
+        const BufRsrc rs = make_rsrc(tbase + o, i < nbw ? tleft - o : 0);
+        if constexpr (TILED)
+            load_blk_t(rs, static_cast<uint32_t>(lane), slot);
+        else
+            load_blk(rs, roff, ln, slot);
+    };
+    auto dec = [&](const B& slot) {
+        if constexpr (TILED)
+            return decode_t(slot, tl);
+        else
+            return decode(slot, ln);
     };
 
     // The scheduling barriers keep the ring's loads in slot order, so that
     // slot j's data is always the oldest in flight when it is consumed and
     // the waits stay partial (s_waitcnt vmcnt(3*(D-1))); in the main loop
     // the barrier sits between decoding a slot and refilling it.
-    Blk ring[D];
+    B ring[D];
 #pragma unroll
     for (int j = 0; j < D; ++j) {
         issue(ring[j], j);
@@ -157,7 +178,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q4k_mfma(const Jobs jobs,
     for (; i + D < nbw; i += D) {
 #pragma unroll
         for (int j = 0; j < D; ++j) {
-            const Dec dc = decode(ring[j], ln);
+            const Dec dc = dec(ring[j]);
             __builtin_amdgcn_sched_barrier(0);
             issue(ring[j], i + D + j);
             acc = dot(dc, b0 + i + j, ln, lds, acc);
@@ -165,7 +186,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q4k_mfma(const Jobs jobs,
     }
 #pragma unroll
     for (int j = 0; j < D; ++j)
-        if (i + j < nbw) acc = dot(decode(ring[j], ln), b0 + i + j, ln, lds, acc);
+        if (i + j < nbw) acc = dot(dec(ring[j]), b0 + i + j, ln, lds, acc);
 
     // Row n's partial: sum the four chunk lanes g.
     float v = acc;
@@ -190,28 +211,44 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q4k_mfma(const Jobs jobs,
     }
 }
 
-template <int D, int KS, int XP>
+template <int D, int KS, int XP, bool TILED>
 hipError_t run(const Jobs& jobs, const float* x, int64_t k, hipStream_t s) {
     constexpr int TPW = 4 / KS;
     const int64_t wgs = (static_cast<int64_t>(jobs.total) + TPW - 1) / TPW;
     const size_t lds = lds_bytes(static_cast<int>(k)) + TPW * KS * 16 * sizeof(float);
-    hipLaunchKernelGGL((k_gemv_q4k_mfma<D, KS, XP>), dim3(static_cast<unsigned>(wgs)), dim3(kThreads),
+    hipLaunchKernelGGL((k_gemv_q4k_mfma<D, KS, XP, TILED>), dim3(static_cast<unsigned>(wgs)), dim3(kThreads),
                        lds, s, jobs, x, static_cast<int>(k));
     return hipGetLastError();
 }
 
 // x prefetch depth: all of x (up to K = 8192) before the weight prologue.
-template <int D, int KS>
+template <int D, int KS, bool TILED>
 hipError_t run_xp(const Jobs& jobs, const float* x, int64_t k, hipStream_t s) {
-    return k > 4 * kThreads * 4 ? run<D, KS, 8>(jobs, x, k, s) : run<D, KS, 4>(jobs, x, k, s);
+    return k > 4 * kThreads * 4 ? run<D, KS, 8, TILED>(jobs, x, k, s) : run<D, KS, 4, TILED>(jobs, x, k, s);
+}
+
+// K-split per tile: enough waves to cover the chip for short outputs, whole
+// rows per wave for long ones.
+template <bool TILED>
+hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s) {
+    const int64_t tiles = jobs.total;
+    const int64_t nb = k / 256;
+    const int64_t want = static_cast<int64_t>(device_info().cus) * tune_param("Q4K_WANT_WAVES_PER_CU", 8);
+    // every wave of a split must own at least one super-block
+    auto splits_ok = [&](int64_t ks) { return (ks - 1) * ((nb + ks - 1) / ks) < nb; };
+    const int d = tune_param("Q4K_RING", 4);
+    if (tiles >= want || !splits_ok(2))
+        return d == 8 ? run_xp<8, 1, TILED>(jobs, x, k, s) : run_xp<4, 1, TILED>(jobs, x, k, s);
+    if (tiles * 2 >= want || !splits_ok(4))
+        return d == 8 ? run_xp<8, 2, TILED>(jobs, x, k, s) : run_xp<4, 2, TILED>(jobs, x, k, s);
+    return d == 8 ? run_xp<8, 4, TILED>(jobs, x, k, s) : run_xp<4, 4, TILED>(jobs, x, k, s);
 }
 
 }  // namespace
 
-// K-split per tile: enough waves to cover the chip for short outputs, whole
-// rows per wave for long ones.
 hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* const* y,
-                                      const int64_t* n, const float* x, int64_t k, hipStream_t s) {
+                                      const int64_t* n, const float* x, int64_t k, hipStream_t s,
+                                      bool tiled) {
     if (count < 1 || count > kMaxJobs) return hipErrorInvalidValue;
     Jobs jobs{};
     jobs.count = count;
@@ -230,21 +267,12 @@ hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* co
         jobs.tile0[j] = static_cast<int>(tiles);
     }
     jobs.total = static_cast<int>(tiles);
-    const int64_t nb = k / 256;
-    const int64_t want = static_cast<int64_t>(device_info().cus) * tune_param("Q4K_WANT_WAVES_PER_CU", 8);
-    // every wave of a split must own at least one super-block
-    auto splits_ok = [&](int64_t ks) { return (ks - 1) * ((nb + ks - 1) / ks) < nb; };
-    const int d = tune_param("Q4K_RING", 4);
-    if (tiles >= want || !splits_ok(2))
-        return d == 8 ? run_xp<8, 1>(jobs, x, k, s) : run_xp<4, 1>(jobs, x, k, s);
-    if (tiles * 2 >= want || !splits_ok(4))
-        return d == 8 ? run_xp<8, 2>(jobs, x, k, s) : run_xp<4, 2>(jobs, x, k, s);
-    return d == 8 ? run_xp<8, 4>(jobs, x, k, s) : run_xp<4, 4>(jobs, x, k, s);
+    return tiled ? dispatch<true>(jobs, x, k, s) : dispatch<false>(jobs, x, k, s);
 }
 
 hipError_t launch_gemv_q4k_mfma(const void* w, const float* x, float* y, int64_t n, int64_t k,
                                 hipStream_t s) {
-    return launch_gemv_q4k_mfma_multi(1, &w, &y, &n, x, k, s);
+    return launch_gemv_q4k_mfma_multi(1, &w, &y, &n, x, k, s, false);
 }
 
 }  // namespace rt_hip

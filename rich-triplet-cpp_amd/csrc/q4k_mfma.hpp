@@ -141,13 +141,22 @@ __device__ __forceinline__ void load_blk(BufRsrc rs, uint32_t roff, const Lane& 
 }
 
 // A super-block with its loaded registers already taken apart: the nibble
-// planes as MFMA B operands and this lane's two scales and mins.  Once a
-// block is decoded its load registers are free for the next load.
+// planes as MFMA B operands and this lane's two scale and min products.
+// Once a block is decoded its load registers are free for the next load.
+// The products d*sv and dmin*mv are exact in f32 (11 + 6 significant bits),
+// so every layout that yields the same (d, dmin, sv, mv) gives the same bits.
 struct Dec {
     i32x4 B0, B1, B2, B3;
-    uint32_t svp, mvp;  // (scale, min) 6-bit values of sub-blocks 2g, 2g+1
-    float d, dm;
+    float ds0, ds1;  // d * sv of sub-blocks 2g, 2g+1
+    float dm0, dm1;  // dmin * mv of sub-blocks 2g, 2g+1
 };
+
+__device__ __forceinline__ void nibble_planes(const u32x4 q0, const u32x4 q1, Dec& o) {
+    o.B0 = __builtin_bit_cast(i32x4, q0 & 0x0f0f0f0fu);
+    o.B1 = __builtin_bit_cast(i32x4, q1 & 0x0f0f0f0fu);
+    o.B2 = __builtin_bit_cast(i32x4, (q0 >> 4) & 0x0f0f0f0fu);
+    o.B3 = __builtin_bit_cast(i32x4, (q1 >> 4) & 0x0f0f0f0fu);
+}
 
 __device__ __forceinline__ Dec decode(const Blk& r, const Lane& ln) {
     Dec o;
@@ -161,14 +170,81 @@ __device__ __forceinline__ Dec decode(const Blk& r, const Lane& ln) {
     const uint32_t sv_lo = a0 & 0x3f3fu, mv_lo = a1 & 0x3f3fu;
     const uint32_t sv_hi = (a2 & 0x0f0fu) | ((a0 >> 2) & 0x3030u);
     const uint32_t mv_hi = ((a2 >> 4) & 0x0f0fu) | ((a1 >> 2) & 0x3030u);
-    o.svp = sv_lo ^ ((sv_lo ^ sv_hi) & ln.hmask);
-    o.mvp = mv_lo ^ ((mv_lo ^ mv_hi) & ln.hmask);
-    o.d = f16_bits_to_f32(r.h[0] & 0xffffu);
-    o.dm = f16_bits_to_f32(r.h[0] >> 16);
-    o.B0 = __builtin_bit_cast(i32x4, r.q0 & 0x0f0f0f0fu);
-    o.B1 = __builtin_bit_cast(i32x4, r.q1 & 0x0f0f0f0fu);
-    o.B2 = __builtin_bit_cast(i32x4, (r.q0 >> 4) & 0x0f0f0f0fu);
-    o.B3 = __builtin_bit_cast(i32x4, (r.q1 >> 4) & 0x0f0f0f0fu);
+    const uint32_t svp = sv_lo ^ ((sv_lo ^ sv_hi) & ln.hmask);
+    const uint32_t mvp = mv_lo ^ ((mv_lo ^ mv_hi) & ln.hmask);
+    const float d = f16_bits_to_f32(r.h[0] & 0xffffu);
+    const float dm = f16_bits_to_f32(r.h[0] >> 16);
+    o.ds0 = d * ubyte_f32(svp, 0);
+    o.ds1 = d * ubyte_f32(svp, 1);
+    o.dm0 = dm * ubyte_f32(mvp, 0);
+    o.dm1 = dm * ubyte_f32(mvp, 1);
+    nibble_planes(r.q0, r.q1, o);
+    return o;
+}
+
+// ---- tiled layout ---------------------------------------------------------
+// A 16-row tile's super-block b is 2304 contiguous bytes in lane order
+// (lane l = n + 16 g: row n of the tile, chunk g):
+//   [0, 256)      one dword per lane: sv(2g) | sv(2g+1) << 6 | mv(2g) << 12 |
+//                 mv(2g+1) << 18 | byte g of (d | dmin << 16) << 24
+//   [256, 1280)   16 bytes per lane: qs[32g, 32g+16) of row n
+//   [1280, 2304)  16 bytes per lane: qs[32g+16, 32g+32) of row n
+// Tiles are stored one after another, each as its nb super-blocks in order,
+// so a tile is 16 * row_bytes bytes, the same as its 16 rows; rows past N in
+// the last tile are zero.  Every load of the GEMV reads contiguous memory.
+constexpr int kTiledHdr = 256;
+constexpr int kTiledQa = 256;
+constexpr int kTiledQb = 1280;
+constexpr int kTiledBlockBytes = 2304;
+
+struct BlkT {
+    uint32_t h;
+    u32x4 q0, q1;
+};
+
+// Lane constants for reassembling (d | dmin << 16) from the byte each of the
+// four lanes of a row holds: shift of bytes g, g^1, g^2, g^3.
+struct TLane {
+    uint32_t s0, s1, s2, s3;
+    bool odd_row, high_half;  // 16-lane row g is odd / g >= 2
+};
+
+__device__ __forceinline__ TLane make_tlane(int lane) {
+    const uint32_t g = static_cast<uint32_t>(lane >> 4);
+    return TLane{8u * g, 8u * (g ^ 1u), 8u * (g ^ 2u), 8u * (g ^ 3u), (g & 1u) != 0, g >= 2u};
+}
+
+// x from lane l ^ 16 and from lane l ^ 32 (gfx950 permlane swaps: a swap of
+// a register with itself exchanges whole 16- or 32-lane groups).
+__device__ __forceinline__ uint32_t xor16(uint32_t x, bool odd_row) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return odd_row ? r[0] : r[1];
+}
+__device__ __forceinline__ uint32_t xor32(uint32_t x, bool high_half) {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return high_half ? r[0] : r[1];
+}
+
+__device__ __forceinline__ void load_blk_t(BufRsrc rs, uint32_t lane, BlkT& r) {
+    r.h = __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(lane * 4u), 0, 0);
+    r.q0 = ld16(rs, kTiledQa + lane * 16u);
+    r.q1 = ld16(rs, kTiledQb + lane * 16u);
+}
+
+__device__ __forceinline__ Dec decode_t(const BlkT& r, const TLane& tl) {
+    Dec o;
+    const uint32_t b = r.h >> 24;
+    const uint32_t b1 = xor16(b, tl.odd_row);
+    const uint32_t b2 = xor32(b, tl.high_half);
+    const uint32_t b3 = xor32(b1, tl.high_half);
+    const uint32_t dd = (b << tl.s0) | (b1 << tl.s1) | (b2 << tl.s2) | (b3 << tl.s3);
+    const float d = f16_bits_to_f32(dd & 0xffffu);
+    const float dm = f16_bits_to_f32(dd >> 16);
+    o.ds0 = d * static_cast<float>(__builtin_amdgcn_ubfe(r.h, 0, 6));
+    o.ds1 = d * static_cast<float>(__builtin_amdgcn_ubfe(r.h, 6, 6));
+    o.dm0 = dm * static_cast<float>(__builtin_amdgcn_ubfe(r.h, 12, 6));
+    o.dm1 = dm * static_cast<float>(__builtin_amdgcn_ubfe(r.h, 18, 6));
+    nibble_planes(r.q0, r.q1, o);
     return o;
 }
 
@@ -186,8 +262,6 @@ __device__ __forceinline__ float dot(const Dec& r, int b, const Lane& ln, const 
     clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, r.B1, clo, 0, 0, 0);
     i32x4 chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, r.B2, z, 0, 0, 0);
     chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A3, r.B3, chi, 0, 0, 0);
-    const float d = r.d, dm = r.dm;
-    const uint32_t svp = r.svp, mvp = r.mvp;
 
     const uint32_t c_addr = ln.cst_base + (static_cast<uint32_t>(b) << 7);
     const f32x4 kl = lds_f4(c_addr), kh = lds_f4(c_addr + 16);
@@ -199,10 +273,10 @@ __device__ __forceinline__ float dot(const Dec& r, int b, const Lane& ln, const 
     dh = __builtin_fmaf(static_cast<float>(chi[1]), kh[1], dh);
     dh = __builtin_fmaf(static_cast<float>(chi[2]), kh[2], dh);
     // sum_w x = (d*sv) * dot - (dmin*mv) * sum(x), per sub-block
-    acc = __builtin_fmaf(d * ubyte_f32(svp, 0), dl, acc);
-    acc = __builtin_fmaf(-(dm * ubyte_f32(mvp, 0)), kl[3], acc);
-    acc = __builtin_fmaf(d * ubyte_f32(svp, 1), dh, acc);
-    acc = __builtin_fmaf(-(dm * ubyte_f32(mvp, 1)), kh[3], acc);
+    acc = __builtin_fmaf(r.ds0, dl, acc);
+    acc = __builtin_fmaf(-r.dm0, kl[3], acc);
+    acc = __builtin_fmaf(r.ds1, dh, acc);
+    acc = __builtin_fmaf(-r.dm1, kh[3], acc);
     return acc;
 }
 

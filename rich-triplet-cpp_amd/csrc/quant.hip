@@ -14,6 +14,7 @@
 // reciprocal (hipcc's default correctly-rounded f32 divide), no
 // contraction (the library builds with -ffp-contract=off), and the f16
 // header conversion is the reference's truncating one restated on bits.
+#include "q4k_mfma.hpp"
 #include "rt_common.hpp"
 #include "rt_launch.hpp"
 
@@ -197,6 +198,39 @@ __global__ __launch_bounds__(256) void k_quantize_q4k(const float* __restrict__ 
     }
 }
 
+// Reference row-major Q4_K blocks -> tiled layout (q4k_mfma.hpp): one thread
+// per (tile, super-block, lane) writes that lane's header dword and its two
+// 16-byte halves of qs; rows past N are written as zeros.
+__global__ __launch_bounds__(256) void k_q4k_tile(const uint8_t* __restrict__ src,
+                                                  uint8_t* __restrict__ dst, int64_t n, int nb,
+                                                  int64_t threads) {
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (gid >= threads) return;
+    const int l = static_cast<int>(gid & 63);
+    const int64_t tb = gid >> 6;  // tile * nb + b
+    const int b = static_cast<int>(tb % nb);
+    const int64_t t = tb / nb;
+    const int g = l >> 4;
+    const int64_t row = t * 16 + (l & 15);
+    uint8_t* out = dst + tb * q4k_mfma::kTiledBlockBytes;
+    uint32_t hdr = 0;
+    u32x4 qa = {0u, 0u, 0u, 0u}, qb = {0u, 0u, 0u, 0u};
+    if (row < n) {
+        const uint8_t* blk = src + (row * nb + b) * kQ4kBlockBytes;
+        const u32x4 h = ld16(blk);
+        uint32_t sv0, mv0, sv1, mv1;
+        decode_scale_min(make_scale_sel(2 * g), h[1], h[2], h[3], sv0, mv0);
+        decode_scale_min(make_scale_sel(2 * g + 1), h[1], h[2], h[3], sv1, mv1);
+        const uint32_t dbyte = (h[0] >> (8 * g)) & 0xffu;
+        hdr = sv0 | (sv1 << 6) | (mv0 << 12) | (mv1 << 18) | (dbyte << 24);
+        qa = ld16(blk + 16 + 32 * g);
+        qb = ld16(blk + 32 + 32 * g);
+    }
+    reinterpret_cast<uint32_t*>(out)[l] = hdr;
+    reinterpret_cast<u32x4*>(out + q4k_mfma::kTiledQa)[l] = qa;
+    reinterpret_cast<u32x4*>(out + q4k_mfma::kTiledQb)[l] = qb;
+}
+
 }  // namespace
 
 hipError_t launch_dequant_q4k(const void* w, void* out, bool bf16, int64_t n, int64_t k,
@@ -214,6 +248,16 @@ hipError_t launch_quantize_q4k(const float* w, void* blocks, int64_t n, int64_t 
     const unsigned grid = static_cast<unsigned>((nblk + 3) / 4);
     hipLaunchKernelGGL(k_quantize_q4k, dim3(grid), dim3(256), 0, s, w,
                        static_cast<uint8_t*>(blocks), n, k);
+    return hipGetLastError();
+}
+
+hipError_t launch_q4k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, hipStream_t s) {
+    const int nb = static_cast<int>(k / 256);
+    const int64_t threads = (n + 15) / 16 * nb * 64;
+    const int64_t grid = (threads + 255) / 256;
+    hipLaunchKernelGGL(k_q4k_tile, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s,
+                       static_cast<const uint8_t*>(blocks), static_cast<uint8_t*>(tiled), n, nb,
+                       threads);
     return hipGetLastError();
 }
 

@@ -63,6 +63,15 @@ __device__ __forceinline__ u32x4 ld16_stream(const void* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
+// Argmax key of (value, index): an order-preserving map of the f32 (-0
+// folded onto +0) in the high half and (0xffffffff - index) in the low half,
+// so the maximum key is the largest value with the lowest index.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
+    uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (static_cast<uint64_t>(u) << 32) | (0xffffffffu - idx);
+}
+
 // f32 -> bf16 round-to-nearest-even with NaN quieting (bf16.hpp:50-60).
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float v) {
     const uint32_t bits = __float_as_uint(v);

@@ -31,10 +31,19 @@ hipError_t launch_gemv_q4k(const void* w, const float* x, float* y, int64_t n, i
                            int m, hipStream_t s);
 hipError_t launch_gemv_q4k_mfma(const void* w, const float* x, float* y, int64_t n, int64_t k,
                                 hipStream_t s);
+// Up to four M = 1 Q4_K GEMVs sharing x, K; `tiled`: the weights are in the
+// tiled layout (q4k_mfma.hpp) rather than reference row-major blocks.
 hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* const* y,
-                                      const int64_t* n, const float* x, int64_t k, hipStream_t s);
+                                      const int64_t* n, const float* x, int64_t k, hipStream_t s,
+                                      bool tiled);
+hipError_t launch_q4k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, hipStream_t s);
 hipError_t launch_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
                             int m, uint64_t* argmax_key, hipStream_t s);
+// M = 1 BF16 GEMV (gemv_bf16.hip); `key` (may be null) receives the fused
+// argmax.  LDS: bf16_m1_lds_bytes(k).
+size_t bf16_m1_lds_bytes(int64_t k);
+hipError_t launch_gemv_bf16_m1(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
+                               uint64_t* key, hipStream_t s);
 hipError_t launch_gemv_q4_0(const void* w, const float* x, float* y, int64_t n, int64_t k,
                             int m, hipStream_t s);
 

@@ -27,6 +27,9 @@ _SIGNATURES = {
     "rt_hip_gemv_q4k": [_vp, _vp, _vp, _i64, _i64, _i32, _vp],
     "rt_hip_gemv_bf16": [_vp, _vp, _vp, _i64, _i64, _i32, _vp],
     "rt_hip_gemv_q4k_multi": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _i64, _vp],
+    "rt_hip_q4k_tile": [_vp, _vp, _i64, _i64, _vp],
+    "rt_hip_gemv_q4k_tiled": [_vp, _vp, _vp, _i64, _i64, _vp],
+    "rt_hip_gemv_q4k_tiled_multi": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _i64, _vp],
     "rt_hip_gemv_q4_0": [_vp, _vp, _vp, _i64, _i64, _i32, _vp],
     "rt_hip_argmax": [_vp, _i64, _i64, _vp, _vp, _vp],
     "rt_hip_gemv_bf16_argmax": [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp],
@@ -64,6 +67,8 @@ class Library:
         self.lib = C.CDLL(path)
         self.lib.rt_hip_last_error.restype = C.c_char_p
         self.lib.rt_hip_version.restype = C.c_char_p
+        self.lib.rt_hip_q4k_tiled_bytes.restype = C.c_int64
+        self.lib.rt_hip_q4k_tiled_bytes.argtypes = [_i64, _i64]
         for name, args in _SIGNATURES.items():
             fn = getattr(self.lib, name)
             fn.restype = C.c_int
@@ -145,6 +150,44 @@ def gemv_q4k_multi(ws, x, ns, k: int, ys=None, stream=None):
     yp = (_vp * count)(*[y.data_ptr() for y in ys])
     npp = (_i64 * count)(*ns)
     library().call("rt_hip_gemv_q4k_multi", count, wp, yp, npp, _ptr(x), k, _stream(stream))
+    return ys
+
+
+def q4k_tiled_bytes(n: int, k: int) -> int:
+    return library().lib.rt_hip_q4k_tiled_bytes(n, k)
+
+
+def q4k_tile(blocks, n: int, k: int, stream=None):
+    """Tiled copy of row-major Q4_K blocks (for gemv_q4k_tiled*)."""
+    torch = _torch()
+    size = q4k_tiled_bytes(n, k)
+    if size < 0:
+        raise ValueError(f"rt_hip: invalid Q4_K shape n={n} k={k}")
+    tiled = torch.empty(size, dtype=torch.uint8, device=blocks.device)
+    _dev_check(blocks)
+    library().call("rt_hip_q4k_tile", _ptr(blocks), _ptr(tiled), n, k, _stream(stream))
+    return tiled
+
+
+def gemv_q4k_tiled(tiled, x, n: int, k: int, y=None, stream=None):
+    torch = _torch()
+    if y is None:
+        y = torch.empty((1, n), dtype=torch.float32, device=x.device)
+    _dev_check(tiled, x, y)
+    library().call("rt_hip_gemv_q4k_tiled", _ptr(tiled), _ptr(x), _ptr(y), n, k, _stream(stream))
+    return y
+
+
+def gemv_q4k_tiled_multi(ws, x, ns, k: int, ys=None, stream=None):
+    torch = _torch()
+    count = len(ws)
+    if ys is None:
+        ys = [torch.empty((1, n), dtype=torch.float32, device=x.device) for n in ns]
+    _dev_check(x, *ws, *ys)
+    wp = (_vp * count)(*[w.data_ptr() for w in ws])
+    yp = (_vp * count)(*[y.data_ptr() for y in ys])
+    npp = (_i64 * count)(*ns)
+    library().call("rt_hip_gemv_q4k_tiled_multi", count, wp, yp, npp, _ptr(x), k, _stream(stream))
     return ys
 
 
