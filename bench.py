@@ -30,6 +30,11 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 WIDENED_LAYERS = {0, 1, 2, 5, 8, 11, 14, 17, 20, 23, 24, 25, 26, 27}
 HIDDEN, KV, FFN, VOCAB, LAYERS = 3072, 1024, 8192, 128256, 28
+# HBM bytes per launch of the dominant kernel (fused gate+up, tiled layout),
+# measured with rocprofv3 FETCH_SIZE / WRITE_SIZE and scaled by a 1 GiB device
+# copy: profiles/decode_kernels_hbm_traffic.md (command there).  The
+# row-major layout has no measured figure.
+DOMINANT_TRAFFIC_BYTES = {"tiled": 28660679}
 
 
 def log(*a):
@@ -52,7 +57,29 @@ def q4k_bytes(n, k):
 
 
 def weight_bytes(fmt, n, k, rt):
-    return q4k_bytes(n, k) if fmt == rt.Q4K else n * k * 2
+    if fmt == rt.Q4K:
+        return q4k_bytes(n, k)
+    if fmt == rt.Q4_0:
+        return n * (k // 32) * 18
+    return n * k * 2
+
+
+def q4_0_blocks(torch, w):
+    """GGUF Q4_0 blocks of w [n, k] on the GPU: per 32 values d = absmax/7
+    (rounded to f16), q = clamp(round(v/d), -8, 7) + 8, value j < 16 in the
+    low nibble of qs[j] and value j + 16 in its high nibble (the layout
+    decoded at src/gguf.cpp:495-529).  Synthetic data only."""
+    n, k = w.shape
+    b = w.reshape(n, k // 32, 32)
+    d = (b.abs().amax(dim=-1) / 7.0).half()
+    df = d.float()
+    q = torch.where(df[..., None] > 0, torch.round(b / df[..., None].clamp_min(1e-30)),
+                    torch.zeros_like(b)).clamp(-8, 7).to(torch.int32) + 8
+    qs = (q[..., :16] | (q[..., 16:] << 4)).to(torch.uint8)
+    out = torch.empty((n, k // 32, 18), dtype=torch.uint8, device=w.device)
+    out[..., 0:2] = d.view(torch.uint8).reshape(n, k // 32, 2)
+    out[..., 2:] = qs
+    return out.reshape(-1)
 
 
 # --------------------------------------------------------------- config 3 --
@@ -279,7 +306,8 @@ def bench_decode(args, rt, torch):
     log(f"[bench] dominant kernel: {dom}")
     roof = {"bound": "hbm", "achieved": round(dom["achieved_gbs"], 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(dom["achieved_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": args.traffic_bytes, "kernel": dom["kernel"],
+            "traffic": (args.traffic_bytes if args.traffic_bytes is not None
+                        else DOMINANT_TRAFFIC_BYTES.get(args.layout)), "kernel": dom["kernel"],
             "us_per_launch": round(dom["us_per_launch"], 3),
             "bytes_per_launch": dom["bytes_per_launch"]}
     cpu = None if args.no_cpu_baseline else cpu_baseline(rt, torch, model)
@@ -318,6 +346,8 @@ def bench_single_gemv(args, rt, torch, fmt, n, k, label, copies_bytes=768 << 20)
             ws.append(rt.quantize_q4k(w))
         elif fmt == rt.BF16:
             ws.append(w.to(torch.bfloat16).view(torch.int16))
+        elif fmt == rt.Q4_0:
+            ws.append(q4_0_blocks(torch, w))
         else:
             raise ValueError(fmt)
         del w
@@ -373,6 +403,10 @@ def main() -> int:
                              "flux"])
     ap.add_argument("--mix", default="q4km", choices=["q4km", "q4k"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibration-copy-mb", type=int, default=0,
+                    help="before the workload, copy a buffer of this many MiB once with a plain "
+                         "device copy (the known-size kernel that HBM traffic counters are "
+                         "scaled by); untimed")
     ap.add_argument("--layout", default="tiled", choices=["tiled", "rows"],
                     help="Q4_K weights tiled once at load (default) or the reference's row-major "
                          "blocks through rt_hip_gemv_q4k*")
@@ -390,11 +424,22 @@ def main() -> int:
     rt = load_rt()
     rt.init(0)
     log(f"[bench] {rt.library().version()} on {torch.cuda.get_device_name(0)}")
+    if args.calibration_copy_mb:
+        nel = args.calibration_copy_mb * (1 << 20) // 4
+        src = torch.ones(nel, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration copy: {nel * 4} bytes read, {nel * 4} bytes written")
+        del src, dst
     if args.workload == "llama_decode":
         out = bench_decode(args, rt, torch)
     elif args.workload == "q4k_gemv":
         out = bench_single_gemv(args, rt, torch, rt.Q4K, 6912, 1024,
                                 "config 1 Q4_K GEMV 6912x1152 (Release semantics: K=1024)")
+    elif args.workload == "q4_0_gemv":
+        out = bench_single_gemv(args, rt, torch, rt.Q4_0, 4096, 4096, "config 2a GGUF Q4_0 GEMV 4096x4096")
     elif args.workload == "bf16_lm_head":
         out = bench_single_gemv(args, rt, torch, rt.BF16, 262144, 1152, "config 2b BF16 GEMV 262144x1152")
     elif args.workload == "prefill":
