@@ -5,9 +5,11 @@
 // gate/up): their 16-row tiles are numbered consecutively and each wave looks
 // its tile up in the job table.
 //
-// A wave owns 16-row tiles (q4k_mfma.hpp: lane = (row n, chunk g)); a
-// workgroup of 4 waves works on 4/KS tiles at a time, the KS waves of a tile
-// splitting its super-blocks and combining their partial rows through LDS.
+// A wave owns one 16-row tile (q4k_mfma.hpp: lane = (row n, chunk g)), or
+// 1/KS of its super-blocks: the KS waves of a tile combine their partial rows
+// through LDS.  A workgroup holds max(4, KS) waves, i.e. 4/KS tiles for
+// KS <= 4 and one tile of KS waves beyond, so short outputs still put enough
+// loads in flight per CU.
 // Each wave keeps a ring of D super-blocks of its tile loaded ahead of the
 // one it computes, so D * 16 rows * 144 bytes stay in flight per wave.
 // The activation is staged once per workgroup as int8 limbs in LDS; its
@@ -23,7 +25,7 @@ namespace {
 
 using namespace q4k_mfma;
 
-constexpr int kThreads = 256;
+constexpr int kMaxThreads = 768;  // up to 12 waves per workgroup
 constexpr int kMaxJobs = 4;
 
 // LDS-only workgroup barrier: waits for this wave's LDS traffic, not for its
@@ -79,11 +81,15 @@ __device__ __forceinline__ SJobs to_sregs(const Jobs& j) {
     return s;
 }
 
-template <int D, int KS, int XP, bool TILED>
-__global__ __launch_bounds__(kThreads) void k_gemv_q4k_mfma(const Jobs jobs,
-                                                            const float* __restrict__ X, int K) {
+// KS waves split a tile's super-blocks; a workgroup of blockDim.x / 64 waves
+// holds TPW = waves / KS tiles.
+template <int D, int XP, bool TILED>
+__global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(const Jobs jobs,
+                                                               const float* __restrict__ X, int K,
+                                                               int KS) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    constexpr int TPW = 4 / KS;  // tiles per workgroup
+    const int nthreads = static_cast<int>(blockDim.x);
+    const int TPW = (nthreads >> 6) / KS;  // tiles per workgroup
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nb = K >> 8;
@@ -101,7 +107,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q4k_mfma(const Jobs jobs,
     f32x4 xv[XP];
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
-        const int f = tid + kThreads * i;
+        const int f = tid + nthreads * i;
         xv[i] = X4[f < nx ? f : 0];
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -161,10 +167,10 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q4k_mfma(const Jobs jobs,
     // is not stored), so the loads are consumed where they were issued.
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
-        const int f = tid + kThreads * i;
+        const int f = tid + nthreads * i;
         limbs_of(xv[i], lds, K, f, f < nx);
     }
-    for (int f = tid + kThreads * XP; f < nx; f += kThreads) limbs_of(X4[f], lds, K, f);
+    for (int f = tid + nthreads * XP; f < nx; f += nthreads) limbs_of(X4[f], lds, K, f);
     if (tid < 4) reinterpret_cast<u32x4*>(lds + 3 * static_cast<size_t>(K))[tid] = u32x4{0u, 0u, 0u, 0u};
     lds_barrier();
 
@@ -195,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q4k_mfma(const Jobs jobs,
     const int row = row0 + ln.n;
     const bool keep = row < n_job;  // false for tile slots past the last tile
     float* const yj = reinterpret_cast<float*>(sj.y[job]);
-    if constexpr (KS == 1) {
+    if (KS == 1) {
         if (lane < 16 && keep) yj[row] = v;
     } else {
         float* red = reinterpret_cast<float*>(lds + lds_bytes(K));  // [TPW][KS][16]
@@ -211,37 +217,57 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q4k_mfma(const Jobs jobs,
     }
 }
 
-template <int D, int KS, int XP, bool TILED>
-hipError_t run(const Jobs& jobs, const float* x, int64_t k, hipStream_t s) {
-    constexpr int TPW = 4 / KS;
-    const int64_t wgs = (static_cast<int64_t>(jobs.total) + TPW - 1) / TPW;
-    const size_t lds = lds_bytes(static_cast<int>(k)) + TPW * KS * 16 * sizeof(float);
-    hipLaunchKernelGGL((k_gemv_q4k_mfma<D, KS, XP, TILED>), dim3(static_cast<unsigned>(wgs)), dim3(kThreads),
-                       lds, s, jobs, x, static_cast<int>(k));
+template <int D, int XP, bool TILED>
+hipError_t run(const Jobs& jobs, const float* x, int64_t k, int ks, int waves, hipStream_t s) {
+    const int tpw = waves / ks;
+    const int64_t wgs = (static_cast<int64_t>(jobs.total) + tpw - 1) / tpw;
+    const size_t lds = lds_bytes(static_cast<int>(k)) + static_cast<size_t>(waves) * 16 * sizeof(float);
+    hipLaunchKernelGGL((k_gemv_q4k_mfma<D, XP, TILED>), dim3(static_cast<unsigned>(wgs)),
+                       dim3(static_cast<unsigned>(waves * kWave)), lds, s, jobs, x, static_cast<int>(k), ks);
     return hipGetLastError();
 }
 
-// x prefetch depth: all of x (up to K = 8192) before the weight prologue.
-template <int D, int KS, bool TILED>
-hipError_t run_xp(const Jobs& jobs, const float* x, int64_t k, hipStream_t s) {
-    return k > 4 * kThreads * 4 ? run<D, KS, 8, TILED>(jobs, x, k, s) : run<D, KS, 4, TILED>(jobs, x, k, s);
+// x prefetch depth: enough f32x4 per thread for all of x (up to K = 8192 at
+// 256 threads) before the weight prologue.
+template <int D, bool TILED>
+hipError_t run_xp(const Jobs& jobs, const float* x, int64_t k, int ks, int waves, hipStream_t s) {
+    const int64_t per = (k / 4 + waves * kWave - 1) / (waves * kWave);
+    if (per <= 2) return run<D, 2, TILED>(jobs, x, k, ks, waves, s);
+    if (per <= 4) return run<D, 4, TILED>(jobs, x, k, ks, waves, s);
+    return run<D, 8, TILED>(jobs, x, k, ks, waves, s);
 }
 
-// K-split per tile: enough waves to cover the chip for short outputs, whole
-// rows per wave for long ones.
+// K-split per tile.  One round of workgroups (at most one per CU) is what
+// matters for the short outputs of a decode step: a launch whose last few
+// CUs get a second workgroup takes twice as long.  So: the largest split of
+// {1, 2, 3, 4, 6, 8, 12} that divides the super-block count, leaves every
+// wave at least two super-blocks and still fits one workgroup per CU.
+// Outputs too long for one round even at KS = 1 use KS = 2 (measured best
+// for the lm_head).  KS = 1, 2, 4 run 4 waves per workgroup (4/KS tiles);
+// other splits one tile per workgroup of KS waves.
 template <bool TILED>
 hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s) {
     const int64_t tiles = jobs.total;
     const int64_t nb = k / 256;
-    const int64_t want = static_cast<int64_t>(device_info().cus) * tune_param("Q4K_WANT_WAVES_PER_CU", 8);
-    // every wave of a split must own at least one super-block
-    auto splits_ok = [&](int64_t ks) { return (ks - 1) * ((nb + ks - 1) / ks) < nb; };
+    const int64_t cus = device_info().cus;
+    static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12};
+    auto wgs_for = [&](int c) {
+        const int64_t tpw = c <= 4 ? 4 / c : 1;
+        return (tiles + tpw - 1) / tpw;
+    };
+    int ks = 1;
+    for (int c : kSplits) {
+        if (nb % c != 0 || (c > 1 && 2 * c > nb)) continue;
+        if (wgs_for(c) <= cus) ks = c;
+    }
+    if (wgs_for(1) > cus && nb % 2 == 0) ks = 2;
+    if (const int forced = tune_param("Q4K_KS", 0)) ks = (nb % forced == 0 && forced <= 12) ? forced : ks;
+    // a whole number of tiles per workgroup: 4 waves for KS = 1, 2, 4;
+    // exactly KS waves (one tile) otherwise
+    const int waves = ks <= 4 ? (4 / ks) * ks : ks;
+    if (waves % ks != 0 || waves > kMaxThreads / kWave) return hipErrorInvalidValue;
     const int d = tune_param("Q4K_RING", 4);
-    if (tiles >= want || !splits_ok(2))
-        return d == 8 ? run_xp<8, 1, TILED>(jobs, x, k, s) : run_xp<4, 1, TILED>(jobs, x, k, s);
-    if (tiles * 2 >= want || !splits_ok(4))
-        return d == 8 ? run_xp<8, 2, TILED>(jobs, x, k, s) : run_xp<4, 2, TILED>(jobs, x, k, s);
-    return d == 8 ? run_xp<8, 4, TILED>(jobs, x, k, s) : run_xp<4, 4, TILED>(jobs, x, k, s);
+    return d == 8 ? run_xp<8, TILED>(jobs, x, k, ks, waves, s) : run_xp<4, TILED>(jobs, x, k, ks, waves, s);
 }
 
 }  // namespace
