@@ -45,11 +45,9 @@ struct Jobs {
     int count;
 };
 
-// The job table held in scalar registers.  Each field goes through
-// readfirstlane once and is kept as four named values, so that selecting a
-// job is a chain of scalar selects: read from the kernel arguments (or from
-// an array), a job lookup becomes an indexed load and a wait in the middle
-// of the pipeline.
+// Job-table fields read into scalar registers through readfirstlane, and
+// picked with scalar selects: read straight from the kernel arguments (or
+// from an array), a job lookup becomes an indexed load and a wait.
 template <typename T>
 struct Four {
     T a, b, c, d;
@@ -64,29 +62,17 @@ __device__ __forceinline__ uint64_t sreg(const void* p) {
     return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
-struct SJobs {
-    Four<uint64_t> w, y;
-    Four<int> n, tile0;
-    int count;
-};
-
-__device__ __forceinline__ SJobs to_sregs(const Jobs& j) {
-    static_assert(kMaxJobs == 4, "SJobs holds four jobs");
-    SJobs s;
-    s.w = {sreg(j.w[0]), sreg(j.w[1]), sreg(j.w[2]), sreg(j.w[3])};
-    s.y = {sreg(j.y[0]), sreg(j.y[1]), sreg(j.y[2]), sreg(j.y[3])};
-    s.n = {sreg(j.n[0]), sreg(j.n[1]), sreg(j.n[2]), sreg(j.n[3])};
-    s.tile0 = {sreg(j.tile0[0]), sreg(j.tile0[1]), sreg(j.tile0[2]), sreg(j.tile0[3])};
-    s.count = sreg(j.count);
-    return s;
-}
-
 // KS waves split a tile's super-blocks; a workgroup of blockDim.x / 64 waves
 // holds TPW = waves / KS tiles.
+// The arguments every wave needs before its first load come first, as
+// scalars: they are preloaded into SGPRs at wave launch (the library builds
+// with -amdgpu-kernarg-preload-count), so x and the weight prologue issue
+// without waiting for a kernel-argument load.  Jobs 2 and 3 (and every
+// output pointer) come from the table.
 template <int D, int XP, bool TILED>
-__global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(const Jobs jobs,
-                                                               const float* __restrict__ X, int K,
-                                                               int KS) {
+__global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
+    const float* __restrict__ X, int K, int KS, const uint8_t* w0, const uint8_t* w1, int n0, int n1,
+    int tile1, int count, const Jobs jobs) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int nthreads = static_cast<int>(blockDim.x);
     const int TPW = (nthreads >> 6) / KS;  // tiles per workgroup
@@ -115,12 +101,25 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(const Jobs jobs,
     // This wave's tile: job and first row (wave-uniform).  A tile slot past
     // the last tile belongs to the last job with rows past its end, so its
     // loads read zeros and it stores nothing.
-    const SJobs sj = to_sregs(jobs);
     const int t = static_cast<int>(blockIdx.x) * TPW + tslot;
-    const int job = (sj.count > 1 && t >= sj.tile0.b ? 1 : 0) + (sj.count > 2 && t >= sj.tile0.c ? 1 : 0) +
-                    (sj.count > 3 && t >= sj.tile0.d ? 1 : 0);
-    const int row0 = 16 * (t - sj.tile0[job]);
-    const int n_job = sj.n[job];
+    int job, tile_base, n_job;
+    const uint8_t* wj;
+    job = (count > 1 && t >= tile1) ? 1 : 0;
+    tile_base = job ? tile1 : 0;
+    n_job = job ? n1 : n0;
+    wj = job ? w1 : w0;
+    if (count > 2) {
+        // jobs 2 and 3 (a layer's k/v after q): from the table
+        const int t2 = sreg(jobs.tile0[2]), t3 = sreg(jobs.tile0[3]);
+        if (t >= t2) {
+            const bool j3 = count > 3 && t >= t3;
+            job = j3 ? 3 : 2;
+            tile_base = j3 ? t3 : t2;
+            n_job = j3 ? sreg(jobs.n[3]) : sreg(jobs.n[2]);
+            wj = reinterpret_cast<const uint8_t*>(j3 ? sreg(jobs.w[3]) : sreg(jobs.w[2]));
+        }
+    }
+    const int row0 = 16 * (t - tile_base);
     // Row-major blocks: the tile's rows are rb apart and block b sits at
     // b * 144 in its row.  Tiled: the tile's block b is 2304 contiguous bytes
     // at (tile * nb + b) * 2304, rows past N stored as zeros.
@@ -129,7 +128,7 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(const Jobs jobs,
                                : static_cast<int64_t>(row0) * rb + static_cast<int64_t>(b0) * kQ4kBlockBytes;
     const int64_t job_bytes = TILED ? static_cast<int64_t>((n_job + 15) >> 4) * 16 * rb
                                     : static_cast<int64_t>(n_job) * rb;
-    const uint8_t* const tbase = reinterpret_cast<const uint8_t*>(sj.w[job]) + off0;
+    const uint8_t* const tbase = wj + off0;
     const int64_t tleft = job_bytes - off0;
     const TLane tl = make_tlane(lane);
 
@@ -200,7 +199,8 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(const Jobs jobs,
     v += __shfl_xor(v, 32, kWave);
     const int row = row0 + ln.n;
     const bool keep = row < n_job;  // false for tile slots past the last tile
-    float* const yj = reinterpret_cast<float*>(sj.y[job]);
+    const Four<uint64_t> ys = {sreg(jobs.y[0]), sreg(jobs.y[1]), sreg(jobs.y[2]), sreg(jobs.y[3])};
+    float* const yj = reinterpret_cast<float*>(ys[job]);
     if (KS == 1) {
         if (lane < 16 && keep) yj[row] = v;
     } else {
@@ -223,7 +223,8 @@ hipError_t run(const Jobs& jobs, const float* x, int64_t k, int ks, int waves, h
     const int64_t wgs = (static_cast<int64_t>(jobs.total) + tpw - 1) / tpw;
     const size_t lds = lds_bytes(static_cast<int>(k)) + static_cast<size_t>(waves) * 16 * sizeof(float);
     hipLaunchKernelGGL((k_gemv_q4k_mfma<D, XP, TILED>), dim3(static_cast<unsigned>(wgs)),
-                       dim3(static_cast<unsigned>(waves * kWave)), lds, s, jobs, x, static_cast<int>(k), ks);
+                       dim3(static_cast<unsigned>(waves * kWave)), lds, s, x, static_cast<int>(k), ks,
+                       jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], jobs.count, jobs);
     return hipGetLastError();
 }
 
