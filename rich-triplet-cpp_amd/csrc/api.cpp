@@ -196,7 +196,7 @@ int rt_hip_gemv_q4k_multi(int32_t count, const void* const* blocks, float* const
         int rc = gemv_args("rt_hip_gemv_q4k_multi", blocks[j], x, y[j], n[j], k, 1, 256);
         if (rc) return rc;
     }
-    if (gemv_lds_bytes(RT_HIP_Q4K, 1, k) > 65536)
+    if (q4k_m1_lds_bytes(k) > 65536)
         return fail(RT_HIP_E_SHAPE, "rt_hip_gemv_q4k_multi: k too large");
     return check_stream_launch(launch_gemv_q4k_mfma_multi(count, blocks, y, n, x, k,
                                                           static_cast<hipStream_t>(stream), false),
@@ -229,7 +229,7 @@ int rt_hip_gemv_q4k_tiled_multi(int32_t count, const void* const* tiled, float* 
         int rc = gemv_args("rt_hip_gemv_q4k_tiled_multi", tiled[j], x, y[j], n[j], k, 1, 256);
         if (rc) return rc;
     }
-    if (gemv_lds_bytes(RT_HIP_Q4K, 1, k) > 65536)
+    if (q4k_m1_lds_bytes(k) > 65536)
         return fail(RT_HIP_E_SHAPE, "rt_hip_gemv_q4k_tiled_multi: k too large");
     return check_stream_launch(launch_gemv_q4k_mfma_multi(count, tiled, y, n, x, k,
                                                           static_cast<hipStream_t>(stream), true),

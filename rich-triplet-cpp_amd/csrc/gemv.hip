@@ -509,7 +509,7 @@ size_t gemv_lds_bytes(int fmt, int m, int64_t k) {
 hipError_t launch_gemv_q4k(const void* w, const float* x, float* y, int64_t n, int64_t k, int m,
                            hipStream_t s) {
     // M == 1 (decode) runs on int8 MFMA; small batches on the VALU kernel.
-    if (m == 1) return launch_gemv_q4k_mfma(w, x, y, n, k, s);
+    if (m == 1 && q4k_m1_lds_bytes(k) <= 65536) return launch_gemv_q4k_mfma(w, x, y, n, k, s);
     // Q4_K pieces per row = 8 * K/256, so L >= 8 always.
     return dispatch<Q4kFmt, 8, false>(w, x, y, n, k, m, nullptr, s, RT_HIP_Q4K);
 }

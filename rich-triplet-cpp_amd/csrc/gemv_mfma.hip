@@ -34,6 +34,14 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// s_waitcnt vmcnt(N) alone (gfx9 encoding: vmcnt bits [3:0] and [15:14],
+// expcnt [6:4] and lgkmcnt [11:8] left at their no-wait maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // Job table passed by value: job j owns tiles [tile0[j], tile0[j + 1]), the
 // last one up to `total`; unused entries hold `total`.
 struct Jobs {
@@ -69,12 +77,13 @@ __device__ __forceinline__ uint64_t sreg(const void* p) {
 // with -amdgpu-kernarg-preload-count), so x and the weight prologue issue
 // without waiting for a kernel-argument load.  Jobs 2 and 3 (and every
 // output pointer) come from the table.
-template <int D, int XP, bool TILED>
+template <int D, int XP, bool TILED, bool J34>
 __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
-    const float* __restrict__ X, int K, int KS, const uint8_t* w0, const uint8_t* w1, int n0, int n1,
-    int tile1, int count, const Jobs jobs) {
+    const float* __restrict__ X, int K, int KS, int nthreads, const uint8_t* w0, const uint8_t* w1,
+    int n0, int n1, int tile1, int count, const Jobs jobs) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const int nthreads = static_cast<int>(blockDim.x);
+    // nthreads == blockDim.x, passed as a preloaded argument: blockDim
+    // itself is a kernel-argument load that the first x loads would wait for.
     const int TPW = (nthreads >> 6) / KS;  // tiles per workgroup
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -87,16 +96,17 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
     const int64_t rb = static_cast<int64_t>(nb) * kQ4kBlockBytes;
     const uint32_t roff = static_cast<uint32_t>(ln.n * rb);
     const int nx = K >> 2;
-    const f32x4* X4 = reinterpret_cast<const f32x4*>(X);
 
-    // x first: its loads complete before the weight prologue's.
-    f32x4 xv[XP];
-#pragma unroll
-    for (int i = 0; i < XP; ++i) {
-        const int f = tid + nthreads * i;
-        xv[i] = X4[f < nx ? f : 0];
+    // x first, copied straight into LDS (raw f32 at [0, 4K)) in 1 KB
+    // chunks spread over the waves.  The copies write LDS, so the compiler
+    // keeps them ahead of the weight prologue (plain register loads of x got
+    // sunk below it, and waiting for x then meant waiting for every weight
+    // load); vmcnt counts them in order, so waiting for them is partial.
+    const int nwaves = nthreads >> 6;
+    for (int c = wave; c < (K >> 8); c += nwaves) {
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(X + c * 256 + lane * 4),
+                                         (__attribute__((address_space(3))) void*)(lds + c * 1024), 16, 0, 0);
     }
-    __builtin_amdgcn_sched_barrier(0);
 
     // This wave's tile: job and first row (wave-uniform).  A tile slot past
     // the last tile belongs to the last job with rows past its end, so its
@@ -108,8 +118,10 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
     tile_base = job ? tile1 : 0;
     n_job = job ? n1 : n0;
     wj = job ? w1 : w0;
-    if (count > 2) {
-        // jobs 2 and 3 (a layer's k/v after q): from the table
+    if (J34 && count > 2) {
+        // jobs 2 and 3 (a layer's k/v after q): from the table.  A separate
+        // instantiation, so that launches of one or two jobs never wait for
+        // a table load before their first weight load.
         const int t2 = sreg(jobs.tile0[2]), t3 = sreg(jobs.tile0[3]);
         if (t >= t2) {
             const bool j3 = count > 3 && t >= t3;
@@ -162,14 +174,26 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // Every lane converts its prefetched values (past the end: a dummy that
-    // is not stored), so the loads are consumed where they were issued.
+    // This wave's copies of x are older than the 3*D prologue loads: wait
+    // for them alone, then for every wave's.  Then x goes to registers
+    // (XP * nthreads >= K/4, checked by the host) and, once every wave has
+    // read it, its LDS area becomes the limb planes.
+    wait_vmcnt<3 * D>();
+    lds_barrier();
+    f32x4 xv[XP];
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+        const int f = tid + nthreads * i;
+        xv[i] = *reinterpret_cast<const f32x4*>(lds + 16 * (f < nx ? f : 0));
+    }
+    lds_barrier();
+    // Every lane converts its values (past the end: a dummy that is not
+    // stored; the 8-lane reductions need the whole group).
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
         const int f = tid + nthreads * i;
         limbs_of(xv[i], lds, K, f, f < nx);
     }
-    for (int f = tid + nthreads * XP; f < nx; f += nthreads) limbs_of(X4[f], lds, K, f);
     if (tid < 4) reinterpret_cast<u32x4*>(lds + 3 * static_cast<size_t>(K))[tid] = u32x4{0u, 0u, 0u, 0u};
     lds_barrier();
 
@@ -204,7 +228,7 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
     if (KS == 1) {
         if (lane < 16 && keep) yj[row] = v;
     } else {
-        float* red = reinterpret_cast<float*>(lds + lds_bytes(K));  // [TPW][KS][16]
+        float* red = reinterpret_cast<float*>(lds + stage_bytes(K));  // [TPW][KS][16]
         float* rp = red + tslot * KS * 16;
         if (lane < 16) rp[ks * 16 + lane] = v;
         lds_barrier();
@@ -217,14 +241,15 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
     }
 }
 
-template <int D, int XP, bool TILED>
+template <int D, int XP, bool TILED, bool J34>
 hipError_t run(const Jobs& jobs, const float* x, int64_t k, int ks, int waves, hipStream_t s) {
     const int tpw = waves / ks;
     const int64_t wgs = (static_cast<int64_t>(jobs.total) + tpw - 1) / tpw;
-    const size_t lds = lds_bytes(static_cast<int>(k)) + static_cast<size_t>(waves) * 16 * sizeof(float);
-    hipLaunchKernelGGL((k_gemv_q4k_mfma<D, XP, TILED>), dim3(static_cast<unsigned>(wgs)),
+    const size_t lds = mfma_gemv_lds_bytes(k, waves);
+    hipLaunchKernelGGL((k_gemv_q4k_mfma<D, XP, TILED, J34>), dim3(static_cast<unsigned>(wgs)),
                        dim3(static_cast<unsigned>(waves * kWave)), lds, s, x, static_cast<int>(k), ks,
-                       jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], jobs.count, jobs);
+                       waves * kWave, jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], jobs.count,
+                       jobs);
     return hipGetLastError();
 }
 
@@ -233,9 +258,17 @@ hipError_t run(const Jobs& jobs, const float* x, int64_t k, int ks, int waves, h
 template <int D, bool TILED>
 hipError_t run_xp(const Jobs& jobs, const float* x, int64_t k, int ks, int waves, hipStream_t s) {
     const int64_t per = (k / 4 + waves * kWave - 1) / (waves * kWave);
-    if (per <= 2) return run<D, 2, TILED>(jobs, x, k, ks, waves, s);
-    if (per <= 4) return run<D, 4, TILED>(jobs, x, k, ks, waves, s);
-    return run<D, 8, TILED>(jobs, x, k, ks, waves, s);
+    if (per > 16) return hipErrorInvalidValue;  // the host keeps K within the staging bound
+    if (jobs.count > 2) {
+        if (per <= 2) return run<D, 2, TILED, true>(jobs, x, k, ks, waves, s);
+        if (per <= 4) return run<D, 4, TILED, true>(jobs, x, k, ks, waves, s);
+        if (per <= 8) return run<D, 8, TILED, true>(jobs, x, k, ks, waves, s);
+        return run<D, 16, TILED, true>(jobs, x, k, ks, waves, s);
+    }
+    if (per <= 2) return run<D, 2, TILED, false>(jobs, x, k, ks, waves, s);
+    if (per <= 4) return run<D, 4, TILED, false>(jobs, x, k, ks, waves, s);
+    if (per <= 8) return run<D, 8, TILED, false>(jobs, x, k, ks, waves, s);
+    return run<D, 16, TILED, false>(jobs, x, k, ks, waves, s);
 }
 
 // K-split per tile.  One round of workgroups (at most one per CU) is what
@@ -272,6 +305,12 @@ hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s) 
 }
 
 }  // namespace
+
+size_t mfma_gemv_lds_bytes(int64_t k, int waves) {
+    return stage_bytes(static_cast<int>(k)) + static_cast<size_t>(waves) * 16 * sizeof(float);
+}
+
+size_t q4k_m1_lds_bytes(int64_t k) { return mfma_gemv_lds_bytes(k, kMaxThreads / kWave); }
 
 hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* const* y,
                                       const int64_t* n, const float* x, int64_t k, hipStream_t s,

@@ -36,6 +36,12 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 __host__ __device__ inline size_t lds_bytes(int K) {
     return 3 * static_cast<size_t>(K) + 64 + static_cast<size_t>(K / 32) * 16;
 }
+// The GEMV first lands x as raw f32 in the same area, so it needs the
+// larger of the two (4K bytes for every K > 128).
+__host__ __device__ inline size_t stage_bytes(int K) {
+    const size_t raw = 4 * static_cast<size_t>(K), limbs = lds_bytes(K);
+    return raw > limbs ? raw : limbs;
+}
 
 // DPP lane swizzles within a row of 16 lanes (VALU, no LDS round trip).
 constexpr int kDppQuadSwap1 = 0xb1;    // quad_perm [1,0,3,2]: lane ^ 1

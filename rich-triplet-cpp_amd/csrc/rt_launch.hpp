@@ -36,6 +36,10 @@ hipError_t launch_gemv_q4k_mfma(const void* w, const float* x, float* y, int64_t
 hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* const* y,
                                       const int64_t* n, const float* x, int64_t k, hipStream_t s,
                                       bool tiled);
+// LDS of the M = 1 Q4_K GEMV for `waves` waves per workgroup, and its
+// worst case over the splits it picks (the callers' K bound: <= 64 KB).
+size_t mfma_gemv_lds_bytes(int64_t k, int waves);
+size_t q4k_m1_lds_bytes(int64_t k);
 hipError_t launch_q4k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, hipStream_t s);
 hipError_t launch_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
                             int m, uint64_t* argmax_key, hipStream_t s);
