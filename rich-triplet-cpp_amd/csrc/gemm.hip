@@ -181,6 +181,259 @@ __global__ __launch_bounds__(256) void k_gemm(const void* __restrict__ Ap,
     }
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined kernel (K % 256 == 0): bf16 A, Q4_K or bf16 W.
+//
+// LDS tiles are 128 rows x 64 bf16 (128 B per row, unpadded) with the 16-byte
+// chunk c of row r stored at chunk slot c ^ (r & 7), so the MFMA fragment
+// reads (16 rows x one chunk) are conflict-free and whole tiles can be
+// written by direct-to-LDS buffer loads (1 KB per wave instruction: 8 rows).
+//  * A (and a bf16 W) stream through a ring of kStages LDS tiles, copied by
+//    buffer loads straight into LDS kStages-1 steps ahead; rows past M (N)
+//    read as zeros through the buffer range check.
+//  * A Q4_K W goes through a ring of kRing register slots (header + 16 qs
+//    bytes per thread and step), kRing steps ahead, and is dequantized into
+//    one of two LDS tiles one step ahead of its use: w = (d*sv)*q - dmin*mv
+//    exact in f32, then round-to-nearest-even bf16 (v_cvt_pk_bf16_f32), as
+//    the reference's flux_dequant_q4k (shaders/flux.msl:69-81).
+//  * One barrier per 64-wide K step.  Tiles are assigned XCD by XCD (a
+//    workgroup's XCD is its id mod 8), each XCD getting a contiguous range
+//    of a grouped tile order (8 M-tiles per N column), so the tiles resident
+//    on an XCD at once share A rows and W rows in its L2.
+constexpr int kPThreads = 256;
+constexpr int kStages = 4;
+constexpr int kTile = 128 * 128;    // bytes of one 128 x 64 bf16 tile
+constexpr int kRawStage = 8192;     // raw Q4_K bytes of one step: headers 4 KB, qs 4 KB
+constexpr int kGroupM = 8;
+
+__device__ __forceinline__ uint32_t swz(int r, int c) {
+    return static_cast<uint32_t>(r * 128 + ((c ^ (r & 7)) << 4));
+}
+
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// s_waitcnt vmcnt(N) alone (vmcnt bits [3:0] and [15:14]; expcnt, lgkmcnt
+// left at their no-wait maxima).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier that waits for this wave's LDS traffic only (not for its
+// global loads and copies in flight).
+__device__ __forceinline__ void lds_sync() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <bool W_Q4K>
+__global__ __launch_bounds__(kPThreads) void k_gemm_pipe(const uint16_t* __restrict__ A,
+                                                         const void* __restrict__ Wp,
+                                                         const float* __restrict__ bias,
+                                                         float* __restrict__ C, int M, int N, int K,
+                                                         int mt) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    uint8_t* const sA = lds;                        // [kStages][kTile]
+    uint8_t* const sW = lds + kStages * kTile;      // bf16: [kStages][kTile]; Q4_K: [2][kTile] + raw ring
+
+    // XCD-contiguous tile id, then grouped order: consecutive ids walk
+    // kGroupM M-tiles of one N column before the next column, so the tiles
+    // resident together share A rows and W rows in L2.
+    const int G = static_cast<int>(gridDim.x), bid = static_cast<int>(blockIdx.x);
+    const int xcd = bid & 7, idx = bid >> 3, q8 = G >> 3, r8 = G & 7;
+    const int tile = xcd < r8 ? xcd * (q8 + 1) + idx : r8 * (q8 + 1) + (xcd - r8) * q8 + idx;
+    const int nt = G / mt;
+    const int group = tile / (kGroupM * nt), first_m = group * kGroupM;
+    const int gm = min(mt - first_m, kGroupM);
+    const int m0 = (first_m + (tile % (kGroupM * nt)) % gm) * 128;
+    const int n0 = ((tile % (kGroupM * nt)) / gm) * 128;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int S = K >> 6;
+    const int64_t rowA = static_cast<int64_t>(K) * 2;
+
+    // Copy roles: wave instruction i (0..3) covers tile rows 8*(4*wave+i) ..
+    // +7; lane l fills chunk slot l%8 of row 8*(4*wave+i) + l/8, i.e. global
+    // chunk (l%8) ^ (row & 7).
+    uint32_t coff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 8 * (4 * wave + i) + (lane >> 3);
+        coff[i] = static_cast<uint32_t>(r * rowA + (((lane & 7) ^ (r & 7)) << 4));
+    }
+    const uint8_t* const Ab = reinterpret_cast<const uint8_t*>(A) + static_cast<int64_t>(m0) * rowA;
+    const int64_t Aleft = static_cast<int64_t>(M - m0) * rowA;
+    auto copy_tile = [&](uint8_t* dst, const uint8_t* base, int64_t left, int step) {
+        const int64_t o = static_cast<int64_t>(step) * 128;  // 64 bf16 per step
+        const BufRsrc rs = make_rsrc(base + o, step < S ? left - o : 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void*)(dst + (4 * wave + i) * 1024), 16,
+                static_cast<int>(coff[i]), 0, 0, 0);
+    };
+    const uint8_t* const Wb16 = static_cast<const uint8_t*>(Wp) + static_cast<int64_t>(n0) * rowA;
+    const int64_t Wleft16 = static_cast<int64_t>(N - n0) * rowA;
+
+    // Q4_K: the raw bytes of a step (per tile row: the super-block header
+    // and the step's 32-byte qs chunk) are copied straight into a raw ring
+    // of kStages LDS stages (kRawStage bytes each): wave w copies rows
+    // 32w .. 32w+31, one instruction for their headers (lanes 0-31; lanes
+    // 32-63 read past the resource and load nothing) and one for their qs
+    // (lane l: row 32w + l/2, half l%2).  Dequantized one step ahead by
+    // thread (row sr, half sh) into one of two bf16 LDS tiles.
+    const int nb = K >> 8;
+    const int64_t rbq = static_cast<int64_t>(nb) * kQ4kBlockBytes;
+    const uint8_t* const Wq = static_cast<const uint8_t*>(Wp) + static_cast<int64_t>(n0) * rbq;
+    const int64_t Wleftq = static_cast<int64_t>(N - n0) * rbq;
+    const uint32_t hoff = lane < 32 ? static_cast<uint32_t>((32 * wave + lane) * rbq) : 0x7fffffffu;
+    const uint32_t qoff = static_cast<uint32_t>((32 * wave + (lane >> 1)) * rbq) + 16u + 16u * (lane & 1);
+    auto copy_q4k = [&](uint8_t* raw, int step) {
+        const int b = step >> 2, c = step & 3;
+        const int64_t o = static_cast<int64_t>(b) * kQ4kBlockBytes;
+        const BufRsrc rs = make_rsrc(Wq + o, step < S ? Wleftq - o : 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (__attribute__((address_space(3))) void*)(raw + wave * 1024), 16, static_cast<int>(hoff), 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (__attribute__((address_space(3))) void*)(raw + 4096 + wave * 1024), 16,
+            static_cast<int>(qoff + 32u * static_cast<uint32_t>(c)), 0, 0, 0);
+    };
+    // Values k0 + 16 sh .. +15 (low nibbles, sub-block 2c) and k0 + 32 + 16 sh
+    // .. +15 (high nibbles, sub-block 2c + 1) of row sr: chunks 2 sh, 2 sh + 1,
+    // 4 + 2 sh, 5 + 2 sh of the tile row.
+    const int sr = tid >> 1, sh = tid & 1;
+    auto dequant = [&](const uint8_t* raw, uint8_t* dst, int step) {
+        const int c = step & 3;
+        const u32x4 h = *reinterpret_cast<const u32x4*>(raw + (sr >> 5) * 1024 + (sr & 31) * 16);
+        const u32x4 qv = *reinterpret_cast<const u32x4*>(raw + 4096 + sr * 32 + sh * 16);
+        const float d = f16_bits_to_f32(h[0] & 0xffffu), dm = f16_bits_to_f32(h[0] >> 16);
+        uint32_t sv1, mv1, sv2, mv2;
+        decode_scale_min(make_scale_sel(2 * c), h[1], h[2], h[3], sv1, mv1);
+        decode_scale_min(make_scale_sel(2 * c + 1), h[1], h[2], h[3], sv2, mv2);
+        const float s1 = d * static_cast<float>(sv1), n1 = dm * static_cast<float>(mv1);
+        const float s2 = d * static_cast<float>(sv2), n2 = dm * static_cast<float>(mv2);
+        u32x4 lo[2], hi[2];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t wl = qv[j] & 0x0f0f0f0fu, wh = (qv[j] >> 4) & 0x0f0f0f0fu;
+            lo[j >> 1][2 * (j & 1)] = pk_bf16(s1 * ubyte_f32(wl, 0) - n1, s1 * ubyte_f32(wl, 1) - n1);
+            lo[j >> 1][2 * (j & 1) + 1] = pk_bf16(s1 * ubyte_f32(wl, 2) - n1, s1 * ubyte_f32(wl, 3) - n1);
+            hi[j >> 1][2 * (j & 1)] = pk_bf16(s2 * ubyte_f32(wh, 0) - n2, s2 * ubyte_f32(wh, 1) - n2);
+            hi[j >> 1][2 * (j & 1) + 1] = pk_bf16(s2 * ubyte_f32(wh, 2) - n2, s2 * ubyte_f32(wh, 3) - n2);
+        }
+        *reinterpret_cast<u32x4*>(dst + swz(sr, 2 * sh)) = lo[0];
+        *reinterpret_cast<u32x4*>(dst + swz(sr, 2 * sh + 1)) = lo[1];
+        *reinterpret_cast<u32x4*>(dst + swz(sr, 4 + 2 * sh)) = hi[0];
+        *reinterpret_cast<u32x4*>(dst + swz(sr, 5 + 2 * sh)) = hi[1];
+    };
+    uint8_t* const sRaw = sW + 2 * kTile;  // Q4_K: [kStages][kRawStage]
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int fr = lane & 15, fc = lane >> 4;
+    auto mfma_step = [&](const uint8_t* ta, const uint8_t* tw) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            bf16x8 af[4], bf[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                af[i] = *reinterpret_cast<const bf16x8*>(ta + swz(wm + 16 * i + fr, 4 * ks + fc));
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                bf[j] = *reinterpret_cast<const bf16x8*>(tw + swz(wn + 16 * j + fr, 4 * ks + fc));
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // Prologue: copies of steps 0 .. kStages-2; step 0's W dequantized.
+#pragma unroll
+    for (int j = 0; j < kStages - 1; ++j) {
+        if constexpr (W_Q4K) {
+            copy_q4k(sRaw + j * kRawStage, j);
+            copy_tile(sA + j * kTile, Ab, Aleft, j);
+        } else {
+            copy_tile(sA + j * kTile, Ab, Aleft, j);
+            copy_tile(sW + j * kTile, Wb16, Wleft16, j);
+        }
+    }
+    wait_vm<0>();
+    lds_sync();
+    if constexpr (W_Q4K) {
+        dequant(sRaw, sW, 0);
+        lds_sync();
+    }
+
+    // Step s: copy step t = s+kStages-1 (Q4_K: raw W, then A; bf16: A, then
+    // W); (Q4_K) dequantize step s+1 into the other bf16 W tile; MFMAs of
+    // step s; wait for this wave's copies that step s+1 needs, then the
+    // barrier.  Copies are ordered and counted by vmcnt: after the last one
+    // step s+1 needs (Q4_K: raw W of step s+2, for its dequant; bf16: W of
+    // s+1) this wave has issued 10 (Q4_K: A(s+2), raw(s+3), A(s+3)) or 16
+    // (bf16: A, W of s+2 and s+3) more.  kStages == 4 and S % 4 == 0: the
+    // unrolled round keeps every ring index a compile-time constant.
+    static_assert(kStages == 4, "the unrolled round assumes a 4-stage ring");
+    for (int s0 = 0; s0 < S; s0 += 4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int s = s0 + j;
+            const int t = (j + kStages - 1) % kStages;
+            if constexpr (W_Q4K) {
+                copy_q4k(sRaw + t * kRawStage, s + kStages - 1);
+                copy_tile(sA + t * kTile, Ab, Aleft, s + kStages - 1);
+                dequant(sRaw + ((j + 1) % kStages) * kRawStage, sW + ((j + 1) & 1) * kTile, s + 1);
+                mfma_step(sA + j * kTile, sW + (j & 1) * kTile);
+                wait_vm<10>();
+            } else {
+                copy_tile(sA + t * kTile, Ab, Aleft, s + kStages - 1);
+                copy_tile(sW + t * kTile, Wb16, Wleft16, s + kStages - 1);
+                mfma_step(sA + j * kTile, sW + j * kTile);
+                wait_vm<16>();
+            }
+            lds_sync();
+        }
+    }
+
+    // Epilogue (+ bias).
+    const int cr = 4 * (lane >> 4), cc = lane & 15;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int col = n0 + wn + 16 * j + cc;
+        if (col >= N) continue;
+        const float bv = bias ? bias[col] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + wm + 16 * i + cr + r;
+                if (row < M) C[static_cast<size_t>(row) * N + col] = acc[i][j][r] + bv;
+            }
+        }
+    }
+}
+
+// f32 -> bf16 round-to-nearest-even, 8 values per thread.
+__global__ __launch_bounds__(256) void k_f32_to_bf16(const float* __restrict__ x,
+                                                     uint16_t* __restrict__ y, int64_t n8) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n8) return;
+    const f32x4 a = reinterpret_cast<const f32x4*>(x)[2 * i];
+    const f32x4 b = reinterpret_cast<const f32x4*>(x)[2 * i + 1];
+    reinterpret_cast<u32x4*>(y)[i] = u32x4{pk_bf16(a[0], a[1]), pk_bf16(a[2], a[3]),
+                                           pk_bf16(b[0], b[1]), pk_bf16(b[2], b[3])};
+}
+
 __global__ void k_add_bias(float* __restrict__ y, const float* __restrict__ bias, int64_t m,
                            int64_t n) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -191,8 +444,50 @@ __global__ void k_add_bias(float* __restrict__ y, const float* __restrict__ bias
 
 hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, const float* bias,
                        float* c, int64_t m, int64_t n, int64_t k, hipStream_t s) {
-    const dim3 grid(static_cast<unsigned>((n + BN - 1) / BN), static_cast<unsigned>((m + BM - 1) / BM));
     if (k % BK) return hipErrorInvalidValue;
+    if (k % 256 == 0 && (w_fmt == RT_HIP_Q4K || w_fmt == RT_HIP_BF16)) {
+        // Pipelined kernel on bf16 A (f32 A converted once into the
+        // workspace).  A Q4_K weight used by more than one M tile is
+        // dequantized once into the workspace (bf16, round-to-nearest-even of
+        // the exact f32 value, as the fused path and the reference's
+        // flux_dequant_q4k) instead of once per M tile inside the GEMM.
+        const int64_t mt = (m + 127) / 128, nt = (n + 127) / 128;
+        const bool fused_q4k = w_fmt == RT_HIP_Q4K && mt == 1;
+        const size_t a_bytes = a_bf16 ? 0 : static_cast<size_t>(m * k) * 2;
+        const size_t w_bytes = (w_fmt == RT_HIP_Q4K && !fused_q4k) ? static_cast<size_t>(n * k) * 2 : 0;
+        uint8_t* ws = nullptr;
+        if (a_bytes + w_bytes) {
+            hipError_t e;
+            ws = static_cast<uint8_t*>(workspace(a_bytes + w_bytes, &e));
+            if (!ws) return e;
+        }
+        const uint16_t* a16 = static_cast<const uint16_t*>(a);
+        if (!a_bf16) {
+            uint16_t* ab = reinterpret_cast<uint16_t*>(ws);
+            const int64_t n8 = m * k / 8;
+            hipLaunchKernelGGL(k_f32_to_bf16, dim3(static_cast<unsigned>((n8 + 255) / 256)), dim3(256), 0, s,
+                               static_cast<const float*>(a), ab, n8);
+            a16 = ab;
+        }
+        if (w_bytes) {
+            const hipError_t e = launch_dequant_q4k(w, ws + a_bytes, true, n, k, s);
+            if (e != hipSuccess) return e;
+            w = ws + a_bytes;
+        }
+        const bool q4k = fused_q4k;
+        const size_t lds = q4k ? static_cast<size_t>(kStages + 2) * kTile + kStages * kRawStage
+                               : static_cast<size_t>(2 * kStages) * kTile;
+        if (q4k)
+            hipLaunchKernelGGL((k_gemm_pipe<true>), dim3(static_cast<unsigned>(mt * nt)), dim3(kPThreads), lds, s,
+                               a16, w, bias, c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
+                               static_cast<int>(mt));
+        else
+            hipLaunchKernelGGL((k_gemm_pipe<false>), dim3(static_cast<unsigned>(mt * nt)), dim3(kPThreads), lds, s,
+                               a16, w, bias, c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
+                               static_cast<int>(mt));
+        return hipGetLastError();
+    }
+    const dim3 grid(static_cast<unsigned>((n + BN - 1) / BN), static_cast<unsigned>((m + BM - 1) / BM));
     if (w_fmt == RT_HIP_Q4K) {
         if (a_bf16)
             hipLaunchKernelGGL((k_gemm<RT_HIP_Q4K, true>), grid, dim3(256), 0, s, a, w, bias, c,
