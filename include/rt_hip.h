@@ -111,6 +111,41 @@ int rt_hip_gemv_q4k_tiled(const void* tiled, const float* x, float* y, int64_t n
 int rt_hip_gemv_q4k_tiled_multi(int32_t count, const void* const* tiled, float* const* y,
                                 const int64_t* n, const float* x, int64_t k, rt_hip_stream stream);
 
+/* ---- decode chain: a step's dependent GEMV stages in one launch -----------
+ * Replace: MetalDecodeContext::create / decode_step, the per-token sequence
+ * of GEMV dispatches encoded into one command buffer
+ * (include/rt/metal_decode.hpp:41-69, src/metal_decode.mm:436-482).
+ *
+ * A stage is one tiled-Q4_K GEMV, or up to four that share x (q/k/v,
+ * gate/up), exactly as rt_hip_gemv_q4k_tiled_multi.  Stage s starts reading
+ * x only after every earlier stage has stored its outputs, so x may point at
+ * an earlier stage's y.  The chain runs as one persistent launch (one
+ * workgroup per CU); each CU loads its share of stage s+1's weights while
+ * stage s finishes elsewhere.
+ *
+ * create validates the stages and copies them to the device (the pointers
+ * are baked in: buffers must outlive the chain).  run launches one pass and
+ * allocates nothing, so it can be captured in a hipGraph.  Runs of one chain
+ * must not overlap (one stream, or ordered streams).  status waits for the
+ * device and reports RT_HIP_E_HIP if a stage barrier timed out in an earlier
+ * run (the outputs of that run are then invalid); reset != 0 also re-arms
+ * the chain's barrier flags.  Results match rt_hip_gemv_q4k_tiled_multi to
+ * f32 rounding (same tile arithmetic; the K split may differ).
+ * Limits: 1 <= k / 256 <= 32 (k <= 8192), 1..4 jobs per stage. */
+typedef struct rt_hip_chain_stage {
+    const float* x;        /* activation [k], device */
+    int64_t k;             /* in_features, multiple of 256 */
+    int32_t count;         /* GEMVs sharing x: 1..4 */
+    const void* w[4];      /* tiled Q4_K weights (rt_hip_q4k_tile) */
+    float* y[4];           /* outputs [n[j]] */
+    int64_t n[4];          /* out_features */
+} rt_hip_chain_stage;
+typedef struct rt_hip_chain rt_hip_chain;
+int rt_hip_chain_create(const rt_hip_chain_stage* stages, int32_t count, rt_hip_chain** out);
+int rt_hip_chain_run(rt_hip_chain* chain, rt_hip_stream stream);
+int rt_hip_chain_status(rt_hip_chain* chain, int32_t reset);
+int rt_hip_chain_destroy(rt_hip_chain* chain);
+
 /* Replace: MatBf16::matmul_by_t for M <= 8 (src/mat.cpp:318-414); Metal
  * metal_gemv_bf16_t (metal_ops.hpp:64-65) and gemv_bf16_t / _batch
  * (decode_gemma3.msl:390-518).  Requires K % 8 == 0. */
@@ -159,8 +194,10 @@ int rt_hip_quantize_q4k(const float* w, void* blocks, int64_t n, int64_t k,
  * Replace: Q4KMat::matmul_q4k_t_exact (src/quant_q4k.cpp:636-710) and
  * QLinear::forward (src/qlinear.cpp:55-80); the FLUX gemm_into sequence
  * flux_dequant_q4k + flux_gemm_bt + flux_add_bias (src/metal_flux.mm:155-185,
- * src/shaders/flux.msl:51-143).  The Q4_K weight is dequantized into LDS tile
- * by tile; no dequantized copy is ever written to HBM.  K % 256 == 0. */
+ * src/shaders/flux.msl:51-143).  When M fits one 128-row tile the Q4_K
+ * weight is dequantized into LDS tile by tile; for larger M it is dequantized
+ * once into the library workspace as bf16 (the same bits), as
+ * flux_dequant_q4k does, and shared by every M tile.  K % 256 == 0. */
 int rt_hip_gemm_q4k(const void* a, int32_t a_dtype, const void* blocks, const float* bias,
                     float* c, int64_t m, int64_t n, int64_t k, rt_hip_stream stream);
 /* Replace: MatBf16::matmul_by_t for M > 1 (src/mat.cpp:351-414).  K % 64 == 0. */

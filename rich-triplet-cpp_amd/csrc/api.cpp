@@ -241,6 +241,125 @@ int rt_hip_gemv_q4k_tiled(const void* tiled, const float* x, float* y, int64_t n
     return rt_hip_gemv_q4k_tiled_multi(1, &tiled, &y, &n, x, k, stream);
 }
 
+}  // extern "C"
+
+struct rt_hip_chain {
+    int device = -1;
+    void* stages = nullptr;  // device Stage table
+    int nst = 0;
+    uint32_t* sync = nullptr;  // flags, group flags, error word
+    size_t sync_words = 0;
+    int grid = 0;
+    int ring = 8;
+};
+
+extern "C" {
+
+int rt_hip_chain_create(const rt_hip_chain_stage* stages, int32_t count, rt_hip_chain** out) {
+    const char* fn = "rt_hip_chain_create";
+    if (!out) return fail(RT_HIP_E_ARG, std::string(fn) + ": null output");
+    *out = nullptr;
+    if (!stages || count < 1) return fail(RT_HIP_E_ARG, std::string(fn) + ": need at least one stage");
+    hipError_t e;
+    DeviceState* ds = state_for_current(&e);
+    if (!ds) return hip_fail(e, fn);
+    const int waves = chain_waves_per_wg();
+    const int grid = ds->info.cus;
+    if (grid < 1 || grid > chain_max_grid()) return fail(RT_HIP_E_UNSUPPORTED, std::string(fn) + ": CU count");
+    const int ring = 4;
+    // Every workgroup must be resident at once (the stage barrier waits for
+    // all of them): one per CU.
+    int per_cu = 0;
+    e = chain_occupancy(ring, &per_cu);
+    if (e != hipSuccess) return hip_fail(e, fn);
+    if (per_cu < 1) return fail(RT_HIP_E_UNSUPPORTED, std::string(fn) + ": chain kernel does not fit a CU");
+
+    const size_t sb = chain_stage_bytes();
+    std::vector<uint8_t> table(sb * static_cast<size_t>(count));
+    for (int32_t s = 0; s < count; ++s) {
+        const rt_hip_chain_stage& st = stages[s];
+        const std::string at = std::string(fn) + ": stage " + std::to_string(s);
+        if (st.count < 1 || st.count > RT_HIP_MULTI_MAX) return fail(RT_HIP_E_ARG, at + ": count must be in [1, 4]");
+        if (!st.x || !aligned16(st.x)) return fail(RT_HIP_E_ALIGN, at + ": x must be non-null and 16-byte aligned");
+        if (st.k <= 0 || st.k % 256 != 0) return fail(RT_HIP_E_ALIGN, at + ": k must be a positive multiple of 256");
+        if (st.k > chain_max_k()) return fail(RT_HIP_E_SHAPE, at + ": k above 8192");
+        int tile0[4] = {0, 0, 0, 0};
+        int64_t tiles = 0;
+        for (int j = 0; j < st.count; ++j) {
+            if (!st.w[j] || !st.y[j] || !aligned16(st.w[j]))
+                return fail(RT_HIP_E_ARG, at + ": null or unaligned weight/output");
+            if (st.n[j] <= 0 || st.n[j] > (1 << 26)) return fail(RT_HIP_E_SHAPE, at + ": n out of range");
+            tile0[j] = static_cast<int>(tiles);
+            tiles += (st.n[j] + 15) / 16;
+        }
+        if (tiles > (1 << 24)) return fail(RT_HIP_E_SHAPE, at + ": too many rows");
+        // K split: the largest of 16, 8, 4, 2 that divides the super-block
+        // count and still gives every wave of the grid at most one share;
+        // outputs with more tiles than waves take several rounds at ks = 1.
+        const int64_t nb = st.k / 256, slots = static_cast<int64_t>(grid) * waves;
+        int ks = 1;
+        for (int c : {16, 8, 4, 2})
+            if (nb % c == 0 && tiles * c <= slots) {
+                ks = c;
+                break;
+            }
+        const int64_t per_round = static_cast<int64_t>(grid) * (waves / ks);
+        const int rounds = static_cast<int>((tiles + per_round - 1) / per_round);
+        chain_fill_stage(table.data() + sb * s, st.x, st.count, st.w, st.y, st.n, st.k, ks,
+                         static_cast<int>(tiles), rounds, tile0);
+    }
+
+    auto* c = new rt_hip_chain();
+    c->device = ds->info.ordinal;
+    c->nst = count;
+    c->grid = grid;
+    c->ring = ring;
+    c->sync_words = chain_sync_words(grid);
+    e = hipMalloc(&c->stages, table.size());
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->sync), c->sync_words * 4);
+    if (e == hipSuccess) e = hipMemcpy(c->stages, table.data(), table.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(c->sync, 0, c->sync_words * 4);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        rt_hip_chain_destroy(c);
+        return e == hipErrorOutOfMemory ? fail(RT_HIP_E_OOM, std::string(fn) + ": device allocation failed")
+                                        : hip_fail(e, fn);
+    }
+    *out = c;
+    return RT_HIP_OK;
+}
+
+int rt_hip_chain_run(rt_hip_chain* chain, rt_hip_stream stream) {
+    if (!chain) return fail(RT_HIP_E_ARG, "rt_hip_chain_run: null chain");
+    return check_stream_launch(launch_chain(chain->stages, chain->nst, chain->sync, chain->grid, chain->ring,
+                                            static_cast<hipStream_t>(stream)),
+                               "rt_hip_chain_run");
+}
+
+int rt_hip_chain_status(rt_hip_chain* chain, int32_t reset) {
+    if (!chain) return fail(RT_HIP_E_ARG, "rt_hip_chain_status: null chain");
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return hip_fail(e, "rt_hip_chain_status");
+    uint32_t err = 0;
+    e = hipMemcpy(&err, chain->sync + chain_err_word(chain->grid), 4, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "rt_hip_chain_status");
+    if (reset) {
+        e = hipMemset(chain->sync, 0, chain->sync_words * 4);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) return hip_fail(e, "rt_hip_chain_status");
+    }
+    if (err) return fail(RT_HIP_E_HIP, "rt_hip_chain_status: a stage barrier timed out; outputs are invalid");
+    return RT_HIP_OK;
+}
+
+int rt_hip_chain_destroy(rt_hip_chain* chain) {
+    if (!chain) return RT_HIP_OK;
+    if (chain->stages) (void)hipFree(chain->stages);
+    if (chain->sync) (void)hipFree(chain->sync);
+    delete chain;
+    return RT_HIP_OK;
+}
+
 int rt_hip_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
                      int32_t m, rt_hip_stream stream) {
     int rc = gemv_args("rt_hip_gemv_bf16", w, x, y, n, k, m, 8);

@@ -41,6 +41,23 @@ hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* co
 size_t mfma_gemv_lds_bytes(int64_t k, int waves);
 size_t q4k_m1_lds_bytes(int64_t k);
 hipError_t launch_q4k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, hipStream_t s);
+
+// Persistent decode chain (chain.hip).  The host builds the stage table with
+// chain_fill_stage (chain_stage_bytes() each) in device memory and a zeroed
+// sync area of chain_sync_words(grid) dwords; launch_chain runs one pass.
+size_t chain_lds_bytes();
+int chain_threads();
+int chain_waves_per_wg();
+int chain_max_k();
+int chain_max_grid();
+size_t chain_sync_words(int grid);
+size_t chain_err_word(int grid);  // index of the error word in the sync area
+size_t chain_stage_bytes();
+void chain_fill_stage(void* dst, const float* x, int count, const void* const* w, float* const* y,
+                      const int64_t* n, int64_t k, int ks, int tiles, int rounds, const int* tile0);
+hipError_t chain_occupancy(int ring, int* blocks_per_cu);
+hipError_t launch_chain(const void* stages, int nst, uint32_t* sync_words, int grid, int ring,
+                        hipStream_t s);
 hipError_t launch_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
                             int m, uint64_t* argmax_key, hipStream_t s);
 // M = 1 BF16 GEMV (gemv_bf16.hip); `key` (may be null) receives the fused

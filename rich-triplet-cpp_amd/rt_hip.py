@@ -39,7 +39,16 @@ _SIGNATURES = {
     "rt_hip_gemm_q4k": [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "rt_hip_gemm_bf16": [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "rt_hip_linear_forward": [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "rt_hip_chain_run": [_vp, _vp],
+    "rt_hip_chain_status": [_vp, _i32],
+    "rt_hip_chain_destroy": [_vp],
 }
+
+
+class ChainStage(C.Structure):
+    """rt_hip_chain_stage (include/rt_hip.h)."""
+    _fields_ = [("x", _vp), ("k", _i64), ("count", _i32), ("w", _vp * 4), ("y", _vp * 4),
+                ("n", _i64 * 4)]
 
 
 class RtHipError(RuntimeError):
@@ -69,6 +78,8 @@ class Library:
         self.lib.rt_hip_version.restype = C.c_char_p
         self.lib.rt_hip_q4k_tiled_bytes.restype = C.c_int64
         self.lib.rt_hip_q4k_tiled_bytes.argtypes = [_i64, _i64]
+        self.lib.rt_hip_chain_create.restype = C.c_int
+        self.lib.rt_hip_chain_create.argtypes = [C.POINTER(ChainStage), _i32, C.POINTER(_vp)]
         for name, args in _SIGNATURES.items():
             fn = getattr(self.lib, name)
             fn.restype = C.c_int
@@ -189,6 +200,46 @@ def gemv_q4k_tiled_multi(ws, x, ns, k: int, ys=None, stream=None):
     npp = (_i64 * count)(*ns)
     library().call("rt_hip_gemv_q4k_tiled_multi", count, wp, yp, npp, _ptr(x), k, _stream(stream))
     return ys
+
+
+class Chain:
+    """A decode step's dependent tiled-Q4_K GEMV stages run as one persistent
+    launch (rt_hip_chain_*).  ``stages`` is a list of (x, [tiled w], [y], [n], k);
+    the tensors must outlive the chain (their pointers are baked in)."""
+
+    def __init__(self, stages):
+        arr = (ChainStage * len(stages))()
+        self._keep = []
+        for i, (x, ws, ys, ns, k) in enumerate(stages):
+            if not 1 <= len(ws) <= 4 or len(ws) != len(ys) or len(ws) != len(ns):
+                raise ValueError("a stage has 1..4 GEMVs with matching w, y, n")
+            _dev_check(x, *ws, *ys)
+            st = arr[i]
+            st.x, st.k, st.count = x.data_ptr(), k, len(ws)
+            for j in range(len(ws)):
+                st.w[j], st.y[j], st.n[j] = ws[j].data_ptr(), ys[j].data_ptr(), ns[j]
+            self._keep += [x, *ws, *ys]
+        h = _vp()
+        library().call("rt_hip_chain_create", arr, len(stages), C.byref(h))
+        self.handle = h
+
+    def run(self, stream=None) -> None:
+        library().call("rt_hip_chain_run", self.handle, _stream(stream))
+
+    def status(self, reset: bool = False) -> int:
+        """0, or the error code if a stage barrier timed out in an earlier run."""
+        return library().status("rt_hip_chain_status", self.handle, 1 if reset else 0)
+
+    def close(self) -> None:
+        if self.handle:
+            library().call("rt_hip_chain_destroy", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001  (interpreter shutdown)
+            pass
 
 
 def gemv_bf16_argmax(w, x, n: int, k: int, y=None, stream=None):
