@@ -155,8 +155,9 @@ class DecodeModel:
 
     def launches(self):
         """The step as launches in model order.  GEMVs that read the same
-        activation and share the Q4_K format run as one multi-job launch
-        (q/k/v, gate/up); a BF16-widened v runs on its own."""
+        activation run as one launch: the Q4_K ones as one multi-job launch
+        (q/k/v, gate/up), and with the tiled layout a BF16-widened v joins
+        its layer's q/k launch (rt_hip_gemv_q4k_tiled_bf16)."""
         out = []
         by = {gv[0]: gv for gv in self.gemvs}
         for layer in range(LAYERS):
@@ -165,6 +166,9 @@ class DecodeModel:
                 gvs = [by[f"L{layer}.{nm}"] for nm in grp]
                 q4 = [gv for gv in gvs if gv[1] == self.rt.Q4K]
                 rest = [gv for gv in gvs if gv[1] != self.rt.Q4K]
+                if self.layout == "tiled" and q4 and len(rest) == 1 and rest[0][1] == self.rt.BF16:
+                    out.append(("fused", (q4, rest[0])))
+                    continue
                 if len(q4) > 1:
                     out.append(("multi", q4))
                 elif q4:
@@ -174,10 +178,17 @@ class DecodeModel:
         out.append(("one", by["lm_head"]))
         return out
 
+    def fused(self, item):
+        q4, (_, _, wb, x, yb, nb, k) = item
+        self.rt.gemv_q4k_tiled_bf16([self.tiled[gv[0]] for gv in q4], [gv[5] for gv in q4], wb, nb, x, k,
+                                    ys=[gv[4] for gv in q4], yb=yb)
+
     def step(self):
         for kind, item in self.plan:
             if kind == "multi":
                 self.q4k_multi(item)
+            elif kind == "fused":
+                self.fused(item)
             else:
                 self.one(item)
 
@@ -324,7 +335,7 @@ def bench_decode(args, rt, torch):
                    "gemvs_per_token": len(model.gemvs), "bytes_per_token": nbytes,
                    "us_per_token": round(us, 2), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
                    "launches_per_token": len(model.plan),
-                   "launch": "one hipGraph per token; q/k/v and gate/up fused per layer",
+                   "launch": "one hipGraph per token; q/k/v (BF16 v included) and gate/up fused per layer",
                    "q4k_layout": ("tiled (rt_hip_q4k_tile once at load; bit-identical results)"
                                   if args.layout == "tiled" else "reference row-major blocks")},
         "roofline": roof, "cpu_baseline": cpu,

@@ -111,6 +111,18 @@ int rt_hip_gemv_q4k_tiled(const void* tiled, const float* x, float* y, int64_t n
 int rt_hip_gemv_q4k_tiled_multi(int32_t count, const void* const* tiled, float* const* y,
                                 const int64_t* n, const float* x, int64_t k, rt_hip_stream stream);
 
+/* A layer's q/k/v when v is BF16 (the Q6_K-widened v of a Q4_K_M model,
+ * src/transformer4_load.cpp:141-143): up to four tiled-Q4_K GEMVs and one
+ * BF16 GEMV w_bf16 [n_bf16, k] that all read x, in one launch.
+ * Replace: the q/k/v projections of one layer (src/transformer5.cpp:152-172,
+ * Linear2::fused_linear per weight) and their three decode dispatches
+ * (src/metal_decode.mm:436-482).  Outputs equal those of
+ * rt_hip_gemv_q4k_tiled_multi (to f32 rounding: the Q4_K K split may differ)
+ * and, bit for bit, of rt_hip_gemv_bf16.  k % 256 == 0, k <= 8192. */
+int rt_hip_gemv_q4k_tiled_bf16(int32_t count, const void* const* tiled, float* const* y,
+                               const int64_t* n, const uint16_t* w_bf16, float* y_bf16,
+                               int64_t n_bf16, const float* x, int64_t k, rt_hip_stream stream);
+
 /* ---- decode chain: a step's dependent GEMV stages in one launch -----------
  * Replace: MetalDecodeContext::create / decode_step, the per-token sequence
  * of GEMV dispatches encoded into one command buffer
@@ -120,8 +132,10 @@ int rt_hip_gemv_q4k_tiled_multi(int32_t count, const void* const* tiled, float* 
  * gate/up), exactly as rt_hip_gemv_q4k_tiled_multi.  Stage s starts reading
  * x only after every earlier stage has stored its outputs, so x may point at
  * an earlier stage's y.  The chain runs as one persistent launch (one
- * workgroup per CU); each CU loads its share of stage s+1's weights while
- * stage s finishes elsewhere.
+ * workgroup per CU) with a stage barrier between stages.  On MI355X it is
+ * measured slower than one launch per stage (877 vs 743 us for a
+ * Llama-3.2-3B step of pure Q4_K): the cross-CU handoff costs about as much
+ * as a kernel boundary.  It is an opt-in alternative, not the fast path.
  *
  * create validates the stages and copies them to the device (the pointers
  * are baked in: buffers must outlive the chain).  run launches one pass and

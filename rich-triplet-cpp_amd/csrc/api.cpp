@@ -236,6 +236,27 @@ int rt_hip_gemv_q4k_tiled_multi(int32_t count, const void* const* tiled, float* 
                                "rt_hip_gemv_q4k_tiled_multi");
 }
 
+int rt_hip_gemv_q4k_tiled_bf16(int32_t count, const void* const* tiled, float* const* y,
+                               const int64_t* n, const uint16_t* w_bf16, float* y_bf16,
+                               int64_t n_bf16, const float* x, int64_t k, rt_hip_stream stream) {
+    const char* fn = "rt_hip_gemv_q4k_tiled_bf16";
+    if (count < 1 || count > RT_HIP_MULTI_MAX || !tiled || !y || !n)
+        return fail(RT_HIP_E_ARG, std::string(fn) + ": count must be in [1, 4] with arrays");
+    for (int32_t j = 0; j < count; ++j) {
+        int rc = gemv_args(fn, tiled[j], x, y[j], n[j], k, 1, 256);
+        if (rc) return rc;
+    }
+    int rc = gemv_args(fn, w_bf16, x, y_bf16, n_bf16, k, 1, 256);
+    if (rc) return rc;
+    if (k > 8192 || q4k_bf16_fused_lds_bytes(k) > 65536)
+        return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 8192");
+    hipError_t e;
+    if (!state_for_current(&e)) return hip_fail(e, fn);
+    return check_stream_launch(launch_gemv_q4k_bf16_fused(count, tiled, y, n, w_bf16, y_bf16, n_bf16, x, k,
+                                                          static_cast<hipStream_t>(stream)),
+                               fn);
+}
+
 int rt_hip_gemv_q4k_tiled(const void* tiled, const float* x, float* y, int64_t n, int64_t k,
                           rt_hip_stream stream) {
     return rt_hip_gemv_q4k_tiled_multi(1, &tiled, &y, &n, x, k, stream);

@@ -90,16 +90,6 @@ __device__ __forceinline__ void st_coherent(float* p, float v) {
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 __device__ __forceinline__ int sreg(int v) { return __builtin_amdgcn_readfirstlane(v); }
 template <typename T>
 __device__ __forceinline__ T* sreg(T* p) {

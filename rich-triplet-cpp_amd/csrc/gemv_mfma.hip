@@ -17,6 +17,7 @@
 // them does not drain the weight loads (vmcnt completes in order).
 #include <type_traits>
 
+#include "gemv_bf16.hpp"
 #include "q4k_mfma.hpp"
 #include "rt_launch.hpp"
 
@@ -27,20 +28,6 @@ using namespace q4k_mfma;
 
 constexpr int kMaxThreads = 768;  // up to 12 waves per workgroup
 constexpr int kMaxJobs = 4;
-
-// LDS-only workgroup barrier: waits for this wave's LDS traffic, not for its
-// global loads, so the weight pipeline keeps running across it.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// s_waitcnt vmcnt(N) alone (gfx9 encoding: vmcnt bits [3:0] and [15:14],
-// expcnt [6:4] and lgkmcnt [11:8] left at their no-wait maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 // Job table passed by value: job j owns tiles [tile0[j], tile0[j + 1]), the
 // last one up to `total`; unused entries hold `total`.
@@ -77,11 +64,12 @@ __device__ __forceinline__ uint64_t sreg(const void* p) {
 // with -amdgpu-kernarg-preload-count), so x and the weight prologue issue
 // without waiting for a kernel-argument load.  Jobs 2 and 3 (and every
 // output pointer) come from the table.
+// The body of workgroup `blk` (the kernel below, and the Q4_K workgroups of
+// the fused q/k/v launch); `lds` holds mfma_gemv_lds_bytes(K, waves).
 template <int D, int XP, bool TILED, bool J34>
-__global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
-    const float* __restrict__ X, int K, int KS, int nthreads, const uint8_t* w0, const uint8_t* w1,
-    int n0, int n1, int tile1, int count, const Jobs jobs) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+__device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, int K, int KS, int nthreads,
+                                          const uint8_t* w0, const uint8_t* w1, int n0, int n1, int tile1,
+                                          int count, const Jobs& jobs, uint8_t* lds) {
     // nthreads == blockDim.x, passed as a preloaded argument: blockDim
     // itself is a kernel-argument load that the first x loads would wait for.
     const int TPW = (nthreads >> 6) / KS;  // tiles per workgroup
@@ -111,7 +99,7 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
     // This wave's tile: job and first row (wave-uniform).  A tile slot past
     // the last tile belongs to the last job with rows past its end, so its
     // loads read zeros and it stores nothing.
-    const int t = static_cast<int>(blockIdx.x) * TPW + tslot;
+    const int t = blk * TPW + tslot;
     int job, tile_base, n_job;
     const uint8_t* wj;
     job = (count > 1 && t >= tile1) ? 1 : 0;
@@ -242,6 +230,32 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
 }
 
 template <int D, int XP, bool TILED, bool J34>
+__global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
+    const float* __restrict__ X, int K, int KS, int nthreads, const uint8_t* w0, const uint8_t* w1,
+    int n0, int n1, int tile1, int count, const Jobs jobs) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    q4k_tiles<D, XP, TILED, J34>(static_cast<int>(blockIdx.x), X, K, KS, nthreads, w0, w1, n0, n1, tile1, count,
+                                 jobs, lds);
+}
+
+// A layer's q/k/v when v is BF16 (Q6_K widened): the first q4k_wgs
+// workgroups run the tiled Q4_K GEMVs, the rest the BF16 rows, all on the
+// same x.  One launch instead of two dependent ones; each workgroup's work is
+// exactly that of the separate kernels (4 waves per workgroup on both sides).
+template <int XPQ, bool J34, int XPB>
+__global__ __launch_bounds__(bf16_gemv::kThreads) void k_gemv_q4k_bf16(
+    const float* __restrict__ X, int K, int KS, int nthreads, const uint8_t* w0, const uint8_t* w1,
+    int n0, int n1, int tile1, int count, int q4k_wgs, const uint16_t* __restrict__ wb, float* __restrict__ yb,
+    int nb_rows, const Jobs jobs) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int blk = static_cast<int>(blockIdx.x);
+    if (blk < q4k_wgs)
+        q4k_tiles<4, XPQ, true, J34>(blk, X, K, KS, nthreads, w0, w1, n0, n1, tile1, count, jobs, lds);
+    else
+        bf16_gemv::rows<1, 8, XPB, false>(blk - q4k_wgs, wb, X, yb, nb_rows, K, nullptr, lds);
+}
+
+template <int D, int XP, bool TILED, bool J34>
 hipError_t run(const Jobs& jobs, const float* x, int64_t k, int ks, int waves, hipStream_t s) {
     const int tpw = waves / ks;
     const int64_t wgs = (static_cast<int64_t>(jobs.total) + tpw - 1) / tpw;
@@ -334,6 +348,75 @@ hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* co
     }
     jobs.total = static_cast<int>(tiles);
     return tiled ? dispatch<true>(jobs, x, k, s) : dispatch<false>(jobs, x, k, s);
+}
+
+namespace {
+
+template <int XPQ, bool J34, int XPB>
+hipError_t run_fused(const Jobs& jobs, int ks, int q4k_wgs, const uint16_t* wb, float* yb, int64_t nb_rows,
+                     const float* x, int64_t k, size_t lds, hipStream_t s) {
+    const int64_t bwgs = (nb_rows + 3) / 4;  // one row per wave, 4 waves
+    hipLaunchKernelGGL((k_gemv_q4k_bf16<XPQ, J34, XPB>), dim3(static_cast<unsigned>(q4k_wgs + bwgs)),
+                       dim3(bf16_gemv::kThreads), lds, s, x, static_cast<int>(k), ks, bf16_gemv::kThreads,
+                       jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], jobs.count, q4k_wgs, wb, yb,
+                       static_cast<int>(nb_rows), jobs);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+size_t q4k_bf16_fused_lds_bytes(int64_t k) {
+    const size_t a = mfma_gemv_lds_bytes(k, 4), b = bf16_gemv::lds_bytes(k);
+    return a > b ? a : b;
+}
+
+hipError_t launch_gemv_q4k_bf16_fused(int count, const void* const* w, float* const* y, const int64_t* n,
+                                      const uint16_t* wb, float* yb, int64_t nb_rows, const float* x,
+                                      int64_t k, hipStream_t s) {
+    if (count < 1 || count > kMaxJobs || k > 8192) return hipErrorInvalidValue;
+    Jobs jobs{};
+    jobs.count = count;
+    int64_t tiles = 0;
+    for (int j = 0; j < count; ++j) {
+        jobs.w[j] = static_cast<const uint8_t*>(w[j]);
+        jobs.y[j] = y[j];
+        jobs.n[j] = static_cast<int>(n[j]);
+        jobs.tile0[j] = static_cast<int>(tiles);
+        tiles += (n[j] + 15) / 16;
+    }
+    for (int j = count; j < kMaxJobs; ++j) {
+        jobs.w[j] = jobs.w[0];
+        jobs.y[j] = jobs.y[0];
+        jobs.n[j] = jobs.n[0];
+        jobs.tile0[j] = static_cast<int>(tiles);
+    }
+    jobs.total = static_cast<int>(tiles);
+    // Four waves per workgroup on both sides, so the Q4_K split is 4, 2 or 1
+    // waves per tile: the largest that divides the super-blocks, leaves two
+    // per wave and keeps the Q4_K part to one workgroup per CU.
+    const int64_t nb = k / 256, cus = device_info().cus;
+    int ks = 1;
+    for (int c : {4, 2})
+        if (nb % c == 0 && 2 * c <= nb && (tiles + (4 / c) - 1) / (4 / c) <= cus) {
+            ks = c;
+            break;
+        }
+    const int tpw = 4 / ks;
+    const int q4k_wgs = static_cast<int>((tiles + tpw - 1) / tpw);
+    const size_t lds = q4k_bf16_fused_lds_bytes(k);
+    const bool j34 = count > 2;
+    const int64_t per = (k / 4 + 255) / 256;  // f32x4 of x per thread
+    if (k <= 4096) {
+        if (per <= 2)
+            return j34 ? run_fused<2, true, 4>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s)
+                       : run_fused<2, false, 4>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s);
+        return j34 ? run_fused<4, true, 4>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s)
+                   : run_fused<4, false, 4>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s);
+    }
+    if (per <= 8)
+        return j34 ? run_fused<8, true, 8>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s)
+                   : run_fused<8, false, 8>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s);
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv_q4k_mfma(const void* w, const float* x, float* y, int64_t n, int64_t k,

@@ -41,6 +41,12 @@ hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* co
 size_t mfma_gemv_lds_bytes(int64_t k, int waves);
 size_t q4k_m1_lds_bytes(int64_t k);
 hipError_t launch_q4k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, hipStream_t s);
+// Up to four tiled-Q4_K GEMVs and one BF16 GEMV sharing x (K <= 8192) in one
+// launch; LDS: q4k_bf16_fused_lds_bytes(k).
+size_t q4k_bf16_fused_lds_bytes(int64_t k);
+hipError_t launch_gemv_q4k_bf16_fused(int count, const void* const* w, float* const* y, const int64_t* n,
+                                      const uint16_t* wb, float* yb, int64_t nb_rows, const float* x,
+                                      int64_t k, hipStream_t s);
 
 // Persistent decode chain (chain.hip).  The host builds the stage table with
 // chain_fill_stage (chain_stage_bytes() each) in device memory and a zeroed

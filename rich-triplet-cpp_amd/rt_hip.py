@@ -39,6 +39,8 @@ _SIGNATURES = {
     "rt_hip_gemm_q4k": [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "rt_hip_gemm_bf16": [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "rt_hip_linear_forward": [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "rt_hip_gemv_q4k_tiled_bf16": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp, _i64,
+                                   _vp, _i64, _vp],
     "rt_hip_chain_run": [_vp, _vp],
     "rt_hip_chain_status": [_vp, _i32],
     "rt_hip_chain_destroy": [_vp],
@@ -200,6 +202,24 @@ def gemv_q4k_tiled_multi(ws, x, ns, k: int, ys=None, stream=None):
     npp = (_i64 * count)(*ns)
     library().call("rt_hip_gemv_q4k_tiled_multi", count, wp, yp, npp, _ptr(x), k, _stream(stream))
     return ys
+
+
+def gemv_q4k_tiled_bf16(ws, ns, wb, nb: int, x, k: int, ys=None, yb=None, stream=None):
+    """Tiled-Q4_K GEMVs ws (out_features ns) and one BF16 GEMV wb [nb, k], all
+    on x, in one launch (a layer's q/k and BF16-widened v)."""
+    torch = _torch()
+    count = len(ws)
+    if ys is None:
+        ys = [torch.empty((1, n), dtype=torch.float32, device=x.device) for n in ns]
+    if yb is None:
+        yb = torch.empty((1, nb), dtype=torch.float32, device=x.device)
+    _dev_check(x, wb, yb, *ws, *ys)
+    wp = (_vp * count)(*[w.data_ptr() for w in ws])
+    yp = (_vp * count)(*[y.data_ptr() for y in ys])
+    npp = (_i64 * count)(*ns)
+    library().call("rt_hip_gemv_q4k_tiled_bf16", count, wp, yp, npp, _ptr(wb), _ptr(yb), nb, _ptr(x), k,
+                   _stream(stream))
+    return ys, yb
 
 
 class Chain:

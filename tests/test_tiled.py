@@ -10,7 +10,8 @@ GEMV on the row-major blocks (same arithmetic on the same values).
 import numpy as np
 import pytest
 
-from helpers import (GEMV_TOL, from_dev, normwise_err, q4k_dequant_tiled_np, q4k_tile_np,
+from helpers import (GEMV_TOL, bf16_bits_to_f32, f32_to_bf16_rne, from_dev, normwise_err,
+                     q4k_dequant_tiled_np, q4k_tile_np,
                      q4k_untile_np, say, to_dev)
 
 SHAPES = [(37, 256), (130, 1024), (1, 512), (16, 2304), (300, 3072)]
@@ -114,3 +115,33 @@ def test_tile_rejects_bad_shapes(rt):
     assert lib.status("rt_hip_q4k_tile", buf.data_ptr(), buf.data_ptr(), 1, 256, None) == 1
     assert rt.q4k_tiled_bytes(17, 256) == 32 * 144
     assert rt.q4k_tiled_bytes(17, 255) == -1
+
+
+FUSED = [([3072, 1024], 1024, 3072), ([3072], 3072, 8192), ([37, 130, 5, 16], 37, 512),
+         ([8192, 8192], 100, 3072)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ns,nb,k", FUSED)
+def test_fused_q4k_bf16_equals_separate(rt, orc, ns, nb, k):
+    """q/k (tiled Q4_K) + BF16 v in one launch: the BF16 rows are the bits of
+    rt_hip_gemv_bf16, the Q4_K rows those of the separate multi launch to f32
+    rounding, and both meet the oracle."""
+    say(f"[fused q4k+bf16] ns={ns} bf16 rows={nb} K={k}")
+    rng = np.random.default_rng(sum(ns) + nb + k)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    bl = [orc.q4k_quantize((rng.standard_normal((n, k)) * 0.02).astype(np.float32)) for n in ns]
+    wb32 = (rng.standard_normal((nb, k)) * 0.02).astype(np.float32)
+    wbits = f32_to_bf16_rne(wb32)
+    dx = to_dev(x)
+    tl = [rt.q4k_tile(to_dev(b), n, k) for b, n in zip(bl, ns)]
+    dwb = to_dev(wbits.view(np.int16))
+    ys, yb = rt.gemv_q4k_tiled_bf16(tl, ns, dwb, nb, dx, k)
+    yb_sep = from_dev(rt.gemv(rt.BF16, dwb, dx, nb, k))
+    assert np.array_equal(from_dev(yb).view(np.uint32), yb_sep.view(np.uint32))
+    ref_b = bf16_bits_to_f32(wbits).astype(np.float64) @ x[0].astype(np.float64)
+    assert normwise_err(from_dev(yb)[0], ref_b) <= GEMV_TOL
+    sep = rt.gemv_q4k_tiled_multi(tl, dx, ns, k)
+    for b, n, y, y2 in zip(bl, ns, ys, sep):
+        assert normwise_err(from_dev(y), from_dev(y2)) <= 1e-6
+        assert normwise_err(from_dev(y), orc.q4k_matmul_t(b, n, k, x)) <= GEMV_TOL
