@@ -8,42 +8,49 @@ namespace {
 
 using namespace bf16_gemv;
 
-template <int RPW, int D, int XP, bool ARGMAX>
-__global__ __launch_bounds__(kThreads) void k_gemv_bf16(const uint16_t* __restrict__ W,
-                                                        const float* __restrict__ X,
-                                                        float* __restrict__ Y, int N, int K,
-                                                        uint64_t* __restrict__ key) {
+template <int D, int XP, bool ARGMAX, int T>
+__global__ __launch_bounds__(T) void k_gemv_bf16(const uint16_t* __restrict__ W, const float* __restrict__ X,
+                                                 float* __restrict__ Y, int N, int K,
+                                                 uint64_t* __restrict__ key) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    rows<RPW, D, XP, ARGMAX>(static_cast<int>(blockIdx.x), W, X, Y, N, K, key, lds);
+    rows<D, XP, ARGMAX, T>(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), W, X, Y, N, K, key, lds);
 }
 
-template <int RPW, int D, bool ARGMAX>
+// T threads per workgroup, each wave looping over its rows; x is prefetched into registers before the
+// weight prologue when XP * T covers K / 4 (else the rest is copied after).
+template <bool ARGMAX, int T>
 hipError_t run(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k, uint64_t* key,
                hipStream_t s) {
-    const int64_t rows_per_wg = static_cast<int64_t>(kThreads / kWave) * RPW;
-    const int64_t wgs = (n + rows_per_wg - 1) / rows_per_wg;
+    // Rows per wave (at most 64: the row sums stay in lanes), measured: 4
+    // for short rows (<= 3 pieces: one row alone leaves the ring part
+    // empty), 2 for long ones (x is staged by half as many workgroups), else 1.
+    const int64_t waves = T / kWave, pieces = (k + kPiece - 1) / kPiece;
+    int64_t rpw = tune_param("BF16_ROWS_PER_WAVE", pieces <= 3 ? 4 : (pieces >= 12 ? 2 : 1));
+    rpw = rpw < 1 ? 1 : (rpw > 64 ? 64 : rpw);
+    const int64_t wgs = (n + waves * rpw - 1) / (waves * rpw);
     const size_t lds = bf16_m1_lds_bytes(k);
     const int ik = static_cast<int>(k), in = static_cast<int>(n);
-    if (k <= 4 * kThreads * 4)
-        hipLaunchKernelGGL((k_gemv_bf16<RPW, D, 4, ARGMAX>), dim3(static_cast<unsigned>(wgs)),
-                           dim3(kThreads), lds, s, w, x, y, in, ik, key);
+    const int64_t per = (k / 4 + T - 1) / T;
+    const dim3 g(static_cast<unsigned>(wgs)), b(T);
+    if (per <= 2)
+        hipLaunchKernelGGL((k_gemv_bf16<8, 2, ARGMAX, T>), g, b, lds, s, w, x, y, in, ik, key);
+    else if (per <= 4)
+        hipLaunchKernelGGL((k_gemv_bf16<8, 4, ARGMAX, T>), g, b, lds, s, w, x, y, in, ik, key);
     else
-        hipLaunchKernelGGL((k_gemv_bf16<RPW, D, 8, ARGMAX>), dim3(static_cast<unsigned>(wgs)),
-                           dim3(kThreads), lds, s, w, x, y, in, ik, key);
+        hipLaunchKernelGGL((k_gemv_bf16<8, 8, ARGMAX, T>), g, b, lds, s, w, x, y, in, ik, key);
     return hipGetLastError();
 }
 
 template <bool ARGMAX>
 hipError_t run_rows(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k, uint64_t* key,
                     hipStream_t s) {
-    // One row per wave measured fastest at every decode shape (more, smaller
-    // workgroups balance better over the CUs); RT_HIP_BF16_RPW overrides.
-    const int rpw = tune_param("BF16_RPW", 1);
-    const int ring = tune_param("BF16_RING", 8);
-    if (rpw <= 1) return ring >= 16 ? run<1, 16, ARGMAX>(w, x, y, n, k, key, s) : run<1, 8, ARGMAX>(w, x, y, n, k, key, s);
-    if (rpw == 2) return run<2, 8, ARGMAX>(w, x, y, n, k, key, s);
-    if (rpw == 3) return run<3, 8, ARGMAX>(w, x, y, n, k, key, s);
-    return run<4, 4, ARGMAX>(w, x, y, n, k, key, s);
+    // One row per wave at a time, ring of 8 pieces; RT_HIP_BF16_WAVES (waves
+    // per workgroup) overrides the measured default.
+    const int waves = tune_param("BF16_WAVES", 8);
+    if (waves == 4) return run<ARGMAX, 256>(w, x, y, n, k, key, s);
+    if (waves == 12) return run<ARGMAX, 768>(w, x, y, n, k, key, s);
+    if (waves == 16) return run<ARGMAX, 1024>(w, x, y, n, k, key, s);
+    return run<ARGMAX, 512>(w, x, y, n, k, key, s);
 }
 
 }  // namespace

@@ -2,18 +2,17 @@
 // W row-major bf16 (MatBf16, include/rt/mat.hpp), x and y f32), shared by
 // the BF16 GEMV kernel and the fused q/k/v launch of gemv_mfma.hip.
 //
-// A wave owns RPW consecutive rows and walks them side by side, one "piece"
-// (512 values = 1 KB of one row, 16 bytes per lane) per row per step, so a
-// load instruction reads 1 KB of contiguous memory and one activation read
-// from LDS feeds RPW rows.  Rows are never split across waves: a wave's
-// partial sums only need a butterfly at the end.
+// A wave walks its rows one "piece" (512 values = 1 KB of one row, 16 bytes
+// per lane) at a time, so a load instruction reads 1 KB of contiguous
+// memory.  Rows are never split across waves: a row's partial sums only
+// need a butterfly once its last piece is in.
 //
-// Pipeline: a ring of D slots (RPW pieces each) is loaded ahead of the
-// compute; each slot is refilled as soon as it is consumed.  The steady loop
-// is straight-line and the last <= D pieces are a tail that issues nothing,
-// so the compiler keeps the ring in place and every wait is partial.  x is
-// loaded into registers before the weight prologue and staged in LDS after
-// it, so waiting for x never waits for weight loads.
+// Pipeline: a ring of D pieces is loaded ahead of the compute; each slot is
+// refilled as soon as it is consumed, running on into the wave's next row.
+// The steady loop is straight-line and the last <= D pieces are a tail that
+// issues nothing, so the compiler keeps the ring in place and every wait is
+// partial.  x is loaded into registers before the weight prologue and
+// staged in LDS after it, so waiting for x never waits for weight loads.
 //
 // Loads go through per-(row, piece) buffer resources: rows past N and bytes
 // past the end of a row (K % 512 != 0) read as zeros, with no clamping.
@@ -28,7 +27,7 @@
 namespace rt_hip {
 namespace bf16_gemv {
 
-constexpr int kThreads = 256;  // one workgroup: 4 waves
+constexpr int kThreads = 256;  // default workgroup: 4 waves
 constexpr int kPiece = 512;  // bf16 values per wave-wide 16-byte-per-lane load
 
 // LDS byte offset of x[4f .. 4f+3]: piece i = f / 128 holds, for lane
@@ -40,12 +39,36 @@ __device__ __forceinline__ uint32_t x_off(int f) {
     return static_cast<uint32_t>((((i << 1) + h) << 6) + l) << 4;
 }
 
-// Workgroup `blk` of a launch of kThreads-thread workgroups; `lds` holds
-// lds_bytes(K).
-template <int RPW, int D, int XP, bool ARGMAX>
-__device__ __forceinline__ void rows(int blk, const uint16_t* __restrict__ W, const float* __restrict__ X,
-                                     float* __restrict__ Y, int N, int K, uint64_t* __restrict__ key,
-                                     uint8_t* lds) {
+// Workgroup `blk` of `nblk` T-thread workgroups; `lds` holds lds_bytes(K).
+// Wave gw = blk * (T / 64) + wave of the NW = nblk * (T / 64) waves takes
+// rows gw, gw + NW, gw + 2 NW, ... (at most 64: the launcher sizes the
+// grid); the pieces of its rows form one sequence that the ring streams
+// without a break between rows, so a short row (small K) costs no pipeline
+// ramp and x is staged once per workgroup, not once per row.  A row's sum is
+// reduced as soon as its last piece is in and kept by lane r (the wave's
+// r-th row); the sums are stored after the loop, since a store among the
+// ring's loads makes the compiler wait for all of them.
+// Sum over the 64 lanes, in VALU only: DPP within each row of 16 lanes
+// (quad swaps, half-row and row mirrors), then the gfx950 permlane swaps
+// across rows.  Every lane ends with the same bits.
+__device__ __forceinline__ float wave_sum(float v, int lane) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1, 0xf, 0xf, false));   // l ^ 1
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4e, 0xf, 0xf, false));   // l ^ 2
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));  // half mirror
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false));  // row mirror
+    const uint32_t u = __float_as_uint(v);
+    const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    v += __uint_as_float(((lane >> 4) & 1) ? r16[0] : r16[1]);  // lane ^ 16
+    const uint32_t u2 = __float_as_uint(v);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(u2, u2, false, false);
+    v += __uint_as_float(lane >= 32 ? r32[0] : r32[1]);  // lane ^ 32
+    return v;
+}
+
+template <int D, int XP, bool ARGMAX, int T = kThreads>
+__device__ __forceinline__ void rows(int blk, int nblk, const uint16_t* __restrict__ W,
+                                     const float* __restrict__ X, float* __restrict__ Y, int N, int K,
+                                     uint64_t* __restrict__ key, uint8_t* lds) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int P = (K + kPiece - 1) / kPiece;  // pieces per row (the last may be partial)
@@ -56,103 +79,104 @@ __device__ __forceinline__ void rows(int blk, const uint16_t* __restrict__ W, co
     f32x4 xv[XP];
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
-        const int f = tid + kThreads * i;
+        const int f = tid + T * i;
         xv[i] = X4[f < kx4 ? f : 0];
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    const int row0 = (blk * (kThreads / kWave) + wave) * RPW;
+    const int NW = nblk * (T / kWave);
+    const int gw = blk * (T / kWave) + wave;
+    const int R = gw < N ? (N - 1 - gw) / NW + 1 : 0;  // this wave's rows
+    const int L = R * P;                                // and their pieces
     const int64_t rowb = static_cast<int64_t>(K) * 2;
-    const uint8_t* const wb = reinterpret_cast<const uint8_t*>(W);
+    const int64_t stride = static_cast<int64_t>(NW) * rowb;
+    const uint8_t* const wb = reinterpret_cast<const uint8_t*>(W) + static_cast<int64_t>(gw) * rowb;
     const uint32_t loff = static_cast<uint32_t>(lane) * 16u;
+    auto* const Yg = (__attribute__((address_space(1))) float*)Y;
 
-    // Piece i of each of the wave's rows; empty resources past N or past
-    // the last piece.
-    auto issue = [&](u32x4 (&slot)[RPW], int i) {
-        const int64_t o = static_cast<int64_t>(i) * (kPiece * 2);
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            const int row = row0 + r;
-            const int64_t left = (row < N && i < P) ? rowb - o : 0;
-            slot[r] = ld16(make_rsrc(wb + static_cast<int64_t>(row) * rowb + o, left), loff);
-        }
-    };
-
-    u32x4 ring[D][RPW];
+    // Cursors (wave-uniform, kept in SGPRs): the issue side is at row ir,
+    // piece ip; the consume side at row cr, piece cp.  Past the last row the
+    // resource is empty (zeros, no memory traffic).
+    int ir = 0, ip = 0, cr = 0, cp = 0;
+    u32x4 ring[D];
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-        issue(ring[j], j);
+        const int64_t o = static_cast<int64_t>(ip) * (kPiece * 2);
+        ring[j] = ld16(make_rsrc(wb + ir * stride + o, ir < R ? rowb - o : 0), loff);
+        const bool wrap = ip == P - 1;
+        ip = __builtin_amdgcn_readfirstlane(wrap ? 0 : ip + 1);
+        ir = __builtin_amdgcn_readfirstlane(wrap ? ir + 1 : ir);
         __builtin_amdgcn_sched_barrier(0);
     }
 
     // Stage x (zeros past K, up to the whole last piece).
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
-        const int f = tid + kThreads * i;
+        const int f = tid + T * i;
         const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
         if (f < nx4) *reinterpret_cast<f32x4*>(lds + x_off(f)) = f < kx4 ? xv[i] : z;
     }
-    for (int f = tid + kThreads * XP; f < nx4; f += kThreads) {
+    for (int f = tid + T * XP; f < nx4; f += T) {
         const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
         *reinterpret_cast<f32x4*>(lds + x_off(f)) = f < kx4 ? X4[f] : z;
     }
     lds_barrier();
 
-    float acc[RPW];
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
-    // Values 8l .. 8l+7 of piece i: dword e holds values 2e (low half) and
-    // 2e + 1 (high half).
-    auto fma_piece = [&](const u32x4 (&w)[RPW], int i) {
-        const f32x4 xa = *reinterpret_cast<const f32x4*>(lds + ((((i << 1) + 0) << 6) + lane) * 16);
-        const f32x4 xb = *reinterpret_cast<const f32x4*>(lds + ((((i << 1) + 1) << 6) + lane) * 16);
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            float a = acc[r];
-            a = __builtin_fmaf(bf16_lo_to_f32(w[r][0]), xa[0], a);
-            a = __builtin_fmaf(bf16_hi_to_f32(w[r][0]), xa[1], a);
-            a = __builtin_fmaf(bf16_lo_to_f32(w[r][1]), xa[2], a);
-            a = __builtin_fmaf(bf16_hi_to_f32(w[r][1]), xa[3], a);
-            a = __builtin_fmaf(bf16_lo_to_f32(w[r][2]), xb[0], a);
-            a = __builtin_fmaf(bf16_hi_to_f32(w[r][2]), xb[1], a);
-            a = __builtin_fmaf(bf16_lo_to_f32(w[r][3]), xb[2], a);
-            a = __builtin_fmaf(bf16_hi_to_f32(w[r][3]), xb[3], a);
-            acc[r] = a;
-        }
-    };
+    // Values 8l .. 8l+7 of a piece: dword e holds values 2e (low half) and
+    // 2e + 1 (high half).  A row's sum stays with lane cr of the wave.
+    float acc = 0.0f, res = 0.0f;
+    uint64_t best = 0;
+#define RT_BF16_CONSUME(w)                                                                                  \
+    do {                                                                                                    \
+        const f32x4 xa = *reinterpret_cast<const f32x4*>(lds + ((((cp << 1) + 0) << 6) + lane) * 16);       \
+        const f32x4 xb = *reinterpret_cast<const f32x4*>(lds + ((((cp << 1) + 1) << 6) + lane) * 16);       \
+        float a = acc;                                                                                      \
+        a = __builtin_fmaf(bf16_lo_to_f32((w)[0]), xa[0], a);                                               \
+        a = __builtin_fmaf(bf16_hi_to_f32((w)[0]), xa[1], a);                                               \
+        a = __builtin_fmaf(bf16_lo_to_f32((w)[1]), xa[2], a);                                               \
+        a = __builtin_fmaf(bf16_hi_to_f32((w)[1]), xa[3], a);                                               \
+        a = __builtin_fmaf(bf16_lo_to_f32((w)[2]), xb[0], a);                                               \
+        a = __builtin_fmaf(bf16_hi_to_f32((w)[2]), xb[1], a);                                               \
+        a = __builtin_fmaf(bf16_lo_to_f32((w)[3]), xb[2], a);                                               \
+        a = __builtin_fmaf(bf16_hi_to_f32((w)[3]), xb[3], a);                                               \
+        acc = a;                                                                                            \
+        if (cp == P - 1) {                                                                                  \
+            const float v = wave_sum(acc, lane);                                                            \
+            res = lane == cr ? v : res;                                                                     \
+            if constexpr (ARGMAX) {                                                                         \
+                if (v == v) {                                                                               \
+                    const uint64_t kk = argmax_key(v, static_cast<uint32_t>(gw + cr * NW));                 \
+                    best = kk > best ? kk : best;                                                           \
+                }                                                                                           \
+            }                                                                                               \
+            acc = 0.0f;                                                                                     \
+        }                                                                                                   \
+        const bool cwrap = cp == P - 1;                                                                     \
+        cp = __builtin_amdgcn_readfirstlane(cwrap ? 0 : cp + 1);                                            \
+        cr = __builtin_amdgcn_readfirstlane(cwrap ? cr + 1 : cr);                                           \
+    } while (0)
 
     // Steady rounds (straight-line: compute slot j, then refill it with the
     // piece D steps ahead), then the tail of the last <= D pieces.
     int i = 0;
-    for (; i + D < P; i += D) {
+    for (; i + D < L; i += D) {
 #pragma unroll
         for (int j = 0; j < D; ++j) {
-            fma_piece(ring[j], i + j);
+            RT_BF16_CONSUME(ring[j]);
             __builtin_amdgcn_sched_barrier(0);
-            issue(ring[j], i + D + j);
+            const int64_t o = static_cast<int64_t>(ip) * (kPiece * 2);
+            ring[j] = ld16(make_rsrc(wb + ir * stride + o, ir < R ? rowb - o : 0), loff);
+            const bool wrap = ip == P - 1;
+            ip = __builtin_amdgcn_readfirstlane(wrap ? 0 : ip + 1);
+            ir = __builtin_amdgcn_readfirstlane(wrap ? ir + 1 : ir);
         }
     }
 #pragma unroll
     for (int j = 0; j < D; ++j)
-        if (i + j < P) fma_piece(ring[j], i + j);
+        if (i + j < L) RT_BF16_CONSUME(ring[j]);
+#undef RT_BF16_CONSUME
 
-    uint64_t best = 0;
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        float v = acc[r];
-#pragma unroll
-        for (int off = kWave / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-        const int row = row0 + r;
-        if (row < N) {
-            if (lane == 0) Y[row] = v;
-            if constexpr (ARGMAX) {
-                if (v == v) {
-                    const uint64_t kk = argmax_key(v, static_cast<uint32_t>(row));
-                    best = kk > best ? kk : best;
-                }
-            }
-        }
-    }
+    if (lane < R) Yg[gw + lane * NW] = res;
     if constexpr (ARGMAX) {
         if (lane == 0 && best != 0)
             atomicMax(reinterpret_cast<unsigned long long*>(key), static_cast<unsigned long long>(best));

@@ -252,7 +252,7 @@ __global__ __launch_bounds__(bf16_gemv::kThreads) void k_gemv_q4k_bf16(
     if (blk < q4k_wgs)
         q4k_tiles<4, XPQ, true, J34>(blk, X, K, KS, nthreads, w0, w1, n0, n1, tile1, count, jobs, lds);
     else
-        bf16_gemv::rows<1, 8, XPB, false>(blk - q4k_wgs, wb, X, yb, nb_rows, K, nullptr, lds);
+        bf16_gemv::rows<8, XPB, false>(blk - q4k_wgs, (nb_rows + 3) / 4, wb, X, yb, nb_rows, K, nullptr, lds);
 }
 
 template <int D, int XP, bool TILED, bool J34>
