@@ -423,6 +423,164 @@ __global__ __launch_bounds__(kPThreads) void k_gemm_pipe(const uint16_t* __restr
     }
 }
 
+// Large-tile bf16 GEMM (both operands bf16 in HBM): C = A * W^T (+ bias).
+//  * 256 x 256 workgroup tile, 8 waves of 128 x 64 (2 per SIMD): 384 B of
+//    LDS fragment reads per 16x16x32 MFMA (a 64 x 64 wave tile needs 512 B,
+//    more than the CU's LDS bandwidth at full MFMA rate).
+//  * K steps of 32: a 4-stage ring of A and W tiles (16 KB each) filled by
+//    direct-to-LDS buffer loads three steps ahead; one barrier per step.
+//  * LDS rows are 64 bytes (32 bf16); chunk c of row r sits at chunk
+//    c ^ ((r / 2) % 4).  A 16-byte-per-lane LDS read is served 8 lanes (one
+//    128-byte bank line) at a time; the 8 lanes of a fragment read are 8
+//    consecutive rows, two per 128 bytes, and the swizzle gives the rows of
+//    each parity four different chunks: no bank conflicts.  The copies apply
+//    the swizzle on the global side: lane l fills LDS chunk slot l % 4 of
+//    row l / 4 with global chunk (l % 4) ^ f(row).
+//  * Tile order: XCD-contiguous ranges of a grouped order (as k_gemm_pipe).
+constexpr int kBThreads = 512;
+constexpr int kBTile = 256 * 64;  // bytes of one 256 x 32 bf16 tile
+constexpr int kBGroupM = 4;
+
+__device__ __forceinline__ uint32_t swz64(int r, int c) {
+    return static_cast<uint32_t>(r * 64 + ((c ^ ((r >> 1) & 3)) << 4));
+}
+
+// NS: ring stages (A and W tile pairs, 32 KB each).
+template <int NS>
+__global__ __launch_bounds__(kBThreads) void k_gemm_256(const uint16_t* __restrict__ A,
+                                                        const uint16_t* __restrict__ W,
+                                                        const float* __restrict__ bias,
+                                                        float* __restrict__ C, int M, int N, int K, int mt) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    uint8_t* const sA = lds;                 // [NS][kBTile]
+    uint8_t* const sW = lds + NS * kBTile;   // [NS][kBTile]
+
+    const int G = static_cast<int>(gridDim.x), bid = static_cast<int>(blockIdx.x);
+    const int xcd = bid & 7, idx = bid >> 3, q8 = G >> 3, r8 = G & 7;
+    const int tile = xcd < r8 ? xcd * (q8 + 1) + idx : r8 * (q8 + 1) + (xcd - r8) * q8 + idx;
+    const int nt = G / mt;
+    const int group = tile / (kBGroupM * nt), first_m = group * kBGroupM;
+    const int gm = min(mt - first_m, kBGroupM);
+    const int m0 = (first_m + (tile % (kBGroupM * nt)) % gm) * 256;
+    const int n0 = ((tile % (kBGroupM * nt)) / gm) * 256;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
+    const int S = K >> 5;
+    const int64_t rowb = static_cast<int64_t>(K) * 2;
+
+    // Copy roles: wave instruction i (0, 1) covers tile rows 16 (2 wave + i)
+    // .. +15.
+    uint32_t coff[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = 16 * (2 * wave + i) + (lane >> 2);
+        coff[i] = static_cast<uint32_t>(r * rowb + (((lane & 3) ^ ((r >> 1) & 3)) << 4));
+    }
+    const uint8_t* const Ab = reinterpret_cast<const uint8_t*>(A) + static_cast<int64_t>(m0) * rowb;
+    const uint8_t* const Wb = reinterpret_cast<const uint8_t*>(W) + static_cast<int64_t>(n0) * rowb;
+    const int64_t Aleft = static_cast<int64_t>(M - m0) * rowb, Wleft = static_cast<int64_t>(N - n0) * rowb;
+    auto copy = [&](uint8_t* dst, const uint8_t* base, int64_t left, int step) {
+        const int64_t o = static_cast<int64_t>(step) * 64;  // 32 bf16 per step
+        const BufRsrc rs = make_rsrc(base + o, step < S ? left - o : 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void*)(dst + (2 * wave + i) * 1024), 16,
+                static_cast<int>(coff[i]), 0, 0, 0);
+    };
+
+    f32x4 acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int fr = lane & 15, fc = lane >> 4;
+    uint32_t aoff[8], woff[4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) aoff[i] = swz64(wm + 16 * i + fr, fc);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) woff[j] = swz64(wn + 16 * j + fr, fc);
+    // Fragments are double-buffered in registers: step s reads step s + 1's
+    // 12 fragments while its own 32 MFMAs run on the ones read during step
+    // s - 1, so LDS reads and MFMAs overlap within every wave (the step
+    // barrier aligns the waves, so they cannot rely on each other for it).
+    bf16x8 af[2][8], bf[2][4];
+    auto read_frags = [&](int buf, const uint8_t* ta, const uint8_t* tw) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bf[buf][j] = *reinterpret_cast<const bf16x8*>(tw + woff[j]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) af[buf][i] = *reinterpret_cast<const bf16x8*>(ta + aoff[i]);
+    };
+    auto mfmas = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[buf][i], bf[buf][j], acc[i][j], 0, 0, 0);
+    };
+
+#pragma unroll
+    for (int j = 0; j < NS - 1; ++j) {
+        copy(sA + j * kBTile, Ab, Aleft, j);
+        copy(sW + j * kBTile, Wb, Wleft, j);
+    }
+    wait_vm<0>();
+    lds_sync();
+    read_frags(0, sA, sW);
+
+    // Step s: copy step s + NS - 1 into the stage of step s - 1 (last read
+    // during step s - 2, before the barrier that ended it); read step s + 1's
+    // fragments; MFMAs of step s; then wait for this wave's copies of step
+    // s + 2 (4 (NS - 3) younger copy instructions: steps s + 3 .. s + NS - 1)
+    // and the barrier, after which step s + 2's stage is complete for every
+    // wave.  Two steps per round keep the fragment buffers compile-time;
+    // S is even (K % 64 == 0).  Stage offsets are scalars.
+    static_assert(NS >= 4, "fragments of step s + 1 are read one step early");
+    int st_cur = 0;  // stage of step s
+    for (int s = 0; s < S; s += 2) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int step = s + h;
+            // This step's fragments (read a step ago) are in: saying so
+            // here keeps the compiler from waiting for the reads issued
+            // below before the MFMAs.
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) alone
+            const int st_copy = st_cur == 0 ? NS - 1 : st_cur - 1;
+            const int st_next = st_cur == NS - 1 ? 0 : st_cur + 1;
+            copy(sA + st_copy * kBTile, Ab, Aleft, step + NS - 1);
+            copy(sW + st_copy * kBTile, Wb, Wleft, step + NS - 1);
+            if (step + 1 < S) read_frags(h ^ 1, sA + st_next * kBTile, sW + st_next * kBTile);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(h);
+            __builtin_amdgcn_sched_barrier(0);  // the MFMAs stay ahead of the barrier
+            wait_vm<4 * (NS - 3)>();
+            // A plain barrier: the fragment reads just issued may stay in
+            // flight across it (their stage is overwritten two barriers
+            // later), so the MFMAs scheduled after it overlap them.
+            asm volatile("s_barrier" ::: "memory");
+            st_cur = st_next;
+        }
+    }
+
+    const int cr = 4 * (lane >> 4), cc = lane & 15;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int col = n0 + wn + 16 * j + cc;
+        if (col >= N) continue;
+        const float bv = bias ? bias[col] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + wm + 16 * i + cr + r;
+                if (row < M) C[static_cast<size_t>(row) * N + col] = acc[i][j][r] + bv;
+            }
+        }
+    }
+}
+
 // f32 -> bf16 round-to-nearest-even, 8 values per thread.
 __global__ __launch_bounds__(256) void k_f32_to_bf16(const float* __restrict__ x,
                                                      uint16_t* __restrict__ y, int64_t n8) {
@@ -475,6 +633,21 @@ hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, con
             w = ws + a_bytes;
         }
         const bool q4k = fused_q4k;
+        // Large outputs: the 256 x 256 kernel when its tiles cover at least
+        // three quarters of the CUs (k % 64 == 0 always holds here).
+        const int64_t mt2 = (m + 255) / 256, nt2 = (n + 255) / 256;
+        if (!q4k && 4 * mt2 * nt2 >= 3 * static_cast<int64_t>(device_info().cus) && tune_param("GEMM_BIG", 1)) {
+            const dim3 g(static_cast<unsigned>(mt2 * nt2)), b(kBThreads);
+            const uint16_t* w16 = static_cast<const uint16_t*>(w);
+            const int im = static_cast<int>(m), in = static_cast<int>(n), ik = static_cast<int>(k);
+            if (tune_param("GEMM_BIG_STAGES", 5) == 4)
+                hipLaunchKernelGGL(k_gemm_256<4>, g, b, static_cast<size_t>(8) * kBTile, s, a16, w16, bias, c, im,
+                                   in, ik, static_cast<int>(mt2));
+            else
+                hipLaunchKernelGGL(k_gemm_256<5>, g, b, static_cast<size_t>(10) * kBTile, s, a16, w16, bias, c,
+                                   im, in, ik, static_cast<int>(mt2));
+            return hipGetLastError();
+        }
         const size_t lds = q4k ? static_cast<size_t>(kStages + 2) * kTile + kStages * kRawStage
                                : static_cast<size_t>(2 * kStages) * kTile;
         if (q4k)

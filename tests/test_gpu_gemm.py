@@ -23,6 +23,7 @@ CASES = [
     (64, 1000, 768, True),
     (513, 260, 1024, False),
     (9, 64, 256, False),
+    (4100, 4000, 512, True),   # enough 256 x 256 tiles for the large-tile kernel, ragged edges
 ]
 
 
@@ -49,7 +50,7 @@ def test_gemm_q4k(rt, orc, m, n, k, a_bf16):
 
 
 @pytest.mark.parametrize("m,n,k,a_bf16", [(128, 128, 128, False), (300, 200, 576, True),
-                                         (17, 520, 192, False)])
+                                         (17, 520, 192, False), (4133, 4044, 256, True)])
 def test_gemm_bf16(rt, orc, m, n, k, a_bf16):
     say(f"[gemm bf16] M={m} N={n} K={k}")
     import torch
@@ -77,6 +78,23 @@ def test_gemm_prefill_shape_properties(rt):
     blocks = rt.quantize_q4k(w)
     wd = rt.dequant_q4k(blocks, n, k, bf16=True).view(torch.bfloat16).float()
     ref = a.bfloat16().float() @ wd.T
+    c = rt.gemm(rt.Q4K, a, blocks, n, k)
+    err = ((c - ref).abs().max() / ref.abs().max()).item()
+    assert err <= 1e-5 * 4  # f32 torch reference itself rounds differently
+
+
+def test_gemm_flux_shape_properties(rt):
+    """BASELINE config 5 MLP-in shape (M=4608, N=12288, K=3072, bf16 A) at
+    full size, through the large-tile kernel: equals the f32 product of the
+    same bf16 operands (torch, tolerance (i))."""
+    import torch
+    m, n, k = 4608, 12288, 3072
+    g = torch.Generator(device="cuda").manual_seed(2)
+    w = torch.randn((n, k), generator=g, device="cuda") * 0.02
+    a = torch.randn((m, k), generator=g, device="cuda").bfloat16()
+    blocks = rt.quantize_q4k(w)
+    wd = rt.dequant_q4k(blocks, n, k, bf16=True).view(torch.bfloat16).float()
+    ref = a.float() @ wd.T
     c = rt.gemm(rt.Q4K, a, blocks, n, k)
     err = ((c - ref).abs().max() / ref.abs().max()).item()
     assert err <= 1e-5 * 4  # f32 torch reference itself rounds differently
