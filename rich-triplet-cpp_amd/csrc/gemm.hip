@@ -445,9 +445,11 @@ __device__ __forceinline__ uint32_t swz64(int r, int c) {
     return static_cast<uint32_t>(r * 64 + ((c ^ ((r >> 1) & 3)) << 4));
 }
 
-// NS: ring stages (A and W tile pairs, 32 KB each).
-template <int NS>
-__global__ __launch_bounds__(kBThreads) void k_gemm_256(const uint16_t* __restrict__ A,
+// NS: ring stages (A and W tile pairs, 32 KB each).  WAVES: 8 (tiles of
+// 128 x 64 per wave, 2 waves per SIMD) or 4 (128 x 128 per wave, one per
+// SIMD, accumulators in AGPRs: a third fewer fragment reads per MFMA).
+template <int NS, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void k_gemm_256(const uint16_t* __restrict__ A,
                                                         const uint16_t* __restrict__ W,
                                                         const float* __restrict__ bias,
                                                         float* __restrict__ C, int M, int N, int K, int mt) {
@@ -466,16 +468,18 @@ __global__ __launch_bounds__(kBThreads) void k_gemm_256(const uint16_t* __restri
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
+    constexpr int NJ = WAVES == 8 ? 4 : 8;  // 16-column fragments per wave
+    constexpr int CP = 16 / WAVES;          // copy instructions per wave and operand
+    const int wm = (wave / (256 / (16 * NJ))) * 128, wn = (wave % (256 / (16 * NJ))) * 16 * NJ;
     const int S = K >> 5;
     const int64_t rowb = static_cast<int64_t>(K) * 2;
 
-    // Copy roles: wave instruction i (0, 1) covers tile rows 16 (2 wave + i)
-    // .. +15.
-    uint32_t coff[2];
+    // Copy roles: wave instruction i (0 .. CP - 1) covers tile rows
+    // 16 (CP wave + i) .. +15.
+    uint32_t coff[CP];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int r = 16 * (2 * wave + i) + (lane >> 2);
+    for (int i = 0; i < CP; ++i) {
+        const int r = 16 * (CP * wave + i) + (lane >> 2);
         coff[i] = static_cast<uint32_t>(r * rowb + (((lane & 3) ^ ((r >> 1) & 3)) << 4));
     }
     const uint8_t* const Ab = reinterpret_cast<const uint8_t*>(A) + static_cast<int64_t>(m0) * rowb;
@@ -485,31 +489,31 @@ __global__ __launch_bounds__(kBThreads) void k_gemm_256(const uint16_t* __restri
         const int64_t o = static_cast<int64_t>(step) * 64;  // 32 bf16 per step
         const BufRsrc rs = make_rsrc(base + o, step < S ? left - o : 0);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < CP; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rs, (__attribute__((address_space(3))) void*)(dst + (2 * wave + i) * 1024), 16,
+                rs, (__attribute__((address_space(3))) void*)(dst + (CP * wave + i) * 1024), 16,
                 static_cast<int>(coff[i]), 0, 0, 0);
     };
 
-    f32x4 acc[8][4];
+    f32x4 acc[8][NJ];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int fr = lane & 15, fc = lane >> 4;
-    uint32_t aoff[8], woff[4];
+    uint32_t aoff[8], woff[NJ];
 #pragma unroll
     for (int i = 0; i < 8; ++i) aoff[i] = swz64(wm + 16 * i + fr, fc);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) woff[j] = swz64(wn + 16 * j + fr, fc);
+    for (int j = 0; j < NJ; ++j) woff[j] = swz64(wn + 16 * j + fr, fc);
     // Fragments are double-buffered in registers: step s reads step s + 1's
-    // 12 fragments while its own 32 MFMAs run on the ones read during step
-    // s - 1, so LDS reads and MFMAs overlap within every wave (the step
-    // barrier aligns the waves, so they cannot rely on each other for it).
-    bf16x8 af[2][8], bf[2][4];
+    // fragments while its own MFMAs run on the ones read during step s - 1,
+    // so LDS reads and MFMAs overlap within every wave (the step barrier
+    // aligns the waves, so they cannot rely on each other for it).
+    bf16x8 af[2][8], bf[2][NJ];
     auto read_frags = [&](int buf, const uint8_t* ta, const uint8_t* tw) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bf[buf][j] = *reinterpret_cast<const bf16x8*>(tw + woff[j]);
+        for (int j = 0; j < NJ; ++j) bf[buf][j] = *reinterpret_cast<const bf16x8*>(tw + woff[j]);
 #pragma unroll
         for (int i = 0; i < 8; ++i) af[buf][i] = *reinterpret_cast<const bf16x8*>(ta + aoff[i]);
     };
@@ -517,7 +521,7 @@ __global__ __launch_bounds__(kBThreads) void k_gemm_256(const uint16_t* __restri
 #pragma unroll
         for (int i = 0; i < 8; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < NJ; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[buf][i], bf[buf][j], acc[i][j], 0, 0, 0);
     };
 
@@ -533,7 +537,7 @@ __global__ __launch_bounds__(kBThreads) void k_gemm_256(const uint16_t* __restri
     // Step s: copy step s + NS - 1 into the stage of step s - 1 (last read
     // during step s - 2, before the barrier that ended it); read step s + 1's
     // fragments; MFMAs of step s; then wait for this wave's copies of step
-    // s + 2 (4 (NS - 3) younger copy instructions: steps s + 3 .. s + NS - 1)
+    // s + 2 (2 CP (NS - 3) younger copy instructions: steps s + 3 .. s + NS - 1)
     // and the barrier, after which step s + 2's stage is complete for every
     // wave.  Two steps per round keep the fragment buffers compile-time;
     // S is even (K % 64 == 0).  Stage offsets are scalars.
@@ -555,10 +559,10 @@ __global__ __launch_bounds__(kBThreads) void k_gemm_256(const uint16_t* __restri
             __builtin_amdgcn_sched_barrier(0);
             mfmas(h);
             __builtin_amdgcn_sched_barrier(0);  // the MFMAs stay ahead of the barrier
-            wait_vm<4 * (NS - 3)>();
+            wait_vm<2 * CP * (NS - 3)>();
             // A plain barrier: the fragment reads just issued may stay in
             // flight across it (their stage is overwritten two barriers
-            // later), so the MFMAs scheduled after it overlap them.
+            // later).
             asm volatile("s_barrier" ::: "memory");
             st_cur = st_next;
         }
@@ -566,7 +570,7 @@ __global__ __launch_bounds__(kBThreads) void k_gemm_256(const uint16_t* __restri
 
     const int cr = 4 * (lane >> 4), cc = lane & 15;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
         const int col = n0 + wn + 16 * j + cc;
         if (col >= N) continue;
         const float bv = bias ? bias[col] : 0.0f;
@@ -640,12 +644,13 @@ hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, con
             const dim3 g(static_cast<unsigned>(mt2 * nt2)), b(kBThreads);
             const uint16_t* w16 = static_cast<const uint16_t*>(w);
             const int im = static_cast<int>(m), in = static_cast<int>(n), ik = static_cast<int>(k);
-            if (tune_param("GEMM_BIG_STAGES", 5) == 4)
-                hipLaunchKernelGGL(k_gemm_256<4>, g, b, static_cast<size_t>(8) * kBTile, s, a16, w16, bias, c, im,
-                                   in, ik, static_cast<int>(mt2));
+            const int imt = static_cast<int>(mt2);
+            if (tune_param("GEMM_BIG_WAVES", 8) == 4)
+                hipLaunchKernelGGL((k_gemm_256<5, 4>), g, dim3(256), static_cast<size_t>(10) * kBTile, s, a16, w16,
+                                   bias, c, im, in, ik, imt);
             else
-                hipLaunchKernelGGL(k_gemm_256<5>, g, b, static_cast<size_t>(10) * kBTile, s, a16, w16, bias, c,
-                                   im, in, ik, static_cast<int>(mt2));
+                hipLaunchKernelGGL((k_gemm_256<5, 8>), g, b, static_cast<size_t>(10) * kBTile, s, a16, w16, bias,
+                                   c, im, in, ik, imt);
             return hipGetLastError();
         }
         const size_t lds = q4k ? static_cast<size_t>(kStages + 2) * kTile + kStages * kRawStage
