@@ -34,7 +34,7 @@ HIDDEN, KV, FFN, VOCAB, LAYERS = 3072, 1024, 8192, 128256, 28
 # measured with rocprofv3 FETCH_SIZE / WRITE_SIZE and scaled by a 1 GiB device
 # copy: profiles/decode_kernels_hbm_traffic.md (command there).  The
 # row-major layout has no measured figure.
-DOMINANT_TRAFFIC_BYTES = {"tiled": 28660679}
+DOMINANT_TRAFFIC_BYTES = {"tiled": 28655556}
 
 
 def log(*a):

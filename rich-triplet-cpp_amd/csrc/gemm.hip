@@ -233,8 +233,8 @@ template <bool W_Q4K>
 __global__ __launch_bounds__(kPThreads) void k_gemm_pipe(const uint16_t* __restrict__ A,
                                                          const void* __restrict__ Wp,
                                                          const float* __restrict__ bias,
-                                                         float* __restrict__ C, int M, int N, int K,
-                                                         int mt) {
+                                                         float* __restrict__ Cp, int M, int N, int K,
+                                                         int mt, int ldk, int64_t c_split) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     uint8_t* const sA = lds;                        // [kStages][kTile]
     uint8_t* const sW = lds + kStages * kTile;      // bf16: [kStages][kTile]; Q4_K: [2][kTile] + raw ring
@@ -254,8 +254,13 @@ __global__ __launch_bounds__(kPThreads) void k_gemm_pipe(const uint16_t* __restr
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    // Split-K slice blockIdx.y: columns [k0, k0 + K) of rows of ldk
+    // elements, into C + blockIdx.y * c_split (the Q4_K path and unsplit
+    // calls have one slice: k0 = 0, ldk = K).
+    const int k0 = static_cast<int>(blockIdx.y) * K;
+    float* const C = Cp + static_cast<int64_t>(blockIdx.y) * c_split;
     const int S = K >> 6;
-    const int64_t rowA = static_cast<int64_t>(K) * 2;
+    const int64_t rowA = static_cast<int64_t>(ldk) * 2;
 
     // Copy roles: wave instruction i (0..3) covers tile rows 8*(4*wave+i) ..
     // +7; lane l fills chunk slot l%8 of row 8*(4*wave+i) + l/8, i.e. global
@@ -266,8 +271,8 @@ __global__ __launch_bounds__(kPThreads) void k_gemm_pipe(const uint16_t* __restr
         const int r = 8 * (4 * wave + i) + (lane >> 3);
         coff[i] = static_cast<uint32_t>(r * rowA + (((lane & 7) ^ (r & 7)) << 4));
     }
-    const uint8_t* const Ab = reinterpret_cast<const uint8_t*>(A) + static_cast<int64_t>(m0) * rowA;
-    const int64_t Aleft = static_cast<int64_t>(M - m0) * rowA;
+    const uint8_t* const Ab = reinterpret_cast<const uint8_t*>(A) + static_cast<int64_t>(m0) * rowA + 2 * k0;
+    const int64_t Aleft = static_cast<int64_t>(M - m0) * rowA - 2 * k0;
     auto copy_tile = [&](uint8_t* dst, const uint8_t* base, int64_t left, int step) {
         const int64_t o = static_cast<int64_t>(step) * 128;  // 64 bf16 per step
         const BufRsrc rs = make_rsrc(base + o, step < S ? left - o : 0);
@@ -277,8 +282,8 @@ __global__ __launch_bounds__(kPThreads) void k_gemm_pipe(const uint16_t* __restr
                 rs, (__attribute__((address_space(3))) void*)(dst + (4 * wave + i) * 1024), 16,
                 static_cast<int>(coff[i]), 0, 0, 0);
     };
-    const uint8_t* const Wb16 = static_cast<const uint8_t*>(Wp) + static_cast<int64_t>(n0) * rowA;
-    const int64_t Wleft16 = static_cast<int64_t>(N - n0) * rowA;
+    const uint8_t* const Wb16 = static_cast<const uint8_t*>(Wp) + static_cast<int64_t>(n0) * rowA + 2 * k0;
+    const int64_t Wleft16 = static_cast<int64_t>(N - n0) * rowA - 2 * k0;
 
     // Q4_K: the raw bytes of a step (per tile row: the super-block header
     // and the step's 32-byte qs chunk) are copied straight into a raw ring
@@ -596,6 +601,19 @@ __global__ __launch_bounds__(256) void k_f32_to_bf16(const float* __restrict__ x
                                            pk_bf16(b[0], b[1]), pk_bf16(b[2], b[3])};
 }
 
+// Split-K: C = sum of the `splits` partial products (in split order, so the
+// result does not depend on scheduling) + bias.  mn % 4 == 0, n % 4 == 0.
+__global__ __launch_bounds__(256) void k_splitk_sum(const float* __restrict__ parts, int splits,
+                                                    const float* __restrict__ bias, float* __restrict__ C,
+                                                    int64_t mn, int64_t n) {
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+    if (i >= mn) return;
+    f32x4 v = *reinterpret_cast<const f32x4*>(parts + i);
+    for (int q = 1; q < splits; ++q) v += *reinterpret_cast<const f32x4*>(parts + q * mn + i);
+    if (bias) v += *reinterpret_cast<const f32x4*>(bias + i % n);
+    *reinterpret_cast<f32x4*>(C + i) = v;
+}
+
 __global__ void k_add_bias(float* __restrict__ y, const float* __restrict__ bias, int64_t m,
                            int64_t n) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -615,12 +633,26 @@ hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, con
         // flux_dequant_q4k) instead of once per M tile inside the GEMM.
         const int64_t mt = (m + 127) / 128, nt = (n + 127) / 128;
         const bool fused_q4k = w_fmt == RT_HIP_Q4K && mt == 1;
+        const int64_t cus = device_info().cus;
+        const int64_t mt2 = (m + 255) / 256, nt2 = (n + 255) / 256;
+        const bool big = !fused_q4k && 4 * mt2 * nt2 >= 3 * cus && tune_param("GEMM_BIG", 1);
+        // Split-K for the 128 x 128 bf16 kernel when its tiles leave at least
+        // half the CUs idle: up to 4 slices of K, each a multiple of 64,
+        // summed afterwards in a fixed order (deterministic).
+        int splits = 1;
+        if (!fused_q4k && !big && 2 * mt * nt <= cus && n % 4 == 0) {
+            splits = static_cast<int>(cus / (mt * nt));
+            splits = splits > 4 ? 4 : splits;
+            while (splits > 1 && k % (64 * splits) != 0) --splits;
+            if (const int forced = tune_param("GEMM_SPLITK", 0)) splits = forced;
+        }
         const size_t a_bytes = a_bf16 ? 0 : static_cast<size_t>(m * k) * 2;
         const size_t w_bytes = (w_fmt == RT_HIP_Q4K && !fused_q4k) ? static_cast<size_t>(n * k) * 2 : 0;
+        const size_t p_bytes = splits > 1 ? static_cast<size_t>(splits) * m * n * 4 : 0;
         uint8_t* ws = nullptr;
-        if (a_bytes + w_bytes) {
+        if (a_bytes + w_bytes + p_bytes) {
             hipError_t e;
-            ws = static_cast<uint8_t*>(workspace(a_bytes + w_bytes, &e));
+            ws = static_cast<uint8_t*>(workspace(a_bytes + w_bytes + p_bytes, &e));
             if (!ws) return e;
         }
         const uint16_t* a16 = static_cast<const uint16_t*>(a);
@@ -639,8 +671,7 @@ hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, con
         const bool q4k = fused_q4k;
         // Large outputs: the 256 x 256 kernel when its tiles cover at least
         // three quarters of the CUs (k % 64 == 0 always holds here).
-        const int64_t mt2 = (m + 255) / 256, nt2 = (n + 255) / 256;
-        if (!q4k && 4 * mt2 * nt2 >= 3 * static_cast<int64_t>(device_info().cus) && tune_param("GEMM_BIG", 1)) {
+        if (big) {
             const dim3 g(static_cast<unsigned>(mt2 * nt2)), b(kBThreads);
             const uint16_t* w16 = static_cast<const uint16_t*>(w);
             const int im = static_cast<int>(m), in = static_cast<int>(n), ik = static_cast<int>(k);
@@ -655,14 +686,22 @@ hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, con
         }
         const size_t lds = q4k ? static_cast<size_t>(kStages + 2) * kTile + kStages * kRawStage
                                : static_cast<size_t>(2 * kStages) * kTile;
-        if (q4k)
-            hipLaunchKernelGGL((k_gemm_pipe<true>), dim3(static_cast<unsigned>(mt * nt)), dim3(kPThreads), lds, s,
-                               a16, w, bias, c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
-                               static_cast<int>(mt));
-        else
-            hipLaunchKernelGGL((k_gemm_pipe<false>), dim3(static_cast<unsigned>(mt * nt)), dim3(kPThreads), lds, s,
-                               a16, w, bias, c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
-                               static_cast<int>(mt));
+        const int im = static_cast<int>(m), in = static_cast<int>(n), ik = static_cast<int>(k);
+        const dim3 g(static_cast<unsigned>(mt * nt)), b(kPThreads);
+        if (q4k) {
+            hipLaunchKernelGGL((k_gemm_pipe<true>), g, b, lds, s, a16, w, bias, c, im, in, ik,
+                               static_cast<int>(mt), ik, int64_t{0});
+        } else if (splits == 1) {
+            hipLaunchKernelGGL((k_gemm_pipe<false>), g, b, lds, s, a16, w, bias, c, im, in, ik,
+                               static_cast<int>(mt), ik, int64_t{0});
+        } else {
+            float* parts = reinterpret_cast<float*>(ws + a_bytes + w_bytes);
+            const int64_t mn = m * n;
+            hipLaunchKernelGGL((k_gemm_pipe<false>), dim3(g.x, static_cast<unsigned>(splits)), b, lds, s, a16, w,
+                               nullptr, parts, im, in, ik / splits, static_cast<int>(mt), ik, mn);
+            hipLaunchKernelGGL(k_splitk_sum, dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0, s,
+                               parts, splits, bias, c, mn, n);
+        }
         return hipGetLastError();
     }
     const dim3 grid(static_cast<unsigned>((n + BN - 1) / BN), static_cast<unsigned>((m + BM - 1) / BM));
