@@ -523,6 +523,9 @@ hipError_t launch_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t
 
 hipError_t launch_gemv_q4_0(const void* w, const float* x, float* y, int64_t n, int64_t k, int m,
                             hipStream_t s) {
+    // M == 1 (decode): whole blocks per lane, rows streamed (gemv_q40.hip).
+    if (m == 1 && q40_m1_lds_bytes(k) <= 65536 && n <= 64ll * 0x7fffffff / 4)
+        return launch_gemv_q4_0_m1(w, x, y, n, k, s);
     return dispatch<Q40Fmt, 1, false>(w, x, y, n, k, m, nullptr, s, RT_HIP_Q4_0);
 }
 

@@ -73,6 +73,9 @@ hipError_t launch_gemv_bf16_m1(const uint16_t* w, const float* x, float* y, int6
                                uint64_t* key, hipStream_t s);
 hipError_t launch_gemv_q4_0(const void* w, const float* x, float* y, int64_t n, int64_t k,
                             int m, hipStream_t s);
+// M = 1 GGUF Q4_0 GEMV (gemv_q40.hip); LDS q40_m1_lds_bytes(k).
+size_t q40_m1_lds_bytes(int64_t k);
+hipError_t launch_gemv_q4_0_m1(const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t s);
 
 hipError_t launch_argmax_init(uint64_t* keys, int64_t rows, hipStream_t s);
 hipError_t launch_argmax_scan(const float* v, int64_t rows, int64_t cols, uint64_t* keys,
