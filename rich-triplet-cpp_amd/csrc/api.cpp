@@ -271,7 +271,6 @@ struct rt_hip_chain {
     uint32_t* sync = nullptr;  // flags, group flags, error word
     size_t sync_words = 0;
     int grid = 0;
-    int ring = 8;
 };
 
 extern "C" {
@@ -287,11 +286,10 @@ int rt_hip_chain_create(const rt_hip_chain_stage* stages, int32_t count, rt_hip_
     const int waves = chain_waves_per_wg();
     const int grid = ds->info.cus;
     if (grid < 1 || grid > chain_max_grid()) return fail(RT_HIP_E_UNSUPPORTED, std::string(fn) + ": CU count");
-    const int ring = 4;
     // Every workgroup must be resident at once (the stage barrier waits for
     // all of them): one per CU.
     int per_cu = 0;
-    e = chain_occupancy(ring, &per_cu);
+    e = chain_occupancy(&per_cu);
     if (e != hipSuccess) return hip_fail(e, fn);
     if (per_cu < 1) return fail(RT_HIP_E_UNSUPPORTED, std::string(fn) + ": chain kernel does not fit a CU");
 
@@ -334,7 +332,6 @@ int rt_hip_chain_create(const rt_hip_chain_stage* stages, int32_t count, rt_hip_
     c->device = ds->info.ordinal;
     c->nst = count;
     c->grid = grid;
-    c->ring = ring;
     c->sync_words = chain_sync_words(grid);
     e = hipMalloc(&c->stages, table.size());
     if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->sync), c->sync_words * 4);
@@ -352,7 +349,7 @@ int rt_hip_chain_create(const rt_hip_chain_stage* stages, int32_t count, rt_hip_
 
 int rt_hip_chain_run(rt_hip_chain* chain, rt_hip_stream stream) {
     if (!chain) return fail(RT_HIP_E_ARG, "rt_hip_chain_run: null chain");
-    return check_stream_launch(launch_chain(chain->stages, chain->nst, chain->sync, chain->grid, chain->ring,
+    return check_stream_launch(launch_chain(chain->stages, chain->nst, chain->sync, chain->grid,
                                             static_cast<hipStream_t>(stream)),
                                "rt_hip_chain_run");
 }

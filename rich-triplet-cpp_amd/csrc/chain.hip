@@ -336,19 +336,16 @@ void chain_fill_stage(void* dst, const float* x, int count, const void* const* w
 
 int chain_waves_per_wg() { return kWaves; }
 
-hipError_t chain_occupancy(int ring, int* blocks_per_cu) {
-    (void)ring;
+hipError_t chain_occupancy(int* blocks_per_cu) {
     return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, k_chain<4, 4>, kThreads, chain_lds_bytes());
 }
 
-hipError_t launch_chain(const void* stages, int nst, uint32_t* sync_words, int grid, int ring,
-                        hipStream_t s) {
+hipError_t launch_chain(const void* stages, int nst, uint32_t* sync_words, int grid, hipStream_t s) {
     Sync sy;
     sy.flags = sync_words;
     sy.gflags = sync_words + static_cast<size_t>(grid) * kFlagDw;
     sy.err = sync_words + chain_err_word(grid);
     const Stage* st = static_cast<const Stage*>(stages);
-    (void)ring;
     const int pre = tune_param("CHAIN_PREFETCH", 0);
     const dim3 g(static_cast<unsigned>(grid)), b(kThreads);
     const size_t lds = chain_lds_bytes();

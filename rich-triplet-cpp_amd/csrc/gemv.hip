@@ -40,7 +40,6 @@ constexpr int kWavesPerBlock = kBlock / kWave;
 // Q4_K: piece = (block b, 16-byte qs half-chunk p); regs = {header, qs}.
 struct Q4kFmt {
     static constexpr int kRegs = 2;
-    static constexpr bool kSums = true;
     __host__ __device__ static int pieces_per_row(int K) { return (K >> 8) * 8; }
     __host__ __device__ static size_t row_bytes(int K) {
         return static_cast<size_t>(K >> 8) * kQ4kBlockBytes;
@@ -161,7 +160,6 @@ struct Q4kFmt {
 // BF16: piece = 8 consecutive values.
 struct Bf16Fmt {
     static constexpr int kRegs = 1;
-    static constexpr bool kSums = false;
     __host__ __device__ static int pieces_per_row(int K) { return K / 8; }
     __host__ __device__ static size_t row_bytes(int K) { return static_cast<size_t>(K) * 2; }
     // LDS layout: piece s (values 8s..8s+7) of activation row m as two
@@ -215,7 +213,6 @@ struct Bf16Fmt {
 // GGUF Q4_0: piece = 8 blocks = 144 bytes = 256 values, 9 x 16-byte loads.
 struct Q40Fmt {
     static constexpr int kRegs = 9;
-    static constexpr bool kSums = true;
     __host__ __device__ static int pieces_per_row(int K) { return K >> 8; }
     __host__ __device__ static size_t row_bytes(int K) { return static_cast<size_t>(K >> 8) * 144; }
     // LDS layout: piece s (values 256s..256s+255) of activation row m as 64

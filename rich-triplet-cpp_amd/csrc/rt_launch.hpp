@@ -61,9 +61,8 @@ size_t chain_err_word(int grid);  // index of the error word in the sync area
 size_t chain_stage_bytes();
 void chain_fill_stage(void* dst, const float* x, int count, const void* const* w, float* const* y,
                       const int64_t* n, int64_t k, int ks, int tiles, int rounds, const int* tile0);
-hipError_t chain_occupancy(int ring, int* blocks_per_cu);
-hipError_t launch_chain(const void* stages, int nst, uint32_t* sync_words, int grid, int ring,
-                        hipStream_t s);
+hipError_t chain_occupancy(int* blocks_per_cu);
+hipError_t launch_chain(const void* stages, int nst, uint32_t* sync_words, int grid, hipStream_t s);
 hipError_t launch_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
                             int m, uint64_t* argmax_key, hipStream_t s);
 // M = 1 BF16 GEMV (gemv_bf16.hip); `key` (may be null) receives the fused
