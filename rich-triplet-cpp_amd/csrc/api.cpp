@@ -181,6 +181,9 @@ int rt_hip_gemv_q4k(const void* blocks, const float* x, float* y, int64_t n, int
                     int32_t m, rt_hip_stream stream) {
     int rc = gemv_args("rt_hip_gemv_q4k", blocks, x, y, n, k, m, 256);
     if (rc) return rc;
+    if (m > 1 && tune_param("GEMV_BATCH_MFMA", 1))
+        return check_stream_launch(launch_gemv_batch(RT_HIP_Q4K, blocks, x, y, n, k, m, static_cast<hipStream_t>(stream)),
+                                   "rt_hip_gemv_q4k");
     return gemv_batched("rt_hip_gemv_q4k", RT_HIP_Q4K, x, y, n, k, m,
                         [&](const float* xx, float* yy, int mm) {
                             return launch_gemv_q4k(blocks, xx, yy, n, k, mm,
@@ -382,6 +385,9 @@ int rt_hip_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int
                      int32_t m, rt_hip_stream stream) {
     int rc = gemv_args("rt_hip_gemv_bf16", w, x, y, n, k, m, 8);
     if (rc) return rc;
+    if (m > 1 && tune_param("GEMV_BATCH_MFMA", 1))
+        return check_stream_launch(launch_gemv_batch(RT_HIP_BF16, w, x, y, n, k, m, static_cast<hipStream_t>(stream)),
+                                   "rt_hip_gemv_bf16");
     return gemv_batched("rt_hip_gemv_bf16", RT_HIP_BF16, x, y, n, k, m,
                         [&](const float* xx, float* yy, int mm) {
                             return launch_gemv_bf16(w, xx, yy, n, k, mm, nullptr,

@@ -63,7 +63,7 @@ struct Q4kFmt {
     // values 32 later; f32x4 number j (0-3 low, 4-7 high) of piece s of
     // activation row m sits at xs4[(m*8 + j)*NP + s], NP = K/32 pieces.
     // The two 16-value sums of piece s sit at sums2[m*NP + s].
-    static size_t lds_floats(int M, int K) {
+    __host__ __device__ static size_t lds_floats(int M, int K) {
         return static_cast<size_t>(M) * K + static_cast<size_t>(M) * (K / 16);
     }
     template <int M>
@@ -165,7 +165,7 @@ struct Bf16Fmt {
     // LDS layout: piece s (values 8s..8s+7) of activation row m as two
     // f32x4 at xs4[(m*2 + j)*NP + s], NP = K/8 (consecutive lanes read
     // consecutive 16-byte chunks).
-    static size_t lds_floats(int M, int K) { return static_cast<size_t>(M) * K; }
+    __host__ __device__ static size_t lds_floats(int M, int K) { return static_cast<size_t>(M) * K; }
     template <int M>
     __device__ static void stage(float* lds, const float* __restrict__ X, int K, int tid, int nthr) {
         const int np = K >> 3;
@@ -218,7 +218,7 @@ struct Q40Fmt {
     // LDS layout: piece s (values 256s..256s+255) of activation row m as 64
     // f32x4 at xs4[(m*64 + j)*NP + s], NP = K/256; the sum of each 32-value
     // block blk of piece s at sums[(m*8 + blk)*NP + s].
-    static size_t lds_floats(int M, int K) { return static_cast<size_t>(M) * K * 33 / 32; }
+    __host__ __device__ static size_t lds_floats(int M, int K) { return static_cast<size_t>(M) * K * 33 / 32; }
     template <int M>
     __device__ static void stage(float* lds, const float* __restrict__ X, int K, int tid, int nthr) {
         const int np = K >> 8;
@@ -310,6 +310,15 @@ struct Q40Fmt {
 
 // ------------------------------------------------------------- driver --
 
+// Row groups a wave may own: its row sums (RG rows x M) wait in a 256-float
+// LDS area per wave until the loop is over, because an output store among
+// the ring's loads makes the compiler wait for every load in flight.
+template <int RG, int M>
+struct ResArea {
+    static constexpr int kGroups = 256 / (RG * M) > 0 ? 256 / (RG * M) : 1;
+};
+constexpr int kResFloatsPerWave = 256;
+
 template <class F, int L, int P, int M, int D, bool ARGMAX>
 __global__ __launch_bounds__(kBlock) void k_gemv(const uint8_t* __restrict__ W,
                                                  const float* __restrict__ X,
@@ -324,17 +333,23 @@ __global__ __launch_bounds__(kBlock) void k_gemv(const uint8_t* __restrict__ W,
     const int S = F::pieces_per_row(K) / L;
     const int G = (N + RG - 1) / RG;
     const int nwaves = gridDim.x * kWavesPerBlock;
-    const int g0 = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const int wave = threadIdx.x >> 6;
+    const int g0 = blockIdx.x * kWavesPerBlock + wave;
     const size_t rb = F::row_bytes(K);
     const typename F::Lane ln = F::lane(li);
+    // This wave's row groups g0, g0 + nwaves, ... (at most
+    // ResArea::kGroups: the launcher sizes the grid) and their pieces, as
+    // one sequence the ring streams without a break between groups.
+    const int Gw = g0 < G ? (G - 1 - g0) / nwaves + 1 : 0;
+    const int Ltot = Gw * S;
 
     u32x4 ring[D][P][F::kRegs];
 
-    // Issue cursor: the next (row group, piece) whose loads go out.
-    int ig = g0, it = 0;
-    // Loads are unconditional (a finished wave re-reads row N-1, in
+    // Issue cursor: the next (row group, piece) whose loads go out.  Loads
+    // are unconditional (past the wave's groups they re-read row N-1, in
     // bounds): a conditional load would make the compiler merge register
-    // versions at every branch and drain the pipeline there.
+    // versions and drain the pipeline.
+    int ig = g0, it = 0;
     auto issue = [&](u32x4 (&slot)[P][F::kRegs]) {
 #pragma unroll
         for (int i = 0; i < P; ++i) {
@@ -342,58 +357,77 @@ __global__ __launch_bounds__(kBlock) void k_gemv(const uint8_t* __restrict__ W,
             row = row < N ? row : N - 1;
             F::template load<L>(W + static_cast<size_t>(row) * rb, li, it, ln, slot[i]);
         }
-        if (++it == S) {
-            it = 0;
-            ig += nwaves;
-        }
+        const bool wrap = it == S - 1;
+        it = __builtin_amdgcn_readfirstlane(wrap ? 0 : it + 1);
+        ig = __builtin_amdgcn_readfirstlane(wrap ? ig + nwaves : ig);
     };
 
 #pragma unroll
-    for (int j = 0; j < D; ++j) issue(ring[j]);
+    for (int j = 0; j < D; ++j) {
+        issue(ring[j]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     F::template stage<M>(lds, X, K, threadIdx.x, kBlock);
 
+    const float* xs = lds;
+    const float* xsum = lds + static_cast<size_t>(M) * K;
+    float* const res = lds + F::lds_floats(M, K) + wave * kResFloatsPerWave;
     uint64_t best = 0;
-    if (g0 < G) {
-        const float* xs = lds;
-        const float* xsum = lds + static_cast<size_t>(M) * K;
-        float acc[P][M];
+    float acc[P][M];
 #pragma unroll
-        for (int i = 0; i < P; ++i)
+    for (int i = 0; i < P; ++i)
 #pragma unroll
-            for (int m = 0; m < M; ++m) acc[i][m] = 0.0f;
-        int cg = g0, ct = 0;
-        for (;;) {
+        for (int m = 0; m < M; ++m) acc[i][m] = 0.0f;
+    int ct = 0, cj = 0;  // consume cursor: piece ct of the wave's group cj
+    // After a group's last piece: reduce its rows over their L lanes and
+    // park the sums in the wave's LDS area.
+    auto finish = [&]() {
+        if (ct == S - 1 && cj < Gw) {
 #pragma unroll
-            for (int j = 0; j < D; ++j) {
-                F::template compute<L, P, M>(ring[j], li, ct, ln, xs, xsum, K, acc);
-                issue(ring[j]);
-                if (++ct == S) {
+            for (int i = 0; i < P; ++i) {
+                const int r = i * R + seg;
 #pragma unroll
-                    for (int i = 0; i < P; ++i) {
-                        const int row = cg * RG + i * R + seg;
-#pragma unroll
-                        for (int m = 0; m < M; ++m) {
-                            const float val = segment_sum<L>(acc[i][m]);
-                            acc[i][m] = 0.0f;
-                            if (li == 0 && row < N) {
-                                Y[static_cast<size_t>(m) * N + row] = val;
-                                if constexpr (ARGMAX) {
-                                    if (val == val) {
-                                        const uint64_t kk = argmax_key(val, static_cast<uint32_t>(row));
-                                        best = kk > best ? kk : best;
-                                    }
-                                }
-                            }
+                for (int m = 0; m < M; ++m) {
+                    const float val = segment_sum<L>(acc[i][m]);
+                    acc[i][m] = 0.0f;
+                    if (li == 0) res[(cj * RG + r) * M + m] = val;
+                    if constexpr (ARGMAX) {
+                        const int row = (g0 + cj * nwaves) * RG + r;
+                        if (val == val && row < N) {
+                            const uint64_t kk = argmax_key(val, static_cast<uint32_t>(row));
+                            best = kk > best ? kk : best;
                         }
                     }
-                    ct = 0;
-                    cg += nwaves;
-                    if (cg >= G) goto done;
                 }
             }
         }
+        const bool wrap = ct == S - 1;
+        ct = __builtin_amdgcn_readfirstlane(wrap ? 0 : ct + 1);
+        cj = __builtin_amdgcn_readfirstlane(wrap ? cj + 1 : cj);
+    };
+
+    // Straight-line rounds: compute slot j, refill it D pieces ahead.  The
+    // last round may run past the wave's pieces: those computes land in a
+    // group the wave does not own and finish() drops them, and the loads
+    // re-read row N-1 -- cheaper than a tail, which the compiler would
+    // specialise into a second copy of the body with its own registers.
+    for (int i0 = 0; i0 < Ltot; i0 += D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            F::template compute<L, P, M>(ring[j], li, ct, ln, xs, xsum, K, acc);
+            __builtin_amdgcn_sched_barrier(0);
+            issue(ring[j]);
+            finish();
+        }
     }
-done:
+
+    // The wave's sums, written out by all its lanes.
+    for (int idx = lane; idx < Gw * RG * M; idx += kWave) {
+        const int j = idx / (RG * M), rem = idx - j * (RG * M);
+        const int r = rem / M, m = rem - r * M;
+        const int row = (g0 + j * nwaves) * RG + r;
+        if (row < N) Y[static_cast<size_t>(m) * N + row] = res[idx];
+    }
     if constexpr (ARGMAX) {
 #pragma unroll
         for (int off = kWave / 2; off >= 1; off >>= 1) {
@@ -432,6 +466,10 @@ hipError_t run(const void* w, const float* x, float* y, int64_t n, int64_t k, ui
     int64_t blocks = (groups + kWavesPerBlock - 1) / kWavesPerBlock;
     const int64_t cap = static_cast<int64_t>(device_info().cus) * 4;
     if (blocks > cap) blocks = cap;
+    // No wave may own more row groups than its result area holds.
+    constexpr int64_t gpw = ResArea<RG, M>::kGroups;
+    const int64_t need = (groups + gpw * kWavesPerBlock - 1) / (gpw * kWavesPerBlock);
+    if (blocks < need) blocks = need;
     hipLaunchKernelGGL((k_gemv<F, L, P, M, D, AM>), dim3(static_cast<unsigned>(blocks)),
                        dim3(kBlock), lds, s, static_cast<const uint8_t*>(w), x, y,
                        static_cast<int>(n), static_cast<int>(k), key);
@@ -496,10 +534,11 @@ hipError_t dispatch(const void* w, const float* x, float* y, int64_t n, int64_t 
 
 size_t gemv_lds_bytes(int fmt, int m, int64_t k) {
     const int kk = static_cast<int>(k);
+    const size_t res = 4 * static_cast<size_t>(kWavesPerBlock) * kResFloatsPerWave;
     switch (fmt) {
-        case RT_HIP_Q4K: return 4 * Q4kFmt::lds_floats(m, kk);
-        case RT_HIP_BF16: return 4 * Bf16Fmt::lds_floats(m, kk);
-        default: return 4 * Q40Fmt::lds_floats(m, kk);
+        case RT_HIP_Q4K: return 4 * Q4kFmt::lds_floats(m, kk) + res;
+        case RT_HIP_BF16: return 4 * Bf16Fmt::lds_floats(m, kk) + res;
+        default: return 4 * Q40Fmt::lds_floats(m, kk) + res;
     }
 }
 

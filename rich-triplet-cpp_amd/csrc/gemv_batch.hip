@@ -1,0 +1,432 @@
+// gemv_batch.hip -- batched GEMV, M = 2..8 activation rows (speculative
+// verify): Y[m][n] = sum_k X[m][k] * W[n][k] on MFMA, every weight byte read
+// once for all M rows (decode_gemma3.msl:416-518, MAX_BATCH 8).
+//
+// One MFMA step covers 32 values of K for a 16-row weight tile and up to four
+// activation rows t of a group q (Q = ceil(M / 4) groups, one MFMA each):
+//  * B is the weight tile: lane l = (n = l%16, g = l/16) supplies the 8
+//    weights of row n at k-slots 8g..8g+7 of the step.
+//  * A row i = 4t + lambda (lambda < 3; row 4t + 3 is zero) is limb lambda of
+//    activation row 4q + t over the same k-slots.
+//  * The output lane (n, g) holds C[4g + r][n], r = 0..3: the three limb
+//    dots of activation row 4q + g for weight row n, combined in the lane.
+//
+// Exact activation limbs, so that the MFMA products are exact:
+//  * BF16 weights (v_mfma_f32_16x16x32_bf16): three bf16 limbs with
+//    h + m + l == x exactly -- h = bf16(x), m = bf16(x - h), l = x - h - m
+//    (each difference is exact in f32, the last has at most 8 significant
+//    bits).  Products of bf16 values are exact in f32, so only the f32
+//    accumulation rounds, as in an f32 dot product.
+//  * Q4_K weights (v_mfma_i32_16x16x32_i8): the step is one 32-value
+//    sub-block, and x carries the int8 limbs of the M = 1 kernel
+//    (q4k_mfma.hpp): per sub-block a power-of-two s and A0 + A1/254 + A2/254^2
+//    == x / s to 2.5e-7 * absmax.  Each limb dot against the nibbles is an
+//    exact int32, and per sub-block j (quant_q4k.cpp:482-523)
+//        sum x * w = (d*sv_j) * (s*C0 + s/254*C1 + s/254^2*C2) - (dmin*mv_j) * sum(x).
+//    Sub-block j's values k = 32j + t sit in byte 32*(j/2) + t of qs, low
+//    nibble for even j and high for odd (quant_q4k.cpp:280-317).
+//
+// Work split.  A workgroup of kWaves waves stages one K-slice of all M rows
+// as limbs in LDS and each wave runs one 16-row tile over that slice, its
+// weights streamed through a ring of D slots.  LDS bounds the slice, so long
+// rows are cut into slices whose partial products a second kernel adds in
+// slice order (deterministic); one slice writes Y directly.  A slice is
+// padded with zero activation steps to whole ring rounds, so the loop has
+// no tail: padded steps add exact zeros, and weight loads past the slice's
+// real slots get an empty buffer range (zeros, no memory traffic).
+#include "rt_common.hpp"
+#include "rt_launch.hpp"
+
+namespace rt_hip {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * kWave;
+constexpr int kZeroBytes = 16;
+
+// ---- formats -------------------------------------------------------------
+// A slot is the unit the ring loads: kSteps 32-value steps of one tile.
+// LDS per (step, group): kLimb bytes of A limbs ([g][t][lambda] x kFrag)
+// and kCst bytes of per-row constants.
+
+struct BBf16 {
+    static constexpr int kSteps = 4;  // 128 values
+    static constexpr int kFrag = 16;  // 8 bf16
+    static constexpr int kLimb = 48 * kFrag;
+    static constexpr int kCst = 0;
+    struct Slot { u32x4 v[4]; };
+    // The tile's rows start at `tile` (row-major, rb bytes apart); the slot
+    // covers values [k, k + 128).  Lane (n, g) reads 16 bytes of row n per
+    // step; pieces past K (K % 8 == 0: all or nothing) read zeros.
+    __device__ static void load(const uint8_t* tile, int64_t left, int64_t rb, int k, int K, int lane,
+                                Slot& s) {
+        const BufRsrc rs = make_rsrc(tile + 2 * static_cast<int64_t>(k), left - 2 * static_cast<int64_t>(k));
+        const uint32_t roff = static_cast<uint32_t>((lane & 15) * rb);
+        const int g = lane >> 4;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const bool in = k + 32 * st + 8 * g < K;
+            s.v[st] = ld16(rs, in ? roff + static_cast<uint32_t>(64 * st + 16 * g) : 0xfffffff0u);
+        }
+    }
+};
+
+struct BQ4k {
+    static constexpr int kSteps = 8;  // one super-block
+    static constexpr int kFrag = 8;   // 8 int8
+    static constexpr int kLimb = 48 * kFrag;
+    static constexpr int kCst = 64;   // 4 rows x {s, s/254, s/254^2, sum}
+    struct Slot {
+        u32x4 h;      // d | dmin << 16, scales[12]
+        u32x2 p[4];   // qs[32c + 8g, +8), c = 0..3
+    };
+    __device__ static void load(const uint8_t* tile, int64_t left, int64_t rb, int k, int, int lane, Slot& s) {
+        const int64_t o = static_cast<int64_t>(k >> 8) * kQ4kBlockBytes;
+        const BufRsrc rs = make_rsrc(tile + o, left - o);
+        const uint32_t roff = static_cast<uint32_t>((lane & 15) * rb);
+        const uint32_t g8 = static_cast<uint32_t>(lane >> 4) * 8u;
+        s.h = ld16(rs, roff);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            s.p[c] = __builtin_bit_cast(
+                u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, static_cast<int>(roff + 16u + 32u * c + g8), 0, 0));
+    }
+};
+
+template <class F>
+__host__ __device__ inline size_t batch_lds_bytes(int steps, int q) {
+    return static_cast<size_t>(steps) * q * (F::kLimb + F::kCst) + kZeroBytes;
+}
+
+// bf16 limbs of four activations (one f32x4): three 8-byte bf16 quads.  An
+// infinite x keeps its infinity in h and zero low limbs.
+__device__ __forceinline__ void bf16_limbs4(const f32x4 v, u32x2& h, u32x2& m, u32x2& l) {
+    uint32_t hb[4], mb[4], lb[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float x = v[e];
+        hb[e] = f32_to_bf16_rne(x);
+        const float hf = __uint_as_float(hb[e] << 16);
+        const float r1 = __builtin_isinf(hf) ? 0.0f : x - hf;
+        mb[e] = f32_to_bf16_rne(r1);
+        const float r2 = r1 - __uint_as_float(mb[e] << 16);
+        lb[e] = f32_to_bf16_rne(r2);
+    }
+    h = u32x2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
+    m = u32x2{mb[0] | (mb[1] << 16), mb[2] | (mb[3] << 16)};
+    l = u32x2{lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
+}
+
+// int8 limbs of four activations scaled by inv = 1/s (exact, power of two),
+// as in q4k_mfma::limbs_of: one dword per limb plane.
+__device__ __forceinline__ void i8_limbs4(const f32x4 v, float inv, uint32_t& w0, uint32_t& w1, uint32_t& w2) {
+    w0 = w1 = w2 = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float r = v[e] * inv;
+        const float a0 = __builtin_rintf(r);
+        const float r1 = (r - a0) * 254.0f;
+        const float a1 = __builtin_rintf(r1);
+        const float a2 = __builtin_rintf((r1 - a1) * 254.0f);
+        w0 |= (static_cast<uint32_t>(static_cast<int>(a0)) & 0xffu) << (8 * e);
+        w1 |= (static_cast<uint32_t>(static_cast<int>(a1)) & 0xffu) << (8 * e);
+        w2 |= (static_cast<uint32_t>(static_cast<int>(a2)) & 0xffu) << (8 * e);
+    }
+}
+
+// Sum and max over the aligned quad of lanes (every lane gets the same bits).
+__device__ __forceinline__ float quad_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4e, 0xf, 0xf, false));
+    return v;
+}
+__device__ __forceinline__ float quad_max(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4e, 0xf, 0xf, false)));
+    return v;
+}
+
+// Workgroup (blockIdx.x, blockIdx.y) = (group of kWaves tiles, K-slice).
+// The slice is `slots` ring slots from slot slice * slots (the last slice may
+// hold fewer real ones); `psteps` = slots padded to whole rounds of D, in
+// steps, is what LDS holds.  Outputs: Y + slice * ystride, [M][N].
+template <class F, int Q, int D, int XP>
+__global__ __launch_bounds__(kThreads) void k_gemv_batch(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                                         float* __restrict__ Y, int N, int K, int M, int slots,
+                                                         int psteps, int64_t ystride) {
+    constexpr bool kQ4 = F::kSteps == 8;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int slice = blockIdx.y;
+    const int k0 = slice * slots * F::kSteps * 32;          // first value of the slice
+    const int kend = min(K, k0 + slots * F::kSteps * 32);  // end of its real values
+    const int tile = blockIdx.x * kWaves + wave;
+    const int row0 = 16 * tile;
+    const int64_t rb = kQ4 ? static_cast<int64_t>(K >> 8) * kQ4kBlockBytes : 2 * static_cast<int64_t>(K);
+    const uint8_t* const tbase = W + static_cast<int64_t>(row0) * rb;
+    const int64_t tleft = static_cast<int64_t>(N - row0) * rb;  // <= 0 past the last tile: zeros
+    // Real slots of this slice; loads of later ones (the padding and the
+    // ring's last refills) get an empty range, so no wave reads a byte of
+    // the next slice.
+    const int nreal = min(slots, (K + F::kSteps * 32 - 1) / (F::kSteps * 32) - slice * slots);
+    auto load = [&](int sl, typename F::Slot& dst) {
+        F::load(tbase, sl < nreal ? tleft : 0, rb, k0 + sl * F::kSteps * 32, K, lane, dst);
+    };
+
+    // x of the slice first, into registers: unit u = (step s, row m, g) is
+    // the 8 values k0 + 32 s + 8 g .. + 8 of row m (zero past the slice).
+    const int units = psteps * M * 4;
+    f32x4 xa[XP], xb[XP];
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+        const int u = tid + kThreads * i;
+        const int g = u & 3, sm = u >> 2;
+        const int s = sm / M, m = sm - s * M;
+        const int kk = k0 + 32 * s + 8 * g;
+        const bool in = u < units && kk < kend;
+        const f32x4* src = reinterpret_cast<const f32x4*>(X + static_cast<int64_t>(in ? m : 0) * K + (in ? kk : 0));
+        const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+        xa[i] = in ? src[0] : z;
+        xb[i] = in ? src[1] : z;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    typename F::Slot ring[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+        load(j, ring[j]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // Limbs (and, for Q4_K, the per-row sub-block constants) into LDS.
+    const uint32_t zoff = static_cast<uint32_t>(psteps * Q * F::kLimb);
+    uint8_t* const cst = lds + zoff + kZeroBytes;
+    if (tid == 0) *reinterpret_cast<u32x4*>(lds + zoff) = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+        const int u = tid + kThreads * i;
+        const int g = u & 3, sm = u >> 2;
+        const int s = sm / M, m = sm - s * M;
+        const int q = m >> 2, t = m & 3;
+        uint8_t* const dst = lds + (static_cast<size_t>(s) * Q + q) * F::kLimb + ((g * 4 + t) * 3) * F::kFrag;
+        if constexpr (kQ4) {
+            // Sub-block (s, m) is the quad of units g = 0..3.
+            float amax = fmaxf(fmaxf(fmaxf(fabsf(xa[i][0]), fabsf(xa[i][1])), fmaxf(fabsf(xa[i][2]), fabsf(xa[i][3]))),
+                               fmaxf(fmaxf(fabsf(xb[i][0]), fabsf(xb[i][1])), fmaxf(fabsf(xb[i][2]), fabsf(xb[i][3]))));
+            float sum = ((xa[i][0] + xa[i][1]) + (xa[i][2] + xa[i][3])) + ((xb[i][0] + xb[i][1]) + (xb[i][2] + xb[i][3]));
+            amax = quad_max(amax);
+            sum = quad_sum(sum);
+            // s = 2^(E-5) for the absmax exponent E; zero (or subnormal-range)
+            // sub-blocks get s = 0 and zero limbs; an Inf/NaN makes s
+            // non-finite, so the output is non-finite as in f32 arithmetic.
+            const uint32_t eb = (__float_as_uint(amax) >> 23) & 0xffu;
+            const bool live = eb > 6 && eb < 0xff;
+            const float sc = live ? __uint_as_float((eb - 5u) << 23) : (eb == 0xff ? amax : 0.0f);
+            const float inv = live ? __uint_as_float((254u - (eb - 5u)) << 23) : 0.0f;
+            uint32_t a0, a1, a2, b0, b1, b2;
+            i8_limbs4(xa[i], inv, a0, a1, a2);
+            i8_limbs4(xb[i], inv, b0, b1, b2);
+            if (u < units) {
+                *reinterpret_cast<u32x2*>(dst) = u32x2{a0, b0};
+                *reinterpret_cast<u32x2*>(dst + 8) = u32x2{a1, b1};
+                *reinterpret_cast<u32x2*>(dst + 16) = u32x2{a2, b2};
+                if (g == 0)
+                    *reinterpret_cast<f32x4*>(cst + ((static_cast<size_t>(s) * Q + q) * 4 + t) * 16) =
+                        f32x4{sc, sc * (1.0f / 254.0f), sc * (1.0f / 64516.0f), sum};
+            }
+        } else {
+            u32x2 ha, ma, la, hb, mb, lb;
+            bf16_limbs4(xa[i], ha, ma, la);
+            bf16_limbs4(xb[i], hb, mb, lb);
+            if (u < units) {
+                u32x4* d4 = reinterpret_cast<u32x4*>(dst);
+                d4[0] = u32x4{ha[0], ha[1], hb[0], hb[1]};
+                d4[1] = u32x4{ma[0], ma[1], mb[0], mb[1]};
+                d4[2] = u32x4{la[0], la[1], lb[0], lb[1]};
+            }
+        }
+    }
+    lds_barrier();
+
+    // This lane's A rows: (t, lambda) = ((l % 16) / 4, l % 4) of group q; a
+    // zero row (lambda == 3, or a row past M) reads the zero line.
+    const int ai = lane & 15, g = lane >> 4;
+    const int at = ai >> 2, al = ai & 3;
+    uint32_t abase[Q], amask[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const bool live = al < 3 && 4 * q + at < M;
+        abase[q] = live ? static_cast<uint32_t>(q * F::kLimb + ((g * 4 + at) * 3 + al) * F::kFrag) : zoff;
+        amask[q] = live ? 0xffffffffu : 0u;
+    }
+    auto a_off = [&](int s, int q) {
+        return abase[q] + ((static_cast<uint32_t>(s) * (Q * F::kLimb)) & amask[q]);
+    };
+
+    f32x4 C[Q];
+    float acc[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        C[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        acc[q] = 0.0f;
+    }
+
+    // Steady rounds (straight-line; slots past the slice load zeros and
+    // compute against zero limbs).
+    const int rounds = psteps / (F::kSteps * D);
+    for (int r = 0; r < rounds; ++r) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            const int slot = r * D + j;
+            const int s0 = slot * F::kSteps;
+            if constexpr (!kQ4) {
+                bf16x8 B[4];
+#pragma unroll
+                for (int st = 0; st < 4; ++st) B[st] = __builtin_bit_cast(bf16x8, ring[j].v[st]);
+                __builtin_amdgcn_sched_barrier(0);
+                load(slot + D, ring[j]);
+#pragma unroll
+                for (int st = 0; st < 4; ++st)
+#pragma unroll
+                    for (int q = 0; q < Q; ++q) {
+                        const bf16x8 A = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(lds + a_off(s0 + st, q)));
+                        C[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B[st], C[q], 0, 0, 0);
+                    }
+            } else {
+                const u32x4 h = ring[j].h;
+                u32x2 p[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) p[c] = ring[j].p[c];
+                __builtin_amdgcn_sched_barrier(0);
+                load(slot + D, ring[j]);
+                const float d = f16_bits_to_f32(h[0] & 0xffffu);
+                const float dmin = f16_bits_to_f32(h[0] >> 16);
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    uint32_t sv, mv;
+                    decode_scale_min(make_scale_sel(jj), h[1], h[2], h[3], sv, mv);
+                    const float a = d * static_cast<float>(sv);
+                    const float dm = dmin * static_cast<float>(mv);
+                    const u32x2 pc = p[jj >> 1];
+                    const uint32_t n0 = (jj & 1) ? (pc[0] >> 4) & 0x0f0f0f0fu : pc[0] & 0x0f0f0f0fu;
+                    const uint32_t n1 = (jj & 1) ? (pc[1] >> 4) & 0x0f0f0f0fu : pc[1] & 0x0f0f0f0fu;
+                    const long B = static_cast<long>((static_cast<uint64_t>(n1) << 32) | n0);
+                    const int s = s0 + jj;
+#pragma unroll
+                    for (int q = 0; q < Q; ++q) {
+                        const long A = *reinterpret_cast<const long*>(lds + a_off(s, q));
+                        const i32x4 z = {0, 0, 0, 0};
+                        const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, z, 0, 0, 0);
+                        const f32x4 k4 = *reinterpret_cast<const f32x4*>(
+                            cst + ((static_cast<uint32_t>(s) * Q + q) * 4 + g) * 16);
+                        float dot = static_cast<float>(c[0]) * k4[0];
+                        dot = __builtin_fmaf(static_cast<float>(c[1]), k4[1], dot);
+                        dot = __builtin_fmaf(static_cast<float>(c[2]), k4[2], dot);
+                        acc[q] = __builtin_fmaf(a, dot, acc[q]);
+                        acc[q] = __builtin_fmaf(-dm, k4[3], acc[q]);
+                    }
+                }
+            }
+        }
+    }
+
+    // Row n of the tile, activation row 4q + g.
+    const int row = row0 + (lane & 15);
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int m = 4 * q + g;
+        const float v = kQ4 ? acc[q] : (C[q][0] + C[q][1]) + C[q][2];
+        if (m < M && row < N) Y[static_cast<int64_t>(slice) * ystride + static_cast<int64_t>(m) * N + row] = v;
+    }
+}
+
+// Y[i] = sum over slices of P[s * total + i], in slice order.
+__global__ __launch_bounds__(256) void k_slice_sum(const float* __restrict__ P, float* __restrict__ Y,
+                                                  int64_t total, int slices) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= total) return;
+    float s = P[i];
+    for (int j = 1; j < slices; ++j) s += P[static_cast<int64_t>(j) * total + i];
+    Y[i] = s;
+}
+
+template <class F, int Q, int D, int XP>
+hipError_t run(const void* w, const float* x, float* y, int64_t n, int64_t k, int m, int slots, int slices,
+               int psteps, int64_t ystride, hipStream_t s) {
+    const int64_t tiles = (n + 15) / 16;
+    const dim3 grid(static_cast<unsigned>((tiles + kWaves - 1) / kWaves), static_cast<unsigned>(slices));
+    hipLaunchKernelGGL((k_gemv_batch<F, Q, D, XP>), grid, dim3(kThreads), batch_lds_bytes<F>(psteps, Q), s,
+                       static_cast<const uint8_t*>(w), x, y, static_cast<int>(n), static_cast<int>(k), m, slots,
+                       psteps, ystride);
+    return hipGetLastError();
+}
+
+template <class F, int D>
+hipError_t dispatch(const void* w, const float* x, float* y, int64_t n, int64_t k, int m, hipStream_t s) {
+    const int q = (m + 3) / 4;
+    const int64_t total_slots = (k + F::kSteps * 32 - 1) / (F::kSteps * 32);
+    // Slots per slice: what the LDS budget holds once padded to whole
+    // rounds, and what XP <= 4 registers of x per thread cover.
+    const size_t budget = static_cast<size_t>(tune_param("BATCH_LDS", 65536));
+    auto padded = [&](int64_t sl) { return (sl + D - 1) / D * D * F::kSteps; };
+    auto fits = [&](int64_t sl) {
+        const int64_t ps = padded(sl);
+        return batch_lds_bytes<F>(static_cast<int>(ps), q) <= budget && ps * m * 4 <= 4 * static_cast<int64_t>(kThreads);
+    };
+    if (!fits(1)) return hipErrorInvalidValue;
+    int64_t per = 1;
+    while (per < total_slots && fits(per + 1)) ++per;
+    // Enough workgroups for every CU: split further while a slice keeps at
+    // least one full round.
+    const int64_t groups = ((n + 15) / 16 + kWaves - 1) / kWaves;
+    const int64_t cus = device_info().cus;
+    int64_t slices = (total_slots + per - 1) / per;
+    while (groups * slices < cus && per > D) {
+        per = (per + 1) / 2;
+        slices = (total_slots + per - 1) / per;
+    }
+    per = (total_slots + slices - 1) / slices;  // balance
+    slices = (total_slots + per - 1) / per;
+    const int psteps = static_cast<int>(padded(per));
+    const int xp = static_cast<int>((static_cast<int64_t>(psteps) * m * 4 + kThreads - 1) / kThreads);
+
+    float* out = y;
+    const int64_t total = static_cast<int64_t>(m) * n;
+    if (slices > 1) {
+        hipError_t e;
+        out = static_cast<float*>(workspace(static_cast<size_t>(slices) * total * sizeof(float), &e));
+        if (!out) return e;
+    }
+    hipError_t e;
+    const int sl = static_cast<int>(per), nsl = static_cast<int>(slices);
+    if (q == 1) {
+        if (xp <= 1) e = run<F, 1, D, 1>(w, x, out, n, k, m, sl, nsl, psteps, total, s);
+        else if (xp <= 2) e = run<F, 1, D, 2>(w, x, out, n, k, m, sl, nsl, psteps, total, s);
+        else e = run<F, 1, D, 4>(w, x, out, n, k, m, sl, nsl, psteps, total, s);
+    } else {
+        if (xp <= 1) e = run<F, 2, D, 1>(w, x, out, n, k, m, sl, nsl, psteps, total, s);
+        else if (xp <= 2) e = run<F, 2, D, 2>(w, x, out, n, k, m, sl, nsl, psteps, total, s);
+        else e = run<F, 2, D, 4>(w, x, out, n, k, m, sl, nsl, psteps, total, s);
+    }
+    if (e != hipSuccess || slices == 1) return e;
+    hipLaunchKernelGGL(k_slice_sum, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s, out, y, total,
+                       nsl);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemv_batch(int fmt, const void* w, const float* x, float* y, int64_t n, int64_t k, int m,
+                             hipStream_t s) {
+    if (m < 2 || m > 8) return hipErrorInvalidValue;
+    if (fmt == RT_HIP_Q4K) return dispatch<BQ4k, 2>(w, x, y, n, k, m, s);
+    if (fmt == RT_HIP_BF16) return dispatch<BBf16, 4>(w, x, y, n, k, m, s);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace rt_hip

@@ -72,6 +72,11 @@ hipError_t launch_gemv_bf16_m1(const uint16_t* w, const float* x, float* y, int6
                                uint64_t* key, hipStream_t s);
 hipError_t launch_gemv_q4_0(const void* w, const float* x, float* y, int64_t n, int64_t k,
                             int m, hipStream_t s);
+// Batched GEMV, 2 <= m <= 8, Q4_K (K % 256 == 0) or BF16 (K % 8 == 0) on
+// bf16 MFMA (gemv_batch.hip): every weight byte is read once for all m rows;
+// K-slices beyond the LDS budget are summed through the library workspace.
+hipError_t launch_gemv_batch(int fmt, const void* w, const float* x, float* y, int64_t n, int64_t k, int m,
+                             hipStream_t s);
 // M = 1 GGUF Q4_0 GEMV (gemv_q40.hip); LDS q40_m1_lds_bytes(k).
 size_t q40_m1_lds_bytes(int64_t k);
 hipError_t launch_gemv_q4_0_m1(const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t s);

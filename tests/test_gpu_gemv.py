@@ -26,6 +26,10 @@ Q4K_CASES = [
     (33, 2304, 1, "K=9 super-blocks (8 lanes per row)"),
     (513, 768, 2, "K=3 super-blocks, M=2"),
     (100, 3072, 8, "speculative batch M=8"),
+    (8192, 3072, 8, "llama gate/up, M=8: K-slices summed in order"),
+    (3072, 8192, 5, "llama down, M=5: a part-filled row group"),
+    (1000, 768, 4, "ragged N, M=4"),
+    (3072, 3072, 2, "llama q/o, M=2"),
     (7, 512, 3, "tiny N"),
     (1, 12288, 1, "single row, K=12288"),
 ]
@@ -124,6 +128,10 @@ BF16_CASES = [
     (131, 200, 1, "K=200 (K/8 = 25: 1 lane per row)"),
     (64, 96, 4, "M=4"),
     (257, 1152, 8, "M=8"),
+    (3072, 8192, 8, "llama down widened, M=8: K-slices"),
+    (1024, 3072, 6, "llama v widened, M=6"),
+    (300, 1000, 2, "K=1000: a part-filled last 128-value slot, M=2"),
+    (33, 8, 3, "K=8, M=3"),
 ]
 
 
