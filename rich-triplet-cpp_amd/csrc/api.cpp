@@ -31,6 +31,7 @@ struct DeviceState {
     bool ok = false;
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    uint32_t* counters = nullptr;  // arrival counters, zero between launches
 };
 
 std::mutex g_mu;
@@ -146,6 +147,26 @@ void* workspace(size_t bytes, hipError_t* err) {
     }
     *err = hipSuccess;
     return st->ws;
+}
+
+uint32_t* arrival_counters(hipError_t* err) {
+    DeviceState* st = state_for_current(err);
+    if (!st) return nullptr;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!st->counters) {
+        void* p = nullptr;
+        *err = hipMalloc(&p, kArrivalCounters * sizeof(uint32_t));
+        if (*err != hipSuccess) return nullptr;
+        *err = hipMemset(p, 0, kArrivalCounters * sizeof(uint32_t));
+        if (*err == hipSuccess) *err = hipDeviceSynchronize();
+        if (*err != hipSuccess) {
+            (void)hipFree(p);
+            return nullptr;
+        }
+        st->counters = static_cast<uint32_t*>(p);
+    }
+    *err = hipSuccess;
+    return st->counters;
 }
 
 }  // namespace rt_hip

@@ -28,9 +28,12 @@
 //
 // Work split.  A workgroup of kWaves waves stages one K-slice of all M rows
 // as limbs in LDS and each wave runs one 16-row tile over that slice, its
-// weights streamed through a ring of D slots.  LDS bounds the slice, so long
-// rows are cut into slices whose partial products a second kernel adds in
-// slice order (deterministic); one slice writes Y directly.  A slice is
+// weights streamed through a ring of D slots.  LDS bounds the slice, and
+// short outputs need several slices to occupy the CUs.  With one slice the
+// workgroup writes Y.  With more, every workgroup writes its partial
+// products to a workspace and counts its arrival for its tile group; the
+// last to arrive adds the group's partials in slice order (so the result
+// does not depend on arrival order) and resets the counter.  A slice is
 // padded with zero activation steps to whole ring rounds, so the loop has
 // no tail: padded steps add exact zeros, and weight loads past the slice's
 // real slots get an empty buffer range (zeros, no memory traffic).
@@ -55,6 +58,7 @@ constexpr int kZeroBytes = 16;
 
 struct BBf16 {
     static constexpr int kSteps = 4;  // 128 values
+    static constexpr int kSlotCost = 1;  // one slot's time, in units of one slice's reduction
     static constexpr int kFrag = 16;  // 8 bf16
     static constexpr int kLimb = 48 * kFrag;
     static constexpr int kCst = 0;
@@ -77,6 +81,7 @@ struct BBf16 {
 
 struct BQ4k {
     static constexpr int kSteps = 8;  // one super-block
+    static constexpr int kSlotCost = 2;  // one slot's time, in units of one slice's reduction
     static constexpr int kFrag = 8;   // 8 int8
     static constexpr int kLimb = 48 * kFrag;
     static constexpr int kCst = 64;   // 4 rows x {s, s/254, s/254^2, sum}
@@ -150,14 +155,27 @@ __device__ __forceinline__ float quad_max(float v) {
     return v;
 }
 
+// Partials are stored and reloaded with agent-scope (device-coherent)
+// accesses: they bypass the per-XCD L2, so the workgroup that reduces them
+// sees every other XCD's stores once those have completed.
+__device__ __forceinline__ void st_dev(float* p, float v) {
+    __hip_atomic_store((__attribute__((address_space(1))) float*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+    return __hip_atomic_load((const __attribute__((address_space(1))) float*)p, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Workgroup (blockIdx.x, blockIdx.y) = (group of kWaves tiles, K-slice).
 // The slice is `slots` ring slots from slot slice * slots (the last slice may
 // hold fewer real ones); `psteps` = slots padded to whole rounds of D, in
-// steps, is what LDS holds.  Outputs: Y + slice * ystride, [M][N].
+// steps, is what LDS holds.  Y is [M][N]; with gridDim.y > 1 slices, P holds
+// the partials ([slice][M][N]) and counters[blockIdx.x] the arrivals.
 template <class F, int Q, int D, int XP>
 __global__ __launch_bounds__(kThreads) void k_gemv_batch(const uint8_t* __restrict__ W, const float* __restrict__ X,
-                                                         float* __restrict__ Y, int N, int K, int M, int slots,
-                                                         int psteps, int64_t ystride) {
+                                                         float* __restrict__ Y, float* __restrict__ P,
+                                                         uint32_t* __restrict__ counters, int N, int K, int M,
+                                                         int slots, int psteps) {
     constexpr bool kQ4 = F::kSteps == 8;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -337,86 +355,123 @@ __global__ __launch_bounds__(kThreads) void k_gemv_batch(const uint8_t* __restri
 
     // Row n of the tile, activation row 4q + g.
     const int row = row0 + (lane & 15);
+    const int nslices = gridDim.y;
+    const int64_t total = static_cast<int64_t>(M) * N;
+    bool keep[Q];
+    int64_t idx[Q];
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
         const int m = 4 * q + g;
+        keep[q] = m < M && row < N;
+        idx[q] = static_cast<int64_t>(m) * N + row;
         const float v = kQ4 ? acc[q] : (C[q][0] + C[q][1]) + C[q][2];
-        if (m < M && row < N) Y[static_cast<int64_t>(slice) * ystride + static_cast<int64_t>(m) * N + row] = v;
+        if (nslices == 1) {
+            if (keep[q]) Y[idx[q]] = v;
+        } else if (keep[q]) {
+            st_dev(P + slice * total + idx[q], v);
+        }
     }
-}
+    if (nslices == 1) return;
 
-// Y[i] = sum over slices of P[s * total + i], in slice order.
-__global__ __launch_bounds__(256) void k_slice_sum(const float* __restrict__ P, float* __restrict__ Y,
-                                                  int64_t total, int slices) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= total) return;
-    float s = P[i];
-    for (int j = 1; j < slices; ++j) s += P[static_cast<int64_t>(j) * total + i];
-    Y[i] = s;
+    // Every wave's partials have completed, then one arrival per workgroup.
+    // The limbs are dead: LDS dword 0 carries the arrival number.
+    wait_vmcnt<0>();
+    lds_barrier();
+    uint32_t* const flag = reinterpret_cast<uint32_t*>(lds);
+    if (tid == 0)
+        *flag = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    lds_barrier();
+    if (*flag != static_cast<uint32_t>(nslices - 1)) return;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        if (!keep[q]) continue;
+        float sum = ld_dev(P + idx[q]);
+        for (int j = 1; j < nslices; ++j) sum += ld_dev(P + j * total + idx[q]);
+        Y[idx[q]] = sum;
+    }
+    if (tid == 0) __hip_atomic_store(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <class F, int Q, int D, int XP>
-hipError_t run(const void* w, const float* x, float* y, int64_t n, int64_t k, int m, int slots, int slices,
-               int psteps, int64_t ystride, hipStream_t s) {
+hipError_t run(const void* w, const float* x, float* y, float* p, uint32_t* counters, int64_t n, int64_t k, int m,
+               int slots, int slices, int psteps, hipStream_t s) {
     const int64_t tiles = (n + 15) / 16;
     const dim3 grid(static_cast<unsigned>((tiles + kWaves - 1) / kWaves), static_cast<unsigned>(slices));
     hipLaunchKernelGGL((k_gemv_batch<F, Q, D, XP>), grid, dim3(kThreads), batch_lds_bytes<F>(psteps, Q), s,
-                       static_cast<const uint8_t*>(w), x, y, static_cast<int>(n), static_cast<int>(k), m, slots,
-                       psteps, ystride);
+                       static_cast<const uint8_t*>(w), x, y, p, counters, static_cast<int>(n), static_cast<int>(k), m,
+                       slots, psteps);
     return hipGetLastError();
 }
 
-template <class F, int D>
+template <class F, int Q, int D>
+hipError_t run_d(const void* w, const float* x, float* y, float* p, uint32_t* counters, int64_t n, int64_t k, int m,
+                 int per, int slices, hipStream_t s) {
+    const int psteps = per * F::kSteps;
+    const int xp = static_cast<int>((static_cast<int64_t>(psteps) * m * 4 + kThreads - 1) / kThreads);
+    if (xp <= 1) return run<F, Q, D, 1>(w, x, y, p, counters, n, k, m, per, slices, psteps, s);
+    if (xp <= 2) return run<F, Q, D, 2>(w, x, y, p, counters, n, k, m, per, slices, psteps, s);
+    return run<F, Q, D, 4>(w, x, y, p, counters, n, k, m, per, slices, psteps, s);
+}
+
+template <class F, int Q>
+hipError_t run_q(const void* w, const float* x, float* y, float* p, uint32_t* counters, int64_t n, int64_t k, int m,
+                 int per, int slices, hipStream_t s) {
+    const int dmax = tune_param("BATCH_DMAX", 1);
+    if (per % 4 == 0 && dmax >= 4) return run_d<F, Q, 4>(w, x, y, p, counters, n, k, m, per, slices, s);
+    if (per % 2 == 0 && dmax >= 2) return run_d<F, Q, 2>(w, x, y, p, counters, n, k, m, per, slices, s);
+    return run_d<F, Q, 1>(w, x, y, p, counters, n, k, m, per, slices, s);
+}
+
+// Slots per slice: what the LDS budget holds and XP <= 4 registers of x per
+// thread cover; among those, the least estimated time
+//     rounds of workgroups over the CUs * kSlotCost * slots per slice
+//     + slices (the last workgroup's reduction reads one partial per slice),
+// ties to the longer slice.  Candidates are the shortest slice for each
+// slice count.  (Fitted to times measured at N x K = 3072x3072, 8192x3072,
+// 3072x8192 (Q4_K), 3072x8192 and 1024x3072 (BF16), M = 2 and 8.)
+// The ring depth: one slot.  Deeper rings (2, 4 slots, selectable for
+// measurement) measured slower at those shapes -- their registers cost
+// resident workgroups, and other waves hide a slot's load better.
+template <class F>
 hipError_t dispatch(const void* w, const float* x, float* y, int64_t n, int64_t k, int m, hipStream_t s) {
     const int q = (m + 3) / 4;
     const int64_t total_slots = (k + F::kSteps * 32 - 1) / (F::kSteps * 32);
-    // Slots per slice: what the LDS budget holds once padded to whole
-    // rounds, and what XP <= 4 registers of x per thread cover.
+    const int64_t groups = ((n + 15) / 16 + kWaves - 1) / kWaves;
+    const int64_t cus = device_info().cus;
     const size_t budget = static_cast<size_t>(tune_param("BATCH_LDS", 65536));
-    auto padded = [&](int64_t sl) { return (sl + D - 1) / D * D * F::kSteps; };
-    auto fits = [&](int64_t sl) {
-        const int64_t ps = padded(sl);
+    auto fits = [&](int64_t per) {
+        const int64_t ps = per * F::kSteps;
         return batch_lds_bytes<F>(static_cast<int>(ps), q) <= budget && ps * m * 4 <= 4 * static_cast<int64_t>(kThreads);
     };
     if (!fits(1)) return hipErrorInvalidValue;
-    int64_t per = 1;
-    while (per < total_slots && fits(per + 1)) ++per;
-    // Enough workgroups for every CU: split further while a slice keeps at
-    // least one full round.
-    const int64_t groups = ((n + 15) / 16 + kWaves - 1) / kWaves;
-    const int64_t cus = device_info().cus;
-    int64_t slices = (total_slots + per - 1) / per;
-    while (groups * slices < cus && per > D) {
-        per = (per + 1) / 2;
-        slices = (total_slots + per - 1) / per;
+    int64_t per = 1, best = -1, prev = 0;
+    for (int64_t sl = 1; sl <= total_slots; ++sl) {
+        const int64_t c = (total_slots + sl - 1) / sl;
+        if (c == prev || !fits(c)) continue;
+        prev = c;
+        const int64_t cost = (groups * sl + cus - 1) / cus * F::kSlotCost * c + sl;
+        if (best < 0 || cost < best) {
+            best = cost;
+            per = c;
+        }
     }
-    per = (total_slots + slices - 1) / slices;  // balance
-    slices = (total_slots + per - 1) / per;
-    const int psteps = static_cast<int>(padded(per));
-    const int xp = static_cast<int>((static_cast<int64_t>(psteps) * m * 4 + kThreads - 1) / kThreads);
+    const int forced = tune_param("BATCH_SLOTS", 0);
+    if (forced > 0 && fits(forced)) per = forced;
+    const int64_t slices = (total_slots + per - 1) / per;
 
-    float* out = y;
-    const int64_t total = static_cast<int64_t>(m) * n;
+    float* part = nullptr;
+    uint32_t* counters = nullptr;
     if (slices > 1) {
+        if (groups > static_cast<int64_t>(kArrivalCounters)) return hipErrorInvalidValue;
         hipError_t e;
-        out = static_cast<float*>(workspace(static_cast<size_t>(slices) * total * sizeof(float), &e));
-        if (!out) return e;
+        counters = arrival_counters(&e);
+        if (!counters) return e;
+        part = static_cast<float*>(workspace(static_cast<size_t>(slices) * m * n * sizeof(float), &e));
+        if (!part) return e;
     }
-    hipError_t e;
     const int sl = static_cast<int>(per), nsl = static_cast<int>(slices);
-    if (q == 1) {
-        if (xp <= 1) e = run<F, 1, D, 1>(w, x, out, n, k, m, sl, nsl, psteps, total, s);
-        else if (xp <= 2) e = run<F, 1, D, 2>(w, x, out, n, k, m, sl, nsl, psteps, total, s);
-        else e = run<F, 1, D, 4>(w, x, out, n, k, m, sl, nsl, psteps, total, s);
-    } else {
-        if (xp <= 1) e = run<F, 2, D, 1>(w, x, out, n, k, m, sl, nsl, psteps, total, s);
-        else if (xp <= 2) e = run<F, 2, D, 2>(w, x, out, n, k, m, sl, nsl, psteps, total, s);
-        else e = run<F, 2, D, 4>(w, x, out, n, k, m, sl, nsl, psteps, total, s);
-    }
-    if (e != hipSuccess || slices == 1) return e;
-    hipLaunchKernelGGL(k_slice_sum, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s, out, y, total,
-                       nsl);
-    return hipGetLastError();
+    if (q == 1) return run_q<F, 1>(w, x, y, part, counters, n, k, m, sl, nsl, s);
+    return run_q<F, 2>(w, x, y, part, counters, n, k, m, sl, nsl, s);
 }
 
 }  // namespace
@@ -424,8 +479,8 @@ hipError_t dispatch(const void* w, const float* x, float* y, int64_t n, int64_t 
 hipError_t launch_gemv_batch(int fmt, const void* w, const float* x, float* y, int64_t n, int64_t k, int m,
                              hipStream_t s) {
     if (m < 2 || m > 8) return hipErrorInvalidValue;
-    if (fmt == RT_HIP_Q4K) return dispatch<BQ4k, 2>(w, x, y, n, k, m, s);
-    if (fmt == RT_HIP_BF16) return dispatch<BBf16, 4>(w, x, y, n, k, m, s);
+    if (fmt == RT_HIP_Q4K) return dispatch<BQ4k>(w, x, y, n, k, m, s);
+    if (fmt == RT_HIP_BF16) return dispatch<BBf16>(w, x, y, n, k, m, s);
     return hipErrorInvalidValue;
 }
 

@@ -23,6 +23,10 @@ int tune_param(const char* name, int fallback);
 
 // Library-owned device workspace, grown on demand, one per device.
 void* workspace(size_t bytes, hipError_t* err);
+// kArrivalCounters zeroed u32 counters per device (allocated on first use).
+// A kernel that counts arrivals in them returns each to zero before it ends.
+constexpr size_t kArrivalCounters = 16384;
+uint32_t* arrival_counters(hipError_t* err);
 
 // Largest M*K the GEMV kernels stage in LDS (f32 activations + 16-value sums).
 size_t gemv_lds_bytes(int fmt, int m, int64_t k);

@@ -223,6 +223,25 @@ def test_q4_0_gemv_matches_oracle(rt, orc, n, k, m, note):
     assert normwise_err(y, y_ref) <= GEMV_TOL
 
 
+@pytest.mark.parametrize("fmt_name,n,k,m", [("Q4K", 8192, 3072, 8), ("BF16", 3072, 8192, 3), ("Q4K", 1024, 3072, 2)])
+def test_batched_gemv_is_deterministic(rt, orc, fmt_name, n, k, m):
+    """Batched GEMVs whose K is cut into slices add the slices' partial
+    products in slice order, whichever workgroup finishes last: repeated
+    calls give the same bits."""
+    say(f"[batched gemv determinism] {fmt_name} N={n} K={k} M={m}")
+    rng = np.random.default_rng(n + k + m)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    fmt = getattr(rt, fmt_name)
+    wb = orc.q4k_quantize(w) if fmt_name == "Q4K" else orc.f32_to_bf16_n(w)
+    dw, dx = to_dev(wb), to_dev(x)
+    first = from_dev(rt.gemv(fmt, dw, dx, n, k))
+    for _ in range(5):
+        assert np.array_equal(from_dev(rt.gemv(fmt, dw, dx, n, k)).view(np.uint32), first.view(np.uint32))
+    ref = orc.q4k_matmul_t(wb, n, k, x) if fmt_name == "Q4K" else orc.bf16_matmul_t(wb, x)
+    assert normwise_err(first, ref) <= GEMV_TOL
+
+
 def test_linear_forward_dispatch_with_bias(rt, orc):
     """QLinear::forward semantics: product plus bias on every row."""
     rng = np.random.default_rng(12)
