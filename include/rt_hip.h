@@ -13,9 +13,11 @@
  * (The reference aborts in its GPU ops, metal_ops.mm:312-315, and asserts
  * on the CPU; a C ABI reports instead.)  Kernels run asynchronously on the
  * given stream (NULL = the legacy default stream); a status of 0 means the
- * launch was accepted.  Calls on different streams may run concurrently;
- * calls that share a workspace (argmax, GEMM) are serialised per stream by
- * the caller's stream order.
+ * launch was accepted.  Calls on different streams may run concurrently,
+ * except calls that use the per-device library workspace -- argmax, GEMM,
+ * and GEMV with m > 1 (its K-slice partials and arrival counters): those
+ * must not overlap on one device (issue them on one stream, or order the
+ * streams).
  *
  * Weight byte formats (verbatim, as the reference holds them in memory):
  *   RT_HIP_Q4K   144-byte GGUF Q4_K super-blocks, K/256 per row
@@ -74,7 +76,9 @@ int rt_hip_init(int ordinal);
  * and the engine kernels gemv_q4k_t / gemv_q4k_t_batch
  * (src/shaders/decode_gemma3.msl:328-470).
  * Requires K % 256 == 0 (the reference's Q4_K precondition, quant.hpp:139,
- * which its Release build does not check -- here it is an error). */
+ * which its Release build does not check -- here it is an error).
+ * m == 1 runs the decode GEMV; m = 2..8 one batched launch that reads each
+ * weight byte once for all m rows. */
 int rt_hip_gemv_q4k(const void* blocks, const float* x, float* y, int64_t n, int64_t k,
                     int32_t m, rt_hip_stream stream);
 
