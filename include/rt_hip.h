@@ -177,6 +177,28 @@ int rt_hip_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int
 int rt_hip_gemv_q4_0(const void* blocks, const float* x, float* y, int64_t n, int64_t k,
                      int32_t m, rt_hip_stream stream);
 
+/* ---- GGUF Q6_K -------------------------------------------------------------
+ * 210-byte blocks, K/256 per row: ql[128] | qh[64] | sc[16] (int8) | d (f16)
+ * (GgufFile::decode_q6k_to_f32, src/gguf.cpp:531-580).  The reference widens
+ * a Q6_K projection to bf16 when it loads it (f32s_to_bf16_and_drop of the
+ * decoded values, src/transformer4_load.cpp:33-41, 141-143) and then runs the
+ * BF16 GEMV.  K % 256 == 0.
+ * rt_hip_dequant_q6k_bf16: that widening on the device, bit-identical:
+ *   out[n][k] = bf16_rne(decode(blocks)[n][k]).
+ * rt_hip_q6k_tiled_bytes / rt_hip_q6k_tile: a size-preserving tiled copy
+ *   (16-row tiles in the GEMV's lane order; no counterpart in the reference,
+ *   made once at load like rt_hip_q4k_tile); -1 for invalid n, k.
+ * rt_hip_gemv_q6k_tiled: y = x * W^T (M == 1, K <= 8192) reading the Q6_K
+ *   bytes (0.82 byte per weight instead of 2) and widening each weight to the
+ *   same bf16 value in registers; equals rt_hip_gemv_bf16 on the widened
+ *   weights to f32 rounding.  Replace: the BF16 GEMV of a Q6_K-widened v or
+ *   down (MatBf16::matmul_by_t, src/mat.cpp:318-414). */
+int rt_hip_dequant_q6k_bf16(const void* blocks, uint16_t* out, int64_t n, int64_t k, rt_hip_stream stream);
+int64_t rt_hip_q6k_tiled_bytes(int64_t n, int64_t k);
+int rt_hip_q6k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, rt_hip_stream stream);
+int rt_hip_gemv_q6k_tiled(const void* tiled, const float* x, float* y, int64_t n, int64_t k,
+                          rt_hip_stream stream);
+
 /* ---- argmax ---------------------------------------------------------------
  * Replace: greedy sampling, src/transformer5.cpp:382-391 -- the first index
  * of the strict maximum of each row; NaN never wins; a row with no value

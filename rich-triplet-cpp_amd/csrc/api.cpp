@@ -427,6 +427,43 @@ int rt_hip_gemv_q4_0(const void* blocks, const float* x, float* y, int64_t n, in
                         });
 }
 
+int rt_hip_dequant_q6k_bf16(const void* blocks, uint16_t* out, int64_t n, int64_t k, rt_hip_stream stream) {
+    const char* fn = "rt_hip_dequant_q6k_bf16";
+    if (!blocks || !out) return fail(RT_HIP_E_ARG, std::string(fn) + ": null pointer");
+    if (n <= 0 || k <= 0) return fail(RT_HIP_E_ARG, std::string(fn) + ": n and k must be > 0");
+    if (k % 256 != 0) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": k must be a multiple of 256");
+    if (n > 0x7fffffffLL || k > 0x7fffffffLL) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": n, k must fit in int32");
+    hipError_t e;
+    if (!state_for_current(&e)) return hip_fail(e, fn);
+    return check_stream_launch(launch_q6k_to_bf16(blocks, out, n, k, static_cast<hipStream_t>(stream)), fn);
+}
+
+int64_t rt_hip_q6k_tiled_bytes(int64_t n, int64_t k) {
+    if (n <= 0 || k <= 0 || k % 256 != 0 || n > 0x7fffffffLL || k > 0x7fffffffLL) return -1;
+    return q6k_tiled_bytes(n, k);
+}
+
+int rt_hip_q6k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, rt_hip_stream stream) {
+    const char* fn = "rt_hip_q6k_tile";
+    if (!blocks || !tiled) return fail(RT_HIP_E_ARG, std::string(fn) + ": null pointer");
+    if (rt_hip_q6k_tiled_bytes(n, k) < 0) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": invalid n, k");
+    if ((n + 15) / 16 > 65535) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": n too large");
+    hipError_t e;
+    if (!state_for_current(&e)) return hip_fail(e, fn);
+    return check_stream_launch(launch_q6k_tile(blocks, tiled, n, k, static_cast<hipStream_t>(stream)), fn);
+}
+
+int rt_hip_gemv_q6k_tiled(const void* tiled, const float* x, float* y, int64_t n, int64_t k,
+                          rt_hip_stream stream) {
+    const char* fn = "rt_hip_gemv_q6k_tiled";
+    int rc = gemv_args(fn, tiled, x, y, n, k, 1, 256);
+    if (rc) return rc;
+    if (k > 8192) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 8192");
+    hipError_t e;
+    if (!state_for_current(&e)) return hip_fail(e, fn);
+    return check_stream_launch(launch_gemv_q6k(tiled, x, y, n, k, static_cast<hipStream_t>(stream)), fn);
+}
+
 int rt_hip_argmax(const float* logits, int64_t rows, int64_t cols, int64_t* idx, float* val,
                   rt_hip_stream stream) {
     if (!logits || !idx) return fail(RT_HIP_E_ARG, "rt_hip_argmax: null pointer");

@@ -85,6 +85,14 @@ hipError_t launch_gemv_batch(int fmt, const void* w, const float* x, float* y, i
 size_t q40_m1_lds_bytes(int64_t k);
 hipError_t launch_gemv_q4_0_m1(const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t s);
 
+// GGUF Q6_K (gemv_q6k.hip): the widening to bf16 (the reference's load),
+// the tiled copy and the M = 1 GEMV on it (K % 256 == 0, K <= 8192).
+size_t q6k_gemv_lds_bytes(int64_t k);
+int64_t q6k_tiled_bytes(int64_t n, int64_t k);
+hipError_t launch_q6k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, hipStream_t s);
+hipError_t launch_q6k_to_bf16(const void* blocks, uint16_t* dst, int64_t n, int64_t k, hipStream_t s);
+hipError_t launch_gemv_q6k(const void* tiled, const float* x, float* y, int64_t n, int64_t k, hipStream_t s);
+
 hipError_t launch_argmax_init(uint64_t* keys, int64_t rows, hipStream_t s);
 hipError_t launch_argmax_scan(const float* v, int64_t rows, int64_t cols, uint64_t* keys,
                               hipStream_t s);

@@ -41,6 +41,9 @@ _SIGNATURES = {
     "rt_hip_linear_forward": [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_bf16": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp, _i64,
                                    _vp, _i64, _vp],
+    "rt_hip_dequant_q6k_bf16": [_vp, _vp, _i64, _i64, _vp],
+    "rt_hip_q6k_tile": [_vp, _vp, _i64, _i64, _vp],
+    "rt_hip_gemv_q6k_tiled": [_vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_chain_run": [_vp, _vp],
     "rt_hip_chain_status": [_vp, _i32],
     "rt_hip_chain_destroy": [_vp],
@@ -80,6 +83,8 @@ class Library:
         self.lib.rt_hip_version.restype = C.c_char_p
         self.lib.rt_hip_q4k_tiled_bytes.restype = C.c_int64
         self.lib.rt_hip_q4k_tiled_bytes.argtypes = [_i64, _i64]
+        self.lib.rt_hip_q6k_tiled_bytes.restype = C.c_int64
+        self.lib.rt_hip_q6k_tiled_bytes.argtypes = [_i64, _i64]
         self.lib.rt_hip_chain_create.restype = C.c_int
         self.lib.rt_hip_chain_create.argtypes = [C.POINTER(ChainStage), _i32, C.POINTER(_vp)]
         for name, args in _SIGNATURES.items():
@@ -220,6 +225,36 @@ def gemv_q4k_tiled_bf16(ws, ns, wb, nb: int, x, k: int, ys=None, yb=None, stream
     library().call("rt_hip_gemv_q4k_tiled_bf16", count, wp, yp, npp, _ptr(wb), _ptr(yb), nb, _ptr(x), k,
                    _stream(stream))
     return ys, yb
+
+
+def dequant_q6k_bf16(blocks, n: int, k: int, stream=None):
+    """GGUF Q6_K blocks -> bf16 [n, k] (as int16 bits), the reference's widening."""
+    torch = _torch()
+    out = torch.empty((n, k), dtype=torch.int16, device=blocks.device)
+    _dev_check(blocks, out)
+    library().call("rt_hip_dequant_q6k_bf16", _ptr(blocks), _ptr(out), n, k, _stream(stream))
+    return out
+
+
+def q6k_tiled_bytes(n: int, k: int) -> int:
+    return library().lib.rt_hip_q6k_tiled_bytes(n, k)
+
+
+def q6k_tile(blocks, n: int, k: int, stream=None):
+    torch = _torch()
+    out = torch.empty(q6k_tiled_bytes(n, k), dtype=torch.uint8, device=blocks.device)
+    _dev_check(blocks, out)
+    library().call("rt_hip_q6k_tile", _ptr(blocks), _ptr(out), n, k, _stream(stream))
+    return out
+
+
+def gemv_q6k_tiled(tiled, x, n: int, k: int, y=None, stream=None):
+    torch = _torch()
+    if y is None:
+        y = torch.empty((1, n), dtype=torch.float32, device=x.device)
+    _dev_check(tiled, x, y)
+    library().call("rt_hip_gemv_q6k_tiled", _ptr(tiled), _ptr(x), _ptr(y), n, k, _stream(stream))
+    return y
 
 
 class Chain:
