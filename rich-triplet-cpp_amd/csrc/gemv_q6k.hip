@@ -50,7 +50,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kBlk = 210;
 constexpr int kTileBlk = 16 * kBlk;  // 3360
 constexpr int kOffQh = 2048, kOffSc = 3072, kOffD = 3328;
-constexpr int kThreads = 256;        // 4 waves
+constexpr int kThreads = 256;        // 4 waves (K splits up to 4)
+constexpr int kMaxThreads = 1024;    // 16 waves (one tile split 6, 8, 12 or 16 ways)
 constexpr int kStepBytes = 192;      // x limbs of one 32-value step: 3 limbs x 32 bf16
 constexpr int kMaxK = 8192;
 
@@ -170,17 +171,18 @@ __device__ __forceinline__ void limbs4(const f32x4 v, u32x2& h, u32x2& m, u32x2&
     l = u32x2{lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
 }
 
-// Workgroup of 4 waves: TPW = 4 / KS tiles, each split over KS waves by
-// blocks.  LDS: x limbs [K/32 steps][3][32] bf16, a zero line, then the KS
-// partial rows.
-template <int D, int XP>
-__global__ __launch_bounds__(kThreads) void k_gemv_q6k(const uint8_t* __restrict__ W, const float* __restrict__ X,
-                                                      float* __restrict__ Y, int N, int K, int KS) {
+// Workgroup of T threads: KS <= 4 runs 4 waves, TPW = 4 / KS tiles each
+// split over KS waves by blocks; larger KS runs one tile on KS waves.  LDS:
+// x limbs [K/32 steps][3][32] bf16, a zero line, then the KS partial rows.
+template <int D, int XP, int T>
+__global__ __launch_bounds__(T) void k_gemv_q6k(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                               float* __restrict__ Y, int N, int K, int KS) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nb = K >> 8;
-    const int tpw = 4 / KS;
+    const int nthr = static_cast<int>(blockDim.x);
+    const int tpw = (nthr >> 6) / KS;
     const int ks = wave % KS, tslot = wave / KS;
     const int tile = blockIdx.x * tpw + tslot;
     const int bpw = nb / KS;  // the host picks KS | nb
@@ -195,7 +197,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q6k(const uint8_t* __restrict
     f32x4 xa[XP], xb[XP];
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
-        const int u = tid + kThreads * i;
+        const int u = tid + nthr * i;
         const f32x4* src = reinterpret_cast<const f32x4*>(X) + 2 * (u < units ? u : 0);
         xa[i] = src[0];
         xb[i] = src[1];
@@ -217,7 +219,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q6k(const uint8_t* __restrict
     if (tid == 0) *reinterpret_cast<u32x4*>(lds + zoff) = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
-        const int u = tid + kThreads * i;
+        const int u = tid + nthr * i;
         u32x2 ha, ma, la, hb, mb, lb;
         limbs4(xa[i], ha, ma, la);
         limbs4(xb[i], hb, mb, lb);
@@ -277,7 +279,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q6k(const uint8_t* __restrict
     if (KS == 1) {
         if (lane < 16 && row < N) Y[row] = v;
     } else {
-        float* red = reinterpret_cast<float*>(lds + zoff + 16);  // [tpw][KS][16]
+        float* red = reinterpret_cast<float*>(lds + zoff + 16);  // [tpw][KS][16], tpw * KS <= 16
         float* rp = red + tslot * KS * 16;
         if (lane < 16) rp[ks * 16 + lane] = v;
         lds_barrier();
@@ -289,19 +291,30 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q6k(const uint8_t* __restrict
     }
 }
 
-template <int D, int XP>
+template <int D, int XP, int T>
 hipError_t run(const void* w, const float* x, float* y, int64_t n, int64_t k, int ks, hipStream_t s) {
     const int64_t tiles = (n + 15) / 16;
-    const int tpw = 4 / ks;
+    const int waves = ks <= 4 ? 4 : ks;
+    const int tpw = waves / ks;
     const int64_t wgs = (tiles + tpw - 1) / tpw;
-    hipLaunchKernelGGL((k_gemv_q6k<D, XP>), dim3(static_cast<unsigned>(wgs)), dim3(kThreads), q6k_gemv_lds_bytes(k), s,
-                       static_cast<const uint8_t*>(w), x, y, static_cast<int>(n), static_cast<int>(k), ks);
+    hipLaunchKernelGGL((k_gemv_q6k<D, XP, T>), dim3(static_cast<unsigned>(wgs)), dim3(static_cast<unsigned>(waves * kWave)),
+                       q6k_gemv_lds_bytes(k), s, static_cast<const uint8_t*>(w), x, y, static_cast<int>(n),
+                       static_cast<int>(k), ks);
     return hipGetLastError();
+}
+
+template <int D, int T>
+hipError_t run_xp(const void* w, const float* x, float* y, int64_t n, int64_t k, int ks, hipStream_t s) {
+    const int waves = ks <= 4 ? 4 : ks;
+    const int64_t per = (k / 8 + waves * kWave - 1) / (waves * kWave);  // 8-value units of x per thread
+    if (per <= 1) return run<D, 1, T>(w, x, y, n, k, ks, s);
+    if (per <= 2) return run<D, 2, T>(w, x, y, n, k, ks, s);
+    return run<D, 4, T>(w, x, y, n, k, ks, s);
 }
 
 }  // namespace
 
-size_t q6k_gemv_lds_bytes(int64_t k) { return static_cast<size_t>(k / 32) * kStepBytes + 16 + 4 * 16 * sizeof(float); }
+size_t q6k_gemv_lds_bytes(int64_t k) { return static_cast<size_t>(k / 32) * kStepBytes + 16 + 16 * 16 * sizeof(float); }
 
 int64_t q6k_tiled_bytes(int64_t n, int64_t k) { return (n + 15) / 16 * (k / 256) * kTileBlk; }
 
@@ -322,23 +335,30 @@ hipError_t launch_q6k_to_bf16(const void* blocks, uint16_t* dst, int64_t n, int6
     return hipGetLastError();
 }
 
-// K split per tile, as the Q4_K GEMV: 4 waves per workgroup (4 / KS tiles),
-// the largest KS in {4, 2, 1} that divides the blocks, leaves each wave two
-// and keeps one round of workgroups.
+// K split per tile, as the Q4_K GEMV: the largest split of {1, 2, 3, 4, 6,
+// 8, 12, 16} that divides the blocks, leaves every wave two of them and keeps
+// one round of workgroups.  The widening makes this GEMV VALU-heavy (about
+// four VALU per weight), so it wants more waves than the streaming GEMVs:
+// splits above 4 run one tile on KS waves with a two-slot ring (<= 128 VGPRs,
+// four waves per SIMD).
 hipError_t launch_gemv_q6k(const void* tiled, const float* x, float* y, int64_t n, int64_t k, hipStream_t s) {
     if (k % 256 != 0 || k > kMaxK) return hipErrorInvalidValue;
     const int64_t nb = k / 256, tiles = (n + 15) / 16, cus = device_info().cus;
+    static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16};
+    auto wgs_for = [&](int c) {
+        const int64_t tpw = c <= 4 ? 4 / c : 1;
+        return (tiles + tpw - 1) / tpw;
+    };
     int ks = 1;
-    for (int c : {4, 2})
-        if (nb % c == 0 && 2 * c <= nb && (tiles + (4 / c) - 1) / (4 / c) <= cus) {
-            ks = c;
-            break;
-        }
-    if (const int forced = tune_param("Q6K_KS", 0)) ks = (forced == 1 || forced == 2 || forced == 4) && nb % forced == 0 ? forced : ks;
-    const int64_t per = (k / 8 + kThreads - 1) / kThreads;  // 8-value units of x per thread
-    if (per <= 1) return run<4, 1>(tiled, x, y, n, k, ks, s);
-    if (per <= 2) return run<4, 2>(tiled, x, y, n, k, ks, s);
-    return run<4, 4>(tiled, x, y, n, k, ks, s);
+    for (int c : kSplits) {
+        if (nb % c != 0 || (c > 1 && 2 * c > nb) || (c == 3)) continue;
+        if (wgs_for(c) <= cus) ks = c;
+    }
+    if (const int forced = tune_param("Q6K_KS", 0))
+        for (int c : kSplits)
+            if (c == forced && nb % c == 0 && c != 3) ks = c;
+    if (ks <= 4) return run_xp<4, kThreads>(tiled, x, y, n, k, ks, s);
+    return run_xp<2, kMaxThreads>(tiled, x, y, n, k, ks, s);
 }
 
 }  // namespace rt_hip
