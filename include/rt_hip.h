@@ -46,7 +46,8 @@ typedef enum {
                                   pointer not 16-byte aligned */
     RT_HIP_E_OOM = 4,          /* device allocation failed */
     RT_HIP_E_HIP = 5,          /* a HIP runtime call failed */
-    RT_HIP_E_UNSUPPORTED = 6   /* no gfx950 device, or format not handled */
+    RT_HIP_E_UNSUPPORTED = 6,  /* no gfx950 device, or format not handled */
+    RT_HIP_E_FORMAT = 7        /* a GGUF file that is not one, or is corrupt */
 } rt_hip_status;
 
 typedef enum {
@@ -198,6 +199,64 @@ int64_t rt_hip_q6k_tiled_bytes(int64_t n, int64_t k);
 int rt_hip_q6k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, rt_hip_stream stream);
 int rt_hip_gemv_q6k_tiled(const void* tiled, const float* x, float* y, int64_t n, int64_t k,
                           rt_hip_stream stream);
+
+/* ---- GGUF files: reading and uploading weights ------------------------------
+ * Replace: GgufFile::open, find_tensor, read_tensor_bytes and the metadata
+ * accessors (include/rt/gguf.hpp:130-200, src/gguf.cpp:100-368), and the
+ * engine's verbatim upload (upload_linear_detect_type,
+ * src/metal_decode.mm:157-176).  GGUF v2/v3: header, typed metadata (nested
+ * arrays), tensor infos, data at an aligned offset (metadata
+ * "general.alignment", default 32).  The file is mapped read-only; a file
+ * that is not GGUF ("not a GGUF file: <path>"), an unsupported version, or a
+ * header or tensor running past the end of the file fails with
+ * RT_HIP_E_FORMAT.  Tensor types are the ggml ids (gguf.hpp:46-77); bytes
+ * are sized for F32, F16, BF16, Q4_0, Q8_0, Q4_K, Q5_K and Q6_K
+ * (gguf_block_info, gguf.cpp:81-93) and -1 otherwise.
+ * The layer formats: a Q4_K tensor's bytes are rt_hip_gemv_q4k's blocks; a
+ * Q4_0 tensor's, rt_hip_gemv_q4_0's; BF16, rt_hip_gemv_bf16's; a Q6_K
+ * tensor is widened by rt_hip_dequant_q6k_bf16 (or tiled for
+ * rt_hip_gemv_q6k_tiled).  A 2-D tensor [in, out] is the [out, in] weight
+ * of y = x W^T (rt_hip_gguf_linear_shape, as the reference's
+ * transposed_shape, gguf.cpp:371-381). */
+enum {
+    RT_HIP_GGUF_F32 = 0, RT_HIP_GGUF_F16 = 1, RT_HIP_GGUF_Q4_0 = 2, RT_HIP_GGUF_Q8_0 = 8,
+    RT_HIP_GGUF_Q4_K = 12, RT_HIP_GGUF_Q5_K = 13, RT_HIP_GGUF_Q6_K = 14, RT_HIP_GGUF_BF16 = 30
+};
+#define RT_HIP_GGUF_MAX_DIMS 4
+
+typedef struct rt_hip_gguf rt_hip_gguf;
+
+typedef struct rt_hip_gguf_tensor {
+    const char* name;     /* valid until rt_hip_gguf_close */
+    int32_t type;         /* ggml type id */
+    int32_t n_dims;
+    int64_t dims[RT_HIP_GGUF_MAX_DIMS];  /* GGUF order: dims[0] is the fastest */
+    int64_t n_elements;
+    int64_t bytes;        /* -1 for a type this reader does not size */
+    int64_t file_offset;  /* of the data in the file, -1 if not sized */
+} rt_hip_gguf_tensor;
+
+int64_t rt_hip_gguf_type_bytes(int32_t type, int64_t n_elements);
+int rt_hip_gguf_open(const char* path, rt_hip_gguf** out);
+void rt_hip_gguf_close(rt_hip_gguf* file);
+int64_t rt_hip_gguf_tensor_count(const rt_hip_gguf* file);
+int64_t rt_hip_gguf_find_tensor(const rt_hip_gguf* file, const char* name); /* -1 if absent */
+int rt_hip_gguf_tensor_info(const rt_hip_gguf* file, int64_t index, rt_hip_gguf_tensor* out);
+int rt_hip_gguf_linear_shape(const rt_hip_gguf* file, int64_t index, int64_t* rows, int64_t* cols);
+/* bytes must equal the tensor's size.  read: into host memory; upload: to
+ * device memory (returns once the copy is complete). */
+int rt_hip_gguf_read_tensor(const rt_hip_gguf* file, int64_t index, void* host_dst, int64_t bytes);
+int rt_hip_gguf_upload(const rt_hip_gguf* file, int64_t index, void* device_dst, int64_t bytes,
+                       rt_hip_stream stream);
+/* Metadata by key; index >= 0 selects an element of an array value.  Strings
+ * stay valid until rt_hip_gguf_close.  As the reference's accessors
+ * (GgufMetaValue::as_u64 / as_f32 / as_str, gguf.cpp:104-128): u64 reads
+ * u8, u16, u32, u64, i32 and i64 (signed ones sign-extended), f32 reads
+ * f32 and f64; other types are RT_HIP_E_UNSUPPORTED. */
+int rt_hip_gguf_meta_u64(const rt_hip_gguf* file, const char* key, int64_t index, uint64_t* out);
+int rt_hip_gguf_meta_f32(const rt_hip_gguf* file, const char* key, int64_t index, float* out);
+int rt_hip_gguf_meta_str(const rt_hip_gguf* file, const char* key, int64_t index, const char** out);
+int64_t rt_hip_gguf_meta_array_len(const rt_hip_gguf* file, const char* key); /* -1 if not an array */
 
 /* ---- argmax ---------------------------------------------------------------
  * Replace: greedy sampling, src/transformer5.cpp:382-391 -- the first index

@@ -109,6 +109,8 @@ int gemv_batched(const char* fn, int fmt, const float* x, float* y, int64_t n, i
 
 }  // namespace
 
+int set_error(int code, const std::string& msg) { return fail(code, msg); }
+
 const DeviceInfo& device_info() {
     hipError_t e;
     DeviceState* st = state_for_current(&e);

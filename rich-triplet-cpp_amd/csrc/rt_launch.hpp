@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <string>
+
 #include "rt_hip.h"
 
 namespace rt_hip {
@@ -16,6 +18,10 @@ struct DeviceInfo {
     size_t lds_per_block = 65536;
 };
 const DeviceInfo& device_info();
+
+// Records `msg` as the calling thread's last error (rt_hip_last_error) and
+// returns `code` (host code outside api.cpp).
+int set_error(int code, const std::string& msg);
 
 // Integer tuning knob read once from the environment (RT_HIP_<name>), else
 // `fallback`.  Used for launch-shape sweeps; defaults are the measured best.

@@ -50,6 +50,29 @@ _SIGNATURES = {
 }
 
 
+class GgufTensor(C.Structure):
+    """rt_hip_gguf_tensor (include/rt_hip.h)."""
+    _fields_ = [("name", C.c_char_p), ("type", _i32), ("n_dims", _i32), ("dims", _i64 * 4), ("n_elements", _i64),
+                ("bytes", _i64), ("file_offset", _i64)]
+
+
+_GGUF_SIGNATURES = [
+    ("rt_hip_gguf_type_bytes", _i64, [_i32, _i64]),
+    ("rt_hip_gguf_open", C.c_int, [C.c_char_p, C.POINTER(_vp)]),
+    ("rt_hip_gguf_close", None, [_vp]),
+    ("rt_hip_gguf_tensor_count", _i64, [_vp]),
+    ("rt_hip_gguf_find_tensor", _i64, [_vp, C.c_char_p]),
+    ("rt_hip_gguf_tensor_info", C.c_int, [_vp, _i64, C.POINTER(GgufTensor)]),
+    ("rt_hip_gguf_linear_shape", C.c_int, [_vp, _i64, C.POINTER(_i64), C.POINTER(_i64)]),
+    ("rt_hip_gguf_read_tensor", C.c_int, [_vp, _i64, _vp, _i64]),
+    ("rt_hip_gguf_upload", C.c_int, [_vp, _i64, _vp, _i64, _vp]),
+    ("rt_hip_gguf_meta_u64", C.c_int, [_vp, C.c_char_p, _i64, C.POINTER(C.c_uint64)]),
+    ("rt_hip_gguf_meta_f32", C.c_int, [_vp, C.c_char_p, _i64, C.POINTER(C.c_float)]),
+    ("rt_hip_gguf_meta_str", C.c_int, [_vp, C.c_char_p, _i64, C.POINTER(C.c_char_p)]),
+    ("rt_hip_gguf_meta_array_len", _i64, [_vp, C.c_char_p]),
+]
+
+
 class ChainStage(C.Structure):
     """rt_hip_chain_stage (include/rt_hip.h)."""
     _fields_ = [("x", _vp), ("k", _i64), ("count", _i32), ("w", _vp * 4), ("y", _vp * 4),
@@ -85,6 +108,10 @@ class Library:
         self.lib.rt_hip_q4k_tiled_bytes.argtypes = [_i64, _i64]
         self.lib.rt_hip_q6k_tiled_bytes.restype = C.c_int64
         self.lib.rt_hip_q6k_tiled_bytes.argtypes = [_i64, _i64]
+        for name, res, args in _GGUF_SIGNATURES:
+            fn = getattr(self.lib, name)
+            fn.restype = res
+            fn.argtypes = args
         self.lib.rt_hip_chain_create.restype = C.c_int
         self.lib.rt_hip_chain_create.argtypes = [C.POINTER(ChainStage), _i32, C.POINTER(_vp)]
         for name, args in _SIGNATURES.items():
@@ -255,6 +282,74 @@ def gemv_q6k_tiled(tiled, x, n: int, k: int, y=None, stream=None):
     _dev_check(tiled, x, y)
     library().call("rt_hip_gemv_q6k_tiled", _ptr(tiled), _ptr(x), _ptr(y), n, k, _stream(stream))
     return y
+
+
+class GgufFile:
+    """A GGUF file opened through rt_hip_gguf_* (the reference's GgufFile)."""
+
+    def __init__(self, path: str):
+        self._lib = library()
+        h = _vp()
+        self._lib.call("rt_hip_gguf_open", os.fsencode(path), C.byref(h))
+        self.h = h
+
+    def close(self) -> None:
+        if self.h:
+            self._lib.lib.rt_hip_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __len__(self) -> int:
+        return self._lib.lib.rt_hip_gguf_tensor_count(self.h)
+
+    def find(self, name: str) -> int:
+        return self._lib.lib.rt_hip_gguf_find_tensor(self.h, name.encode())
+
+    def info(self, idx: int) -> dict:
+        t = GgufTensor()
+        self._lib.call("rt_hip_gguf_tensor_info", self.h, idx, C.byref(t))
+        return {"name": t.name.decode(), "type": t.type, "dims": [t.dims[d] for d in range(t.n_dims)],
+                "n_elements": t.n_elements, "bytes": t.bytes, "file_offset": t.file_offset}
+
+    def linear_shape(self, idx: int):
+        r, c = _i64(), _i64()
+        self._lib.call("rt_hip_gguf_linear_shape", self.h, idx, C.byref(r), C.byref(c))
+        return r.value, c.value
+
+    def read(self, idx: int):
+        import numpy as np
+        out = np.empty(self.info(idx)["bytes"], np.uint8)
+        self._lib.call("rt_hip_gguf_read_tensor", self.h, idx, out.ctypes.data, out.size)
+        return out
+
+    def upload(self, idx: int, device=None, stream=None):
+        torch = _torch()
+        out = torch.empty(self.info(idx)["bytes"], dtype=torch.uint8, device=device or "cuda")
+        self._lib.call("rt_hip_gguf_upload", self.h, idx, _ptr(out), out.numel(), _stream(stream))
+        return out
+
+    def meta_u64(self, key: str, index: int = -1) -> int:
+        v = C.c_uint64()
+        self._lib.call("rt_hip_gguf_meta_u64", self.h, key.encode(), index, C.byref(v))
+        return v.value
+
+    def meta_f32(self, key: str, index: int = -1) -> float:
+        v = C.c_float()
+        self._lib.call("rt_hip_gguf_meta_f32", self.h, key.encode(), index, C.byref(v))
+        return v.value
+
+    def meta_str(self, key: str, index: int = -1) -> str:
+        v = C.c_char_p()
+        self._lib.call("rt_hip_gguf_meta_str", self.h, key.encode(), index, C.byref(v))
+        return v.value.decode()
+
+    def meta_array_len(self, key: str) -> int:
+        return self._lib.lib.rt_hip_gguf_meta_array_len(self.h, key.encode())
 
 
 class Chain:
