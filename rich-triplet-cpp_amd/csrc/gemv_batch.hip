@@ -19,10 +19,10 @@
 //    accumulation rounds, as in an f32 dot product.
 //  * Q4_K weights (v_mfma_i32_16x16x32_i8): the step is one 32-value
 //    sub-block, and x carries the int8 limbs of the M = 1 kernel
-//    (q4k_mfma.hpp): per sub-block a power-of-two s and A0 + A1/254 + A2/254^2
+//    (q4k_mfma.hpp): per sub-block a power-of-two s and A0 + A1/256 + A2/65536
 //    == x / s to 2.5e-7 * absmax.  Each limb dot against the nibbles is an
 //    exact int32, and per sub-block j (quant_q4k.cpp:482-523)
-//        sum x * w = (d*sv_j) * (s*C0 + s/254*C1 + s/254^2*C2) - (dmin*mv_j) * sum(x).
+//        sum x * w = (d*sv_j) * (s*C0 + s/256*C1 + s/65536*C2) - (dmin*mv_j) * sum(x).
 //    Sub-block j's values k = 32j + t sit in byte 32*(j/2) + t of qs, low
 //    nibble for even j and high for odd (quant_q4k.cpp:280-317).
 //
@@ -37,6 +37,7 @@
 // padded with zero activation steps to whole ring rounds, so the loop has
 // no tail: padded steps add exact zeros, and weight loads past the slice's
 // real slots get an empty buffer range (zeros, no memory traffic).
+#include "q4k_mfma.hpp"
 #include "rt_common.hpp"
 #include "rt_launch.hpp"
 
@@ -84,7 +85,7 @@ struct BQ4k {
     static constexpr int kSlotCost = 2;  // one slot's time, in units of one slice's reduction
     static constexpr int kFrag = 8;   // 8 int8
     static constexpr int kLimb = 48 * kFrag;
-    static constexpr int kCst = 64;   // 4 rows x {s, s/254, s/254^2, sum}
+    static constexpr int kCst = 64;   // 4 rows x {s, s/256, s/65536, sum}
     struct Slot {
         u32x4 h;      // d | dmin << 16, scales[12]
         u32x2 p[4];   // qs[32c + 8g, +8), c = 0..3
@@ -124,23 +125,6 @@ __device__ __forceinline__ void bf16_limbs4(const f32x4 v, u32x2& h, u32x2& m, u
     h = u32x2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
     m = u32x2{mb[0] | (mb[1] << 16), mb[2] | (mb[3] << 16)};
     l = u32x2{lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
-}
-
-// int8 limbs of four activations scaled by inv = 1/s (exact, power of two),
-// as in q4k_mfma::limbs_of: one dword per limb plane.
-__device__ __forceinline__ void i8_limbs4(const f32x4 v, float inv, uint32_t& w0, uint32_t& w1, uint32_t& w2) {
-    w0 = w1 = w2 = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float r = v[e] * inv;
-        const float a0 = __builtin_rintf(r);
-        const float r1 = (r - a0) * 254.0f;
-        const float a1 = __builtin_rintf(r1);
-        const float a2 = __builtin_rintf((r1 - a1) * 254.0f);
-        w0 |= (static_cast<uint32_t>(static_cast<int>(a0)) & 0xffu) << (8 * e);
-        w1 |= (static_cast<uint32_t>(static_cast<int>(a1)) & 0xffu) << (8 * e);
-        w2 |= (static_cast<uint32_t>(static_cast<int>(a2)) & 0xffu) << (8 * e);
-    }
 }
 
 // Sum and max over the aligned quad of lanes (every lane gets the same bits).
@@ -239,23 +223,18 @@ __global__ __launch_bounds__(kThreads) void k_gemv_batch(const uint8_t* __restri
             float sum = ((xa[i][0] + xa[i][1]) + (xa[i][2] + xa[i][3])) + ((xb[i][0] + xb[i][1]) + (xb[i][2] + xb[i][3]));
             amax = quad_max(amax);
             sum = quad_sum(sum);
-            // s = 2^(E-5) for the absmax exponent E; zero (or subnormal-range)
-            // sub-blocks get s = 0 and zero limbs; an Inf/NaN makes s
-            // non-finite, so the output is non-finite as in f32 arithmetic.
-            const uint32_t eb = (__float_as_uint(amax) >> 23) & 0xffu;
-            const bool live = eb > 6 && eb < 0xff;
-            const float sc = live ? __uint_as_float((eb - 5u) << 23) : (eb == 0xff ? amax : 0.0f);
-            const float inv = live ? __uint_as_float((254u - (eb - 5u)) << 23) : 0.0f;
+            float sc, inv;
+            q4k_mfma::sub_block_scale(amax, sc, inv);
             uint32_t a0, a1, a2, b0, b1, b2;
-            i8_limbs4(xa[i], inv, a0, a1, a2);
-            i8_limbs4(xb[i], inv, b0, b1, b2);
+            q4k_mfma::limb_words(xa[i], inv, a0, a1, a2);
+            q4k_mfma::limb_words(xb[i], inv, b0, b1, b2);
             if (u < units) {
                 *reinterpret_cast<u32x2*>(dst) = u32x2{a0, b0};
                 *reinterpret_cast<u32x2*>(dst + 8) = u32x2{a1, b1};
                 *reinterpret_cast<u32x2*>(dst + 16) = u32x2{a2, b2};
                 if (g == 0)
                     *reinterpret_cast<f32x4*>(cst + ((static_cast<size_t>(s) * Q + q) * 4 + t) * 16) =
-                        f32x4{sc, sc * (1.0f / 254.0f), sc * (1.0f / 64516.0f), sum};
+                        f32x4{sc, sc * (1.0f / 256.0f), sc * (1.0f / 65536.0f), sum};
             }
         } else {
             u32x2 ha, ma, la, hb, mb, lb;

@@ -85,16 +85,19 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     const uint32_t roff = static_cast<uint32_t>(ln.n * rb);
     const int nx = K >> 2;
 
-    // x first, copied straight into LDS (raw f32 at [0, 4K)) in 1 KB
-    // chunks spread over the waves.  The copies write LDS, so the compiler
-    // keeps them ahead of the weight prologue (plain register loads of x got
-    // sunk below it, and waiting for x then meant waiting for every weight
-    // load); vmcnt counts them in order, so waiting for them is partial.
-    const int nwaves = nthreads >> 6;
-    for (int c = wave; c < (K >> 8); c += nwaves) {
-        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(X + c * 256 + lane * 4),
-                                         (__attribute__((address_space(3))) void*)(lds + c * 1024), 16, 0, 0);
+    // x first, straight into registers: XP f32x4 per thread, thread tid
+    // holding x[4f .. 4f+3] for f = tid + nthreads * i, so each aligned
+    // 8-lane group holds one 32-value sub-block.  The scheduling barrier
+    // keeps these loads ahead of the weight prologue; vmcnt counts them in
+    // order, so waiting for them is partial.
+    const f32x4* const X4 = reinterpret_cast<const f32x4*>(X);
+    f32x4 xv[XP];
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+        const int f = tid + nthreads * i;
+        xv[i] = X4[f < nx ? f : 0];
     }
+    __builtin_amdgcn_sched_barrier(0);
 
     // This wave's tile: job and first row (wave-uniform).  A tile slot past
     // the last tile belongs to the last job with rows past its end, so its
@@ -162,21 +165,13 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // This wave's copies of x are older than the 3*D prologue loads: wait
-    // for them alone, then for every wave's.  Then x goes to registers
-    // (XP * nthreads >= K/4, checked by the host) and, once every wave has
-    // read it, its LDS area becomes the limb planes.
+    // The x loads are older than the 3*D prologue loads: wait for them
+    // alone (XP * nthreads >= K/4, checked by the host), then convert.
     wait_vmcnt<3 * D>();
-    lds_barrier();
-    f32x4 xv[XP];
-#pragma unroll
-    for (int i = 0; i < XP; ++i) {
-        const int f = tid + nthreads * i;
-        xv[i] = *reinterpret_cast<const f32x4*>(lds + 16 * (f < nx ? f : 0));
-    }
-    lds_barrier();
     // Every lane converts its values (past the end: a dummy that is not
-    // stored; the 8-lane reductions need the whole group).
+    // stored; the 8-lane reductions need the whole group).  No branch may
+    // skip a round: the compiler would sink that round's x load below the
+    // weight prologue.  The host picks the smallest XP that covers x.
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
         const int f = tid + nthreads * i;
@@ -216,7 +211,7 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     if (KS == 1) {
         if (lane < 16 && keep) yj[row] = v;
     } else {
-        float* red = reinterpret_cast<float*>(lds + stage_bytes(K));  // [TPW][KS][16]
+        float* red = reinterpret_cast<float*>(lds + lds_bytes(K));  // [TPW][KS][16]
         float* rp = red + tslot * KS * 16;
         if (lane < 16) rp[ks * 16 + lane] = v;
         lds_barrier();
@@ -275,11 +270,13 @@ hipError_t run_xp(const Jobs& jobs, const float* x, int64_t k, int ks, int waves
     if (per > 16) return hipErrorInvalidValue;  // the host keeps K within the staging bound
     if (jobs.count > 2) {
         if (per <= 2) return run<D, 2, TILED, true>(jobs, x, k, ks, waves, s);
+        if (per <= 3) return run<D, 3, TILED, true>(jobs, x, k, ks, waves, s);
         if (per <= 4) return run<D, 4, TILED, true>(jobs, x, k, ks, waves, s);
         if (per <= 8) return run<D, 8, TILED, true>(jobs, x, k, ks, waves, s);
         return run<D, 16, TILED, true>(jobs, x, k, ks, waves, s);
     }
     if (per <= 2) return run<D, 2, TILED, false>(jobs, x, k, ks, waves, s);
+    if (per <= 3) return run<D, 3, TILED, false>(jobs, x, k, ks, waves, s);
     if (per <= 4) return run<D, 4, TILED, false>(jobs, x, k, ks, waves, s);
     if (per <= 8) return run<D, 8, TILED, false>(jobs, x, k, ks, waves, s);
     return run<D, 16, TILED, false>(jobs, x, k, ks, waves, s);
@@ -321,7 +318,7 @@ hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s) 
 }  // namespace
 
 size_t mfma_gemv_lds_bytes(int64_t k, int waves) {
-    return stage_bytes(static_cast<int>(k)) + static_cast<size_t>(waves) * 16 * sizeof(float);
+    return lds_bytes(static_cast<int>(k)) + static_cast<size_t>(waves) * 16 * sizeof(float);
 }
 
 size_t q4k_m1_lds_bytes(int64_t k) { return mfma_gemv_lds_bytes(k, kMaxThreads / kWave); }
@@ -410,6 +407,9 @@ hipError_t launch_gemv_q4k_bf16_fused(int count, const void* const* w, float* co
         if (per <= 2)
             return j34 ? run_fused<2, true, 4>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s)
                        : run_fused<2, false, 4>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s);
+        if (per <= 3)
+            return j34 ? run_fused<3, true, 4>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s)
+                       : run_fused<3, false, 4>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s);
         return j34 ? run_fused<4, true, 4>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s)
                    : run_fused<4, false, 4>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s);
     }

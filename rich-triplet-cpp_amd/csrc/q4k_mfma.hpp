@@ -3,9 +3,10 @@
 // The f32 activation is represented exactly enough to stand in for f32: per
 // 32-value sub-block (the Q4_K sub-block size), a power-of-two scale s
 // (2^(E-5) for the sub-block's absmax exponent E) and three int8 limbs
-//     a = s * (A0 + A1/254 + A2/254^2) + e,   |A0| <= 64, |A1|,|A2| <= 127,
-//     |e| <= 0.5 * s / 254^2 <= 2.5e-7 * absmax.
-// A power-of-two s keeps the one-hot case exact: x = e_k gives A0 = 1/s,
+//     a = s * (A0 + A1/256 + A2/65536) + e,   |A0| <= 64, -128 <= A1,A2 <= 127,
+//     |e| <= 0.5 * s / 65536 <= 2.4e-7 * absmax,
+// i.e. R = rint(a/s * 2^16) written in signed base-256 digits.  A
+// power-of-two s keeps the one-hot case exact: x = e_k gives A0 = 1/s,
 // A1 = A2 = 0, and the result is the dequantized weight bit-for-bit.
 //
 // v_mfma_i32_16x16x64_i8 computes C[16x16] += A[16x64] * B[64x16] exactly in
@@ -17,7 +18,7 @@
 // C[4g + r][n], r = 0..3, i.e. exactly the three limb dots of its own
 // sub-block for its own row -- no cross-lane traffic before the epilogue.
 //
-// Exactness of the integer part: |C| <= 32 * 15 * 127 < 2^24, so the int32
+// Exactness of the integer part: |C| <= 32 * 15 * 128 < 2^24, so the int32
 // sums and their f32 conversions are exact; the only roundings are the
 // epilogue's f32 operations.
 #pragma once
@@ -32,12 +33,12 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 // LDS layout of one staged activation vector of length K (K % 256 == 0):
 //   [0, 3K)            limb planes lambda = 0, 1, 2 (int8, K bytes each)
 //   [3K, 3K + 64)      zeros (the A operand of inactive lanes)
-//   [3K + 64, ...)     per sub-block f32x4 {s, s/254, s/254^2, sum}
+//   [3K + 64, ...)     per sub-block f32x4 {s, s/256, s/65536, sum}
 __host__ __device__ inline size_t lds_bytes(int K) {
     return 3 * static_cast<size_t>(K) + 64 + static_cast<size_t>(K / 32) * 16;
 }
-// The GEMV first lands x as raw f32 in the same area, so it needs the
-// larger of the two (4K bytes for every K > 128).
+// The decode chain first lands x as raw f32 in the same area, so it needs
+// the larger of the two (4K bytes for every K > 128).
 __host__ __device__ inline size_t stage_bytes(int K) {
     const size_t raw = 4 * static_cast<size_t>(K), limbs = lds_bytes(K);
     return raw > limbs ? raw : limbs;
@@ -64,6 +65,49 @@ __device__ __forceinline__ void group8_sum_max(float& sum, float& amax) {
     amax = fmaxf(amax, dpp<kDppHalfMirror>(amax));
 }
 
+// Scale of a sub-block from its absmax: s = 2^(E-5), E = unbiased exponent
+// of amax, and inv = 1/s; zero (or subnormal-range) sub-blocks get s = 0
+// and zero limbs.  An Inf/NaN activation makes s non-finite so the output
+// is NaN/Inf, as the reference's f32 arithmetic would make it.  Masks
+// rather than conditionals: written as selects, the compiler made branches
+// of them, with exec-mask saves around each.
+__device__ __forceinline__ void sub_block_scale(float amax, float& s, float& inv) {
+    const uint32_t eb = (__float_as_uint(amax) >> 23) & 0xffu;
+    const uint32_t live = 0u - static_cast<uint32_t>(eb - 7u < 248u);  // 7 <= eb <= 254
+    const uint32_t nonfinite = 0u - static_cast<uint32_t>(eb == 0xffu);
+    s = __uint_as_float((((eb - 5u) << 23) & live) | (__float_as_uint(amax) & nonfinite));
+    inv = __uint_as_float(((259u - eb) << 23) & live);
+}
+
+// The three limb words (planes A0, A1, A2; value e in byte e) of four
+// activations of one sub-block, inv = 1/s.  |v * inv| < 64 and the scaling
+// is exact, so b = v * inv * 2^16 + 1.5 * 2^23 is rounded once, to the
+// nearest integer, and its bits are 0x4B400000 + R with R = rint(v/s * 2^16),
+// |R| < 2^22.  The signed base-256 digits of R are then bytes of b:
+//     A2 = R mod 256 (as int8)          = byte 0 of b
+//     A1 = ((R + 128) >> 8) mod 256     = byte 1 of b + 128
+//     A0 = (R + 32896) >> 16            = byte 2 of b + 0x8080 - 0x400000
+// (the last subtracts the magic's own 0x40 in bits 16..23), so that
+// R = 65536 A0 + 256 A1 + A2 with |A0| <= 64.  v_perm gathers each plane.
+__device__ __forceinline__ void limb_words(const f32x4 v, float inv, uint32_t& w0, uint32_t& w1, uint32_t& w2) {
+    uint32_t b[4], m[4], h[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        b[e] = __float_as_uint(__builtin_fmaf(v[e] * inv, 65536.0f, 12582912.0f));
+        m[e] = b[e] + 128u;
+        h[e] = b[e] - 4161408u;  // + 0x8080 - 0x400000
+    }
+    // perm(hi, lo, sel): byte j of the result is byte sel_j of {hi:lo}
+    auto gather = [](const uint32_t (&x)[4], uint32_t byte) {
+        const uint32_t pair = 0x0c0c0400u | (byte * 0x0101u);
+        return __builtin_amdgcn_perm(__builtin_amdgcn_perm(x[3], x[2], pair),
+                                     __builtin_amdgcn_perm(x[1], x[0], pair), 0x05040100u);
+    };
+    w0 = gather(h, 2);
+    w1 = gather(m, 1);
+    w2 = gather(b, 0);
+}
+
 // Limbs of 4 activations (one f32x4) of a sub-block whose 8 holders are the
 // aligned 8-lane group of the calling lane.  Writes the limb bytes and, from
 // the group's first lane, the sub-block constants; with store == false it
@@ -72,26 +116,10 @@ __device__ __forceinline__ void limbs_of(const f32x4 v, uint8_t* lds, int K, int
     float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     float sum = (v[0] + v[1]) + (v[2] + v[3]);
     group8_sum_max(sum, amax);
-    // s = 2^(E-5), E = unbiased exponent of amax; zero (or subnormal-range)
-    // sub-blocks get s = 0 and zero limbs.
-    // An Inf/NaN activation makes s non-finite so the output is NaN/Inf,
-    // as the reference's f32 arithmetic would make it.
-    const uint32_t eb = (__float_as_uint(amax) >> 23) & 0xffu;
-    const bool live = eb > 6 && eb < 0xff;
-    const float s = live ? __uint_as_float((eb - 5u) << 23) : (eb == 0xff ? amax : 0.0f);
-    const float inv = live ? __uint_as_float((254u - (eb - 5u)) << 23) : 0.0f;
-    uint32_t w0 = 0, w1 = 0, w2 = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float r = v[e] * inv;  // exact: power-of-two scaling
-        const float a0 = __builtin_rintf(r);
-        const float r1 = (r - a0) * 254.0f;
-        const float a1 = __builtin_rintf(r1);
-        const float a2 = __builtin_rintf((r1 - a1) * 254.0f);
-        w0 |= (static_cast<uint32_t>(static_cast<int>(a0)) & 0xffu) << (8 * e);
-        w1 |= (static_cast<uint32_t>(static_cast<int>(a1)) & 0xffu) << (8 * e);
-        w2 |= (static_cast<uint32_t>(static_cast<int>(a2)) & 0xffu) << (8 * e);
-    }
+    float s, inv;
+    sub_block_scale(amax, s, inv);
+    uint32_t w0, w1, w2;
+    limb_words(v, inv, w0, w1, w2);
     if (!store) return;
     uint32_t* l32 = reinterpret_cast<uint32_t*>(lds);
     l32[f] = w0;
@@ -99,7 +127,7 @@ __device__ __forceinline__ void limbs_of(const f32x4 v, uint8_t* lds, int K, int
     l32[(K >> 1) + f] = w2;
     if ((f & 7) == 0) {
         f32x4* cst = reinterpret_cast<f32x4*>(lds + 3 * static_cast<size_t>(K) + 64);
-        cst[f >> 3] = f32x4{s, s * (1.0f / 254.0f), s * (1.0f / 64516.0f), sum};
+        cst[f >> 3] = f32x4{s, s * (1.0f / 256.0f), s * (1.0f / 65536.0f), sum};
     }
 }
 
@@ -271,7 +299,7 @@ __device__ __forceinline__ float dot(const Dec& r, int b, const Lane& ln, const 
 
     const uint32_t c_addr = ln.cst_base + (static_cast<uint32_t>(b) << 7);
     const f32x4 kl = lds_f4(c_addr), kh = lds_f4(c_addr + 16);
-    // dot of the sub-block in activation units: s*C0 + s/254*C1 + s/254^2*C2
+    // dot of the sub-block in activation units: s*C0 + s/256*C1 + s/65536*C2
     float dl = static_cast<float>(clo[0]) * kl[0];
     dl = __builtin_fmaf(static_cast<float>(clo[1]), kl[1], dl);
     dl = __builtin_fmaf(static_cast<float>(clo[2]), kl[2], dl);
