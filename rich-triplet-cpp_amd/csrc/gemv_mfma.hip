@@ -284,28 +284,34 @@ hipError_t run_xp(const Jobs& jobs, const float* x, int64_t k, int ks, int waves
 
 // K-split per tile.  One round of workgroups (at most one per CU) is what
 // matters for the short outputs of a decode step: a launch whose last few
-// CUs get a second workgroup takes twice as long.  So: the largest split of
-// {1, 2, 3, 4, 6, 8, 12} that divides the super-block count, leaves every
-// wave at least two super-blocks and still fits one workgroup per CU.
-// Outputs too long for one round even at KS = 1 use KS = 2 (measured best
-// for the lm_head).  KS = 1, 2, 4 run 4 waves per workgroup (4/KS tiles);
-// other splits one tile per workgroup of KS waves.
+// CUs get a second workgroup takes twice as long.  Among the splits of
+// {1, 2, 3, 4, 6, 8, 12} that divide the super-block count, leave every
+// wave at least two super-blocks and fit one workgroup per CU, the one with
+// the fewest rounds of x conversion per SIMD (every wave converts its share
+// of x before it uses any weight: waves per SIMD x f32x4 per thread), and
+// among those the largest (more loads in flight).  Measured: o 3072 x 3072
+// 3.84 us at KS = 4 (3 rounds) against 4.41 us at KS = 6 (4 rounds); down
+// 3072 x 8192 best at KS = 8.  Outputs too long for one round even at
+// KS = 1 use KS = 4 (the lm_head: 38.0 us against 40.9 us at KS = 2).
+// KS = 1, 2, 4 run 4 waves per workgroup (4/KS tiles); other splits one
+// tile per workgroup of KS waves.
 template <bool TILED>
 hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s) {
     const int64_t tiles = jobs.total;
     const int64_t nb = k / 256;
     const int64_t cus = device_info().cus;
     static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12};
-    auto wgs_for = [&](int c) {
-        const int64_t tpw = c <= 4 ? 4 / c : 1;
-        return (tiles + tpw - 1) / tpw;
+    auto waves_for = [](int c) { return c <= 4 ? (4 / c) * c : c; };
+    auto wgs_for = [&](int c) { return (tiles + waves_for(c) / c - 1) / (waves_for(c) / c); };
+    auto rounds = [&](int c) {
+        const int64_t w = waves_for(c), per = (k / 4 + 64 * w - 1) / (64 * w);
+        return (w + 3) / 4 * per;
     };
+    auto usable = [&](int c) { return nb % c == 0 && (c == 1 || 2 * c <= nb); };
     int ks = 1;
-    for (int c : kSplits) {
-        if (nb % c != 0 || (c > 1 && 2 * c > nb)) continue;
-        if (wgs_for(c) <= cus) ks = c;
-    }
-    if (wgs_for(1) > cus && nb % 2 == 0) ks = 2;
+    for (int c : kSplits)
+        if (usable(c) && wgs_for(c) <= cus && rounds(c) <= rounds(ks)) ks = c;
+    if (wgs_for(1) > cus) ks = usable(4) ? 4 : (usable(2) ? 2 : 1);
     if (const int forced = tune_param("Q4K_KS", 0)) ks = (nb % forced == 0 && forced <= 12) ? forced : ks;
     // a whole number of tiles per workgroup: 4 waves for KS = 1, 2, 4;
     // exactly KS waves (one tile) otherwise
