@@ -57,6 +57,16 @@ __device__ __forceinline__ uint64_t sreg(const void* p) {
     return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
+// The K-split of a launch, packed by the host into one preloaded argument
+// so that no wave divides: bits 0-3 KS (waves per tile), 4-7 TPW (tiles per
+// workgroup), 8-15 super-blocks per wave, 16-28 ceil(4096 / KS), with which
+// wave / KS = (wave * m) >> 12 exactly for wave < 16 and KS <= 12 (the
+// rounding adds < 16/4096, below the gap 1/KS to the next integer).
+__host__ __device__ inline uint32_t pack_split(int ks, int tpw, int bpw) {
+    return static_cast<uint32_t>(ks) | (static_cast<uint32_t>(tpw) << 4) | (static_cast<uint32_t>(bpw) << 8) |
+           (static_cast<uint32_t>((4096 + ks - 1) / ks) << 16);
+}
+
 // KS waves split a tile's super-blocks; a workgroup of blockDim.x / 64 waves
 // holds TPW = waves / KS tiles.
 // The arguments every wave needs before its first load come first, as
@@ -67,17 +77,18 @@ __device__ __forceinline__ uint64_t sreg(const void* p) {
 // The body of workgroup `blk` (the kernel below, and the Q4_K workgroups of
 // the fused q/k/v launch); `lds` holds mfma_gemv_lds_bytes(K, waves).
 template <int D, int XP, bool TILED, bool J34>
-__device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, int K, int KS, int nthreads,
+__device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, int K, uint32_t split, int nthreads,
                                           const uint8_t* w0, const uint8_t* w1, int n0, int n1, int tile1,
                                           int count, const Jobs& jobs, uint8_t* lds) {
     // nthreads == blockDim.x, passed as a preloaded argument: blockDim
     // itself is a kernel-argument load that the first x loads would wait for.
-    const int TPW = (nthreads >> 6) / KS;  // tiles per workgroup
+    const int KS = static_cast<int>(split & 15u), TPW = static_cast<int>((split >> 4) & 15u);
+    const int bpw = static_cast<int>((split >> 8) & 255u);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nb = K >> 8;
-    const int ks = wave % KS, tslot = wave / KS;
-    const int bpw = (nb + KS - 1) / KS;
+    const int tslot = (wave * static_cast<int>(split >> 16)) >> 12;
+    const int ks = wave - tslot * KS;
     const int b0 = ks * bpw;
     const int nbw = min(nb, b0 + bpw) - b0;  // >= 1: the host picks KS so every split is non-empty
     const Lane ln = make_lane(lane, K);
@@ -139,9 +150,15 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     // the tile; past the range (or past the job) the resource is empty:
     // zeros, no memory traffic.
     using B = typename std::conditional<TILED, BlkT, Blk>::type;
+    // 32-bit bounds: the clamp is done once per wave, not per slot.
+    const uint32_t tl32 = rsrc_bytes(tleft);
     auto issue = [&](B& slot, int i) {
-        const int64_t o = static_cast<int64_t>(i) * kStride;
-        const BufRsrc rs = make_rsrc(tbase + o, i < nbw ? tleft - o : 0);
+        const uint32_t o = static_cast<uint32_t>(i) * static_cast<uint32_t>(kStride);
+        // readfirstlane: the compiler may compute the (uniform) size on the
+        // VALU, and a resource in VGPRs becomes a waterfall loop per load.
+        const uint32_t left = static_cast<uint32_t>(
+            __builtin_amdgcn_readfirstlane(static_cast<int>(i < nbw && o < tl32 ? tl32 - o : 0u)));
+        const BufRsrc rs = make_rsrc_n(tbase + o, left);
         if constexpr (TILED)
             load_blk_t(rs, static_cast<uint32_t>(lane), slot);
         else
@@ -226,10 +243,10 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
 
 template <int D, int XP, bool TILED, bool J34>
 __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
-    const float* __restrict__ X, int K, int KS, int nthreads, const uint8_t* w0, const uint8_t* w1,
+    const float* __restrict__ X, int K, uint32_t split, int nthreads, const uint8_t* w0, const uint8_t* w1,
     int n0, int n1, int tile1, int count, const Jobs jobs) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    q4k_tiles<D, XP, TILED, J34>(static_cast<int>(blockIdx.x), X, K, KS, nthreads, w0, w1, n0, n1, tile1, count,
+    q4k_tiles<D, XP, TILED, J34>(static_cast<int>(blockIdx.x), X, K, split, nthreads, w0, w1, n0, n1, tile1, count,
                                  jobs, lds);
 }
 
@@ -239,13 +256,13 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
 // exactly that of the separate kernels (4 waves per workgroup on both sides).
 template <int XPQ, bool J34, int XPB>
 __global__ __launch_bounds__(bf16_gemv::kThreads) void k_gemv_q4k_bf16(
-    const float* __restrict__ X, int K, int KS, int nthreads, const uint8_t* w0, const uint8_t* w1,
+    const float* __restrict__ X, int K, uint32_t split, int nthreads, const uint8_t* w0, const uint8_t* w1,
     int n0, int n1, int tile1, int count, int q4k_wgs, const uint16_t* __restrict__ wb, float* __restrict__ yb,
     int nb_rows, const Jobs jobs) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int blk = static_cast<int>(blockIdx.x);
     if (blk < q4k_wgs)
-        q4k_tiles<4, XPQ, true, J34>(blk, X, K, KS, nthreads, w0, w1, n0, n1, tile1, count, jobs, lds);
+        q4k_tiles<4, XPQ, true, J34>(blk, X, K, split, nthreads, w0, w1, n0, n1, tile1, count, jobs, lds);
     else
         bf16_gemv::rows<8, XPB, false>(blk - q4k_wgs, (nb_rows + 3) / 4, wb, X, yb, nb_rows, K, nullptr, lds);
 }
@@ -255,8 +272,9 @@ hipError_t run(const Jobs& jobs, const float* x, int64_t k, int ks, int waves, h
     const int tpw = waves / ks;
     const int64_t wgs = (static_cast<int64_t>(jobs.total) + tpw - 1) / tpw;
     const size_t lds = mfma_gemv_lds_bytes(k, waves);
+    const uint32_t split = pack_split(ks, tpw, static_cast<int>((k / 256 + ks - 1) / ks));
     hipLaunchKernelGGL((k_gemv_q4k_mfma<D, XP, TILED, J34>), dim3(static_cast<unsigned>(wgs)),
-                       dim3(static_cast<unsigned>(waves * kWave)), lds, s, x, static_cast<int>(k), ks,
+                       dim3(static_cast<unsigned>(waves * kWave)), lds, s, x, static_cast<int>(k), split,
                        waves * kWave, jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], jobs.count,
                        jobs);
     return hipGetLastError();
@@ -360,7 +378,8 @@ hipError_t run_fused(const Jobs& jobs, int ks, int q4k_wgs, const uint16_t* wb, 
                      const float* x, int64_t k, size_t lds, hipStream_t s) {
     const int64_t bwgs = (nb_rows + 3) / 4;  // one row per wave, 4 waves
     hipLaunchKernelGGL((k_gemv_q4k_bf16<XPQ, J34, XPB>), dim3(static_cast<unsigned>(q4k_wgs + bwgs)),
-                       dim3(bf16_gemv::kThreads), lds, s, x, static_cast<int>(k), ks, bf16_gemv::kThreads,
+                       dim3(bf16_gemv::kThreads), lds, s, x, static_cast<int>(k),
+                       pack_split(ks, 4 / ks, static_cast<int>((k / 256 + ks - 1) / ks)), bf16_gemv::kThreads,
                        jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], jobs.count, q4k_wgs, wb, yb,
                        static_cast<int>(nb_rows), jobs);
     return hipGetLastError();

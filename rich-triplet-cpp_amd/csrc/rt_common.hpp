@@ -49,10 +49,16 @@ __device__ __forceinline__ u32x4 ld16(const void* p) {
 // per-lane offset and the instruction offset, not soffset, so callers move
 // the base rather than pass soffset.
 typedef __amdgpu_buffer_rsrc_t BufRsrc;
-__device__ __forceinline__ BufRsrc make_rsrc(const void* base, int64_t bytes) {
-    const uint32_t n = bytes <= 0 ? 0u : (bytes >= 0xffffffffll ? 0xffffffffu : static_cast<uint32_t>(bytes));
+__device__ __forceinline__ BufRsrc make_rsrc_n(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
-                                             static_cast<int>(n), 0x00020000);
+                                             static_cast<int>(bytes), 0x00020000);
+}
+// `bytes` clamped to [0, 2^32 - 1].
+__device__ __forceinline__ uint32_t rsrc_bytes(int64_t bytes) {
+    return bytes <= 0 ? 0u : (bytes >= 0xffffffffll ? 0xffffffffu : static_cast<uint32_t>(bytes));
+}
+__device__ __forceinline__ BufRsrc make_rsrc(const void* base, int64_t bytes) {
+    return make_rsrc_n(base, rsrc_bytes(bytes));
 }
 __device__ __forceinline__ u32x4 ld16(BufRsrc r, uint32_t off) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0));
