@@ -333,7 +333,8 @@ hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s) 
     if (const int forced = tune_param("Q4K_KS", 0)) ks = (nb % forced == 0 && forced <= 12) ? forced : ks;
     // a whole number of tiles per workgroup: 4 waves for KS = 1, 2, 4;
     // exactly KS waves (one tile) otherwise
-    const int waves = ks <= 4 ? (4 / ks) * ks : ks;
+    int waves = ks <= 4 ? (4 / ks) * ks : ks;
+    if (const int tpw = tune_param("Q4K_TPW", 0)) waves = ks * tpw;
     if (waves % ks != 0 || waves > kMaxThreads / kWave) return hipErrorInvalidValue;
     const int d = tune_param("Q4K_RING", 4);
     return d == 8 ? run_xp<8, TILED>(jobs, x, k, ks, waves, s) : run_xp<4, TILED>(jobs, x, k, ks, waves, s);
