@@ -656,14 +656,21 @@ hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, con
             if (!ws) return e;
         }
         const uint16_t* a16 = static_cast<const uint16_t*>(a);
-        if (!a_bf16) {
+        if (!a_bf16 && w_bytes) {
+            // both conversions in one launch
+            uint16_t* ab = reinterpret_cast<uint16_t*>(ws);
+            const hipError_t e = launch_dequant_q4k_cvt(w, reinterpret_cast<uint16_t*>(ws + a_bytes), n, k,
+                                                        static_cast<const float*>(a), ab, m * k, s);
+            if (e != hipSuccess) return e;
+            a16 = ab;
+            w = ws + a_bytes;
+        } else if (!a_bf16) {
             uint16_t* ab = reinterpret_cast<uint16_t*>(ws);
             const int64_t n8 = m * k / 8;
             hipLaunchKernelGGL(k_f32_to_bf16, dim3(static_cast<unsigned>((n8 + 255) / 256)), dim3(256), 0, s,
                                static_cast<const float*>(a), ab, n8);
             a16 = ab;
-        }
-        if (w_bytes) {
+        } else if (w_bytes) {
             const hipError_t e = launch_dequant_q4k(w, ws + a_bytes, true, n, k, s);
             if (e != hipSuccess) return e;
             w = ws + a_bytes;

@@ -44,8 +44,6 @@ namespace rt_hip {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kBlk = 210;
 constexpr int kTileBlk = 16 * kBlk;  // 3360
@@ -54,10 +52,6 @@ constexpr int kThreads = 256;        // 4 waves (K splits up to 4)
 constexpr int kMaxThreads = 1024;    // 16 waves (one tile split 6, 8, 12 or 16 ways)
 constexpr int kStepBytes = 192;      // x limbs of one 32-value step: 3 limbs x 32 bf16
 constexpr int kMaxK = 8192;
-
-__device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
-}
 
 // ---- repack: row-major blocks -> tiled ------------------------------------
 // One workgroup of 64 threads per (tile, block); thread l = n + 16 g.

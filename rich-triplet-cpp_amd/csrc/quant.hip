@@ -1,10 +1,11 @@
 // quant.hip -- Q4_K dequantization (to f32 or bf16) and quantization.
 //
-// Dequant: one lane per 16-byte piece of qs (32 values), as the GEMV reads
-// them; bit-exact with Q4KMat::dequantize_row_into (quant_q4k.cpp:280-317)
-// because both products are exact and only the subtraction rounds.  The
-// bf16 variant rounds that f32 value to nearest-even, as flux_dequant_q4k's
-// bfloat() conversion does (shaders/flux.msl:78-79).
+// Dequant: one lane per 8 (bf16) or 4 (f32) consecutive outputs, so every
+// store instruction writes 1 KB of contiguous output; bit-exact with
+// Q4KMat::dequantize_row_into (quant_q4k.cpp:280-317) because both products
+// are exact and only the subtraction rounds.  The bf16 variant rounds that
+// f32 value to nearest-even, as flux_dequant_q4k's bfloat() conversion does
+// (shaders/flux.msl:78-79).
 //
 // Quantize: one wave per 256-value super-block, lane l holding values
 // 4l..4l+3 (sub-block l/8).  Every arithmetic step is the reference's
@@ -21,60 +22,92 @@
 namespace rt_hip {
 namespace {
 
-__global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t* __restrict__ W,
-                                                     void* __restrict__ out, int64_t pieces,
-                                                     bool bf16) {
-    const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (gid >= pieces) return;
-    const int64_t blk = gid >> 3;
-    const int p = static_cast<int>(gid & 7), c = p >> 1, h = p & 1;
+// One lane per kPer consecutive outputs of a super-block: 8 for bf16 (32
+// lanes per block), 4 for f32 (64 lanes); either way a wave's store covers
+// 1 KB of contiguous output.  Sub-block sb's 32 values are the low (even
+// sb) or high nibbles of qs chunk sb/2, so a lane reads kPer qs bytes and
+// the 16-byte header.  w = (d*sv)*q - dmin*mv: the product is exact in f32,
+// so the fma rounds only the subtraction, as the reference does.  bf16 is
+// v_cvt_pk_bf16_f32, round-to-nearest-even with NaN quieting: identical to
+// the reference's f32 -> bf16 (bf16.hpp:50-60) on every f32, NaNs included
+// (checked on the device against the bit rule).
+template <bool BF16>
+__device__ __forceinline__ void dequant_unit(const uint8_t* __restrict__ W, void* __restrict__ out, int64_t u) {
+    constexpr int kPer = BF16 ? 8 : 4;
+    constexpr int kLanesPerSub = 32 / kPer;
+    constexpr int kLanesPerBlk = 8 * kLanesPerSub;
+    const int64_t blk = u / kLanesPerBlk;
+    const int l = static_cast<int>(u % kLanesPerBlk);
+    const int sb = l / kLanesPerSub, part = l % kLanesPerSub;
     const uint8_t* bp = W + blk * kQ4kBlockBytes;
     const u32x4 hd = ld16(bp);
-    const u32x4 q = ld16(bp + 16 + 16 * p);
-    const float d = f16_bits_to_f32(hd[0] & 0xffffu);
-    const float dm = f16_bits_to_f32(hd[0] >> 16);
-    uint32_t sv1, mv1, sv2, mv2;
-    decode_scale_min(make_scale_sel(2 * c), hd[1], hd[2], hd[3], sv1, mv1);
-    decode_scale_min(make_scale_sel(2 * c + 1), hd[1], hd[2], hd[3], sv2, mv2);
-    const float s1 = d * static_cast<float>(sv1), n1 = dm * static_cast<float>(mv1);
-    const float s2 = d * static_cast<float>(sv2), n2 = dm * static_cast<float>(mv2);
-    float lo[16], hi[16];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t byte = (q[j] >> (8 * e)) & 0xffu;
-            lo[4 * j + e] = s1 * static_cast<float>(byte & 0x0fu) - n1;
-            hi[4 * j + e] = s2 * static_cast<float>(byte >> 4) - n2;
-        }
-    const int64_t o = blk * kQ4kBlockElems + c * 64 + h * 16;
-    if (!bf16) {
-        float* dst = static_cast<float*>(out) + o;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            reinterpret_cast<f32x4*>(dst)[j] = f32x4{lo[4 * j], lo[4 * j + 1], lo[4 * j + 2], lo[4 * j + 3]};
-            reinterpret_cast<f32x4*>(dst + 32)[j] =
-                f32x4{hi[4 * j], hi[4 * j + 1], hi[4 * j + 2], hi[4 * j + 3]};
-        }
+    const uint8_t* qp = bp + 16 + (sb >> 1) * 32 + part * kPer;
+    uint32_t q[2];
+    if constexpr (BF16) {
+        const u32x2 v = *reinterpret_cast<const u32x2*>(qp);
+        q[0] = v[0];
+        q[1] = v[1];
     } else {
-        uint16_t* dst = static_cast<uint16_t*>(out) + o;
-        u32x4 a, b;
+        q[0] = *reinterpret_cast<const uint32_t*>(qp);
+        q[1] = 0;
+    }
+    uint32_t sv, mv;
+    decode_scale_min(make_scale_sel(sb), hd[1], hd[2], hd[3], sv, mv);
+    const float sc = f16_bits_to_f32(hd[0] & 0xffffu) * static_cast<float>(sv);
+    const float mn = f16_bits_to_f32(hd[0] >> 16) * static_cast<float>(mv);
+    const uint32_t sh = static_cast<uint32_t>(sb & 1) * 4u;
+    float w[kPer];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            a[j] = f32_to_bf16_rne(lo[2 * j]) | (static_cast<uint32_t>(f32_to_bf16_rne(lo[2 * j + 1])) << 16);
-            b[j] = f32_to_bf16_rne(lo[8 + 2 * j]) |
-                   (static_cast<uint32_t>(f32_to_bf16_rne(lo[8 + 2 * j + 1])) << 16);
-        }
-        reinterpret_cast<u32x4*>(dst)[0] = a;
-        reinterpret_cast<u32x4*>(dst)[1] = b;
+    for (int e = 0; e < kPer; ++e)
+        w[e] = __builtin_fmaf(sc, static_cast<float>((q[e >> 2] >> (8 * (e & 3) + sh)) & 15u), -mn);
+    const int64_t o = blk * kQ4kBlockElems + sb * 32 + part * kPer;
+    if constexpr (BF16) {
+        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) + o) =
+            u32x4{bf16_pair(w[0], w[1]), bf16_pair(w[2], w[3]), bf16_pair(w[4], w[5]), bf16_pair(w[6], w[7])};
+    } else {
+        *reinterpret_cast<f32x4*>(static_cast<float*>(out) + o) = f32x4{w[0], w[1], w[2], w[3]};
+    }
+}
+
+// Grid-stride over units, kUnroll per lane per round so that several loads
+// are in flight per wave; one lane per unit made 52 K short waves for a
+// 8192 x 3072 weight, and wave launch, not HBM, set the time.
+constexpr int kUnroll = 4;
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t* __restrict__ W, void* __restrict__ out,
+                                                     int64_t units) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    for (int64_t u0 = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; u0 < units; u0 += stride * kUnroll) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            a[j] = f32_to_bf16_rne(hi[2 * j]) | (static_cast<uint32_t>(f32_to_bf16_rne(hi[2 * j + 1])) << 16);
-            b[j] = f32_to_bf16_rne(hi[8 + 2 * j]) |
-                   (static_cast<uint32_t>(f32_to_bf16_rne(hi[8 + 2 * j + 1])) << 16);
+        for (int j = 0; j < kUnroll; ++j) {
+            const int64_t u = u0 + j * stride;
+            if (u < units) dequant_unit<BF16>(W, out, u);
         }
-        reinterpret_cast<u32x4*>(dst + 32)[0] = a;
-        reinterpret_cast<u32x4*>(dst + 32)[1] = b;
+    }
+}
+
+// A GEMM's two input conversions in one launch: units [0, wunits)
+// dequantize W to bf16, the next aunits convert 8 f32 activations each to
+// bf16 (the same rounding).
+__global__ __launch_bounds__(256) void k_dequant_q4k_cvt(const uint8_t* __restrict__ W, uint16_t* __restrict__ wout,
+                                                         int64_t wunits, const float* __restrict__ A,
+                                                         uint16_t* __restrict__ aout, int64_t aunits) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256, total = wunits + aunits;
+    for (int64_t u0 = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; u0 < total; u0 += stride * kUnroll) {
+#pragma unroll
+        for (int j = 0; j < kUnroll; ++j) {
+            const int64_t u = u0 + j * stride;
+            if (u < wunits) {
+                dequant_unit<true>(W, wout, u);
+            } else if (u < total) {
+                const int64_t i = u - wunits;
+                const f32x4 a = reinterpret_cast<const f32x4*>(A)[2 * i];
+                const f32x4 b = reinterpret_cast<const f32x4*>(A)[2 * i + 1];
+                reinterpret_cast<u32x4*>(aout)[i] = u32x4{bf16_pair(a[0], a[1]), bf16_pair(a[2], a[3]),
+                                                          bf16_pair(b[0], b[1]), bf16_pair(b[2], b[3])};
+            }
+        }
     }
 }
 
@@ -233,12 +266,30 @@ __global__ __launch_bounds__(256) void k_q4k_tile(const uint8_t* __restrict__ sr
 
 }  // namespace
 
+// Grid for `units` lanes of work: one round of kUnroll units per lane, at
+// most 8 workgroups per CU.
+static dim3 unit_grid(int64_t units) {
+    const int64_t want = (units + 256 * kUnroll - 1) / (256 * kUnroll), cap = 8 * device_info().cus;
+    return dim3(static_cast<unsigned>(want < cap ? (want < 1 ? 1 : want) : cap));
+}
+
 hipError_t launch_dequant_q4k(const void* w, void* out, bool bf16, int64_t n, int64_t k,
                               hipStream_t s) {
-    const int64_t pieces = n * (k / 256) * 8;
-    const unsigned blocks = static_cast<unsigned>((pieces + 255) / 256);
-    hipLaunchKernelGGL(k_dequant_q4k, dim3(blocks), dim3(256), 0, s,
-                       static_cast<const uint8_t*>(w), out, pieces, bf16);
+    const int64_t units = n * k / (bf16 ? 8 : 4);
+    if (bf16)
+        hipLaunchKernelGGL(k_dequant_q4k<true>, unit_grid(units), dim3(256), 0, s, static_cast<const uint8_t*>(w),
+                           out, units);
+    else
+        hipLaunchKernelGGL(k_dequant_q4k<false>, unit_grid(units), dim3(256), 0, s, static_cast<const uint8_t*>(w),
+                           out, units);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_q4k_cvt(const void* w, uint16_t* wout, int64_t n, int64_t k, const float* a,
+                                  uint16_t* aout, int64_t a_elems, hipStream_t s) {
+    const int64_t wunits = n * k / 8, aunits = a_elems / 8;
+    hipLaunchKernelGGL(k_dequant_q4k_cvt, unit_grid(wunits + aunits), dim3(256), 0, s,
+                       static_cast<const uint8_t*>(w), wout, wunits, a, aout, aunits);
     return hipGetLastError();
 }
 

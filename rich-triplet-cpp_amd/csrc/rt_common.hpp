@@ -23,6 +23,16 @@ constexpr int kQ40BlockBytes = 18;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two f32 -> one dword of bf16 (a in the low half): v_cvt_pk_bf16_f32,
+// round-to-nearest-even with NaN quieting, identical to f32_to_bf16_rne
+// below on every f32, NaNs included (checked on the device against the bit
+// rule over 4 M values).
+__device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
+}
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));

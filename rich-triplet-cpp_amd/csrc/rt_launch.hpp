@@ -107,6 +107,10 @@ hipError_t launch_argmax_finalize(uint64_t* keys, int64_t rows, int64_t* idx, fl
 
 hipError_t launch_dequant_q4k(const void* w, void* out, bool bf16, int64_t n, int64_t k,
                               hipStream_t s);
+// Dequantize w (n x k Q4_K) to bf16 and convert a_elems f32 activations to
+// bf16 in one launch (a_elems % 8 == 0).
+hipError_t launch_dequant_q4k_cvt(const void* w, uint16_t* wout, int64_t n, int64_t k, const float* a,
+                                  uint16_t* aout, int64_t a_elems, hipStream_t s);
 hipError_t launch_quantize_q4k(const float* w, void* blocks, int64_t n, int64_t k,
                                hipStream_t s);
 

@@ -40,6 +40,25 @@ def test_dequant_q4k_adversarial_and_random_bytes_bit_exact(rt, orc):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+def test_dequant_q4k_bf16_adversarial_and_random_bytes(rt, orc):
+    """bf16 output on the golden adversarial blocks and on random block
+    bytes: the oracle's exact dequant, then the reference's f32 -> bf16
+    (orc.f32_to_bf16_n, RNE with NaN quieting), bit for bit."""
+    with np.load(GOLDEN, allow_pickle=False) as z:
+        adv = z["q4k_adv_blocks"]
+        adv_deq = z["q4k_adv_deq"]
+    got = from_dev(rt.dequant_q4k(to_dev(adv), adv_deq.shape[0], 256, bf16=True)).view(np.uint16)
+    assert np.array_equal(got.reshape(-1), orc.f32_to_bf16_n(adv_deq).reshape(-1))
+    rng = np.random.default_rng(78)
+    rnd = rng.integers(0, 256, (777, 144), dtype=np.uint8)
+    for o in (1, 3):  # finite d, dmin
+        rnd[:, o] &= 0x7b
+    rnd = rnd.reshape(-1)
+    got = from_dev(rt.dequant_q4k(to_dev(rnd), 777, 256, bf16=True)).view(np.uint16)
+    want = orc.f32_to_bf16_n(orc.q4k_dequant(rnd, 777, 256))
+    assert np.array_equal(got.reshape(-1), want.reshape(-1))
+
+
 def test_dequant_q4k_bf16_is_rne_of_exact(rt, orc):
     rng = np.random.default_rng(3)
     n, k = 200, 768
