@@ -6,10 +6,10 @@
 // of 144 bytes, so rows (and runs of 64 blocks) start 16-byte aligned.
 //
 // A lane owns whole blocks: lane l reads block 64 p + l of a row as the five
-// dwords covering bytes [18 l, 18 l + 18) of the 64-block run (18 l is 0 or
-// 2 mod 4; an odd lane's d sits in the high half of its first dword and
-// its qs are its next four dwords, an even lane's qs straddle dwords and are
-// rebuilt with funnel shifts).  The activation is staged in LDS chunk-major
+// dwords covering bytes [18 l, 18 l + 18) of the 64-block run, one 16-byte
+// and one 4-byte load (18 l is 0 or 2 mod 4; an odd lane's d sits in the
+// high half of its first dword and its qs are its next four dwords, an even
+// lane's qs straddle dwords and are rebuilt with funnel shifts).  The activation is staged in LDS chunk-major
 // -- 16-byte chunk c of block b at (c * NB + b) * 16 -- so the 8 lanes an
 // LDS read serves together (consecutive blocks) hit consecutive chunks, and
 // each block's sum of x is precomputed for the -8 offset:
@@ -29,6 +29,11 @@ namespace {
 
 constexpr int kT = 256;  // 4 waves
 constexpr int kBlockBytes = 18;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
 
 struct Slot {
     uint32_t w0, w1, w2, w3, w4;
@@ -72,10 +77,13 @@ __global__ __launch_bounds__(kT) void k_gemv_q40(const uint8_t* __restrict__ W, 
     auto issue = [&](Slot& sl) {
         const int64_t o = static_cast<int64_t>(ip) * (64 * kBlockBytes);
         const BufRsrc rs = make_rsrc(wb + ir * stride + o, ir < R ? rowb - o : 0);
-        sl.w0 = __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(loff), 0, 0);
-        sl.w1 = __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(loff + 4), 0, 0);
-        sl.w2 = __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(loff + 8), 0, 0);
-        sl.w3 = __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(loff + 12), 0, 0);
+        // a 16-byte load at a 4-byte aligned offset (buffer loads need only
+        // dword alignment), then the fifth dword: two instructions, not five
+        const u32x4 v = ld16(rs, loff);
+        sl.w0 = v[0];
+        sl.w1 = v[1];
+        sl.w2 = v[2];
+        sl.w3 = v[3];
         sl.w4 = __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(loff + 16), 0, 0);
         const bool wrap = ip == SP - 1;
         ip = __builtin_amdgcn_readfirstlane(wrap ? 0 : ip + 1);
@@ -87,22 +95,25 @@ __global__ __launch_bounds__(kT) void k_gemv_q40(const uint8_t* __restrict__ W, 
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // Stage x chunk-major, then the per-block sums.
-#pragma unroll
-    for (int i = 0; i < XP; ++i) {
-        const int f = tid + kT * i;
-        if (f < nx4) xs[(f & 7) * NB + (f >> 3)] = xv[i];
-    }
-    for (int f = tid + kT * XP; f < nx4; f += kT) xs[(f & 7) * NB + (f >> 3)] = X4[f];
-    lds_barrier();
-    for (int b = tid; b < NB; b += kT) {
-        float s = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const f32x4 a = xs[c * NB + b];
-            s += (a[0] + a[1]) + (a[2] + a[3]);
+    // Stage x chunk-major, with the per-block sums: a block's 8 chunks sit in
+    // 8 consecutive lanes (f = tid + kT * i), summed by DPP within the group
+    // (every lane of the group ends with the same bits); its first lane
+    // stores the sum.
+    auto stage = [&](const f32x4 v, int f) {
+        float sm = (v[0] + v[1]) + (v[2] + v[3]);
+        sm += dpp_f<0xb1>(sm);   // lane ^ 1
+        sm += dpp_f<0x4e>(sm);   // lane ^ 2
+        sm += dpp_f<0x141>(sm);  // half-row mirror: lane i <-> 7 - i
+        if (f < nx4) {
+            xs[(f & 7) * NB + (f >> 3)] = v;
+            if ((f & 7) == 0) sums[f >> 3] = sm;
         }
-        sums[b] = s;
+    };
+#pragma unroll
+    for (int i = 0; i < XP; ++i) stage(xv[i], tid + kT * i);
+    for (int f0 = kT * XP; f0 < nx4; f0 += kT) {
+        const int f = f0 + tid;
+        stage(X4[f < nx4 ? f : 0], f);
     }
     lds_barrier();
 
@@ -117,21 +128,25 @@ __global__ __launch_bounds__(kT) void k_gemv_q40(const uint8_t* __restrict__ W, 
         const uint32_t q3 = odd ? sl.w4 : __builtin_amdgcn_alignbyte(sl.w4, sl.w3, 2);
         const float d = f16_bits_to_f32(odd ? (sl.w0 >> 16) : (sl.w0 & 0xffffu));
         const uint32_t q[4] = {q0, q1, q2, q3};
-        float dot = 0.0f;
+        // Four independent chains (one per qs dword): one wave per SIMD
+        // leaves a single chain latency-bound.
+        float dc[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const f32x4 lo = xs[c * NB + bb], hi = xs[(c + 4) * NB + bb];
             const uint32_t v = q[c];
-            dot = __builtin_fmaf(ubyte_f32(v & 0x0f0f0f0fu, 0), lo[0], dot);
-            dot = __builtin_fmaf(ubyte_f32(v & 0x0f0f0f0fu, 1), lo[1], dot);
-            dot = __builtin_fmaf(ubyte_f32(v & 0x0f0f0f0fu, 2), lo[2], dot);
-            dot = __builtin_fmaf(ubyte_f32(v & 0x0f0f0f0fu, 3), lo[3], dot);
+            float t = ubyte_f32(v & 0x0f0f0f0fu, 0) * lo[0];
+            t = __builtin_fmaf(ubyte_f32(v & 0x0f0f0f0fu, 1), lo[1], t);
+            t = __builtin_fmaf(ubyte_f32(v & 0x0f0f0f0fu, 2), lo[2], t);
+            t = __builtin_fmaf(ubyte_f32(v & 0x0f0f0f0fu, 3), lo[3], t);
             const uint32_t h = (v >> 4) & 0x0f0f0f0fu;
-            dot = __builtin_fmaf(ubyte_f32(h, 0), hi[0], dot);
-            dot = __builtin_fmaf(ubyte_f32(h, 1), hi[1], dot);
-            dot = __builtin_fmaf(ubyte_f32(h, 2), hi[2], dot);
-            dot = __builtin_fmaf(ubyte_f32(h, 3), hi[3], dot);
+            t = __builtin_fmaf(ubyte_f32(h, 0), hi[0], t);
+            t = __builtin_fmaf(ubyte_f32(h, 1), hi[1], t);
+            t = __builtin_fmaf(ubyte_f32(h, 2), hi[2], t);
+            t = __builtin_fmaf(ubyte_f32(h, 3), hi[3], t);
+            dc[c] = t;
         }
+        const float dot = (dc[0] + dc[1]) + (dc[2] + dc[3]);
         const float blk = d * __builtin_fmaf(-8.0f, sums[bb], dot);
         acc += b < NB ? blk : 0.0f;
         if (cp == SP - 1) {
