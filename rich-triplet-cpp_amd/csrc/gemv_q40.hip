@@ -181,10 +181,12 @@ __global__ __launch_bounds__(kT) void k_gemv_q40(const uint8_t* __restrict__ W, 
 size_t q40_m1_lds_bytes(int64_t k) { return static_cast<size_t>(k) * 4 + static_cast<size_t>(k / 32) * 4; }
 
 hipError_t launch_gemv_q4_0_m1(const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t s) {
-    // Rows per wave: enough 64-block runs to fill the ring of 8 slots, at
-    // most 64 (row sums stay in lanes).
+    // Rows per wave: four 64-block runs per wave, at most 64 rows (row sums
+    // stay in lanes).  Measured at 4096 x 4096 (two runs per row): 2 rows
+    // per wave 5.65 us, 4 rows (a full ring of 8) 5.92 us, 1 row 6.26 us --
+    // more waves per CU hide more latency than a fuller ring.
     const int64_t runs = (k / 32 + 63) / 64;
-    int64_t rpw = tune_param("Q40_ROWS_PER_WAVE", static_cast<int>((8 + runs - 1) / runs));
+    int64_t rpw = tune_param("Q40_ROWS_PER_WAVE", static_cast<int>((4 + runs - 1) / runs));
     rpw = rpw < 1 ? 1 : (rpw > 64 ? 64 : rpw);
     const int64_t waves = kT / kWave;
     const int64_t wgs = (n + waves * rpw - 1) / (waves * rpw);
