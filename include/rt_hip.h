@@ -128,6 +128,35 @@ int rt_hip_gemv_q4k_tiled_bf16(int32_t count, const void* const* tiled, float* c
                                const int64_t* n, const uint16_t* w_bf16, float* y_bf16,
                                int64_t n_bf16, const float* x, int64_t k, rt_hip_stream stream);
 
+/* ---- layer operations fused into a decode GEMV's activation staging ------
+ * The first part of the full-graph decode engine: the operation that feeds a
+ * projection runs inside the projection's launch, on the activation as each
+ * workgroup stages it, instead of as a launch of its own.
+ *
+ * rt_hip_gemv_q4k_tiled_rmsnorm_multi: y_j = W_j . RMSNorm(x) for up to four
+ * tiled Q4_K weights sharing x (a layer's q/k/v, or gate/up).
+ * Replace: RmsNorm2::forward then the projections (include/rt/nn2.hpp:246-257,
+ * src/transformer5.cpp:198-203), i.e. TensorNode::rms_norm
+ * (src/tensor_node.cpp:320-344, 383): rms_inv = 1 / sqrt(sum(x^2) / k + eps),
+ * x_hat = x * rms_inv, then x_hat * gamma; gemma3 != 0 uses (1 + gamma)
+ * (TensorNode::rms_norm_gemma3, :387; the Gemma 3 Metal kernel
+ * rms_norm_gemma3, shaders/decode_gemma3.msl:7-53).  gamma [k] device f32.
+ *
+ * rt_hip_gemv_q4k_tiled_swiglu: y = W . (silu(gate) * up), the Llama MLP's
+ * down projection on its gate/up outputs.
+ * Replace: LlamaMlp::forward's silu, mul_elem_node and down_proj
+ * (src/transformer5.cpp:186-190; TensorNode::silu, src/tensor_node.cpp:
+ * 391-402, sigmoid first, then the product).
+ *
+ * Outputs match the separate operations followed by rt_hip_gemv_q4k_tiled_multi
+ * to f32 rounding (the sum of squares is reduced in a tree, not in sequence).
+ * k % 256 == 0, k <= 8192. */
+int rt_hip_gemv_q4k_tiled_rmsnorm_multi(int32_t count, const void* const* tiled, float* const* y,
+                                        const int64_t* n, const float* x, const float* gamma, float eps,
+                                        int32_t gemma3, int64_t k, rt_hip_stream stream);
+int rt_hip_gemv_q4k_tiled_swiglu(const void* tiled, const float* gate, const float* up, float* y, int64_t n,
+                                 int64_t k, rt_hip_stream stream);
+
 /* ---- decode chain: a step's dependent GEMV stages in one launch -----------
  * Replace: MetalDecodeContext::create / decode_step, the per-token sequence
  * of GEMV dispatches encoded into one command buffer

@@ -71,9 +71,29 @@ class Oracle:
         self._q40_enc = _bind(L, "orc_q4_0_encode_block", None, _f32p, C.c_float, _u8p)
         self._q40_quant = _bind(L, "orc_q4_0_quantize", None, _f32p, _sz, _u8p)
         self._q6k_dec = _bind(L, "orc_q6k_decode_f32", None, _u8p, _sz, _f32p)
+        self._rmsnorm = _bind(L, "orc_rmsnorm", None, _f32p, _f32p, _sz, C.c_float, C.c_int, _f32p)
+        self._swiglu = _bind(L, "orc_swiglu", None, _f32p, _f32p, _sz, _f32p)
         self._argmax = _bind(L, "orc_argmax_first", C.c_int64, _f32p, _sz)
         self._normal = _bind(L, "orc_initrng_normal", None, C.c_uint64, _sz, C.c_float, _f32p)
         self._hw = _bind(L, "orc_hardware_threads", C.c_int)
+
+    # layer operations -- tensor_node.cpp:320-344, 383-402; transformer5.cpp:186-190
+    def rmsnorm(self, x: np.ndarray, gamma: np.ndarray, eps: float, gemma3: bool = False) -> np.ndarray:
+        """Row-wise RMSNorm of x [rows, d] (or [d])."""
+        x = np.ascontiguousarray(x, np.float32)
+        g = np.ascontiguousarray(gamma, np.float32).reshape(-1)
+        rows = x.reshape(-1, g.size)
+        out = np.empty_like(rows)
+        for r in range(rows.shape[0]):
+            self._rmsnorm(np.ascontiguousarray(rows[r]), g, g.size, eps, 1 if gemma3 else 0, out[r])
+        return out.reshape(x.shape)
+
+    def swiglu(self, gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+        g = np.ascontiguousarray(gate, np.float32).reshape(-1)
+        u = np.ascontiguousarray(up, np.float32).reshape(-1)
+        out = np.empty_like(g)
+        self._swiglu(g, u, g.size, out)
+        return out.reshape(np.shape(gate))
 
     # conversions -- bf16.hpp:42-126
     def f16_to_f32(self, b: int) -> float:

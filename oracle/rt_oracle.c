@@ -619,6 +619,36 @@ int64_t orc_argmax_first(const float* v, size_t n) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* Layer operations either side of a decode GEMV                            */
+/* ------------------------------------------------------------------------ */
+
+/* TensorNode::rms_norm / rms_norm_gemma3 on one row (src/tensor_node.cpp:
+ * 320-344, 383-389): mean_sq summed in sequence in f32, times 1/d;
+ * rms_inv = 1 / sqrt(mean_sq + eps); x_hat = x * rms_inv; out = x_hat * g,
+ * g = gamma or 1 + gamma. */
+void orc_rmsnorm(const float* x, const float* gamma, size_t d, float eps, int gemma3, float* out) {
+    const float inv_d = 1.0f / (float)d;
+    float mean_sq = 0.0f;
+    for (size_t c = 0; c < d; ++c) mean_sq += x[c] * x[c];
+    mean_sq *= inv_d;
+    const float rms_inv = 1.0f / sqrtf(mean_sq + eps);
+    for (size_t c = 0; c < d; ++c) {
+        const float g = gemma3 ? 1.0f + gamma[c] : gamma[c];
+        out[c] = (x[c] * rms_inv) * g;
+    }
+}
+
+/* LlamaMlp::forward's activation (src/transformer5.cpp:186-190): silu(gate)
+ * as TensorNode::silu computes it (src/tensor_node.cpp:391-402: the sigmoid
+ * 1 / (1 + exp(-x)) first, then x * sigmoid), times up. */
+void orc_swiglu(const float* gate, const float* up, size_t n, float* out) {
+    for (size_t i = 0; i < n; ++i) {
+        const float sig = 1.0f / (1.0f + expf(-gate[i]));
+        out[i] = (gate[i] * sig) * up[i];
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* InitRng: include/rt/init_rng.hpp:14-47                                   */
 /* ------------------------------------------------------------------------ */
 

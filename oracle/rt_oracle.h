@@ -112,6 +112,18 @@ void orc_q4_0_quantize(const float* w, size_t n_elem, uint8_t* out);
 /* src/gguf.cpp:531-580 */
 void orc_q6k_decode_f32(const uint8_t* blocks, size_t n_elem, float* out);
 
+/* RMSNorm of one row and SwiGLU, as the reference computes them
+ * (tensor_node.cpp:320-344, 383-402; transformer5.cpp:186-190).
+ * Pinned by: closed forms (a constant row c gives c / sqrt(c^2 + eps) * g;
+ * gemma3 = the plain form with 1 + gamma), the scale invariance
+ * rmsnorm(a x) = rmsnorm(x) for eps = 0 and a power of two, silu's fixed
+ * points (silu(0) = 0, silu(x) -> x and -> 0 at the tails) and its identity
+ * silu(x) - silu(-x) = x, each checked in float64 by tests/test_oracle_layer_ops.py.
+ * The reference's own tensor_node.cpp needs its autograd graph (TensorNode,
+ * Mat and their sources) and is not built here. */
+void orc_rmsnorm(const float* x, const float* gamma, size_t d, float eps, int gemma3, float* out);
+void orc_swiglu(const float* gate, const float* up, size_t n, float* out);
+
 /* src/transformer5.cpp:382-391: first index of the strict maximum; NaN never wins */
 int64_t orc_argmax_first(const float* v, size_t n);
 

@@ -262,6 +262,38 @@ int rt_hip_gemv_q4k_tiled_multi(int32_t count, const void* const* tiled, float* 
                                "rt_hip_gemv_q4k_tiled_multi");
 }
 
+namespace {
+int gemv_xop(const char* fn, int xop, int32_t count, const void* const* tiled, float* const* y, const int64_t* n,
+             const float* x, const float* aux, float eps, int64_t k, rt_hip_stream stream) {
+    if (count < 1 || count > RT_HIP_MULTI_MAX || !tiled || !y || !n)
+        return fail(RT_HIP_E_ARG, std::string(fn) + ": count must be in [1, 4] with arrays");
+    for (int32_t j = 0; j < count; ++j) {
+        int rc = gemv_args(fn, tiled[j], x, y[j], n[j], k, 1, 256);
+        if (rc) return rc;
+    }
+    if (!aux) return fail(RT_HIP_E_ARG, std::string(fn) + ": null gamma / up");
+    if (!aligned16(aux)) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": gamma / up must be 16-byte aligned");
+    if (k > 8192 || q4k_m1_lds_bytes(k) > 65536) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 8192");
+    if (!(eps >= 0.0f)) return fail(RT_HIP_E_ARG, std::string(fn) + ": eps must be >= 0");
+    hipError_t e;
+    if (!state_for_current(&e)) return hip_fail(e, fn);
+    return check_stream_launch(
+        launch_gemv_q4k_xop(xop, count, tiled, y, n, x, aux, eps, k, static_cast<hipStream_t>(stream)), fn);
+}
+}  // namespace
+
+int rt_hip_gemv_q4k_tiled_rmsnorm_multi(int32_t count, const void* const* tiled, float* const* y,
+                                        const int64_t* n, const float* x, const float* gamma, float eps,
+                                        int32_t gemma3, int64_t k, rt_hip_stream stream) {
+    return gemv_xop("rt_hip_gemv_q4k_tiled_rmsnorm_multi", gemma3 ? 2 : 1, count, tiled, y, n, x, gamma, eps, k,
+                    stream);
+}
+
+int rt_hip_gemv_q4k_tiled_swiglu(const void* tiled, const float* gate, const float* up, float* y, int64_t n,
+                                 int64_t k, rt_hip_stream stream) {
+    return gemv_xop("rt_hip_gemv_q4k_tiled_swiglu", 3, 1, &tiled, &y, &n, gate, up, 0.0f, k, stream);
+}
+
 int rt_hip_gemv_q4k_tiled_bf16(int32_t count, const void* const* tiled, float* const* y,
                                const int64_t* n, const uint16_t* w_bf16, float* y_bf16,
                                int64_t n_bf16, const float* x, int64_t k, rt_hip_stream stream) {

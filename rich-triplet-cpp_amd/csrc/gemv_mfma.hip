@@ -57,15 +57,26 @@ __device__ __forceinline__ uint64_t sreg(const void* p) {
     return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
-// The K-split of a launch, packed by the host into one preloaded argument
-// so that no wave divides: bits 0-3 KS (waves per tile), 4-7 TPW (tiles per
-// workgroup), 8-15 super-blocks per wave, 16-28 ceil(4096 / KS), with which
-// wave / KS = (wave * m) >> 12 exactly for wave < 16 and KS <= 12 (the
-// rounding adds < 16/4096, below the gap 1/KS to the next integer).
-__host__ __device__ inline uint32_t pack_split(int ks, int tpw, int bpw) {
+// The K-split of a launch and its job count, packed by the host into one
+// preloaded argument so that no wave divides: bits 0-3 KS (waves per tile),
+// 4-7 TPW (tiles per workgroup), 8-15 super-blocks per wave, 16-28
+// ceil(4096 / KS), with which wave / KS = (wave * m) >> 12 exactly for
+// wave < 16 and KS <= 12 (the rounding adds < 16/4096, below the gap 1/KS
+// to the next integer), 29-31 the job count (1..4).
+__host__ __device__ inline uint32_t pack_split(int ks, int tpw, int bpw, int count) {
     return static_cast<uint32_t>(ks) | (static_cast<uint32_t>(tpw) << 4) | (static_cast<uint32_t>(bpw) << 8) |
-           (static_cast<uint32_t>((4096 + ks - 1) / ks) << 16);
+           (static_cast<uint32_t>((4096 + ks - 1) / ks) << 16) | (static_cast<uint32_t>(count) << 29);
 }
+
+// What the kernel applies to the activation while staging it (the layer
+// operations either side of a decode GEMV, fused into its launch):
+//   kXNone     x as given;
+//   kXRmsNorm  RMSNorm(x) * gamma            (tensor_node.cpp:320-344, 383);
+//   kXRmsNorm1 RMSNorm(x) * (1 + gamma)      (the Gemma 3 form, :387);
+//   kXSwiGlu   silu(gate) * up, x = gate     (tensor_node.cpp:391-402,
+//              transformer5.cpp:186-190).
+// `aux` is gamma or up.
+enum XOp { kXNone = 0, kXRmsNorm = 1, kXRmsNorm1 = 2, kXSwiGlu = 3 };
 
 // KS waves split a tile's super-blocks; a workgroup of blockDim.x / 64 waves
 // holds TPW = waves / KS tiles.
@@ -76,10 +87,12 @@ __host__ __device__ inline uint32_t pack_split(int ks, int tpw, int bpw) {
 // output pointer) come from the table.
 // The body of workgroup `blk` (the kernel below, and the Q4_K workgroups of
 // the fused q/k/v launch); `lds` holds mfma_gemv_lds_bytes(K, waves).
-template <int D, int XP, bool TILED, bool J34>
+template <int D, int XP, bool TILED, bool J34, int XOP = kXNone>
 __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, int K, uint32_t split, int nthreads,
                                           const uint8_t* w0, const uint8_t* w1, int n0, int n1, int tile1,
-                                          int count, const Jobs& jobs, uint8_t* lds) {
+                                          const Jobs& jobs, uint8_t* lds, const float* __restrict__ aux = nullptr,
+                                          float eps = 0.0f) {
+    const int count = static_cast<int>(split >> 29);
     // nthreads == blockDim.x, passed as a preloaded argument: blockDim
     // itself is a kernel-argument load that the first x loads would wait for.
     const int KS = static_cast<int>(split & 15u), TPW = static_cast<int>((split >> 4) & 15u);
@@ -87,7 +100,7 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nb = K >> 8;
-    const int tslot = (wave * static_cast<int>(split >> 16)) >> 12;
+    const int tslot = (wave * static_cast<int>((split >> 16) & 0x1fffu)) >> 12;
     const int ks = wave - tslot * KS;
     const int b0 = ks * bpw;
     const int nbw = min(nb, b0 + bpw) - b0;  // >= 1: the host picks KS so every split is non-empty
@@ -102,11 +115,19 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     // keeps these loads ahead of the weight prologue; vmcnt counts them in
     // order, so waiting for them is partial.
     const f32x4* const X4 = reinterpret_cast<const f32x4*>(X);
-    f32x4 xv[XP];
+    f32x4 xv[XP], av[XP];
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
         const int f = tid + nthreads * i;
         xv[i] = X4[f < nx ? f : 0];
+    }
+    if constexpr (XOP != kXNone) {
+        const f32x4* const A4 = reinterpret_cast<const f32x4*>(aux);
+#pragma unroll
+        for (int i = 0; i < XP; ++i) {
+            const int f = tid + nthreads * i;
+            av[i] = A4[f < nx ? f : 0];
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -185,6 +206,41 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     // The x loads are older than the 3*D prologue loads: wait for them
     // alone (XP * nthreads >= K/4, checked by the host), then convert.
     wait_vmcnt<3 * D>();
+    if constexpr (XOP == kXRmsNorm || XOP == kXRmsNorm1) {
+        // Sum of squares: per thread, then over the wave (DPP and permlane),
+        // then over the workgroup's waves through LDS (the partial-row area,
+        // free until the loop ends).  Then, as the reference does,
+        // rms_inv = 1 / sqrt(sum * (1/K) + eps) and x * rms_inv * g.
+        float sq = 0.0f;
+#pragma unroll
+        for (int i = 0; i < XP; ++i) {
+            const f32x4 v = tid + nthreads * i < nx ? xv[i] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            sq += (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+        }
+        sq = bf16_gemv::wave_sum(sq, lane);
+        float* const part = reinterpret_cast<float*>(lds + lds_bytes(K));
+        if (lane == 0) part[wave] = sq;
+        lds_barrier();
+        float tot = 0.0f;
+        for (int w = 0; w < (nthreads >> 6); ++w) tot += part[w];
+        const float rms_inv = 1.0f / __builtin_sqrtf(tot * (1.0f / static_cast<float>(K)) + eps);
+#pragma unroll
+        for (int i = 0; i < XP; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float g = XOP == kXRmsNorm1 ? 1.0f + av[i][e] : av[i][e];
+                xv[i][e] = (xv[i][e] * rms_inv) * g;
+            }
+    } else if constexpr (XOP == kXSwiGlu) {
+#pragma unroll
+        for (int i = 0; i < XP; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float g = xv[i][e];
+                const float sig = 1.0f / (1.0f + expf(-g));
+                xv[i][e] = (g * sig) * av[i][e];
+            }
+    }
     // Every lane converts its values (past the end: a dummy that is not
     // stored; the 8-lane reductions need the whole group).  No branch may
     // skip a round: the compiler would sink that round's x load below the
@@ -244,10 +300,21 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
 template <int D, int XP, bool TILED, bool J34>
 __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
     const float* __restrict__ X, int K, uint32_t split, int nthreads, const uint8_t* w0, const uint8_t* w1,
-    int n0, int n1, int tile1, int count, const Jobs jobs) {
+    int n0, int n1, int tile1, const Jobs jobs) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    q4k_tiles<D, XP, TILED, J34>(static_cast<int>(blockIdx.x), X, K, split, nthreads, w0, w1, n0, n1, tile1, count,
-                                 jobs, lds);
+    q4k_tiles<D, XP, TILED, J34>(static_cast<int>(blockIdx.x), X, K, split, nthreads, w0, w1, n0, n1, tile1, jobs,
+                                 lds);
+}
+
+// The same with a layer operation applied to x while it is staged (XOp);
+// aux (gamma or up) is preloaded with the other pointers.
+template <int XP, bool J34, int XOP>
+__global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_xop(
+    const float* __restrict__ X, const float* __restrict__ aux, int K, uint32_t split, int nthreads,
+    const uint8_t* w0, const uint8_t* w1, int n0, int n1, int tile1, const Jobs jobs, float eps) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    q4k_tiles<4, XP, true, J34, XOP>(static_cast<int>(blockIdx.x), X, K, split, nthreads, w0, w1, n0, n1, tile1,
+                                     jobs, lds, aux, eps);
 }
 
 // A layer's q/k/v when v is BF16 (Q6_K widened): the first q4k_wgs
@@ -257,47 +324,62 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
 template <int XPQ, bool J34, int XPB>
 __global__ __launch_bounds__(bf16_gemv::kThreads) void k_gemv_q4k_bf16(
     const float* __restrict__ X, int K, uint32_t split, int nthreads, const uint8_t* w0, const uint8_t* w1,
-    int n0, int n1, int tile1, int count, int q4k_wgs, const uint16_t* __restrict__ wb, float* __restrict__ yb,
+    int n0, int n1, int tile1, int q4k_wgs, const uint16_t* __restrict__ wb, float* __restrict__ yb,
     int nb_rows, const Jobs jobs) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int blk = static_cast<int>(blockIdx.x);
     if (blk < q4k_wgs)
-        q4k_tiles<4, XPQ, true, J34>(blk, X, K, split, nthreads, w0, w1, n0, n1, tile1, count, jobs, lds);
+        q4k_tiles<4, XPQ, true, J34>(blk, X, K, split, nthreads, w0, w1, n0, n1, tile1, jobs, lds);
     else
         bf16_gemv::rows<8, XPB, false>(blk - q4k_wgs, (nb_rows + 3) / 4, wb, X, yb, nb_rows, K, nullptr, lds);
 }
 
-template <int D, int XP, bool TILED, bool J34>
-hipError_t run(const Jobs& jobs, const float* x, int64_t k, int ks, int waves, hipStream_t s) {
+// The x operation, its second vector and eps (XOp).
+struct XArgs {
+    const float* aux = nullptr;
+    float eps = 0.0f;
+};
+
+template <int D, int XP, bool TILED, bool J34, int XOP>
+hipError_t run(const Jobs& jobs, const float* x, const XArgs& xa, int64_t k, int ks, int waves, hipStream_t s) {
     const int tpw = waves / ks;
     const int64_t wgs = (static_cast<int64_t>(jobs.total) + tpw - 1) / tpw;
     const size_t lds = mfma_gemv_lds_bytes(k, waves);
-    const uint32_t split = pack_split(ks, tpw, static_cast<int>((k / 256 + ks - 1) / ks));
-    hipLaunchKernelGGL((k_gemv_q4k_mfma<D, XP, TILED, J34>), dim3(static_cast<unsigned>(wgs)),
-                       dim3(static_cast<unsigned>(waves * kWave)), lds, s, x, static_cast<int>(k), split,
-                       waves * kWave, jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], jobs.count,
-                       jobs);
+    const uint32_t split = pack_split(ks, tpw, static_cast<int>((k / 256 + ks - 1) / ks), jobs.count);
+    const dim3 g(static_cast<unsigned>(wgs)), b(static_cast<unsigned>(waves * kWave));
+    if constexpr (XOP == kXNone) {
+        hipLaunchKernelGGL((k_gemv_q4k_mfma<D, XP, TILED, J34>), g, b, lds, s, x, static_cast<int>(k), split,
+                           waves * kWave, jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], jobs);
+    } else {
+        static_assert(D == 4 && TILED, "x operations run on the tiled layout, ring depth 4");
+        hipLaunchKernelGGL((k_gemv_q4k_xop<XP, J34, XOP>), g, b, lds, s, x, xa.aux, static_cast<int>(k), split,
+                           waves * kWave, jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], jobs, xa.eps);
+    }
     return hipGetLastError();
 }
 
 // x prefetch depth: enough f32x4 per thread for all of x (up to K = 8192 at
 // 256 threads) before the weight prologue.
-template <int D, bool TILED>
-hipError_t run_xp(const Jobs& jobs, const float* x, int64_t k, int ks, int waves, hipStream_t s) {
+template <int D, bool TILED, int XOP>
+hipError_t run_xp(const Jobs& jobs, const float* x, const XArgs& xa, int64_t k, int ks, int waves,
+                  hipStream_t s) {
     const int64_t per = (k / 4 + waves * kWave - 1) / (waves * kWave);
-    if (per > 16) return hipErrorInvalidValue;  // the host keeps K within the staging bound
+    // The host keeps K within the staging bound: 16 float4 per thread, 8
+    // with an x operation (its second vector doubles the registers).
+    if (per > (XOP == kXNone ? 16 : 8)) return hipErrorInvalidValue;
     if (jobs.count > 2) {
-        if (per <= 2) return run<D, 2, TILED, true>(jobs, x, k, ks, waves, s);
-        if (per <= 3) return run<D, 3, TILED, true>(jobs, x, k, ks, waves, s);
-        if (per <= 4) return run<D, 4, TILED, true>(jobs, x, k, ks, waves, s);
-        if (per <= 8) return run<D, 8, TILED, true>(jobs, x, k, ks, waves, s);
-        return run<D, 16, TILED, true>(jobs, x, k, ks, waves, s);
+        if (per <= 2) return run<D, 2, TILED, true, XOP>(jobs, x, xa, k, ks, waves, s);
+        if (per <= 3) return run<D, 3, TILED, true, XOP>(jobs, x, xa, k, ks, waves, s);
+        if (per <= 4) return run<D, 4, TILED, true, XOP>(jobs, x, xa, k, ks, waves, s);
+        if (per <= 8 || XOP != kXNone) return run<D, 8, TILED, true, XOP>(jobs, x, xa, k, ks, waves, s);
+        if constexpr (XOP == kXNone) return run<D, 16, TILED, true, XOP>(jobs, x, xa, k, ks, waves, s);
     }
-    if (per <= 2) return run<D, 2, TILED, false>(jobs, x, k, ks, waves, s);
-    if (per <= 3) return run<D, 3, TILED, false>(jobs, x, k, ks, waves, s);
-    if (per <= 4) return run<D, 4, TILED, false>(jobs, x, k, ks, waves, s);
-    if (per <= 8) return run<D, 8, TILED, false>(jobs, x, k, ks, waves, s);
-    return run<D, 16, TILED, false>(jobs, x, k, ks, waves, s);
+    if (per <= 2) return run<D, 2, TILED, false, XOP>(jobs, x, xa, k, ks, waves, s);
+    if (per <= 3) return run<D, 3, TILED, false, XOP>(jobs, x, xa, k, ks, waves, s);
+    if (per <= 4) return run<D, 4, TILED, false, XOP>(jobs, x, xa, k, ks, waves, s);
+    if (per <= 8 || XOP != kXNone) return run<D, 8, TILED, false, XOP>(jobs, x, xa, k, ks, waves, s);
+    if constexpr (XOP == kXNone) return run<D, 16, TILED, false, XOP>(jobs, x, xa, k, ks, waves, s);
+    return hipErrorInvalidValue;
 }
 
 // K-split per tile.  One round of workgroups (at most one per CU) is what
@@ -313,8 +395,8 @@ hipError_t run_xp(const Jobs& jobs, const float* x, int64_t k, int ks, int waves
 // KS = 1 use KS = 4 (the lm_head: 38.0 us against 40.9 us at KS = 2).
 // KS = 1, 2, 4 run 4 waves per workgroup (4/KS tiles); other splits one
 // tile per workgroup of KS waves.
-template <bool TILED>
-hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s) {
+template <bool TILED, int XOP = kXNone>
+hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s, const XArgs& xa = XArgs{}) {
     const int64_t tiles = jobs.total;
     const int64_t nb = k / 256;
     const int64_t cus = device_info().cus;
@@ -336,8 +418,13 @@ hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s) 
     int waves = ks <= 4 ? (4 / ks) * ks : ks;
     if (const int tpw = tune_param("Q4K_TPW", 0)) waves = ks * tpw;
     if (waves % ks != 0 || waves > kMaxThreads / kWave) return hipErrorInvalidValue;
-    const int d = tune_param("Q4K_RING", 4);
-    return d == 8 ? run_xp<8, TILED>(jobs, x, k, ks, waves, s) : run_xp<4, TILED>(jobs, x, k, ks, waves, s);
+    if constexpr (XOP != kXNone) {
+        return run_xp<4, TILED, XOP>(jobs, x, xa, k, ks, waves, s);
+    } else {
+        const int d = tune_param("Q4K_RING", 4);
+        return d == 8 ? run_xp<8, TILED, XOP>(jobs, x, xa, k, ks, waves, s)
+                      : run_xp<4, TILED, XOP>(jobs, x, xa, k, ks, waves, s);
+    }
 }
 
 }  // namespace
@@ -347,6 +434,37 @@ size_t mfma_gemv_lds_bytes(int64_t k, int waves) {
 }
 
 size_t q4k_m1_lds_bytes(int64_t k) { return mfma_gemv_lds_bytes(k, kMaxThreads / kWave); }
+
+hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* const* y, const int64_t* n,
+                              const float* x, const float* aux, float eps, int64_t k, hipStream_t s) {
+    if (count < 1 || count > kMaxJobs || aux == nullptr) return hipErrorInvalidValue;
+    Jobs jobs{};
+    jobs.count = count;
+    int64_t tiles = 0;
+    for (int j = 0; j < count; ++j) {
+        jobs.w[j] = static_cast<const uint8_t*>(w[j]);
+        jobs.y[j] = y[j];
+        jobs.n[j] = static_cast<int>(n[j]);
+        jobs.tile0[j] = static_cast<int>(tiles);
+        tiles += (n[j] + 15) / 16;
+    }
+    for (int j = count; j < kMaxJobs; ++j) {
+        jobs.w[j] = jobs.w[0];
+        jobs.y[j] = jobs.y[0];
+        jobs.n[j] = jobs.n[0];
+        jobs.tile0[j] = static_cast<int>(tiles);
+    }
+    jobs.total = static_cast<int>(tiles);
+    XArgs xa;
+    xa.aux = aux;
+    xa.eps = eps;
+    switch (xop) {
+        case kXRmsNorm: return dispatch<true, kXRmsNorm>(jobs, x, k, s, xa);
+        case kXRmsNorm1: return dispatch<true, kXRmsNorm1>(jobs, x, k, s, xa);
+        case kXSwiGlu: return dispatch<true, kXSwiGlu>(jobs, x, k, s, xa);
+        default: return hipErrorInvalidValue;
+    }
+}
 
 hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* const* y,
                                       const int64_t* n, const float* x, int64_t k, hipStream_t s,
@@ -380,8 +498,8 @@ hipError_t run_fused(const Jobs& jobs, int ks, int q4k_wgs, const uint16_t* wb, 
     const int64_t bwgs = (nb_rows + 3) / 4;  // one row per wave, 4 waves
     hipLaunchKernelGGL((k_gemv_q4k_bf16<XPQ, J34, XPB>), dim3(static_cast<unsigned>(q4k_wgs + bwgs)),
                        dim3(bf16_gemv::kThreads), lds, s, x, static_cast<int>(k),
-                       pack_split(ks, 4 / ks, static_cast<int>((k / 256 + ks - 1) / ks)), bf16_gemv::kThreads,
-                       jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], jobs.count, q4k_wgs, wb, yb,
+                       pack_split(ks, 4 / ks, static_cast<int>((k / 256 + ks - 1) / ks), jobs.count),
+                       bf16_gemv::kThreads, jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], q4k_wgs, wb, yb,
                        static_cast<int>(nb_rows), jobs);
     return hipGetLastError();
 }

@@ -43,6 +43,11 @@ hipError_t launch_gemv_q4k_mfma(const void* w, const float* x, float* y, int64_t
                                 hipStream_t s);
 // Up to four M = 1 Q4_K GEMVs sharing x, K; `tiled`: the weights are in the
 // tiled layout (q4k_mfma.hpp) rather than reference row-major blocks.
+// Tiled Q4_K GEMVs sharing x, with a layer operation applied to x while it
+// is staged: xop 1 RMSNorm * gamma, 2 RMSNorm * (1 + gamma), 3 silu(x) * aux
+// (aux = gamma or up; eps for the norms).
+hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* const* y, const int64_t* n,
+                              const float* x, const float* aux, float eps, int64_t k, hipStream_t s);
 hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* const* y,
                                       const int64_t* n, const float* x, int64_t k, hipStream_t s,
                                       bool tiled);

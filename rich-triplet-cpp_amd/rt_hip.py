@@ -41,6 +41,9 @@ _SIGNATURES = {
     "rt_hip_linear_forward": [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_bf16": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp, _i64,
                                    _vp, _i64, _vp],
+    "rt_hip_gemv_q4k_tiled_rmsnorm_multi": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp,
+                                            C.c_float, _i32, _i64, _vp],
+    "rt_hip_gemv_q4k_tiled_swiglu": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_dequant_q6k_bf16": [_vp, _vp, _i64, _i64, _vp],
     "rt_hip_q6k_tile": [_vp, _vp, _i64, _i64, _vp],
     "rt_hip_gemv_q6k_tiled": [_vp, _vp, _vp, _i64, _i64, _vp],
@@ -252,6 +255,33 @@ def gemv_q4k_tiled_bf16(ws, ns, wb, nb: int, x, k: int, ys=None, yb=None, stream
     library().call("rt_hip_gemv_q4k_tiled_bf16", count, wp, yp, npp, _ptr(wb), _ptr(yb), nb, _ptr(x), k,
                    _stream(stream))
     return ys, yb
+
+
+def gemv_q4k_tiled_rmsnorm_multi(ws, x, gamma, eps: float, ns, k: int, gemma3: bool = False, ys=None,
+                                 stream=None):
+    """y_j = W_j . RMSNorm(x) (gamma, or 1 + gamma for gemma3) for tiled Q4_K
+    weights sharing x, the norm applied while x is staged."""
+    torch = _torch()
+    count = len(ws)
+    if ys is None:
+        ys = [torch.empty((1, n), dtype=torch.float32, device=x.device) for n in ns]
+    _dev_check(x, gamma, *ws, *ys)
+    wp = (_vp * count)(*[w.data_ptr() for w in ws])
+    yp = (_vp * count)(*[y.data_ptr() for y in ys])
+    npp = (_i64 * count)(*ns)
+    library().call("rt_hip_gemv_q4k_tiled_rmsnorm_multi", count, wp, yp, npp, _ptr(x), _ptr(gamma),
+                   C.c_float(eps), 1 if gemma3 else 0, k, _stream(stream))
+    return ys
+
+
+def gemv_q4k_tiled_swiglu(w, gate, up, n: int, k: int, y=None, stream=None):
+    """y = W . (silu(gate) * up) for a tiled Q4_K weight (the down projection)."""
+    torch = _torch()
+    if y is None:
+        y = torch.empty((1, n), dtype=torch.float32, device=gate.device)
+    _dev_check(w, gate, up, y)
+    library().call("rt_hip_gemv_q4k_tiled_swiglu", _ptr(w), _ptr(gate), _ptr(up), _ptr(y), n, k, _stream(stream))
+    return y
 
 
 def dequant_q6k_bf16(blocks, n: int, k: int, stream=None):

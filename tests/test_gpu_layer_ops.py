@@ -1,0 +1,87 @@
+"""GPU parity: layer operations fused into the decode GEMV's activation
+staging (rt_hip_gemv_q4k_tiled_rmsnorm_multi / _swiglu).
+
+Expected values: the oracle's RMSNorm / SwiGLU (tensor_node.cpp:320-402,
+transformer5.cpp:186-190, pinned in test_oracle_layer_ops.py), then the
+oracle's Q4_K product, normwise within the GEMV bar (1e-5); and the product's
+own unfused path on the same normalized activation, to the same bar."""
+import numpy as np
+import pytest
+
+from helpers import GEMV_TOL, from_dev, normwise_err, say, to_dev
+
+pytestmark = pytest.mark.gpu
+E_ARG, E_SHAPE = 1, 2
+
+
+def _weights(orc, rng, ns, k):
+    return [orc.q4k_quantize((rng.standard_normal((n, k)) * 0.02).astype(np.float32)) for n in ns]
+
+
+@pytest.mark.parametrize("ns,k,gemma3,note", [
+    ([3072, 1024, 1024], 3072, False, "llama q/k/v"),
+    ([8192, 8192], 3072, False, "llama gate/up"),
+    ([1152, 256, 256], 1152 // 256 * 256, True, "gemma3 form"),
+    ([40], 512, False, "short output"),
+])
+def test_rmsnorm_fused_gemv(rt, orc, ns, k, gemma3, note):
+    say(f"[rmsnorm gemv] ns={ns} K={k} gemma3={gemma3} ({note})")
+    rng = np.random.default_rng(sum(ns) + k)
+    blocks = _weights(orc, rng, ns, k)
+    x = (rng.standard_normal(k) * 3).astype(np.float32)
+    gamma = (rng.standard_normal(k) * (0.1 if gemma3 else 1.0)).astype(np.float32)
+    eps = 1e-6 if gemma3 else 1e-5
+    tiled = [rt.q4k_tile(to_dev(b), n, k) for b, n in zip(blocks, ns)]
+    ys = rt.gemv_q4k_tiled_rmsnorm_multi(tiled, to_dev(x), to_dev(gamma), eps, ns, k, gemma3=gemma3)
+    xn = orc.rmsnorm(x, gamma, eps, gemma3=gemma3).reshape(1, k)
+    unfused = rt.gemv_q4k_tiled_multi(tiled, to_dev(xn), ns, k)
+    for b, n, y, u in zip(blocks, ns, ys, unfused):
+        want = orc.q4k_matmul_t(b, n, k, xn)
+        got = from_dev(y)
+        assert normwise_err(got, want) <= GEMV_TOL, normwise_err(got, want)
+        assert normwise_err(got, from_dev(u)) <= GEMV_TOL
+
+
+def test_rmsnorm_zero_activation_gives_zero(rt, orc):
+    k, n = 1024, 64
+    rng = np.random.default_rng(9)
+    (b,) = _weights(orc, rng, [n], k)
+    t = rt.q4k_tile(to_dev(b), n, k)
+    (y,) = rt.gemv_q4k_tiled_rmsnorm_multi([t], to_dev(np.zeros(k, np.float32)),
+                                           to_dev(np.ones(k, np.float32)), 1e-5, [n], k)
+    assert not np.any(from_dev(y))
+
+
+@pytest.mark.parametrize("n,k,note", [(3072, 8192, "llama down"), (100, 512, "ragged N"), (16, 256, "one block")])
+def test_swiglu_fused_gemv(rt, orc, n, k, note):
+    say(f"[swiglu gemv] N={n} K={k} ({note})")
+    rng = np.random.default_rng(n + 3 * k)
+    (b,) = _weights(orc, rng, [n], k)
+    gate = (rng.standard_normal(k) * 2).astype(np.float32)
+    up = rng.standard_normal(k).astype(np.float32)
+    t = rt.q4k_tile(to_dev(b), n, k)
+    got = from_dev(rt.gemv_q4k_tiled_swiglu(t, to_dev(gate), to_dev(up), n, k))
+    act = orc.swiglu(gate, up).reshape(1, k)
+    want = orc.q4k_matmul_t(b, n, k, act)
+    assert normwise_err(got, want) <= GEMV_TOL, normwise_err(got, want)
+    unfused = from_dev(rt.gemv_q4k_tiled(t, to_dev(act), n, k))
+    assert normwise_err(got, unfused) <= GEMV_TOL
+
+
+def test_layer_ops_reject_bad_arguments(rt):
+    import ctypes as C
+    lib = rt.library()
+    t = to_dev(np.zeros(2304, np.uint8))
+    x = to_dev(np.zeros(16384, np.float32))
+    y = to_dev(np.zeros(16, np.float32))
+    wp = (C.c_void_p * 1)(t.data_ptr())
+    yp = (C.c_void_p * 1)(y.data_ptr())
+    npp = (C.c_int64 * 1)(16)
+    assert lib.status("rt_hip_gemv_q4k_tiled_rmsnorm_multi", 1, wp, yp, npp, x.data_ptr(), None,
+                      C.c_float(1e-5), 0, 256, None) == E_ARG
+    assert lib.status("rt_hip_gemv_q4k_tiled_rmsnorm_multi", 1, wp, yp, npp, x.data_ptr(), x.data_ptr(),
+                      C.c_float(-1.0), 0, 256, None) == E_ARG
+    assert lib.status("rt_hip_gemv_q4k_tiled_swiglu", t.data_ptr(), x.data_ptr(), x.data_ptr(), y.data_ptr(),
+                      16, 16384, None) == E_SHAPE
+    assert lib.status("rt_hip_gemv_q4k_tiled_swiglu", t.data_ptr(), x.data_ptr(), None, y.data_ptr(),
+                      16, 256, None) == E_ARG

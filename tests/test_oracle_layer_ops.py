@@ -1,0 +1,72 @@
+"""Pins the oracle's RMSNorm and SwiGLU (orc_rmsnorm / orc_swiglu, restating
+tensor_node.cpp:320-344, 383-402 and transformer5.cpp:186-190) by what the
+mathematics fixes: closed forms, exact invariances and float64 evaluations of
+the same formulas.  CPU only."""
+import numpy as np
+
+
+def test_rmsnorm_constant_row_closed_form(orc):
+    d = 3072
+    rng = np.random.default_rng(0)
+    gamma = rng.standard_normal(d).astype(np.float32)
+    for c, eps in ((0.5, 1e-5), (3.0, 1e-6), (-2.0, 0.0), (1e-3, 1e-5)):
+        x = np.full(d, c, np.float32)
+        got = orc.rmsnorm(x, gamma, eps).astype(np.float64)
+        want = c / np.sqrt(c * c + eps) * gamma.astype(np.float64)
+        assert np.allclose(got, want, rtol=2e-6, atol=0), (c, eps)
+
+
+def test_rmsnorm_gemma3_is_the_plain_form_on_one_plus_gamma(orc):
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((3, 1024)).astype(np.float32)
+    gamma = (rng.standard_normal(1024) * 0.1).astype(np.float32)
+    one_plus = (np.float32(1.0) + gamma).astype(np.float32)
+    assert np.array_equal(orc.rmsnorm(x, gamma, 1e-6, gemma3=True), orc.rmsnorm(x, one_plus, 1e-6))
+
+
+def test_rmsnorm_power_of_two_scale_invariance(orc):
+    """With eps = 0 every step commutes with scaling x by 2^s: the outputs
+    are identical bit for bit (a missing sqrt or a wrong divisor breaks it)."""
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(2048).astype(np.float32)
+    gamma = rng.standard_normal(2048).astype(np.float32)
+    base = orc.rmsnorm(x, gamma, 0.0)
+    for s in (-6, -1, 3, 9):
+        assert np.array_equal(orc.rmsnorm(x * np.float32(2.0 ** s), gamma, 0.0), base), s
+
+
+def test_rmsnorm_random_rows_against_float64(orc):
+    rng = np.random.default_rng(3)
+    for d in (256, 3072, 8192):
+        x = (rng.standard_normal(d) * rng.uniform(0.01, 10)).astype(np.float32)
+        gamma = rng.standard_normal(d).astype(np.float32)
+        x64 = x.astype(np.float64)
+        want = x64 / np.sqrt(np.mean(x64 * x64) + 1e-5) * gamma
+        got = orc.rmsnorm(x, gamma, 1e-5)
+        assert np.max(np.abs(got - want)) <= 4e-6 * np.max(np.abs(want)), d
+
+
+def test_silu_fixed_points_and_odd_identity(orc):
+    ones = np.ones(7, np.float32)
+    g = np.array([0.0, 30.0, 100.0, -30.0, -100.0, 1.0, -1.0], np.float32)
+    s = orc.swiglu(g, ones)
+    assert s[0] == 0.0
+    assert s[1] == np.float32(30.0) and s[2] == np.float32(100.0)  # sigmoid rounds to 1
+    assert -1e-11 < s[3] < 0.0  # -30 * sigmoid(-30)
+    assert abs(s[4]) < 1e-40
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal(4096) * 4).astype(np.float32)
+    one = np.ones_like(x)
+    # silu(x) - silu(-x) = x (sigmoid(x) + sigmoid(-x) = 1)
+    diff = orc.swiglu(x, one).astype(np.float64) - orc.swiglu(-x, one).astype(np.float64)
+    assert np.allclose(diff, x.astype(np.float64), rtol=0, atol=4e-6 * (1 + np.abs(x)).max())
+
+
+def test_swiglu_against_float64(orc):
+    rng = np.random.default_rng(5)
+    g = (rng.standard_normal(8192) * 3).astype(np.float32)
+    u = rng.standard_normal(8192).astype(np.float32)
+    g64 = g.astype(np.float64)
+    want = g64 / (1.0 + np.exp(-g64)) * u.astype(np.float64)
+    got = orc.swiglu(g, u).astype(np.float64)
+    assert np.allclose(got, want, rtol=1e-6, atol=1e-30)
