@@ -342,6 +342,74 @@ def bench_decode(args, rt, torch):
     }
 
 
+# ------------------------------------- layer operations fused into the GEMVs --
+
+def bench_layer_ops(args, rt, torch):
+    """28 pure-Q4_K Llama-3.2-3B layers' linear work with the operations that
+    feed the projections: RMSNorm before q/k/v and before gate/up, SwiGLU
+    before down, a final RMSNorm before the lm_head.  Fused: the norms and
+    the SwiGLU run inside the GEMV launches (4 launches per layer).  Separate:
+    the same operations as torch kernels between the GEMVs (rms_norm, silu,
+    mul).  Attention and the residual adds are outside
+    both.  Weights and inputs are synthetic; the gate/up outputs feed down."""
+    g = torch.Generator(device="cuda").manual_seed(0)
+    dev = "cuda"
+
+    def tiled(n, k):
+        w = torch.randn((n, k), generator=g, device=dev) * 0.02
+        return rt.q4k_tile(rt.quantize_q4k(w), n, k)
+
+    layers = []
+    for _ in range(LAYERS):
+        L = {"qkv": [tiled(HIDDEN, HIDDEN), tiled(KV, HIDDEN), tiled(KV, HIDDEN)], "o": tiled(HIDDEN, HIDDEN),
+             "gu": [tiled(FFN, HIDDEN), tiled(FFN, HIDDEN)], "down": tiled(HIDDEN, FFN),
+             "x": torch.randn((1, HIDDEN), generator=g, device=dev),
+             "x_o": torch.randn((1, HIDDEN), generator=g, device=dev),
+             "g1": 1.0 + 0.1 * torch.randn((HIDDEN,), generator=g, device=dev),
+             "g2": 1.0 + 0.1 * torch.randn((HIDDEN,), generator=g, device=dev)}
+        L["y_qkv"] = [torch.empty((1, n), device=dev) for n in (HIDDEN, KV, KV)]
+        L["y_o"] = torch.empty((1, HIDDEN), device=dev)
+        L["y_gu"] = [torch.empty((1, FFN), device=dev) for _ in range(2)]
+        L["y_d"] = torch.empty((1, HIDDEN), device=dev)
+        layers.append(L)
+    head = {"w": tiled(VOCAB, HIDDEN), "x": torch.randn((1, HIDDEN), generator=g, device=dev),
+            "g": 1.0 + 0.1 * torch.randn((HIDDEN,), generator=g, device=dev),
+            "y": torch.empty((1, VOCAB), device=dev)}
+    eps = 1e-5
+    qkv_n, gu_n = [HIDDEN, KV, KV], [FFN, FFN]
+    F = torch.nn.functional
+
+    def fused():
+        for L in layers:
+            rt.gemv_q4k_tiled_rmsnorm_multi(L["qkv"], L["x"], L["g1"], eps, qkv_n, HIDDEN, ys=L["y_qkv"])
+            rt.gemv_q4k_tiled(L["o"], L["x_o"], HIDDEN, HIDDEN, y=L["y_o"])
+            rt.gemv_q4k_tiled_rmsnorm_multi(L["gu"], L["x"], L["g2"], eps, gu_n, HIDDEN, ys=L["y_gu"])
+            rt.gemv_q4k_tiled_swiglu(L["down"], L["y_gu"][0], L["y_gu"][1], HIDDEN, FFN, y=L["y_d"])
+        rt.gemv_q4k_tiled_rmsnorm_multi([head["w"]], head["x"], head["g"], eps, [VOCAB], HIDDEN, ys=[head["y"]])
+
+    def separate():
+        for L in layers:
+            xn = F.rms_norm(L["x"], (HIDDEN,), L["g1"], eps)
+            rt.gemv_q4k_tiled_multi(L["qkv"], xn, qkv_n, HIDDEN, ys=L["y_qkv"])
+            rt.gemv_q4k_tiled(L["o"], L["x_o"], HIDDEN, HIDDEN, y=L["y_o"])
+            xn = F.rms_norm(L["x"], (HIDDEN,), L["g2"], eps)
+            rt.gemv_q4k_tiled_multi(L["gu"], xn, gu_n, HIDDEN, ys=L["y_gu"])
+            act = F.silu(L["y_gu"][0]) * L["y_gu"][1]
+            rt.gemv_q4k_tiled(L["down"], act, HIDDEN, FFN, y=L["y_d"])
+        xn = F.rms_norm(head["x"], (HIDDEN,), head["g"], eps)
+        rt.gemv_q4k_tiled(head["w"], xn, VOCAB, HIDDEN, y=head["y"])
+
+    ms_f, _ = time_graph(torch, fused, args.warmup, args.steps)
+    ms_s, _ = time_graph(torch, separate, args.warmup, args.steps)
+    log(f"[bench] layer ops fused: {ms_f * 1e3:.1f} us/token; separate torch kernels: {ms_s * 1e3:.1f} us/token")
+    return {"metric": "Llama-3.2-3B pure-Q4_K linear work + RMSNorm/SwiGLU per token, fused into the GEMVs",
+            "value": round(ms_f * 1e3, 2), "unit": "us/token", "higher_is_better": False,
+            "separate_us_per_token": round(ms_s * 1e3, 2), "steps": args.steps, "warmup": args.warmup,
+            "launches_per_token_fused": 4 * LAYERS + 1,
+            "separate": "the same GEMVs with torch's rms_norm, silu and mul kernels between them",
+            "data": "synthetic"}
+
+
 # ------------------------------------------------------ other BASELINE configs --
 
 def bench_single_gemv(args, rt, torch, fmt, n, k, label, copies_bytes=768 << 20):
@@ -411,7 +479,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="llama_decode",
                     choices=["llama_decode", "q4k_gemv", "q4_0_gemv", "bf16_lm_head", "prefill",
-                             "flux"])
+                             "flux", "layer_ops"])
     ap.add_argument("--mix", default="q4km", choices=["q4km", "q4k"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibration-copy-mb", type=int, default=0,
@@ -456,6 +524,8 @@ def main() -> int:
     elif args.workload == "prefill":
         out = bench_gemm(args, rt, torch, [(512, FFN, HIDDEN), (512, FFN, HIDDEN), (512, HIDDEN, FFN)],
                          "config 4 prefill Q4_K GEMM M=512 (gate, up, down)", False)
+    elif args.workload == "layer_ops":
+        out = bench_layer_ops(args, rt, torch)
     elif args.workload == "flux":
         out = bench_gemm(args, rt, torch, [(4608, 9216, 3072), (4608, 12288, 3072), (4608, 3072, 12288)],
                          "config 5 FLUX linears M=4608 (QKV, MLP-in, MLP-out)", True)

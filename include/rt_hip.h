@@ -149,7 +149,9 @@ int rt_hip_gemv_q4k_tiled_bf16(int32_t count, const void* const* tiled, float* c
  * 391-402, sigmoid first, then the product).
  *
  * Outputs match the separate operations followed by rt_hip_gemv_q4k_tiled_multi
- * to f32 rounding (the sum of squares is reduced in a tree, not in sequence).
+ * to f32 rounding: the sum of squares is reduced in a tree, not in sequence,
+ * and the scalar rms_inv multiplies the finished dot product rather than
+ * each activation (equal in exact arithmetic).
  * k % 256 == 0, k <= 8192. */
 int rt_hip_gemv_q4k_tiled_rmsnorm_multi(int32_t count, const void* const* tiled, float* const* y,
                                         const int64_t* n, const float* x, const float* gamma, float eps,

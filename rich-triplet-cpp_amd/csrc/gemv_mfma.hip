@@ -78,6 +78,12 @@ __host__ __device__ inline uint32_t pack_split(int ks, int tpw, int bpw, int cou
 // `aux` is gamma or up.
 enum XOp { kXNone = 0, kXRmsNorm = 1, kXRmsNorm1 = 2, kXSwiGlu = 3 };
 
+// LDS byte offset of the RMSNorm partial sums (one float per wave, after
+// the limb planes and the K-split partial rows).
+__host__ __device__ inline size_t norm_offset(int K, int waves) {
+    return lds_bytes(K) + static_cast<size_t>(waves) * 16 * sizeof(float);
+}
+
 // KS waves split a tile's super-blocks; a workgroup of blockDim.x / 64 waves
 // holds TPW = waves / KS tiles.
 // The arguments every wave needs before its first load come first, as
@@ -207,10 +213,12 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     // alone (XP * nthreads >= K/4, checked by the host), then convert.
     wait_vmcnt<3 * D>();
     if constexpr (XOP == kXRmsNorm || XOP == kXRmsNorm1) {
-        // Sum of squares: per thread, then over the wave (DPP and permlane),
-        // then over the workgroup's waves through LDS (the partial-row area,
-        // free until the loop ends).  Then, as the reference does,
-        // rms_inv = 1 / sqrt(sum * (1/K) + eps) and x * rms_inv * g.
+        // RMSNorm(x) * g = rms_inv * (x * g) with one scalar rms_inv per
+        // launch, so the staged activation is x * g and rms_inv multiplies
+        // the finished dot product: equal in exact arithmetic, and the sum
+        // of squares then needs no barrier of its own.  Per thread, then
+        // over the wave (DPP and permlane); each wave's partial goes to LDS
+        // before the limb barrier below and is summed after it.
         float sq = 0.0f;
 #pragma unroll
         for (int i = 0; i < XP; ++i) {
@@ -218,26 +226,24 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
             sq += (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
         }
         sq = bf16_gemv::wave_sum(sq, lane);
-        float* const part = reinterpret_cast<float*>(lds + lds_bytes(K));
-        if (lane == 0) part[wave] = sq;
-        lds_barrier();
-        float tot = 0.0f;
-        for (int w = 0; w < (nthreads >> 6); ++w) tot += part[w];
-        const float rms_inv = 1.0f / __builtin_sqrtf(tot * (1.0f / static_cast<float>(K)) + eps);
+        if (lane == 0) reinterpret_cast<float*>(lds + norm_offset(K, nthreads >> 6))[wave] = sq;
 #pragma unroll
         for (int i = 0; i < XP; ++i)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float g = XOP == kXRmsNorm1 ? 1.0f + av[i][e] : av[i][e];
-                xv[i][e] = (xv[i][e] * rms_inv) * g;
-            }
+            for (int e = 0; e < 4; ++e) xv[i][e] *= XOP == kXRmsNorm1 ? 1.0f + av[i][e] : av[i][e];
     } else if constexpr (XOP == kXSwiGlu) {
+        // The sigmoid from the hardware exp2 and reciprocal (v_exp_f32,
+        // v_rcp_f32, about 1 ulp each) rather than the correctly rounded
+        // library expf and division, which cost ~30 VALU per value on the
+        // down projection's 8192 inputs.  Then silu = g * sigmoid and times
+        // up, in the reference's order.  Tails: exp overflows to inf for
+        // g < -88 and the sigmoid is 0, as the reference's is.
 #pragma unroll
         for (int i = 0; i < XP; ++i)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float g = xv[i][e];
-                const float sig = 1.0f / (1.0f + expf(-g));
+                const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
                 xv[i][e] = (g * sig) * av[i][e];
             }
     }
@@ -252,6 +258,15 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     }
     if (tid < 4) reinterpret_cast<u32x4*>(lds + 3 * static_cast<size_t>(K))[tid] = u32x4{0u, 0u, 0u, 0u};
     lds_barrier();
+    // rms_inv = 1 / sqrt(sum(x^2) * (1/K) + eps), as the reference forms it
+    // (the sum itself is reduced in a tree).
+    float out_scale = 1.0f;
+    if constexpr (XOP == kXRmsNorm || XOP == kXRmsNorm1) {
+        const float* part = reinterpret_cast<const float*>(lds + norm_offset(K, nthreads >> 6));
+        float tot = 0.0f;
+        for (int w = 0; w < (nthreads >> 6); ++w) tot += part[w];
+        out_scale = 1.0f / __builtin_sqrtf(tot * (1.0f / static_cast<float>(K)) + eps);
+    }
 
     // Steady rounds: straight-line, no branch around the ring's loads (a
     // branch there makes the compiler merge register versions and drain
@@ -282,7 +297,7 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     const Four<uint64_t> ys = {sreg(jobs.y[0]), sreg(jobs.y[1]), sreg(jobs.y[2]), sreg(jobs.y[3])};
     float* const yj = reinterpret_cast<float*>(ys[job]);
     if (KS == 1) {
-        if (lane < 16 && keep) yj[row] = v;
+        if (lane < 16 && keep) yj[row] = XOP == kXRmsNorm || XOP == kXRmsNorm1 ? v * out_scale : v;
     } else {
         float* red = reinterpret_cast<float*>(lds + lds_bytes(K));  // [TPW][KS][16]
         float* rp = red + tslot * KS * 16;
@@ -292,7 +307,7 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
             float s = rp[lane];
 #pragma unroll
             for (int q = 1; q < KS; ++q) s += rp[q * 16 + lane];
-            yj[row] = s;
+            yj[row] = XOP == kXRmsNorm || XOP == kXRmsNorm1 ? s * out_scale : s;
         }
     }
 }
@@ -430,7 +445,9 @@ hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s, 
 }  // namespace
 
 size_t mfma_gemv_lds_bytes(int64_t k, int waves) {
-    return lds_bytes(static_cast<int>(k)) + static_cast<size_t>(waves) * 16 * sizeof(float);
+    // limb planes, the K-split partial rows, then one float per wave for
+    // the RMSNorm partial sums
+    return norm_offset(static_cast<int>(k), waves) + 16 * sizeof(float);
 }
 
 size_t q4k_m1_lds_bytes(int64_t k) { return mfma_gemv_lds_bytes(k, kMaxThreads / kWave); }
