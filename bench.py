@@ -345,13 +345,15 @@ def bench_decode(args, rt, torch):
 # ------------------------------------- layer operations fused into the GEMVs --
 
 def bench_layer_ops(args, rt, torch):
-    """28 pure-Q4_K Llama-3.2-3B layers' linear work with the operations that
-    feed the projections: RMSNorm before q/k/v and before gate/up, SwiGLU
-    before down, a final RMSNorm before the lm_head.  Fused: the norms and
-    the SwiGLU run inside the GEMV launches (4 launches per layer).  Separate:
-    the same operations as torch kernels between the GEMVs (rms_norm, silu,
-    mul).  Attention and the residual adds are outside
-    both.  Weights and inputs are synthetic; the gate/up outputs feed down."""
+    """28 Llama-3.2-3B layers' linear work with the operations that feed the
+    projections: RMSNorm before q/k/v and before gate/up, SwiGLU before
+    down, a final RMSNorm before the lm_head.  Weights follow --mix (the
+    Q4_K_M mix widens v and down to BF16 in the same 14 layers as the decode
+    bench).  Fused: the norms and the SwiGLU run inside the GEMV launches (4
+    launches per layer).  Separate: the same operations as torch kernels
+    between the same GEMVs (rms_norm, silu, mul).  Attention and the residual
+    adds are outside both.  Synthetic weights and inputs; the gate/up
+    outputs feed down."""
     g = torch.Generator(device="cuda").manual_seed(0)
     dev = "cuda"
 
@@ -359,10 +361,16 @@ def bench_layer_ops(args, rt, torch):
         w = torch.randn((n, k), generator=g, device=dev) * 0.02
         return rt.q4k_tile(rt.quantize_q4k(w), n, k)
 
+    def bf16(n, k):
+        return (torch.randn((n, k), generator=g, device=dev) * 0.02).to(torch.bfloat16).view(torch.int16)
+
     layers = []
-    for _ in range(LAYERS):
-        L = {"qkv": [tiled(HIDDEN, HIDDEN), tiled(KV, HIDDEN), tiled(KV, HIDDEN)], "o": tiled(HIDDEN, HIDDEN),
-             "gu": [tiled(FFN, HIDDEN), tiled(FFN, HIDDEN)], "down": tiled(HIDDEN, FFN),
+    for layer in range(LAYERS):
+        wide = args.mix == "q4km" and layer in WIDENED_LAYERS
+        L = {"wide": wide, "qk": [tiled(HIDDEN, HIDDEN), tiled(KV, HIDDEN)],
+             "v": bf16(KV, HIDDEN) if wide else tiled(KV, HIDDEN), "o": tiled(HIDDEN, HIDDEN),
+             "gu": [tiled(FFN, HIDDEN), tiled(FFN, HIDDEN)],
+             "down": bf16(HIDDEN, FFN) if wide else tiled(HIDDEN, FFN),
              "x": torch.randn((1, HIDDEN), generator=g, device=dev),
              "x_o": torch.randn((1, HIDDEN), generator=g, device=dev),
              "g1": 1.0 + 0.1 * torch.randn((HIDDEN,), generator=g, device=dev),
@@ -376,35 +384,51 @@ def bench_layer_ops(args, rt, torch):
             "g": 1.0 + 0.1 * torch.randn((HIDDEN,), generator=g, device=dev),
             "y": torch.empty((1, VOCAB), device=dev)}
     eps = 1e-5
-    qkv_n, gu_n = [HIDDEN, KV, KV], [FFN, FFN]
     F = torch.nn.functional
 
     def fused():
         for L in layers:
-            rt.gemv_q4k_tiled_rmsnorm_multi(L["qkv"], L["x"], L["g1"], eps, qkv_n, HIDDEN, ys=L["y_qkv"])
+            if L["wide"]:
+                rt.gemv_q4k_tiled_bf16_rmsnorm(L["qk"], [HIDDEN, KV], L["v"], KV, L["x"], L["g1"], eps, HIDDEN,
+                                               ys=L["y_qkv"][:2], yb=L["y_qkv"][2])
+            else:
+                rt.gemv_q4k_tiled_rmsnorm_multi(L["qk"] + [L["v"]], L["x"], L["g1"], eps, [HIDDEN, KV, KV],
+                                                HIDDEN, ys=L["y_qkv"])
             rt.gemv_q4k_tiled(L["o"], L["x_o"], HIDDEN, HIDDEN, y=L["y_o"])
-            rt.gemv_q4k_tiled_rmsnorm_multi(L["gu"], L["x"], L["g2"], eps, gu_n, HIDDEN, ys=L["y_gu"])
-            rt.gemv_q4k_tiled_swiglu(L["down"], L["y_gu"][0], L["y_gu"][1], HIDDEN, FFN, y=L["y_d"])
+            rt.gemv_q4k_tiled_rmsnorm_multi(L["gu"], L["x"], L["g2"], eps, [FFN, FFN], HIDDEN, ys=L["y_gu"])
+            if L["wide"]:
+                rt.gemv_bf16_swiglu(L["down"], L["y_gu"][0], L["y_gu"][1], HIDDEN, FFN, y=L["y_d"])
+            else:
+                rt.gemv_q4k_tiled_swiglu(L["down"], L["y_gu"][0], L["y_gu"][1], HIDDEN, FFN, y=L["y_d"])
         rt.gemv_q4k_tiled_rmsnorm_multi([head["w"]], head["x"], head["g"], eps, [VOCAB], HIDDEN, ys=[head["y"]])
 
     def separate():
         for L in layers:
             xn = F.rms_norm(L["x"], (HIDDEN,), L["g1"], eps)
-            rt.gemv_q4k_tiled_multi(L["qkv"], xn, qkv_n, HIDDEN, ys=L["y_qkv"])
+            if L["wide"]:
+                rt.gemv_q4k_tiled_bf16(L["qk"], [HIDDEN, KV], L["v"], KV, xn, HIDDEN, ys=L["y_qkv"][:2],
+                                       yb=L["y_qkv"][2])
+            else:
+                rt.gemv_q4k_tiled_multi(L["qk"] + [L["v"]], xn, [HIDDEN, KV, KV], HIDDEN, ys=L["y_qkv"])
             rt.gemv_q4k_tiled(L["o"], L["x_o"], HIDDEN, HIDDEN, y=L["y_o"])
             xn = F.rms_norm(L["x"], (HIDDEN,), L["g2"], eps)
-            rt.gemv_q4k_tiled_multi(L["gu"], xn, gu_n, HIDDEN, ys=L["y_gu"])
+            rt.gemv_q4k_tiled_multi(L["gu"], xn, [FFN, FFN], HIDDEN, ys=L["y_gu"])
             act = F.silu(L["y_gu"][0]) * L["y_gu"][1]
-            rt.gemv_q4k_tiled(L["down"], act, HIDDEN, FFN, y=L["y_d"])
+            if L["wide"]:
+                rt.gemv(rt.BF16, L["down"], act, HIDDEN, FFN, y=L["y_d"])
+            else:
+                rt.gemv_q4k_tiled(L["down"], act, HIDDEN, FFN, y=L["y_d"])
         xn = F.rms_norm(head["x"], (HIDDEN,), head["g"], eps)
         rt.gemv_q4k_tiled(head["w"], xn, VOCAB, HIDDEN, y=head["y"])
 
     ms_f, _ = time_graph(torch, fused, args.warmup, args.steps)
     ms_s, _ = time_graph(torch, separate, args.warmup, args.steps)
-    log(f"[bench] layer ops fused: {ms_f * 1e3:.1f} us/token; separate torch kernels: {ms_s * 1e3:.1f} us/token")
-    return {"metric": "Llama-3.2-3B pure-Q4_K linear work + RMSNorm/SwiGLU per token, fused into the GEMVs",
+    log(f"[bench] layer ops fused ({args.mix}): {ms_f * 1e3:.1f} us/token; "
+        f"separate torch kernels: {ms_s * 1e3:.1f} us/token")
+    return {"metric": "Llama-3.2-3B linear work + RMSNorm/SwiGLU per token, fused into the GEMVs",
             "value": round(ms_f * 1e3, 2), "unit": "us/token", "higher_is_better": False,
             "separate_us_per_token": round(ms_s * 1e3, 2), "steps": args.steps, "warmup": args.warmup,
+            "weights": "Q4_K_M mix" if args.mix == "q4km" else "pure Q4_K",
             "launches_per_token_fused": 4 * LAYERS + 1,
             "separate": "the same GEMVs with torch's rms_norm, silu and mul kernels between them",
             "data": "synthetic"}

@@ -158,6 +158,16 @@ int rt_hip_gemv_q4k_tiled_rmsnorm_multi(int32_t count, const void* const* tiled,
                                         int32_t gemma3, int64_t k, rt_hip_stream stream);
 int rt_hip_gemv_q4k_tiled_swiglu(const void* tiled, const float* gate, const float* up, float* y, int64_t n,
                                  int64_t k, rt_hip_stream stream);
+/* The same two operations for the BF16-widened projections of a Q4_K_M
+ * model (src/transformer4_load.cpp:141-143): q/k (tiled Q4_K) and a BF16 v
+ * on RMSNorm(x) in one launch, as rt_hip_gemv_q4k_tiled_bf16; and a BF16
+ * down on silu(gate) * up, as rt_hip_gemv_bf16 at m = 1. */
+int rt_hip_gemv_q4k_tiled_bf16_rmsnorm(int32_t count, const void* const* tiled, float* const* y,
+                                       const int64_t* n, const uint16_t* w_bf16, float* y_bf16, int64_t n_bf16,
+                                       const float* x, const float* gamma, float eps, int32_t gemma3, int64_t k,
+                                       rt_hip_stream stream);
+int rt_hip_gemv_bf16_swiglu(const uint16_t* w, const float* gate, const float* up, float* y, int64_t n, int64_t k,
+                            rt_hip_stream stream);
 
 /* ---- decode chain: a step's dependent GEMV stages in one launch -----------
  * Replace: MetalDecodeContext::create / decode_step, the per-token sequence

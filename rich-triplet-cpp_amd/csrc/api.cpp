@@ -294,6 +294,46 @@ int rt_hip_gemv_q4k_tiled_swiglu(const void* tiled, const float* gate, const flo
     return gemv_xop("rt_hip_gemv_q4k_tiled_swiglu", 3, 1, &tiled, &y, &n, gate, up, 0.0f, k, stream);
 }
 
+int rt_hip_gemv_q4k_tiled_bf16_rmsnorm(int32_t count, const void* const* tiled, float* const* y,
+                                       const int64_t* n, const uint16_t* w_bf16, float* y_bf16, int64_t n_bf16,
+                                       const float* x, const float* gamma, float eps, int32_t gemma3, int64_t k,
+                                       rt_hip_stream stream) {
+    const char* fn = "rt_hip_gemv_q4k_tiled_bf16_rmsnorm";
+    if (count < 1 || count > RT_HIP_MULTI_MAX || !tiled || !y || !n)
+        return fail(RT_HIP_E_ARG, std::string(fn) + ": count must be in [1, 4] with arrays");
+    for (int32_t j = 0; j < count; ++j) {
+        int rc = gemv_args(fn, tiled[j], x, y[j], n[j], k, 1, 256);
+        if (rc) return rc;
+    }
+    int rc = gemv_args(fn, w_bf16, x, y_bf16, n_bf16, k, 1, 256);
+    if (rc) return rc;
+    if (!gamma) return fail(RT_HIP_E_ARG, std::string(fn) + ": null gamma");
+    if (!aligned16(gamma)) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": gamma must be 16-byte aligned");
+    if (!(eps >= 0.0f)) return fail(RT_HIP_E_ARG, std::string(fn) + ": eps must be >= 0");
+    if (k > 8192 || q4k_bf16_fused_lds_bytes(k) > 65536)
+        return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 8192");
+    hipError_t e;
+    if (!state_for_current(&e)) return hip_fail(e, fn);
+    return check_stream_launch(launch_gemv_q4k_bf16_fused(count, tiled, y, n, w_bf16, y_bf16, n_bf16, x, k,
+                                                          static_cast<hipStream_t>(stream), gemma3 ? 2 : 1, gamma,
+                                                          eps),
+                               fn);
+}
+
+int rt_hip_gemv_bf16_swiglu(const uint16_t* w, const float* gate, const float* up, float* y, int64_t n, int64_t k,
+                            rt_hip_stream stream) {
+    const char* fn = "rt_hip_gemv_bf16_swiglu";
+    int rc = gemv_args(fn, w, gate, y, n, k, 1, 256);
+    if (rc) return rc;
+    if (!up) return fail(RT_HIP_E_ARG, std::string(fn) + ": null up");
+    if (!aligned16(up)) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": up must be 16-byte aligned");
+    if (k > 8192) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 8192");
+    hipError_t e;
+    if (!state_for_current(&e)) return hip_fail(e, fn);
+    return check_stream_launch(launch_gemv_bf16_xop(3, w, gate, up, 0.0f, y, n, k, static_cast<hipStream_t>(stream)),
+                               fn);
+}
+
 int rt_hip_gemv_q4k_tiled_bf16(int32_t count, const void* const* tiled, float* const* y,
                                const int64_t* n, const uint16_t* w_bf16, float* y_bf16,
                                int64_t n_bf16, const float* x, int64_t k, rt_hip_stream stream) {

@@ -16,6 +16,16 @@ __global__ __launch_bounds__(T) void k_gemv_bf16(const uint16_t* __restrict__ W,
     rows<D, XP, ARGMAX, T>(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), W, X, Y, N, K, key, lds);
 }
 
+// The same with a layer operation applied to x while it is staged (XOp).
+template <int D, int XP, int T, int XOP>
+__global__ __launch_bounds__(T) void k_gemv_bf16_xop(const uint16_t* __restrict__ W, const float* __restrict__ X,
+                                                    const float* __restrict__ aux, float* __restrict__ Y, int N,
+                                                    int K, float eps) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    rows<D, XP, false, T, XOP>(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), W, X, Y, N, K, nullptr,
+                               lds, aux, eps);
+}
+
 // T threads per workgroup, each wave looping over its rows; x is prefetched into registers before the
 // weight prologue when XP * T covers K / 4 (else the rest is copied after).
 template <bool ARGMAX, int T>
@@ -60,6 +70,39 @@ size_t bf16_m1_lds_bytes(int64_t k) { return bf16_gemv::lds_bytes(k); }
 hipError_t launch_gemv_bf16_m1(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
                                uint64_t* key, hipStream_t s) {
     return key ? run_rows<true>(w, x, y, n, k, key, s) : run_rows<false>(w, x, y, n, k, key, s);
+}
+
+namespace {
+// The default launch shape of run() (8 waves), with an x operation.
+template <int XOP>
+hipError_t run_xop(const uint16_t* w, const float* x, const float* aux, float eps, float* y, int64_t n, int64_t k,
+                   hipStream_t s) {
+    constexpr int T = 512;
+    const int64_t waves = T / kWave, pieces = (k + kPiece - 1) / kPiece;
+    const int64_t rpw = pieces <= 3 ? 4 : (pieces >= 12 ? 2 : 1);
+    const int64_t wgs = (n + waves * rpw - 1) / (waves * rpw);
+    const int64_t per = (k / 4 + T - 1) / T;
+    const dim3 g(static_cast<unsigned>(wgs)), b(T);
+    const size_t lds = bf16_m1_lds_bytes(k);
+    const int ik = static_cast<int>(k), in = static_cast<int>(n);
+    if (per <= 2)
+        hipLaunchKernelGGL((k_gemv_bf16_xop<8, 2, T, XOP>), g, b, lds, s, w, x, aux, y, in, ik, eps);
+    else if (per <= 4)
+        hipLaunchKernelGGL((k_gemv_bf16_xop<8, 4, T, XOP>), g, b, lds, s, w, x, aux, y, in, ik, eps);
+    else
+        hipLaunchKernelGGL((k_gemv_bf16_xop<8, 8, T, XOP>), g, b, lds, s, w, x, aux, y, in, ik, eps);
+    return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_gemv_bf16_xop(int xop, const uint16_t* w, const float* x, const float* aux, float eps, float* y,
+                                int64_t n, int64_t k, hipStream_t s) {
+    switch (xop) {
+        case kXRmsNorm: return run_xop<kXRmsNorm>(w, x, aux, eps, y, n, k, s);
+        case kXRmsNorm1: return run_xop<kXRmsNorm1>(w, x, aux, eps, y, n, k, s);
+        case kXSwiGlu: return run_xop<kXSwiGlu>(w, x, aux, eps, y, n, k, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace rt_hip

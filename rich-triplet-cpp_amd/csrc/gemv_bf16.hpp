@@ -25,6 +25,28 @@
 #include "rt_common.hpp"
 
 namespace rt_hip {
+
+// What a decode GEMV applies to its activation while staging it (the layer
+// operations either side of the projection, fused into its launch):
+//   kXNone     x as given;
+//   kXRmsNorm  RMSNorm(x) * gamma            (tensor_node.cpp:320-344, 383);
+//   kXRmsNorm1 RMSNorm(x) * (1 + gamma)      (the Gemma 3 form, :387);
+//   kXSwiGlu   silu(gate) * up, x = gate     (tensor_node.cpp:391-402,
+//              transformer5.cpp:186-190).
+// `aux` is gamma or up.  RMSNorm(x) * g = rms_inv * (x * g) with one scalar
+// rms_inv per vector, so kernels stage x * g and scale the finished dot
+// products by rms_inv (equal in exact arithmetic); the sum of squares is
+// reduced per wave and across waves through LDS at the staging barrier.
+enum XOp { kXNone = 0, kXRmsNorm = 1, kXRmsNorm1 = 2, kXSwiGlu = 3 };
+
+// silu(g) * u in the reference's order, the sigmoid from the hardware exp2
+// and reciprocal (about 1 ulp each; exp overflows to inf for g < -88 and
+// the sigmoid is then 0, as the reference's is).
+__device__ __forceinline__ float swiglu1(float g, float u) {
+    const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
+    return (g * sig) * u;
+}
+
 namespace bf16_gemv {
 
 constexpr int kThreads = 256;  // default workgroup: 4 waves
@@ -38,6 +60,13 @@ __device__ __forceinline__ uint32_t x_off(int f) {
     const int i = f >> 7, l = (f >> 1) & 63, h = f & 1;
     return static_cast<uint32_t>((((i << 1) + h) << 6) + l) << 4;
 }
+
+// Staged x (zero-padded to whole pieces), then one float per wave (up to
+// 16) for the RMSNorm partial sums.
+__host__ __device__ inline size_t x_bytes(int64_t k) {
+    return static_cast<size_t>((k + kPiece - 1) / kPiece) * kPiece * sizeof(float);
+}
+__host__ __device__ inline size_t lds_bytes(int64_t k) { return x_bytes(k) + 16 * sizeof(float); }
 
 // Workgroup `blk` of `nblk` T-thread workgroups; `lds` holds lds_bytes(K).
 // Wave gw = blk * (T / 64) + wave of the NW = nblk * (T / 64) waves takes
@@ -65,10 +94,13 @@ __device__ __forceinline__ float wave_sum(float v, int lane) {
     return v;
 }
 
-template <int D, int XP, bool ARGMAX, int T = kThreads>
+template <int D, int XP, bool ARGMAX, int T = kThreads, int XOP = kXNone>
 __device__ __forceinline__ void rows(int blk, int nblk, const uint16_t* __restrict__ W,
                                      const float* __restrict__ X, float* __restrict__ Y, int N, int K,
-                                     uint64_t* __restrict__ key, uint8_t* lds) {
+                                     uint64_t* __restrict__ key, uint8_t* lds,
+                                     const float* __restrict__ aux = nullptr, float eps = 0.0f) {
+    static_assert(XOP == kXNone || !ARGMAX, "x operations run without the argmax epilogue");
+    constexpr bool kNorm = XOP == kXRmsNorm || XOP == kXRmsNorm1;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int P = (K + kPiece - 1) / kPiece;  // pieces per row (the last may be partial)
@@ -76,11 +108,19 @@ __device__ __forceinline__ void rows(int blk, int nblk, const uint16_t* __restri
     const int kx4 = K >> 2;                   // f32x4 of x (K % 8 == 0)
     const f32x4* X4 = reinterpret_cast<const f32x4*>(X);
 
-    f32x4 xv[XP];
+    const f32x4* A4 = reinterpret_cast<const f32x4*>(aux);
+    f32x4 xv[XP], av[XP];
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
         const int f = tid + T * i;
         xv[i] = X4[f < kx4 ? f : 0];
+    }
+    if constexpr (XOP != kXNone) {
+#pragma unroll
+        for (int i = 0; i < XP; ++i) {
+            const int f = tid + T * i;
+            av[i] = A4[f < kx4 ? f : 0];
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -109,18 +149,44 @@ __device__ __forceinline__ void rows(int blk, int nblk, const uint16_t* __restri
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // Stage x (zeros past K, up to the whole last piece).
+    // Stage x (zeros past K, up to the whole last piece), with the x
+    // operation applied.
+    float sq = 0.0f;
+    auto op = [&](f32x4 v, f32x4 a) {
+        if constexpr (kNorm) {
+            sq += (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] *= XOP == kXRmsNorm1 ? 1.0f + a[e] : a[e];
+        } else if constexpr (XOP == kXSwiGlu) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = swiglu1(v[e], a[e]);
+        }
+        return v;
+    };
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
         const int f = tid + T * i;
         const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (f < nx4) *reinterpret_cast<f32x4*>(lds + x_off(f)) = f < kx4 ? xv[i] : z;
+        if (f < nx4) *reinterpret_cast<f32x4*>(lds + x_off(f)) = f < kx4 ? op(xv[i], av[i]) : z;
     }
     for (int f = tid + T * XP; f < nx4; f += T) {
         const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-        *reinterpret_cast<f32x4*>(lds + x_off(f)) = f < kx4 ? X4[f] : z;
+        f32x4 a = z;
+        if constexpr (XOP != kXNone) a = f < kx4 ? A4[f] : z;
+        *reinterpret_cast<f32x4*>(lds + x_off(f)) = f < kx4 ? op(X4[f], a) : z;
+    }
+    float* const part = reinterpret_cast<float*>(lds + x_bytes(K));
+    if constexpr (kNorm) {
+        sq = wave_sum(sq, lane);
+        if (lane == 0) part[wave] = sq;
     }
     lds_barrier();
+    float out_scale = 1.0f;
+    if constexpr (kNorm) {
+        float tot = 0.0f;
+        for (int w = 0; w < T / kWave; ++w) tot += part[w];
+        out_scale = 1.0f / __builtin_sqrtf(tot * (1.0f / static_cast<float>(K)) + eps);
+    }
 
     // Values 8l .. 8l+7 of a piece: dword e holds values 2e (low half) and
     // 2e + 1 (high half).  A row's sum stays with lane cr of the wave.
@@ -176,16 +242,13 @@ __device__ __forceinline__ void rows(int blk, int nblk, const uint16_t* __restri
         if (i + j < L) RT_BF16_CONSUME(ring[j]);
 #undef RT_BF16_CONSUME
 
-    if (lane < R) Yg[gw + lane * NW] = res;
+    if (lane < R) Yg[gw + lane * NW] = kNorm ? res * out_scale : res;
     if constexpr (ARGMAX) {
         if (lane == 0 && best != 0)
             atomicMax(reinterpret_cast<unsigned long long*>(key), static_cast<unsigned long long>(best));
     }
 }
 
-__host__ __device__ inline size_t lds_bytes(int64_t k) {
-    return static_cast<size_t>((k + kPiece - 1) / kPiece) * kPiece * sizeof(float);
-}
 
 }  // namespace bf16_gemv
 }  // namespace rt_hip

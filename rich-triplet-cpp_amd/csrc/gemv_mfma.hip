@@ -68,15 +68,7 @@ __host__ __device__ inline uint32_t pack_split(int ks, int tpw, int bpw, int cou
            (static_cast<uint32_t>((4096 + ks - 1) / ks) << 16) | (static_cast<uint32_t>(count) << 29);
 }
 
-// What the kernel applies to the activation while staging it (the layer
-// operations either side of a decode GEMV, fused into its launch):
-//   kXNone     x as given;
-//   kXRmsNorm  RMSNorm(x) * gamma            (tensor_node.cpp:320-344, 383);
-//   kXRmsNorm1 RMSNorm(x) * (1 + gamma)      (the Gemma 3 form, :387);
-//   kXSwiGlu   silu(gate) * up, x = gate     (tensor_node.cpp:391-402,
-//              transformer5.cpp:186-190).
-// `aux` is gamma or up.
-enum XOp { kXNone = 0, kXRmsNorm = 1, kXRmsNorm1 = 2, kXSwiGlu = 3 };
+// The x operations (XOp) are declared with the BF16 body (gemv_bf16.hpp).
 
 // LDS byte offset of the RMSNorm partial sums (one float per wave, after
 // the limb planes and the K-split partial rows).
@@ -241,11 +233,7 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
 #pragma unroll
         for (int i = 0; i < XP; ++i)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float g = xv[i][e];
-                const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
-                xv[i][e] = (g * sig) * av[i][e];
-            }
+            for (int e = 0; e < 4; ++e) xv[i][e] = swiglu1(xv[i][e], av[i][e]);
     }
     // Every lane converts its values (past the end: a dummy that is not
     // stored; the 8-lane reductions need the whole group).  No branch may
@@ -336,17 +324,18 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_xop(
 // workgroups run the tiled Q4_K GEMVs, the rest the BF16 rows, all on the
 // same x.  One launch instead of two dependent ones; each workgroup's work is
 // exactly that of the separate kernels (4 waves per workgroup on both sides).
-template <int XPQ, bool J34, int XPB>
+template <int XPQ, bool J34, int XPB, int XOP = kXNone>
 __global__ __launch_bounds__(bf16_gemv::kThreads) void k_gemv_q4k_bf16(
-    const float* __restrict__ X, int K, uint32_t split, int nthreads, const uint8_t* w0, const uint8_t* w1,
-    int n0, int n1, int tile1, int q4k_wgs, const uint16_t* __restrict__ wb, float* __restrict__ yb,
-    int nb_rows, const Jobs jobs) {
+    const float* __restrict__ X, const float* __restrict__ aux, int K, uint32_t split, int nthreads,
+    const uint8_t* w0, const uint8_t* w1, int n0, int n1, int tile1, int q4k_wgs, const uint16_t* __restrict__ wb,
+    float* __restrict__ yb, int nb_rows, const Jobs jobs, float eps) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int blk = static_cast<int>(blockIdx.x);
     if (blk < q4k_wgs)
-        q4k_tiles<4, XPQ, true, J34>(blk, X, K, split, nthreads, w0, w1, n0, n1, tile1, jobs, lds);
+        q4k_tiles<4, XPQ, true, J34, XOP>(blk, X, K, split, nthreads, w0, w1, n0, n1, tile1, jobs, lds, aux, eps);
     else
-        bf16_gemv::rows<8, XPB, false>(blk - q4k_wgs, (nb_rows + 3) / 4, wb, X, yb, nb_rows, K, nullptr, lds);
+        bf16_gemv::rows<8, XPB, false, bf16_gemv::kThreads, XOP>(blk - q4k_wgs, (nb_rows + 3) / 4, wb, X, yb,
+                                                                 nb_rows, K, nullptr, lds, aux, eps);
 }
 
 // The x operation, its second vector and eps (XOp).
@@ -509,16 +498,37 @@ hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* co
 
 namespace {
 
-template <int XPQ, bool J34, int XPB>
+template <int XPQ, bool J34, int XPB, int XOP>
 hipError_t run_fused(const Jobs& jobs, int ks, int q4k_wgs, const uint16_t* wb, float* yb, int64_t nb_rows,
-                     const float* x, int64_t k, size_t lds, hipStream_t s) {
+                     const float* x, const XArgs& xa, int64_t k, size_t lds, hipStream_t s) {
     const int64_t bwgs = (nb_rows + 3) / 4;  // one row per wave, 4 waves
-    hipLaunchKernelGGL((k_gemv_q4k_bf16<XPQ, J34, XPB>), dim3(static_cast<unsigned>(q4k_wgs + bwgs)),
-                       dim3(bf16_gemv::kThreads), lds, s, x, static_cast<int>(k),
+    hipLaunchKernelGGL((k_gemv_q4k_bf16<XPQ, J34, XPB, XOP>), dim3(static_cast<unsigned>(q4k_wgs + bwgs)),
+                       dim3(bf16_gemv::kThreads), lds, s, x, xa.aux, static_cast<int>(k),
                        pack_split(ks, 4 / ks, static_cast<int>((k / 256 + ks - 1) / ks), jobs.count),
                        bf16_gemv::kThreads, jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], q4k_wgs, wb, yb,
-                       static_cast<int>(nb_rows), jobs);
+                       static_cast<int>(nb_rows), jobs, xa.eps);
     return hipGetLastError();
+}
+
+template <int XOP>
+hipError_t fused_xp(const Jobs& jobs, int ks, int q4k_wgs, const uint16_t* wb, float* yb, int64_t nb_rows,
+                    const float* x, const XArgs& xa, int64_t k, size_t lds, hipStream_t s) {
+    const bool j34 = jobs.count > 2;
+    const int64_t per = (k / 4 + 255) / 256;  // f32x4 of x per thread
+    if (k <= 4096) {
+        if (per <= 2)
+            return j34 ? run_fused<2, true, 4, XOP>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s)
+                       : run_fused<2, false, 4, XOP>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
+        if (per <= 3)
+            return j34 ? run_fused<3, true, 4, XOP>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s)
+                       : run_fused<3, false, 4, XOP>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
+        return j34 ? run_fused<4, true, 4, XOP>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s)
+                   : run_fused<4, false, 4, XOP>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
+    }
+    if (per <= 8)
+        return j34 ? run_fused<8, true, 8, XOP>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s)
+                   : run_fused<8, false, 8, XOP>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
@@ -530,7 +540,7 @@ size_t q4k_bf16_fused_lds_bytes(int64_t k) {
 
 hipError_t launch_gemv_q4k_bf16_fused(int count, const void* const* w, float* const* y, const int64_t* n,
                                       const uint16_t* wb, float* yb, int64_t nb_rows, const float* x,
-                                      int64_t k, hipStream_t s) {
+                                      int64_t k, hipStream_t s, int xop, const float* aux, float eps) {
     if (count < 1 || count > kMaxJobs || k > 8192) return hipErrorInvalidValue;
     Jobs jobs{};
     jobs.count = count;
@@ -562,22 +572,15 @@ hipError_t launch_gemv_q4k_bf16_fused(int count, const void* const* w, float* co
     const int tpw = 4 / ks;
     const int q4k_wgs = static_cast<int>((tiles + tpw - 1) / tpw);
     const size_t lds = q4k_bf16_fused_lds_bytes(k);
-    const bool j34 = count > 2;
-    const int64_t per = (k / 4 + 255) / 256;  // f32x4 of x per thread
-    if (k <= 4096) {
-        if (per <= 2)
-            return j34 ? run_fused<2, true, 4>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s)
-                       : run_fused<2, false, 4>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s);
-        if (per <= 3)
-            return j34 ? run_fused<3, true, 4>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s)
-                       : run_fused<3, false, 4>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s);
-        return j34 ? run_fused<4, true, 4>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s)
-                   : run_fused<4, false, 4>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s);
+    XArgs xa;
+    xa.aux = aux;
+    xa.eps = eps;
+    switch (xop) {
+        case kXNone: return fused_xp<kXNone>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
+        case kXRmsNorm: return fused_xp<kXRmsNorm>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
+        case kXRmsNorm1: return fused_xp<kXRmsNorm1>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
+        default: return hipErrorInvalidValue;
     }
-    if (per <= 8)
-        return j34 ? run_fused<8, true, 8>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s)
-                   : run_fused<8, false, 8>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, k, lds, s);
-    return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv_q4k_mfma(const void* w, const float* x, float* y, int64_t n, int64_t k,

@@ -43,6 +43,10 @@ hipError_t launch_gemv_q4k_mfma(const void* w, const float* x, float* y, int64_t
                                 hipStream_t s);
 // Up to four M = 1 Q4_K GEMVs sharing x, K; `tiled`: the weights are in the
 // tiled layout (q4k_mfma.hpp) rather than reference row-major blocks.
+// M = 1 BF16 GEMV with a layer operation applied to x while it is staged
+// (xop as below), k <= 8192.
+hipError_t launch_gemv_bf16_xop(int xop, const uint16_t* w, const float* x, const float* aux, float eps, float* y,
+                                int64_t n, int64_t k, hipStream_t s);
 // Tiled Q4_K GEMVs sharing x, with a layer operation applied to x while it
 // is staged: xop 1 RMSNorm * gamma, 2 RMSNorm * (1 + gamma), 3 silu(x) * aux
 // (aux = gamma or up; eps for the norms).
@@ -59,9 +63,12 @@ hipError_t launch_q4k_tile(const void* blocks, void* tiled, int64_t n, int64_t k
 // Up to four tiled-Q4_K GEMVs and one BF16 GEMV sharing x (K <= 8192) in one
 // launch; LDS: q4k_bf16_fused_lds_bytes(k).
 size_t q4k_bf16_fused_lds_bytes(int64_t k);
+// xop: kXNone, or an RMSNorm form (1, 2) with gamma in aux, applied on both
+// sides of the launch.
 hipError_t launch_gemv_q4k_bf16_fused(int count, const void* const* w, float* const* y, const int64_t* n,
                                       const uint16_t* wb, float* yb, int64_t nb_rows, const float* x,
-                                      int64_t k, hipStream_t s);
+                                      int64_t k, hipStream_t s, int xop = 0, const float* aux = nullptr,
+                                      float eps = 0.0f);
 
 // Persistent decode chain (chain.hip).  The host builds the stage table with
 // chain_fill_stage (chain_stage_bytes() each) in device memory and a zeroed

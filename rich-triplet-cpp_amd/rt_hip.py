@@ -44,6 +44,9 @@ _SIGNATURES = {
     "rt_hip_gemv_q4k_tiled_rmsnorm_multi": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp,
                                             C.c_float, _i32, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_swiglu": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
+    "rt_hip_gemv_q4k_tiled_bf16_rmsnorm": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp, _i64,
+                                           _vp, _vp, C.c_float, _i32, _i64, _vp],
+    "rt_hip_gemv_bf16_swiglu": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_dequant_q6k_bf16": [_vp, _vp, _i64, _i64, _vp],
     "rt_hip_q6k_tile": [_vp, _vp, _i64, _i64, _vp],
     "rt_hip_gemv_q6k_tiled": [_vp, _vp, _vp, _i64, _i64, _vp],
@@ -281,6 +284,34 @@ def gemv_q4k_tiled_swiglu(w, gate, up, n: int, k: int, y=None, stream=None):
         y = torch.empty((1, n), dtype=torch.float32, device=gate.device)
     _dev_check(w, gate, up, y)
     library().call("rt_hip_gemv_q4k_tiled_swiglu", _ptr(w), _ptr(gate), _ptr(up), _ptr(y), n, k, _stream(stream))
+    return y
+
+
+def gemv_q4k_tiled_bf16_rmsnorm(ws, ns, wb, nb: int, x, gamma, eps: float, k: int, gemma3: bool = False,
+                                ys=None, yb=None, stream=None):
+    """gemv_q4k_tiled_bf16 on RMSNorm(x) (gamma, or 1 + gamma for gemma3)."""
+    torch = _torch()
+    count = len(ws)
+    if ys is None:
+        ys = [torch.empty((1, n), dtype=torch.float32, device=x.device) for n in ns]
+    if yb is None:
+        yb = torch.empty((1, nb), dtype=torch.float32, device=x.device)
+    _dev_check(x, gamma, wb, yb, *ws, *ys)
+    wp = (_vp * count)(*[w.data_ptr() for w in ws])
+    yp = (_vp * count)(*[y.data_ptr() for y in ys])
+    npp = (_i64 * count)(*ns)
+    library().call("rt_hip_gemv_q4k_tiled_bf16_rmsnorm", count, wp, yp, npp, _ptr(wb), _ptr(yb), nb, _ptr(x),
+                   _ptr(gamma), C.c_float(eps), 1 if gemma3 else 0, k, _stream(stream))
+    return ys, yb
+
+
+def gemv_bf16_swiglu(w, gate, up, n: int, k: int, y=None, stream=None):
+    """y = W . (silu(gate) * up) for a BF16 weight [n, k] (int16 bits)."""
+    torch = _torch()
+    if y is None:
+        y = torch.empty((1, n), dtype=torch.float32, device=gate.device)
+    _dev_check(w, gate, up, y)
+    library().call("rt_hip_gemv_bf16_swiglu", _ptr(w), _ptr(gate), _ptr(up), _ptr(y), n, k, _stream(stream))
     return y
 
 

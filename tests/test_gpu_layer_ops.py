@@ -85,3 +85,33 @@ def test_layer_ops_reject_bad_arguments(rt):
                       16, 16384, None) == E_SHAPE
     assert lib.status("rt_hip_gemv_q4k_tiled_swiglu", t.data_ptr(), x.data_ptr(), None, y.data_ptr(),
                       16, 256, None) == E_ARG
+
+
+def test_rmsnorm_fused_qk_plus_bf16_v(rt, orc):
+    """A widened layer's q/k (Q4_K) and BF16 v on RMSNorm(x), one launch."""
+    k, ns, nb = 3072, [3072, 1024], 1024
+    say(f"[rmsnorm q/k + bf16 v] K={k}")
+    rng = np.random.default_rng(21)
+    blocks = _weights(orc, rng, ns, k)
+    wv = orc.f32_to_bf16_n((rng.standard_normal((nb, k)) * 0.02).astype(np.float32))
+    x = (rng.standard_normal(k) * 2).astype(np.float32)
+    gamma = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    tiled = [rt.q4k_tile(to_dev(b), n, k) for b, n in zip(blocks, ns)]
+    ys, yb = rt.gemv_q4k_tiled_bf16_rmsnorm(tiled, ns, to_dev(wv.view(np.int16)), nb, to_dev(x), to_dev(gamma),
+                                            1e-5, k)
+    xn = orc.rmsnorm(x, gamma, 1e-5).reshape(1, k)
+    for b, n, y in zip(blocks, ns, ys):
+        assert normwise_err(from_dev(y), orc.q4k_matmul_t(b, n, k, xn)) <= GEMV_TOL
+    assert normwise_err(from_dev(yb), orc.bf16_matmul_t(wv, xn)) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("n,k", [(3072, 8192), (100, 512)])
+def test_bf16_swiglu(rt, orc, n, k):
+    say(f"[bf16 swiglu] N={n} K={k}")
+    rng = np.random.default_rng(n + k + 5)
+    w = orc.f32_to_bf16_n((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    gate = (rng.standard_normal(k) * 2).astype(np.float32)
+    up = rng.standard_normal(k).astype(np.float32)
+    got = from_dev(rt.gemv_bf16_swiglu(to_dev(w.view(np.int16)), to_dev(gate), to_dev(up), n, k))
+    act = orc.swiglu(gate, up).reshape(1, k)
+    assert normwise_err(got, orc.bf16_matmul_t(w, act)) <= GEMV_TOL
