@@ -309,12 +309,13 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
                                  lds);
 }
 
-// The same with a layer operation applied to x while it is staged (XOp);
-// aux (gamma or up) is preloaded with the other pointers.
+// The same with a layer operation applied to x while it is staged (XOp).
+// Pointers first, then the 32-bit arguments: no padding, so all fourteen
+// leading dwords (aux, gamma or up, included) are preloaded.
 template <int XP, bool J34, int XOP>
 __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_xop(
-    const float* __restrict__ X, const float* __restrict__ aux, int K, uint32_t split, int nthreads,
-    const uint8_t* w0, const uint8_t* w1, int n0, int n1, int tile1, const Jobs jobs, float eps) {
+    const float* __restrict__ X, const float* __restrict__ aux, const uint8_t* w0, const uint8_t* w1, int K,
+    uint32_t split, int nthreads, int n0, int n1, int tile1, const Jobs jobs, float eps) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     q4k_tiles<4, XP, true, J34, XOP>(static_cast<int>(blockIdx.x), X, K, split, nthreads, w0, w1, n0, n1, tile1,
                                      jobs, lds, aux, eps);
@@ -324,15 +325,19 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_xop(
 // workgroups run the tiled Q4_K GEMVs, the rest the BF16 rows, all on the
 // same x.  One launch instead of two dependent ones; each workgroup's work is
 // exactly that of the separate kernels (4 waves per workgroup on both sides).
+// Pointers first, then the 32-bit arguments, so the fourteen preloaded
+// dwords hold everything a Q4_K workgroup needs before its first loads
+// (the block size is the compile-time bf16_gemv::kThreads).
 template <int XPQ, bool J34, int XPB, int XOP = kXNone>
 __global__ __launch_bounds__(bf16_gemv::kThreads) void k_gemv_q4k_bf16(
-    const float* __restrict__ X, const float* __restrict__ aux, int K, uint32_t split, int nthreads,
-    const uint8_t* w0, const uint8_t* w1, int n0, int n1, int tile1, int q4k_wgs, const uint16_t* __restrict__ wb,
-    float* __restrict__ yb, int nb_rows, const Jobs jobs, float eps) {
+    const float* __restrict__ X, const float* __restrict__ aux, const uint8_t* w0, const uint8_t* w1, int K,
+    uint32_t split, int q4k_wgs, int n0, int n1, int tile1, const uint16_t* __restrict__ wb, float* __restrict__ yb,
+    int nb_rows, const Jobs jobs, float eps) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int blk = static_cast<int>(blockIdx.x);
     if (blk < q4k_wgs)
-        q4k_tiles<4, XPQ, true, J34, XOP>(blk, X, K, split, nthreads, w0, w1, n0, n1, tile1, jobs, lds, aux, eps);
+        q4k_tiles<4, XPQ, true, J34, XOP>(blk, X, K, split, bf16_gemv::kThreads, w0, w1, n0, n1, tile1, jobs, lds,
+                                          aux, eps);
     else
         bf16_gemv::rows<8, XPB, false, bf16_gemv::kThreads, XOP>(blk - q4k_wgs, (nb_rows + 3) / 4, wb, X, yb,
                                                                  nb_rows, K, nullptr, lds, aux, eps);
@@ -356,8 +361,9 @@ hipError_t run(const Jobs& jobs, const float* x, const XArgs& xa, int64_t k, int
                            waves * kWave, jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], jobs);
     } else {
         static_assert(D == 4 && TILED, "x operations run on the tiled layout, ring depth 4");
-        hipLaunchKernelGGL((k_gemv_q4k_xop<XP, J34, XOP>), g, b, lds, s, x, xa.aux, static_cast<int>(k), split,
-                           waves * kWave, jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], jobs, xa.eps);
+        hipLaunchKernelGGL((k_gemv_q4k_xop<XP, J34, XOP>), g, b, lds, s, x, xa.aux, jobs.w[0], jobs.w[1],
+                           static_cast<int>(k), split, waves * kWave, jobs.n[0], jobs.n[1], jobs.tile0[1], jobs,
+                           xa.eps);
     }
     return hipGetLastError();
 }
@@ -503,10 +509,9 @@ hipError_t run_fused(const Jobs& jobs, int ks, int q4k_wgs, const uint16_t* wb, 
                      const float* x, const XArgs& xa, int64_t k, size_t lds, hipStream_t s) {
     const int64_t bwgs = (nb_rows + 3) / 4;  // one row per wave, 4 waves
     hipLaunchKernelGGL((k_gemv_q4k_bf16<XPQ, J34, XPB, XOP>), dim3(static_cast<unsigned>(q4k_wgs + bwgs)),
-                       dim3(bf16_gemv::kThreads), lds, s, x, xa.aux, static_cast<int>(k),
-                       pack_split(ks, 4 / ks, static_cast<int>((k / 256 + ks - 1) / ks), jobs.count),
-                       bf16_gemv::kThreads, jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], q4k_wgs, wb, yb,
-                       static_cast<int>(nb_rows), jobs, xa.eps);
+                       dim3(bf16_gemv::kThreads), lds, s, x, xa.aux, jobs.w[0], jobs.w[1], static_cast<int>(k),
+                       pack_split(ks, 4 / ks, static_cast<int>((k / 256 + ks - 1) / ks), jobs.count), q4k_wgs,
+                       jobs.n[0], jobs.n[1], jobs.tile0[1], wb, yb, static_cast<int>(nb_rows), jobs, xa.eps);
     return hipGetLastError();
 }
 
