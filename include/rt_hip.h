@@ -158,6 +158,22 @@ int rt_hip_gemv_q4k_tiled_rmsnorm_multi(int32_t count, const void* const* tiled,
                                         int32_t gemma3, int64_t k, rt_hip_stream stream);
 int rt_hip_gemv_q4k_tiled_swiglu(const void* tiled, const float* gate, const float* up, float* y, int64_t n,
                                  int64_t k, rt_hip_stream stream);
+/* rt_hip_gemv_q4k_tiled_rmsnorm_rope: rt_hip_gemv_q4k_tiled_rmsnorm_multi
+ * plus rotary position embedding on the outputs of the jobs in rope_jobs (a
+ * bit mask: 0x3 for q and k of a q/k/v launch), at position pos, in the
+ * interleaved pairing of GGUF's llama weights.
+ * Replace: llama_rope (src/transformer5.cpp:95-125, RopePairing::Interleaved):
+ * for the pair (2i, 2i + 1) of each head, a = pos * inv_freq[i],
+ * out_2i = x_2i cos a - x_2i+1 sin a, out_2i+1 = x_2i sin a + x_2i+1 cos a.
+ * inv_freq [head_dim / 2] is the caller's (Config5::inv_freq,
+ * transformer5.cpp:36-52).  Writing k and v through y pointers into the KV
+ * cache rows of position pos is LlamaLayerKvCache::append (:59-68).  Each
+ * rotated job's n must be a multiple of head_dim (even). */
+int rt_hip_gemv_q4k_tiled_rmsnorm_rope(int32_t count, const void* const* tiled, float* const* y, const int64_t* n,
+                                       const float* x, const float* gamma, float eps, int32_t gemma3,
+                                       const float* inv_freq, int32_t pos, int32_t head_dim, int32_t rope_jobs,
+                                       int64_t k, rt_hip_stream stream);
+
 /* The same two operations for the BF16-widened projections of a Q4_K_M
  * model (src/transformer4_load.cpp:141-143): q/k (tiled Q4_K) and a BF16 v
  * on RMSNorm(x) in one launch, as rt_hip_gemv_q4k_tiled_bf16; and a BF16

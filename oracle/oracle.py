@@ -73,6 +73,8 @@ class Oracle:
         self._q6k_dec = _bind(L, "orc_q6k_decode_f32", None, _u8p, _sz, _f32p)
         self._rmsnorm = _bind(L, "orc_rmsnorm", None, _f32p, _f32p, _sz, C.c_float, C.c_int, _f32p)
         self._swiglu = _bind(L, "orc_swiglu", None, _f32p, _f32p, _sz, _f32p)
+        self._inv_freq = _bind(L, "orc_llama_inv_freq", None, C.c_float, _sz, _f32p, _sz, _f32p)
+        self._rope = _bind(L, "orc_llama_rope_interleaved", None, _f32p, _sz, _sz, _sz, _f32p, _f32p)
         self._argmax = _bind(L, "orc_argmax_first", C.c_int64, _f32p, _sz)
         self._normal = _bind(L, "orc_initrng_normal", None, C.c_uint64, _sz, C.c_float, _f32p)
         self._hw = _bind(L, "orc_hardware_threads", C.c_int)
@@ -87,6 +89,19 @@ class Oracle:
         for r in range(rows.shape[0]):
             self._rmsnorm(np.ascontiguousarray(rows[r]), g, g.size, eps, 1 if gemma3 else 0, out[r])
         return out.reshape(x.shape)
+
+    def llama_inv_freq(self, theta: float, head_dim: int, divisors=None) -> np.ndarray:
+        d = np.ascontiguousarray(divisors if divisors is not None else np.zeros(1), np.float32)
+        out = np.empty(head_dim // 2, np.float32)
+        self._inv_freq(theta, head_dim, d, 0 if divisors is None else d.size, out)
+        return out
+
+    def llama_rope(self, x: np.ndarray, n_heads: int, head_dim: int, pos: int, inv_freq: np.ndarray) -> np.ndarray:
+        """Interleaved-pairing RoPE of one row [n_heads * head_dim]."""
+        xx = np.ascontiguousarray(x, np.float32).reshape(-1)
+        out = np.empty_like(xx)
+        self._rope(xx, n_heads, head_dim, pos, np.ascontiguousarray(inv_freq, np.float32), out)
+        return out.reshape(np.shape(x))
 
     def swiglu(self, gate: np.ndarray, up: np.ndarray) -> np.ndarray:
         g = np.ascontiguousarray(gate, np.float32).reshape(-1)

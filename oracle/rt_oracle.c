@@ -648,6 +648,37 @@ void orc_swiglu(const float* gate, const float* up, size_t n, float* out) {
     }
 }
 
+/* Config5::inv_freq (src/transformer5.cpp:36-52): f = 1 / pow(theta,
+ * 2i / head_dim) in f32, divided by divisors[i] where one is given (> 0). */
+void orc_llama_inv_freq(float theta, size_t head_dim, const float* divisors, size_t n_div, float* out) {
+    const size_t half = head_dim / 2;
+    for (size_t i = 0; i < half; ++i) {
+        const float exponent = 2.0f * (float)i / (float)head_dim;
+        float f = 1.0f / powf(theta, exponent);
+        if (i < n_div && divisors[i] > 0.0f) f /= divisors[i];
+        out[i] = f;
+    }
+}
+
+/* llama_rope on one row, RopePairing::Interleaved (src/transformer5.cpp:
+ * 95-125): for each pair i, a = pos * inv_freq[i], cos and sin of a, then
+ * per head out[2i] = x0 cos - x1 sin, out[2i+1] = x0 sin + x1 cos. */
+void orc_llama_rope_interleaved(const float* x, size_t n_heads, size_t head_dim, size_t pos, const float* inv_freq,
+                                float* out) {
+    const size_t half = head_dim / 2;
+    memcpy(out, x, n_heads * head_dim * sizeof(float));
+    for (size_t i = 0; i < half; ++i) {
+        const float angle = (float)pos * inv_freq[i];
+        const float c = cosf(angle), s = sinf(angle);
+        for (size_t h = 0; h < n_heads; ++h) {
+            const size_t c0 = h * head_dim + 2 * i, c1 = c0 + 1;
+            const float x0 = x[c0], x1 = x[c1];
+            out[c0] = x0 * c - x1 * s;
+            out[c1] = x0 * s + x1 * c;
+        }
+    }
+}
+
 /* ------------------------------------------------------------------------ */
 /* InitRng: include/rt/init_rng.hpp:14-47                                   */
 /* ------------------------------------------------------------------------ */

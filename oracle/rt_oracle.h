@@ -122,6 +122,16 @@ void orc_q6k_decode_f32(const uint8_t* blocks, size_t n_elem, float* out);
  * The reference's own tensor_node.cpp needs its autograd graph (TensorNode,
  * Mat and their sources) and is not built here. */
 void orc_rmsnorm(const float* x, const float* gamma, size_t d, float eps, int gemma3, float* out);
+
+/* Config5::inv_freq and llama_rope, interleaved pairing (transformer5.cpp:
+ * 36-52, 95-125).  Pinned in tests/test_oracle_layer_ops.py by: pos 0 is the
+ * identity bit for bit; each pair keeps its length; the output equals the
+ * float64 rotation of the same pairs by the same f32 angles; the pairing is
+ * (2i, 2i + 1), not (i, i + head_dim / 2); inv_freq matches the float64
+ * formula, divisors included. */
+void orc_llama_inv_freq(float theta, size_t head_dim, const float* divisors, size_t n_div, float* out);
+void orc_llama_rope_interleaved(const float* x, size_t n_heads, size_t head_dim, size_t pos, const float* inv_freq,
+                                float* out);
 void orc_swiglu(const float* gate, const float* up, size_t n, float* out);
 
 /* src/transformer5.cpp:382-391: first index of the strict maximum; NaN never wins */

@@ -264,7 +264,8 @@ int rt_hip_gemv_q4k_tiled_multi(int32_t count, const void* const* tiled, float* 
 
 namespace {
 int gemv_xop(const char* fn, int xop, int32_t count, const void* const* tiled, float* const* y, const int64_t* n,
-             const float* x, const float* aux, float eps, int64_t k, rt_hip_stream stream) {
+             const float* x, const float* aux, float eps, int64_t k, rt_hip_stream stream,
+             const float* inv_freq = nullptr, int pos = 0, int head_dim = 0, int rope_jobs = 0) {
     if (count < 1 || count > RT_HIP_MULTI_MAX || !tiled || !y || !n)
         return fail(RT_HIP_E_ARG, std::string(fn) + ": count must be in [1, 4] with arrays");
     for (int32_t j = 0; j < count; ++j) {
@@ -277,8 +278,10 @@ int gemv_xop(const char* fn, int xop, int32_t count, const void* const* tiled, f
     if (!(eps >= 0.0f)) return fail(RT_HIP_E_ARG, std::string(fn) + ": eps must be >= 0");
     hipError_t e;
     if (!state_for_current(&e)) return hip_fail(e, fn);
-    return check_stream_launch(
-        launch_gemv_q4k_xop(xop, count, tiled, y, n, x, aux, eps, k, static_cast<hipStream_t>(stream)), fn);
+    return check_stream_launch(launch_gemv_q4k_xop(xop, count, tiled, y, n, x, aux, eps, k,
+                                                   static_cast<hipStream_t>(stream), inv_freq, pos, head_dim,
+                                                   rope_jobs),
+                               fn);
 }
 }  // namespace
 
@@ -287,6 +290,25 @@ int rt_hip_gemv_q4k_tiled_rmsnorm_multi(int32_t count, const void* const* tiled,
                                         int32_t gemma3, int64_t k, rt_hip_stream stream) {
     return gemv_xop("rt_hip_gemv_q4k_tiled_rmsnorm_multi", gemma3 ? 2 : 1, count, tiled, y, n, x, gamma, eps, k,
                     stream);
+}
+
+int rt_hip_gemv_q4k_tiled_rmsnorm_rope(int32_t count, const void* const* tiled, float* const* y, const int64_t* n,
+                                       const float* x, const float* gamma, float eps, int32_t gemma3,
+                                       const float* inv_freq, int32_t pos, int32_t head_dim, int32_t rope_jobs,
+                                       int64_t k, rt_hip_stream stream) {
+    const char* fn = "rt_hip_gemv_q4k_tiled_rmsnorm_rope";
+    if (count < 1 || count > RT_HIP_MULTI_MAX || !tiled || !y || !n)
+        return fail(RT_HIP_E_ARG, std::string(fn) + ": count must be in [1, 4] with arrays");
+    if (!inv_freq) return fail(RT_HIP_E_ARG, std::string(fn) + ": null inv_freq");
+    if (pos < 0) return fail(RT_HIP_E_ARG, std::string(fn) + ": pos must be >= 0");
+    if (head_dim < 2 || head_dim % 2 != 0) return fail(RT_HIP_E_ARG, std::string(fn) + ": head_dim must be even");
+    if (rope_jobs <= 0 || rope_jobs >= (1 << count))
+        return fail(RT_HIP_E_ARG, std::string(fn) + ": rope_jobs must name jobs in [0, count)");
+    for (int32_t j = 0; j < count; ++j)
+        if (((rope_jobs >> j) & 1) && n[j] % head_dim != 0)
+            return fail(RT_HIP_E_SHAPE, std::string(fn) + ": a rotated output is not whole heads");
+    return gemv_xop(fn, gemma3 ? 2 : 1, count, tiled, y, n, x, gamma, eps, k, stream, inv_freq, pos, head_dim,
+                    rope_jobs);
 }
 
 int rt_hip_gemv_q4k_tiled_swiglu(const void* tiled, const float* gate, const float* up, float* y, int64_t n,

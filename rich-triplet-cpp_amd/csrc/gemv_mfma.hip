@@ -40,6 +40,21 @@ struct Jobs {
     int count;
 };
 
+// Rotary position embedding on the outputs of the jobs in `jobs` (a bit
+// mask), in the interleaved pairing of GGUF's llama weights (rows 2i and
+// 2i + 1 of a head, llama_rope in transformer5.cpp:95-125):
+//     out_2i   = x_2i * cos(a) - x_2i+1 * sin(a)
+//     out_2i+1 = x_2i * sin(a) + x_2i+1 * cos(a),   a = pos * inv_freq[i]
+// with i the pair within the head.  Rows 2i and 2i + 1 of a 16-row tile are
+// lanes n and n ^ 1 of the wave that stores them, so the pair meets in one
+// lane swap.
+struct Rope {
+    const float* inv_freq = nullptr;  // [head_dim / 2], device
+    int pos = 0;
+    int head_dim = 0;
+    int jobs = 0;
+};
+
 // Job-table fields read into scalar registers through readfirstlane, and
 // picked with scalar selects: read straight from the kernel arguments (or
 // from an array), a job lookup becomes an indexed load and a wait.
@@ -85,11 +100,11 @@ __host__ __device__ inline size_t norm_offset(int K, int waves) {
 // output pointer) come from the table.
 // The body of workgroup `blk` (the kernel below, and the Q4_K workgroups of
 // the fused q/k/v launch); `lds` holds mfma_gemv_lds_bytes(K, waves).
-template <int D, int XP, bool TILED, bool J34, int XOP = kXNone>
+template <int D, int XP, bool TILED, bool J34, int XOP = kXNone, bool ROPE = false>
 __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, int K, uint32_t split, int nthreads,
                                           const uint8_t* w0, const uint8_t* w1, int n0, int n1, int tile1,
                                           const Jobs& jobs, uint8_t* lds, const float* __restrict__ aux = nullptr,
-                                          float eps = 0.0f) {
+                                          float eps = 0.0f, const Rope& rope = Rope{}) {
     const int count = static_cast<int>(split >> 29);
     // nthreads == blockDim.x, passed as a preloaded argument: blockDim
     // itself is a kernel-argument load that the first x loads would wait for.
@@ -284,18 +299,35 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     const bool keep = row < n_job;  // false for tile slots past the last tile
     const Four<uint64_t> ys = {sreg(jobs.y[0]), sreg(jobs.y[1]), sreg(jobs.y[2]), sreg(jobs.y[3])};
     float* const yj = reinterpret_cast<float*>(ys[job]);
+    // The row's final value, computed by every lane of the storing wave (the
+    // RoPE partner exchange needs the whole wave).
+    auto finish = [&](float val) {
+        if constexpr (XOP == kXRmsNorm || XOP == kXRmsNorm1) val *= out_scale;
+        if constexpr (ROPE) {
+            const float other = __shfl_xor(val, 1, kWave);
+            if ((rope.jobs >> job) & 1) {  // wave-uniform
+                const int j = row % rope.head_dim;
+                const float ang = static_cast<float>(rope.pos) * rope.inv_freq[j >> 1];
+                const float c = cosf(ang), sn = sinf(ang);
+                val = (j & 1) ? other * sn + val * c : val * c - other * sn;
+            }
+        }
+        return val;
+    };
     if (KS == 1) {
-        if (lane < 16 && keep) yj[row] = XOP == kXRmsNorm || XOP == kXRmsNorm1 ? v * out_scale : v;
+        const float out = finish(v);
+        if (lane < 16 && keep) yj[row] = out;
     } else {
         float* red = reinterpret_cast<float*>(lds + lds_bytes(K));  // [TPW][KS][16]
         float* rp = red + tslot * KS * 16;
         if (lane < 16) rp[ks * 16 + lane] = v;
         lds_barrier();
-        if (ks == 0 && lane < 16 && keep) {
-            float s = rp[lane];
+        if (ks == 0) {  // the whole wave: lanes past 16 repeat rows, unstored
+            float s = rp[lane & 15];
 #pragma unroll
-            for (int q = 1; q < KS; ++q) s += rp[q * 16 + lane];
-            yj[row] = XOP == kXRmsNorm || XOP == kXRmsNorm1 ? s * out_scale : s;
+            for (int q = 1; q < KS; ++q) s += rp[q * 16 + (lane & 15)];
+            const float out = finish(s);
+            if (lane < 16 && keep) yj[row] = out;
         }
     }
 }
@@ -312,13 +344,13 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
 // The same with a layer operation applied to x while it is staged (XOp).
 // Pointers first, then the 32-bit arguments: no padding, so all fourteen
 // leading dwords (aux, gamma or up, included) are preloaded.
-template <int XP, bool J34, int XOP>
+template <int XP, bool J34, int XOP, bool ROPE>
 __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_xop(
     const float* __restrict__ X, const float* __restrict__ aux, const uint8_t* w0, const uint8_t* w1, int K,
-    uint32_t split, int nthreads, int n0, int n1, int tile1, const Jobs jobs, float eps) {
+    uint32_t split, int nthreads, int n0, int n1, int tile1, const Jobs jobs, float eps, const Rope rope) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    q4k_tiles<4, XP, true, J34, XOP>(static_cast<int>(blockIdx.x), X, K, split, nthreads, w0, w1, n0, n1, tile1,
-                                     jobs, lds, aux, eps);
+    q4k_tiles<4, XP, true, J34, XOP, ROPE>(static_cast<int>(blockIdx.x), X, K, split, nthreads, w0, w1, n0, n1,
+                                           tile1, jobs, lds, aux, eps, rope);
 }
 
 // A layer's q/k/v when v is BF16 (Q6_K widened): the first q4k_wgs
@@ -347,48 +379,50 @@ __global__ __launch_bounds__(bf16_gemv::kThreads) void k_gemv_q4k_bf16(
 struct XArgs {
     const float* aux = nullptr;
     float eps = 0.0f;
+    Rope rope;
 };
 
-template <int D, int XP, bool TILED, bool J34, int XOP>
+template <int D, int XP, bool TILED, bool J34, int XOP, bool ROPE>
 hipError_t run(const Jobs& jobs, const float* x, const XArgs& xa, int64_t k, int ks, int waves, hipStream_t s) {
     const int tpw = waves / ks;
     const int64_t wgs = (static_cast<int64_t>(jobs.total) + tpw - 1) / tpw;
     const size_t lds = mfma_gemv_lds_bytes(k, waves);
     const uint32_t split = pack_split(ks, tpw, static_cast<int>((k / 256 + ks - 1) / ks), jobs.count);
     const dim3 g(static_cast<unsigned>(wgs)), b(static_cast<unsigned>(waves * kWave));
-    if constexpr (XOP == kXNone) {
+    if constexpr (XOP == kXNone && !ROPE) {
         hipLaunchKernelGGL((k_gemv_q4k_mfma<D, XP, TILED, J34>), g, b, lds, s, x, static_cast<int>(k), split,
                            waves * kWave, jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], jobs);
     } else {
-        static_assert(D == 4 && TILED, "x operations run on the tiled layout, ring depth 4");
-        hipLaunchKernelGGL((k_gemv_q4k_xop<XP, J34, XOP>), g, b, lds, s, x, xa.aux, jobs.w[0], jobs.w[1],
+        static_assert(D == 4 && TILED, "x operations and RoPE run on the tiled layout, ring depth 4");
+        hipLaunchKernelGGL((k_gemv_q4k_xop<XP, J34, XOP, ROPE>), g, b, lds, s, x, xa.aux, jobs.w[0], jobs.w[1],
                            static_cast<int>(k), split, waves * kWave, jobs.n[0], jobs.n[1], jobs.tile0[1], jobs,
-                           xa.eps);
+                           xa.eps, xa.rope);
     }
     return hipGetLastError();
 }
 
 // x prefetch depth: enough f32x4 per thread for all of x (up to K = 8192 at
 // 256 threads) before the weight prologue.
-template <int D, bool TILED, int XOP>
+template <int D, bool TILED, int XOP, bool ROPE>
 hipError_t run_xp(const Jobs& jobs, const float* x, const XArgs& xa, int64_t k, int ks, int waves,
                   hipStream_t s) {
     const int64_t per = (k / 4 + waves * kWave - 1) / (waves * kWave);
     // The host keeps K within the staging bound: 16 float4 per thread, 8
     // with an x operation (its second vector doubles the registers).
-    if (per > (XOP == kXNone ? 16 : 8)) return hipErrorInvalidValue;
+    constexpr bool kPlain = XOP == kXNone && !ROPE;
+    if (per > (kPlain ? 16 : 8)) return hipErrorInvalidValue;
     if (jobs.count > 2) {
-        if (per <= 2) return run<D, 2, TILED, true, XOP>(jobs, x, xa, k, ks, waves, s);
-        if (per <= 3) return run<D, 3, TILED, true, XOP>(jobs, x, xa, k, ks, waves, s);
-        if (per <= 4) return run<D, 4, TILED, true, XOP>(jobs, x, xa, k, ks, waves, s);
-        if (per <= 8 || XOP != kXNone) return run<D, 8, TILED, true, XOP>(jobs, x, xa, k, ks, waves, s);
-        if constexpr (XOP == kXNone) return run<D, 16, TILED, true, XOP>(jobs, x, xa, k, ks, waves, s);
+        if (per <= 2) return run<D, 2, TILED, true, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
+        if (per <= 3) return run<D, 3, TILED, true, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
+        if (per <= 4) return run<D, 4, TILED, true, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
+        if (per <= 8 || !kPlain) return run<D, 8, TILED, true, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
+        if constexpr (kPlain) return run<D, 16, TILED, true, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
     }
-    if (per <= 2) return run<D, 2, TILED, false, XOP>(jobs, x, xa, k, ks, waves, s);
-    if (per <= 3) return run<D, 3, TILED, false, XOP>(jobs, x, xa, k, ks, waves, s);
-    if (per <= 4) return run<D, 4, TILED, false, XOP>(jobs, x, xa, k, ks, waves, s);
-    if (per <= 8 || XOP != kXNone) return run<D, 8, TILED, false, XOP>(jobs, x, xa, k, ks, waves, s);
-    if constexpr (XOP == kXNone) return run<D, 16, TILED, false, XOP>(jobs, x, xa, k, ks, waves, s);
+    if (per <= 2) return run<D, 2, TILED, false, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
+    if (per <= 3) return run<D, 3, TILED, false, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
+    if (per <= 4) return run<D, 4, TILED, false, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
+    if (per <= 8 || !kPlain) return run<D, 8, TILED, false, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
+    if constexpr (kPlain) return run<D, 16, TILED, false, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
     return hipErrorInvalidValue;
 }
 
@@ -405,7 +439,7 @@ hipError_t run_xp(const Jobs& jobs, const float* x, const XArgs& xa, int64_t k, 
 // KS = 1 use KS = 4 (the lm_head: 38.0 us against 40.9 us at KS = 2).
 // KS = 1, 2, 4 run 4 waves per workgroup (4/KS tiles); other splits one
 // tile per workgroup of KS waves.
-template <bool TILED, int XOP = kXNone>
+template <bool TILED, int XOP = kXNone, bool ROPE = false>
 hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s, const XArgs& xa = XArgs{}) {
     const int64_t tiles = jobs.total;
     const int64_t nb = k / 256;
@@ -428,12 +462,12 @@ hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s, 
     int waves = ks <= 4 ? (4 / ks) * ks : ks;
     if (const int tpw = tune_param("Q4K_TPW", 0)) waves = ks * tpw;
     if (waves % ks != 0 || waves > kMaxThreads / kWave) return hipErrorInvalidValue;
-    if constexpr (XOP != kXNone) {
-        return run_xp<4, TILED, XOP>(jobs, x, xa, k, ks, waves, s);
+    if constexpr (XOP != kXNone || ROPE) {
+        return run_xp<4, TILED, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
     } else {
         const int d = tune_param("Q4K_RING", 4);
-        return d == 8 ? run_xp<8, TILED, XOP>(jobs, x, xa, k, ks, waves, s)
-                      : run_xp<4, TILED, XOP>(jobs, x, xa, k, ks, waves, s);
+        return d == 8 ? run_xp<8, TILED, XOP, ROPE>(jobs, x, xa, k, ks, waves, s)
+                      : run_xp<4, TILED, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
     }
 }
 
@@ -448,7 +482,8 @@ size_t mfma_gemv_lds_bytes(int64_t k, int waves) {
 size_t q4k_m1_lds_bytes(int64_t k) { return mfma_gemv_lds_bytes(k, kMaxThreads / kWave); }
 
 hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* const* y, const int64_t* n,
-                              const float* x, const float* aux, float eps, int64_t k, hipStream_t s) {
+                              const float* x, const float* aux, float eps, int64_t k, hipStream_t s,
+                              const float* inv_freq, int pos, int head_dim, int rope_jobs) {
     if (count < 1 || count > kMaxJobs || aux == nullptr) return hipErrorInvalidValue;
     Jobs jobs{};
     jobs.count = count;
@@ -470,6 +505,17 @@ hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* 
     XArgs xa;
     xa.aux = aux;
     xa.eps = eps;
+    if (rope_jobs) {
+        xa.rope.inv_freq = inv_freq;
+        xa.rope.pos = pos;
+        xa.rope.head_dim = head_dim;
+        xa.rope.jobs = rope_jobs;
+        switch (xop) {
+            case kXRmsNorm: return dispatch<true, kXRmsNorm, true>(jobs, x, k, s, xa);
+            case kXRmsNorm1: return dispatch<true, kXRmsNorm1, true>(jobs, x, k, s, xa);
+            default: return hipErrorInvalidValue;
+        }
+    }
     switch (xop) {
         case kXRmsNorm: return dispatch<true, kXRmsNorm>(jobs, x, k, s, xa);
         case kXRmsNorm1: return dispatch<true, kXRmsNorm1>(jobs, x, k, s, xa);

@@ -44,6 +44,8 @@ _SIGNATURES = {
     "rt_hip_gemv_q4k_tiled_rmsnorm_multi": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp,
                                             C.c_float, _i32, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_swiglu": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
+    "rt_hip_gemv_q4k_tiled_rmsnorm_rope": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp,
+                                           C.c_float, _i32, _vp, _i32, _i32, _i32, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_bf16_rmsnorm": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp, _i64,
                                            _vp, _vp, C.c_float, _i32, _i64, _vp],
     "rt_hip_gemv_bf16_swiglu": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
@@ -274,6 +276,24 @@ def gemv_q4k_tiled_rmsnorm_multi(ws, x, gamma, eps: float, ns, k: int, gemma3: b
     npp = (_i64 * count)(*ns)
     library().call("rt_hip_gemv_q4k_tiled_rmsnorm_multi", count, wp, yp, npp, _ptr(x), _ptr(gamma),
                    C.c_float(eps), 1 if gemma3 else 0, k, _stream(stream))
+    return ys
+
+
+def gemv_q4k_tiled_rmsnorm_rope(ws, x, gamma, eps: float, ns, k: int, inv_freq, pos: int, head_dim: int,
+                                rope_jobs: int, gemma3: bool = False, ys=None, stream=None):
+    """gemv_q4k_tiled_rmsnorm_multi, then interleaved RoPE at `pos` on the
+    outputs of the jobs in the bit mask rope_jobs; ys may point into a KV
+    cache (the append)."""
+    torch = _torch()
+    count = len(ws)
+    if ys is None:
+        ys = [torch.empty((1, n), dtype=torch.float32, device=x.device) for n in ns]
+    _dev_check(x, gamma, inv_freq, *ws, *ys)
+    wp = (_vp * count)(*[w.data_ptr() for w in ws])
+    yp = (_vp * count)(*[y.data_ptr() for y in ys])
+    npp = (_i64 * count)(*ns)
+    library().call("rt_hip_gemv_q4k_tiled_rmsnorm_rope", count, wp, yp, npp, _ptr(x), _ptr(gamma), C.c_float(eps),
+                   1 if gemma3 else 0, _ptr(inv_freq), pos, head_dim, rope_jobs, k, _stream(stream))
     return ys
 
 

@@ -115,3 +115,35 @@ def test_bf16_swiglu(rt, orc, n, k):
     got = from_dev(rt.gemv_bf16_swiglu(to_dev(w.view(np.int16)), to_dev(gate), to_dev(up), n, k))
     act = orc.swiglu(gate, up).reshape(1, k)
     assert normwise_err(got, orc.bf16_matmul_t(w, act)) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("pos", [0, 5, 1000, 70000])
+def test_rmsnorm_rope_qkv_into_kv_cache(rt, orc, pos):
+    """q/k/v of a Llama layer on RMSNorm(x), q and k rotated at `pos`
+    (interleaved pairing), k and v written straight into their KV-cache rows."""
+    import torch
+    k, hd, nq, nkv = 3072, 128, 24, 8
+    ns = [nq * hd, nkv * hd, nkv * hd]
+    say(f"[rmsnorm+rope qkv] pos={pos}")
+    rng = np.random.default_rng(pos + 1)
+    blocks = _weights(orc, rng, ns, k)
+    x = (rng.standard_normal(k) * 2).astype(np.float32)
+    gamma = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    inv = orc.llama_inv_freq(500000.0, hd)
+    tiled = [rt.q4k_tile(to_dev(b), n, k) for b, n in zip(blocks, ns)]
+    max_tok = 8
+    row = min(pos, max_tok - 1)
+    kc = torch.zeros((max_tok, nkv * hd), device="cuda")
+    vc = torch.zeros((max_tok, nkv * hd), device="cuda")
+    q = torch.empty((1, ns[0]), device="cuda")
+    rt.gemv_q4k_tiled_rmsnorm_rope(tiled, to_dev(x), to_dev(gamma), 1e-5, ns, k, to_dev(inv), pos, hd, 0x3,
+                                   ys=[q, kc[row:row + 1], vc[row:row + 1]])
+    xn = orc.rmsnorm(x, gamma, 1e-5).reshape(1, k)
+    lin = [orc.q4k_matmul_t(b, n, k, xn).reshape(-1) for b, n in zip(blocks, ns)]
+    want_q = orc.llama_rope(lin[0], nq, hd, pos, inv)
+    want_k = orc.llama_rope(lin[1], nkv, hd, pos, inv)
+    assert normwise_err(from_dev(q).reshape(-1), want_q) <= GEMV_TOL
+    assert normwise_err(from_dev(kc)[row], want_k) <= GEMV_TOL
+    assert normwise_err(from_dev(vc)[row], lin[2]) <= GEMV_TOL
+    others = [r for r in range(max_tok) if r != row]
+    assert not np.any(from_dev(kc)[others]) and not np.any(from_dev(vc)[others])

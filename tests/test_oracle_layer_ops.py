@@ -70,3 +70,35 @@ def test_swiglu_against_float64(orc):
     want = g64 / (1.0 + np.exp(-g64)) * u.astype(np.float64)
     got = orc.swiglu(g, u).astype(np.float64)
     assert np.allclose(got, want, rtol=1e-6, atol=1e-30)
+
+
+def test_llama_inv_freq_against_float64(orc):
+    theta, hd = 500000.0, 128
+    got = orc.llama_inv_freq(theta, hd).astype(np.float64)
+    want = 1.0 / theta ** (2.0 * np.arange(hd // 2) / hd)
+    assert np.allclose(got, want, rtol=2e-6, atol=0)
+    div = np.array([1.0, 2.0, 0.0, 32.0], np.float32)
+    got_d = orc.llama_inv_freq(theta, hd, div).astype(np.float64)
+    want_d = want.copy()
+    for i, d in enumerate(div):
+        if d > 0:
+            want_d[i] /= d
+    assert np.allclose(got_d, want_d, rtol=3e-6, atol=0)
+
+
+def test_llama_rope_interleaved(orc):
+    rng = np.random.default_rng(6)
+    n_heads, hd = 8, 128
+    inv = orc.llama_inv_freq(500000.0, hd)
+    x = rng.standard_normal(n_heads * hd).astype(np.float32)
+    assert np.array_equal(orc.llama_rope(x, n_heads, hd, 0, inv), x)  # pos 0: identity
+    for pos in (1, 17, 1000, 100000):
+        got = orc.llama_rope(x, n_heads, hd, pos, inv).astype(np.float64)
+        ang = (np.float32(pos) * inv).astype(np.float32).astype(np.float64)  # the f32 angle
+        c, s = np.cos(ang), np.sin(ang)
+        x2 = x.astype(np.float64).reshape(n_heads, hd // 2, 2)
+        want = np.stack([x2[..., 0] * c - x2[..., 1] * s, x2[..., 0] * s + x2[..., 1] * c], axis=-1).reshape(-1)
+        assert np.allclose(got, want, rtol=0, atol=1e-5 * np.abs(x).max()), pos
+        # each pair keeps its length
+        g2 = got.reshape(n_heads, hd // 2, 2)
+        assert np.allclose(np.hypot(g2[..., 0], g2[..., 1]), np.hypot(x2[..., 0], x2[..., 1]), rtol=1e-5)
