@@ -174,6 +174,21 @@ int rt_hip_gemv_q4k_tiled_rmsnorm_rope(int32_t count, const void* const* tiled, 
                                        const float* inv_freq, int32_t pos, int32_t head_dim, int32_t rope_jobs,
                                        int64_t k, rt_hip_stream stream);
 
+/* rt_hip_attention_decode: one query token's grouped-query attention over
+ * positions [0, seq_len) of a layer's KV cache.
+ * Replace: gqa_attention_cached's decode path (src/transformer4.cpp:379-432),
+ * as LlamaAttention::forward_cached calls it (src/transformer5.cpp:152-172):
+ * per query head h (KV head h / (n_q / n_kv)), s_c = (q_h . k_c) * scale,
+ * p = softmax(s), out_h = sum_c p_c v_c.  q [n_q * 128], k_cache / v_cache
+ * row-major [>= seq_len, n_kv * 128] f32 (LlamaLayerKvCache), out
+ * [n_q * 128]; head_dim 128, n_q / n_kv in {1, 2, 3, 4}, seq_len >= 1.
+ * Results match to f32 rounding (online softmax over position splits,
+ * merged in a fixed order: deterministic).  Uses the per-device workspace,
+ * as the GEMM and batched GEMV do. */
+int rt_hip_attention_decode(const float* q, const float* k_cache, const float* v_cache, float* out,
+                            int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int64_t seq_len, float scale,
+                            rt_hip_stream stream);
+
 /* The same two operations for the BF16-widened projections of a Q4_K_M
  * model (src/transformer4_load.cpp:141-143): q/k (tiled Q4_K) and a BF16 v
  * on RMSNorm(x) in one launch, as rt_hip_gemv_q4k_tiled_bf16; and a BF16

@@ -75,6 +75,8 @@ class Oracle:
         self._swiglu = _bind(L, "orc_swiglu", None, _f32p, _f32p, _sz, _f32p)
         self._inv_freq = _bind(L, "orc_llama_inv_freq", None, C.c_float, _sz, _f32p, _sz, _f32p)
         self._rope = _bind(L, "orc_llama_rope_interleaved", None, _f32p, _sz, _sz, _sz, _f32p, _f32p)
+        self._attn = _bind(L, "orc_gqa_attention_decode", None, _f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _sz,
+                           C.c_float, _f32p)
         self._argmax = _bind(L, "orc_argmax_first", C.c_int64, _f32p, _sz)
         self._normal = _bind(L, "orc_initrng_normal", None, C.c_uint64, _sz, C.c_float, _f32p)
         self._hw = _bind(L, "orc_hardware_threads", C.c_int)
@@ -102,6 +104,15 @@ class Oracle:
         out = np.empty_like(xx)
         self._rope(xx, n_heads, head_dim, pos, np.ascontiguousarray(inv_freq, np.float32), out)
         return out.reshape(np.shape(x))
+
+    def gqa_attention_decode(self, q, k_cache, v_cache, seq_len: int, n_q: int, n_kv: int, d: int,
+                             scale: float) -> np.ndarray:
+        qq = np.ascontiguousarray(q, np.float32).reshape(-1)
+        kc = np.ascontiguousarray(k_cache, np.float32).reshape(-1)
+        vc = np.ascontiguousarray(v_cache, np.float32).reshape(-1)
+        out = np.empty(n_q * d, np.float32)
+        self._attn(qq, kc, vc, 0, seq_len, n_q, n_kv, d, scale, out)
+        return out
 
     def swiglu(self, gate: np.ndarray, up: np.ndarray) -> np.ndarray:
         g = np.ascontiguousarray(gate, np.float32).reshape(-1)

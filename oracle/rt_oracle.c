@@ -679,6 +679,41 @@ void orc_llama_rope_interleaved(const float* x, size_t n_heads, size_t head_dim,
     }
 }
 
+/* gqa_attention_cached, decode path (src/transformer4.cpp:379-432): one
+ * query row; for each query head, scores[c] = dot(q_h, k_h[c]) * scale over
+ * c in [k_start, k_end) (sequential dot), max, exp(s - max) summed in order,
+ * divided by the sum when positive, then out_h = sum_c p_c v_h[c] in order. */
+void orc_gqa_attention_decode(const float* q, const float* k_cache, const float* v_cache, size_t k_start,
+                              size_t k_end, size_t n_q_heads, size_t n_kv_heads, size_t d_head, float scale,
+                              float* out) {
+    const size_t t_kv = k_end - k_start, kv_stride = n_kv_heads * d_head, group = n_q_heads / n_kv_heads;
+    float* scores = (float*)malloc((t_kv ? t_kv : 1) * sizeof(float));
+    memset(out, 0, n_q_heads * d_head * sizeof(float));
+    for (size_t qh = 0; qh < n_q_heads; ++qh) {
+        const size_t kvh = qh / group, q_off = qh * d_head, kv_off = kvh * d_head, out_off = qh * d_head;
+        for (size_t ci = 0; ci < t_kv; ++ci) {
+            const size_t k_base = (k_start + ci) * kv_stride + kv_off;
+            float dot = 0.0f;
+            for (size_t di = 0; di < d_head; ++di) dot += q[q_off + di] * k_cache[k_base + di];
+            scores[ci] = dot * scale;
+        }
+        float max_s = -INFINITY;
+        for (size_t ci = 0; ci < t_kv; ++ci) max_s = max_s < scores[ci] ? scores[ci] : max_s;
+        float sum_exp = 0.0f;
+        for (size_t ci = 0; ci < t_kv; ++ci) {
+            scores[ci] = expf(scores[ci] - max_s);
+            sum_exp += scores[ci];
+        }
+        if (sum_exp > 0.0f)
+            for (size_t ci = 0; ci < t_kv; ++ci) scores[ci] /= sum_exp;
+        for (size_t ci = 0; ci < t_kv; ++ci) {
+            const size_t v_base = (k_start + ci) * kv_stride + kv_off;
+            for (size_t di = 0; di < d_head; ++di) out[out_off + di] += scores[ci] * v_cache[v_base + di];
+        }
+    }
+    free(scores);
+}
+
 /* ------------------------------------------------------------------------ */
 /* InitRng: include/rt/init_rng.hpp:14-47                                   */
 /* ------------------------------------------------------------------------ */

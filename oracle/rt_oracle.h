@@ -130,6 +130,15 @@ void orc_rmsnorm(const float* x, const float* gamma, size_t d, float eps, int ge
  * (2i, 2i + 1), not (i, i + head_dim / 2); inv_freq matches the float64
  * formula, divisors included. */
 void orc_llama_inv_freq(float theta, size_t head_dim, const float* divisors, size_t n_div, float* out);
+
+/* gqa_attention_cached's decode path (transformer4.cpp:379-432).  Pinned in
+ * tests/test_oracle_layer_ops.py by: one cached position gives out = v
+ * exactly; equal keys give the mean of the values; the float64 softmax of
+ * the same scores; and the GQA head mapping (query head h reads KV head
+ * h / group, checked with distinct per-head values). */
+void orc_gqa_attention_decode(const float* q, const float* k_cache, const float* v_cache, size_t k_start,
+                              size_t k_end, size_t n_q_heads, size_t n_kv_heads, size_t d_head, float scale,
+                              float* out);
 void orc_llama_rope_interleaved(const float* x, size_t n_heads, size_t head_dim, size_t pos, const float* inv_freq,
                                 float* out);
 void orc_swiglu(const float* gate, const float* up, size_t n, float* out);

@@ -311,6 +311,26 @@ int rt_hip_gemv_q4k_tiled_rmsnorm_rope(int32_t count, const void* const* tiled, 
                     rope_jobs);
 }
 
+int rt_hip_attention_decode(const float* q, const float* k_cache, const float* v_cache, float* out,
+                            int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int64_t seq_len, float scale,
+                            rt_hip_stream stream) {
+    const char* fn = "rt_hip_attention_decode";
+    if (!q || !k_cache || !v_cache || !out) return fail(RT_HIP_E_ARG, std::string(fn) + ": null pointer");
+    if (head_dim != 128) return fail(RT_HIP_E_UNSUPPORTED, std::string(fn) + ": head_dim must be 128");
+    if (n_kv_heads < 1 || n_q_heads < n_kv_heads || n_q_heads % n_kv_heads != 0 || n_q_heads / n_kv_heads > 4)
+        return fail(RT_HIP_E_SHAPE, std::string(fn) + ": need n_q = g * n_kv with g in [1, 4]");
+    if (seq_len < 1 || seq_len > 0x7fffffffLL) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": seq_len out of range");
+    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
+        return fail(RT_HIP_E_ALIGN, std::string(fn) + ": buffers must be 16-byte aligned");
+    hipError_t e;
+    if (!state_for_current(&e)) return hip_fail(e, fn);
+    float* part = static_cast<float*>(workspace(attention_decode_workspace(n_q_heads, n_kv_heads, seq_len), &e));
+    if (!part) return hip_fail(e, fn);
+    return check_stream_launch(launch_attention_decode(q, k_cache, v_cache, out, part, n_q_heads, n_kv_heads,
+                                                       seq_len, scale, static_cast<hipStream_t>(stream)),
+                               fn);
+}
+
 int rt_hip_gemv_q4k_tiled_swiglu(const void* tiled, const float* gate, const float* up, float* y, int64_t n,
                                  int64_t k, rt_hip_stream stream) {
     return gemv_xop("rt_hip_gemv_q4k_tiled_swiglu", 3, 1, &tiled, &y, &n, gate, up, 0.0f, k, stream);

@@ -1,0 +1,191 @@
+// attention.hip -- decode attention over a KV cache: one query token, grouped
+// query heads (gqa_attention_cached's decode path, transformer4.cpp:379-432).
+//
+// For each query head h (KV head h / group): s_c = (q_h . k_c) * scale over
+// the cached positions c < seq_len, p = softmax(s), out_h = sum_c p_c v_c.
+// The cache is f32 rows of n_kv * head_dim (LlamaLayerKvCache), head_dim 128,
+// up to 4 query heads per KV head (the partial states of a workgroup live in
+// static LDS: 16 groups x 4 heads x 528 bytes).
+//
+// Split over positions (flash decoding): workgroup (kv head, split) streams
+// its chunk of positions once for all the query heads of its group and keeps
+// an online softmax per head -- running max m, sum l = sum exp(s - m) and
+// o = sum exp(s - m) v.  A position is read by 16 lanes, 8 values each, so
+// a wave covers 4 positions per step and a 16-lane DPP reduction finishes
+// each dot.  The workgroup's 16 partial states merge through LDS into one
+// (m, l, o[128]) per head and split; a second launch merges the splits in
+// split order and divides: out = o / l.  The order of every sum is fixed,
+// so results are deterministic.  exp is the hardware exp2 on a log2(e)
+// scaled argument (about 1 ulp).
+#include "rt_common.hpp"
+#include "rt_launch.hpp"
+
+namespace rt_hip {
+namespace {
+
+constexpr int kHd = 128;      // head_dim
+constexpr int kT = 256;       // threads per partial workgroup
+constexpr int kGroups = 16;   // 4 waves x 4 sixteen-lane position groups
+constexpr float kLog2e = 1.44269504088896341f;
+
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the aligned 16-lane row; every lane of the row ends with the same bits.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dppf<0xb1>(v);   // lane ^ 1
+    v += dppf<0x4e>(v);   // lane ^ 2
+    v += dppf<0x141>(v);  // half-row mirror
+    v += dppf<0x140>(v);  // row mirror
+    return v;
+}
+
+// Partial state of one (query head, split): m, l, then o[128].
+constexpr int kPart = 2 + kHd;
+
+template <int G>
+__global__ __launch_bounds__(kT) void k_attn_partial(const float* __restrict__ q, const float* __restrict__ kc,
+                                                     const float* __restrict__ vc, float* __restrict__ part,
+                                                     int n_kv, int seq_len, int chunk, float scale) {
+    __shared__ float sm[kGroups][G][2];
+    __shared__ f32x4 so[kGroups][G][kHd / 4];
+    const int kvh = blockIdx.x, sp = blockIdx.y, S = gridDim.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grp = wave * 4 + (lane >> 4), sub = lane & 15;
+    const int p0 = sp * chunk, p1 = min(seq_len, p0 + chunk);
+    const int64_t row = static_cast<int64_t>(n_kv) * kHd;
+
+    f32x4 qa[G], qb[G], oa[G], ob[G];
+    float m[G], l[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        const float* qp = q + (static_cast<int64_t>(kvh) * G + h) * kHd + sub * 8;
+        qa[h] = *reinterpret_cast<const f32x4*>(qp);
+        qb[h] = *reinterpret_cast<const f32x4*>(qp + 4);
+        oa[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        ob[h] = oa[h];
+        m[h] = -__builtin_inff();
+        l[h] = 0.0f;
+    }
+    // Positions p0 + grp, p0 + grp + 16, ...: the loop bound is uniform per
+    // 16-lane group, and the DPP reductions stay inside the group.
+    for (int p = p0 + grp; p < p1; p += kGroups) {
+        const float* kp = kc + p * row + kvh * kHd + sub * 8;
+        const float* vp = vc + p * row + kvh * kHd + sub * 8;
+        const f32x4 ka = *reinterpret_cast<const f32x4*>(kp), kb = *reinterpret_cast<const f32x4*>(kp + 4);
+        const f32x4 va = *reinterpret_cast<const f32x4*>(vp), vb = *reinterpret_cast<const f32x4*>(vp + 4);
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float d = (qa[h][0] * ka[0] + qa[h][1] * ka[1]) + (qa[h][2] * ka[2] + qa[h][3] * ka[3]);
+            d += (qb[h][0] * kb[0] + qb[h][1] * kb[1]) + (qb[h][2] * kb[2] + qb[h][3] * kb[3]);
+            const float s = row16_sum(d) * scale;
+            const float mn = fmaxf(m[h], s);
+            const float a = exp_fast(m[h] - mn), b = exp_fast(s - mn);
+            l[h] = l[h] * a + b;
+            oa[h] = oa[h] * a + va * b;
+            ob[h] = ob[h] * a + vb * b;
+            m[h] = mn;
+        }
+    }
+    // Merge the 16 group states: every group writes, then thread (h, d4)
+    // folds them in group order.
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        if (sub == 0) {
+            sm[grp][h][0] = m[h];
+            sm[grp][h][1] = l[h];
+        }
+        so[grp][h][sub * 2] = oa[h];
+        so[grp][h][sub * 2 + 1] = ob[h];
+    }
+    __syncthreads();
+    for (int t = tid; t < G * (kHd / 4); t += kT) {
+        const int h = t / (kHd / 4), d4 = t % (kHd / 4);
+        float M = -__builtin_inff();
+        for (int g = 0; g < kGroups; ++g) M = fmaxf(M, sm[g][h][0]);
+        float L = 0.0f;
+        f32x4 O = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (M != -__builtin_inff()) {
+            for (int g = 0; g < kGroups; ++g) {
+                const float w = exp_fast(sm[g][h][0] - M);
+                L += sm[g][h][1] * w;
+                O += so[g][h][d4] * w;
+            }
+        }
+        float* dst = part + (static_cast<int64_t>(kvh * G + h) * S + sp) * kPart;
+        if (d4 == 0) {
+            dst[0] = M;
+            dst[1] = L;
+        }
+        *reinterpret_cast<f32x4*>(dst + 2 + d4 * 4) = O;
+    }
+}
+
+// One workgroup of 128 threads per query head: fold the splits in order.
+__global__ __launch_bounds__(kHd) void k_attn_combine(const float* __restrict__ part, float* __restrict__ out,
+                                                      int S) {
+    const int h = blockIdx.x, d = threadIdx.x;
+    const float* ph = part + static_cast<int64_t>(h) * S * kPart;
+    float M = -__builtin_inff();
+    for (int s = 0; s < S; ++s) M = fmaxf(M, ph[s * kPart]);
+    float L = 0.0f, O = 0.0f;
+    if (M != -__builtin_inff()) {
+        for (int s = 0; s < S; ++s) {
+            const float w = exp_fast(ph[s * kPart] - M);
+            L += ph[s * kPart + 1] * w;
+            O += ph[s * kPart + 2 + d] * w;
+        }
+    }
+    out[static_cast<int64_t>(h) * kHd + d] = L > 0.0f ? O / L : 0.0f;
+}
+
+template <int G>
+hipError_t run(const float* q, const float* kc, const float* vc, float* out, float* part, int n_kv, int seq_len,
+               int S, int chunk, float scale, hipStream_t s) {
+    hipLaunchKernelGGL(k_attn_partial<G>, dim3(static_cast<unsigned>(n_kv), static_cast<unsigned>(S)), dim3(kT), 0,
+                       s, q, kc, vc, part, n_kv, seq_len, chunk, scale);
+    hipLaunchKernelGGL(k_attn_combine, dim3(static_cast<unsigned>(n_kv * G)), dim3(kHd), 0, s, part, out, S);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+void attention_decode_shape(int64_t n_kv, int64_t seq_len, int* splits, int* chunk) {
+    // About two workgroups per CU in all, at least 16 positions per split.
+    const int64_t cus = device_info().cus;
+    int64_t S = (2 * cus + n_kv - 1) / n_kv;
+    const int64_t most = (seq_len + 15) / 16;
+    S = S > most ? most : S;
+    S = S < 1 ? 1 : S;
+    int64_t c = (seq_len + S - 1) / S;
+    c = (c + 15) / 16 * 16;
+    S = (seq_len + c - 1) / c;
+    *splits = static_cast<int>(S < 1 ? 1 : S);
+    *chunk = static_cast<int>(c);
+}
+
+size_t attention_decode_workspace(int64_t n_q, int64_t n_kv, int64_t seq_len) {
+    int S, c;
+    attention_decode_shape(n_kv, seq_len, &S, &c);
+    return static_cast<size_t>(n_q) * S * kPart * sizeof(float);
+}
+
+hipError_t launch_attention_decode(const float* q, const float* kc, const float* vc, float* out, float* part,
+                                   int64_t n_q, int64_t n_kv, int64_t seq_len, float scale, hipStream_t s) {
+    int S, chunk;
+    attention_decode_shape(n_kv, seq_len, &S, &chunk);
+    const int G = static_cast<int>(n_q / n_kv), nk = static_cast<int>(n_kv), L = static_cast<int>(seq_len);
+    switch (G) {
+        case 1: return run<1>(q, kc, vc, out, part, nk, L, S, chunk, scale, s);
+        case 2: return run<2>(q, kc, vc, out, part, nk, L, S, chunk, scale, s);
+        case 3: return run<3>(q, kc, vc, out, part, nk, L, S, chunk, scale, s);
+        case 4: return run<4>(q, kc, vc, out, part, nk, L, S, chunk, scale, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace rt_hip

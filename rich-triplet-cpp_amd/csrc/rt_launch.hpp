@@ -43,6 +43,12 @@ hipError_t launch_gemv_q4k_mfma(const void* w, const float* x, float* y, int64_t
                                 hipStream_t s);
 // Up to four M = 1 Q4_K GEMVs sharing x, K; `tiled`: the weights are in the
 // tiled layout (q4k_mfma.hpp) rather than reference row-major blocks.
+// Decode attention (attention.hip): head_dim 128, n_q / n_kv in {1, 2, 3, 4};
+// `part` holds attention_decode_workspace(...) bytes.
+void attention_decode_shape(int64_t n_kv, int64_t seq_len, int* splits, int* chunk);
+size_t attention_decode_workspace(int64_t n_q, int64_t n_kv, int64_t seq_len);
+hipError_t launch_attention_decode(const float* q, const float* kc, const float* vc, float* out, float* part,
+                                   int64_t n_q, int64_t n_kv, int64_t seq_len, float scale, hipStream_t s);
 // M = 1 BF16 GEMV with a layer operation applied to x while it is staged
 // (xop as below), k <= 8192.
 hipError_t launch_gemv_bf16_xop(int xop, const uint16_t* w, const float* x, const float* aux, float eps, float* y,

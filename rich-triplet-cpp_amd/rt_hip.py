@@ -44,6 +44,7 @@ _SIGNATURES = {
     "rt_hip_gemv_q4k_tiled_rmsnorm_multi": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp,
                                             C.c_float, _i32, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_swiglu": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
+    "rt_hip_attention_decode": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, C.c_float, _vp],
     "rt_hip_gemv_q4k_tiled_rmsnorm_rope": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp,
                                            C.c_float, _i32, _vp, _i32, _i32, _i32, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_bf16_rmsnorm": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp, _i64,
@@ -295,6 +296,18 @@ def gemv_q4k_tiled_rmsnorm_rope(ws, x, gamma, eps: float, ns, k: int, inv_freq, 
     library().call("rt_hip_gemv_q4k_tiled_rmsnorm_rope", count, wp, yp, npp, _ptr(x), _ptr(gamma), C.c_float(eps),
                    1 if gemma3 else 0, _ptr(inv_freq), pos, head_dim, rope_jobs, k, _stream(stream))
     return ys
+
+
+def attention_decode(q, k_cache, v_cache, seq_len: int, n_q: int, n_kv: int, scale: float, head_dim: int = 128,
+                     out=None, stream=None):
+    """One query token's GQA attention over KV-cache positions [0, seq_len)."""
+    torch = _torch()
+    if out is None:
+        out = torch.empty((1, n_q * head_dim), dtype=torch.float32, device=q.device)
+    _dev_check(q, k_cache, v_cache, out)
+    library().call("rt_hip_attention_decode", _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), n_q, n_kv, head_dim,
+                   seq_len, C.c_float(scale), _stream(stream))
+    return out
 
 
 def gemv_q4k_tiled_swiglu(w, gate, up, n: int, k: int, y=None, stream=None):

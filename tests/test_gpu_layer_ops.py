@@ -147,3 +147,44 @@ def test_rmsnorm_rope_qkv_into_kv_cache(rt, orc, pos):
     assert normwise_err(from_dev(vc)[row], lin[2]) <= GEMV_TOL
     others = [r for r in range(max_tok) if r != row]
     assert not np.any(from_dev(kc)[others]) and not np.any(from_dev(vc)[others])
+
+
+@pytest.mark.parametrize("nq,nkv,seq_len", [(24, 8, 1), (24, 8, 7), (24, 8, 300), (24, 8, 4096), (32, 8, 1000),
+                                            (8, 8, 129), (16, 8, 50)])
+def test_attention_decode(rt, orc, nq, nkv, seq_len):
+    """rt_hip_attention_decode against the oracle's gqa_attention_cached
+    (decode path), positions [0, seq_len) of a longer cache."""
+    say(f"[attention decode] n_q={nq} n_kv={nkv} L={seq_len}")
+    d = 128
+    rng = np.random.default_rng(nq * 7 + seq_len)
+    cap = seq_len + 5
+    kc = rng.standard_normal((cap, nkv * d)).astype(np.float32)
+    vc = rng.standard_normal((cap, nkv * d)).astype(np.float32)
+    q = (rng.standard_normal(nq * d) * 0.5).astype(np.float32)
+    scale = float(1.0 / np.sqrt(np.float32(d)))
+    got = from_dev(rt.attention_decode(to_dev(q), to_dev(kc), to_dev(vc), seq_len, nq, nkv, scale)).reshape(-1)
+    want = orc.gqa_attention_decode(q, kc, vc, seq_len, nq, nkv, d, scale)
+    assert normwise_err(got, want) <= GEMV_TOL, normwise_err(got, want)
+    if seq_len == 1:  # one position: the value row itself, to rounding
+        g = nq // nkv
+        for h in range(nq):
+            assert np.allclose(got[h * d:(h + 1) * d], vc[0, (h // g) * d:(h // g + 1) * d], rtol=1e-6, atol=1e-6)
+
+
+def test_attention_decode_is_deterministic_and_rejects_bad_shapes(rt):
+    import ctypes as C
+    rng = np.random.default_rng(3)
+    kc = to_dev(rng.standard_normal((2048, 1024)).astype(np.float32))
+    vc = to_dev(rng.standard_normal((2048, 1024)).astype(np.float32))
+    q = to_dev(rng.standard_normal(3072).astype(np.float32))
+    a = from_dev(rt.attention_decode(q, kc, vc, 2048, 24, 8, 0.088))
+    b = from_dev(rt.attention_decode(q, kc, vc, 2048, 24, 8, 0.088))
+    assert np.array_equal(a, b)
+    lib = rt.library()
+    p = q.data_ptr()
+    assert lib.status("rt_hip_attention_decode", p, kc.data_ptr(), vc.data_ptr(), p, 24, 8, 64, 10,
+                      C.c_float(0.1), None) == 6  # head_dim 64: unsupported
+    assert lib.status("rt_hip_attention_decode", p, kc.data_ptr(), vc.data_ptr(), p, 24, 7, 128, 10,
+                      C.c_float(0.1), None) == E_SHAPE
+    assert lib.status("rt_hip_attention_decode", p, kc.data_ptr(), vc.data_ptr(), p, 24, 8, 128, 0,
+                      C.c_float(0.1), None) == E_SHAPE

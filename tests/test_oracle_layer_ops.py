@@ -102,3 +102,36 @@ def test_llama_rope_interleaved(orc):
         # each pair keeps its length
         g2 = got.reshape(n_heads, hd // 2, 2)
         assert np.allclose(np.hypot(g2[..., 0], g2[..., 1]), np.hypot(x2[..., 0], x2[..., 1]), rtol=1e-5)
+
+
+def test_gqa_attention_decode(orc):
+    rng = np.random.default_rng(7)
+    nq, nkv, d = 6, 2, 128
+    scale = 1.0 / np.sqrt(d)
+    q = rng.standard_normal(nq * d).astype(np.float32)
+    # one cached position: out = v exactly
+    k1 = rng.standard_normal((1, nkv * d)).astype(np.float32)
+    v1 = rng.standard_normal((1, nkv * d)).astype(np.float32)
+    out = orc.gqa_attention_decode(q, k1, v1, 1, nq, nkv, d, scale).reshape(nq, d)
+    for h in range(nq):
+        assert np.array_equal(out[h], v1[0, (h // 3) * d:(h // 3 + 1) * d]), h
+    # equal keys: the mean of the values (per KV head)
+    L = 10
+    kc = np.tile(rng.standard_normal((1, nkv * d)).astype(np.float32), (L, 1))
+    vc = rng.standard_normal((L, nkv * d)).astype(np.float32)
+    out = orc.gqa_attention_decode(q, kc, vc, L, nq, nkv, d, scale).reshape(nq, d)
+    for h in range(nq):
+        want = vc[:, (h // 3) * d:(h // 3 + 1) * d].astype(np.float64).mean(axis=0)
+        assert np.allclose(out[h], want, rtol=1e-5, atol=1e-6), h
+    # random: float64 softmax of the same scores
+    L = 37
+    kc = rng.standard_normal((L, nkv * d)).astype(np.float32)
+    vc = rng.standard_normal((L, nkv * d)).astype(np.float32)
+    out = orc.gqa_attention_decode(q, kc, vc, L, nq, nkv, d, scale).reshape(nq, d)
+    for h in range(nq):
+        kh = kc[:, (h // 3) * d:(h // 3 + 1) * d].astype(np.float64)
+        vh = vc[:, (h // 3) * d:(h // 3 + 1) * d].astype(np.float64)
+        s = kh @ q[h * d:(h + 1) * d].astype(np.float64) * scale
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        assert np.allclose(out[h], p @ vh, rtol=0, atol=2e-6), h
