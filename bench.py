@@ -434,6 +434,72 @@ def bench_layer_ops(args, rt, torch):
             "data": "synthetic"}
 
 
+# ------------------------------------------------- one decode token, fused --
+
+def bench_decode_layers(args, rt, torch):
+    """One Llama-3.2-3B decode token through every operation of the layers
+    except the embedding lookup, pure Q4_K weights, at --context cached
+    positions: per layer RMSNorm + q/k/v + RoPE + KV append (one launch),
+    attention over the cache (two), o + residual (one), RMSNorm + gate/up
+    (one), SwiGLU + down + residual (one); then the final RMSNorm + lm_head.
+    The KV caches hold random keys and values for positions < context; the
+    token is written at position context.  Synthetic weights and inputs."""
+    g = torch.Generator(device="cuda").manual_seed(0)
+    dev = "cuda"
+    ctx = args.context
+    nq, nkv, hd = 24, 8, 128
+
+    def tiled(n, k):
+        w = torch.randn((n, k), generator=g, device=dev) * 0.02
+        return rt.q4k_tile(rt.quantize_q4k(w), n, k)
+
+    layers = []
+    for _ in range(LAYERS):
+        L = {"qkv": [tiled(HIDDEN, HIDDEN), tiled(KV, HIDDEN), tiled(KV, HIDDEN)], "o": tiled(HIDDEN, HIDDEN),
+             "gu": [tiled(FFN, HIDDEN), tiled(FFN, HIDDEN)], "down": tiled(HIDDEN, FFN),
+             "g1": 1.0 + 0.1 * torch.randn((HIDDEN,), generator=g, device=dev),
+             "g2": 1.0 + 0.1 * torch.randn((HIDDEN,), generator=g, device=dev),
+             "kc": torch.randn((ctx + 1, KV), generator=g, device=dev),
+             "vc": torch.randn((ctx + 1, KV), generator=g, device=dev)}
+        layers.append(L)
+    head = tiled(VOCAB, HIDDEN)
+    gf = 1.0 + 0.1 * torch.randn((HIDDEN,), generator=g, device=dev)
+    resid = torch.randn((1, HIDDEN), generator=g, device=dev)
+    q = torch.empty((1, HIDDEN), device=dev)
+    attn = torch.empty((1, HIDDEN), device=dev)
+    gate, up = torch.empty((1, FFN), device=dev), torch.empty((1, FFN), device=dev)
+    logits = torch.empty((1, VOCAB), device=dev)
+    # Config5::inv_freq (transformer5.cpp:36-52), rope_theta 500000
+    inv = torch.tensor([1.0 / (500000.0 ** (2.0 * i / hd)) for i in range(hd // 2)], dtype=torch.float32, device=dev)
+    eps, scale = 1e-5, float(1.0 / (hd ** 0.5))
+
+    def step():
+        for L in layers:
+            rt.gemv_q4k_tiled_rmsnorm_rope(L["qkv"], resid, L["g1"], eps, [HIDDEN, KV, KV], HIDDEN, inv, ctx, hd, 0x3,
+                                           ys=[q, L["kc"][ctx:ctx + 1], L["vc"][ctx:ctx + 1]])
+            rt.attention_decode(q, L["kc"], L["vc"], ctx + 1, nq, nkv, scale, out=attn)
+            rt.gemv_q4k_tiled_residual(L["o"], attn, resid, HIDDEN, HIDDEN)
+            rt.gemv_q4k_tiled_rmsnorm_multi(L["gu"], resid, L["g2"], eps, [FFN, FFN], HIDDEN, ys=[gate, up])
+            rt.gemv_swiglu_residual(rt.Q4K, L["down"], gate, up, resid, HIDDEN, FFN)
+        rt.gemv_q4k_tiled_rmsnorm_multi([head], resid, gf, eps, [VOCAB], HIDDEN, ys=[logits])
+
+    def attention_only():
+        for L in layers:
+            rt.attention_decode(q, L["kc"], L["vc"], ctx + 1, nq, nkv, scale, out=attn)
+
+    ms, _ = time_graph(torch, step, args.warmup, args.steps)
+    ms_a, _ = time_graph(torch, attention_only, args.warmup, args.steps)
+    kv_bytes = LAYERS * 2 * (ctx + 1) * KV * 4
+    log(f"[bench] decode token (fused layers, context {ctx}): {ms * 1e3:.1f} us/token; "
+        f"attention alone {ms_a * 1e3:.1f} us ({kv_bytes / (ms_a * 1e-3) / 1e9:.0f} GB/s of KV cache)")
+    return {"metric": "Llama-3.2-3B decode token through every layer operation (pure Q4_K), fused engine path",
+            "value": round(ms * 1e3, 2), "unit": "us/token", "higher_is_better": False, "context": ctx,
+            "attention_us_per_token": round(ms_a * 1e3, 2),
+            "attention_kv_gbs": round(kv_bytes / (ms_a * 1e-3) / 1e9, 1),
+            "launches_per_token": 6 * LAYERS + 1, "steps": args.steps, "warmup": args.warmup,
+            "data": "synthetic"}
+
+
 # ------------------------------------------------------ other BASELINE configs --
 
 def bench_single_gemv(args, rt, torch, fmt, n, k, label, copies_bytes=768 << 20):
@@ -503,8 +569,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="llama_decode",
                     choices=["llama_decode", "q4k_gemv", "q4_0_gemv", "bf16_lm_head", "prefill",
-                             "flux", "layer_ops"])
+                             "flux", "layer_ops", "decode_layers"])
     ap.add_argument("--mix", default="q4km", choices=["q4km", "q4k"])
+    ap.add_argument("--context", type=int, default=1024,
+                    help="cached positions for --workload decode_layers")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibration-copy-mb", type=int, default=0,
                     help="before the workload, copy a buffer of this many MiB once with a plain "
@@ -550,6 +618,8 @@ def main() -> int:
                          "config 4 prefill Q4_K GEMM M=512 (gate, up, down)", False)
     elif args.workload == "layer_ops":
         out = bench_layer_ops(args, rt, torch)
+    elif args.workload == "decode_layers":
+        out = bench_decode_layers(args, rt, torch)
     elif args.workload == "flux":
         out = bench_gemm(args, rt, torch, [(4608, 9216, 3072), (4608, 12288, 3072), (4608, 3072, 12288)],
                          "config 5 FLUX linears M=4608 (QKV, MLP-in, MLP-out)", True)

@@ -174,6 +174,19 @@ int rt_hip_gemv_q4k_tiled_rmsnorm_rope(int32_t count, const void* const* tiled, 
                                        const float* inv_freq, int32_t pos, int32_t head_dim, int32_t rope_jobs,
                                        int64_t k, rt_hip_stream stream);
 
+/* The residual adds: resid += W . x (the attention output projection) and
+ * resid += W . (silu(gate) * up) (the MLP's down projection, Q4_K or
+ * BF16-widened), the finished rows added to resid in the store.
+ * Replace: LlamaBlock::forward_cached's `x + attn(...)` and `h + mlp(...)`
+ * (src/transformer5.cpp:205-212) with the o / down projections before them.
+ * resid [n] is read and written; it must not alias x, gate or up. */
+int rt_hip_gemv_q4k_tiled_residual(const void* tiled, const float* x, float* resid, int64_t n, int64_t k,
+                                   rt_hip_stream stream);
+int rt_hip_gemv_q4k_tiled_swiglu_residual(const void* tiled, const float* gate, const float* up, float* resid,
+                                          int64_t n, int64_t k, rt_hip_stream stream);
+int rt_hip_gemv_bf16_swiglu_residual(const uint16_t* w, const float* gate, const float* up, float* resid, int64_t n,
+                                     int64_t k, rt_hip_stream stream);
+
 /* rt_hip_attention_decode: one query token's grouped-query attention over
  * positions [0, seq_len) of a layer's KV cache.
  * Replace: gqa_attention_cached's decode path (src/transformer4.cpp:379-432),

@@ -265,22 +265,24 @@ int rt_hip_gemv_q4k_tiled_multi(int32_t count, const void* const* tiled, float* 
 namespace {
 int gemv_xop(const char* fn, int xop, int32_t count, const void* const* tiled, float* const* y, const int64_t* n,
              const float* x, const float* aux, float eps, int64_t k, rt_hip_stream stream,
-             const float* inv_freq = nullptr, int pos = 0, int head_dim = 0, int rope_jobs = 0) {
+             const float* inv_freq = nullptr, int pos = 0, int head_dim = 0, int rope_jobs = 0, bool add = false) {
     if (count < 1 || count > RT_HIP_MULTI_MAX || !tiled || !y || !n)
         return fail(RT_HIP_E_ARG, std::string(fn) + ": count must be in [1, 4] with arrays");
     for (int32_t j = 0; j < count; ++j) {
         int rc = gemv_args(fn, tiled[j], x, y[j], n[j], k, 1, 256);
         if (rc) return rc;
     }
-    if (!aux) return fail(RT_HIP_E_ARG, std::string(fn) + ": null gamma / up");
-    if (!aligned16(aux)) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": gamma / up must be 16-byte aligned");
+    if (xop != 0 && !aux) return fail(RT_HIP_E_ARG, std::string(fn) + ": null gamma / up");
+    if (xop != 0 && !aligned16(aux))
+        return fail(RT_HIP_E_ALIGN, std::string(fn) + ": gamma / up must be 16-byte aligned");
+    if (add && (y[0] == x || y[0] == aux)) return fail(RT_HIP_E_ARG, std::string(fn) + ": resid aliases an input");
     if (k > 8192 || q4k_m1_lds_bytes(k) > 65536) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 8192");
     if (!(eps >= 0.0f)) return fail(RT_HIP_E_ARG, std::string(fn) + ": eps must be >= 0");
     hipError_t e;
     if (!state_for_current(&e)) return hip_fail(e, fn);
     return check_stream_launch(launch_gemv_q4k_xop(xop, count, tiled, y, n, x, aux, eps, k,
                                                    static_cast<hipStream_t>(stream), inv_freq, pos, head_dim,
-                                                   rope_jobs),
+                                                   rope_jobs, add),
                                fn);
 }
 }  // namespace
@@ -309,6 +311,33 @@ int rt_hip_gemv_q4k_tiled_rmsnorm_rope(int32_t count, const void* const* tiled, 
             return fail(RT_HIP_E_SHAPE, std::string(fn) + ": a rotated output is not whole heads");
     return gemv_xop(fn, gemma3 ? 2 : 1, count, tiled, y, n, x, gamma, eps, k, stream, inv_freq, pos, head_dim,
                     rope_jobs);
+}
+
+int rt_hip_gemv_q4k_tiled_residual(const void* tiled, const float* x, float* resid, int64_t n, int64_t k,
+                                   rt_hip_stream stream) {
+    return gemv_xop("rt_hip_gemv_q4k_tiled_residual", 0, 1, &tiled, &resid, &n, x, nullptr, 0.0f, k, stream, nullptr,
+                    0, 0, 0, true);
+}
+
+int rt_hip_gemv_q4k_tiled_swiglu_residual(const void* tiled, const float* gate, const float* up, float* resid,
+                                          int64_t n, int64_t k, rt_hip_stream stream) {
+    return gemv_xop("rt_hip_gemv_q4k_tiled_swiglu_residual", 3, 1, &tiled, &resid, &n, gate, up, 0.0f, k, stream,
+                    nullptr, 0, 0, 0, true);
+}
+
+int rt_hip_gemv_bf16_swiglu_residual(const uint16_t* w, const float* gate, const float* up, float* resid, int64_t n,
+                                     int64_t k, rt_hip_stream stream) {
+    const char* fn = "rt_hip_gemv_bf16_swiglu_residual";
+    int rc = gemv_args(fn, w, gate, resid, n, k, 1, 256);
+    if (rc) return rc;
+    if (!up) return fail(RT_HIP_E_ARG, std::string(fn) + ": null up");
+    if (!aligned16(up)) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": up must be 16-byte aligned");
+    if (resid == gate || resid == up) return fail(RT_HIP_E_ARG, std::string(fn) + ": resid aliases an input");
+    if (k > 8192) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 8192");
+    hipError_t e;
+    if (!state_for_current(&e)) return hip_fail(e, fn);
+    return check_stream_launch(
+        launch_gemv_bf16_xop(3, w, gate, up, 0.0f, resid, n, k, static_cast<hipStream_t>(stream), true), fn);
 }
 
 int rt_hip_attention_decode(const float* q, const float* k_cache, const float* v_cache, float* out,

@@ -26,6 +26,7 @@ namespace {
 constexpr int kHd = 128;      // head_dim
 constexpr int kT = 256;       // threads per partial workgroup
 constexpr int kGroups = 16;   // 4 waves x 4 sixteen-lane position groups
+constexpr int kU = 4;         // positions per group loaded ahead
 constexpr float kLog2e = 1.44269504088896341f;
 
 __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
@@ -71,24 +72,38 @@ __global__ __launch_bounds__(kT) void k_attn_partial(const float* __restrict__ q
         m[h] = -__builtin_inff();
         l[h] = 0.0f;
     }
-    // Positions p0 + grp, p0 + grp + 16, ...: the loop bound is uniform per
-    // 16-lane group, and the DPP reductions stay inside the group.
-    for (int p = p0 + grp; p < p1; p += kGroups) {
-        const float* kp = kc + p * row + kvh * kHd + sub * 8;
-        const float* vp = vc + p * row + kvh * kHd + sub * 8;
-        const f32x4 ka = *reinterpret_cast<const f32x4*>(kp), kb = *reinterpret_cast<const f32x4*>(kp + 4);
-        const f32x4 va = *reinterpret_cast<const f32x4*>(vp), vb = *reinterpret_cast<const f32x4*>(vp + 4);
+    // Positions p0 + grp + 16 j: the bound is uniform per 16-lane group, and
+    // the DPP reductions stay inside the group.  kU positions per group are
+    // loaded before any is used, so each batch costs one memory latency.
+    for (int pb = p0 + grp; pb < p1; pb += kGroups * kU) {
+        f32x4 ka[kU], kb[kU], va[kU], vb[kU];
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float d = (qa[h][0] * ka[0] + qa[h][1] * ka[1]) + (qa[h][2] * ka[2] + qa[h][3] * ka[3]);
-            d += (qb[h][0] * kb[0] + qb[h][1] * kb[1]) + (qb[h][2] * kb[2] + qb[h][3] * kb[3]);
-            const float s = row16_sum(d) * scale;
-            const float mn = fmaxf(m[h], s);
-            const float a = exp_fast(m[h] - mn), b = exp_fast(s - mn);
-            l[h] = l[h] * a + b;
-            oa[h] = oa[h] * a + va * b;
-            ob[h] = ob[h] * a + vb * b;
-            m[h] = mn;
+        for (int u = 0; u < kU; ++u) {
+            const int p = pb + u * kGroups;
+            if (p < p1) {
+                const float* kp = kc + p * row + kvh * kHd + sub * 8;
+                const float* vp = vc + p * row + kvh * kHd + sub * 8;
+                ka[u] = *reinterpret_cast<const f32x4*>(kp);
+                kb[u] = *reinterpret_cast<const f32x4*>(kp + 4);
+                va[u] = *reinterpret_cast<const f32x4*>(vp);
+                vb[u] = *reinterpret_cast<const f32x4*>(vp + 4);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            if (pb + u * kGroups >= p1) break;  // uniform per group
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                float d = (qa[h][0] * ka[u][0] + qa[h][1] * ka[u][1]) + (qa[h][2] * ka[u][2] + qa[h][3] * ka[u][3]);
+                d += (qb[h][0] * kb[u][0] + qb[h][1] * kb[u][1]) + (qb[h][2] * kb[u][2] + qb[h][3] * kb[u][3]);
+                const float sc = row16_sum(d) * scale;
+                const float mn = fmaxf(m[h], sc);
+                const float a = exp_fast(m[h] - mn), b = exp_fast(sc - mn);
+                l[h] = l[h] * a + b;
+                oa[h] = oa[h] * a + va[u] * b;
+                ob[h] = ob[h] * a + vb[u] * b;
+                m[h] = mn;
+            }
         }
     }
     // Merge the 16 group states: every group writes, then thread (h, d4)
@@ -131,9 +146,11 @@ __global__ __launch_bounds__(kHd) void k_attn_combine(const float* __restrict__ 
     const int h = blockIdx.x, d = threadIdx.x;
     const float* ph = part + static_cast<int64_t>(h) * S * kPart;
     float M = -__builtin_inff();
+#pragma unroll 8
     for (int s = 0; s < S; ++s) M = fmaxf(M, ph[s * kPart]);
     float L = 0.0f, O = 0.0f;
     if (M != -__builtin_inff()) {
+#pragma unroll 8
         for (int s = 0; s < S; ++s) {
             const float w = exp_fast(ph[s * kPart] - M);
             L += ph[s * kPart + 1] * w;
@@ -155,15 +172,14 @@ hipError_t run(const float* q, const float* kc, const float* vc, float* out, flo
 }  // namespace
 
 void attention_decode_shape(int64_t n_kv, int64_t seq_len, int* splits, int* chunk) {
-    // About two workgroups per CU in all, at least 16 positions per split.
+    // About one workgroup per CU, and whole batches: at least one batch of
+    // kU positions per group (64 positions) per split.
     const int64_t cus = device_info().cus;
-    int64_t S = (2 * cus + n_kv - 1) / n_kv;
-    const int64_t most = (seq_len + 15) / 16;
-    S = S > most ? most : S;
-    S = S < 1 ? 1 : S;
-    int64_t c = (seq_len + S - 1) / S;
-    c = (c + 15) / 16 * 16;
-    S = (seq_len + c - 1) / c;
+    const int64_t want = (cus + n_kv - 1) / n_kv;
+    const int64_t batch = kGroups * kU;
+    int64_t c = (seq_len + want - 1) / want;
+    c = (c + batch - 1) / batch * batch;
+    const int64_t S = (seq_len + c - 1) / c;
     *splits = static_cast<int>(S < 1 ? 1 : S);
     *chunk = static_cast<int>(c);
 }

@@ -17,13 +17,13 @@ __global__ __launch_bounds__(T) void k_gemv_bf16(const uint16_t* __restrict__ W,
 }
 
 // The same with a layer operation applied to x while it is staged (XOp).
-template <int D, int XP, int T, int XOP>
+template <int D, int XP, int T, int XOP, bool ADD>
 __global__ __launch_bounds__(T) void k_gemv_bf16_xop(const uint16_t* __restrict__ W, const float* __restrict__ X,
                                                     const float* __restrict__ aux, float* __restrict__ Y, int N,
                                                     int K, float eps) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    rows<D, XP, false, T, XOP>(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), W, X, Y, N, K, nullptr,
-                               lds, aux, eps);
+    rows<D, XP, false, T, XOP, ADD>(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), W, X, Y, N, K,
+                                    nullptr, lds, aux, eps);
 }
 
 // T threads per workgroup, each wave looping over its rows; x is prefetched into registers before the
@@ -74,7 +74,7 @@ hipError_t launch_gemv_bf16_m1(const uint16_t* w, const float* x, float* y, int6
 
 namespace {
 // The default launch shape of run() (8 waves), with an x operation.
-template <int XOP>
+template <int XOP, bool ADD>
 hipError_t run_xop(const uint16_t* w, const float* x, const float* aux, float eps, float* y, int64_t n, int64_t k,
                    hipStream_t s) {
     constexpr int T = 512;
@@ -86,21 +86,22 @@ hipError_t run_xop(const uint16_t* w, const float* x, const float* aux, float ep
     const size_t lds = bf16_m1_lds_bytes(k);
     const int ik = static_cast<int>(k), in = static_cast<int>(n);
     if (per <= 2)
-        hipLaunchKernelGGL((k_gemv_bf16_xop<8, 2, T, XOP>), g, b, lds, s, w, x, aux, y, in, ik, eps);
+        hipLaunchKernelGGL((k_gemv_bf16_xop<8, 2, T, XOP, ADD>), g, b, lds, s, w, x, aux, y, in, ik, eps);
     else if (per <= 4)
-        hipLaunchKernelGGL((k_gemv_bf16_xop<8, 4, T, XOP>), g, b, lds, s, w, x, aux, y, in, ik, eps);
+        hipLaunchKernelGGL((k_gemv_bf16_xop<8, 4, T, XOP, ADD>), g, b, lds, s, w, x, aux, y, in, ik, eps);
     else
-        hipLaunchKernelGGL((k_gemv_bf16_xop<8, 8, T, XOP>), g, b, lds, s, w, x, aux, y, in, ik, eps);
+        hipLaunchKernelGGL((k_gemv_bf16_xop<8, 8, T, XOP, ADD>), g, b, lds, s, w, x, aux, y, in, ik, eps);
     return hipGetLastError();
 }
 }  // namespace
 
 hipError_t launch_gemv_bf16_xop(int xop, const uint16_t* w, const float* x, const float* aux, float eps, float* y,
-                                int64_t n, int64_t k, hipStream_t s) {
+                                int64_t n, int64_t k, hipStream_t s, bool add) {
+    if (add) return xop == kXSwiGlu ? run_xop<kXSwiGlu, true>(w, x, aux, eps, y, n, k, s) : hipErrorInvalidValue;
     switch (xop) {
-        case kXRmsNorm: return run_xop<kXRmsNorm>(w, x, aux, eps, y, n, k, s);
-        case kXRmsNorm1: return run_xop<kXRmsNorm1>(w, x, aux, eps, y, n, k, s);
-        case kXSwiGlu: return run_xop<kXSwiGlu>(w, x, aux, eps, y, n, k, s);
+        case kXRmsNorm: return run_xop<kXRmsNorm, false>(w, x, aux, eps, y, n, k, s);
+        case kXRmsNorm1: return run_xop<kXRmsNorm1, false>(w, x, aux, eps, y, n, k, s);
+        case kXSwiGlu: return run_xop<kXSwiGlu, false>(w, x, aux, eps, y, n, k, s);
         default: return hipErrorInvalidValue;
     }
 }

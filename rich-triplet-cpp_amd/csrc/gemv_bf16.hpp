@@ -94,7 +94,9 @@ __device__ __forceinline__ float wave_sum(float v, int lane) {
     return v;
 }
 
-template <int D, int XP, bool ARGMAX, int T = kThreads, int XOP = kXNone>
+// ADD: the rows are added to what Y holds (the residual add) instead of
+// stored.
+template <int D, int XP, bool ARGMAX, int T = kThreads, int XOP = kXNone, bool ADD = false>
 __device__ __forceinline__ void rows(int blk, int nblk, const uint16_t* __restrict__ W,
                                      const float* __restrict__ X, float* __restrict__ Y, int N, int K,
                                      uint64_t* __restrict__ key, uint8_t* lds,
@@ -242,7 +244,10 @@ __device__ __forceinline__ void rows(int blk, int nblk, const uint16_t* __restri
         if (i + j < L) RT_BF16_CONSUME(ring[j]);
 #undef RT_BF16_CONSUME
 
-    if (lane < R) Yg[gw + lane * NW] = kNorm ? res * out_scale : res;
+    if (lane < R) {
+        const float out = kNorm ? res * out_scale : res;
+        Yg[gw + lane * NW] = ADD ? Yg[gw + lane * NW] + out : out;
+    }
     if constexpr (ARGMAX) {
         if (lane == 0 && best != 0)
             atomicMax(reinterpret_cast<unsigned long long*>(key), static_cast<unsigned long long>(best));

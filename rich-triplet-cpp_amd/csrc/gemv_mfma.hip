@@ -48,6 +48,12 @@ struct Jobs {
 // with i the pair within the head.  Rows 2i and 2i + 1 of a 16-row tile are
 // lanes n and n ^ 1 of the wave that stores them, so the pair meets in one
 // lane swap.
+// What the epilogue does with a finished row: store it, rotate it first
+// (RoPE, below), or add it to what y holds (the residual add of
+// LlamaBlock::forward_cached, transformer5.cpp:205-212: x = x + attn(...),
+// x = x + mlp(...)).
+enum Epi { kEpiNone = 0, kEpiRope = 1, kEpiAdd = 2 };
+
 struct Rope {
     const float* inv_freq = nullptr;  // [head_dim / 2], device
     int pos = 0;
@@ -100,7 +106,7 @@ __host__ __device__ inline size_t norm_offset(int K, int waves) {
 // output pointer) come from the table.
 // The body of workgroup `blk` (the kernel below, and the Q4_K workgroups of
 // the fused q/k/v launch); `lds` holds mfma_gemv_lds_bytes(K, waves).
-template <int D, int XP, bool TILED, bool J34, int XOP = kXNone, bool ROPE = false>
+template <int D, int XP, bool TILED, bool J34, int XOP = kXNone, int EPI = kEpiNone>
 __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, int K, uint32_t split, int nthreads,
                                           const uint8_t* w0, const uint8_t* w1, int n0, int n1, int tile1,
                                           const Jobs& jobs, uint8_t* lds, const float* __restrict__ aux = nullptr,
@@ -303,7 +309,7 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     // RoPE partner exchange needs the whole wave).
     auto finish = [&](float val) {
         if constexpr (XOP == kXRmsNorm || XOP == kXRmsNorm1) val *= out_scale;
-        if constexpr (ROPE) {
+        if constexpr (EPI == kEpiRope) {
             const float other = __shfl_xor(val, 1, kWave);
             if ((rope.jobs >> job) & 1) {  // wave-uniform
                 const int j = row % rope.head_dim;
@@ -316,7 +322,7 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     };
     if (KS == 1) {
         const float out = finish(v);
-        if (lane < 16 && keep) yj[row] = out;
+        if (lane < 16 && keep) yj[row] = EPI == kEpiAdd ? yj[row] + out : out;
     } else {
         float* red = reinterpret_cast<float*>(lds + lds_bytes(K));  // [TPW][KS][16]
         float* rp = red + tslot * KS * 16;
@@ -327,7 +333,7 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
 #pragma unroll
             for (int q = 1; q < KS; ++q) s += rp[q * 16 + (lane & 15)];
             const float out = finish(s);
-            if (lane < 16 && keep) yj[row] = out;
+            if (lane < 16 && keep) yj[row] = EPI == kEpiAdd ? yj[row] + out : out;
         }
     }
 }
@@ -344,12 +350,12 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
 // The same with a layer operation applied to x while it is staged (XOp).
 // Pointers first, then the 32-bit arguments: no padding, so all fourteen
 // leading dwords (aux, gamma or up, included) are preloaded.
-template <int XP, bool J34, int XOP, bool ROPE>
+template <int XP, bool J34, int XOP, int EPI>
 __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_xop(
     const float* __restrict__ X, const float* __restrict__ aux, const uint8_t* w0, const uint8_t* w1, int K,
     uint32_t split, int nthreads, int n0, int n1, int tile1, const Jobs jobs, float eps, const Rope rope) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    q4k_tiles<4, XP, true, J34, XOP, ROPE>(static_cast<int>(blockIdx.x), X, K, split, nthreads, w0, w1, n0, n1,
+    q4k_tiles<4, XP, true, J34, XOP, EPI>(static_cast<int>(blockIdx.x), X, K, split, nthreads, w0, w1, n0, n1,
                                            tile1, jobs, lds, aux, eps, rope);
 }
 
@@ -382,19 +388,19 @@ struct XArgs {
     Rope rope;
 };
 
-template <int D, int XP, bool TILED, bool J34, int XOP, bool ROPE>
+template <int D, int XP, bool TILED, bool J34, int XOP, int EPI>
 hipError_t run(const Jobs& jobs, const float* x, const XArgs& xa, int64_t k, int ks, int waves, hipStream_t s) {
     const int tpw = waves / ks;
     const int64_t wgs = (static_cast<int64_t>(jobs.total) + tpw - 1) / tpw;
     const size_t lds = mfma_gemv_lds_bytes(k, waves);
     const uint32_t split = pack_split(ks, tpw, static_cast<int>((k / 256 + ks - 1) / ks), jobs.count);
     const dim3 g(static_cast<unsigned>(wgs)), b(static_cast<unsigned>(waves * kWave));
-    if constexpr (XOP == kXNone && !ROPE) {
+    if constexpr (XOP == kXNone && EPI == kEpiNone) {
         hipLaunchKernelGGL((k_gemv_q4k_mfma<D, XP, TILED, J34>), g, b, lds, s, x, static_cast<int>(k), split,
                            waves * kWave, jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], jobs);
     } else {
         static_assert(D == 4 && TILED, "x operations and RoPE run on the tiled layout, ring depth 4");
-        hipLaunchKernelGGL((k_gemv_q4k_xop<XP, J34, XOP, ROPE>), g, b, lds, s, x, xa.aux, jobs.w[0], jobs.w[1],
+        hipLaunchKernelGGL((k_gemv_q4k_xop<XP, J34, XOP, EPI>), g, b, lds, s, x, xa.aux, jobs.w[0], jobs.w[1],
                            static_cast<int>(k), split, waves * kWave, jobs.n[0], jobs.n[1], jobs.tile0[1], jobs,
                            xa.eps, xa.rope);
     }
@@ -403,26 +409,26 @@ hipError_t run(const Jobs& jobs, const float* x, const XArgs& xa, int64_t k, int
 
 // x prefetch depth: enough f32x4 per thread for all of x (up to K = 8192 at
 // 256 threads) before the weight prologue.
-template <int D, bool TILED, int XOP, bool ROPE>
+template <int D, bool TILED, int XOP, int EPI>
 hipError_t run_xp(const Jobs& jobs, const float* x, const XArgs& xa, int64_t k, int ks, int waves,
                   hipStream_t s) {
     const int64_t per = (k / 4 + waves * kWave - 1) / (waves * kWave);
     // The host keeps K within the staging bound: 16 float4 per thread, 8
     // with an x operation (its second vector doubles the registers).
-    constexpr bool kPlain = XOP == kXNone && !ROPE;
+    constexpr bool kPlain = XOP == kXNone && EPI == kEpiNone;
     if (per > (kPlain ? 16 : 8)) return hipErrorInvalidValue;
     if (jobs.count > 2) {
-        if (per <= 2) return run<D, 2, TILED, true, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
-        if (per <= 3) return run<D, 3, TILED, true, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
-        if (per <= 4) return run<D, 4, TILED, true, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
-        if (per <= 8 || !kPlain) return run<D, 8, TILED, true, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
-        if constexpr (kPlain) return run<D, 16, TILED, true, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
+        if (per <= 2) return run<D, 2, TILED, true, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
+        if (per <= 3) return run<D, 3, TILED, true, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
+        if (per <= 4) return run<D, 4, TILED, true, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
+        if (per <= 8 || !kPlain) return run<D, 8, TILED, true, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
+        if constexpr (kPlain) return run<D, 16, TILED, true, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
     }
-    if (per <= 2) return run<D, 2, TILED, false, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
-    if (per <= 3) return run<D, 3, TILED, false, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
-    if (per <= 4) return run<D, 4, TILED, false, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
-    if (per <= 8 || !kPlain) return run<D, 8, TILED, false, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
-    if constexpr (kPlain) return run<D, 16, TILED, false, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
+    if (per <= 2) return run<D, 2, TILED, false, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
+    if (per <= 3) return run<D, 3, TILED, false, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
+    if (per <= 4) return run<D, 4, TILED, false, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
+    if (per <= 8 || !kPlain) return run<D, 8, TILED, false, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
+    if constexpr (kPlain) return run<D, 16, TILED, false, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
     return hipErrorInvalidValue;
 }
 
@@ -439,7 +445,7 @@ hipError_t run_xp(const Jobs& jobs, const float* x, const XArgs& xa, int64_t k, 
 // KS = 1 use KS = 4 (the lm_head: 38.0 us against 40.9 us at KS = 2).
 // KS = 1, 2, 4 run 4 waves per workgroup (4/KS tiles); other splits one
 // tile per workgroup of KS waves.
-template <bool TILED, int XOP = kXNone, bool ROPE = false>
+template <bool TILED, int XOP = kXNone, int EPI = kEpiNone>
 hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s, const XArgs& xa = XArgs{}) {
     const int64_t tiles = jobs.total;
     const int64_t nb = k / 256;
@@ -462,12 +468,12 @@ hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s, 
     int waves = ks <= 4 ? (4 / ks) * ks : ks;
     if (const int tpw = tune_param("Q4K_TPW", 0)) waves = ks * tpw;
     if (waves % ks != 0 || waves > kMaxThreads / kWave) return hipErrorInvalidValue;
-    if constexpr (XOP != kXNone || ROPE) {
-        return run_xp<4, TILED, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
+    if constexpr (XOP != kXNone || EPI != kEpiNone) {
+        return run_xp<4, TILED, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
     } else {
         const int d = tune_param("Q4K_RING", 4);
-        return d == 8 ? run_xp<8, TILED, XOP, ROPE>(jobs, x, xa, k, ks, waves, s)
-                      : run_xp<4, TILED, XOP, ROPE>(jobs, x, xa, k, ks, waves, s);
+        return d == 8 ? run_xp<8, TILED, XOP, EPI>(jobs, x, xa, k, ks, waves, s)
+                      : run_xp<4, TILED, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
     }
 }
 
@@ -483,8 +489,8 @@ size_t q4k_m1_lds_bytes(int64_t k) { return mfma_gemv_lds_bytes(k, kMaxThreads /
 
 hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* const* y, const int64_t* n,
                               const float* x, const float* aux, float eps, int64_t k, hipStream_t s,
-                              const float* inv_freq, int pos, int head_dim, int rope_jobs) {
-    if (count < 1 || count > kMaxJobs || aux == nullptr) return hipErrorInvalidValue;
+                              const float* inv_freq, int pos, int head_dim, int rope_jobs, bool add) {
+    if (count < 1 || count > kMaxJobs || (aux == nullptr && xop != kXNone)) return hipErrorInvalidValue;
     Jobs jobs{};
     jobs.count = count;
     int64_t tiles = 0;
@@ -511,8 +517,15 @@ hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* 
         xa.rope.head_dim = head_dim;
         xa.rope.jobs = rope_jobs;
         switch (xop) {
-            case kXRmsNorm: return dispatch<true, kXRmsNorm, true>(jobs, x, k, s, xa);
-            case kXRmsNorm1: return dispatch<true, kXRmsNorm1, true>(jobs, x, k, s, xa);
+            case kXRmsNorm: return dispatch<true, kXRmsNorm, kEpiRope>(jobs, x, k, s, xa);
+            case kXRmsNorm1: return dispatch<true, kXRmsNorm1, kEpiRope>(jobs, x, k, s, xa);
+            default: return hipErrorInvalidValue;
+        }
+    }
+    if (add) {
+        switch (xop) {
+            case kXNone: return dispatch<true, kXNone, kEpiAdd>(jobs, x, k, s, xa);
+            case kXSwiGlu: return dispatch<true, kXSwiGlu, kEpiAdd>(jobs, x, k, s, xa);
             default: return hipErrorInvalidValue;
         }
     }

@@ -52,15 +52,17 @@ hipError_t launch_attention_decode(const float* q, const float* kc, const float*
 // M = 1 BF16 GEMV with a layer operation applied to x while it is staged
 // (xop as below), k <= 8192.
 hipError_t launch_gemv_bf16_xop(int xop, const uint16_t* w, const float* x, const float* aux, float eps, float* y,
-                                int64_t n, int64_t k, hipStream_t s);
+                                int64_t n, int64_t k, hipStream_t s, bool add = false);
 // Tiled Q4_K GEMVs sharing x, with a layer operation applied to x while it
 // is staged: xop 1 RMSNorm * gamma, 2 RMSNorm * (1 + gamma), 3 silu(x) * aux
 // (aux = gamma or up; eps for the norms).
 // rope_jobs != 0: interleaved RoPE (position pos, inv_freq [head_dim / 2])
 // on the outputs of the jobs in that bit mask; only with an RMSNorm xop.
+// add: y += the product (the residual add); with xop 0 (none) or 3 (SwiGLU).
 hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* const* y, const int64_t* n,
                               const float* x, const float* aux, float eps, int64_t k, hipStream_t s,
-                              const float* inv_freq = nullptr, int pos = 0, int head_dim = 0, int rope_jobs = 0);
+                              const float* inv_freq = nullptr, int pos = 0, int head_dim = 0, int rope_jobs = 0,
+                              bool add = false);
 hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* const* y,
                                       const int64_t* n, const float* x, int64_t k, hipStream_t s,
                                       bool tiled);

@@ -45,6 +45,9 @@ _SIGNATURES = {
                                             C.c_float, _i32, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_swiglu": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_attention_decode": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, C.c_float, _vp],
+    "rt_hip_gemv_q4k_tiled_residual": [_vp, _vp, _vp, _i64, _i64, _vp],
+    "rt_hip_gemv_q4k_tiled_swiglu_residual": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
+    "rt_hip_gemv_bf16_swiglu_residual": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_rmsnorm_rope": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp,
                                            C.c_float, _i32, _vp, _i32, _i32, _i32, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_bf16_rmsnorm": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp, _i64,
@@ -296,6 +299,21 @@ def gemv_q4k_tiled_rmsnorm_rope(ws, x, gamma, eps: float, ns, k: int, inv_freq, 
     library().call("rt_hip_gemv_q4k_tiled_rmsnorm_rope", count, wp, yp, npp, _ptr(x), _ptr(gamma), C.c_float(eps),
                    1 if gemma3 else 0, _ptr(inv_freq), pos, head_dim, rope_jobs, k, _stream(stream))
     return ys
+
+
+def gemv_q4k_tiled_residual(w, x, resid, n: int, k: int, stream=None):
+    """resid += W . x (tiled Q4_K)."""
+    _dev_check(w, x, resid)
+    library().call("rt_hip_gemv_q4k_tiled_residual", _ptr(w), _ptr(x), _ptr(resid), n, k, _stream(stream))
+    return resid
+
+
+def gemv_swiglu_residual(fmt: int, w, gate, up, resid, n: int, k: int, stream=None):
+    """resid += W . (silu(gate) * up), W tiled Q4_K (fmt Q4K) or BF16 bits."""
+    _dev_check(w, gate, up, resid)
+    name = "rt_hip_gemv_q4k_tiled_swiglu_residual" if fmt == Q4K else "rt_hip_gemv_bf16_swiglu_residual"
+    library().call(name, _ptr(w), _ptr(gate), _ptr(up), _ptr(resid), n, k, _stream(stream))
+    return resid
 
 
 def attention_decode(q, k_cache, v_cache, seq_len: int, n_q: int, n_kv: int, scale: float, head_dim: int = 128,

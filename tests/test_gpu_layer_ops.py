@@ -188,3 +188,35 @@ def test_attention_decode_is_deterministic_and_rejects_bad_shapes(rt):
                       C.c_float(0.1), None) == E_SHAPE
     assert lib.status("rt_hip_attention_decode", p, kc.data_ptr(), vc.data_ptr(), p, 24, 8, 128, 0,
                       C.c_float(0.1), None) == E_SHAPE
+
+
+def test_residual_adds(rt, orc):
+    """resid += W . x and resid += W . (silu(gate) * up), Q4_K and BF16."""
+    rng = np.random.default_rng(31)
+    k, n = 3072, 3072
+    (b,) = _weights(orc, rng, [n], k)
+    t = rt.q4k_tile(to_dev(b), n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    r0 = rng.standard_normal(n).astype(np.float32)
+    resid = to_dev(r0)
+    rt.gemv_q4k_tiled_residual(t, to_dev(x), resid, n, k)
+    want = r0 + orc.q4k_matmul_t(b, n, k, x.reshape(1, k)).reshape(-1)
+    assert normwise_err(from_dev(resid), want) <= GEMV_TOL
+    kf = 8192
+    (bd,) = _weights(orc, rng, [n], kf)
+    td = rt.q4k_tile(to_dev(bd), n, kf)
+    gate = (rng.standard_normal(kf) * 2).astype(np.float32)
+    up = rng.standard_normal(kf).astype(np.float32)
+    act = orc.swiglu(gate, up).reshape(1, kf)
+    resid = to_dev(r0)
+    rt.gemv_swiglu_residual(rt.Q4K, td, to_dev(gate), to_dev(up), resid, n, kf)
+    assert normwise_err(from_dev(resid), r0 + orc.q4k_matmul_t(bd, n, kf, act).reshape(-1)) <= GEMV_TOL
+    wb = orc.f32_to_bf16_n((rng.standard_normal((n, kf)) * 0.02).astype(np.float32))
+    resid = to_dev(r0)
+    rt.gemv_swiglu_residual(rt.BF16, to_dev(wb.view(np.int16)), to_dev(gate), to_dev(up), resid, n, kf)
+    assert normwise_err(from_dev(resid), r0 + orc.bf16_matmul_t(wb, act).reshape(-1)) <= GEMV_TOL
+    # an aliased residual is refused
+    lib = rt.library()
+    xd = to_dev(x)
+    assert lib.status("rt_hip_gemv_q4k_tiled_residual", t.data_ptr(), xd.data_ptr(), xd.data_ptr(), n, k,
+                      None) == E_ARG
