@@ -141,20 +141,44 @@ __global__ __launch_bounds__(kT) void k_attn_partial(const float* __restrict__ q
 }
 
 // One workgroup of 128 threads per query head: fold the splits in order.
+// Up to kBatch splits load in one batch (indices past S repeat split S - 1,
+// in bounds, and get weight 0), so the merge costs one memory latency.
+constexpr int kBatch = 32;
+
 __global__ __launch_bounds__(kHd) void k_attn_combine(const float* __restrict__ part, float* __restrict__ out,
                                                       int S) {
     const int h = blockIdx.x, d = threadIdx.x;
     const float* ph = part + static_cast<int64_t>(h) * S * kPart;
-    float M = -__builtin_inff();
+    float M = -__builtin_inff(), L = 0.0f, O = 0.0f;
+    if (S <= kBatch) {
+        float ms[kBatch], ls[kBatch], os[kBatch];
+#pragma unroll
+        for (int s = 0; s < kBatch; ++s) {
+            const float* ps = ph + min(s, S - 1) * kPart;
+            ms[s] = ps[0];
+            ls[s] = ps[1];
+            os[s] = ps[2 + d];
+        }
+#pragma unroll
+        for (int s = 0; s < kBatch; ++s) M = fmaxf(M, ms[s]);
+        if (M != -__builtin_inff()) {
+#pragma unroll
+            for (int s = 0; s < kBatch; ++s) {
+                const float w = s < S ? exp_fast(ms[s] - M) : 0.0f;
+                L += ls[s] * w;
+                O += os[s] * w;
+            }
+        }
+    } else {
 #pragma unroll 8
-    for (int s = 0; s < S; ++s) M = fmaxf(M, ph[s * kPart]);
-    float L = 0.0f, O = 0.0f;
-    if (M != -__builtin_inff()) {
+        for (int s = 0; s < S; ++s) M = fmaxf(M, ph[s * kPart]);
+        if (M != -__builtin_inff()) {
 #pragma unroll 8
-        for (int s = 0; s < S; ++s) {
-            const float w = exp_fast(ph[s * kPart] - M);
-            L += ph[s * kPart + 1] * w;
-            O += ph[s * kPart + 2 + d] * w;
+            for (int s = 0; s < S; ++s) {
+                const float w = exp_fast(ph[s * kPart] - M);
+                L += ph[s * kPart + 1] * w;
+                O += ph[s * kPart + 2 + d] * w;
+            }
         }
     }
     out[static_cast<int64_t>(h) * kHd + d] = L > 0.0f ? O / L : 0.0f;

@@ -190,6 +190,24 @@ def test_attention_decode_is_deterministic_and_rejects_bad_shapes(rt):
                       C.c_float(0.1), None) == E_SHAPE
 
 
+def test_attention_decode_back_to_back_shapes(rt, orc):
+    """Calls in a row whose split counts and KV-head counts differ (1 KV head
+    and 79 splits, past the one-batch merge; 64 KV heads; 1 split): every
+    call matches the oracle."""
+    d = 128
+    scale = float(1.0 / np.sqrt(np.float32(d)))
+    for i, (nq, nkv, seq_len) in enumerate([(4, 1, 5000), (24, 8, 300), (64, 64, 700), (24, 8, 4096),
+                                            (4, 1, 5000), (3, 1, 64)]):
+        say(f"[attention back-to-back] call {i}: n_q={nq} n_kv={nkv} L={seq_len}")
+        rng = np.random.default_rng(100 + i)
+        kc = rng.standard_normal((seq_len, nkv * d)).astype(np.float32)
+        vc = rng.standard_normal((seq_len, nkv * d)).astype(np.float32)
+        q = (rng.standard_normal(nq * d) * 0.5).astype(np.float32)
+        got = from_dev(rt.attention_decode(to_dev(q), to_dev(kc), to_dev(vc), seq_len, nq, nkv, scale)).reshape(-1)
+        want = orc.gqa_attention_decode(q, kc, vc, seq_len, nq, nkv, d, scale)
+        assert normwise_err(got, want) <= GEMV_TOL, (i, normwise_err(got, want))
+
+
 def test_residual_adds(rt, orc):
     """resid += W . x and resid += W . (silu(gate) * up), Q4_K and BF16."""
     rng = np.random.default_rng(31)
