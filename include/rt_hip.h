@@ -107,6 +107,16 @@ int rt_hip_gemv_q4k_multi(int32_t count, const void* const* blocks, float* const
  * rt_hip_q4k_tile: device blocks -> device tiled copy (not in place). */
 int64_t rt_hip_q4k_tiled_bytes(int64_t n, int64_t k);
 int rt_hip_q4k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, rt_hip_stream stream);
+/* rt_hip_q4k_tile_rope_half: rt_hip_q4k_tile for a q or k projection whose
+ * output takes RoPE in the half-split pairing (llama_rope,
+ * src/transformer5.cpp:95-125, RopePairing::HalfSplit: HuggingFace's
+ * weights).  The rows of each head of head_dim rows are interleaved on the
+ * way (tiled row 2j <- row j, 2j + 1 <- row j + head_dim / 2), so that each
+ * rotated pair is two adjacent rows; rt_hip_gemv_q4k_tiled_rmsnorm_rope with
+ * RT_HIP_ROPE_HALF stores them back in place.  n % head_dim == 0, head_dim
+ * even.  The values are not changed. */
+int rt_hip_q4k_tile_rope_half(const void* blocks, void* tiled, int64_t n, int64_t k, int32_t head_dim,
+                              rt_hip_stream stream);
 
 /* M == 1 Q4_K GEMV on a tiled copy: same contract and results as
  * rt_hip_gemv_q4k (m == 1) / rt_hip_gemv_q4k_multi.
@@ -168,7 +178,12 @@ int rt_hip_gemv_q4k_tiled_swiglu(const void* tiled, const float* gate, const flo
  * inv_freq [head_dim / 2] is the caller's (Config5::inv_freq,
  * transformer5.cpp:36-52).  Writing k and v through y pointers into the KV
  * cache rows of position pos is LlamaLayerKvCache::append (:59-68).  Each
- * rotated job's n must be a multiple of head_dim (even). */
+ * rotated job's n must be a multiple of head_dim (even).
+ * rope_jobs | RT_HIP_ROPE_HALF selects RopePairing::HalfSplit instead: pair
+ * (i, i + head_dim/2), angle pos * inv_freq[i], with the rotated jobs'
+ * weights tiled by rt_hip_q4k_tile_rope_half (the other jobs' by
+ * rt_hip_q4k_tile). */
+#define RT_HIP_ROPE_HALF 0x100
 int rt_hip_gemv_q4k_tiled_rmsnorm_rope(int32_t count, const void* const* tiled, float* const* y, const int64_t* n,
                                        const float* x, const float* gamma, float eps, int32_t gemma3,
                                        const float* inv_freq, int32_t pos, int32_t head_dim, int32_t rope_jobs,

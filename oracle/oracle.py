@@ -75,6 +75,7 @@ class Oracle:
         self._swiglu = _bind(L, "orc_swiglu", None, _f32p, _f32p, _sz, _f32p)
         self._inv_freq = _bind(L, "orc_llama_inv_freq", None, C.c_float, _sz, _f32p, _sz, _f32p)
         self._rope = _bind(L, "orc_llama_rope_interleaved", None, _f32p, _sz, _sz, _sz, _f32p, _f32p)
+        self._rope_half = _bind(L, "orc_llama_rope_half", None, _f32p, _sz, _sz, _sz, _f32p, _f32p)
         self._attn = _bind(L, "orc_gqa_attention_decode", None, _f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _sz,
                            C.c_float, _f32p)
         self._argmax = _bind(L, "orc_argmax_first", C.c_int64, _f32p, _sz)
@@ -98,11 +99,14 @@ class Oracle:
         self._inv_freq(theta, head_dim, d, 0 if divisors is None else d.size, out)
         return out
 
-    def llama_rope(self, x: np.ndarray, n_heads: int, head_dim: int, pos: int, inv_freq: np.ndarray) -> np.ndarray:
-        """Interleaved-pairing RoPE of one row [n_heads * head_dim]."""
+    def llama_rope(self, x: np.ndarray, n_heads: int, head_dim: int, pos: int, inv_freq: np.ndarray,
+                   half: bool = False) -> np.ndarray:
+        """RoPE of one row [n_heads * head_dim]: interleaved pairing, or the
+        half-split pairing with half=True."""
         xx = np.ascontiguousarray(x, np.float32).reshape(-1)
         out = np.empty_like(xx)
-        self._rope(xx, n_heads, head_dim, pos, np.ascontiguousarray(inv_freq, np.float32), out)
+        fn = self._rope_half if half else self._rope
+        fn(xx, n_heads, head_dim, pos, np.ascontiguousarray(inv_freq, np.float32), out)
         return out.reshape(np.shape(x))
 
     def gqa_attention_decode(self, q, k_cache, v_cache, seq_len: int, n_q: int, n_kv: int, d: int,

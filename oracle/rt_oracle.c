@@ -679,6 +679,26 @@ void orc_llama_rope_interleaved(const float* x, size_t n_heads, size_t head_dim,
     }
 }
 
+/* llama_rope on one row, RopePairing::HalfSplit (src/transformer5.cpp:
+ * 95-125, the pairing of HuggingFace's weights): pair (i, i + head_dim/2)
+ * of each head, a = pos * inv_freq[i], out_i = x0 cos - x1 sin,
+ * out_{i+half} = x0 sin + x1 cos. */
+void orc_llama_rope_half(const float* x, size_t n_heads, size_t head_dim, size_t pos, const float* inv_freq,
+                         float* out) {
+    const size_t half = head_dim / 2;
+    memcpy(out, x, n_heads * head_dim * sizeof(float));
+    for (size_t i = 0; i < half; ++i) {
+        const float angle = (float)pos * inv_freq[i];
+        const float c = cosf(angle), s = sinf(angle);
+        for (size_t h = 0; h < n_heads; ++h) {
+            const size_t c0 = h * head_dim + i, c1 = c0 + half;
+            const float x0 = x[c0], x1 = x[c1];
+            out[c0] = x0 * c - x1 * s;
+            out[c1] = x0 * s + x1 * c;
+        }
+    }
+}
+
 /* gqa_attention_cached, decode path (src/transformer4.cpp:379-432): one
  * query row; for each query head, scores[c] = dot(q_h, k_h[c]) * scale over
  * c in [k_start, k_end) (sequential dot), max, exp(s - max) summed in order,

@@ -139,6 +139,8 @@ void orc_llama_inv_freq(float theta, size_t head_dim, const float* divisors, siz
 void orc_gqa_attention_decode(const float* q, const float* k_cache, const float* v_cache, size_t k_start,
                               size_t k_end, size_t n_q_heads, size_t n_kv_heads, size_t d_head, float scale,
                               float* out);
+void orc_llama_rope_half(const float* x, size_t n_heads, size_t head_dim, size_t pos, const float* inv_freq,
+                         float* out);
 void orc_llama_rope_interleaved(const float* x, size_t n_heads, size_t head_dim, size_t pos, const float* inv_freq,
                                 float* out);
 void orc_swiglu(const float* gate, const float* up, size_t n, float* out);

@@ -234,17 +234,30 @@ int64_t rt_hip_q4k_tiled_bytes(int64_t n, int64_t k) {
     return (n + 15) / 16 * 16 * (k / 256) * 144;
 }
 
-int rt_hip_q4k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, rt_hip_stream stream) {
-    if (!blocks || !tiled) return fail(RT_HIP_E_ARG, "rt_hip_q4k_tile: null pointer");
+static int q4k_tile(const char* fn, const void* blocks, void* tiled, int64_t n, int64_t k, int32_t head_dim,
+                    rt_hip_stream stream) {
+    if (!blocks || !tiled) return fail(RT_HIP_E_ARG, std::string(fn) + ": null pointer");
     if (rt_hip_q4k_tiled_bytes(n, k) < 0)
-        return fail(RT_HIP_E_SHAPE, "rt_hip_q4k_tile: need n > 0, k > 0, k % 256 == 0, int32 sizes");
+        return fail(RT_HIP_E_SHAPE, std::string(fn) + ": need n > 0, k > 0, k % 256 == 0, int32 sizes");
     if (!aligned16(blocks) || !aligned16(tiled))
-        return fail(RT_HIP_E_ALIGN, "rt_hip_q4k_tile: blocks and tiled must be 16-byte aligned");
-    if (blocks == tiled) return fail(RT_HIP_E_ARG, "rt_hip_q4k_tile: in-place tiling is not supported");
+        return fail(RT_HIP_E_ALIGN, std::string(fn) + ": blocks and tiled must be 16-byte aligned");
+    if (blocks == tiled) return fail(RT_HIP_E_ARG, std::string(fn) + ": in-place tiling is not supported");
     hipError_t e;
-    if (!state_for_current(&e)) return hip_fail(e, "rt_hip_q4k_tile");
-    return check_stream_launch(launch_q4k_tile(blocks, tiled, n, k, static_cast<hipStream_t>(stream)),
-                               "rt_hip_q4k_tile");
+    if (!state_for_current(&e)) return hip_fail(e, fn);
+    return check_stream_launch(launch_q4k_tile(blocks, tiled, n, k, static_cast<hipStream_t>(stream), head_dim),
+                               fn);
+}
+
+int rt_hip_q4k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, rt_hip_stream stream) {
+    return q4k_tile("rt_hip_q4k_tile", blocks, tiled, n, k, 0, stream);
+}
+
+int rt_hip_q4k_tile_rope_half(const void* blocks, void* tiled, int64_t n, int64_t k, int32_t head_dim,
+                              rt_hip_stream stream) {
+    const char* fn = "rt_hip_q4k_tile_rope_half";
+    if (head_dim < 2 || head_dim % 2 != 0) return fail(RT_HIP_E_ARG, std::string(fn) + ": head_dim must be even");
+    if (n % head_dim != 0) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": n is not whole heads");
+    return q4k_tile(fn, blocks, tiled, n, k, head_dim, stream);
 }
 
 int rt_hip_gemv_q4k_tiled_multi(int32_t count, const void* const* tiled, float* const* y,
@@ -304,10 +317,11 @@ int rt_hip_gemv_q4k_tiled_rmsnorm_rope(int32_t count, const void* const* tiled, 
     if (!inv_freq) return fail(RT_HIP_E_ARG, std::string(fn) + ": null inv_freq");
     if (pos < 0) return fail(RT_HIP_E_ARG, std::string(fn) + ": pos must be >= 0");
     if (head_dim < 2 || head_dim % 2 != 0) return fail(RT_HIP_E_ARG, std::string(fn) + ": head_dim must be even");
-    if (rope_jobs <= 0 || rope_jobs >= (1 << count))
+    const int32_t mask = rope_jobs & ~RT_HIP_ROPE_HALF;
+    if (mask <= 0 || mask >= (1 << count))
         return fail(RT_HIP_E_ARG, std::string(fn) + ": rope_jobs must name jobs in [0, count)");
     for (int32_t j = 0; j < count; ++j)
-        if (((rope_jobs >> j) & 1) && n[j] % head_dim != 0)
+        if (((mask >> j) & 1) && n[j] % head_dim != 0)
             return fail(RT_HIP_E_SHAPE, std::string(fn) + ": a rotated output is not whole heads");
     return gemv_xop(fn, gemma3 ? 2 : 1, count, tiled, y, n, x, gamma, eps, k, stream, inv_freq, pos, head_dim,
                     rope_jobs);

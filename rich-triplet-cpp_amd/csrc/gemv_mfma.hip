@@ -59,6 +59,7 @@ struct Rope {
     int pos = 0;
     int head_dim = 0;
     int jobs = 0;
+    int half = 0;  // half-split pairing: rows of rotated jobs tiled interleaved
 };
 
 // Job-table fields read into scalar registers through readfirstlane, and
@@ -305,6 +306,16 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     const bool keep = row < n_job;  // false for tile slots past the last tile
     const Four<uint64_t> ys = {sreg(jobs.y[0]), sreg(jobs.y[1]), sreg(jobs.y[2]), sreg(jobs.y[3])};
     float* const yj = reinterpret_cast<float*>(ys[job]);
+    // Where the row is stored: with the half-split pairing the rows of a
+    // rotated job were tiled interleaved (row 2j of a head holds element j,
+    // row 2j + 1 element j + head_dim / 2), and go back to their places here.
+    int drow = row;
+    if constexpr (EPI == kEpiRope) {
+        if (rope.half && ((rope.jobs >> job) & 1)) {
+            const int r = row % rope.head_dim;
+            drow = row - r + (r >> 1) + ((r & 1) ? rope.head_dim / 2 : 0);
+        }
+    }
     // The row's final value, computed by every lane of the storing wave (the
     // RoPE partner exchange needs the whole wave).
     auto finish = [&](float val) {
@@ -322,7 +333,7 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     };
     if (KS == 1) {
         const float out = finish(v);
-        if (lane < 16 && keep) yj[row] = EPI == kEpiAdd ? yj[row] + out : out;
+        if (lane < 16 && keep) yj[drow] = EPI == kEpiAdd ? yj[drow] + out : out;
     } else {
         float* red = reinterpret_cast<float*>(lds + lds_bytes(K));  // [TPW][KS][16]
         float* rp = red + tslot * KS * 16;
@@ -333,7 +344,7 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
 #pragma unroll
             for (int q = 1; q < KS; ++q) s += rp[q * 16 + (lane & 15)];
             const float out = finish(s);
-            if (lane < 16 && keep) yj[row] = EPI == kEpiAdd ? yj[row] + out : out;
+            if (lane < 16 && keep) yj[drow] = EPI == kEpiAdd ? yj[drow] + out : out;
         }
     }
 }
@@ -515,7 +526,8 @@ hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* 
         xa.rope.inv_freq = inv_freq;
         xa.rope.pos = pos;
         xa.rope.head_dim = head_dim;
-        xa.rope.jobs = rope_jobs;
+        xa.rope.jobs = rope_jobs & 0xff;
+        xa.rope.half = (rope_jobs >> 8) & 1;
         switch (xop) {
             case kXRmsNorm: return dispatch<true, kXRmsNorm, kEpiRope>(jobs, x, k, s, xa);
             case kXRmsNorm1: return dispatch<true, kXRmsNorm1, kEpiRope>(jobs, x, k, s, xa);

@@ -233,10 +233,13 @@ __global__ __launch_bounds__(256) void k_quantize_q4k(const float* __restrict__ 
 
 // Reference row-major Q4_K blocks -> tiled layout (q4k_mfma.hpp): one thread
 // per (tile, super-block, lane) writes that lane's header dword and its two
-// 16-byte halves of qs; rows past N are written as zeros.
+// 16-byte halves of qs; rows past N are written as zeros.  With hd > 0 the
+// rows of each head of hd rows are interleaved on the way: tiled row 2j of a
+// head takes source row j, row 2j + 1 takes source row j + hd / 2 (the
+// half-split RoPE pairs become adjacent rows).
 __global__ __launch_bounds__(256) void k_q4k_tile(const uint8_t* __restrict__ src,
                                                   uint8_t* __restrict__ dst, int64_t n, int nb,
-                                                  int64_t threads) {
+                                                  int64_t threads, int hd) {
     const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (gid >= threads) return;
     const int l = static_cast<int>(gid & 63);
@@ -249,7 +252,12 @@ __global__ __launch_bounds__(256) void k_q4k_tile(const uint8_t* __restrict__ sr
     uint32_t hdr = 0;
     u32x4 qa = {0u, 0u, 0u, 0u}, qb = {0u, 0u, 0u, 0u};
     if (row < n) {
-        const uint8_t* blk = src + (row * nb + b) * kQ4kBlockBytes;
+        int64_t srow = row;
+        if (hd > 0) {
+            const int64_t r = row % hd;
+            srow = row - r + (r >> 1) + ((r & 1) ? hd / 2 : 0);
+        }
+        const uint8_t* blk = src + (srow * nb + b) * kQ4kBlockBytes;
         const u32x4 h = ld16(blk);
         uint32_t sv0, mv0, sv1, mv1;
         decode_scale_min(make_scale_sel(2 * g), h[1], h[2], h[3], sv0, mv0);
@@ -302,13 +310,13 @@ hipError_t launch_quantize_q4k(const float* w, void* blocks, int64_t n, int64_t 
     return hipGetLastError();
 }
 
-hipError_t launch_q4k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, hipStream_t s) {
+hipError_t launch_q4k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, hipStream_t s, int head_dim) {
     const int nb = static_cast<int>(k / 256);
     const int64_t threads = (n + 15) / 16 * nb * 64;
     const int64_t grid = (threads + 255) / 256;
     hipLaunchKernelGGL(k_q4k_tile, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s,
                        static_cast<const uint8_t*>(blocks), static_cast<uint8_t*>(tiled), n, nb,
-                       threads);
+                       threads, head_dim);
     return hipGetLastError();
 }
 

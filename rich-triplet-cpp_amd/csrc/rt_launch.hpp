@@ -70,7 +70,8 @@ hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* co
 // worst case over the splits it picks (the callers' K bound: <= 64 KB).
 size_t mfma_gemv_lds_bytes(int64_t k, int waves);
 size_t q4k_m1_lds_bytes(int64_t k);
-hipError_t launch_q4k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, hipStream_t s);
+// head_dim > 0: interleave each head's rows (2j <- j, 2j + 1 <- j + head_dim / 2).
+hipError_t launch_q4k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, hipStream_t s, int head_dim = 0);
 // Up to four tiled-Q4_K GEMVs and one BF16 GEMV sharing x (K <= 8192) in one
 // launch; LDS: q4k_bf16_fused_lds_bytes(k).
 size_t q4k_bf16_fused_lds_bytes(int64_t k);

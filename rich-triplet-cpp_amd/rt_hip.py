@@ -28,6 +28,7 @@ _SIGNATURES = {
     "rt_hip_gemv_bf16": [_vp, _vp, _vp, _i64, _i64, _i32, _vp],
     "rt_hip_gemv_q4k_multi": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _i64, _vp],
     "rt_hip_q4k_tile": [_vp, _vp, _i64, _i64, _vp],
+    "rt_hip_q4k_tile_rope_half": [_vp, _vp, _i64, _i64, _i32, _vp],
     "rt_hip_gemv_q4k_tiled": [_vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_multi": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _i64, _vp],
     "rt_hip_gemv_q4_0": [_vp, _vp, _vp, _i64, _i64, _i32, _vp],
@@ -214,15 +215,25 @@ def q4k_tiled_bytes(n: int, k: int) -> int:
     return library().lib.rt_hip_q4k_tiled_bytes(n, k)
 
 
-def q4k_tile(blocks, n: int, k: int, stream=None):
-    """Tiled copy of row-major Q4_K blocks (for gemv_q4k_tiled*)."""
+# rope_jobs flag of gemv_q4k_tiled_rmsnorm_rope: the half-split RoPE pairing.
+ROPE_HALF = 0x100
+
+
+def q4k_tile(blocks, n: int, k: int, stream=None, rope_half_head_dim: int = 0):
+    """Tiled copy of row-major Q4_K blocks (for gemv_q4k_tiled*).  With
+    rope_half_head_dim, each head's rows are interleaved for a q / k
+    projection rotated in the half-split pairing (rope_jobs | ROPE_HALF)."""
     torch = _torch()
     size = q4k_tiled_bytes(n, k)
     if size < 0:
         raise ValueError(f"rt_hip: invalid Q4_K shape n={n} k={k}")
     tiled = torch.empty(size, dtype=torch.uint8, device=blocks.device)
     _dev_check(blocks)
-    library().call("rt_hip_q4k_tile", _ptr(blocks), _ptr(tiled), n, k, _stream(stream))
+    if rope_half_head_dim:
+        library().call("rt_hip_q4k_tile_rope_half", _ptr(blocks), _ptr(tiled), n, k, rope_half_head_dim,
+                       _stream(stream))
+    else:
+        library().call("rt_hip_q4k_tile", _ptr(blocks), _ptr(tiled), n, k, _stream(stream))
     return tiled
 
 
@@ -286,7 +297,8 @@ def gemv_q4k_tiled_rmsnorm_multi(ws, x, gamma, eps: float, ns, k: int, gemma3: b
 def gemv_q4k_tiled_rmsnorm_rope(ws, x, gamma, eps: float, ns, k: int, inv_freq, pos: int, head_dim: int,
                                 rope_jobs: int, gemma3: bool = False, ys=None, stream=None):
     """gemv_q4k_tiled_rmsnorm_multi, then interleaved RoPE at `pos` on the
-    outputs of the jobs in the bit mask rope_jobs; ys may point into a KV
+    outputs of the jobs in the bit mask rope_jobs (| ROPE_HALF: half-split
+    pairing, weights tiled with rope_half_head_dim); ys may point into a KV
     cache (the append)."""
     torch = _torch()
     count = len(ws)

@@ -149,6 +149,39 @@ def test_rmsnorm_rope_qkv_into_kv_cache(rt, orc, pos):
     assert not np.any(from_dev(kc)[others]) and not np.any(from_dev(vc)[others])
 
 
+@pytest.mark.parametrize("pos", [0, 3, 1000, 70000])
+def test_rmsnorm_rope_half_split_qkv(rt, orc, pos):
+    """The half-split pairing (HuggingFace weights): q and k tiled with their
+    head rows interleaved (rt_hip_q4k_tile_rope_half), v tiled plainly, one
+    launch with rope_jobs 0x3 | ROPE_HALF; outputs back in their places."""
+    import torch
+    k, hd, nq, nkv = 3072, 128, 24, 8
+    ns = [nq * hd, nkv * hd, nkv * hd]
+    say(f"[rmsnorm+rope half qkv] pos={pos}")
+    rng = np.random.default_rng(pos + 11)
+    blocks = _weights(orc, rng, ns, k)
+    x = (rng.standard_normal(k) * 2).astype(np.float32)
+    gamma = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    inv = orc.llama_inv_freq(500000.0, hd)
+    tiled = [rt.q4k_tile(to_dev(b), n, k, rope_half_head_dim=(hd if i < 2 else 0))
+             for i, (b, n) in enumerate(zip(blocks, ns))]
+    ys = [torch.full((1, n), float("nan"), device="cuda") for n in ns]
+    rt.gemv_q4k_tiled_rmsnorm_rope(tiled, to_dev(x), to_dev(gamma), 1e-5, ns, k, to_dev(inv), pos, hd,
+                                   0x3 | rt.ROPE_HALF, ys=ys)
+    xn = orc.rmsnorm(x, gamma, 1e-5).reshape(1, k)
+    lin = [orc.q4k_matmul_t(b, n, k, xn).reshape(-1) for b, n in zip(blocks, ns)]
+    got = [from_dev(y).reshape(-1) for y in ys]
+    assert all(np.all(np.isfinite(g)) for g in got)  # every element stored
+    assert normwise_err(got[0], orc.llama_rope(lin[0], nq, hd, pos, inv, half=True)) <= GEMV_TOL
+    assert normwise_err(got[1], orc.llama_rope(lin[1], nkv, hd, pos, inv, half=True)) <= GEMV_TOL
+    assert normwise_err(got[2], lin[2]) <= GEMV_TOL
+    lib = rt.library()
+    b0 = to_dev(blocks[1])
+    out = torch.empty(rt.q4k_tiled_bytes(ns[1], k), dtype=torch.uint8, device="cuda")
+    assert lib.status("rt_hip_q4k_tile_rope_half", b0.data_ptr(), out.data_ptr(), ns[1], k, 127, None) == 1
+    assert lib.status("rt_hip_q4k_tile_rope_half", b0.data_ptr(), out.data_ptr(), 1000, k, 128, None) == E_SHAPE
+
+
 @pytest.mark.parametrize("nq,nkv,seq_len", [(24, 8, 1), (24, 8, 7), (24, 8, 300), (24, 8, 4096), (32, 8, 1000),
                                             (8, 8, 129), (16, 8, 50)])
 def test_attention_decode(rt, orc, nq, nkv, seq_len):

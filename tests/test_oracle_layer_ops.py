@@ -104,6 +104,33 @@ def test_llama_rope_interleaved(orc):
         assert np.allclose(np.hypot(g2[..., 0], g2[..., 1]), np.hypot(x2[..., 0], x2[..., 1]), rtol=1e-5)
 
 
+def test_llama_rope_half_split(orc):
+    """Half-split pairing (i, i + head_dim/2): pos 0 is the identity; a float64
+    rotation by the same f32 angles; and, bit for bit, the interleaved
+    rotation of the head-wise permuted row (2j <- j, 2j+1 <- j + half),
+    permuted back -- the identity the GPU path's row permutation uses."""
+    rng = np.random.default_rng(8)
+    n_heads, hd = 8, 128
+    half = hd // 2
+    inv = orc.llama_inv_freq(500000.0, hd)
+    x = rng.standard_normal(n_heads * hd).astype(np.float32)
+    assert np.array_equal(orc.llama_rope(x, n_heads, hd, 0, inv, half=True), x)
+    perm = np.concatenate([h * hd + np.stack([np.arange(half), np.arange(half) + half], axis=1).reshape(-1)
+                           for h in range(n_heads)])  # interleaved slot -> half-split index
+    for pos in (1, 17, 1000, 100000):
+        got = orc.llama_rope(x, n_heads, hd, pos, inv, half=True)
+        ang = (np.float32(pos) * inv).astype(np.float32).astype(np.float64)
+        c, s = np.cos(ang), np.sin(ang)
+        x3 = x.astype(np.float64).reshape(n_heads, 2, half)
+        want = np.stack([x3[:, 0] * c - x3[:, 1] * s, x3[:, 0] * s + x3[:, 1] * c], axis=1).reshape(-1)
+        assert np.allclose(got, want, rtol=0, atol=1e-5 * np.abs(x).max()), pos
+        inter = orc.llama_rope(x[perm], n_heads, hd, pos, inv)
+        back = np.empty_like(inter)
+        back[perm] = inter
+        assert np.array_equal(back, got), pos
+        assert not np.array_equal(got, orc.llama_rope(x, n_heads, hd, pos, inv)), pos  # the pairings differ
+
+
 def test_gqa_attention_decode(orc):
     rng = np.random.default_rng(7)
     nq, nkv, d = 6, 2, 128
