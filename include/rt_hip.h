@@ -227,6 +227,17 @@ int rt_hip_gemv_q4k_tiled_bf16_rmsnorm(int32_t count, const void* const* tiled, 
                                        rt_hip_stream stream);
 int rt_hip_gemv_bf16_swiglu(const uint16_t* w, const float* gate, const float* up, float* y, int64_t n, int64_t k,
                             rt_hip_stream stream);
+/* rt_hip_gemv_q4k_tiled_bf16_rmsnorm_rope: rt_hip_gemv_q4k_tiled_bf16_rmsnorm
+ * plus RoPE on the Q4_K jobs in rope_jobs, as rt_hip_gemv_q4k_tiled_rmsnorm_rope
+ * (llama_rope, src/transformer5.cpp:95-125; RT_HIP_ROPE_HALF for the
+ * half-split pairing), and the KV-cache append through the y pointers
+ * (LlamaLayerKvCache::append, :59-68): the q/k/v launch of a Q4_K_M layer
+ * whose v is BF16 (src/transformer4_load.cpp:141-143). */
+int rt_hip_gemv_q4k_tiled_bf16_rmsnorm_rope(int32_t count, const void* const* tiled, float* const* y,
+                                            const int64_t* n, const uint16_t* w_bf16, float* y_bf16,
+                                            int64_t n_bf16, const float* x, const float* gamma, float eps,
+                                            int32_t gemma3, const float* inv_freq, int32_t pos, int32_t head_dim,
+                                            int32_t rope_jobs, int64_t k, rt_hip_stream stream);
 
 /* ---- decode chain: a step's dependent GEMV stages in one launch -----------
  * Replace: MetalDecodeContext::create / decode_step, the per-token sequence

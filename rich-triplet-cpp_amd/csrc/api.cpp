@@ -379,11 +379,10 @@ int rt_hip_gemv_q4k_tiled_swiglu(const void* tiled, const float* gate, const flo
     return gemv_xop("rt_hip_gemv_q4k_tiled_swiglu", 3, 1, &tiled, &y, &n, gate, up, 0.0f, k, stream);
 }
 
-int rt_hip_gemv_q4k_tiled_bf16_rmsnorm(int32_t count, const void* const* tiled, float* const* y,
-                                       const int64_t* n, const uint16_t* w_bf16, float* y_bf16, int64_t n_bf16,
-                                       const float* x, const float* gamma, float eps, int32_t gemma3, int64_t k,
-                                       rt_hip_stream stream) {
-    const char* fn = "rt_hip_gemv_q4k_tiled_bf16_rmsnorm";
+static int q4k_bf16_rmsnorm(const char* fn, int32_t count, const void* const* tiled, float* const* y,
+                            const int64_t* n, const uint16_t* w_bf16, float* y_bf16, int64_t n_bf16, const float* x,
+                            const float* gamma, float eps, int32_t gemma3, int64_t k, rt_hip_stream stream,
+                            const float* inv_freq, int32_t pos, int32_t head_dim, int32_t rope_jobs) {
     if (count < 1 || count > RT_HIP_MULTI_MAX || !tiled || !y || !n)
         return fail(RT_HIP_E_ARG, std::string(fn) + ": count must be in [1, 4] with arrays");
     for (int32_t j = 0; j < count; ++j) {
@@ -401,8 +400,37 @@ int rt_hip_gemv_q4k_tiled_bf16_rmsnorm(int32_t count, const void* const* tiled, 
     if (!state_for_current(&e)) return hip_fail(e, fn);
     return check_stream_launch(launch_gemv_q4k_bf16_fused(count, tiled, y, n, w_bf16, y_bf16, n_bf16, x, k,
                                                           static_cast<hipStream_t>(stream), gemma3 ? 2 : 1, gamma,
-                                                          eps),
+                                                          eps, inv_freq, pos, head_dim, rope_jobs),
                                fn);
+}
+
+int rt_hip_gemv_q4k_tiled_bf16_rmsnorm(int32_t count, const void* const* tiled, float* const* y,
+                                       const int64_t* n, const uint16_t* w_bf16, float* y_bf16, int64_t n_bf16,
+                                       const float* x, const float* gamma, float eps, int32_t gemma3, int64_t k,
+                                       rt_hip_stream stream) {
+    return q4k_bf16_rmsnorm("rt_hip_gemv_q4k_tiled_bf16_rmsnorm", count, tiled, y, n, w_bf16, y_bf16, n_bf16, x,
+                            gamma, eps, gemma3, k, stream, nullptr, 0, 0, 0);
+}
+
+int rt_hip_gemv_q4k_tiled_bf16_rmsnorm_rope(int32_t count, const void* const* tiled, float* const* y,
+                                            const int64_t* n, const uint16_t* w_bf16, float* y_bf16,
+                                            int64_t n_bf16, const float* x, const float* gamma, float eps,
+                                            int32_t gemma3, const float* inv_freq, int32_t pos, int32_t head_dim,
+                                            int32_t rope_jobs, int64_t k, rt_hip_stream stream) {
+    const char* fn = "rt_hip_gemv_q4k_tiled_bf16_rmsnorm_rope";
+    if (count < 1 || count > RT_HIP_MULTI_MAX || !tiled || !y || !n)
+        return fail(RT_HIP_E_ARG, std::string(fn) + ": count must be in [1, 4] with arrays");
+    if (!inv_freq) return fail(RT_HIP_E_ARG, std::string(fn) + ": null inv_freq");
+    if (pos < 0) return fail(RT_HIP_E_ARG, std::string(fn) + ": pos must be >= 0");
+    if (head_dim < 2 || head_dim % 2 != 0) return fail(RT_HIP_E_ARG, std::string(fn) + ": head_dim must be even");
+    const int32_t mask = rope_jobs & ~RT_HIP_ROPE_HALF;
+    if (mask <= 0 || mask >= (1 << count))
+        return fail(RT_HIP_E_ARG, std::string(fn) + ": rope_jobs must name Q4_K jobs in [0, count)");
+    for (int32_t j = 0; j < count; ++j)
+        if (((mask >> j) & 1) && n[j] % head_dim != 0)
+            return fail(RT_HIP_E_SHAPE, std::string(fn) + ": a rotated output is not whole heads");
+    return q4k_bf16_rmsnorm(fn, count, tiled, y, n, w_bf16, y_bf16, n_bf16, x, gamma, eps, gemma3, k, stream,
+                            inv_freq, pos, head_dim, rope_jobs);
 }
 
 int rt_hip_gemv_bf16_swiglu(const uint16_t* w, const float* gate, const float* up, float* y, int64_t n, int64_t k,

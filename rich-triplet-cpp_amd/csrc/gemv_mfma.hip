@@ -377,16 +377,16 @@ __global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_xop(
 // Pointers first, then the 32-bit arguments, so the fourteen preloaded
 // dwords hold everything a Q4_K workgroup needs before its first loads
 // (the block size is the compile-time bf16_gemv::kThreads).
-template <int XPQ, bool J34, int XPB, int XOP = kXNone>
+template <int XPQ, bool J34, int XPB, int XOP = kXNone, int EPI = kEpiNone>
 __global__ __launch_bounds__(bf16_gemv::kThreads) void k_gemv_q4k_bf16(
     const float* __restrict__ X, const float* __restrict__ aux, const uint8_t* w0, const uint8_t* w1, int K,
     uint32_t split, int q4k_wgs, int n0, int n1, int tile1, const uint16_t* __restrict__ wb, float* __restrict__ yb,
-    int nb_rows, const Jobs jobs, float eps) {
+    int nb_rows, const Jobs jobs, float eps, const Rope rope) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int blk = static_cast<int>(blockIdx.x);
     if (blk < q4k_wgs)
-        q4k_tiles<4, XPQ, true, J34, XOP>(blk, X, K, split, bf16_gemv::kThreads, w0, w1, n0, n1, tile1, jobs, lds,
-                                          aux, eps);
+        q4k_tiles<4, XPQ, true, J34, XOP, EPI>(blk, X, K, split, bf16_gemv::kThreads, w0, w1, n0, n1, tile1, jobs,
+                                               lds, aux, eps, rope);
     else
         bf16_gemv::rows<8, XPB, false, bf16_gemv::kThreads, XOP>(blk - q4k_wgs, (nb_rows + 3) / 4, wb, X, yb,
                                                                  nb_rows, K, nullptr, lds, aux, eps);
@@ -575,35 +575,36 @@ hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* co
 
 namespace {
 
-template <int XPQ, bool J34, int XPB, int XOP>
+template <int XPQ, bool J34, int XPB, int XOP, int EPI>
 hipError_t run_fused(const Jobs& jobs, int ks, int q4k_wgs, const uint16_t* wb, float* yb, int64_t nb_rows,
                      const float* x, const XArgs& xa, int64_t k, size_t lds, hipStream_t s) {
     const int64_t bwgs = (nb_rows + 3) / 4;  // one row per wave, 4 waves
-    hipLaunchKernelGGL((k_gemv_q4k_bf16<XPQ, J34, XPB, XOP>), dim3(static_cast<unsigned>(q4k_wgs + bwgs)),
+    hipLaunchKernelGGL((k_gemv_q4k_bf16<XPQ, J34, XPB, XOP, EPI>), dim3(static_cast<unsigned>(q4k_wgs + bwgs)),
                        dim3(bf16_gemv::kThreads), lds, s, x, xa.aux, jobs.w[0], jobs.w[1], static_cast<int>(k),
                        pack_split(ks, 4 / ks, static_cast<int>((k / 256 + ks - 1) / ks), jobs.count), q4k_wgs,
-                       jobs.n[0], jobs.n[1], jobs.tile0[1], wb, yb, static_cast<int>(nb_rows), jobs, xa.eps);
+                       jobs.n[0], jobs.n[1], jobs.tile0[1], wb, yb, static_cast<int>(nb_rows), jobs, xa.eps,
+                       xa.rope);
     return hipGetLastError();
 }
 
-template <int XOP>
+template <int XOP, int EPI>
 hipError_t fused_xp(const Jobs& jobs, int ks, int q4k_wgs, const uint16_t* wb, float* yb, int64_t nb_rows,
                     const float* x, const XArgs& xa, int64_t k, size_t lds, hipStream_t s) {
     const bool j34 = jobs.count > 2;
     const int64_t per = (k / 4 + 255) / 256;  // f32x4 of x per thread
     if (k <= 4096) {
         if (per <= 2)
-            return j34 ? run_fused<2, true, 4, XOP>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s)
-                       : run_fused<2, false, 4, XOP>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
+            return j34 ? run_fused<2, true, 4, XOP, EPI>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s)
+                       : run_fused<2, false, 4, XOP, EPI>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
         if (per <= 3)
-            return j34 ? run_fused<3, true, 4, XOP>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s)
-                       : run_fused<3, false, 4, XOP>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
-        return j34 ? run_fused<4, true, 4, XOP>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s)
-                   : run_fused<4, false, 4, XOP>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
+            return j34 ? run_fused<3, true, 4, XOP, EPI>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s)
+                       : run_fused<3, false, 4, XOP, EPI>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
+        return j34 ? run_fused<4, true, 4, XOP, EPI>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s)
+                   : run_fused<4, false, 4, XOP, EPI>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
     }
     if (per <= 8)
-        return j34 ? run_fused<8, true, 8, XOP>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s)
-                   : run_fused<8, false, 8, XOP>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
+        return j34 ? run_fused<8, true, 8, XOP, EPI>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s)
+                   : run_fused<8, false, 8, XOP, EPI>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
     return hipErrorInvalidValue;
 }
 
@@ -616,7 +617,8 @@ size_t q4k_bf16_fused_lds_bytes(int64_t k) {
 
 hipError_t launch_gemv_q4k_bf16_fused(int count, const void* const* w, float* const* y, const int64_t* n,
                                       const uint16_t* wb, float* yb, int64_t nb_rows, const float* x,
-                                      int64_t k, hipStream_t s, int xop, const float* aux, float eps) {
+                                      int64_t k, hipStream_t s, int xop, const float* aux, float eps,
+                                      const float* inv_freq, int pos, int head_dim, int rope_jobs) {
     if (count < 1 || count > kMaxJobs || k > 8192) return hipErrorInvalidValue;
     Jobs jobs{};
     jobs.count = count;
@@ -651,10 +653,23 @@ hipError_t launch_gemv_q4k_bf16_fused(int count, const void* const* w, float* co
     XArgs xa;
     xa.aux = aux;
     xa.eps = eps;
+    if (rope_jobs) {
+        xa.rope.inv_freq = inv_freq;
+        xa.rope.pos = pos;
+        xa.rope.head_dim = head_dim;
+        xa.rope.jobs = rope_jobs & 0xff;
+        xa.rope.half = (rope_jobs >> 8) & 1;
+        switch (xop) {
+            case kXRmsNorm: return fused_xp<kXRmsNorm, kEpiRope>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
+            case kXRmsNorm1:
+                return fused_xp<kXRmsNorm1, kEpiRope>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
+            default: return hipErrorInvalidValue;
+        }
+    }
     switch (xop) {
-        case kXNone: return fused_xp<kXNone>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
-        case kXRmsNorm: return fused_xp<kXRmsNorm>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
-        case kXRmsNorm1: return fused_xp<kXRmsNorm1>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
+        case kXNone: return fused_xp<kXNone, kEpiNone>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
+        case kXRmsNorm: return fused_xp<kXRmsNorm, kEpiNone>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
+        case kXRmsNorm1: return fused_xp<kXRmsNorm1, kEpiNone>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -80,7 +80,8 @@ size_t q4k_bf16_fused_lds_bytes(int64_t k);
 hipError_t launch_gemv_q4k_bf16_fused(int count, const void* const* w, float* const* y, const int64_t* n,
                                       const uint16_t* wb, float* yb, int64_t nb_rows, const float* x,
                                       int64_t k, hipStream_t s, int xop = 0, const float* aux = nullptr,
-                                      float eps = 0.0f);
+                                      float eps = 0.0f, const float* inv_freq = nullptr, int pos = 0,
+                                      int head_dim = 0, int rope_jobs = 0);
 
 // Persistent decode chain (chain.hip).  The host builds the stage table with
 // chain_fill_stage (chain_stage_bytes() each) in device memory and a zeroed

@@ -53,6 +53,8 @@ _SIGNATURES = {
                                            C.c_float, _i32, _vp, _i32, _i32, _i32, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_bf16_rmsnorm": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp, _i64,
                                            _vp, _vp, C.c_float, _i32, _i64, _vp],
+    "rt_hip_gemv_q4k_tiled_bf16_rmsnorm_rope": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp,
+                                                _i64, _vp, _vp, C.c_float, _i32, _vp, _i32, _i32, _i32, _i64, _vp],
     "rt_hip_gemv_bf16_swiglu": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_dequant_q6k_bf16": [_vp, _vp, _i64, _i64, _vp],
     "rt_hip_q6k_tile": [_vp, _vp, _i64, _i64, _vp],
@@ -351,8 +353,10 @@ def gemv_q4k_tiled_swiglu(w, gate, up, n: int, k: int, y=None, stream=None):
 
 
 def gemv_q4k_tiled_bf16_rmsnorm(ws, ns, wb, nb: int, x, gamma, eps: float, k: int, gemma3: bool = False,
-                                ys=None, yb=None, stream=None):
-    """gemv_q4k_tiled_bf16 on RMSNorm(x) (gamma, or 1 + gamma for gemma3)."""
+                                ys=None, yb=None, stream=None, rope=None):
+    """gemv_q4k_tiled_bf16 on RMSNorm(x) (gamma, or 1 + gamma for gemma3).
+    rope = (inv_freq, pos, head_dim, rope_jobs) also rotates the Q4_K jobs in
+    rope_jobs (| ROPE_HALF: half-split pairing)."""
     torch = _torch()
     count = len(ws)
     if ys is None:
@@ -363,6 +367,13 @@ def gemv_q4k_tiled_bf16_rmsnorm(ws, ns, wb, nb: int, x, gamma, eps: float, k: in
     wp = (_vp * count)(*[w.data_ptr() for w in ws])
     yp = (_vp * count)(*[y.data_ptr() for y in ys])
     npp = (_i64 * count)(*ns)
+    if rope is not None:
+        inv_freq, pos, head_dim, rope_jobs = rope
+        _dev_check(inv_freq)
+        library().call("rt_hip_gemv_q4k_tiled_bf16_rmsnorm_rope", count, wp, yp, npp, _ptr(wb), _ptr(yb), nb,
+                       _ptr(x), _ptr(gamma), C.c_float(eps), 1 if gemma3 else 0, _ptr(inv_freq), pos, head_dim,
+                       rope_jobs, k, _stream(stream))
+        return ys, yb
     library().call("rt_hip_gemv_q4k_tiled_bf16_rmsnorm", count, wp, yp, npp, _ptr(wb), _ptr(yb), nb, _ptr(x),
                    _ptr(gamma), C.c_float(eps), 1 if gemma3 else 0, k, _stream(stream))
     return ys, yb

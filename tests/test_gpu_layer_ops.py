@@ -105,6 +105,39 @@ def test_rmsnorm_fused_qk_plus_bf16_v(rt, orc):
     assert normwise_err(from_dev(yb), orc.bf16_matmul_t(wv, xn)) <= GEMV_TOL
 
 
+@pytest.mark.parametrize("pos,half", [(0, False), (7, False), (1000, True), (70000, True)])
+def test_rmsnorm_rope_qk_plus_bf16_v_into_kv_cache(rt, orc, pos, half):
+    """The q/k/v launch of a widened (Q4_K_M) layer: Q4_K q and k rotated at
+    `pos` (interleaved, or half-split with rows interleaved at tiling), the
+    BF16 v beside them, k and v written into their KV-cache rows."""
+    import torch
+    k, hd, nq, nkv = 3072, 128, 24, 8
+    ns, nb = [nq * hd, nkv * hd], nkv * hd
+    say(f"[rmsnorm+rope q/k + bf16 v] pos={pos} half={half}")
+    rng = np.random.default_rng(pos + 41)
+    blocks = _weights(orc, rng, ns, k)
+    wv = orc.f32_to_bf16_n((rng.standard_normal((nb, k)) * 0.02).astype(np.float32))
+    x = (rng.standard_normal(k) * 2).astype(np.float32)
+    gamma = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    inv = orc.llama_inv_freq(500000.0, hd)
+    tiled = [rt.q4k_tile(to_dev(b), n, k, rope_half_head_dim=hd if half else 0) for b, n in zip(blocks, ns)]
+    max_tok = 4
+    row = pos % max_tok
+    kc = torch.zeros((max_tok, nkv * hd), device="cuda")
+    vc = torch.zeros((max_tok, nkv * hd), device="cuda")
+    q = torch.empty((1, ns[0]), device="cuda")
+    jobs = 0x3 | (rt.ROPE_HALF if half else 0)
+    rt.gemv_q4k_tiled_bf16_rmsnorm(tiled, ns, to_dev(wv.view(np.int16)), nb, to_dev(x), to_dev(gamma), 1e-5, k,
+                                   ys=[q, kc[row:row + 1]], yb=vc[row:row + 1], rope=(to_dev(inv), pos, hd, jobs))
+    xn = orc.rmsnorm(x, gamma, 1e-5).reshape(1, k)
+    lin = [orc.q4k_matmul_t(b, n, k, xn).reshape(-1) for b, n in zip(blocks, ns)]
+    assert normwise_err(from_dev(q).reshape(-1), orc.llama_rope(lin[0], nq, hd, pos, inv, half=half)) <= GEMV_TOL
+    assert normwise_err(from_dev(kc)[row], orc.llama_rope(lin[1], nkv, hd, pos, inv, half=half)) <= GEMV_TOL
+    assert normwise_err(from_dev(vc)[row], orc.bf16_matmul_t(wv, xn).reshape(-1)) <= GEMV_TOL
+    others = [r for r in range(max_tok) if r != row]
+    assert not np.any(from_dev(kc)[others]) and not np.any(from_dev(vc)[others])
+
+
 @pytest.mark.parametrize("n,k", [(3072, 8192), (100, 512)])
 def test_bf16_swiglu(rt, orc, n, k):
     say(f"[bf16 swiglu] N={n} K={k}")
