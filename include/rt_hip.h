@@ -7,6 +7,9 @@
  * in_features), activations [M, K] row-major f32, outputs [M, N] f32:
  * y = x * W^T, exactly the reference's `Mat` / `Q4KMat` / `MatBf16`
  * convention (include/rt/quant.hpp:119-199, include/rt/mat.hpp:157-207).
+ * An output may not overlap an input of the same call (x, gamma, up, gate):
+ * every workgroup reads its inputs while others store outputs.  Such calls
+ * fail with RT_HIP_E_ARG.
  *
  * Errors: every function returns an rt_hip_status; 0 is success.  The
  * message for the last failure on the calling thread is rt_hip_last_error().
@@ -67,8 +70,31 @@ typedef enum {
 const char* rt_hip_last_error(void);
 /* Library version string. */
 const char* rt_hip_version(void);
-/* Checks that device `ordinal` exists and is gfx950; makes it current. */
+/* Checks that device `ordinal` exists and is gfx950; makes it current and
+ * creates its arrival counters (zeroed u32s the batched GEMV counts K-slice
+ * arrivals in).  Call it once per device before any other call on it, and
+ * before capturing library calls into a hipGraph. */
 int rt_hip_init(int ordinal);
+
+/* ---- workspace ------------------------------------------------------------
+ * Some calls take scratch from a per-device library workspace: the GEMM (bf16
+ * copies of f32 A and of a Q4_K weight shared by several M tiles, split-K
+ * partials), the batched GEMV (K-slice partials), decode attention (split
+ * partials) and argmax (8 bytes per row).  It grows on demand (the reference
+ * likewise grows its Metal scratch on demand, src/metal_ops.mm:378-423).  A
+ * replaced buffer is kept until the process ends, because a hipGraph that
+ * captured a call still writes the buffer that call used on every replay.
+ * Growth allocates, so it is refused while the stream is being captured
+ * (RT_HIP_E_HIP, "... before capture"): reserve what a graph's calls need
+ * first.  The *_workspace_bytes functions give one call's need (-1 for
+ * invalid sizes); rt_hip_workspace_bytes the current size of the current
+ * device's workspace.  Calls that share the workspace must not overlap on a
+ * device (one stream, or ordered streams). */
+int rt_hip_reserve_workspace(int64_t bytes);
+int64_t rt_hip_workspace_bytes(void);
+int64_t rt_hip_gemm_workspace_bytes(int32_t format, int32_t a_dtype, int64_t m, int64_t n, int64_t k);
+int64_t rt_hip_gemv_workspace_bytes(int32_t format, int64_t n, int64_t k, int32_t m);
+int64_t rt_hip_attention_workspace_bytes(int32_t n_q_heads, int32_t n_kv_heads, int64_t seq_len);
 
 /* ---- GEMV: M <= 8 activation rows ---------------------------------------
  * Replace: Q4KMat::matmul_q4k_t / _blas for M == 1 (gemv_mt) and the M > 1
@@ -238,43 +264,6 @@ int rt_hip_gemv_q4k_tiled_bf16_rmsnorm_rope(int32_t count, const void* const* ti
                                             int64_t n_bf16, const float* x, const float* gamma, float eps,
                                             int32_t gemma3, const float* inv_freq, int32_t pos, int32_t head_dim,
                                             int32_t rope_jobs, int64_t k, rt_hip_stream stream);
-
-/* ---- decode chain: a step's dependent GEMV stages in one launch -----------
- * Replace: MetalDecodeContext::create / decode_step, the per-token sequence
- * of GEMV dispatches encoded into one command buffer
- * (include/rt/metal_decode.hpp:41-69, src/metal_decode.mm:436-482).
- *
- * A stage is one tiled-Q4_K GEMV, or up to four that share x (q/k/v,
- * gate/up), exactly as rt_hip_gemv_q4k_tiled_multi.  Stage s starts reading
- * x only after every earlier stage has stored its outputs, so x may point at
- * an earlier stage's y.  The chain runs as one persistent launch (one
- * workgroup per CU) with a stage barrier between stages.  On MI355X it is
- * measured slower than one launch per stage (877 vs 743 us for a
- * Llama-3.2-3B step of pure Q4_K): the cross-CU handoff costs about as much
- * as a kernel boundary.  It is an opt-in alternative, not the fast path.
- *
- * create validates the stages and copies them to the device (the pointers
- * are baked in: buffers must outlive the chain).  run launches one pass and
- * allocates nothing, so it can be captured in a hipGraph.  Runs of one chain
- * must not overlap (one stream, or ordered streams).  status waits for the
- * device and reports RT_HIP_E_HIP if a stage barrier timed out in an earlier
- * run (the outputs of that run are then invalid); reset != 0 also re-arms
- * the chain's barrier flags.  Results match rt_hip_gemv_q4k_tiled_multi to
- * f32 rounding (same tile arithmetic; the K split may differ).
- * Limits: 1 <= k / 256 <= 32 (k <= 8192), 1..4 jobs per stage. */
-typedef struct rt_hip_chain_stage {
-    const float* x;        /* activation [k], device */
-    int64_t k;             /* in_features, multiple of 256 */
-    int32_t count;         /* GEMVs sharing x: 1..4 */
-    const void* w[4];      /* tiled Q4_K weights (rt_hip_q4k_tile) */
-    float* y[4];           /* outputs [n[j]] */
-    int64_t n[4];          /* out_features */
-} rt_hip_chain_stage;
-typedef struct rt_hip_chain rt_hip_chain;
-int rt_hip_chain_create(const rt_hip_chain_stage* stages, int32_t count, rt_hip_chain** out);
-int rt_hip_chain_run(rt_hip_chain* chain, rt_hip_stream stream);
-int rt_hip_chain_status(rt_hip_chain* chain, int32_t reset);
-int rt_hip_chain_destroy(rt_hip_chain* chain);
 
 /* Replace: MatBf16::matmul_by_t for M <= 8 (src/mat.cpp:318-414); Metal
  * metal_gemv_bf16_t (metal_ops.hpp:64-65) and gemv_bf16_t / _batch

@@ -11,6 +11,7 @@
 
 #include "rt_hip.h"
 #include "rt_launch.hpp"
+#include "workspace_pool.hpp"
 
 namespace rt_hip {
 namespace {
@@ -29,13 +30,14 @@ int hip_fail(hipError_t e, const char* what) {
 struct DeviceState {
     DeviceInfo info;
     bool ok = false;
-    void* ws = nullptr;
-    size_t ws_bytes = 0;
+    WorkspacePool ws;              // grow-only; replaced buffers are retired, never freed
     uint32_t* counters = nullptr;  // arrival counters, zero between launches
 };
 
+// Fixed storage: a DeviceState's address stays valid for the process.
+constexpr int kMaxDevices = 64;
 std::mutex g_mu;
-std::vector<DeviceState> g_dev;
+DeviceState g_dev[kMaxDevices];
 
 DeviceState* state_for_current(hipError_t* err) {
     int dev = 0;
@@ -44,8 +46,11 @@ DeviceState* state_for_current(hipError_t* err) {
         *err = e;
         return nullptr;
     }
+    if (dev < 0 || dev >= kMaxDevices) {
+        *err = hipErrorInvalidDevice;
+        return nullptr;
+    }
     std::lock_guard<std::mutex> lk(g_mu);
-    if (static_cast<int>(g_dev.size()) <= dev) g_dev.resize(dev + 1);
     DeviceState& st = g_dev[dev];
     if (!st.ok) {
         hipDeviceProp_t prop;
@@ -65,7 +70,17 @@ DeviceState* state_for_current(hipError_t* err) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Byte ranges [a, a + na) and [b, b + nb) intersect.
+bool overlaps(const void* a, int64_t na, const void* b, int64_t nb) {
+    const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+    return pa < pb + static_cast<uintptr_t>(nb) && pb < pa + static_cast<uintptr_t>(na);
+}
+
 int check_stream_launch(hipError_t e, const char* what) {
+    if (e == hipErrorStreamCaptureUnsupported)
+        return fail(RT_HIP_E_HIP, std::string(what) +
+                                      ": the workspace must grow, which cannot happen while the stream is "
+                                      "captured (call rt_hip_reserve_workspace / rt_hip_init before capture)");
     if (e != hipSuccess) return hip_fail(e, what);
     return RT_HIP_OK;
 }
@@ -84,6 +99,8 @@ int gemv_args(const char* fn, const void* w, const float* x, const float* y, int
         return fail(RT_HIP_E_SHAPE, std::string(fn) + ": n and k must fit in int32");
     if (!aligned16(w) || !aligned16(x))
         return fail(RT_HIP_E_ALIGN, std::string(fn) + ": w and x must be 16-byte aligned");
+    // Every workgroup reads all of x while others already store rows of y.
+    if (overlaps(y, n * m * 4, x, k * m * 4)) return fail(RT_HIP_E_ARG, std::string(fn) + ": y overlaps x");
     return RT_HIP_OK;
 }
 
@@ -119,6 +136,9 @@ const DeviceInfo& device_info() {
 }
 
 int tune_param(const char* name, int fallback) {
+#ifdef RT_HIP_TUNING
+    // Sweep builds only (make TUNING=1): RT_HIP_<name> overrides a launch
+    // shape.  The library as shipped always runs the measured defaults.
     static std::mutex mu;
     static std::vector<std::pair<std::string, int>> cache;
     std::lock_guard<std::mutex> lk(mu);
@@ -129,43 +149,72 @@ int tune_param(const char* name, int fallback) {
     if (const char* s = std::getenv(env.c_str())) v = std::atoi(s);
     cache.emplace_back(name, v);
     return v;
+#else
+    (void)name;
+    return fallback;
+#endif
 }
 
-void* workspace(size_t bytes, hipError_t* err) {
+namespace {
+
+// True when `s` (or, for the legacy stream, any stream) is being captured
+// into a hipGraph: no allocation or synchronisation may happen then.
+bool capturing(hipStream_t s) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) return false;
+    return st != hipStreamCaptureStatusNone;
+}
+
+// Grows st's workspace to `bytes` (caller holds g_mu); `capture`: the
+// caller's stream is being captured, so no allocation may happen.
+hipError_t grow_workspace(DeviceState* st, size_t bytes, bool capture) {
+    const int rc = st->ws.reserve(bytes, capture, [](void** p, size_t n) { return static_cast<int>(hipMalloc(p, n)); });
+    if (rc == WorkspacePool::kRefused) return hipErrorStreamCaptureUnsupported;
+    return static_cast<hipError_t>(rc);
+}
+
+// Allocates and zeroes st's arrival counters (caller holds g_mu; never
+// while a stream is being captured).
+hipError_t make_counters(DeviceState* st) {
+    if (st->counters) return hipSuccess;
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, kArrivalCounters * sizeof(uint32_t));
+    if (e != hipSuccess) return e;
+    e = hipMemset(p, 0, kArrivalCounters * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        return e;
+    }
+    st->counters = static_cast<uint32_t*>(p);
+    return hipSuccess;
+}
+
+}  // namespace
+
+void* workspace(size_t bytes, hipStream_t s, hipError_t* err) {
     DeviceState* st = state_for_current(err);
     if (!st) return nullptr;
     std::lock_guard<std::mutex> lk(g_mu);
-    if (st->ws_bytes < bytes) {
-        if (st->ws) {
-            *err = hipFree(st->ws);
-            if (*err != hipSuccess) return nullptr;
-            st->ws = nullptr;
-            st->ws_bytes = 0;
-        }
-        size_t sz = bytes < (1u << 20) ? (1u << 20) : bytes;
-        *err = hipMalloc(&st->ws, sz);
+    if (st->ws.bytes < bytes) {
+        *err = grow_workspace(st, bytes, capturing(s));
         if (*err != hipSuccess) return nullptr;
-        st->ws_bytes = sz;
     }
     *err = hipSuccess;
-    return st->ws;
+    return st->ws.cur;
 }
 
-uint32_t* arrival_counters(hipError_t* err) {
+uint32_t* arrival_counters(hipStream_t s, hipError_t* err) {
     DeviceState* st = state_for_current(err);
     if (!st) return nullptr;
     std::lock_guard<std::mutex> lk(g_mu);
     if (!st->counters) {
-        void* p = nullptr;
-        *err = hipMalloc(&p, kArrivalCounters * sizeof(uint32_t));
-        if (*err != hipSuccess) return nullptr;
-        *err = hipMemset(p, 0, kArrivalCounters * sizeof(uint32_t));
-        if (*err == hipSuccess) *err = hipDeviceSynchronize();
-        if (*err != hipSuccess) {
-            (void)hipFree(p);
+        if (capturing(s)) {
+            *err = hipErrorStreamCaptureUnsupported;
             return nullptr;
         }
-        st->counters = static_cast<uint32_t*>(p);
+        *err = make_counters(st);
+        if (*err != hipSuccess) return nullptr;
     }
     *err = hipSuccess;
     return st->counters;
@@ -197,7 +246,51 @@ int rt_hip_init(int ordinal) {
     if (e != hipSuccess) return hip_fail(e, "rt_hip_init");
     DeviceState* st = state_for_current(&e);
     if (!st) return hip_fail(e, "rt_hip_init");
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        e = make_counters(st);
+    }
+    if (e != hipSuccess) return hip_fail(e, "rt_hip_init: arrival counters");
     return RT_HIP_OK;
+}
+
+int rt_hip_reserve_workspace(int64_t bytes) {
+    const char* fn = "rt_hip_reserve_workspace";
+    if (bytes < 0) return fail(RT_HIP_E_ARG, std::string(fn) + ": bytes must be >= 0");
+    hipError_t e;
+    DeviceState* st = state_for_current(&e);
+    if (!st) return hip_fail(e, fn);
+    std::lock_guard<std::mutex> lk(g_mu);
+    e = make_counters(st);
+    if (e == hipSuccess) e = grow_workspace(st, static_cast<size_t>(bytes), false);
+    if (e == hipErrorOutOfMemory) return fail(RT_HIP_E_OOM, std::string(fn) + ": device allocation failed");
+    if (e != hipSuccess) return hip_fail(e, fn);
+    return RT_HIP_OK;
+}
+
+int64_t rt_hip_gemm_workspace_bytes(int32_t format, int32_t a_dtype, int64_t m, int64_t n, int64_t k) {
+    if (m <= 0 || n <= 0 || k <= 0 || (a_dtype != RT_HIP_F32 && a_dtype != RT_HIP_BF16)) return -1;
+    if (format != RT_HIP_Q4K && format != RT_HIP_BF16) return -1;
+    return static_cast<int64_t>(gemm_workspace_bytes(format, a_dtype == RT_HIP_BF16, m, n, k));
+}
+
+int64_t rt_hip_gemv_workspace_bytes(int32_t format, int64_t n, int64_t k, int32_t m) {
+    if (n <= 0 || k <= 0 || m < 1 || m > RT_HIP_GEMV_MAX_M) return -1;
+    if (m == 1 || (format != RT_HIP_Q4K && format != RT_HIP_BF16)) return 0;
+    return static_cast<int64_t>(gemv_batch_workspace_bytes(format, n, k, m));
+}
+
+int64_t rt_hip_attention_workspace_bytes(int32_t n_q_heads, int32_t n_kv_heads, int64_t seq_len) {
+    if (n_kv_heads < 1 || n_q_heads < n_kv_heads || seq_len < 1) return -1;
+    return static_cast<int64_t>(attention_decode_workspace(n_q_heads, n_kv_heads, seq_len));
+}
+
+int64_t rt_hip_workspace_bytes(void) {
+    hipError_t e;
+    DeviceState* st = state_for_current(&e);
+    if (!st) return -1;
+    std::lock_guard<std::mutex> lk(g_mu);
+    return static_cast<int64_t>(st->ws.bytes);
 }
 
 int rt_hip_gemv_q4k(const void* blocks, const float* x, float* y, int64_t n, int64_t k,
@@ -288,8 +381,13 @@ int gemv_xop(const char* fn, int xop, int32_t count, const void* const* tiled, f
     if (xop != 0 && !aux) return fail(RT_HIP_E_ARG, std::string(fn) + ": null gamma / up");
     if (xop != 0 && !aligned16(aux))
         return fail(RT_HIP_E_ALIGN, std::string(fn) + ": gamma / up must be 16-byte aligned");
-    if (add && (y[0] == x || y[0] == aux)) return fail(RT_HIP_E_ARG, std::string(fn) + ": resid aliases an input");
     if (k > 8192 || q4k_m1_lds_bytes(k) > 65536) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 8192");
+    // Every workgroup reads all of x (and gamma / up) while others already
+    // store rows of y, so no output may overlap an input.
+    for (int32_t j = 0; j < count; ++j) {
+        if (overlaps(y[j], n[j] * 4, x, k * 4) || (aux && overlaps(y[j], n[j] * 4, aux, k * 4)))
+            return fail(RT_HIP_E_ARG, std::string(fn) + ": an output overlaps x, gamma or up");
+    }
     if (!(eps >= 0.0f)) return fail(RT_HIP_E_ARG, std::string(fn) + ": eps must be >= 0");
     hipError_t e;
     if (!state_for_current(&e)) return hip_fail(e, fn);
@@ -346,7 +444,8 @@ int rt_hip_gemv_bf16_swiglu_residual(const uint16_t* w, const float* gate, const
     if (rc) return rc;
     if (!up) return fail(RT_HIP_E_ARG, std::string(fn) + ": null up");
     if (!aligned16(up)) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": up must be 16-byte aligned");
-    if (resid == gate || resid == up) return fail(RT_HIP_E_ARG, std::string(fn) + ": resid aliases an input");
+    if (overlaps(resid, n * 4, gate, k * 4) || overlaps(resid, n * 4, up, k * 4))
+        return fail(RT_HIP_E_ARG, std::string(fn) + ": resid overlaps gate or up");
     if (k > 8192) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 8192");
     hipError_t e;
     if (!state_for_current(&e)) return hip_fail(e, fn);
@@ -367,8 +466,8 @@ int rt_hip_attention_decode(const float* q, const float* k_cache, const float* v
         return fail(RT_HIP_E_ALIGN, std::string(fn) + ": buffers must be 16-byte aligned");
     hipError_t e;
     if (!state_for_current(&e)) return hip_fail(e, fn);
-    float* part = static_cast<float*>(workspace(attention_decode_workspace(n_q_heads, n_kv_heads, seq_len), &e));
-    if (!part) return hip_fail(e, fn);
+    float* part = static_cast<float*>(workspace(attention_decode_workspace(n_q_heads, n_kv_heads, seq_len), static_cast<hipStream_t>(stream), &e));
+    if (!part) return check_stream_launch(e, fn);
     return check_stream_launch(launch_attention_decode(q, k_cache, v_cache, out, part, n_q_heads, n_kv_heads,
                                                        seq_len, scale, static_cast<hipStream_t>(stream)),
                                fn);
@@ -394,6 +493,12 @@ static int q4k_bf16_rmsnorm(const char* fn, int32_t count, const void* const* ti
     if (!gamma) return fail(RT_HIP_E_ARG, std::string(fn) + ": null gamma");
     if (!aligned16(gamma)) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": gamma must be 16-byte aligned");
     if (!(eps >= 0.0f)) return fail(RT_HIP_E_ARG, std::string(fn) + ": eps must be >= 0");
+    for (int32_t j = 0; j <= count; ++j) {
+        const void* yj = j < count ? static_cast<const void*>(y[j]) : static_cast<const void*>(y_bf16);
+        const int64_t nj = j < count ? n[j] : n_bf16;
+        if (overlaps(yj, nj * 4, gamma, k * 4))
+            return fail(RT_HIP_E_ARG, std::string(fn) + ": an output overlaps gamma");
+    }
     if (k > 8192 || q4k_bf16_fused_lds_bytes(k) > 65536)
         return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 8192");
     hipError_t e;
@@ -440,6 +545,7 @@ int rt_hip_gemv_bf16_swiglu(const uint16_t* w, const float* gate, const float* u
     if (rc) return rc;
     if (!up) return fail(RT_HIP_E_ARG, std::string(fn) + ": null up");
     if (!aligned16(up)) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": up must be 16-byte aligned");
+    if (overlaps(y, n * 4, up, k * 4)) return fail(RT_HIP_E_ARG, std::string(fn) + ": y overlaps up");
     if (k > 8192) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 8192");
     hipError_t e;
     if (!state_for_current(&e)) return hip_fail(e, fn);
@@ -475,119 +581,7 @@ int rt_hip_gemv_q4k_tiled(const void* tiled, const float* x, float* y, int64_t n
 
 }  // extern "C"
 
-struct rt_hip_chain {
-    int device = -1;
-    void* stages = nullptr;  // device Stage table
-    int nst = 0;
-    uint32_t* sync = nullptr;  // flags, group flags, error word
-    size_t sync_words = 0;
-    int grid = 0;
-};
-
 extern "C" {
-
-int rt_hip_chain_create(const rt_hip_chain_stage* stages, int32_t count, rt_hip_chain** out) {
-    const char* fn = "rt_hip_chain_create";
-    if (!out) return fail(RT_HIP_E_ARG, std::string(fn) + ": null output");
-    *out = nullptr;
-    if (!stages || count < 1) return fail(RT_HIP_E_ARG, std::string(fn) + ": need at least one stage");
-    hipError_t e;
-    DeviceState* ds = state_for_current(&e);
-    if (!ds) return hip_fail(e, fn);
-    const int waves = chain_waves_per_wg();
-    const int grid = ds->info.cus;
-    if (grid < 1 || grid > chain_max_grid()) return fail(RT_HIP_E_UNSUPPORTED, std::string(fn) + ": CU count");
-    // Every workgroup must be resident at once (the stage barrier waits for
-    // all of them): one per CU.
-    int per_cu = 0;
-    e = chain_occupancy(&per_cu);
-    if (e != hipSuccess) return hip_fail(e, fn);
-    if (per_cu < 1) return fail(RT_HIP_E_UNSUPPORTED, std::string(fn) + ": chain kernel does not fit a CU");
-
-    const size_t sb = chain_stage_bytes();
-    std::vector<uint8_t> table(sb * static_cast<size_t>(count));
-    for (int32_t s = 0; s < count; ++s) {
-        const rt_hip_chain_stage& st = stages[s];
-        const std::string at = std::string(fn) + ": stage " + std::to_string(s);
-        if (st.count < 1 || st.count > RT_HIP_MULTI_MAX) return fail(RT_HIP_E_ARG, at + ": count must be in [1, 4]");
-        if (!st.x || !aligned16(st.x)) return fail(RT_HIP_E_ALIGN, at + ": x must be non-null and 16-byte aligned");
-        if (st.k <= 0 || st.k % 256 != 0) return fail(RT_HIP_E_ALIGN, at + ": k must be a positive multiple of 256");
-        if (st.k > chain_max_k()) return fail(RT_HIP_E_SHAPE, at + ": k above 8192");
-        int tile0[4] = {0, 0, 0, 0};
-        int64_t tiles = 0;
-        for (int j = 0; j < st.count; ++j) {
-            if (!st.w[j] || !st.y[j] || !aligned16(st.w[j]))
-                return fail(RT_HIP_E_ARG, at + ": null or unaligned weight/output");
-            if (st.n[j] <= 0 || st.n[j] > (1 << 26)) return fail(RT_HIP_E_SHAPE, at + ": n out of range");
-            tile0[j] = static_cast<int>(tiles);
-            tiles += (st.n[j] + 15) / 16;
-        }
-        if (tiles > (1 << 24)) return fail(RT_HIP_E_SHAPE, at + ": too many rows");
-        // K split: the largest of 16, 8, 4, 2 that divides the super-block
-        // count and still gives every wave of the grid at most one share;
-        // outputs with more tiles than waves take several rounds at ks = 1.
-        const int64_t nb = st.k / 256, slots = static_cast<int64_t>(grid) * waves;
-        int ks = 1;
-        for (int c : {16, 8, 4, 2})
-            if (nb % c == 0 && tiles * c <= slots) {
-                ks = c;
-                break;
-            }
-        const int64_t per_round = static_cast<int64_t>(grid) * (waves / ks);
-        const int rounds = static_cast<int>((tiles + per_round - 1) / per_round);
-        chain_fill_stage(table.data() + sb * s, st.x, st.count, st.w, st.y, st.n, st.k, ks,
-                         static_cast<int>(tiles), rounds, tile0);
-    }
-
-    auto* c = new rt_hip_chain();
-    c->device = ds->info.ordinal;
-    c->nst = count;
-    c->grid = grid;
-    c->sync_words = chain_sync_words(grid);
-    e = hipMalloc(&c->stages, table.size());
-    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->sync), c->sync_words * 4);
-    if (e == hipSuccess) e = hipMemcpy(c->stages, table.data(), table.size(), hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMemset(c->sync, 0, c->sync_words * 4);
-    if (e == hipSuccess) e = hipDeviceSynchronize();
-    if (e != hipSuccess) {
-        rt_hip_chain_destroy(c);
-        return e == hipErrorOutOfMemory ? fail(RT_HIP_E_OOM, std::string(fn) + ": device allocation failed")
-                                        : hip_fail(e, fn);
-    }
-    *out = c;
-    return RT_HIP_OK;
-}
-
-int rt_hip_chain_run(rt_hip_chain* chain, rt_hip_stream stream) {
-    if (!chain) return fail(RT_HIP_E_ARG, "rt_hip_chain_run: null chain");
-    return check_stream_launch(launch_chain(chain->stages, chain->nst, chain->sync, chain->grid,
-                                            static_cast<hipStream_t>(stream)),
-                               "rt_hip_chain_run");
-}
-
-int rt_hip_chain_status(rt_hip_chain* chain, int32_t reset) {
-    if (!chain) return fail(RT_HIP_E_ARG, "rt_hip_chain_status: null chain");
-    hipError_t e = hipDeviceSynchronize();
-    if (e != hipSuccess) return hip_fail(e, "rt_hip_chain_status");
-    uint32_t err = 0;
-    e = hipMemcpy(&err, chain->sync + chain_err_word(chain->grid), 4, hipMemcpyDeviceToHost);
-    if (e != hipSuccess) return hip_fail(e, "rt_hip_chain_status");
-    if (reset) {
-        e = hipMemset(chain->sync, 0, chain->sync_words * 4);
-        if (e == hipSuccess) e = hipDeviceSynchronize();
-        if (e != hipSuccess) return hip_fail(e, "rt_hip_chain_status");
-    }
-    if (err) return fail(RT_HIP_E_HIP, "rt_hip_chain_status: a stage barrier timed out; outputs are invalid");
-    return RT_HIP_OK;
-}
-
-int rt_hip_chain_destroy(rt_hip_chain* chain) {
-    if (!chain) return RT_HIP_OK;
-    if (chain->stages) (void)hipFree(chain->stages);
-    if (chain->sync) (void)hipFree(chain->sync);
-    delete chain;
-    return RT_HIP_OK;
-}
 
 int rt_hip_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
                      int32_t m, rt_hip_stream stream) {
@@ -658,8 +652,8 @@ int rt_hip_argmax(const float* logits, int64_t rows, int64_t cols, int64_t* idx,
     if (cols > 0xffffffffLL || rows > 65535)
         return fail(RT_HIP_E_SHAPE, "rt_hip_argmax: cols < 2^32 and rows <= 65535 required");
     hipError_t e;
-    uint64_t* keys = static_cast<uint64_t*>(workspace(static_cast<size_t>(rows) * 8, &e));
-    if (!keys) return hip_fail(e, "rt_hip_argmax: workspace");
+    uint64_t* keys = static_cast<uint64_t*>(workspace(static_cast<size_t>(rows) * 8, static_cast<hipStream_t>(stream), &e));
+    if (!keys) return check_stream_launch(e, "rt_hip_argmax: workspace");
     hipStream_t s = static_cast<hipStream_t>(stream);
     if ((e = launch_argmax_init(keys, rows, s)) != hipSuccess) return hip_fail(e, "rt_hip_argmax");
     if ((e = launch_argmax_scan(logits, rows, cols, keys, s)) != hipSuccess)
@@ -677,8 +671,8 @@ int rt_hip_gemv_bf16_argmax(const uint16_t* w, const float* x, float* y, int64_t
     hipError_t e;
     if (gemv_lds_bytes(RT_HIP_BF16, 1, k) > 65536)
         return fail(RT_HIP_E_SHAPE, "rt_hip_gemv_bf16_argmax: k too large");
-    uint64_t* key = static_cast<uint64_t*>(workspace(8, &e));
-    if (!key) return hip_fail(e, "rt_hip_gemv_bf16_argmax: workspace");
+    uint64_t* key = static_cast<uint64_t*>(workspace(8, static_cast<hipStream_t>(stream), &e));
+    if (!key) return check_stream_launch(e, "rt_hip_gemv_bf16_argmax: workspace");
     hipStream_t s = static_cast<hipStream_t>(stream);
     if ((e = launch_argmax_init(key, 1, s)) != hipSuccess)
         return hip_fail(e, "rt_hip_gemv_bf16_argmax");

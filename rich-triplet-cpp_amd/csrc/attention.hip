@@ -45,8 +45,10 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-// Partial state of one (query head, split): m, l, then o[128].
-constexpr int kPart = 2 + kHd;
+// Partial state of one (query head, split): m, l, two pad floats, then
+// o[128]; 528 bytes, so every state and its o vector are 16-byte aligned.
+constexpr int kPO = 4;
+constexpr int kPart = kPO + kHd;
 
 template <int G>
 __global__ __launch_bounds__(kT) void k_attn_partial(const float* __restrict__ q, const float* __restrict__ kc,
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(kT) void k_attn_partial(const float* __restrict__ q
             dst[0] = M;
             dst[1] = L;
         }
-        *reinterpret_cast<f32x4*>(dst + 2 + d4 * 4) = O;
+        *reinterpret_cast<f32x4*>(dst + kPO + d4 * 4) = O;
     }
 }
 
@@ -157,7 +159,7 @@ __global__ __launch_bounds__(kHd) void k_attn_combine(const float* __restrict__ 
             const float* ps = ph + min(s, S - 1) * kPart;
             ms[s] = ps[0];
             ls[s] = ps[1];
-            os[s] = ps[2 + d];
+            os[s] = ps[kPO + d];
         }
 #pragma unroll
         for (int s = 0; s < kBatch; ++s) M = fmaxf(M, ms[s]);
@@ -177,7 +179,7 @@ __global__ __launch_bounds__(kHd) void k_attn_combine(const float* __restrict__ 
             for (int s = 0; s < S; ++s) {
                 const float w = exp_fast(ph[s * kPart] - M);
                 L += ph[s * kPart + 1] * w;
-                O += ph[s * kPart + 2 + d] * w;
+                O += ph[s * kPart + kPO + d] * w;
             }
         }
     }

@@ -622,37 +622,71 @@ __global__ void k_add_bias(float* __restrict__ y, const float* __restrict__ bias
 
 }  // namespace
 
+namespace {
+
+// How one GEMM call runs (shared by the launcher and the workspace query).
+struct GemmPlan {
+    bool pipe = false;       // pipelined bf16-MFMA kernels (k % 256 == 0, Q4_K or BF16 W)
+    bool fused_q4k = false;  // one M tile: Q4_K dequantized into LDS inside the GEMM
+    bool big = false;        // 256 x 256 kernel
+    int splits = 1;          // split-K slices of the 128 x 128 kernel
+    int64_t mt = 0, nt = 0, mt2 = 0, nt2 = 0;
+    size_t a_bytes = 0, w_bytes = 0, p_bytes = 0;
+};
+
+GemmPlan plan_gemm(int w_fmt, bool a_bf16, int64_t m, int64_t n, int64_t k) {
+    GemmPlan p;
+    p.pipe = k % 256 == 0 && (w_fmt == RT_HIP_Q4K || w_fmt == RT_HIP_BF16);
+    if (!p.pipe) return p;
+    // Pipelined kernel on bf16 A (f32 A converted once into the workspace).
+    // A Q4_K weight used by more than one M tile is dequantized once into the
+    // workspace (bf16, round-to-nearest-even of the exact f32 value, as the
+    // fused path and the reference's flux_dequant_q4k) instead of once per M
+    // tile inside the GEMM.
+    p.mt = (m + 127) / 128;
+    p.nt = (n + 127) / 128;
+    p.fused_q4k = w_fmt == RT_HIP_Q4K && p.mt == 1;
+    const int64_t cus = device_info().cus;
+    p.mt2 = (m + 255) / 256;
+    p.nt2 = (n + 255) / 256;
+    p.big = !p.fused_q4k && 4 * p.mt2 * p.nt2 >= 3 * cus && tune_param("GEMM_BIG", 1);
+    // Split-K for the 128 x 128 bf16 kernel when its tiles leave at least
+    // half the CUs idle: up to 4 slices of K, each a multiple of 64, summed
+    // afterwards in a fixed order (deterministic).
+    if (!p.fused_q4k && !p.big && 2 * p.mt * p.nt <= cus && n % 4 == 0) {
+        int splits = static_cast<int>(cus / (p.mt * p.nt));
+        splits = splits > 4 ? 4 : splits;
+        while (splits > 1 && k % (64 * splits) != 0) --splits;
+        const int forced = tune_param("GEMM_SPLITK", 0);
+        if (forced >= 1 && forced <= 4 && k % (64 * forced) == 0) splits = forced;
+        p.splits = splits;
+    }
+    p.a_bytes = a_bf16 ? 0 : static_cast<size_t>(m * k) * 2;
+    p.w_bytes = (w_fmt == RT_HIP_Q4K && !p.fused_q4k) ? static_cast<size_t>(n * k) * 2 : 0;
+    p.p_bytes = p.splits > 1 ? static_cast<size_t>(p.splits) * m * n * 4 : 0;
+    return p;
+}
+
+}  // namespace
+
+size_t gemm_workspace_bytes(int w_fmt, bool a_bf16, int64_t m, int64_t n, int64_t k) {
+    const GemmPlan p = plan_gemm(w_fmt, a_bf16, m, n, k);
+    return p.a_bytes + p.w_bytes + p.p_bytes;
+}
+
 hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, const float* bias,
                        float* c, int64_t m, int64_t n, int64_t k, hipStream_t s) {
     if (k % BK) return hipErrorInvalidValue;
-    if (k % 256 == 0 && (w_fmt == RT_HIP_Q4K || w_fmt == RT_HIP_BF16)) {
-        // Pipelined kernel on bf16 A (f32 A converted once into the
-        // workspace).  A Q4_K weight used by more than one M tile is
-        // dequantized once into the workspace (bf16, round-to-nearest-even of
-        // the exact f32 value, as the fused path and the reference's
-        // flux_dequant_q4k) instead of once per M tile inside the GEMM.
-        const int64_t mt = (m + 127) / 128, nt = (n + 127) / 128;
-        const bool fused_q4k = w_fmt == RT_HIP_Q4K && mt == 1;
-        const int64_t cus = device_info().cus;
-        const int64_t mt2 = (m + 255) / 256, nt2 = (n + 255) / 256;
-        const bool big = !fused_q4k && 4 * mt2 * nt2 >= 3 * cus && tune_param("GEMM_BIG", 1);
-        // Split-K for the 128 x 128 bf16 kernel when its tiles leave at least
-        // half the CUs idle: up to 4 slices of K, each a multiple of 64,
-        // summed afterwards in a fixed order (deterministic).
-        int splits = 1;
-        if (!fused_q4k && !big && 2 * mt * nt <= cus && n % 4 == 0) {
-            splits = static_cast<int>(cus / (mt * nt));
-            splits = splits > 4 ? 4 : splits;
-            while (splits > 1 && k % (64 * splits) != 0) --splits;
-            if (const int forced = tune_param("GEMM_SPLITK", 0)) splits = forced;
-        }
-        const size_t a_bytes = a_bf16 ? 0 : static_cast<size_t>(m * k) * 2;
-        const size_t w_bytes = (w_fmt == RT_HIP_Q4K && !fused_q4k) ? static_cast<size_t>(n * k) * 2 : 0;
-        const size_t p_bytes = splits > 1 ? static_cast<size_t>(splits) * m * n * 4 : 0;
+    const GemmPlan P = plan_gemm(w_fmt, a_bf16, m, n, k);
+    if (P.pipe) {
+        const int64_t mt = P.mt, nt = P.nt, mt2 = P.mt2, nt2 = P.nt2;
+        const bool fused_q4k = P.fused_q4k, big = P.big;
+        const int splits = P.splits;
+        const size_t a_bytes = P.a_bytes, w_bytes = P.w_bytes, p_bytes = P.p_bytes;
         uint8_t* ws = nullptr;
         if (a_bytes + w_bytes + p_bytes) {
             hipError_t e;
-            ws = static_cast<uint8_t*>(workspace(a_bytes + w_bytes + p_bytes, &e));
+            ws = static_cast<uint8_t*>(workspace(a_bytes + w_bytes + p_bytes, s, &e));
             if (!ws) return e;
         }
         const uint16_t* a16 = static_cast<const uint16_t*>(a);

@@ -411,7 +411,7 @@ hipError_t run_q(const void* w, const float* x, float* y, float* p, uint32_t* co
 // measurement) measured slower at those shapes -- their registers cost
 // resident workgroups, and other waves hide a slot's load better.
 template <class F>
-hipError_t dispatch(const void* w, const float* x, float* y, int64_t n, int64_t k, int m, hipStream_t s) {
+bool plan(int64_t n, int64_t k, int m, int64_t* per_out, int64_t* slices_out) {
     const int q = (m + 3) / 4;
     const int64_t total_slots = (k + F::kSteps * 32 - 1) / (F::kSteps * 32);
     const int64_t groups = ((n + 15) / 16 + kWaves - 1) / kWaves;
@@ -421,7 +421,7 @@ hipError_t dispatch(const void* w, const float* x, float* y, int64_t n, int64_t 
         const int64_t ps = per * F::kSteps;
         return batch_lds_bytes<F>(static_cast<int>(ps), q) <= budget && ps * m * 4 <= 4 * static_cast<int64_t>(kThreads);
     };
-    if (!fits(1)) return hipErrorInvalidValue;
+    if (!fits(1)) return false;
     int64_t per = 1, best = -1, prev = 0;
     for (int64_t sl = 1; sl <= total_slots; ++sl) {
         const int64_t c = (total_slots + sl - 1) / sl;
@@ -435,16 +435,26 @@ hipError_t dispatch(const void* w, const float* x, float* y, int64_t n, int64_t 
     }
     const int forced = tune_param("BATCH_SLOTS", 0);
     if (forced > 0 && fits(forced)) per = forced;
-    const int64_t slices = (total_slots + per - 1) / per;
+    *per_out = per;
+    *slices_out = (total_slots + per - 1) / per;
+    return true;
+}
+
+template <class F>
+hipError_t dispatch(const void* w, const float* x, float* y, int64_t n, int64_t k, int m, hipStream_t s) {
+    const int q = (m + 3) / 4;
+    const int64_t groups = ((n + 15) / 16 + kWaves - 1) / kWaves;
+    int64_t per = 0, slices = 0;
+    if (!plan<F>(n, k, m, &per, &slices)) return hipErrorInvalidValue;
 
     float* part = nullptr;
     uint32_t* counters = nullptr;
     if (slices > 1) {
         if (groups > static_cast<int64_t>(kArrivalCounters)) return hipErrorInvalidValue;
         hipError_t e;
-        counters = arrival_counters(&e);
+        counters = arrival_counters(s, &e);
         if (!counters) return e;
-        part = static_cast<float*>(workspace(static_cast<size_t>(slices) * m * n * sizeof(float), &e));
+        part = static_cast<float*>(workspace(static_cast<size_t>(slices) * m * n * sizeof(float), s, &e));
         if (!part) return e;
     }
     const int sl = static_cast<int>(per), nsl = static_cast<int>(slices);
@@ -453,6 +463,14 @@ hipError_t dispatch(const void* w, const float* x, float* y, int64_t n, int64_t 
 }
 
 }  // namespace
+
+size_t gemv_batch_workspace_bytes(int fmt, int64_t n, int64_t k, int m) {
+    if (m < 2 || m > 8) return 0;
+    int64_t per = 0, slices = 0;
+    const bool ok = fmt == RT_HIP_Q4K ? plan<BQ4k>(n, k, m, &per, &slices)
+                                      : (fmt == RT_HIP_BF16 ? plan<BBf16>(n, k, m, &per, &slices) : false);
+    return ok && slices > 1 ? static_cast<size_t>(slices) * m * n * sizeof(float) : 0;
+}
 
 hipError_t launch_gemv_batch(int fmt, const void* w, const float* x, float* y, int64_t n, int64_t k, int m,
                              hipStream_t s) {

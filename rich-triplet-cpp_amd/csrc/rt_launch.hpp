@@ -23,16 +23,19 @@ const DeviceInfo& device_info();
 // returns `code` (host code outside api.cpp).
 int set_error(int code, const std::string& msg);
 
-// Integer tuning knob read once from the environment (RT_HIP_<name>), else
-// `fallback`.  Used for launch-shape sweeps; defaults are the measured best.
+// Launch-shape knob: `fallback` (the measured best) in the shipped library;
+// in a sweep build (-DRT_HIP_TUNING) the environment's RT_HIP_<name>.
 int tune_param(const char* name, int fallback);
 
-// Library-owned device workspace, grown on demand, one per device.
-void* workspace(size_t bytes, hipError_t* err);
-// kArrivalCounters zeroed u32 counters per device (allocated on first use).
+// Library-owned device workspace, one per device.  It grows on demand
+// unless `s` is being captured into a hipGraph (then the call fails with
+// hipErrorStreamCaptureUnsupported); a replaced buffer is kept until the
+// process ends, since a captured graph may still write it.
+void* workspace(size_t bytes, hipStream_t s, hipError_t* err);
+// kArrivalCounters zeroed u32 counters per device (made by rt_hip_init).
 // A kernel that counts arrivals in them returns each to zero before it ends.
 constexpr size_t kArrivalCounters = 16384;
-uint32_t* arrival_counters(hipError_t* err);
+uint32_t* arrival_counters(hipStream_t s, hipError_t* err);
 
 // Largest M*K the GEMV kernels stage in LDS (f32 activations + 16-value sums).
 size_t gemv_lds_bytes(int fmt, int m, int64_t k);
@@ -83,21 +86,6 @@ hipError_t launch_gemv_q4k_bf16_fused(int count, const void* const* w, float* co
                                       float eps = 0.0f, const float* inv_freq = nullptr, int pos = 0,
                                       int head_dim = 0, int rope_jobs = 0);
 
-// Persistent decode chain (chain.hip).  The host builds the stage table with
-// chain_fill_stage (chain_stage_bytes() each) in device memory and a zeroed
-// sync area of chain_sync_words(grid) dwords; launch_chain runs one pass.
-size_t chain_lds_bytes();
-int chain_threads();
-int chain_waves_per_wg();
-int chain_max_k();
-int chain_max_grid();
-size_t chain_sync_words(int grid);
-size_t chain_err_word(int grid);  // index of the error word in the sync area
-size_t chain_stage_bytes();
-void chain_fill_stage(void* dst, const float* x, int count, const void* const* w, float* const* y,
-                      const int64_t* n, int64_t k, int ks, int tiles, int rounds, const int* tile0);
-hipError_t chain_occupancy(int* blocks_per_cu);
-hipError_t launch_chain(const void* stages, int nst, uint32_t* sync_words, int grid, hipStream_t s);
 hipError_t launch_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
                             int m, uint64_t* argmax_key, hipStream_t s);
 // M = 1 BF16 GEMV (gemv_bf16.hip); `key` (may be null) receives the fused
@@ -112,6 +100,8 @@ hipError_t launch_gemv_q4_0(const void* w, const float* x, float* y, int64_t n, 
 // K-slices beyond the LDS budget are summed through the library workspace.
 hipError_t launch_gemv_batch(int fmt, const void* w, const float* x, float* y, int64_t n, int64_t k, int m,
                              hipStream_t s);
+// Workspace bytes one launch_gemv_batch call needs (0 when K fits one slice).
+size_t gemv_batch_workspace_bytes(int fmt, int64_t n, int64_t k, int m);
 // M = 1 GGUF Q4_0 GEMV (gemv_q40.hip); LDS q40_m1_lds_bytes(k).
 size_t q40_m1_lds_bytes(int64_t k);
 hipError_t launch_gemv_q4_0_m1(const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t s);
@@ -141,6 +131,8 @@ hipError_t launch_quantize_q4k(const float* w, void* blocks, int64_t n, int64_t 
 
 hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, const float* bias,
                        float* c, int64_t m, int64_t n, int64_t k, hipStream_t s);
+// Workspace bytes one launch_gemm call needs.
+size_t gemm_workspace_bytes(int w_fmt, bool a_bf16, int64_t m, int64_t n, int64_t k);
 hipError_t launch_add_bias(float* y, const float* bias, int64_t m, int64_t n, hipStream_t s);
 
 }  // namespace rt_hip

@@ -59,9 +59,17 @@ _SIGNATURES = {
     "rt_hip_dequant_q6k_bf16": [_vp, _vp, _i64, _i64, _vp],
     "rt_hip_q6k_tile": [_vp, _vp, _i64, _i64, _vp],
     "rt_hip_gemv_q6k_tiled": [_vp, _vp, _vp, _i64, _i64, _vp],
-    "rt_hip_chain_run": [_vp, _vp],
-    "rt_hip_chain_status": [_vp, _i32],
-    "rt_hip_chain_destroy": [_vp],
+    "rt_hip_reserve_workspace": [_i64],
+}
+
+# name -> argtypes of the int64-returning size queries
+_SIZE_SIGNATURES = {
+    "rt_hip_q4k_tiled_bytes": [_i64, _i64],
+    "rt_hip_q6k_tiled_bytes": [_i64, _i64],
+    "rt_hip_workspace_bytes": [],
+    "rt_hip_gemm_workspace_bytes": [_i32, _i32, _i64, _i64, _i64],
+    "rt_hip_gemv_workspace_bytes": [_i32, _i64, _i64, _i32],
+    "rt_hip_attention_workspace_bytes": [_i32, _i32, _i64],
 }
 
 
@@ -86,12 +94,6 @@ _GGUF_SIGNATURES = [
     ("rt_hip_gguf_meta_str", C.c_int, [_vp, C.c_char_p, _i64, C.POINTER(C.c_char_p)]),
     ("rt_hip_gguf_meta_array_len", _i64, [_vp, C.c_char_p]),
 ]
-
-
-class ChainStage(C.Structure):
-    """rt_hip_chain_stage (include/rt_hip.h)."""
-    _fields_ = [("x", _vp), ("k", _i64), ("count", _i32), ("w", _vp * 4), ("y", _vp * 4),
-                ("n", _i64 * 4)]
 
 
 class RtHipError(RuntimeError):
@@ -119,16 +121,14 @@ class Library:
         self.lib = C.CDLL(path)
         self.lib.rt_hip_last_error.restype = C.c_char_p
         self.lib.rt_hip_version.restype = C.c_char_p
-        self.lib.rt_hip_q4k_tiled_bytes.restype = C.c_int64
-        self.lib.rt_hip_q4k_tiled_bytes.argtypes = [_i64, _i64]
-        self.lib.rt_hip_q6k_tiled_bytes.restype = C.c_int64
-        self.lib.rt_hip_q6k_tiled_bytes.argtypes = [_i64, _i64]
+        for name, args in _SIZE_SIGNATURES.items():
+            fn = getattr(self.lib, name)
+            fn.restype = C.c_int64
+            fn.argtypes = args
         for name, res, args in _GGUF_SIGNATURES:
             fn = getattr(self.lib, name)
             fn.restype = res
             fn.argtypes = args
-        self.lib.rt_hip_chain_create.restype = C.c_int
-        self.lib.rt_hip_chain_create.argtypes = [C.POINTER(ChainStage), _i32, C.POINTER(_vp)]
         for name, args in _SIGNATURES.items():
             fn = getattr(self.lib, name)
             fn.restype = C.c_int
@@ -176,6 +176,15 @@ def _stream(stream=None) -> int:
 
 def init(ordinal: int = 0) -> None:
     library().call("rt_hip_init", ordinal)
+
+
+def reserve_workspace(nbytes: int) -> None:
+    """Pre-size the current device's library workspace (before graph capture)."""
+    library().call("rt_hip_reserve_workspace", int(nbytes))
+
+
+def workspace_bytes() -> int:
+    return int(library().lib.rt_hip_workspace_bytes())
 
 
 def _dev_check(*ts):
@@ -485,46 +494,6 @@ class GgufFile:
 
     def meta_array_len(self, key: str) -> int:
         return self._lib.lib.rt_hip_gguf_meta_array_len(self.h, key.encode())
-
-
-class Chain:
-    """A decode step's dependent tiled-Q4_K GEMV stages run as one persistent
-    launch (rt_hip_chain_*).  ``stages`` is a list of (x, [tiled w], [y], [n], k);
-    the tensors must outlive the chain (their pointers are baked in)."""
-
-    def __init__(self, stages):
-        arr = (ChainStage * len(stages))()
-        self._keep = []
-        for i, (x, ws, ys, ns, k) in enumerate(stages):
-            if not 1 <= len(ws) <= 4 or len(ws) != len(ys) or len(ws) != len(ns):
-                raise ValueError("a stage has 1..4 GEMVs with matching w, y, n")
-            _dev_check(x, *ws, *ys)
-            st = arr[i]
-            st.x, st.k, st.count = x.data_ptr(), k, len(ws)
-            for j in range(len(ws)):
-                st.w[j], st.y[j], st.n[j] = ws[j].data_ptr(), ys[j].data_ptr(), ns[j]
-            self._keep += [x, *ws, *ys]
-        h = _vp()
-        library().call("rt_hip_chain_create", arr, len(stages), C.byref(h))
-        self.handle = h
-
-    def run(self, stream=None) -> None:
-        library().call("rt_hip_chain_run", self.handle, _stream(stream))
-
-    def status(self, reset: bool = False) -> int:
-        """0, or the error code if a stage barrier timed out in an earlier run."""
-        return library().status("rt_hip_chain_status", self.handle, 1 if reset else 0)
-
-    def close(self) -> None:
-        if self.handle:
-            library().call("rt_hip_chain_destroy", self.handle)
-            self.handle = None
-
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:  # noqa: BLE001  (interpreter shutdown)
-            pass
 
 
 def gemv_bf16_argmax(w, x, n: int, k: int, y=None, stream=None):

@@ -9,8 +9,11 @@ GEMV_TOL = 1e-5
 # bf16-MFMA GEMM, against the f32 product of the same bf16-rounded operands.
 GEMM_TOL_SAME_OPERANDS = 1e-5
 # bf16-MFMA GEMM against the reference's f32 CPU output (operand rounding):
-# relative RMS error.
-GEMM_TOL_VS_F32_RMS = 1e-2
+# relative RMS error.  RNE to bf16 leaves a relative error of RMS
+# 2^-9/sqrt(3) = 1.1e-3 per operand, about 1.6e-3 for a product of two
+# rounded operands; measured 1.65e-3 (bf16 A) to 2.33e-3 (f32 A, prefill) at
+# the full config-4/5 shapes.  The bar is 4e-3.
+GEMM_TOL_VS_F32_RMS = 4e-3
 
 
 def say(*a):

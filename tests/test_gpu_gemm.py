@@ -4,7 +4,7 @@ Two stated tolerances:
  (i)  against the f32-accumulated product of the same bf16-rounded operands
       (fp64 reference): normwise <= 1e-5;
  (ii) against the reference's f32 CPU path (Q4KMat::matmul_q4k_t's scalar
-      loop / MatBf16::matmul_by_t): relative RMS <= 1e-2 -- the bf16 operand
+      loop / MatBf16::matmul_by_t): relative RMS <= 4e-3 -- the bf16 operand
       rounding, the same philosophy as the reference's Metal GEMM test bound
       (tests/test_metal_flux.cpp:140-145).
 """
