@@ -71,12 +71,15 @@ def test_graph_replays_survive_workspace_growth(rt, orc):
         assert int(idx.item()) == want_idx
 
     check("replay 1")
-    # an eager GEMM whose bf16 copies need far more workspace: it grows
-    m, gn, gk = 512, 8192, 3072
+    # an eager GEMM whose bf16 copies need more workspace than the device has
+    # now (earlier tests in the process may have grown it): it grows
+    gn, gk = 8192, 3072
+    m = 512
+    while lib.lib.rt_hip_gemm_workspace_bytes(rt.Q4K, rt.F32, m, gn, gk) <= before:
+        m += 512
     gw = rng.standard_normal((gn, gk)).astype(np.float32) * 0.02
     blocks = rt.quantize_q4k(to_dev(gw))
     a = to_dev(rng.standard_normal((m, gk)).astype(np.float32))
-    assert lib.lib.rt_hip_gemm_workspace_bytes(rt.Q4K, rt.F32, m, gn, gk) > before
     c = rt.gemm(rt.Q4K, a, blocks, gn, gk)
     torch.cuda.synchronize()
     assert rt.workspace_bytes() > before
@@ -85,10 +88,11 @@ def test_graph_replays_survive_workspace_growth(rt, orc):
     check("replay 3")
 
     # growth inside a capture is refused with an error, and nothing breaks
-    big = lib.lib.rt_hip_gemm_workspace_bytes(rt.Q4K, rt.F32, 2048, gn, gk)
-    assert big > rt.workspace_bytes()
-    a2 = to_dev(rng.standard_normal((2048, gk)).astype(np.float32))
-    c2 = torch.empty((2048, gn), device="cuda")
+    m2 = m
+    while lib.lib.rt_hip_gemm_workspace_bytes(rt.Q4K, rt.F32, m2, gn, gk) <= rt.workspace_bytes():
+        m2 += 512
+    a2 = to_dev(rng.standard_normal((m2, gk)).astype(np.float32))
+    c2 = torch.empty((m2, gn), device="cuda")
     g2 = torch.cuda.CUDAGraph()
     with pytest.raises(rt.RtHipError, match="before capture"):
         with torch.cuda.graph(g2):
