@@ -243,6 +243,20 @@ int rt_hip_attention_decode(const float* q, const float* k_cache, const float* v
                             int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int64_t seq_len, float scale,
                             rt_hip_stream stream);
 
+/* rt_hip_attention_decode_noalloc: rt_hip_attention_decode, same arguments
+ * and the same results bit for bit, for callers that cannot allocate: code
+ * under hipGraph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  No counterpart in the reference.  It allocates nothing: the
+ * split partials live in a library-owned device array of 1 MiB per device
+ * (held until the process ends), whose address rt_hip_init looks up.  A
+ * shape whose partials exceed 1 MiB (n_q_heads * splits * 528 bytes; about
+ * one split per CU over the KV heads) fails with RT_HIP_E_SHAPE.  Every call
+ * on a device shares that array, so calls that overlap on one device race:
+ * issue them on one stream, or order the streams. */
+int rt_hip_attention_decode_noalloc(const float* q, const float* k_cache, const float* v_cache, float* out,
+                                    int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int64_t seq_len,
+                                    float scale, rt_hip_stream stream);
+
 /* The same two operations for the BF16-widened projections of a Q4_K_M
  * model (src/transformer4_load.cpp:141-143): q/k (tiled Q4_K) and a BF16 v
  * on RMSNorm(x) in one launch, as rt_hip_gemv_q4k_tiled_bf16; and a BF16

@@ -251,6 +251,8 @@ int rt_hip_init(int ordinal) {
         e = make_counters(st);
     }
     if (e != hipSuccess) return hip_fail(e, "rt_hip_init: arrival counters");
+    e = attention_scratch_setup(ordinal, nullptr);
+    if (e != hipSuccess) return hip_fail(e, "rt_hip_init: attention scratch address");
     return RT_HIP_OK;
 }
 
@@ -453,10 +455,9 @@ int rt_hip_gemv_bf16_swiglu_residual(const uint16_t* w, const float* gate, const
         launch_gemv_bf16_xop(3, w, gate, up, 0.0f, resid, n, k, static_cast<hipStream_t>(stream), true), fn);
 }
 
-int rt_hip_attention_decode(const float* q, const float* k_cache, const float* v_cache, float* out,
-                            int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int64_t seq_len, float scale,
-                            rt_hip_stream stream) {
-    const char* fn = "rt_hip_attention_decode";
+namespace {
+int attention_args(const char* fn, const float* q, const float* k_cache, const float* v_cache, const float* out,
+                   int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int64_t seq_len) {
     if (!q || !k_cache || !v_cache || !out) return fail(RT_HIP_E_ARG, std::string(fn) + ": null pointer");
     if (head_dim != 128) return fail(RT_HIP_E_UNSUPPORTED, std::string(fn) + ": head_dim must be 128");
     if (n_kv_heads < 1 || n_q_heads < n_kv_heads || n_q_heads % n_kv_heads != 0 || n_q_heads / n_kv_heads > 4)
@@ -464,12 +465,46 @@ int rt_hip_attention_decode(const float* q, const float* k_cache, const float* v
     if (seq_len < 1 || seq_len > 0x7fffffffLL) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": seq_len out of range");
     if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
         return fail(RT_HIP_E_ALIGN, std::string(fn) + ": buffers must be 16-byte aligned");
+    return RT_HIP_OK;
+}
+}  // namespace
+
+int rt_hip_attention_decode(const float* q, const float* k_cache, const float* v_cache, float* out,
+                            int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int64_t seq_len, float scale,
+                            rt_hip_stream stream) {
+    const char* fn = "rt_hip_attention_decode";
+    int rc = attention_args(fn, q, k_cache, v_cache, out, n_q_heads, n_kv_heads, head_dim, seq_len);
+    if (rc) return rc;
     hipError_t e;
     if (!state_for_current(&e)) return hip_fail(e, fn);
-    float* part = static_cast<float*>(workspace(attention_decode_workspace(n_q_heads, n_kv_heads, seq_len), static_cast<hipStream_t>(stream), &e));
+    float* part = static_cast<float*>(workspace(attention_decode_workspace(n_q_heads, n_kv_heads, seq_len),
+                                                static_cast<hipStream_t>(stream), &e));
     if (!part) return check_stream_launch(e, fn);
     return check_stream_launch(launch_attention_decode(q, k_cache, v_cache, out, part, n_q_heads, n_kv_heads,
                                                        seq_len, scale, static_cast<hipStream_t>(stream)),
+                               fn);
+}
+
+int rt_hip_attention_decode_noalloc(const float* q, const float* k_cache, const float* v_cache, float* out,
+                                    int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int64_t seq_len,
+                                    float scale, rt_hip_stream stream) {
+    const char* fn = "rt_hip_attention_decode_noalloc";
+    int rc = attention_args(fn, q, k_cache, v_cache, out, n_q_heads, n_kv_heads, head_dim, seq_len);
+    if (rc) return rc;
+    hipError_t e;
+    DeviceState* st = state_for_current(&e);
+    if (!st) return hip_fail(e, fn);
+    const size_t need = attention_decode_workspace(n_q_heads, n_kv_heads, seq_len);
+    if (need > attention_scratch_bytes())
+        return fail(RT_HIP_E_SHAPE, std::string(fn) + ": this shape needs " + std::to_string(need) +
+                                        " bytes of split partials, above the " +
+                                        std::to_string(attention_scratch_bytes()) + "-byte scratch maximum");
+    void* part = nullptr;
+    e = attention_scratch_setup(st->info.ordinal, &part);
+    if (e != hipSuccess) return hip_fail(e, fn);
+    return check_stream_launch(launch_attention_decode(q, k_cache, v_cache, out, static_cast<float*>(part),
+                                                       n_q_heads, n_kv_heads, seq_len, scale,
+                                                       static_cast<hipStream_t>(stream)),
                                fn);
 }
 

@@ -17,6 +17,8 @@
 // split order and divides: out = o / l.  The order of every sum is fixed,
 // so results are deterministic.  exp is the hardware exp2 on a log2(e)
 // scaled argument (about 1 ulp).
+#include <mutex>
+
 #include "rt_common.hpp"
 #include "rt_launch.hpp"
 
@@ -208,6 +210,39 @@ void attention_decode_shape(int64_t n_kv, int64_t seq_len, int* splits, int* chu
     const int64_t S = (seq_len + c - 1) / c;
     *splits = static_cast<int>(S < 1 ? 1 : S);
     *chunk = static_cast<int>(c);
+}
+
+// Scratch of rt_hip_attention_decode_noalloc: the split partials of one
+// call in a file-scope device array, so that entry point allocates nothing.
+// Each device holds its own copy at its own address; in host code the
+// array's name is only a stand-in, so its device address is looked up once
+// per device (attention_scratch_setup, with that device current) and that
+// pointer is what kernels receive.  Every call on a device shares the array
+// and leaves the last call's partials in it; the partial kernel writes every
+// state the merge reads, so nothing needs clearing.  Calls that overlap on
+// one device race.
+constexpr size_t kNoallocScratchBytes = size_t{1} << 20;
+static __device__ __align__(256) uint8_t scratch[kNoallocScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+}  // namespace
+
+size_t attention_scratch_bytes() { return kNoallocScratchBytes; }
+
+hipError_t attention_scratch_setup(int dev, void** out) {
+    if (dev < 0 || dev >= kMaxScratchDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[dev] = p;
+    }
+    if (out) *out = g_scratch_ptr[dev];
+    return hipSuccess;
 }
 
 size_t attention_decode_workspace(int64_t n_q, int64_t n_kv, int64_t seq_len) {

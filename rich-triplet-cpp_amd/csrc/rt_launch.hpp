@@ -50,6 +50,11 @@ hipError_t launch_gemv_q4k_mfma(const void* w, const float* x, float* y, int64_t
 // `part` holds attention_decode_workspace(...) bytes.
 void attention_decode_shape(int64_t n_kv, int64_t seq_len, int* splits, int* chunk);
 size_t attention_decode_workspace(int64_t n_q, int64_t n_kv, int64_t seq_len);
+// The allocation-free variant's per-device scratch (a file-scope device
+// array of attention_scratch_bytes()): setup looks up its device address for
+// device `dev`, which must be current, once, and returns it in *out.
+size_t attention_scratch_bytes();
+hipError_t attention_scratch_setup(int dev, void** out);
 hipError_t launch_attention_decode(const float* q, const float* kc, const float* vc, float* out, float* part,
                                    int64_t n_q, int64_t n_kv, int64_t seq_len, float scale, hipStream_t s);
 // M = 1 BF16 GEMV with a layer operation applied to x while it is staged

@@ -46,6 +46,7 @@ _SIGNATURES = {
                                             C.c_float, _i32, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_swiglu": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_attention_decode": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, C.c_float, _vp],
+    "rt_hip_attention_decode_noalloc": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, C.c_float, _vp],
     "rt_hip_gemv_q4k_tiled_residual": [_vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_swiglu_residual": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_gemv_bf16_swiglu_residual": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
