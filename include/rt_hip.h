@@ -28,6 +28,12 @@
  *   RT_HIP_Q4_0  18-byte GGUF Q4_0 blocks, K/32 per row (d:f16 | qs[16]);
  *                gguf.cpp:495-529 -- the form Q4Mat decodes from
  *   RT_HIP_BF16  uint16 bf16 bits; mat.hpp:157-207
+ *   RT_HIP_Q4MAT the reference's Q4Mat (quant.hpp:23-75) in one buffer: its
+ *                `packed` bytes (flat element r*K + c is the low nibble of
+ *                byte (r*K + c)/2 when even, the high nibble when odd; 4-bit
+ *                two's complement) at offset 0, then its f32 `scales` (one
+ *                per 32 flat elements) at rt_hip_q4mat_scales_offset(n, k);
+ *                rt_hip_q4mat_bytes(n, k) in all.  Requires K % 32 == 0.
  */
 #ifndef RT_HIP_H
 #define RT_HIP_H
@@ -57,7 +63,8 @@ typedef enum {
     RT_HIP_F32 = 0,
     RT_HIP_BF16 = 1,
     RT_HIP_Q4K = 2,
-    RT_HIP_Q4_0 = 3
+    RT_HIP_Q4_0 = 3,
+    RT_HIP_Q4MAT = 4
 } rt_hip_format;
 
 /* Largest activation batch the GEMV kernels take; the reference's
@@ -285,6 +292,20 @@ int rt_hip_gemv_q4k_tiled_bf16_rmsnorm_rope(int32_t count, const void* const* ti
 int rt_hip_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
                      int32_t m, rt_hip_stream stream);
 
+/* Q4Mat weights (RT_HIP_Q4MAT layout above), M <= 8: each byte read once for
+ * all M rows.  Replace: Q4Mat::matmul_q4_t / matmul_q4_t_blas for small M
+ * (src/quant_q4.cpp:92-156) and metal_matmul_q4_t (metal_ops.hpp:54-55,
+ * src/metal_ops.mm:117-161, 578-619).  w = s(nibble) * scale, summed in f32
+ * (factorized: agreement to f32 rounding, normwise 1e-5).  K % 32 == 0 and
+ * K <= 15872 (x and its group sums are staged in 64 KB of LDS; larger M is
+ * split into launches that fit).
+ * rt_hip_q4mat_bytes / _scales_offset: the buffer size and where the
+ * scales start (-1 for invalid n, k). */
+int64_t rt_hip_q4mat_bytes(int64_t n, int64_t k);
+int64_t rt_hip_q4mat_scales_offset(int64_t n, int64_t k);
+int rt_hip_gemv_q4mat(const void* w, const float* x, float* y, int64_t n, int64_t k, int32_t m,
+                      rt_hip_stream stream);
+
 /* GGUF Q4_0 weights streamed as 18-byte blocks.
  * Replace: Q4Mat::matmul_q4_t on GgufFile::decode_q4_0_to_q4mat output
  * (src/quant_q4.cpp:92-114, src/gguf.cpp:392-450) and metal_matmul_q4_t
@@ -413,15 +434,78 @@ int rt_hip_quantize_q4k(const float* w, void* blocks, int64_t n, int64_t k,
  * flux_dequant_q4k does, and shared by every M tile.  K % 256 == 0. */
 int rt_hip_gemm_q4k(const void* a, int32_t a_dtype, const void* blocks, const float* bias,
                     float* c, int64_t m, int64_t n, int64_t k, rt_hip_stream stream);
+/* rt_hip_gemm: the GEMM for any weight format -- RT_HIP_Q4K and RT_HIP_BF16
+ * as rt_hip_gemm_q4k / rt_hip_gemm_bf16; RT_HIP_Q4_0 (GGUF blocks) and
+ * RT_HIP_Q4MAT are dequantized once per call into the workspace as bf16 (the
+ * f32 values rounded to nearest-even) and run on the bf16 GEMM.
+ * Replace: Q4Mat::matmul_q4_t / _blas for M > 4 (src/quant_q4.cpp:92-151:
+ * dequantize, then one sgemm) and metal_matmul_q4_t at any M
+ * (src/metal_ops.mm:578-619).  K % 64 == 0.
+ * rt_hip_dequant: weight bytes -> f32 or bf16 [N, K] (out_dtype RT_HIP_F32
+ * or RT_HIP_BF16) for RT_HIP_Q4K (bit-exact dequantize_row_into),
+ * RT_HIP_Q4_0 (decode_q4_0_to_f32, gguf.cpp:495-529) and RT_HIP_Q4MAT
+ * (Q4Mat::dequantize, quant_q4.cpp:67-74). */
+int rt_hip_gemm(int32_t format, const void* a, int32_t a_dtype, const void* w, const float* bias, float* c,
+                int64_t m, int64_t n, int64_t k, rt_hip_stream stream);
+int rt_hip_dequant(int32_t format, const void* w, void* out, int32_t out_dtype, int64_t n, int64_t k,
+                   rt_hip_stream stream);
 /* Replace: MatBf16::matmul_by_t for M > 1 (src/mat.cpp:351-414).  K % 64 == 0. */
 int rt_hip_gemm_bf16(const void* a, int32_t a_dtype, const uint16_t* w, const float* bias,
                      float* c, int64_t m, int64_t n, int64_t k, rt_hip_stream stream);
 
+/* ---- weight handles ---------------------------------------------------------
+ * A weight uploaded once to the current device: the verbatim bytes of any
+ * format (the engines' upload_linear_detect_type, src/metal_decode.mm:
+ * 157-176), and with flags & RT_HIP_WEIGHT_TILED a Q4_K weight's tiled copy
+ * too, which the M == 1 GEMV then reads.  bytes must equal the format's size
+ * for (n, k).  rt_hip_weight_linear runs y[m, n] = x[m, k] W^T (+ bias) on
+ * device activations at any m, as rt_hip_linear_forward.
+ * rt_hip_weight_data: the device copy of the verbatim bytes. */
+#define RT_HIP_WEIGHT_TILED 1
+typedef struct rt_hip_weight rt_hip_weight;
+int rt_hip_weight_upload(int32_t format, const void* host, int64_t bytes, int64_t n, int64_t k, int32_t flags,
+                         rt_hip_weight** out);
+int rt_hip_weight_free(rt_hip_weight* w);
+const void* rt_hip_weight_data(const rt_hip_weight* w);
+int rt_hip_weight_linear(const rt_hip_weight* w, const float* x, const float* bias, float* y, int64_t m,
+                         rt_hip_stream stream);
+
+/* ---- host drop-ins ------------------------------------------------------------
+ * rt_hip_host_matmul: y[m, n] = x[m, k] W^T with host x and y, synchronous.
+ * The weight is uploaded on first use and found again by (host pointer, byte
+ * length) on the current device, exactly the reference's cached_weights
+ * (src/metal_ops.mm:425-434), so the caller keeps the host bytes unchanged
+ * at that address while it uses the cache.  w_host / w_bytes are the
+ * weight's bytes in `format`; for RT_HIP_Q4MAT they are Q4Mat's `packed`
+ * array and w2_host its `scales` (else w2_host is NULL).
+ * Replace: metal_gemv_q4k_t, metal_gemv_bf16_t and metal_matmul_q4_t
+ * (include/rt/metal_ops.hpp:47-68, src/metal_ops.mm:578-675), at any m.
+ * rt_hip_host_cache_clear frees the current device's cached weights;
+ * rt_hip_host_cache_bytes is their total size.  Calls on one device are
+ * serialized by the library. */
+int rt_hip_host_matmul(int32_t format, const void* w_host, int64_t w_bytes, const void* w2_host, int64_t n,
+                       int64_t k, const float* x_host, float* y_host, int64_t m);
+int rt_hip_host_cache_clear(void);
+int64_t rt_hip_host_cache_bytes(void);
+
+/* ---- graphs -------------------------------------------------------------------
+ * Capture a sequence of library calls on `stream` into a hipGraph and replay
+ * it with one launch: the analogue of the decode engine encoding a whole
+ * step into one command buffer (src/metal_decode.mm:436-482).  Pointers and
+ * scalar arguments are fixed at capture.  Reserve the workspace first (see
+ * above); calls that would grow it fail inside a capture. */
+typedef struct rt_hip_graph rt_hip_graph;
+int rt_hip_graph_begin(rt_hip_stream stream);
+int rt_hip_graph_end(rt_hip_stream stream, rt_hip_graph** out);
+int rt_hip_graph_launch(const rt_hip_graph* graph, rt_hip_stream stream);
+int rt_hip_graph_destroy(rt_hip_graph* graph);
+
 /* ---- linear dispatch ------------------------------------------------------
  * The QLinear / Linear2::fused_linear dispatch over whichever weight format
- * is loaded (src/qlinear.cpp:55-80, src/nn2.cpp:143-203): M <= 8 takes the
- * GEMV kernels, larger M the MFMA GEMM; the bias (may be NULL) is added to
- * every row (qlinear.cpp:42-53).  x is f32. */
+ * is loaded (src/qlinear.cpp:55-80, src/nn2.cpp:143-203: Q4Mat, Q4_K, BF16;
+ * GGUF Q4_0 as decoded into Q4Mat by gguf.cpp:495-529): M <= 8 takes the GEMV
+ * kernels, larger M the MFMA GEMM (rt_hip_gemm); the bias (may be NULL) is
+ * added to every row (qlinear.cpp:42-53).  x is f32.  Every format at any M. */
 int rt_hip_linear_forward(int32_t format, const void* w, const float* bias, const float* x,
                           float* y, int64_t m, int64_t n, int64_t k, rt_hip_stream stream);
 

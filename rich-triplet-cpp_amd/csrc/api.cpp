@@ -272,6 +272,10 @@ int rt_hip_reserve_workspace(int64_t bytes) {
 
 int64_t rt_hip_gemm_workspace_bytes(int32_t format, int32_t a_dtype, int64_t m, int64_t n, int64_t k) {
     if (m <= 0 || n <= 0 || k <= 0 || (a_dtype != RT_HIP_F32 && a_dtype != RT_HIP_BF16)) return -1;
+    if (format == RT_HIP_Q4_0 || format == RT_HIP_Q4MAT)
+        return static_cast<int64_t>((gemm_workspace_bytes(RT_HIP_BF16, a_dtype == RT_HIP_BF16, m, n, k) + 255) /
+                                        256 * 256 +
+                                    static_cast<size_t>(n * k) * 2);
     if (format != RT_HIP_Q4K && format != RT_HIP_BF16) return -1;
     return static_cast<int64_t>(gemm_workspace_bytes(format, a_dtype == RT_HIP_BF16, m, n, k));
 }
@@ -632,6 +636,35 @@ int rt_hip_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int
                         });
 }
 
+int64_t rt_hip_q4mat_bytes(int64_t n, int64_t k) {
+    if (n <= 0 || k <= 0 || k % 32 != 0 || n > 0x7fffffffLL || k > 0x7fffffffLL) return -1;
+    return static_cast<int64_t>(q4mat_bytes(n, k));
+}
+
+int64_t rt_hip_q4mat_scales_offset(int64_t n, int64_t k) {
+    if (rt_hip_q4mat_bytes(n, k) < 0) return -1;
+    return static_cast<int64_t>(q4mat_scales_offset(n, k));
+}
+
+int rt_hip_gemv_q4mat(const void* w, const float* x, float* y, int64_t n, int64_t k, int32_t m,
+                      rt_hip_stream stream) {
+    const char* fn = "rt_hip_gemv_q4mat";
+    int rc = gemv_args(fn, w, x, y, n, k, m, 32);
+    if (rc) return rc;
+    if (q4mat_gemv_lds_bytes(1, k) > 65536) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 15872");
+    hipError_t e;
+    if (!state_for_current(&e)) return hip_fail(e, fn);
+    int mb = m;
+    while (mb > 1 && q4mat_gemv_lds_bytes(mb, k) > 65536) --mb;
+    for (int32_t m0 = 0; m0 < m; m0 += mb) {
+        const int32_t mm = (m - m0) < mb ? (m - m0) : mb;
+        e = launch_gemv_q4mat(w, x + static_cast<size_t>(m0) * k, y + static_cast<size_t>(m0) * n, n, k, mm,
+                              static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return hip_fail(e, fn);
+    }
+    return RT_HIP_OK;
+}
+
 int rt_hip_gemv_q4_0(const void* blocks, const float* x, float* y, int64_t n, int64_t k,
                      int32_t m, rt_hip_stream stream) {
     int rc = gemv_args("rt_hip_gemv_q4_0", blocks, x, y, n, k, m, 256);
@@ -786,6 +819,61 @@ int rt_hip_gemm_bf16(const void* a, int32_t a_dtype, const uint16_t* w, const fl
                        stream);
 }
 
+int rt_hip_gemm(int32_t format, const void* a, int32_t a_dtype, const void* w, const float* bias, float* c,
+                int64_t m, int64_t n, int64_t k, rt_hip_stream stream) {
+    const char* fn = "rt_hip_gemm";
+    if (format == RT_HIP_Q4K) return rt_hip_gemm_q4k(a, a_dtype, w, bias, c, m, n, k, stream);
+    if (format == RT_HIP_BF16)
+        return rt_hip_gemm_bf16(a, a_dtype, static_cast<const uint16_t*>(w), bias, c, m, n, k, stream);
+    if (format != RT_HIP_Q4_0 && format != RT_HIP_Q4MAT)
+        return fail(RT_HIP_E_UNSUPPORTED, std::string(fn) + ": unsupported format");
+    // Validate as the bf16 GEMM will (K % 64), then dequantize W once into
+    // the workspace behind the GEMM's own scratch and run the bf16 path.
+    if (!a || !w || !c) return fail(RT_HIP_E_ARG, std::string(fn) + ": null pointer");
+    if (m <= 0 || n <= 0 || k <= 0) return fail(RT_HIP_E_ARG, std::string(fn) + ": sizes must be > 0");
+    if (a_dtype != RT_HIP_F32 && a_dtype != RT_HIP_BF16)
+        return fail(RT_HIP_E_ARG, std::string(fn) + ": a_dtype must be RT_HIP_F32 or RT_HIP_BF16");
+    if (k % 64) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": k must be a multiple of 64");
+    if (m > 0x7fffffffLL || n > 0x7fffffffLL || k > 0x7fffffffLL)
+        return fail(RT_HIP_E_SHAPE, std::string(fn) + ": sizes must fit in int32");
+    if (n % 4) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": n must be a multiple of 4");
+    if (!aligned16(a) || !aligned16(w) || !aligned16(c))
+        return fail(RT_HIP_E_ALIGN, std::string(fn) + ": a, w, c must be 16-byte aligned");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const size_t own = (gemm_workspace_bytes(RT_HIP_BF16, a_dtype == RT_HIP_BF16, m, n, k) + 255) / 256 * 256;
+    hipError_t e;
+    auto* ws = static_cast<uint8_t*>(workspace(own + static_cast<size_t>(n * k) * 2, s, &e));
+    if (!ws) return check_stream_launch(e, fn);
+    uint16_t* wb = reinterpret_cast<uint16_t*>(ws + own);
+    e = launch_dequant_4bit(format, w, wb, true, n, k, s);
+    if (e != hipSuccess) return hip_fail(e, fn);
+    return check_stream_launch(launch_gemm(RT_HIP_BF16, a, a_dtype == RT_HIP_BF16, wb, bias, c, m, n, k, s), fn);
+}
+
+int rt_hip_dequant(int32_t format, const void* w, void* out, int32_t out_dtype, int64_t n, int64_t k,
+                   rt_hip_stream stream) {
+    const char* fn = "rt_hip_dequant";
+    if (out_dtype != RT_HIP_F32 && out_dtype != RT_HIP_BF16)
+        return fail(RT_HIP_E_ARG, std::string(fn) + ": out_dtype must be RT_HIP_F32 or RT_HIP_BF16");
+    if (format == RT_HIP_Q4K)
+        return out_dtype == RT_HIP_BF16 ? rt_hip_dequant_q4k_bf16(w, static_cast<uint16_t*>(out), n, k, stream)
+                                        : rt_hip_dequant_q4k_f32(w, static_cast<float*>(out), n, k, stream);
+    if (format != RT_HIP_Q4_0 && format != RT_HIP_Q4MAT)
+        return fail(RT_HIP_E_UNSUPPORTED, std::string(fn) + ": unsupported format");
+    if (!w || !out) return fail(RT_HIP_E_ARG, std::string(fn) + ": null pointer");
+    if (n <= 0 || k <= 0) return fail(RT_HIP_E_ARG, std::string(fn) + ": n, k must be > 0");
+    if (k % 32) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": k must be a multiple of 32");
+    if (n > 0x7fffffffLL || k > 0x7fffffffLL) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": n, k must fit in int32");
+    if (!aligned16(out) || (format == RT_HIP_Q4MAT && !aligned16(w)))
+        return fail(RT_HIP_E_ALIGN, std::string(fn) + ": pointers must be 16-byte aligned");
+    if (format == RT_HIP_Q4_0 && (reinterpret_cast<uintptr_t>(w) & 1u))
+        return fail(RT_HIP_E_ALIGN, std::string(fn) + ": Q4_0 blocks must be 2-byte aligned");
+    hipError_t e;
+    if (!state_for_current(&e)) return hip_fail(e, fn);
+    return check_stream_launch(
+        launch_dequant_4bit(format, w, out, out_dtype == RT_HIP_BF16, n, k, static_cast<hipStream_t>(stream)), fn);
+}
+
 int rt_hip_linear_forward(int32_t format, const void* w, const float* bias, const float* x,
                           float* y, int64_t m, int64_t n, int64_t k, rt_hip_stream stream) {
     int rc;
@@ -797,19 +885,16 @@ int rt_hip_linear_forward(int32_t format, const void* w, const float* bias, cons
                                       static_cast<int32_t>(m), stream);
                 break;
             case RT_HIP_Q4_0: rc = rt_hip_gemv_q4_0(w, x, y, n, k, static_cast<int32_t>(m), stream); break;
+            case RT_HIP_Q4MAT: rc = rt_hip_gemv_q4mat(w, x, y, n, k, static_cast<int32_t>(m), stream); break;
             default: return fail(RT_HIP_E_UNSUPPORTED, "rt_hip_linear_forward: unsupported format");
         }
         if (rc || !bias) return rc;
         return check_stream_launch(launch_add_bias(y, bias, m, n, static_cast<hipStream_t>(stream)),
                                    "rt_hip_linear_forward");
     }
-    switch (format) {
-        case RT_HIP_Q4K: return rt_hip_gemm_q4k(x, RT_HIP_F32, w, bias, y, m, n, k, stream);
-        case RT_HIP_BF16:
-            return rt_hip_gemm_bf16(x, RT_HIP_F32, static_cast<const uint16_t*>(w), bias, y, m, n,
-                                    k, stream);
-        default: return fail(RT_HIP_E_UNSUPPORTED, "rt_hip_linear_forward: unsupported format for M > 8");
-    }
+    if (format != RT_HIP_Q4K && format != RT_HIP_BF16 && format != RT_HIP_Q4_0 && format != RT_HIP_Q4MAT)
+        return fail(RT_HIP_E_UNSUPPORTED, "rt_hip_linear_forward: unsupported format");
+    return rt_hip_gemm(format, x, RT_HIP_F32, w, bias, y, m, n, k, stream);
 }
 
 }  // extern "C"

@@ -134,6 +134,16 @@ hipError_t launch_dequant_q4k_cvt(const void* w, uint16_t* wout, int64_t n, int6
 hipError_t launch_quantize_q4k(const float* w, void* blocks, int64_t n, int64_t k,
                                hipStream_t s);
 
+// Q4Mat (q4mat.hip): one buffer of packed nibbles then f32 scales at
+// q4mat_scales_offset; K % 32 == 0.  The M <= 8 GEMV stages x [M][K] in LDS
+// (q4mat_gemv_lds_bytes).  launch_dequant_4bit: Q4Mat or GGUF Q4_0 -> bf16
+// or f32 [N, K].
+size_t q4mat_scales_offset(int64_t n, int64_t k);
+size_t q4mat_bytes(int64_t n, int64_t k);
+size_t q4mat_gemv_lds_bytes(int m, int64_t k);
+hipError_t launch_gemv_q4mat(const void* w, const float* x, float* y, int64_t n, int64_t k, int m, hipStream_t s);
+hipError_t launch_dequant_4bit(int fmt, const void* w, void* out, bool bf16, int64_t n, int64_t k, hipStream_t s);
+
 hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, const float* bias,
                        float* c, int64_t m, int64_t n, int64_t k, hipStream_t s);
 // Workspace bytes one launch_gemm call needs.

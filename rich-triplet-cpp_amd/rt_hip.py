@@ -13,10 +13,12 @@ import re
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-LIB_PATH = os.path.join(HERE, "lib", "librt_hip.so")
+# RT_HIP_LIB_PATH selects another build of the same ABI (the host-sanitizer
+# build that tests/test_sanitizers.py runs the host-code tests against).
+LIB_PATH = os.environ.get("RT_HIP_LIB_PATH", os.path.join(HERE, "lib", "librt_hip.so"))
 HEADER_PATH = os.path.join(ROOT, "include", "rt_hip.h")
 
-F32, BF16, Q4K, Q4_0 = 0, 1, 2, 3
+F32, BF16, Q4K, Q4_0, Q4MAT = 0, 1, 2, 3, 4
 GEMV_MAX_M = 8
 
 _vp, _i64, _i32 = C.c_void_p, C.c_int64, C.c_int32
@@ -61,6 +63,9 @@ _SIGNATURES = {
     "rt_hip_q6k_tile": [_vp, _vp, _i64, _i64, _vp],
     "rt_hip_gemv_q6k_tiled": [_vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_reserve_workspace": [_i64],
+    "rt_hip_gemv_q4mat": [_vp, _vp, _vp, _i64, _i64, _i32, _vp],
+    "rt_hip_gemm": [_i32, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "rt_hip_dequant": [_i32, _vp, _vp, _i32, _i64, _i64, _vp],
 }
 
 # name -> argtypes of the int64-returning size queries
@@ -71,6 +76,8 @@ _SIZE_SIGNATURES = {
     "rt_hip_gemm_workspace_bytes": [_i32, _i32, _i64, _i64, _i64],
     "rt_hip_gemv_workspace_bytes": [_i32, _i64, _i64, _i32],
     "rt_hip_attention_workspace_bytes": [_i32, _i32, _i64],
+    "rt_hip_q4mat_bytes": [_i64, _i64],
+    "rt_hip_q4mat_scales_offset": [_i64, _i64],
 }
 
 
@@ -204,7 +211,8 @@ def gemv(fmt: int, w, x, n: int, k: int, y=None, stream=None):
     if y is None:
         y = torch.empty((m, n), dtype=torch.float32, device=x.device)
     _dev_check(w, x, y)
-    name = {Q4K: "rt_hip_gemv_q4k", BF16: "rt_hip_gemv_bf16", Q4_0: "rt_hip_gemv_q4_0"}[fmt]
+    name = {Q4K: "rt_hip_gemv_q4k", BF16: "rt_hip_gemv_bf16", Q4_0: "rt_hip_gemv_q4_0",
+            Q4MAT: "rt_hip_gemv_q4mat"}[fmt]
     library().call(name, _ptr(w), _ptr(x), _ptr(y), n, k, m, _stream(stream))
     return y
 
@@ -546,9 +554,36 @@ def gemm(fmt: int, a, w, n: int, k: int, bias=None, c=None, stream=None):
         c = torch.empty((m, n), dtype=torch.float32, device=a.device)
     a_dtype = BF16 if a.dtype == torch.bfloat16 else F32
     _dev_check(a, w, c, bias)
-    name = {Q4K: "rt_hip_gemm_q4k", BF16: "rt_hip_gemm_bf16"}[fmt]
-    library().call(name, _ptr(a), a_dtype, _ptr(w), _ptr(bias), _ptr(c), m, n, k, _stream(stream))
+    library().call("rt_hip_gemm", fmt, _ptr(a), a_dtype, _ptr(w), _ptr(bias), _ptr(c), m, n, k, _stream(stream))
     return c
+
+
+def q4mat_bytes(n: int, k: int) -> int:
+    v = int(library().lib.rt_hip_q4mat_bytes(n, k))
+    if v < 0:
+        raise ValueError("q4mat: need n > 0, k % 32 == 0")
+    return v
+
+
+def q4mat_upload(packed, scales, n: int, k: int):
+    """The RT_HIP_Q4MAT buffer (uint8 device tensor) from a Q4Mat's host
+    `packed` bytes and f32 `scales` (numpy arrays)."""
+    import numpy as np  # noqa: PLC0415
+    torch = _torch()
+    off = int(library().lib.rt_hip_q4mat_scales_offset(n, k))
+    buf = np.zeros(q4mat_bytes(n, k), np.uint8)
+    buf[:packed.size] = np.asarray(packed, np.uint8).reshape(-1)
+    buf[off:off + 4 * scales.size] = np.ascontiguousarray(scales, np.float32).view(np.uint8).reshape(-1)
+    return torch.from_numpy(buf).cuda()
+
+
+def dequant(fmt: int, w, n: int, k: int, bf16: bool = False, stream=None):
+    """Weight bytes -> [n, k] f32 (or bf16 bits as int16)."""
+    torch = _torch()
+    out = torch.empty((n, k), dtype=torch.int16 if bf16 else torch.float32, device=w.device)
+    _dev_check(w, out)
+    library().call("rt_hip_dequant", fmt, _ptr(w), _ptr(out), BF16 if bf16 else F32, n, k, _stream(stream))
+    return out
 
 
 def linear_forward(fmt: int, w, x, n: int, k: int, bias=None, y=None, stream=None):
