@@ -502,9 +502,43 @@ def bench_decode_layers(args, rt, torch):
 
 # ------------------------------------------------------ other BASELINE configs --
 
-def bench_single_gemv(args, rt, torch, fmt, n, k, label, copies_bytes=768 << 20):
-    """One GEMV shape, rotating through enough distinct weight copies to
-    exceed the 256 MB MALL, so each launch streams from HBM."""
+def _cpu_timed(fn, budget_s: float, min_reps: int = 3, max_reps: int = 50):
+    """Median wall time of fn() after one warm-up, repeated until budget_s."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_reps or (time.perf_counter() < t_end and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2], len(times)
+
+
+def _cpu_handles():
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import Oracle, Reference, reference_available  # noqa: PLC0415
+    if reference_available():
+        ref = Reference()
+        return "reference", ref, ref.hardware_threads(), Oracle()
+    orc = Oracle()
+    return "port", orc, orc.hardware_threads(), orc
+
+
+def line(args, metric, value, unit, ms, higher, dtype, config, roofline, cpu, data=None):
+    return {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": higher, "scaling": "weak",
+            "vs_baseline": None, "dtype": dtype,
+            "data": data or "synthetic: random N(0,0.02) weights quantized on GPU, N(0,1) inputs",
+            "config": config, "roofline": roofline, "cpu_baseline": cpu}
+
+
+def bench_single_gemv(args, rt, torch, fmt, n, k, label, workload, copies_bytes=768 << 20, argmax=False):
+    """One GEMV shape (2a, 2b), rotating through enough
+    distinct weight copies to exceed the 256 MB MALL, so each launch streams
+    from HBM.  The launch is the whole product (and with argmax=True the
+    fused first-max of the logits), so it is also the roofline kernel; its
+    duration is the HIP-event time of the timed replays over the launches."""
+    import numpy as np
     wb = weight_bytes(fmt, n, k, rt)
     copies = max(2, copies_bytes // wb)
     g = torch.Generator(device="cuda").manual_seed(0)
@@ -525,18 +559,74 @@ def bench_single_gemv(args, rt, torch, fmt, n, k, label, copies_bytes=768 << 20)
 
     def run():
         for w in ws:
-            rt.gemv(fmt, w, x, n, k, y=y)
+            if argmax:
+                rt.gemv_bf16_argmax(w, x, n, k, y=y)
+            else:
+                rt.gemv(fmt, w, x, n, k, y=y)
 
     ms, _ = time_graph(torch, run, args.warmup, args.steps)
     us = ms * 1e3 / copies
     nbytes = wb + 4 * k + 4 * n
     gbs = nbytes / (us * 1e-6) / 1e9
-    return {"metric": f"{label} achieved HBM GB/s", "value": round(gbs, 1), "unit": "GB/s",
-            "us_per_launch": round(us, 3), "bytes_per_launch": nbytes, "copies": int(copies),
-            "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}
+    roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "us_per_launch": round(us, 3),
+            "bytes_per_launch": nbytes}
+    cpu = None
+    if not args.no_cpu_baseline:
+        kind, cref, threads, orc = _cpu_handles()
+        wh = ws[0].cpu().numpy()
+        xh = x.cpu().numpy()
+        if fmt == rt.Q4K:
+            desc = f"Q4KMat::matmul_q4k_t -> gemv_mt, threads = min(hw={threads}, N/128), x86 dot_row"
+            if kind == "reference":
+                h = cref.q4k_new(wh, n, k)
+                out = np.empty((1, n), np.float32)
+                med, reps = _cpu_timed(lambda: cref.q4k_handle_matmul_t(h, xh, 1, out), 10.0)
+                cref.q4k_delete(h)
+            else:
+                med, reps = _cpu_timed(lambda: orc.q4k_matmul_t(wh, n, k, xh), 10.0)
+        elif fmt == rt.BF16:
+            wh = wh.view(np.uint16).reshape(n, k)
+            desc = (f"MatBf16::matmul_by_t -> gemv_mt, threads = min(hw={threads}, N/128), x86 dot_row"
+                    + (", then the first-max argmax (transformer5.cpp:382-391)" if argmax else ""))
+            if kind == "reference":
+                h = cref.bf16_new(wh, n, k)
+                out = np.empty((1, n), np.float32)
+
+                def once():
+                    cref.bf16_handle_matmul_t(h, xh, 1, out)
+                    if argmax:
+                        orc.argmax_first(out.reshape(-1))
+                med, reps = _cpu_timed(once, 10.0)
+                cref.bf16_delete(h)
+            else:
+                med, reps = _cpu_timed(lambda: orc.bf16_matmul_t(wh, xh), 10.0)
+        else:  # Q4_0: Q4Mat::matmul_q4_t on decode_q4_0_to_q4mat of the same bytes (single-threaded)
+            packed, scales = orc.q4_0_to_q4mat(wh, n * k)
+            desc = "Q4Mat::matmul_q4_t (single-threaded) on decode_q4_0_to_q4mat of the same blocks"
+            if kind == "reference":
+                med, reps = _cpu_timed(lambda: cref.q4mat_matmul_t(packed, scales, n, k, xh), 10.0)
+            else:
+                med, reps = _cpu_timed(lambda: orc.q4mat_matmul_t(packed, scales, n, k, xh), 10.0)
+            threads = 1
+        cpu = {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+               "sample": f"the whole GEMV, median of {reps} reps ({med * 1e3:.2f} ms each); {desc}",
+               "us_per_launch": round(med * 1e6, 1)}
+    return line(args, f"{label} achieved HBM GB/s", round(gbs, 1), "GB/s", ms / copies, True,
+                "q4_k weights, f32 activations (3 exact int8 limbs per value, power-of-two scale per 32)"
+                if fmt == rt.Q4K else ("bf16 weights, f32 activations" if fmt == rt.BF16
+                                       else "q4_0 weights, f32 activations"),
+                {"workload": workload, "n": n, "k": k, "bytes_per_launch": nbytes, "weight_copies": int(copies),
+                 "us_per_launch": round(us, 3), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)},
+                roof, cpu)
 
 
-def bench_gemm(args, rt, torch, shapes, label, a_bf16):
+def bench_gemm(args, rt, torch, shapes, label, a_bf16, workload):
+    """BASELINE configs 4 and 5: Q4_K GEMMs (dequantize once per call, bf16
+    MFMA, f32 accumulate), one graph of the config's GEMMs per step.  The
+    roofline kernel is the bf16 GEMM of the largest shape alone (a BF16
+    weight of the same shape, so no dequantization in the timed launches)."""
+    import numpy as np
     g = torch.Generator(device="cuda").manual_seed(0)
     items = []
     flops = 0
@@ -548,18 +638,59 @@ def bench_gemm(args, rt, torch, shapes, label, a_bf16):
         if a_bf16:
             a = a.to(torch.bfloat16)
         c = torch.empty((m, n), device="cuda")
-        items.append((a, blocks, c, n, k))
+        items.append((a, blocks, c, m, n, k))
         flops += 2 * m * n * k
+    need = max(rt.library().lib.rt_hip_gemm_workspace_bytes(rt.Q4K, rt.BF16 if a_bf16 else rt.F32, m, n, k)
+               for _, _, _, m, n, k in items)
+    rt.reserve_workspace(need)
 
     def run():
-        for a, blocks, c, n, k in items:
+        for a, blocks, c, _, n, k in items:
             rt.gemm(rt.Q4K, a, blocks, n, k, c=c)
 
     ms, _ = time_graph(torch, run, args.warmup, args.steps)
     tflops = flops / (ms * 1e-3) / 1e12
-    return {"metric": f"{label} bf16-MFMA TFLOP/s", "value": round(tflops, 1), "unit": "TFLOP/s",
-            "ms_per_step": round(ms, 4), "flops": flops,
-            "pct_bf16_peak": round(100 * tflops / BF16_PEAK_TFLOPS, 2)}
+    # roofline kernel: the largest shape's bf16 GEMM, repeated
+    a, blocks, c, m, n, k = max(items, key=lambda it: it[3] * it[4] * it[5])
+    wbf = rt.dequant_q4k(blocks, n, k, bf16=True)
+    ab = a if a_bf16 else a.to(torch.bfloat16)
+    reps = 10
+
+    def run_k():
+        for _ in range(reps):
+            rt.gemm(rt.BF16, ab, wbf, n, k, c=c)
+
+    ms_k, _ = time_graph(torch, run_k, 2, max(3, args.steps // 5))
+    us_k = ms_k * 1e3 / reps
+    kt = 2 * m * n * k / (us_k * 1e-6) / 1e12
+    roof = {"bound": "mfma", "achieved": round(kt, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(kt / BF16_PEAK_TFLOPS, 4), "traffic": None,
+            "kernel": f"bf16 MFMA GEMM {m}x{n}x{k} (bf16 operands, f32 accumulate)",
+            "us_per_launch": round(us_k, 2), "flops_per_launch": 2 * m * n * k}
+    cpu = None
+    if not args.no_cpu_baseline:
+        kind, cref, threads, orc = _cpu_handles()
+        total = 0.0
+        parts = []
+        rows = 64
+        for a, blocks, _, m, n, k in items:
+            bh = blocks.cpu().numpy().reshape(n, -1)[:rows].reshape(-1)
+            ah = a.float().cpu().numpy()
+            fn = (lambda bh=bh, ah=ah, k=k: cref.q4k_matmul_t(bh, rows, k, ah)) if kind == "reference" else \
+                (lambda bh=bh, ah=ah, k=k: orc.q4k_matmul_t(bh, rows, k, ah))
+            med, _ = _cpu_timed(fn, 2.0, min_reps=1, max_reps=3)
+            total += med * n / rows
+            parts.append(f"{m}x{n}x{k}: {med * 1e3:.0f} ms per {rows} rows")
+        cpu = {"value": round(flops / total / 1e9, 3), "unit": "GFLOP/s", "cores": 1, "kind": kind,
+               "sample": ("the reference's Linux M>1 path, Q4KMat::matmul_q4k_t's single-threaded loop "
+                          f"(quant_q4k.cpp:611-623), timed on the first {rows} output rows of each GEMM and "
+                          f"extrapolated linearly to all rows (labelled extrapolation): " + "; ".join(parts)),
+               "ms_per_step_extrapolated": round(total * 1e3, 1)}
+    return line(args, f"{label} bf16-MFMA TFLOP/s", round(tflops, 1), "TFLOP/s", ms, True,
+                "q4_k weights dequantized to bf16, " + ("bf16" if a_bf16 else "f32->bf16") +
+                " activations, f32 accumulate",
+                {"workload": workload, "shapes": [list(s) for s in shapes], "flops": flops,
+                 "pct_bf16_peak": round(100 * tflops / BF16_PEAK_TFLOPS, 2)}, roof, cpu)
 
 
 def main() -> int:
@@ -608,21 +739,30 @@ def main() -> int:
         out = bench_decode(args, rt, torch)
     elif args.workload == "q4k_gemv":
         out = bench_single_gemv(args, rt, torch, rt.Q4K, 6912, 1024,
-                                "config 1 Q4_K GEMV 6912x1152 (Release semantics: K=1024)")
+                                "config 1 Q4_K GEMV 6912x1152 (Release semantics: K=1024)",
+                                "config 1: Q4_K GEMV 6912x1152, 4 super-blocks per row (reference Release "
+                                "semantics), batch 1")
     elif args.workload == "q4_0_gemv":
-        out = bench_single_gemv(args, rt, torch, rt.Q4_0, 4096, 4096, "config 2a GGUF Q4_0 GEMV 4096x4096")
+        out = bench_single_gemv(args, rt, torch, rt.Q4_0, 4096, 4096, "config 2a GGUF Q4_0 GEMV 4096x4096",
+                                "config 2a: GGUF Q4_0 GEMV 4096x4096, batch 1")
     elif args.workload == "bf16_lm_head":
-        out = bench_single_gemv(args, rt, torch, rt.BF16, 262144, 1152, "config 2b BF16 GEMV 262144x1152")
+        out = bench_single_gemv(args, rt, torch, rt.BF16, 262144, 1152,
+                                "config 2b BF16 GEMV 262144x1152 + argmax",
+                                "config 2b: BF16 lm_head GEMV 262144x1152 with the fused first-max argmax, "
+                                "batch 1", argmax=True)
     elif args.workload == "prefill":
         out = bench_gemm(args, rt, torch, [(512, FFN, HIDDEN), (512, FFN, HIDDEN), (512, HIDDEN, FFN)],
-                         "config 4 prefill Q4_K GEMM M=512 (gate, up, down)", False)
+                         "config 4 prefill Q4_K GEMM M=512 (gate, up, down)", False,
+                         "config 4: Llama-3.2-3B prefill gate/up/down Q4_K GEMMs, M=512, f32 activations")
     elif args.workload == "layer_ops":
         out = bench_layer_ops(args, rt, torch)
     elif args.workload == "decode_layers":
         out = bench_decode_layers(args, rt, torch)
     elif args.workload == "flux":
         out = bench_gemm(args, rt, torch, [(4608, 9216, 3072), (4608, 12288, 3072), (4608, 3072, 12288)],
-                         "config 5 FLUX linears M=4608 (QKV, MLP-in, MLP-out)", True)
+                         "config 5 FLUX linears M=4608 (QKV, MLP-in, MLP-out)", True,
+                         "config 5: FLUX.1-schnell MMDiT QKV / MLP-in / MLP-out Q4_K GEMMs, M=4608, bf16 "
+                         "activations")
     else:
         raise SystemExit(f"workload {args.workload} not available yet")
     print(json.dumps(out), flush=True)

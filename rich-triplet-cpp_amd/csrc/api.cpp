@@ -737,16 +737,14 @@ int rt_hip_gemv_bf16_argmax(const uint16_t* w, const float* x, float* y, int64_t
     if (rc) return rc;
     if (!idx) return fail(RT_HIP_E_ARG, "rt_hip_gemv_bf16_argmax: null idx");
     hipError_t e;
-    if (gemv_lds_bytes(RT_HIP_BF16, 1, k) > 65536)
-        return fail(RT_HIP_E_SHAPE, "rt_hip_gemv_bf16_argmax: k too large");
-    uint64_t* key = static_cast<uint64_t*>(workspace(8, static_cast<hipStream_t>(stream), &e));
+    if (bf16_m1_lds_bytes(k) > 65536) return fail(RT_HIP_E_SHAPE, "rt_hip_gemv_bf16_argmax: k too large");
+    const int64_t parts = bf16_argmax_partials(n, k);
+    uint64_t* key = static_cast<uint64_t*>(workspace(static_cast<size_t>(parts) * 8, static_cast<hipStream_t>(stream), &e));
     if (!key) return check_stream_launch(e, "rt_hip_gemv_bf16_argmax: workspace");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if ((e = launch_argmax_init(key, 1, s)) != hipSuccess)
+    if ((e = launch_gemv_bf16_m1(w, x, y, n, k, key, s)) != hipSuccess)
         return hip_fail(e, "rt_hip_gemv_bf16_argmax");
-    if ((e = launch_gemv_bf16(w, x, y, n, k, 1, key, s)) != hipSuccess)
-        return hip_fail(e, "rt_hip_gemv_bf16_argmax");
-    if ((e = launch_argmax_finalize(key, 1, idx, val, s)) != hipSuccess)
+    if ((e = launch_argmax_reduce(key, parts, idx, val, s)) != hipSuccess)
         return hip_fail(e, "rt_hip_gemv_bf16_argmax");
     return RT_HIP_OK;
 }

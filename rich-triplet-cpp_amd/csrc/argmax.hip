@@ -61,7 +61,46 @@ __global__ void k_argmax_finalize(const uint64_t* keys, int64_t rows, int64_t* i
     if (val) val[i] = __uint_as_float(bits);
 }
 
+// Largest of `count` partial keys (0 = empty) -> idx[0], val[0]; one
+// workgroup, order-independent.
+__global__ __launch_bounds__(1024) void k_argmax_reduce(const uint64_t* __restrict__ part, int64_t count,
+                                                        int64_t* idx, float* val) {
+    __shared__ uint64_t wbest[1024 / kWave];
+    uint64_t best = kInitKey;
+    // eight loads in flight per thread before any is compared
+    for (int64_t i0 = threadIdx.x; i0 < count; i0 += 8 * 1024) {
+        uint64_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t i = i0 + u * 1024;
+            v[u] = i < count ? part[i] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) best = v[u] > best ? v[u] : best;
+    }
+#pragma unroll
+    for (int off = kWave / 2; off >= 1; off >>= 1) {
+        const uint64_t o = __shfl_xor(best, off, kWave);
+        best = o > best ? o : best;
+    }
+    if ((threadIdx.x & (kWave - 1)) == 0) wbest[threadIdx.x / kWave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = wbest[0];
+        for (int w = 1; w < 1024 / kWave; ++w) b = wbest[w] > b ? wbest[w] : b;
+        const uint32_t u = static_cast<uint32_t>(b >> 32);
+        const uint32_t bits = (u & 0x80000000u) ? (u & 0x7fffffffu) : ~u;
+        idx[0] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(b));
+        if (val) val[0] = __uint_as_float(bits);
+    }
+}
+
 }  // namespace
+
+hipError_t launch_argmax_reduce(const uint64_t* part, int64_t count, int64_t* idx, float* val, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax_reduce, dim3(1), dim3(1024), 0, s, part, count, idx, val);
+    return hipGetLastError();
+}
 
 hipError_t launch_argmax_init(uint64_t* keys, int64_t rows, hipStream_t s) {
     const unsigned blocks = static_cast<unsigned>((rows + 255) / 256);

@@ -13,7 +13,24 @@ __global__ __launch_bounds__(T) void k_gemv_bf16(const uint16_t* __restrict__ W,
                                                  float* __restrict__ Y, int N, int K,
                                                  uint64_t* __restrict__ key) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    rows<D, XP, ARGMAX, T>(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), W, X, Y, N, K, key, lds);
+    if constexpr (ARGMAX) {
+        // The fused argmax: each wave's best key lands in LDS, the
+        // workgroup's best goes to key[blockIdx.x], and a second launch folds
+        // those partials (one atomic target for every wave serialized the
+        // 262144-row lm_head).
+        __shared__ uint64_t wbest[T / kWave];
+        rows<D, XP, ARGMAX, T>(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), W, X, Y, N, K, wbest,
+                               lds);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint64_t b = wbest[0];
+            for (int w = 1; w < T / kWave; ++w) b = wbest[w] > b ? wbest[w] : b;
+            key[blockIdx.x] = b;
+        }
+    } else {
+        rows<D, XP, ARGMAX, T>(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), W, X, Y, N, K, key,
+                               lds);
+    }
 }
 
 // The same with a layer operation applied to x while it is staged (XOp).
@@ -28,16 +45,20 @@ __global__ __launch_bounds__(T) void k_gemv_bf16_xop(const uint16_t* __restrict_
 
 // T threads per workgroup, each wave looping over its rows; x is prefetched into registers before the
 // weight prologue when XP * T covers K / 4 (else the rest is copied after).
-template <bool ARGMAX, int T>
-hipError_t run(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k, uint64_t* key,
-               hipStream_t s) {
-    // Rows per wave (at most 64: the row sums stay in lanes), measured: 4
-    // for short rows (<= 3 pieces: one row alone leaves the ring part
-    // empty), 2 for long ones (x is staged by half as many workgroups), else 1.
+// Rows per wave (at most 64: the row sums stay in lanes), measured: 4 for
+// short rows (<= 3 pieces: one row alone leaves the ring part empty), 2 for
+// long ones (x is staged by half as many workgroups), else 1.
+int64_t bf16_workgroups(int64_t n, int64_t k, int T) {
     const int64_t waves = T / kWave, pieces = (k + kPiece - 1) / kPiece;
     int64_t rpw = tune_param("BF16_ROWS_PER_WAVE", pieces <= 3 ? 4 : (pieces >= 12 ? 2 : 1));
     rpw = rpw < 1 ? 1 : (rpw > 64 ? 64 : rpw);
-    const int64_t wgs = (n + waves * rpw - 1) / (waves * rpw);
+    return (n + waves * rpw - 1) / (waves * rpw);
+}
+
+template <bool ARGMAX, int T>
+hipError_t run(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k, uint64_t* key,
+               hipStream_t s) {
+    const int64_t wgs = bf16_workgroups(n, k, T);
     const size_t lds = bf16_m1_lds_bytes(k);
     const int ik = static_cast<int>(k), in = static_cast<int>(n);
     const int64_t per = (k / 4 + T - 1) / T;
@@ -66,6 +87,12 @@ hipError_t run_rows(const uint16_t* w, const float* x, float* y, int64_t n, int6
 }  // namespace
 
 size_t bf16_m1_lds_bytes(int64_t k) { return bf16_gemv::lds_bytes(k); }
+
+int64_t bf16_argmax_partials(int64_t n, int64_t k) {
+    const int waves = tune_param("BF16_WAVES", 8);
+    const int T = waves == 4 ? 256 : (waves == 12 ? 768 : (waves == 16 ? 1024 : 512));
+    return bf16_workgroups(n, k, T);
+}
 
 hipError_t launch_gemv_bf16_m1(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
                                uint64_t* key, hipStream_t s) {

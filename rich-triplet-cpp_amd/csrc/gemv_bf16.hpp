@@ -249,8 +249,9 @@ __device__ __forceinline__ void rows(int blk, int nblk, const uint16_t* __restri
         Yg[gw + lane * NW] = ADD ? Yg[gw + lane * NW] + out : out;
     }
     if constexpr (ARGMAX) {
-        if (lane == 0 && best != 0)
-            atomicMax(reinterpret_cast<unsigned long long*>(key), static_cast<unsigned long long>(best));
+        // the wave's best key (0: no row) into slot `wave` of the caller's
+        // per-workgroup array (LDS), which the caller folds
+        if (lane == 0) key[wave] = best;
     }
 }
 
