@@ -500,6 +500,78 @@ int rt_hip_graph_end(rt_hip_stream stream, rt_hip_graph** out);
 int rt_hip_graph_launch(const rt_hip_graph* graph, rt_hip_stream stream);
 int rt_hip_graph_destroy(rt_hip_graph* graph);
 
+/* ---- decode engine -------------------------------------------------------------
+ * A model's decode step on the device: weights uploaded once, a KV cache of
+ * max_seq positions, and the whole step -- embedding, every layer, the final
+ * norm and the lm_head -- replayed as one captured hipGraph per token.  The
+ * token and its position are written to device memory before each replay,
+ * so the graph is captured once (per batch size) and never again.
+ * Replace: MetalDecodeContext::create / decode_step / decode_step_batch /
+ * sync_kv_from_cpu (include/rt/metal_decode.hpp:41-69, src/metal_decode.mm:
+ * 436-938) for Gemma 3, and the Llama 3.2 decode loop
+ * (src/transformer5.cpp:152-266) for Llama.
+ *
+ * RT_HIP_ARCH_GEMMA3 is the Metal engine's layer (metal_decode.mm:436-482):
+ * RMSNorm x (1 + gamma); q/k/v; per-head RMSNorm of q and k (1 + gamma);
+ * NeoX RoPE with angle (pos * scale) / theta^(2i/d); the KV append; attention
+ * scaled by attn_scale over the window [pos + 1 - sliding_window, pos] on
+ * local layers and every position on global ones (layer % global_every ==
+ * global_every - 1: theta rope_theta, scale rope_freq_scale; local layers
+ * rope_theta_local, rope_freq_scale_local); o; the post-attention norm then
+ * the residual add; the pre-FFN norm; gate/up; gelu_tanh(gate) * up; down;
+ * the post-FFN norm then the residual add.  The embedding is scaled by
+ * embed_scale (sqrt(hidden) for Gemma 3).
+ * RT_HIP_ARCH_LLAMA is LlamaBlock::forward_cached (transformer5.cpp:198-212):
+ * RMSNorm x gamma, q/k/v, RoPE (interleaved pairing, or half-split with
+ * rope_half; angle pos * inv_freq[i], inv_freq from llama_inv_freq or
+ * 1 / theta^(2i/d)), attention (1/sqrt(head_dim) unless attn_scale is set),
+ * o + residual, RMSNorm, gate/up, silu(gate) * up, down + residual.
+ * kv_f16 keeps the cache in f16 (RNE), as the Metal engine does.
+ * Projections are Q4_K or BF16 (metal_decode.mm:157-176), the embedding BF16
+ * or F32, norms F32.  head_dim 64, 128 or 256; n_heads = 1..4 x n_kv_heads;
+ * hidden, ffn and n_heads x head_dim multiples of 256.
+ * step returns when the logits are on the host (as decode_step does);
+ * argmax_host receives the first-max index (transformer5.cpp:382-391).
+ * step_batch runs count <= max_batch tokens at positions start_pos.. in one
+ * graph, each weight byte read once for all of them (decode_step_batch,
+ * metal_decode.mm:887-938); logits are [count][vocab].
+ * set_kv loads prefilled cache rows (f32, converted to f16 when kv_f16).
+ * Calls on one decoder must not overlap. */
+enum { RT_HIP_ARCH_LLAMA = 0, RT_HIP_ARCH_GEMMA3 = 1 };
+enum {
+    RT_HIP_T_EMBED = 0, RT_HIP_T_OUTPUT_NORM = 1, RT_HIP_T_LM_HEAD = 2,
+    RT_HIP_T_ATTN_NORM = 3, RT_HIP_T_Q = 4, RT_HIP_T_K = 5, RT_HIP_T_V = 6, RT_HIP_T_O = 7,
+    RT_HIP_T_Q_NORM = 8, RT_HIP_T_K_NORM = 9, RT_HIP_T_POST_ATTN_NORM = 10, RT_HIP_T_FFN_NORM = 11,
+    RT_HIP_T_GATE = 12, RT_HIP_T_UP = 13, RT_HIP_T_DOWN = 14, RT_HIP_T_POST_FFN_NORM = 15
+};
+typedef struct rt_hip_decoder_config {
+    int32_t arch;
+    int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, max_seq;
+    float norm_eps;
+    float rope_theta, rope_theta_local;
+    float rope_freq_scale, rope_freq_scale_local;
+    int32_t rope_half;
+    int32_t sliding_window;   /* 0: none */
+    int32_t global_every;     /* Gemma 3: 6 */
+    float attn_scale;         /* 0: 1/sqrt(head_dim) */
+    float embed_scale;        /* 0: 1 */
+    int32_t kv_f16;
+    int32_t max_batch;        /* 0..8 */
+    const float* llama_inv_freq;  /* [head_dim / 2] or NULL (copied at create) */
+} rt_hip_decoder_config;
+typedef struct rt_hip_decoder rt_hip_decoder;
+int rt_hip_decoder_create(const rt_hip_decoder_config* cfg, rt_hip_decoder** out);
+int rt_hip_decoder_set_tensor(rt_hip_decoder* dec, int32_t layer, int32_t tensor, int32_t format, const void* host,
+                              int64_t bytes);
+int rt_hip_decoder_set_kv(rt_hip_decoder* dec, int32_t layer, const float* k_host, const float* v_host, int64_t rows);
+int rt_hip_decoder_step(rt_hip_decoder* dec, int32_t token, int32_t pos, float* logits_host, int64_t* argmax_host,
+                        rt_hip_stream stream);
+int rt_hip_decoder_step_batch(rt_hip_decoder* dec, const int32_t* tokens, int32_t count, int32_t start_pos,
+                              float* logits_host, rt_hip_stream stream);
+int64_t rt_hip_decoder_vocab(const rt_hip_decoder* dec);
+const float* rt_hip_decoder_logits(const rt_hip_decoder* dec);
+int rt_hip_decoder_destroy(rt_hip_decoder* dec);
+
 /* ---- linear dispatch ------------------------------------------------------
  * The QLinear / Linear2::fused_linear dispatch over whichever weight format
  * is loaded (src/qlinear.cpp:55-80, src/nn2.cpp:143-203: Q4Mat, Q4_K, BF16;

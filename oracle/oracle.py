@@ -78,6 +78,10 @@ class Oracle:
         self._rope_half = _bind(L, "orc_llama_rope_half", None, _f32p, _sz, _sz, _sz, _f32p, _f32p)
         self._attn = _bind(L, "orc_gqa_attention_decode", None, _f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _sz,
                            C.c_float, _f32p)
+        self._rms_head = _bind(L, "orc_rmsnorm_per_head", None, _f32p, _f32p, _sz, _sz, C.c_float, _f32p)
+        self._rope_neox = _bind(L, "orc_rope_neox", None, _f32p, _sz, _sz, C.c_float, C.c_float, _sz, _f32p)
+        self._gelu = _bind(L, "orc_gelu_tanh", None, _f32p, _sz, _f32p)
+        self._f16_rne_n = _bind(L, "orc_f32_to_f16_rne_n", None, _f32p, _u16p, _sz)
         self._argmax = _bind(L, "orc_argmax_first", C.c_int64, _f32p, _sz)
         self._normal = _bind(L, "orc_initrng_normal", None, C.c_uint64, _sz, C.c_float, _f32p)
         self._hw = _bind(L, "orc_hardware_threads", C.c_int)
@@ -110,13 +114,39 @@ class Oracle:
         return out.reshape(np.shape(x))
 
     def gqa_attention_decode(self, q, k_cache, v_cache, seq_len: int, n_q: int, n_kv: int, d: int,
-                             scale: float) -> np.ndarray:
+                             scale: float, k_start: int = 0) -> np.ndarray:
+        """Positions [k_start, seq_len) of the cache (k_start > 0: a sliding window)."""
         qq = np.ascontiguousarray(q, np.float32).reshape(-1)
         kc = np.ascontiguousarray(k_cache, np.float32).reshape(-1)
         vc = np.ascontiguousarray(v_cache, np.float32).reshape(-1)
         out = np.empty(n_q * d, np.float32)
-        self._attn(qq, kc, vc, 0, seq_len, n_q, n_kv, d, scale, out)
+        self._attn(qq, kc, vc, k_start, seq_len, n_q, n_kv, d, scale, out)
         return out
+
+    # Gemma 3 decode operations -- shaders/decode_gemma3.msl
+    def rmsnorm_per_head(self, x, gamma, n_heads: int, head_dim: int, eps: float) -> np.ndarray:
+        xx = np.ascontiguousarray(x, np.float32).reshape(-1)
+        out = np.empty_like(xx)
+        self._rms_head(xx, np.ascontiguousarray(gamma, np.float32), n_heads, head_dim, eps, out)
+        return out.reshape(np.shape(x))
+
+    def rope_neox(self, x, n_heads: int, head_dim: int, theta: float, freq_scale: float, pos: int) -> np.ndarray:
+        xx = np.ascontiguousarray(x, np.float32).reshape(-1)
+        out = np.empty_like(xx)
+        self._rope_neox(xx, n_heads, head_dim, theta, freq_scale, pos, out)
+        return out.reshape(np.shape(x))
+
+    def gelu_tanh(self, x) -> np.ndarray:
+        xx = np.ascontiguousarray(x, np.float32).reshape(-1)
+        out = np.empty_like(xx)
+        self._gelu(xx, xx.size, out)
+        return out.reshape(np.shape(x))
+
+    def f32_to_f16_rne_n(self, x) -> np.ndarray:
+        xx = np.ascontiguousarray(x, np.float32).reshape(-1)
+        out = np.empty(xx.size, np.uint16)
+        self._f16_rne_n(xx, out, xx.size)
+        return out.reshape(np.shape(x))
 
     def swiglu(self, gate: np.ndarray, up: np.ndarray) -> np.ndarray:
         g = np.ascontiguousarray(gate, np.float32).reshape(-1)

@@ -760,3 +760,80 @@ void orc_initrng_normal(uint64_t seed, size_t n, float std_dev, float* out) {
         out[i] = r * cosf(theta) * std_dev;
     }
 }
+
+/* ---- Gemma 3 decode operations (the Metal engine, src/shaders/decode_gemma3.msl,
+ * as src/metal_decode.mm:436-482 sequences them) -------------------------- */
+
+/* rms_norm_per_head (decode_gemma3.msl:63-97): per head of head_dim values,
+ * rms_inv = 1 / sqrt(sum(x^2) / head_dim + eps), out = x * rms_inv * (1 + gamma),
+ * gamma [head_dim] shared by every head. */
+void orc_rmsnorm_per_head(const float* x, const float* gamma, size_t n_heads, size_t head_dim, float eps,
+                          float* out) {
+    for (size_t h = 0; h < n_heads; ++h) {
+        const float* xh = x + h * head_dim;
+        float sq = 0.0f;
+        for (size_t i = 0; i < head_dim; ++i) sq += xh[i] * xh[i];
+        const float rms_inv = 1.0f / sqrtf(sq / (float)head_dim + eps);
+        for (size_t i = 0; i < head_dim; ++i) out[h * head_dim + i] = xh[i] * rms_inv * (1.0f + gamma[i]);
+    }
+}
+
+/* rope_neox (decode_gemma3.msl:99-126): pair (i, i + head_dim/2),
+ * angle = (pos * freq_scale) / pow(theta, 2 i / head_dim), all in f32;
+ * out_i = x0 cos - x1 sin, out_{i+half} = x0 sin + x1 cos. */
+void orc_rope_neox(const float* x, size_t n_heads, size_t head_dim, float theta, float freq_scale, size_t pos,
+                   float* out) {
+    const size_t half = head_dim / 2;
+    for (size_t i = 0; i < half; ++i) {
+        const float angle = ((float)pos * freq_scale) / powf(theta, 2.0f * (float)i / (float)head_dim);
+        const float c = cosf(angle), s = sinf(angle);
+        for (size_t h = 0; h < n_heads; ++h) {
+            const size_t c0 = h * head_dim + i, c1 = c0 + half;
+            const float x0 = x[c0], x1 = x[c1];
+            out[c0] = x0 * c - x1 * s;
+            out[c1] = x0 * s + x1 * c;
+        }
+    }
+}
+
+/* gelu_tanh_kernel (decode_gemma3.msl:128-145): the tanh approximation with
+ * the argument of tanh clamped to [-10, 10]. */
+void orc_gelu_tanh(const float* x, size_t n, float* out) {
+    for (size_t i = 0; i < n; ++i) {
+        const float v = x[i];
+        const float v3 = v * v * v;
+        float inner = 0.7978845608f * (v + 0.044715f * v3);
+        inner = inner < -10.0f ? -10.0f : (inner > 10.0f ? 10.0f : inner);
+        out[i] = 0.5f * v * (1.0f + tanhf(inner));
+    }
+}
+
+/* half(x) of the Metal KV-cache append (decode_gemma3.msl:174-187): IEEE
+ * round to nearest even, overflow to infinity, subnormal halves kept.
+ * (Not the truncating f32_to_f16 of bf16.hpp, which the Q4_K quantizer uses.) */
+uint16_t orc_f32_to_f16_rne(float v) {
+    uint32_t u;
+    memcpy(&u, &v, 4);
+    const uint32_t sign = (u >> 16) & 0x8000u;
+    const uint32_t absu = u & 0x7fffffffu;
+    if (absu > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((absu >> 13) & 0x3ffu));  /* NaN */
+    if (absu >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);  /* rounds to >= 65520: inf */
+    if (absu < 0x38800000u) {  /* below the smallest normal half: subnormal (or zero) */
+        if (absu < 0x33000000u) return (uint16_t)sign;  /* below half of the smallest subnormal */
+        const uint32_t mant = (absu & 0x7fffffu) | 0x800000u;
+        const uint32_t shift = 126u - (absu >> 23);  /* so that the result is in units of 2^-24 */
+        const uint32_t q = mant >> shift, rem = mant & ((1u << shift) - 1u), halfway = 1u << (shift - 1u);
+        const uint32_t r = q + ((rem > halfway || (rem == halfway && (q & 1u))) ? 1u : 0u);
+        return (uint16_t)(sign | r);
+    }
+    const uint32_t e = (absu >> 23) - 112u;  /* rebias 127 -> 15 */
+    const uint32_t m = absu & 0x7fffffu;
+    uint32_t r = (e << 10) | (m >> 13);
+    const uint32_t rem = m & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ++r;
+    return (uint16_t)(sign | r);
+}
+
+void orc_f32_to_f16_rne_n(const float* src, uint16_t* dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = orc_f32_to_f16_rne(src[i]);
+}

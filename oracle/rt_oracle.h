@@ -155,6 +155,20 @@ void orc_initrng_uniform(uint64_t seed, size_t n, float* out);
 /* include/rt/parallel.hpp:18-21 */
 int orc_hardware_threads(void);
 
+/* ---- Gemma 3 decode operations of the Metal engine
+ * (src/shaders/decode_gemma3.msl; sequenced by src/metal_decode.mm:436-482) */
+/* decode_gemma3.msl:63-97 */
+void orc_rmsnorm_per_head(const float* x, const float* gamma, size_t n_heads, size_t head_dim, float eps,
+                          float* out);
+/* decode_gemma3.msl:99-126 (NeoX half-split pairing, pow-form angle) */
+void orc_rope_neox(const float* x, size_t n_heads, size_t head_dim, float theta, float freq_scale, size_t pos,
+                   float* out);
+/* decode_gemma3.msl:128-145 */
+void orc_gelu_tanh(const float* x, size_t n, float* out);
+/* decode_gemma3.msl:174-187: half() of the KV-cache append, IEEE RNE */
+uint16_t orc_f32_to_f16_rne(float v);
+void orc_f32_to_f16_rne_n(const float* src, uint16_t* dst, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

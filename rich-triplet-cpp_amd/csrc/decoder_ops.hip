@@ -1,0 +1,500 @@
+// decoder_ops.hip -- the operations of a decode step between the GEMVs, for the
+// decode engine (decoder.cpp): the embedding lookup, standalone RMSNorm and
+// the norm-then-residual-add of Gemma 3, the q/k preparation (per-head
+// RMSNorm, RoPE in either pairing and either angle form, and the KV-cache
+// append in f32 or f16), grouped-query attention over the cache with a
+// sliding window at head_dim 64/128/256, and the GELU-tanh gating.
+//
+// Every operation that depends on the token or its position reads them from
+// device memory (`tokens`, `pos`), so a captured graph of the step is replayed
+// for every token without being captured again.
+//
+// The references are the Metal decode engine's kernels
+// (src/shaders/decode_gemma3.msl) as src/metal_decode.mm:436-482 sequences
+// them, and the Llama layer's operations (src/transformer5.cpp:95-212).
+#include <math.h>
+
+#include "rt_common.hpp"
+#include "rt_launch.hpp"
+
+namespace rt_hip {
+namespace {
+
+constexpr float kLog2e = 1.44269504088896341f;
+
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+
+// Sum over a workgroup of T threads (result in every thread).
+template <int T>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = segment_sum<kWave>(v);
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    if (T > kWave) {
+        if (lane == 0) red[wave] = v;
+        __syncthreads();
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < T / kWave; ++w) t += red[w];
+        __syncthreads();
+        return t;
+    }
+    return v;
+}
+
+// ---- embedding (decode_gemma3.msl:202-233; the Llama lookup is scale 1) ----
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_embed(const void* __restrict__ table, const int32_t* __restrict__ tokens,
+                                               float scale, float* __restrict__ out, int H) {
+    const int m = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= H) return;
+    const int64_t row = static_cast<int64_t>(tokens[m]) * H;
+    float w;
+    if constexpr (BF16) {
+        w = bf16_lo_to_f32(static_cast<const uint16_t*>(table)[row + i]);
+    } else {
+        w = static_cast<const float*>(table)[row + i];
+    }
+    out[static_cast<int64_t>(m) * H + i] = w * scale;
+}
+
+// ---- RMSNorm rows, and the Gemma 3 post-norm residual add -----------------
+// rms_inv = 1 / sqrt(sum(x^2) * (1/D) + eps); out = (x * rms_inv) * g with
+// g = gamma or 1 + gamma (TensorNode::rms_norm / rms_norm_gemma3,
+// tensor_node.cpp:320-344, 383-387; rms_norm_gemma3, decode_gemma3.msl:7-53).
+// ADD: out = resid + that (metal_decode.mm:468-469, 479-481).  out may be resid.
+template <bool ADD>
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* __restrict__ x, const float* __restrict__ gamma,
+                                                      const float* resid, float* out, int D, float eps,
+                                                      int gemma) {
+    __shared__ float red[4];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * D;
+    float sq = 0.0f;
+    for (int i = threadIdx.x; i < D; i += 256) sq = __builtin_fmaf(x[base + i], x[base + i], sq);
+    sq = block_sum<256>(sq, red);
+    const float rms_inv = 1.0f / sqrtf(sq * (1.0f / static_cast<float>(D)) + eps);
+    for (int i = threadIdx.x; i < D; i += 256) {
+        const float g = gemma ? 1.0f + gamma[i] : gamma[i];
+        const float v = (x[base + i] * rms_inv) * g;
+        out[base + i] = ADD ? resid[base + i] + v : v;
+    }
+}
+
+// ---- q/k preparation ---------------------------------------------------------
+// Workgroup (head slot, row m): slots [0, nq) are query heads, [nq, nq+nkv)
+// key heads, [nq+nkv, nq+2nkv) value heads.  Query and key heads take the
+// optional per-head RMSNorm (x * rms_inv * (1 + gamma), rms_norm_per_head,
+// decode_gemma3.msl:63-97) and RoPE at position pos[0] + m; keys and values
+// are appended to the cache row of that position (kv_cache_append,
+// decode_gemma3.msl:174-187: half() in f16, RNE; LlamaLayerKvCache::append,
+// transformer5.cpp:59-68, f32).
+// RoPE angle: mode 0, pos * tab[i] (llama_rope with Config5::inv_freq,
+// transformer5.cpp:95-125); mode 1, (pos * freq_scale) / tab[i] with tab the
+// pow(theta, 2i/d) denominators (rope_neox, decode_gemma3.msl:99-126).
+// Pairing: half-split (i, i + d/2), or interleaved (2i, 2i + 1).
+struct PrepArgs {
+    const float* q;
+    const float* k;
+    const float* v;
+    float* q_out;
+    void* kc;
+    void* vc;
+    const int32_t* pos;
+    const float* qg;
+    const float* kg;
+    const float* tab;
+    float freq_scale, eps;
+    int nq, nkv, d, half, mode, f16;
+    int64_t q_stride, kv_stride;  // row strides of the M inputs (floats)
+    int64_t cache_row;            // floats (or halves) per cache row: nkv * d
+};
+
+__global__ __launch_bounds__(128) void k_qk_prep(const PrepArgs a) {
+    __shared__ float red[2];
+    const int slot = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
+    const int d = a.d, hd = d / 2;
+    const int p = a.pos[0] + m;
+    const bool is_q = slot < a.nq, is_k = !is_q && slot < a.nq + a.nkv;
+    const int head = is_q ? slot : (is_k ? slot - a.nq : slot - a.nq - a.nkv);
+    const float* src = is_q ? a.q + m * a.q_stride + static_cast<int64_t>(head) * d
+                            : (is_k ? a.k : a.v) + m * a.kv_stride + static_cast<int64_t>(head) * d;
+    // thread t owns the pair (i0, i1)
+    const bool active = t < hd;
+    const int i0 = a.half ? t : 2 * t, i1 = a.half ? t + hd : 2 * t + 1;
+    float x0 = active ? src[i0] : 0.0f, x1 = active ? src[i1] : 0.0f;
+    if (!(is_q || is_k)) {  // value head: append only
+        const int64_t o = static_cast<int64_t>(p) * a.cache_row + static_cast<int64_t>(head) * d;
+        if (active) {
+            if (a.f16) {
+                _Float16* vc = static_cast<_Float16*>(a.vc);
+                vc[o + i0] = static_cast<_Float16>(x0);
+                vc[o + i1] = static_cast<_Float16>(x1);
+            } else {
+                float* vc = static_cast<float*>(a.vc);
+                vc[o + i0] = x0;
+                vc[o + i1] = x1;
+            }
+        }
+        return;
+    }
+    const float* g = is_q ? a.qg : a.kg;
+    if (g) {
+        float sq = x0 * x0;
+        sq = __builtin_fmaf(x1, x1, sq);
+        sq = block_sum<128>(sq, red);
+        const float rms_inv = 1.0f / sqrtf(sq / static_cast<float>(d) + a.eps);
+        if (active) {
+            x0 = x0 * rms_inv * (1.0f + g[i0]);
+            x1 = x1 * rms_inv * (1.0f + g[i1]);
+        }
+    }
+    if (!active) return;
+    const float ang = a.mode == 0 ? static_cast<float>(p) * a.tab[t]
+                                  : (static_cast<float>(p) * a.freq_scale) / a.tab[t];
+    const float c = cosf(ang), s = sinf(ang);
+    const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
+    if (is_q) {
+        float* dst = a.q_out + m * a.q_stride + static_cast<int64_t>(head) * d;
+        dst[i0] = y0;
+        dst[i1] = y1;
+    } else {
+        const int64_t o = static_cast<int64_t>(p) * a.cache_row + static_cast<int64_t>(head) * d;
+        if (a.f16) {
+            _Float16* kc = static_cast<_Float16*>(a.kc);
+            kc[o + i0] = static_cast<_Float16>(y0);
+            kc[o + i1] = static_cast<_Float16>(y1);
+        } else {
+            float* kc = static_cast<float*>(a.kc);
+            kc[o + i0] = y0;
+            kc[o + i1] = y1;
+        }
+    }
+}
+
+// ---- attention over the cache --------------------------------------------------
+// Flash decoding as attention.hip, generalized: head_dim HD (64, 128, 256),
+// an f32 or f16 cache, up to M query rows (row m at position pos[0] + m, or
+// at k_end_host - 1 when pos is null), and a sliding window (0 = none): row
+// m attends over [k_start, k_end) with k_end = its position + 1 and
+// k_start = max(0, k_end - window) (attention_window, metal_decode.mm:
+// 404-411).  Workgroup (kv head, split, row) streams its share of the range
+// once for the G query heads of the group; lanes per position LP = HD / 8,
+// 8 values each.  States merge in a fixed order: deterministic.
+constexpr int kAT = 256;  // 4 waves
+constexpr int kAU = 4;    // positions per group loaded ahead
+
+template <int HD>
+struct AttnGeom {
+    static constexpr int LP = HD / 8;            // lanes per position
+    static constexpr int GPW = kWave / LP;       // position groups per wave
+    static constexpr int NG = (kAT / kWave) * GPW;  // groups per workgroup
+    static constexpr int BATCH = NG * kAU;       // positions per round
+    static constexpr int PART = 4 + HD;          // floats per partial state
+};
+
+struct AttnArgs {
+    const float* q;      // [M][n_q * HD]
+    const void* kc;
+    const void* vc;
+    float* part;         // [M][n_q][S][PART]
+    const int32_t* pos;  // device start position (or null)
+    int k_end_host;      // used when pos is null (row m then ends at k_end_host + m)
+    int window;
+    int n_kv;
+    float scale;
+    int64_t row;         // cache row stride (elements)
+};
+
+template <bool F16>
+__device__ __forceinline__ void load8(const void* base, int64_t off, f32x4& a, f32x4& b) {
+    if constexpr (F16) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const _Float16*>(base) + off);
+        auto h2 = [](uint32_t u) {
+            return f32x2{f16_bits_to_f32(u & 0xffffu), f16_bits_to_f32(u >> 16)};
+        };
+        const f32x2 p0 = h2(w[0]), p1 = h2(w[1]), p2 = h2(w[2]), p3 = h2(w[3]);
+        a = f32x4{p0[0], p0[1], p1[0], p1[1]};
+        b = f32x4{p2[0], p2[1], p3[0], p3[1]};
+    } else {
+        const float* p = static_cast<const float*>(base) + off;
+        a = *reinterpret_cast<const f32x4*>(p);
+        b = *reinterpret_cast<const f32x4*>(p + 4);
+    }
+}
+
+__device__ __forceinline__ void attn_range(const AttnArgs& a, int m, int& k0, int& k1) {
+    k1 = (a.pos ? a.pos[0] + 1 : a.k_end_host) + m;
+    k0 = a.window > 0 && k1 > a.window ? k1 - a.window : 0;
+}
+
+template <int HD, int G, bool F16>
+__global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
+    using Geo = AttnGeom<HD>;
+    constexpr int LP = Geo::LP, NG = Geo::NG;
+    __shared__ float sm[NG][G][2];
+    __shared__ f32x4 so[NG][G][HD / 4];
+    const int kvh = blockIdx.x, sp = blockIdx.y, S = gridDim.y, m = blockIdx.z;
+    const int n_q = a.n_kv * G;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grp = wave * Geo::GPW + lane / LP, sub = lane % LP;
+    int k0, k1;
+    attn_range(a, m, k0, k1);
+    const int len = k1 - k0;
+    int chunk = (len + S - 1) / S;
+    chunk = (chunk + Geo::BATCH - 1) / Geo::BATCH * Geo::BATCH;
+    const int p0 = k0 + sp * chunk, p1 = min(k1, p0 + chunk);
+
+    f32x4 qa[G], qb[G], oa[G], ob[G];
+    float mx[G], l[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        const float* qp = a.q + static_cast<int64_t>(m) * n_q * HD + (static_cast<int64_t>(kvh) * G + h) * HD + sub * 8;
+        qa[h] = *reinterpret_cast<const f32x4*>(qp);
+        qb[h] = *reinterpret_cast<const f32x4*>(qp + 4);
+        oa[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        ob[h] = oa[h];
+        mx[h] = -__builtin_inff();
+        l[h] = 0.0f;
+    }
+    for (int pb = p0 + grp; pb < p1; pb += NG * kAU) {
+        f32x4 ka[kAU], kb[kAU], va[kAU], vb[kAU];
+#pragma unroll
+        for (int u = 0; u < kAU; ++u) {
+            const int p = pb + u * NG;
+            if (p < p1) {
+                const int64_t off = static_cast<int64_t>(p) * a.row + static_cast<int64_t>(kvh) * HD + sub * 8;
+                load8<F16>(a.kc, off, ka[u], kb[u]);
+                load8<F16>(a.vc, off, va[u], vb[u]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kAU; ++u) {
+            if (pb + u * NG >= p1) break;  // uniform per position group
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                float dd = (qa[h][0] * ka[u][0] + qa[h][1] * ka[u][1]) + (qa[h][2] * ka[u][2] + qa[h][3] * ka[u][3]);
+                dd += (qb[h][0] * kb[u][0] + qb[h][1] * kb[u][1]) + (qb[h][2] * kb[u][2] + qb[h][3] * kb[u][3]);
+                const float sc = segment_sum<LP>(dd) * a.scale;
+                const float mn = fmaxf(mx[h], sc);
+                const float al = exp_fast(mx[h] - mn), be = exp_fast(sc - mn);
+                l[h] = l[h] * al + be;
+                oa[h] = oa[h] * al + va[u] * be;
+                ob[h] = ob[h] * al + vb[u] * be;
+                mx[h] = mn;
+            }
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        if (sub == 0) {
+            sm[grp][h][0] = mx[h];
+            sm[grp][h][1] = l[h];
+        }
+        so[grp][h][sub * 2] = oa[h];
+        so[grp][h][sub * 2 + 1] = ob[h];
+    }
+    __syncthreads();
+    for (int t = tid; t < G * (HD / 4); t += kAT) {
+        const int h = t / (HD / 4), d4 = t % (HD / 4);
+        float M = -__builtin_inff();
+        for (int g = 0; g < NG; ++g) M = fmaxf(M, sm[g][h][0]);
+        float L = 0.0f;
+        f32x4 O = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (M != -__builtin_inff()) {
+            for (int g = 0; g < NG; ++g) {
+                const float w = exp_fast(sm[g][h][0] - M);
+                L += sm[g][h][1] * w;
+                O += so[g][h][d4] * w;
+            }
+        }
+        float* dst = a.part + ((static_cast<int64_t>(m) * n_q + kvh * G + h) * S + sp) * Geo::PART;
+        if (d4 == 0) {
+            dst[0] = M;
+            dst[1] = L;
+        }
+        *reinterpret_cast<f32x4*>(dst + 4 + d4 * 4) = O;
+    }
+}
+
+// Workgroup (query head, row): fold the splits in order, out = o / l.
+template <int HD>
+__global__ __launch_bounds__(HD) void k_attn2_combine(const float* __restrict__ part, float* __restrict__ out,
+                                                      int S, int n_q) {
+    constexpr int PART = AttnGeom<HD>::PART;
+    const int h = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
+    const float* ph = part + (static_cast<int64_t>(m) * n_q + h) * S * PART;
+    float M = -__builtin_inff(), L = 0.0f, O = 0.0f;
+    for (int s = 0; s < S; ++s) M = fmaxf(M, ph[s * PART]);
+    if (M != -__builtin_inff()) {
+        for (int s = 0; s < S; ++s) {
+            const float w = exp_fast(ph[s * PART] - M);
+            L += ph[s * PART + 1] * w;
+            O += ph[s * PART + 4 + d] * w;
+        }
+    }
+    out[(static_cast<int64_t>(m) * n_q + h) * HD + d] = L > 0.0f ? O / L : 0.0f;
+}
+
+template <int HD, int G, bool F16>
+hipError_t run_attn(const AttnArgs& a, int S, int M, float* out, hipStream_t s) {
+    hipLaunchKernelGGL((k_attn2_partial<HD, G, F16>), dim3(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(S),
+                                                             static_cast<unsigned>(M)),
+                       dim3(kAT), 0, s, a);
+    hipLaunchKernelGGL(k_attn2_combine<HD>, dim3(static_cast<unsigned>(a.n_kv * G), static_cast<unsigned>(M)),
+                       dim3(HD), 0, s, a.part, out, S, a.n_kv * G);
+    return hipGetLastError();
+}
+
+template <int HD, bool F16>
+hipError_t attn_g(const AttnArgs& a, int G, int S, int M, float* out, hipStream_t s) {
+    switch (G) {
+        case 1: return run_attn<HD, 1, F16>(a, S, M, out, s);
+        case 2: return run_attn<HD, 2, F16>(a, S, M, out, s);
+        case 3: return run_attn<HD, 3, F16>(a, S, M, out, s);
+        case 4: return run_attn<HD, 4, F16>(a, S, M, out, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// ---- GELU-tanh gating (gelu_tanh_kernel + elem_mul, decode_gemma3.msl:128-158) --
+__global__ __launch_bounds__(256) void k_gelu_mul(const float* __restrict__ gate, const float* __restrict__ up,
+                                                  float* __restrict__ out, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float v = gate[i];
+    const float v3 = v * v * v;
+    float inner = 0.7978845608f * (v + 0.044715f * v3);
+    inner = fminf(fmaxf(inner, -10.0f), 10.0f);
+    out[i] = (0.5f * v * (1.0f + tanhf(inner))) * up[i];
+}
+
+}  // namespace
+
+// ---- launchers -------------------------------------------------------------------
+
+hipError_t launch_embed(const void* table, bool bf16, const int32_t* tokens, float scale, float* out, int64_t h,
+                        int m, hipStream_t s) {
+    const dim3 g(static_cast<unsigned>((h + 255) / 256), static_cast<unsigned>(m));
+    if (bf16)
+        hipLaunchKernelGGL(k_embed<true>, g, dim3(256), 0, s, table, tokens, scale, out, static_cast<int>(h));
+    else
+        hipLaunchKernelGGL(k_embed<false>, g, dim3(256), 0, s, table, tokens, scale, out, static_cast<int>(h));
+    return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_rows(const float* x, const float* gamma, const float* resid, float* out, int64_t d,
+                               int rows, float eps, bool gemma, hipStream_t s) {
+    if (resid)
+        hipLaunchKernelGGL(k_rmsnorm_rows<true>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, x, gamma,
+                           resid, out, static_cast<int>(d), eps, gemma ? 1 : 0);
+    else
+        hipLaunchKernelGGL(k_rmsnorm_rows<false>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, x, gamma,
+                           resid, out, static_cast<int>(d), eps, gemma ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_qk_prep(const QkPrep& p, hipStream_t s) {
+    if (p.head_dim < 2 || p.head_dim > 256 || p.head_dim % 2) return hipErrorInvalidValue;
+    PrepArgs a;
+    a.q = p.q;
+    a.k = p.k;
+    a.v = p.v;
+    a.q_out = p.q_out;
+    a.kc = p.k_cache;
+    a.vc = p.v_cache;
+    a.pos = p.pos;
+    a.qg = p.q_gamma;
+    a.kg = p.k_gamma;
+    a.tab = p.rope_tab;
+    a.freq_scale = p.freq_scale;
+    a.eps = p.eps;
+    a.nq = p.n_q;
+    a.nkv = p.n_kv;
+    a.d = p.head_dim;
+    a.half = p.half_split ? 1 : 0;
+    a.mode = p.pow_angle ? 1 : 0;
+    a.f16 = p.f16 ? 1 : 0;
+    a.q_stride = static_cast<int64_t>(p.n_q) * p.head_dim;
+    a.kv_stride = static_cast<int64_t>(p.n_kv) * p.head_dim;
+    a.cache_row = static_cast<int64_t>(p.n_kv) * p.head_dim;
+    hipLaunchKernelGGL(k_qk_prep, dim3(static_cast<unsigned>(p.n_q + 2 * p.n_kv), static_cast<unsigned>(p.m)),
+                       dim3(128), 0, s, a);
+    return hipGetLastError();
+}
+
+int attention2_splits(int n_kv, int m, int64_t max_len) {
+    const int64_t cus = device_info().cus;
+    int64_t want = (cus + n_kv * m - 1) / (n_kv * m);
+    const int64_t by_len = (max_len + 63) / 64;
+    want = want < by_len ? want : by_len;
+    return static_cast<int>(want < 1 ? 1 : want);
+}
+
+size_t attention2_workspace(int n_q, int head_dim, int splits, int m) {
+    return static_cast<size_t>(m) * n_q * splits * (4 + head_dim) * sizeof(float);
+}
+
+hipError_t launch_attention2(const Attn2& p, float* part, hipStream_t s) {
+    AttnArgs a;
+    a.q = p.q;
+    a.kc = p.k_cache;
+    a.vc = p.v_cache;
+    a.part = part;
+    a.pos = p.pos;
+    a.k_end_host = p.k_end;
+    a.window = p.window;
+    a.n_kv = p.n_kv;
+    a.scale = p.scale;
+    a.row = static_cast<int64_t>(p.n_kv) * p.head_dim;
+    const int G = p.n_q / p.n_kv;
+    switch (p.head_dim) {
+        case 64: return p.f16 ? attn_g<64, true>(a, G, p.splits, p.m, p.out, s)
+                              : attn_g<64, false>(a, G, p.splits, p.m, p.out, s);
+        case 128: return p.f16 ? attn_g<128, true>(a, G, p.splits, p.m, p.out, s)
+                               : attn_g<128, false>(a, G, p.splits, p.m, p.out, s);
+        case 256: return p.f16 ? attn_g<256, true>(a, G, p.splits, p.m, p.out, s)
+                               : attn_g<256, false>(a, G, p.splits, p.m, p.out, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_gelu_mul(const float* gate, const float* up, float* out, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(k_gelu_mul, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, gate, up, out, n);
+    return hipGetLastError();
+}
+
+}  // namespace rt_hip
+
+namespace rt_hip {
+namespace {
+
+// out = a + b (n elements; out may alias a).
+__global__ __launch_bounds__(256) void k_add(const float* a, const float* __restrict__ b, float* out, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n) out[i] = a[i] + b[i];
+}
+
+// out = silu(gate) * up with the sigmoid first (TensorNode::silu,
+// tensor_node.cpp:391-402; LlamaMlp::forward, transformer5.cpp:186-190).
+__global__ __launch_bounds__(256) void k_swiglu(const float* __restrict__ gate, const float* __restrict__ up,
+                                                float* __restrict__ out, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float g = gate[i];
+    const float sig = 1.0f / (1.0f + expf(-g));
+    out[i] = (g * sig) * up[i];
+}
+
+}  // namespace
+
+hipError_t launch_add(const float* a, const float* b, float* out, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(k_add, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, a, b, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const float* gate, const float* up, float* out, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(k_swiglu, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, gate, up, out, n);
+    return hipGetLastError();
+}
+
+}  // namespace rt_hip

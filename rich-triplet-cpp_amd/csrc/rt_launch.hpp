@@ -148,6 +148,54 @@ size_t q4mat_gemv_lds_bytes(int m, int64_t k);
 hipError_t launch_gemv_q4mat(const void* w, const float* x, float* y, int64_t n, int64_t k, int m, hipStream_t s);
 hipError_t launch_dequant_4bit(int fmt, const void* w, void* out, bool bf16, int64_t n, int64_t k, hipStream_t s);
 
+// ---- decode-step operations (decoder_ops.hip) ----------------------------------
+// Embedding rows: out[m][i] = table[tokens[m]][i] * scale (bf16 or f32 table).
+hipError_t launch_embed(const void* table, bool bf16, const int32_t* tokens, float scale, float* out, int64_t h,
+                        int m, hipStream_t s);
+// RMSNorm of `rows` rows of d (gamma or 1 + gamma); with resid: out = resid + norm.
+hipError_t launch_rmsnorm_rows(const float* x, const float* gamma, const float* resid, float* out, int64_t d,
+                               int rows, float eps, bool gemma, hipStream_t s);
+// q/k preparation for m rows at positions pos[0] + row: optional per-head
+// RMSNorm (1 + gamma), RoPE, and the K/V append into the cache.
+struct QkPrep {
+    const float* q = nullptr;  // [m][n_q * d] raw projections
+    const float* k = nullptr;  // [m][n_kv * d]
+    const float* v = nullptr;  // [m][n_kv * d]
+    float* q_out = nullptr;    // [m][n_q * d] rotated queries
+    void* k_cache = nullptr;   // [cap][n_kv * d] f32 or f16
+    void* v_cache = nullptr;
+    const int32_t* pos = nullptr;   // device: position of row 0
+    const float* q_gamma = nullptr; // [d] per-head norm (null: none)
+    const float* k_gamma = nullptr;
+    const float* rope_tab = nullptr;  // [d / 2]: inv_freq, or pow denominators (pow_angle)
+    float freq_scale = 1.0f, eps = 0.0f;
+    int n_q = 0, n_kv = 0, head_dim = 0, m = 1;
+    bool half_split = false, pow_angle = false, f16 = false;
+};
+hipError_t launch_qk_prep(const QkPrep& p, hipStream_t s);
+// Attention of m query rows over a KV cache (head_dim 64/128/256, f32 or
+// f16, optional sliding window); row r ends at pos[0] + r + 1 (or
+// k_end + r with pos null).  `part` holds attention2_workspace(...) bytes.
+struct Attn2 {
+    const float* q = nullptr;  // [m][n_q * d]
+    const void* k_cache = nullptr;
+    const void* v_cache = nullptr;
+    float* out = nullptr;      // [m][n_q * d]
+    const int32_t* pos = nullptr;
+    int k_end = 0, window = 0;
+    int n_q = 0, n_kv = 0, head_dim = 0, m = 1, splits = 1;
+    float scale = 1.0f;
+    bool f16 = false;
+};
+int attention2_splits(int n_kv, int m, int64_t max_len);
+size_t attention2_workspace(int n_q, int head_dim, int splits, int m);
+hipError_t launch_attention2(const Attn2& p, float* part, hipStream_t s);
+// out = gelu_tanh(gate) * up (the Gemma 3 MLP activation); silu(gate) * up
+// (the Llama one); a + b.
+hipError_t launch_gelu_mul(const float* gate, const float* up, float* out, int64_t n, hipStream_t s);
+hipError_t launch_swiglu(const float* gate, const float* up, float* out, int64_t n, hipStream_t s);
+hipError_t launch_add(const float* a, const float* b, float* out, int64_t n, hipStream_t s);
+
 hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, const float* bias,
                        float* c, int64_t m, int64_t n, int64_t k, hipStream_t s);
 // Workspace bytes one launch_gemm call needs.

@@ -595,3 +595,93 @@ def linear_forward(fmt: int, w, x, n: int, k: int, bias=None, y=None, stream=Non
     library().call("rt_hip_linear_forward", fmt, _ptr(w), _ptr(bias), _ptr(x), _ptr(y), m, n, k,
                    _stream(stream))
     return y
+
+
+# ---------------------------------------------------------------- decoder --
+
+ARCH_LLAMA, ARCH_GEMMA3 = 0, 1
+(T_EMBED, T_OUTPUT_NORM, T_LM_HEAD, T_ATTN_NORM, T_Q, T_K, T_V, T_O, T_Q_NORM, T_K_NORM, T_POST_ATTN_NORM,
+ T_FFN_NORM, T_GATE, T_UP, T_DOWN, T_POST_FFN_NORM) = range(16)
+
+
+class DecoderConfig(C.Structure):
+    """rt_hip_decoder_config (include/rt_hip.h)."""
+    _fields_ = [("arch", _i32), ("n_layers", _i32), ("hidden", _i32), ("n_heads", _i32), ("n_kv_heads", _i32),
+                ("head_dim", _i32), ("ffn", _i32), ("vocab", _i32), ("max_seq", _i32), ("norm_eps", C.c_float),
+                ("rope_theta", C.c_float), ("rope_theta_local", C.c_float), ("rope_freq_scale", C.c_float),
+                ("rope_freq_scale_local", C.c_float), ("rope_half", _i32), ("sliding_window", _i32),
+                ("global_every", _i32), ("attn_scale", C.c_float), ("embed_scale", C.c_float), ("kv_f16", _i32),
+                ("max_batch", _i32), ("llama_inv_freq", C.POINTER(C.c_float))]
+
+
+class Decoder:
+    """The decode engine (rt_hip_decoder_*): weights from host numpy arrays,
+    steps return host logits."""
+
+    def __init__(self, **cfg):
+        import numpy as np  # noqa: PLC0415
+        lib = library()
+        L = lib.lib
+        for name, res, args in [
+            ("rt_hip_decoder_create", C.c_int, [C.POINTER(DecoderConfig), C.POINTER(_vp)]),
+            ("rt_hip_decoder_set_tensor", C.c_int, [_vp, _i32, _i32, _i32, _vp, _i64]),
+            ("rt_hip_decoder_set_kv", C.c_int, [_vp, _i32, _vp, _vp, _i64]),
+            ("rt_hip_decoder_step", C.c_int, [_vp, _i32, _i32, _vp, _vp, _vp]),
+            ("rt_hip_decoder_step_batch", C.c_int, [_vp, _vp, _i32, _i32, _vp, _vp]),
+            ("rt_hip_decoder_vocab", _i64, [_vp]),
+            ("rt_hip_decoder_destroy", C.c_int, [_vp])]:
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        inv = cfg.pop("llama_inv_freq", None)
+        c = DecoderConfig(**cfg)
+        self._inv = None
+        if inv is not None:
+            self._inv = np.ascontiguousarray(inv, np.float32)
+            c.llama_inv_freq = self._inv.ctypes.data_as(C.POINTER(C.c_float))
+        self.cfg = cfg
+        h = _vp()
+        lib.call("rt_hip_decoder_create", C.byref(c), C.byref(h))
+        self.h = h
+
+    def set(self, layer: int, tensor: int, fmt: int, arr) -> None:
+        import numpy as np  # noqa: PLC0415
+        a = np.ascontiguousarray(arr)
+        library().call("rt_hip_decoder_set_tensor", self.h, layer, tensor, fmt, a.ctypes.data, a.nbytes)
+
+    def set_kv(self, layer: int, k, v, rows: int) -> None:
+        import numpy as np  # noqa: PLC0415
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        library().call("rt_hip_decoder_set_kv", self.h, layer, k.ctypes.data, v.ctypes.data, rows)
+
+    @property
+    def vocab(self) -> int:
+        return int(library().lib.rt_hip_decoder_vocab(self.h))
+
+    def step(self, token: int, pos: int, argmax: bool = False, stream=None):
+        import numpy as np  # noqa: PLC0415
+        out = np.empty(self.vocab, np.float32)
+        idx = np.zeros(1, np.int64)
+        library().call("rt_hip_decoder_step", self.h, token, pos, out.ctypes.data,
+                       idx.ctypes.data if argmax else None, None if stream is None else _stream(stream))
+        return (out, int(idx[0])) if argmax else out
+
+    def step_batch(self, tokens, start_pos: int, stream=None):
+        import numpy as np  # noqa: PLC0415
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty((t.size, self.vocab), np.float32)
+        library().call("rt_hip_decoder_step_batch", self.h, t.ctypes.data, t.size, start_pos, out.ctypes.data,
+                       None if stream is None else _stream(stream))
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            library().call("rt_hip_decoder_destroy", self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001  (interpreter shutdown)
+            pass

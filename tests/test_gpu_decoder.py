@@ -1,0 +1,225 @@
+"""The decode engine (rt_hip_decoder_*) against the oracle, token by token.
+
+Small models of the two architectures with the real layer structure:
+
+* Llama 3.2 (LlamaBlock::forward_cached, src/transformer5.cpp:198-212):
+  RMSNorm, q/k/v, RoPE (interleaved or half-split), f32 KV cache, attention,
+  o + residual, RMSNorm, gate/up, SwiGLU, down + residual; a Q4_K_M-style mix
+  (v and down BF16 in layer 0).
+* Gemma 3 (the Metal engine, src/metal_decode.mm:436-482 with
+  src/shaders/decode_gemma3.msl): bf16 embedding x sqrt(hidden), RMSNorm
+  (1 + gamma), per-head q/k RMSNorm, NeoX RoPE with per-layer theta and
+  scale, f16 KV cache, a sliding window on the local layer, head_dim 256,
+  post-attention and post-FFN norms, GELU-tanh.
+
+The expected logits are the oracle's composition of the reference's
+operations (every product in the reference's sequential f32 order, the f16
+cache rounded by the same RNE), step after step, so errors would accumulate
+in the cache exactly as they would in the engine.  Bar: 1e-5 normwise per
+step's logits; the argmax index exact.  Batch steps (up to max_batch tokens
+in one graph, each weight byte read once for all rows) must agree with the
+single-token steps to the same bar.
+"""
+import numpy as np
+import pytest
+
+from helpers import GEMV_TOL, normwise_err, say
+
+pytestmark = pytest.mark.gpu
+STEP_TOL = 1e-5
+
+
+class Model:
+    """Weights on the host and the oracle's decode step."""
+
+    def __init__(self, orc, arch, rng, **cfg):
+        self.orc, self.arch, self.cfg = orc, arch, cfg
+        self.gemma = arch == "gemma3"
+        H, F, nq, nkv, d, V = (cfg[k] for k in ("hidden", "ffn", "n_heads", "n_kv_heads", "head_dim", "vocab"))
+        self.fmt = {}
+        self.w = {}
+
+        def proj(name, n, k, bf16):
+            w32 = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+            if bf16:
+                self.w[name] = orc.f32_to_bf16_n(w32).reshape(n, k)
+                self.fmt[name] = "bf16"
+            else:
+                self.w[name] = orc.q4k_quantize(w32)
+                self.fmt[name] = "q4k"
+
+        def norm(name, n):
+            # Gemma 3 norms apply 1 + gamma, Llama's gamma itself
+            base = 0.0 if self.gemma else 1.0
+            self.w[name] = (base + 0.1 * rng.standard_normal(n)).astype(np.float32)
+
+        for li in range(cfg["n_layers"]):
+            wide = li == 0 and not self.gemma
+            proj(f"{li}.q", nq * d, H, False)
+            proj(f"{li}.k", nkv * d, H, False)
+            proj(f"{li}.v", nkv * d, H, wide)
+            proj(f"{li}.o", H, nq * d, False)
+            proj(f"{li}.gate", F, H, False)
+            proj(f"{li}.up", F, H, False)
+            proj(f"{li}.down", H, F, wide)
+            for nm in ("attn_norm", "ffn_norm") + (("post_attn_norm", "post_ffn_norm") if self.gemma else ()):
+                norm(f"{li}.{nm}", H)
+            if self.gemma:
+                norm(f"{li}.q_norm", d)
+                norm(f"{li}.k_norm", d)
+        self.w["embed"] = orc.f32_to_bf16_n((rng.standard_normal((V, H)) * 0.5).astype(np.float32)).reshape(V, H)
+        norm("out_norm", H)
+        proj("lm_head", V, H, self.gemma)
+        self.kc = [np.zeros((cfg["max_seq"], nkv * d), np.float32) for _ in range(cfg["n_layers"])]
+        self.vc = [np.zeros((cfg["max_seq"], nkv * d), np.float32) for _ in range(cfg["n_layers"])]
+        if not self.gemma:
+            self.inv = orc.llama_inv_freq(cfg["rope_theta"], d)
+
+    def load(self, rt):
+        c = dict(self.cfg)
+        c["arch"] = rt.ARCH_GEMMA3 if self.gemma else rt.ARCH_LLAMA
+        dec = rt.Decoder(**c)
+        F = {"q4k": rt.Q4K, "bf16": rt.BF16}
+        T = {"q": rt.T_Q, "k": rt.T_K, "v": rt.T_V, "o": rt.T_O, "gate": rt.T_GATE, "up": rt.T_UP,
+             "down": rt.T_DOWN, "attn_norm": rt.T_ATTN_NORM, "ffn_norm": rt.T_FFN_NORM,
+             "post_attn_norm": rt.T_POST_ATTN_NORM, "post_ffn_norm": rt.T_POST_FFN_NORM,
+             "q_norm": rt.T_Q_NORM, "k_norm": rt.T_K_NORM}
+        for name, arr in self.w.items():
+            if name == "embed":
+                dec.set(-1, rt.T_EMBED, rt.BF16, arr)
+            elif name == "out_norm":
+                dec.set(-1, rt.T_OUTPUT_NORM, rt.F32, arr)
+            elif name == "lm_head":
+                dec.set(-1, rt.T_LM_HEAD, F[self.fmt[name]], arr)
+            else:
+                li, nm = name.split(".")
+                dec.set(int(li), T[nm], F.get(self.fmt.get(name), rt.F32), arr)
+        return dec
+
+    def mm(self, name, x, n, k):
+        if self.fmt[name] == "q4k":
+            return self.orc.q4k_matmul_t(self.w[name], n, k, x.reshape(1, k)).reshape(-1)
+        return self.orc.bf16_matmul_t(self.w[name], x.reshape(1, k)).reshape(-1)
+
+    def step(self, token, pos):
+        """The oracle's decode step; updates the oracle's caches."""
+        o, c = self.orc, self.cfg
+        H, F, nq, nkv, d = (c[k] for k in ("hidden", "ffn", "n_heads", "n_kv_heads", "head_dim"))
+        eps = c["norm_eps"]
+        g = self.gemma
+        x = (self.w["embed"][token].astype(np.uint32) << 16).view(np.float32) * np.float32(c.get("embed_scale") or 1.0)
+        x = x.astype(np.float32)
+        for li in range(c["n_layers"]):
+            n1 = o.rmsnorm(x, self.w[f"{li}.attn_norm"], eps, gemma3=g)
+            q = self.mm(f"{li}.q", n1, nq * d, H)
+            k = self.mm(f"{li}.k", n1, nkv * d, H)
+            v = self.mm(f"{li}.v", n1, nkv * d, H)
+            window = 0
+            if g:
+                glob = li % c["global_every"] == c["global_every"] - 1
+                theta = c["rope_theta"] if glob else c["rope_theta_local"]
+                fs = c["rope_freq_scale"] if glob else c["rope_freq_scale_local"]
+                window = 0 if glob else c["sliding_window"]
+                q = o.rmsnorm_per_head(q, self.w[f"{li}.q_norm"], nq, d, eps)
+                k = o.rmsnorm_per_head(k, self.w[f"{li}.k_norm"], nkv, d, eps)
+                q = o.rope_neox(q, nq, d, theta, fs, pos)
+                k = o.rope_neox(k, nkv, d, theta, fs, pos)
+            else:
+                half = bool(c.get("rope_half"))
+                q = o.llama_rope(q, nq, d, pos, self.inv, half=half)
+                k = o.llama_rope(k, nkv, d, pos, self.inv, half=half)
+            if c.get("kv_f16"):  # the cache keeps half(x), RNE
+                k = o.f32_to_f16_rne_n(k).view(np.float16).astype(np.float32)
+                v = o.f32_to_f16_rne_n(v).view(np.float16).astype(np.float32)
+            self.kc[li][pos] = k
+            self.vc[li][pos] = v
+            k_end = pos + 1
+            k_start = max(0, k_end - window) if window else 0
+            scale = c.get("attn_scale") or float(1.0 / np.sqrt(np.float32(d)))
+            attn = o.gqa_attention_decode(q, self.kc[li], self.vc[li], k_end, nq, nkv, d, scale, k_start=k_start)
+            ao = self.mm(f"{li}.o", attn, H, nq * d)
+            h = (x + o.rmsnorm(ao, self.w[f"{li}.post_attn_norm"], eps, gemma3=True)) if g else x + ao
+            n2 = o.rmsnorm(h, self.w[f"{li}.ffn_norm"], eps, gemma3=g)
+            gt = self.mm(f"{li}.gate", n2, F, H)
+            up = self.mm(f"{li}.up", n2, F, H)
+            act = (o.gelu_tanh(gt) * up).astype(np.float32) if g else o.swiglu(gt, up)
+            dn = self.mm(f"{li}.down", act, H, F)
+            x = (h + o.rmsnorm(dn, self.w[f"{li}.post_ffn_norm"], eps, gemma3=True)) if g else h + dn
+            x = x.astype(np.float32)
+        xn = o.rmsnorm(x, self.w["out_norm"], eps, gemma3=g)
+        return self.mm("lm_head", xn, c["vocab"], H)
+
+
+LLAMA = dict(n_layers=2, hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=1024, vocab=1000, max_seq=64,
+             norm_eps=1e-5, rope_theta=500000.0, rope_theta_local=0.0, rope_freq_scale=1.0,
+             rope_freq_scale_local=1.0, rope_half=0, sliding_window=0, global_every=0, attn_scale=0.0,
+             embed_scale=0.0, kv_f16=0, max_batch=4)
+GEMMA = dict(n_layers=2, hidden=512, n_heads=4, n_kv_heads=2, head_dim=256, ffn=1024, vocab=1000, max_seq=32,
+             norm_eps=1e-6, rope_theta=1e6, rope_theta_local=1e4, rope_freq_scale=0.125, rope_freq_scale_local=1.0,
+             rope_half=1, sliding_window=4, global_every=2, attn_scale=1.0 / 16.0,
+             embed_scale=float(np.sqrt(np.float32(512))), kv_f16=1, max_batch=3)
+
+
+@pytest.mark.parametrize("arch,cfg", [("llama", LLAMA), ("llama_half", dict(LLAMA, rope_half=1)),
+                                      ("gemma3", GEMMA)])
+def test_decoder_steps_match_oracle(rt, orc, arch, cfg):
+    rng = np.random.default_rng(len(arch))
+    m = Model(orc, "gemma3" if arch == "gemma3" else "llama", rng, **cfg)
+    dec = m.load(rt)
+    tokens = rng.integers(0, cfg["vocab"], 10)
+    worst = 0.0
+    for pos, tok in enumerate(tokens):
+        say(f"[decoder {arch}] step pos={pos} token={tok}")
+        got, idx = dec.step(int(tok), pos, argmax=True)
+        want = m.step(int(tok), pos)
+        e = normwise_err(got, want)
+        worst = max(worst, e)
+        assert e <= STEP_TOL, (pos, e)
+        assert idx == orc.argmax_first(got) and idx == orc.argmax_first(want), pos
+    say(f"[decoder {arch}] worst step normwise error {worst:.2e}")
+    dec.close()
+
+
+@pytest.mark.parametrize("arch,cfg", [("llama", LLAMA), ("gemma3", GEMMA)])
+def test_decoder_batch_matches_single_steps(rt, orc, arch, cfg):
+    """decode_step_batch: tokens 2..(2 + max_batch) in one graph give the
+    single-token steps' logits (and the oracle's)."""
+    rng = np.random.default_rng(7 + len(arch))
+    m = Model(orc, "gemma3" if arch == "gemma3" else "llama", rng, **cfg)
+    a, b = m.load(rt), m.load(rt)
+    nb = cfg["max_batch"]
+    tokens = rng.integers(0, cfg["vocab"], 2 + nb)
+    single = []
+    for pos, tok in enumerate(tokens):
+        single.append(a.step(int(tok), pos))
+        want = m.step(int(tok), pos)
+        assert normwise_err(single[-1], want) <= STEP_TOL
+    for pos in range(2):
+        b.step(int(tokens[pos]), pos)
+    say(f"[decoder {arch}] batch of {nb} at position 2")
+    batch = b.step_batch(tokens[2:], 2)
+    for i in range(nb):
+        e = normwise_err(batch[i], single[2 + i])
+        assert e <= STEP_TOL, (i, e)
+    a.close()
+    b.close()
+
+
+def test_decoder_rejects_bad_use(rt, orc):
+    import ctypes as C
+    lib = rt.library()
+    bad = dict(LLAMA, head_dim=96)
+    with pytest.raises(rt.RtHipError):
+        rt.Decoder(arch=rt.ARCH_LLAMA, **bad)
+    dec = rt.Decoder(arch=rt.ARCH_LLAMA, **LLAMA)
+    # weights missing: the step is refused with a message
+    out = np.zeros(LLAMA["vocab"], np.float32)
+    rc = lib.lib.rt_hip_decoder_step(dec.h, 1, 0, out.ctypes.data, None, None)
+    assert rc == 1 and b"weights not set" in lib.lib.rt_hip_last_error()
+    # wrong byte count for a projection
+    with pytest.raises(rt.RtHipError, match="bytes given"):
+        dec.set(0, rt.T_Q, rt.BF16, np.zeros(10, np.uint16))
+    with pytest.raises(rt.RtHipError):
+        dec.set(0, rt.T_EMBED, rt.BF16, np.zeros(10, np.uint16))  # model tensor with a layer
+    dec.close()
+    del C
