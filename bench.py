@@ -500,6 +500,106 @@ def bench_decode_layers(args, rt, torch):
             "data": "synthetic"}
 
 
+# ------------------------------------------------------------ decode engine --
+
+ENGINE_MODELS = {
+    # Llama-3.2-3B: the headline shapes, Q4_K_M mix (v and down BF16 in the
+    # widened layers), Q4_K lm_head, f32 KV cache
+    "llama3b": dict(arch=0, n_layers=LAYERS, hidden=HIDDEN, n_heads=24, n_kv_heads=8, head_dim=128, ffn=FFN,
+                    vocab=VOCAB, norm_eps=1e-5, rope_theta=500000.0, rope_theta_local=0.0, rope_freq_scale=1.0,
+                    rope_freq_scale_local=1.0, rope_half=0, sliding_window=0, global_every=0, attn_scale=0.0,
+                    embed_scale=0.0, kv_f16=0, max_batch=0),
+    # Gemma-3-4B shapes (Config4::gemma3_4b): 34 layers, hidden 2560, 8 q / 4 kv
+    # heads of 256, ffn 10240, vocab 262144, window 1024 on 5 of every 6
+    # layers, f16 KV cache, tied bf16 lm_head; projections Q4_K
+    "gemma3_4b": dict(arch=1, n_layers=34, hidden=2560, n_heads=8, n_kv_heads=4, head_dim=256, ffn=10240,
+                      vocab=262144, norm_eps=1e-6, rope_theta=1e6, rope_theta_local=1e4, rope_freq_scale=0.125,
+                      rope_freq_scale_local=1.0, rope_half=1, sliding_window=1024, global_every=6,
+                      attn_scale=1.0 / 16.0, embed_scale=float(2560 ** 0.5), kv_f16=1, max_batch=0),
+}
+
+
+def bench_engine(args, rt, torch, model: str):
+    """A whole decode token through the decode engine (rt_hip_decoder_step):
+    embedding, every layer, final norm, lm_head and the argmax, replayed as
+    one captured graph per token; the context is filled with random keys and
+    values up to --context, and the timed steps run at positions
+    context, context + 1, ...  Synthetic weights (quantized on the GPU by the
+    library's quantizer).  Value: GEMV weight bytes per token / time."""
+    import numpy as np
+    cfg = dict(ENGINE_MODELS[model])
+    ctx = args.context
+    cfg["max_seq"] = ctx + args.warmup + args.steps + 1
+    dec = rt.Decoder(**cfg)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    H, F, nq, nkv, d, V, L = (cfg[k] for k in ("hidden", "ffn", "n_heads", "n_kv_heads", "head_dim", "vocab",
+                                             "n_layers"))
+    gemma = cfg["arch"] == 1
+    wbytes = 0
+
+    def q4(n, k):
+        w = torch.randn((n, k), generator=g, device="cuda") * 0.02
+        return rt.quantize_q4k(w).cpu().numpy()
+
+    def bf(n, k, std=0.02):
+        return (torch.randn((n, k), generator=g, device="cuda") * std).to(torch.bfloat16).view(torch.int16).cpu().numpy()
+
+    def norm(n):
+        base = 0.0 if gemma else 1.0
+        return (base + 0.1 * torch.randn((n,), generator=g, device="cuda")).cpu().numpy()
+
+    for li in range(L):
+        wide = (not gemma) and li in WIDENED_LAYERS
+        for name, t, n, k, use_bf in [("q", rt.T_Q, nq * d, H, False), ("k", rt.T_K, nkv * d, H, False),
+                                      ("v", rt.T_V, nkv * d, H, wide), ("o", rt.T_O, H, nq * d, False),
+                                      ("gate", rt.T_GATE, F, H, False), ("up", rt.T_UP, F, H, False),
+                                      ("down", rt.T_DOWN, H, F, wide)]:
+            arr = bf(n, k) if use_bf else q4(n, k)
+            dec.set(li, t, rt.BF16 if use_bf else rt.Q4K, arr)
+            wbytes += arr.nbytes
+        dec.set(li, rt.T_ATTN_NORM, rt.F32, norm(H))
+        dec.set(li, rt.T_FFN_NORM, rt.F32, norm(H))
+        if gemma:
+            for t in (rt.T_POST_ATTN_NORM, rt.T_POST_FFN_NORM):
+                dec.set(li, t, rt.F32, norm(H))
+            dec.set(li, rt.T_Q_NORM, rt.F32, norm(d))
+            dec.set(li, rt.T_K_NORM, rt.F32, norm(d))
+        if ctx:
+            kv = torch.randn((2, ctx, nkv * d), generator=g, device="cuda").cpu().numpy()
+            dec.set_kv(li, kv[0], kv[1], ctx)
+    emb = bf(V, H, 0.5)
+    dec.set(-1, rt.T_EMBED, rt.BF16, emb)
+    dec.set(-1, rt.T_OUTPUT_NORM, rt.F32, norm(H))
+    head = emb if gemma else q4(V, H)
+    dec.set(-1, rt.T_LM_HEAD, rt.BF16 if gemma else rt.Q4K, head)
+    wbytes += head.nbytes
+    del emb, head
+    log(f"[bench] engine {model}: {L} layers, {wbytes / 1e9:.3f} GB of GEMV weights per token, context {ctx}")
+    tokens = np.random.default_rng(0).integers(0, V, args.warmup + args.steps)
+    pos = ctx
+    for i in range(args.warmup):
+        dec.step(int(tokens[i]), pos, argmax=True)
+        pos += 1
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        dec.step(int(tokens[args.warmup + i]), pos, argmax=True)
+        pos += 1
+    wall = (time.perf_counter() - t0) / args.steps
+    us = wall * 1e6
+    gbs = wbytes / wall / 1e9
+    log(f"[bench] engine {model}: {us:.1f} us/token (synchronous steps, logits and argmax to the host), "
+        f"{gbs:.1f} GB/s of weights")
+    dec.close()
+    return line(args, f"decode engine whole-token latency, {model}", round(us, 2), "us/token", wall * 1e3, False,
+                "q4_k/bf16 weights, f32 activations, " + ("f16" if cfg["kv_f16"] else "f32") + " KV cache",
+                {"workload": f"decode engine (rt_hip_decoder_step), {model}, context {ctx}",
+                 "gemv_weight_bytes_per_token": wbytes, "weight_gbs": round(gbs, 1),
+                 "includes": "embedding, all layers (norms, q/k/v, RoPE, KV append, attention, o, MLP), final "
+                             "norm, lm_head, argmax, the position upload and the host synchronisation"},
+                None, None)
+
+
 # ------------------------------------------------------ other BASELINE configs --
 
 def _cpu_timed(fn, budget_s: float, min_reps: int = 3, max_reps: int = 50):
@@ -700,7 +800,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="llama_decode",
                     choices=["llama_decode", "q4k_gemv", "q4_0_gemv", "bf16_lm_head", "prefill",
-                             "flux", "layer_ops", "decode_layers"])
+                             "flux", "layer_ops", "decode_layers", "engine_llama3b", "engine_gemma3_4b"])
     ap.add_argument("--mix", default="q4km", choices=["q4km", "q4k"])
     ap.add_argument("--context", type=int, default=1024,
                     help="cached positions for --workload decode_layers")
@@ -758,6 +858,8 @@ def main() -> int:
         out = bench_layer_ops(args, rt, torch)
     elif args.workload == "decode_layers":
         out = bench_decode_layers(args, rt, torch)
+    elif args.workload.startswith("engine_"):
+        out = bench_engine(args, rt, torch, args.workload[len("engine_"):])
     elif args.workload == "flux":
         out = bench_gemm(args, rt, torch, [(4608, 9216, 3072), (4608, 12288, 3072), (4608, 3072, 12288)],
                          "config 5 FLUX linears M=4608 (QKV, MLP-in, MLP-out)", True,

@@ -34,11 +34,20 @@ __global__ __launch_bounds__(256) void k_argmax_scan(const float* __restrict__ v
     if (c1 > cols) c1 = cols;
     const float* row = v + r * cols;
     uint64_t best = 0;
-    for (int64_t c = c0 + threadIdx.x; c < c1; c += 256) {
-        const float x = row[c];
-        if (x == x) {
-            const uint64_t k = argmax_key(x, static_cast<uint32_t>(c));
-            best = k > best ? k : best;
+    // four independent loads per thread per round
+    for (int64_t cb = c0 + threadIdx.x; cb < c1; cb += 4 * 256) {
+        float x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t c = cb + u * 256;
+            x[u] = c < c1 ? row[c] : __builtin_nanf("");
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (x[u] == x[u]) {
+                const uint64_t k = argmax_key(x[u], static_cast<uint32_t>(cb + u * 256));
+                best = k > best ? k : best;
+            }
         }
     }
 #pragma unroll
@@ -110,8 +119,13 @@ hipError_t launch_argmax_init(uint64_t* keys, int64_t rows, hipStream_t s) {
 
 hipError_t launch_argmax_scan(const float* v, int64_t rows, int64_t cols, uint64_t* keys,
                               hipStream_t s) {
-    // About 16 K values per block; enough blocks to cover the chip for one row.
-    int64_t chunk = 16384;
+    // About two blocks per CU over the whole matrix, each a whole number of
+    // 1024-value rounds (at least one).
+    const int64_t cus = device_info().cus;
+    int64_t per_row = (2 * cus + rows - 1) / rows;
+    per_row = per_row < 1 ? 1 : per_row;
+    int64_t chunk = (cols + per_row - 1) / per_row;
+    chunk = (chunk + 1023) / 1024 * 1024;
     int64_t chunks = (cols + chunk - 1) / chunk;
     if (chunks < 1) chunks = 1;
     hipLaunchKernelGGL(k_argmax_scan, dim3(static_cast<unsigned>(chunks),

@@ -324,13 +324,34 @@ __global__ __launch_bounds__(HD) void k_attn2_combine(const float* __restrict__ 
     const int h = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
     const float* ph = part + (static_cast<int64_t>(m) * n_q + h) * S * PART;
     float M = -__builtin_inff(), L = 0.0f, O = 0.0f;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, ph[s * PART]);
-    if (M != -__builtin_inff()) {
-        for (int s = 0; s < S; ++s) {
-            const float w = exp_fast(ph[s * PART] - M);
-            L += ph[s * PART + 1] * w;
-            O += ph[s * PART + 4 + d] * w;
+    // Batches of up to kCB splits load before any is used (indices past S
+    // repeat split S - 1, in bounds, with weight 0): one memory latency per
+    // batch instead of one per split.  Running (M, L, O) rescales between
+    // batches, in split order.
+    constexpr int kCB = 16;
+    for (int s0 = 0; s0 < S; s0 += kCB) {
+        float ms[kCB], ls[kCB], os[kCB];
+#pragma unroll
+        for (int j = 0; j < kCB; ++j) {
+            const float* ps = ph + min(s0 + j, S - 1) * PART;
+            ms[j] = ps[0];
+            ls[j] = ps[1];
+            os[j] = ps[4 + d];
         }
+        float Mb = M;
+#pragma unroll
+        for (int j = 0; j < kCB; ++j) Mb = s0 + j < S ? fmaxf(Mb, ms[j]) : Mb;
+        if (Mb == -__builtin_inff()) continue;
+        const float r = M == -__builtin_inff() ? 0.0f : exp_fast(M - Mb);
+        L *= r;
+        O *= r;
+#pragma unroll
+        for (int j = 0; j < kCB; ++j) {
+            const float w = s0 + j < S ? exp_fast(ms[j] - Mb) : 0.0f;
+            L += ls[j] * w;
+            O += os[j] * w;
+        }
+        M = Mb;
     }
     out[(static_cast<int64_t>(m) * n_q + h) * HD + d] = L > 0.0f ? O / L : 0.0f;
 }
