@@ -28,6 +28,7 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+F32_PEAK_TFLOPS = 157.3
 WIDENED_LAYERS = {0, 1, 2, 5, 8, 11, 14, 17, 20, 23, 24, 25, 26, 27}
 HIDDEN, KV, FFN, VOCAB, LAYERS = 3072, 1024, 8192, 128256, 28
 # HBM bytes per launch of the dominant kernel (fused gate+up, tiled layout),
@@ -793,6 +794,50 @@ def bench_gemm(args, rt, torch, shapes, label, a_bf16, workload):
                  "pct_bf16_peak": round(100 * tflops / BF16_PEAK_TFLOPS, 2)}, roof, cpu)
 
 
+def bench_flux_attention(args, rt, torch):
+    """FLUX.1 attention at 1024x1024 (metal_flux.mm:254-272 over
+    flux.cpp:287-321): t = 4352 tokens (4096 image + 256 text), 24 heads of
+    128, f32 throughout.  One launch per step, captured in a graph; it is
+    the roofline kernel (f32 matrix cores).  Algorithmic flops: 2 t^2 d per
+    head for the scores and 2 t^2 d for the weighted sum of v."""
+    import numpy as np
+    t, h, d = 4352, 24, 128
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q, k, v = (torch.randn((t, h * d), generator=g, device="cuda") for _ in range(3))
+    out = torch.empty_like(q)
+
+    def run():
+        rt.flux_attention(q, k, v, h, d, out=out)
+
+    ms, _ = time_graph(torch, run, args.warmup, args.steps)
+    flops = 4 * t * t * d * h
+    tf = flops / (ms * 1e-3) / 1e12
+    log(f"[bench] flux attention {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s f32")
+    roof = {"bound": "mfma", "achieved": round(tf, 2), "peak": F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / F32_PEAK_TFLOPS, 4), "traffic": None,
+            "kernel": "k_flux_attn<128> (f32 MFMA 16x16x4, online softmax, 128 queries x 64-key tiles)",
+            "us_per_launch": round(ms * 1e3, 2), "flops_per_launch": flops}
+    cpu = None
+    if not args.no_cpu_baseline:
+        _, _, _, orc = _cpu_handles()
+        qh, kh, vh = (a.cpu().numpy() for a in (q, k, v))
+        rows = np.linspace(0, t - 1, 32).astype(np.int64)
+        med, reps = _cpu_timed(lambda: orc.flux_attention(qh, kh, vh, h, d, rows=rows), 12.0, min_reps=1,
+                               max_reps=5)
+        per_row = med / rows.size
+        cpu = {"value": round(flops / (per_row * t) / 1e9, 3), "unit": "GFLOP/s", "cores": 1, "kind": "port",
+               "sample": (f"the oracle's restatement of flux.cpp:287-321 (single-threaded, -O3 "
+                          f"-ffp-contract=off, the reference's loop order) on {rows.size} output rows of all "
+                          f"24 heads, median of {reps}, extrapolated linearly to all {t} rows: "
+                          f"{per_row * t:.1f} s per call; flux.cpp's attention is file-local to a "
+                          f"translation unit that needs the whole model, so it is not built into oracle/_ref")}
+    return line(args, "FLUX.1 attention f32 TFLOP/s (t=4352, 24 heads x 128)", round(tf, 2), "TFLOP/s", ms, True,
+                "f32", {"workload": "FLUX.1 1024x1024 attention: 4096 image + 256 text tokens, 24 heads of 128, "
+                                    "no mask", "t": t, "heads": h, "head_dim": d, "flops": flops,
+                        "pct_f32_peak": round(100 * tf / F32_PEAK_TFLOPS, 2)},
+                roof, cpu, data="synthetic: N(0,1) q, k, v")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[1])
     ap.add_argument("--gpus", type=int, default=1)
@@ -800,7 +845,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="llama_decode",
                     choices=["llama_decode", "q4k_gemv", "q4_0_gemv", "bf16_lm_head", "prefill",
-                             "flux", "layer_ops", "decode_layers", "engine_llama3b", "engine_gemma3_4b"])
+                             "flux", "flux_attention", "layer_ops", "decode_layers", "engine_llama3b", "engine_gemma3_4b"])
     ap.add_argument("--mix", default="q4km", choices=["q4km", "q4k"])
     ap.add_argument("--context", type=int, default=1024,
                     help="cached positions for --workload decode_layers")
@@ -854,6 +899,8 @@ def main() -> int:
         out = bench_gemm(args, rt, torch, [(512, FFN, HIDDEN), (512, FFN, HIDDEN), (512, HIDDEN, FFN)],
                          "config 4 prefill Q4_K GEMM M=512 (gate, up, down)", False,
                          "config 4: Llama-3.2-3B prefill gate/up/down Q4_K GEMMs, M=512, f32 activations")
+    elif args.workload == "flux_attention":
+        out = bench_flux_attention(args, rt, torch)
     elif args.workload == "layer_ops":
         out = bench_layer_ops(args, rt, torch)
     elif args.workload == "decode_layers":

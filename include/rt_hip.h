@@ -264,6 +264,23 @@ int rt_hip_attention_decode_noalloc(const float* q, const float* k_cache, const 
                                     int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int64_t seq_len,
                                     float scale, rt_hip_stream stream);
 
+/* rt_hip_flux_attention: FLUX's multi-head attention with no mask (every
+ * token attends to every token).
+ * Replace: the Metal flux_attention kernel (src/shaders/flux.msl:145-331) as
+ * MetalFluxContext::run_attention dispatches it (src/metal_flux.mm:254-272),
+ * and the CPU attention it stands in for (src/flux.cpp:282-323), called by
+ * the double and single blocks (src/flux.cpp:688, 743).
+ * q, k, v, out: [t][n_heads * head_dim] f32 rows; per head h and query i,
+ * s_j = (q_i . k_j) * scale with scale = 1 / sqrt(head_dim) in f32,
+ * out_i = sum_j softmax(s)_j v_j.  head_dim must be a multiple of 8 in
+ * [8, 128] (the Metal path's limits, metal_flux.mm:443-452; else
+ * RT_HIP_E_SHAPE); t = 0 is a no-op.  Buffers 16-byte aligned; out must not
+ * overlap q, k or v.  Products and sums in f32 (matrix cores, online softmax
+ * over tiles of 64 keys): results match the reference to f32 rounding and
+ * are deterministic.  Allocates nothing. */
+int rt_hip_flux_attention(const float* q, const float* k, const float* v, float* out, int64_t t, int32_t n_heads,
+                          int32_t head_dim, rt_hip_stream stream);
+
 /* The same two operations for the BF16-widened projections of a Q4_K_M
  * model (src/transformer4_load.cpp:141-143): q/k (tiled Q4_K) and a BF16 v
  * on RMSNorm(x) in one launch, as rt_hip_gemv_q4k_tiled_bf16; and a BF16

@@ -82,6 +82,8 @@ class Oracle:
         self._rope_neox = _bind(L, "orc_rope_neox", None, _f32p, _sz, _sz, C.c_float, C.c_float, _sz, _f32p)
         self._gelu = _bind(L, "orc_gelu_tanh", None, _f32p, _sz, _f32p)
         self._f16_rne_n = _bind(L, "orc_f32_to_f16_rne_n", None, _f32p, _u16p, _sz)
+        self._flux_attn = _bind(L, "orc_flux_attention", None, _f32p, _f32p, _f32p, _sz, _sz, _sz,
+                                C.c_void_p, _sz, _f32p)
         self._argmax = _bind(L, "orc_argmax_first", C.c_int64, _f32p, _sz)
         self._normal = _bind(L, "orc_initrng_normal", None, C.c_uint64, _sz, C.c_float, _f32p)
         self._hw = _bind(L, "orc_hardware_threads", C.c_int)
@@ -141,6 +143,18 @@ class Oracle:
         out = np.empty_like(xx)
         self._gelu(xx, xx.size, out)
         return out.reshape(np.shape(x))
+
+    def flux_attention(self, q, k, v, n_heads: int, head_dim: int, rows=None) -> np.ndarray:
+        """flux.cpp:287-321 on [t, n_heads * head_dim] f32 q, k, v; the output
+        rows `rows` (all when None), as [len(rows), n_heads * head_dim]."""
+        q, k, v = (np.ascontiguousarray(a, np.float32) for a in (q, k, v))
+        t = q.shape[0]
+        assert q.shape == k.shape == v.shape == (t, n_heads * head_dim)
+        idx = None if rows is None else np.ascontiguousarray(rows, np.int64)
+        n_rows = t if idx is None else idx.size
+        out = np.empty((n_rows, n_heads * head_dim), np.float32)
+        self._flux_attn(q, k, v, t, n_heads, head_dim, None if idx is None else idx.ctypes.data, n_rows, out)
+        return out
 
     def f32_to_f16_rne_n(self, x) -> np.ndarray:
         xx = np.ascontiguousarray(x, np.float32).reshape(-1)

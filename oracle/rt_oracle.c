@@ -837,3 +837,45 @@ uint16_t orc_f32_to_f16_rne(float v) {
 void orc_f32_to_f16_rne_n(const float* src, uint16_t* dst, size_t n) {
     for (size_t i = 0; i < n; ++i) dst[i] = orc_f32_to_f16_rne(src[i]);
 }
+
+/* FLUX attention (flux.cpp:287-321), per head h and output row i: the f32
+ * dot products accumulated in key order times scale = 1/sqrt(head_dim)
+ * (flux.cpp:290), the running maximum, exp(s - max) summed in key order,
+ * inv = 1/denom, then out += (s_j * inv) * v_j in key order (out starts at
+ * zero, flux.cpp:291). */
+void orc_flux_attention(const float* q, const float* k, const float* v, size_t t, size_t n_heads,
+                        size_t head_dim, const int64_t* rows, size_t n_rows, float* out) {
+    const size_t width = n_heads * head_dim;
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    float* scores = (float*)malloc((t ? t : 1) * sizeof(float));
+    if (!scores) return;
+    memset(out, 0, n_rows * width * sizeof(float));
+    for (size_t h = 0; h < n_heads; ++h) {
+        const size_t off = h * head_dim;
+        for (size_t r = 0; r < n_rows; ++r) {
+            const size_t i = rows ? (size_t)rows[r] : r;
+            const float* qi = q + i * width + off;
+            float max_score = -INFINITY;
+            for (size_t j = 0; j < t; ++j) {
+                const float* kj = k + j * width + off;
+                float acc = 0.0f;
+                for (size_t c = 0; c < head_dim; ++c) acc += qi[c] * kj[c];
+                scores[j] = acc * scale;
+                if (scores[j] > max_score) max_score = scores[j];
+            }
+            float denom = 0.0f;
+            for (size_t j = 0; j < t; ++j) {
+                scores[j] = expf(scores[j] - max_score);
+                denom += scores[j];
+            }
+            const float inv = 1.0f / denom;
+            float* dst = out + r * width + off;
+            for (size_t j = 0; j < t; ++j) {
+                const float weight = scores[j] * inv;
+                const float* vj = v + j * width + off;
+                for (size_t c = 0; c < head_dim; ++c) dst[c] += weight * vj[c];
+            }
+        }
+    }
+    free(scores);
+}

@@ -29,6 +29,9 @@
  *                        (tests/test_gguf.cpp:292-335)
  *   argmax ............. hand-built ties, NaN, -inf
  *   initrng ............ _ref (same libm in the same process)
+ *   flux attention ..... closed forms (one key -> v; equal scores -> the
+ *                        mean of v; a dominant key -> its v), float64
+ *                        softmax attention, key-permutation invariance
  */
 #ifndef RT_ORACLE_H
 #define RT_ORACLE_H
@@ -168,6 +171,14 @@ void orc_gelu_tanh(const float* x, size_t n, float* out);
 /* decode_gemma3.msl:174-187: half() of the KV-cache append, IEEE RNE */
 uint16_t orc_f32_to_f16_rne(float v);
 void orc_f32_to_f16_rne_n(const float* src, uint16_t* dst, size_t n);
+
+/* ---- FLUX attention: src/flux.cpp:282-323 (the CPU path the Metal
+ * flux_attention kernel, src/shaders/flux.msl:145-331, stands in for).
+ * q, k, v [t][n_heads * head_dim]; out [n_rows][n_heads * head_dim] holds
+ * the output rows rows[0..n_rows) (all of them: rows = NULL, n_rows = t),
+ * each computed exactly as the reference computes that row. */
+void orc_flux_attention(const float* q, const float* k, const float* v, size_t t, size_t n_heads,
+                        size_t head_dim, const int64_t* rows, size_t n_rows, float* out);
 
 #ifdef __cplusplus
 }

@@ -2,6 +2,7 @@
 // bookkeeping, workspaces and dispatch to the kernel launchers.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -510,6 +511,30 @@ int rt_hip_attention_decode_noalloc(const float* q, const float* k_cache, const 
                                                        n_q_heads, n_kv_heads, seq_len, scale,
                                                        static_cast<hipStream_t>(stream)),
                                fn);
+}
+
+int rt_hip_flux_attention(const float* q, const float* k, const float* v, float* out, int64_t t, int32_t n_heads,
+                          int32_t head_dim, rt_hip_stream stream) {
+    const char* fn = "rt_hip_flux_attention";
+    if (!q || !k || !v || !out) return fail(RT_HIP_E_ARG, std::string(fn) + ": null pointer");
+    if (t < 0 || n_heads < 1) return fail(RT_HIP_E_ARG, std::string(fn) + ": need t >= 0 and n_heads >= 1");
+    if (head_dim < 8 || head_dim > 128 || head_dim % 8 != 0)
+        return fail(RT_HIP_E_SHAPE, std::string(fn) + ": head_dim must be a multiple of 8 in [8, 128]");
+    const int64_t row_bytes = static_cast<int64_t>(n_heads) * head_dim * 4;
+    if (t > 0x7fffffffLL || row_bytes > (int64_t{1} << 40) / (t > 0 ? t : 1))
+        return fail(RT_HIP_E_SHAPE, std::string(fn) + ": t * n_heads * head_dim out of range");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+        return fail(RT_HIP_E_ALIGN, std::string(fn) + ": buffers must be 16-byte aligned");
+    const int64_t bytes = t * row_bytes;
+    if (overlaps(out, bytes, q, bytes) || overlaps(out, bytes, k, bytes) || overlaps(out, bytes, v, bytes))
+        return fail(RT_HIP_E_ARG, std::string(fn) + ": out overlaps q, k or v");
+    if (t == 0) return RT_HIP_OK;
+    hipError_t e;
+    if (!state_for_current(&e)) return hip_fail(e, fn);
+    // the scale of flux.cpp:290 and metal_flux.mm:264, in f32
+    const float scale = 1.0f / std::sqrt(static_cast<float>(head_dim));
+    return check_stream_launch(
+        launch_flux_attention(q, k, v, out, t, n_heads, head_dim, scale, static_cast<hipStream_t>(stream)), fn);
 }
 
 int rt_hip_gemv_q4k_tiled_swiglu(const void* tiled, const float* gate, const float* up, float* y, int64_t n,

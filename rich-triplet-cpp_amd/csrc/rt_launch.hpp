@@ -46,6 +46,11 @@ hipError_t launch_gemv_q4k_mfma(const void* w, const float* x, float* y, int64_t
                                 hipStream_t s);
 // Up to four M = 1 Q4_K GEMVs sharing x, K; `tiled`: the weights are in the
 // tiled layout (q4k_mfma.hpp) rather than reference row-major blocks.
+// FLUX attention (flux_attention.hip): q, k, v, out [t][n_heads * head_dim]
+// f32, head_dim a multiple of 8 in [8, 128], no mask, 16-byte aligned.
+hipError_t launch_flux_attention(const float* q, const float* k, const float* v, float* out, int64_t t, int n_heads,
+                                 int head_dim, float scale, hipStream_t s);
+
 // Decode attention (attention.hip): head_dim 128, n_q / n_kv in {1, 2, 3, 4};
 // `part` holds attention_decode_workspace(...) bytes.
 void attention_decode_shape(int64_t n_kv, int64_t seq_len, int* splits, int* chunk);

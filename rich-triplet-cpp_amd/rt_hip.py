@@ -49,6 +49,7 @@ _SIGNATURES = {
     "rt_hip_gemv_q4k_tiled_swiglu": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_attention_decode": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, C.c_float, _vp],
     "rt_hip_attention_decode_noalloc": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, C.c_float, _vp],
+    "rt_hip_flux_attention": [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _vp],
     "rt_hip_gemv_q4k_tiled_residual": [_vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_swiglu_residual": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_gemv_bf16_swiglu_residual": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
@@ -357,6 +358,19 @@ def attention_decode(q, k_cache, v_cache, seq_len: int, n_q: int, n_kv: int, sca
     _dev_check(q, k_cache, v_cache, out)
     library().call("rt_hip_attention_decode", _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), n_q, n_kv, head_dim,
                    seq_len, C.c_float(scale), _stream(stream))
+    return out
+
+
+def flux_attention(q, k, v, n_heads: int, head_dim: int, out=None, stream=None):
+    """FLUX's unmasked multi-head attention (flux.cpp:287-321) over
+    [t, n_heads * head_dim] f32 q, k, v."""
+    torch = _torch()
+    t = q.shape[0]
+    if out is None:
+        out = torch.empty((t, n_heads * head_dim), dtype=torch.float32, device=q.device)
+    _dev_check(q, k, v, out)
+    library().call("rt_hip_flux_attention", _ptr(q), _ptr(k), _ptr(v), _ptr(out), t, n_heads, head_dim,
+                   _stream(stream))
     return out
 
 
