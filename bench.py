@@ -815,7 +815,7 @@ def bench_flux_attention(args, rt, torch):
     log(f"[bench] flux attention {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s f32")
     roof = {"bound": "mfma", "achieved": round(tf, 2), "peak": F32_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(tf / F32_PEAK_TFLOPS, 4), "traffic": None,
-            "kernel": "k_flux_attn<128> (f32 MFMA 16x16x4, online softmax, 128 queries x 64-key tiles)",
+            "kernel": "k_flux_attn<128> (f32 MFMA 16x16x4, online softmax, 128 queries x 32-key tiles)",
             "us_per_launch": round(ms * 1e3, 2), "flops_per_launch": flops}
     cpu = None
     if not args.no_cpu_baseline:

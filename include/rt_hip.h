@@ -276,7 +276,7 @@ int rt_hip_attention_decode_noalloc(const float* q, const float* k_cache, const 
  * [8, 128] (the Metal path's limits, metal_flux.mm:443-452; else
  * RT_HIP_E_SHAPE); t = 0 is a no-op.  Buffers 16-byte aligned; out must not
  * overlap q, k or v.  Products and sums in f32 (matrix cores, online softmax
- * over tiles of 64 keys): results match the reference to f32 rounding and
+ * over tiles of 32 keys): results match the reference to f32 rounding and
  * are deterministic.  Allocates nothing. */
 int rt_hip_flux_attention(const float* q, const float* k, const float* v, float* out, int64_t t, int32_t n_heads,
                           int32_t head_dim, rt_hip_stream stream);

@@ -8,8 +8,9 @@
 // out[i][h] = sum_j softmax_j(scale * q_i . k_j) v_j for head h.
 //
 // A workgroup owns a block of 128 queries of one head (8 waves x 16) and
-// streams K and V once for all of them in tiles of 64 keys through LDS (K as
-// [key][dim], V transposed to [dim][key], 64 KB at D = 128).  The products run in f32 on the
+// streams K and V once for all of them in tiles of 32 keys through LDS (K as
+// [key][dim], V transposed to [dim][key], 32 KB at D = 128: two workgroups
+// per CU at 125 VGPRs).  The products run in f32 on the
 // matrix cores (v_mfma_f32_16x16x4_f32), so every product and partial sum
 // is an f32 operation, as in the reference:
 //  * S^T = K Q^T per 16-key x 16-query tile: lane (g = l/16, n = l%16)
@@ -17,7 +18,8 @@
 //    assignment of dims to (k-step, lane group) is a valid contraction; dims
 //    16a + 4g + b over steps 4a + b let each lane read 4 consecutive dims
 //    with one 16-byte LDS read.  The result leaves lane (g, n) holding the
-//    scores of query n against keys 16t + 4g + r.
+//    scores of query n against keys 16t + 4g + r (t over the tile's two
+//    16-key halves).
 //  * Online softmax per query: the running maximum and denominator; the
 //    accumulator rows are rescaled by exp(m_old - m_new) before the tile is
 //    folded in (flux.msl:232-271).
@@ -38,7 +40,8 @@ namespace {
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * kWave;
 constexpr int kBQ = 16 * kWaves;  // queries per workgroup
-constexpr int kBK = 64;           // keys per tile
+constexpr int kBK = 32;           // keys per tile
+constexpr int kNT = kBK / 16;     // 16-key MFMA tiles per key tile
 constexpr float kLog2e = 1.44269504088896341f;
 
 __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
@@ -55,7 +58,8 @@ __device__ __forceinline__ int k_off(int key, int gr) {
     return key * DP + ((gr ^ (key & kMask)) << 2);
 }
 __device__ __forceinline__ int vt_off(int dim, int key) {
-    return dim * kBK + ((((key >> 2) ^ (dim & 15))) << 2) + (key & 3);
+    constexpr int kMask = kBK / 4 - 1;  // granules per V^T row, minus one
+    return dim * kBK + ((((key >> 2) ^ (dim & kMask))) << 2) + (key & 3);
 }
 
 template <int DP>
@@ -110,10 +114,10 @@ __global__ __launch_bounds__(kThreads) void k_flux_attn(const float* __restrict_
         }
         __syncthreads();
 
-        // S^T: four 16-key tiles against the wave's 16 queries
-        f32x4 st[4];
+        // S^T: the tile's 16-key halves against the wave's 16 queries
+        f32x4 st[kNT];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int t = 0; t < kNT; ++t) {
             f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int a = 0; a < NA; ++a) {
@@ -123,10 +127,10 @@ __global__ __launch_bounds__(kThreads) void k_flux_attn(const float* __restrict_
             }
             st[t] = c;
         }
-        // scale, mask, the tile's maximum for query n (16 in lane, 4 lanes)
+        // scale, mask, the tile's maximum for query n (8 in lane, 4 lanes)
         float mx = -__builtin_inff();
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < kNT; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const bool valid = base + 16 * t + 4 * g + r < T;
@@ -139,7 +143,7 @@ __global__ __launch_bounds__(kThreads) void k_flux_attn(const float* __restrict_
         const float alpha = exp_fast(m_run - m_new);  // 0 on the first tile
         float sum = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < kNT; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 st[t][r] = exp_fast(st[t][r] - m_new);  // -inf -> 0
@@ -159,7 +163,7 @@ __global__ __launch_bounds__(kThreads) void k_flux_attn(const float* __restrict_
             for (int r = 0; r < 4; ++r) o[c][r] *= ar[r];
         // O += P V
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < kNT; ++t)
 #pragma unroll
             for (int c = 0; c < NA; ++c) {
                 const f32x4 v4 = *reinterpret_cast<const f32x4*>(vt + vt_off(16 * c + n, 16 * t + 4 * g));
