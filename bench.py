@@ -343,94 +343,6 @@ def bench_decode(args, rt, torch):
     }
 
 
-def build_flow(rt, torch, model, seed: int = 1):
-    """The decode step's GEMVs as one flow (rt_hip_flow_*): the model's
-    weights, chained as a Llama layer chains them -- q/k/v on RMSNorm(h); o
-    on q (the attention between them left out) plus the residual; gate/up on
-    RMSNorm(h1), which also stores silu(gate) * up; down on that plus the
-    residual; the lm_head on
-    RMSNorm of the last layer's output.  BF16-widened v runs as a stage of
-    its own on the same input."""
-    g = torch.Generator(device="cuda").manual_seed(seed)
-    by = {gv[0]: gv for gv in model.gemvs}
-    h0 = torch.randn(HIDDEN, generator=g, device="cuda")
-    vecs = [(HIDDEN, h0)]
-    keep = []
-
-    def vec(n):
-        vecs.append((n, None))
-        return len(vecs) - 1
-
-    def gamma():
-        t = 1.0 + 0.1 * torch.randn(HIDDEN, generator=g, device="cuda")
-        keep.append(t)
-        return t
-
-    def job(name, out, add=-1):
-        _, fmt, w, _, _, n, k = by[name]
-        return {"format": fmt, "w": model.tiled[name] if fmt == rt.Q4K else w, "n": n, "out": out, "add": add}
-
-    stages = []
-    h = 0
-    for layer in range(LAYERS):
-        p = f"L{layer}."
-        q, kk, v, h1, gt, up, act, h2 = (vec(HIDDEN), vec(KV), vec(KV), vec(HIDDEN), vec(FFN), vec(FFN), vec(FFN),
-                                         vec(HIDDEN))
-        g1, g2 = gamma(), gamma()
-        norm = {"k": HIDDEN, "xop": rt.XOP_RMSNORM, "in0": h, "gamma": g1, "eps": 1e-5}
-        jq = [job(p + "q", q), job(p + "k", kk)]
-        if by[p + "v"][1] == rt.Q4K:
-            stages.append(dict(norm, jobs=jq + [job(p + "v", v)]))
-        else:
-            stages.append(dict(norm, jobs=jq))
-            stages.append(dict(norm, jobs=[job(p + "v", v)]))
-        stages.append({"k": HIDDEN, "in0": q, "jobs": [job(p + "o", h1, add=h)]})
-        stages.append({"k": HIDDEN, "xop": rt.XOP_RMSNORM, "in0": h1, "gamma": g2, "eps": 1e-5, "act": act,
-                       "jobs": [job(p + "gate", gt), job(p + "up", up)]})
-        stages.append({"k": FFN, "in0": act, "jobs": [job(p + "down", h2, add=h1)]})
-        h = h2
-    logits = vec(VOCAB)
-    lm = job("lm_head", logits)
-    lm["plain"] = torch.empty(VOCAB, device="cuda")
-    stages.append({"k": HIDDEN, "xop": rt.XOP_RMSNORM, "in0": h, "gamma": gamma(), "eps": 1e-5, "jobs": [lm]})
-    flow = rt.Flow(vecs, stages)
-    flow._bench_keep = keep
-    return flow, len(stages)
-
-
-def bench_flow(args, rt, torch):
-    """BASELINE config 3 through one persistent launch per token (GEMV flow)."""
-    model = DecodeModel(rt, torch, args.mix, "tiled")
-    nbytes = model.bytes_per_token()
-    flow, nst = build_flow(rt, torch, model)
-    log(f"[bench] flow: {len(model.gemvs)} GEMVs in {nst} stages, one launch, {nbytes / 1e9:.3f} GB/token")
-    ms, _ = time_graph(torch, flow.run, args.warmup, args.steps)
-    flow.status()
-    us = ms * 1e3
-    gbs = nbytes / (us * 1e-6) / 1e9
-    log(f"[bench] flow {us:.1f} us/token, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s)")
-    roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "k_flow (the whole step's GEMVs in one persistent launch)",
-            "us_per_launch": round(us, 3), "bytes_per_launch": nbytes}
-    cpu = None if args.no_cpu_baseline else cpu_baseline(rt, torch, model)
-    return {
-        "metric": "Q4_K GEMV achieved HBM GB/s (% peak) + us/token all-layer GEMVs @ Llama-3.2-3B",
-        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "q4_k/bf16 weights, f32 activations",
-        "data": "synthetic: random N(0,0.02) weights quantized on GPU, N(0,1) hidden state",
-        "config": {"workload": "llama-3.2-3b decode step, all 28 layers' GEMVs + lm_head, batch 1",
-                   "weights": "Q4_K_M mix" if args.mix == "q4km" else "pure Q4_K",
-                   "gemvs_per_token": len(model.gemvs), "bytes_per_token": nbytes,
-                   "us_per_token": round(us, 2), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-                   "launches_per_token": 1, "stages": nst,
-                   "launch": "one persistent launch per token (rt_hip_flow_run): each stage reads the previous "
-                             "stage's output (RMSNorm, SwiGLU and residual adds fused), attention left out"},
-        "roofline": roof, "cpu_baseline": cpu,
-    }
-
-
 # ------------------------------------- layer operations fused into the GEMVs --
 
 def bench_layer_ops(args, rt, torch):
@@ -932,7 +844,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="llama_decode",
-                    choices=["llama_decode", "llama_decode_flow", "q4k_gemv", "q4_0_gemv", "bf16_lm_head", "prefill",
+                    choices=["llama_decode", "q4k_gemv", "q4_0_gemv", "bf16_lm_head", "prefill",
                              "flux", "flux_attention", "layer_ops", "decode_layers", "engine_llama3b", "engine_gemma3_4b"])
     ap.add_argument("--mix", default="q4km", choices=["q4km", "q4k"])
     ap.add_argument("--context", type=int, default=1024,
@@ -970,8 +882,6 @@ def main() -> int:
         del src, dst
     if args.workload == "llama_decode":
         out = bench_decode(args, rt, torch)
-    elif args.workload == "llama_decode_flow":
-        out = bench_flow(args, rt, torch)
     elif args.workload == "q4k_gemv":
         out = bench_single_gemv(args, rt, torch, rt.Q4K, 6912, 1024,
                                 "config 1 Q4_K GEMV 6912x1152 (Release semantics: K=1024)",

@@ -517,73 +517,6 @@ int rt_hip_graph_end(rt_hip_stream stream, rt_hip_graph** out);
 int rt_hip_graph_launch(const rt_hip_graph* graph, rt_hip_stream stream);
 int rt_hip_graph_destroy(rt_hip_graph* graph);
 
-/* ---- GEMV flows ----------------------------------------------------------------
- * A chain of dependent decode GEMV stages run as ONE persistent launch: the
- * linear work of a decode step (src/metal_decode.mm:436-482 encodes a step's
- * GEMVs -- gemv_q4k_t / gemv_bf16_t, decode_gemma3.msl:310-414 -- with the
- * norms and activations between them into one command buffer; Llama's
- * LlamaBlock::forward_cached, src/transformer5.cpp:198-212, is the same
- * chain).  No kernel boundary separates the stages: each stage's output is
- * stored with a per-run tag and its consumers poll the data itself, while the
- * next stage's weights are already streaming.
- *
- * Vectors (indices into `vectors`) carry values between stages.  An
- * external vector is a device f32 buffer, read as it is when the run starts
- * (the token's hidden state, a residual input); every other vector is
- * internal and is written by exactly one job per run.
- * A stage reads x = in0 (length k) and applies `xop` while staging it:
- *   RT_HIP_XOP_NONE      x
- *   RT_HIP_XOP_RMSNORM   RMSNorm(x) * gamma          (tensor_node.cpp:320-344)
- *   RT_HIP_XOP_RMSNORM1  RMSNorm(x) * (1 + gamma)    (Gemma 3)
- * then runs up to four jobs on it: y = W . x, plus vector `add` when add >= 0
- * (the residual adds of transformer5.cpp:205-212), into vector `out` (and
- * into `plain`, a device f32 copy, when not NULL).  A gate/up stage may set
- * `act` (else -1): its two jobs (gate, up; Q4_K, equal n, no residual) are
- * then computed side by side and vector `act` also receives
- * silu(gate) * up (transformer5.cpp:186-190), the down projection's input.
- * Jobs of one stage share a format: RT_HIP_Q4K weights in the tiled layout
- * (rt_hip_q4k_tile; up to four jobs) or RT_HIP_BF16 row-major (one job).
- * k <= 8192; Q4_K k % 256 == 0, BF16 k % 8 == 0; gamma and external inputs
- * 16-byte aligned.  A stage may only read external vectors and outputs of
- * earlier stages.  Results match the stand-alone GEMVs' numerics (normwise
- * 1e-5 of the reference's f32 loops).
- * rt_hip_flow_run launches the whole chain on `stream` (capturable: it
- * allocates nothing).  The launch keeps one workgroup on every CU until the
- * chain ends, so it needs the device to itself; every wait inside it is
- * bounded, and rt_hip_flow_status (which synchronizes the device) reports a
- * run whose wait ran out.  Runs of one flow must not overlap. */
-typedef struct rt_hip_flow rt_hip_flow;
-enum { RT_HIP_XOP_NONE = 0, RT_HIP_XOP_RMSNORM = 1, RT_HIP_XOP_RMSNORM1 = 2 };
-typedef struct rt_hip_flow_vector {
-    int64_t len;
-    const float* external;  /* device f32 [len], or NULL for an internal vector */
-} rt_hip_flow_vector;
-typedef struct rt_hip_flow_job {
-    int32_t format;         /* RT_HIP_Q4K (tiled) or RT_HIP_BF16 */
-    int32_t out;            /* output vector (internal, length n) */
-    int32_t add;            /* residual vector (length n) added to the output, or -1 */
-    int32_t reserved;
-    const void* w;
-    int64_t n;
-    float* plain;           /* device f32 [n] copy of the output, or NULL */
-} rt_hip_flow_job;
-typedef struct rt_hip_flow_stage {
-    int64_t k;
-    int32_t xop;            /* RT_HIP_XOP_NONE / RMSNORM / RMSNORM1 */
-    int32_t in0;
-    int32_t act;            /* silu(job 0) * job 1 into this vector (gate/up stages), or -1 */
-    float eps;
-    const float* gamma;     /* RMSNorm weight [k] (device) */
-    int32_t njobs;
-    int32_t reserved;
-    rt_hip_flow_job jobs[4];
-} rt_hip_flow_stage;
-int rt_hip_flow_create(const rt_hip_flow_vector* vectors, int32_t nvectors, const rt_hip_flow_stage* stages,
-                       int32_t nstages, rt_hip_flow** out);
-int rt_hip_flow_run(rt_hip_flow* flow, rt_hip_stream stream);
-int rt_hip_flow_status(rt_hip_flow* flow);
-int rt_hip_flow_destroy(rt_hip_flow* flow);
-
 /* ---- decode engine -------------------------------------------------------------
  * A model's decode step on the device: weights uploaded once, a KV cache of
  * max_seq positions, and the whole step -- embedding, every layer, the final

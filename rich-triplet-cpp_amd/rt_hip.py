@@ -700,98 +700,3 @@ class Decoder:
         except Exception:  # noqa: BLE001  (interpreter shutdown)
             pass
 
-
-# ---------------------------------------------------------------- flows --
-
-XOP_NONE, XOP_RMSNORM, XOP_RMSNORM1 = 0, 1, 2
-
-
-class FlowVector(C.Structure):
-    """rt_hip_flow_vector (include/rt_hip.h)."""
-    _fields_ = [("len", _i64), ("external", _vp)]
-
-
-class FlowJob(C.Structure):
-    """rt_hip_flow_job."""
-    _fields_ = [("format", _i32), ("out", _i32), ("add", _i32), ("reserved", _i32), ("w", _vp), ("n", _i64),
-                ("plain", _vp)]
-
-
-class FlowStage(C.Structure):
-    """rt_hip_flow_stage."""
-    _fields_ = [("k", _i64), ("xop", _i32), ("in0", _i32), ("act", _i32), ("eps", C.c_float), ("gamma", _vp),
-                ("njobs", _i32), ("reserved", _i32), ("jobs", FlowJob * 4)]
-
-
-class Flow:
-    """A GEMV flow (rt_hip_flow_*): `vectors` is a list of (length, external
-    device tensor or None); `stages` a list of dicts with keys k, xop, in0,
-    act (gate/up stages: silu(gate) * up), gamma (device tensor), eps and
-    jobs, each job a dict with
-    format (Q4K: tiled weight, or BF16), w, n, out, add (-1: none) and plain
-    (device tensor or None).  The tensors are kept alive with the flow."""
-
-    def __init__(self, vectors, stages):
-        lib = library()
-        L = lib.lib
-        for name, args in [("rt_hip_flow_create", [C.POINTER(FlowVector), _i32, C.POINTER(FlowStage), _i32,
-                                                    C.POINTER(_vp)]),
-                           ("rt_hip_flow_run", [_vp, _vp]), ("rt_hip_flow_status", [_vp]),
-                           ("rt_hip_flow_destroy", [_vp])]:
-            fn = getattr(L, name)
-            fn.restype = C.c_int
-            fn.argtypes = args
-        self._keep = []
-        vs = (FlowVector * len(vectors))()
-        for i, (n, ext) in enumerate(vectors):
-            vs[i].len = int(n)
-            if ext is not None:
-                _dev_check(ext)
-                self._keep.append(ext)
-            vs[i].external = _ptr(ext)
-        ss = (FlowStage * len(stages))()
-        for i, st in enumerate(stages):
-            s = ss[i]
-            s.k = int(st["k"])
-            s.xop = int(st.get("xop", XOP_NONE))
-            s.in0 = int(st["in0"])
-            s.act = int(st.get("act", -1))
-            s.eps = float(st.get("eps", 0.0))
-            g = st.get("gamma")
-            if g is not None:
-                _dev_check(g)
-                self._keep.append(g)
-            s.gamma = _ptr(g)
-            jobs = st["jobs"]
-            s.njobs = len(jobs)
-            for j, jb in enumerate(jobs):
-                J = s.jobs[j]
-                J.format = int(jb["format"])
-                J.out = int(jb["out"])
-                J.add = int(jb.get("add", -1))
-                J.w = _ptr(jb["w"])
-                J.n = int(jb["n"])
-                pl = jb.get("plain")
-                J.plain = _ptr(pl)
-                self._keep += [jb["w"]] + ([pl] if pl is not None else [])
-        h = _vp()
-        lib.call("rt_hip_flow_create", vs, len(vectors), ss, len(stages), C.byref(h))
-        self.h = h
-
-    def run(self, stream=None) -> None:
-        library().call("rt_hip_flow_run", self.h, _stream(stream))
-
-    def status(self) -> None:
-        """Raises RtHipError when a run's wait ran out (synchronizes the device)."""
-        library().call("rt_hip_flow_status", self.h)
-
-    def close(self) -> None:
-        if getattr(self, "h", None):
-            library().call("rt_hip_flow_destroy", self.h)
-            self.h = None
-
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:  # noqa: BLE001  (interpreter shutdown)
-            pass
