@@ -150,14 +150,21 @@ def test_bf16_swiglu(rt, orc, n, k):
     assert normwise_err(got, orc.bf16_matmul_t(w, act)) <= GEMV_TOL
 
 
+# (n_q, n_kv, head_dim): Llama-3.2-3B; 640 tiles, which the launch runs at
+# one wave per tile (KS = 1: the partner row comes from the lane swap of the
+# same wave, no K-split reduction); head_dim 64.
+ROPE_SHAPES = [(24, 8, 128), (48, 16, 128), (48, 16, 64)]
+
+
 @pytest.mark.parametrize("pos", [0, 5, 1000, 70000])
-def test_rmsnorm_rope_qkv_into_kv_cache(rt, orc, pos):
+@pytest.mark.parametrize("nq,nkv,hd", ROPE_SHAPES)
+def test_rmsnorm_rope_qkv_into_kv_cache(rt, orc, pos, nq, nkv, hd):
     """q/k/v of a Llama layer on RMSNorm(x), q and k rotated at `pos`
     (interleaved pairing), k and v written straight into their KV-cache rows."""
     import torch
-    k, hd, nq, nkv = 3072, 128, 24, 8
+    k = 3072
     ns = [nq * hd, nkv * hd, nkv * hd]
-    say(f"[rmsnorm+rope qkv] pos={pos}")
+    say(f"[rmsnorm+rope qkv] pos={pos} n_q={nq} n_kv={nkv} head_dim={hd}")
     rng = np.random.default_rng(pos + 1)
     blocks = _weights(orc, rng, ns, k)
     x = (rng.standard_normal(k) * 2).astype(np.float32)
@@ -183,14 +190,15 @@ def test_rmsnorm_rope_qkv_into_kv_cache(rt, orc, pos):
 
 
 @pytest.mark.parametrize("pos", [0, 3, 1000, 70000])
-def test_rmsnorm_rope_half_split_qkv(rt, orc, pos):
+@pytest.mark.parametrize("nq,nkv,hd", ROPE_SHAPES)
+def test_rmsnorm_rope_half_split_qkv(rt, orc, pos, nq, nkv, hd):
     """The half-split pairing (HuggingFace weights): q and k tiled with their
     head rows interleaved (rt_hip_q4k_tile_rope_half), v tiled plainly, one
     launch with rope_jobs 0x3 | ROPE_HALF; outputs back in their places."""
     import torch
-    k, hd, nq, nkv = 3072, 128, 24, 8
+    k = 3072
     ns = [nq * hd, nkv * hd, nkv * hd]
-    say(f"[rmsnorm+rope half qkv] pos={pos}")
+    say(f"[rmsnorm+rope half qkv] pos={pos} n_q={nq} n_kv={nkv} head_dim={hd}")
     rng = np.random.default_rng(pos + 11)
     blocks = _weights(orc, rng, ns, k)
     x = (rng.standard_normal(k) * 2).astype(np.float32)
