@@ -229,6 +229,63 @@ __device__ __forceinline__ void lds_sync() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Epilogue through LDS.  A wave's accumulators hold C in the MFMA layout
+// (lane l: rows 4 (l / 16) + r of each 16-row fragment, column l % 16), so
+// storing them directly writes 64-byte pieces of four rows per instruction.
+// Instead each wave writes 64 rows of its tile at a time, row-major, into its
+// own LDS region of 64 x kEpiStride floats, and stores them back as whole
+// 256-byte row segments (16 lanes x 16 bytes per row, 4 rows per
+// instruction) plus the bias.  Measured on the FLUX shapes: 11-25% faster
+// than the direct stores, identical results.  The caller has waited for its
+// copies and passed a barrier, so no wave still writes or reads the ring.
+constexpr int kEpiStride = 68;  // floats per LDS row: 64 + 4 (the 4 row groups of a write hit distinct banks)
+constexpr int kEpiWaveBytes = 64 * kEpiStride * 4;
+
+template <int NI>
+__device__ __forceinline__ void store_tile_staged(const f32x4 (&acc)[NI][4], float* reg, float* __restrict__ C,
+                                                  int M, int N, int row0, int col0, const float* __restrict__ bias,
+                                                  int lane) {
+    static_assert(NI % 4 == 0, "64-row halves");
+    const int q = lane >> 4, c16 = lane & 15;
+    const int col = col0 + 4 * c16;
+    const bool full = (N & 3) == 0 && col + 3 < N;  // whole, 16-byte aligned groups of 4
+    f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+    if (bias) {
+        if (full) {
+            bv = f32x4{bias[col], bias[col + 1], bias[col + 2], bias[col + 3]};
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bv[e] = col + e < N ? bias[col + e] : 0.f;
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < NI / 4; ++h) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) reg[(16 * i + 4 * q + r) * kEpiStride + 16 * j + c16] = acc[4 * h + i][j][r];
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's writes are in
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int lr = 4 * k + q;
+            const int row = row0 + 64 * h + lr;
+            const f32x4 v = *reinterpret_cast<const f32x4*>(reg + lr * kEpiStride + 4 * c16) + bv;
+            if (row >= M) continue;
+            float* dst = C + static_cast<size_t>(row) * N + col;
+            if (full) {
+                *reinterpret_cast<f32x4*>(dst) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (col + e < N) dst[e] = v[e];
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // reads done before the region is rewritten
+    }
+}
+
 template <bool W_Q4K>
 __global__ __launch_bounds__(kPThreads) void k_gemm_pipe(const uint16_t* __restrict__ A,
                                                          const void* __restrict__ Wp,
@@ -410,22 +467,13 @@ __global__ __launch_bounds__(kPThreads) void k_gemm_pipe(const uint16_t* __restr
         }
     }
 
-    // Epilogue (+ bias).
-    const int cr = 4 * (lane >> 4), cc = lane & 15;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int col = n0 + wn + 16 * j + cc;
-        if (col >= N) continue;
-        const float bv = bias ? bias[col] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = m0 + wm + 16 * i + cr + r;
-                if (row < M) C[static_cast<size_t>(row) * N + col] = acc[i][j][r] + bv;
-            }
-        }
-    }
+    // Epilogue (+ bias) through LDS, once the copies issued for steps past
+    // the end (zero fill) have landed in every wave.
+    static_assert(4 * kEpiWaveBytes <= 2 * kStages * kTile, "the epilogue's LDS regions fit");
+    wait_vm<0>();
+    __syncthreads();
+    store_tile_staged<4>(acc, reinterpret_cast<float*>(lds + wave * kEpiWaveBytes), C, M, N, m0 + wm, n0 + wn, bias,
+                         lane);
 }
 
 // Large-tile bf16 GEMM (both operands bf16 in HBM): C = A * W^T (+ bias).
@@ -450,11 +498,11 @@ __device__ __forceinline__ uint32_t swz64(int r, int c) {
     return static_cast<uint32_t>(r * 64 + ((c ^ ((r >> 1) & 3)) << 4));
 }
 
-// NS: ring stages (A and W tile pairs, 32 KB each).  WAVES: 8 (tiles of
-// 128 x 64 per wave, 2 waves per SIMD) or 4 (128 x 128 per wave, one per
-// SIMD, accumulators in AGPRs: a third fewer fragment reads per MFMA).
-template <int NS, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) void k_gemm_256(const uint16_t* __restrict__ A,
+// NS: ring stages (A and W tile pairs, 32 KB each); 8 waves of 128 x 64.
+// (4 waves of 128 x 128, one per SIMD with the accumulators in AGPRs, have a
+// third fewer fragment reads per MFMA but measured slower.)
+template <int NS>
+__global__ __launch_bounds__(kBThreads) void k_gemm_256(const uint16_t* __restrict__ A,
                                                         const uint16_t* __restrict__ W,
                                                         const float* __restrict__ bias,
                                                         float* __restrict__ C, int M, int N, int K, int mt) {
@@ -473,9 +521,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_256(const uint16_t* __restr
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    constexpr int NJ = WAVES == 8 ? 4 : 8;  // 16-column fragments per wave
-    constexpr int CP = 16 / WAVES;          // copy instructions per wave and operand
-    const int wm = (wave / (256 / (16 * NJ))) * 128, wn = (wave % (256 / (16 * NJ))) * 16 * NJ;
+    constexpr int NJ = 4;  // 16-column fragments per wave
+    constexpr int CP = 2;  // copy instructions per wave and operand
+    static_assert(NS * 2 * kBTile >= 8 * kEpiWaveBytes, "the epilogue's LDS regions fit in the ring");
+    const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
     const int S = K >> 5;
     const int64_t rowb = static_cast<int64_t>(K) * 2;
 
@@ -573,21 +622,12 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_256(const uint16_t* __restr
         }
     }
 
-    const int cr = 4 * (lane >> 4), cc = lane & 15;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const int col = n0 + wn + 16 * j + cc;
-        if (col >= N) continue;
-        const float bv = bias ? bias[col] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = m0 + wm + 16 * i + cr + r;
-                if (row < M) C[static_cast<size_t>(row) * N + col] = acc[i][j][r] + bv;
-            }
-        }
-    }
+    // Epilogue through LDS: the copies issued for steps past the end (zero
+    // fill) land first, then every wave is past its last fragment read.
+    wait_vm<0>();
+    __syncthreads();
+    store_tile_staged<8>(acc, reinterpret_cast<float*>(lds + wave * kEpiWaveBytes), C, M, N, m0 + wm, n0 + wn, bias,
+                         lane);
 }
 
 // f32 -> bf16 round-to-nearest-even, 8 values per thread.
@@ -645,7 +685,7 @@ GemmPlan plan_gemm(int w_fmt, bool a_bf16, int64_t m, int64_t n, int64_t k) {
     // tile inside the GEMM.
     p.mt = (m + 127) / 128;
     p.nt = (n + 127) / 128;
-    p.fused_q4k = w_fmt == RT_HIP_Q4K && p.mt == 1;
+    p.fused_q4k = w_fmt == RT_HIP_Q4K && p.mt <= tune_param("GEMM_FUSED_MT", 1);
     const int64_t cus = device_info().cus;
     p.mt2 = (m + 255) / 256;
     p.nt2 = (n + 255) / 256;
@@ -717,12 +757,8 @@ hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, con
             const uint16_t* w16 = static_cast<const uint16_t*>(w);
             const int im = static_cast<int>(m), in = static_cast<int>(n), ik = static_cast<int>(k);
             const int imt = static_cast<int>(mt2);
-            if (tune_param("GEMM_BIG_WAVES", 8) == 4)
-                hipLaunchKernelGGL((k_gemm_256<5, 4>), g, dim3(256), static_cast<size_t>(10) * kBTile, s, a16, w16,
-                                   bias, c, im, in, ik, imt);
-            else
-                hipLaunchKernelGGL((k_gemm_256<5, 8>), g, b, static_cast<size_t>(10) * kBTile, s, a16, w16, bias,
-                                   c, im, in, ik, imt);
+            hipLaunchKernelGGL((k_gemm_256<5>), g, b, static_cast<size_t>(10) * kBTile, s, a16, w16, bias, c, im,
+                               in, ik, imt);
             return hipGetLastError();
         }
         const size_t lds = q4k ? static_cast<size_t>(kStages + 2) * kTile + kStages * kRawStage
