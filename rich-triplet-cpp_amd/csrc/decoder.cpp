@@ -85,6 +85,7 @@ struct rt_hip_decoder {
           *q_rot = nullptr, *attn = nullptr, *o = nullptr, *gate = nullptr, *up = nullptr, *act = nullptr,
           *down = nullptr, *logits = nullptr, *part = nullptr;
     size_t part_bytes = 0;
+    uint32_t* attn_cnt = nullptr;  // attention arrival counters, [max rows][n_kv], zero between launches
     int32_t* dstate = nullptr;  // [0] position of row 0, [1..8] tokens
     int32_t* hstate = nullptr;  // pinned host mirror
     uint64_t* argmax_keys = nullptr;
@@ -145,8 +146,32 @@ int layer_step1(rt_hip_decoder* d, int li, hipStream_t s) {
     const int H = c.hidden, nq = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim, F = c.ffn;
     const int xop_gemma = d->gemma ? 1 : 0;
     int rc;
-    // q/k/v on RMSNorm(hidden), the norm inside the GEMVs' staging where possible
-    if (L.q.q4k() && L.k.q4k() && L.v.q4k()) {
+    // Llama with an f32 cache and the interleaved pairing: q/k/v, RoPE and
+    // the KV append in one launch -- the epilogue rotates q and k at the
+    // position it reads from device memory and stores k and v straight into
+    // the cache row of that position (LlamaAttention::forward_cached,
+    // transformer5.cpp:152-172), so no separate q/k pass runs.
+    const bool fused_kv = !d->gemma && !c.kv_f16 && !c.rope_half && L.q.q4k() && L.k.q4k();
+    constexpr int kXopRmsNorm = 1;  // launch_gemv_q4k_xop's xop 1: RMSNorm(x) * gamma
+    if (fused_kv) {
+        const int64_t kvd = static_cast<int64_t>(nkv) * hd;
+        const int64_t n[3] = {L.q.n, L.k.n, L.v.n};
+        if (L.v.q4k()) {
+            const void* w[3] = {L.q.tiled, L.k.tiled, L.v.tiled};
+            float* y[3] = {d->q_rot, static_cast<float*>(L.kc), static_cast<float*>(L.vc)};
+            rc = chk(launch_gemv_q4k_xop(kXopRmsNorm, 3, w, y, n, d->hidden, L.attn_norm, c.norm_eps, H, s, L.rope_tab,
+                                         0, hd, 0x3, false, RopeCache{d->dstate, kvd, 0x6}),
+                     "decoder: q/k/v + RoPE + KV append");
+        } else {
+            const void* w[2] = {L.q.tiled, L.k.tiled};
+            float* y[2] = {d->q_rot, static_cast<float*>(L.kc)};
+            rc = chk(launch_gemv_q4k_bf16_fused(2, w, y, n, static_cast<const uint16_t*>(L.v.data),
+                                                static_cast<float*>(L.vc), L.v.n, d->hidden, H, s, kXopRmsNorm,
+                                                L.attn_norm, c.norm_eps, L.rope_tab, 0, hd, 0x3,
+                                                RopeCache{d->dstate, kvd, 0x2 | kRopeCacheBf16}),
+                     "decoder: q/k/v + RoPE + KV append");
+        }
+    } else if (L.q.q4k() && L.k.q4k() && L.v.q4k()) {
         const void* w[3] = {L.q.tiled, L.k.tiled, L.v.tiled};
         float* y[3] = {d->q, d->k, d->v};
         const int64_t n[3] = {L.q.n, L.k.n, L.v.n};
@@ -166,28 +191,30 @@ int layer_step1(rt_hip_decoder* d, int li, hipStream_t s) {
     }
     if (rc) return rc;
     // per-head norms, RoPE, KV append
-    QkPrep p;
-    p.q = d->q;
-    p.k = d->k;
-    p.v = d->v;
-    p.q_out = d->q_rot;
-    p.k_cache = L.kc;
-    p.v_cache = L.vc;
-    p.pos = d->dstate;
-    p.q_gamma = L.q_norm;
-    p.k_gamma = L.k_norm;
-    p.rope_tab = L.rope_tab;
-    p.freq_scale = L.freq_scale;
-    p.eps = c.norm_eps;
-    p.n_q = nq;
-    p.n_kv = nkv;
-    p.head_dim = hd;
-    p.m = 1;
-    p.half_split = d->gemma || c.rope_half;
-    p.pow_angle = d->gemma;
-    p.f16 = c.kv_f16 != 0;
-    rc = chk(launch_qk_prep(p, s), "decoder: q/k prep");
-    if (rc) return rc;
+    if (!fused_kv) {
+        QkPrep p;
+        p.q = d->q;
+        p.k = d->k;
+        p.v = d->v;
+        p.q_out = d->q_rot;
+        p.k_cache = L.kc;
+        p.v_cache = L.vc;
+        p.pos = d->dstate;
+        p.q_gamma = L.q_norm;
+        p.k_gamma = L.k_norm;
+        p.rope_tab = L.rope_tab;
+        p.freq_scale = L.freq_scale;
+        p.eps = c.norm_eps;
+        p.n_q = nq;
+        p.n_kv = nkv;
+        p.head_dim = hd;
+        p.m = 1;
+        p.half_split = d->gemma || c.rope_half;
+        p.pow_angle = d->gemma;
+        p.f16 = c.kv_f16 != 0;
+        rc = chk(launch_qk_prep(p, s), "decoder: q/k prep");
+        if (rc) return rc;
+    }
     Attn2 a;
     a.q = d->q_rot;
     a.k_cache = L.kc;
@@ -202,7 +229,7 @@ int layer_step1(rt_hip_decoder* d, int li, hipStream_t s) {
     a.splits = attention2_splits(nkv, 1, L.window > 0 ? L.window : c.max_seq);
     a.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt(static_cast<float>(hd));
     a.f16 = c.kv_f16 != 0;
-    rc = chk(launch_attention2(a, d->part, s), "decoder: attention");
+    rc = chk(launch_attention2(a, d->part, d->attn_cnt, s), "decoder: attention");
     if (rc) return rc;
     // o
     if (!d->gemma) {
@@ -295,7 +322,7 @@ int layer_stepm(rt_hip_decoder* d, int li, int m, hipStream_t s) {
     a.splits = attention2_splits(nkv, m, L.window > 0 ? L.window : c.max_seq);
     a.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt(static_cast<float>(hd));
     a.f16 = c.kv_f16 != 0;
-    rc = chk(launch_attention2(a, d->part, s), "decoder: attention");
+    rc = chk(launch_attention2(a, d->part, d->attn_cnt, s), "decoder: attention");
     if (!rc) rc = gemvm(L.o, d->attn, d->o, m, s);
     if (rc) return rc;
     if (!d->gemma)
@@ -480,6 +507,10 @@ int rt_hip_decoder_create(const rt_hip_decoder_config* cfg, rt_hip_decoder** out
     }
     d->part_bytes = pb;
     if ((e = dev_alloc(d, reinterpret_cast<void**>(&d->part), pb)) != hipSuccess) return cleanup(e);
+    const size_t cb = static_cast<size_t>(R) * c.n_kv_heads * sizeof(uint32_t);
+    if ((e = dev_alloc(d, reinterpret_cast<void**>(&d->attn_cnt), cb)) != hipSuccess ||
+        (e = hipMemset(d->attn_cnt, 0, cb)) != hipSuccess)
+        return cleanup(e);
     // KV caches (zeroed) and RoPE tables, per layer
     std::vector<float> tab(hd / 2);
     for (int i = 0; i < c.n_layers; ++i) {

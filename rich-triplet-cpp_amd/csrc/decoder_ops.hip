@@ -179,7 +179,10 @@ __global__ __launch_bounds__(128) void k_qk_prep(const PrepArgs a) {
 // k_start = max(0, k_end - window) (attention_window, metal_decode.mm:
 // 404-411).  Workgroup (kv head, split, row) streams its share of the range
 // once for the G query heads of the group; lanes per position LP = HD / 8,
-// 8 values each.  States merge in a fixed order: deterministic.
+// 8 values each.  Each workgroup stores its (max, denominator, weighted sum)
+// state per query head; the last of the S workgroups of a (row, kv head) to
+// arrive merges the S states in split order into out, so one launch does
+// the whole attention and the result does not depend on arrival order.
 constexpr int kAT = 256;  // 4 waves
 constexpr int kAU = 4;    // positions per group loaded ahead
 
@@ -203,7 +206,56 @@ struct AttnArgs {
     int n_kv;
     float scale;
     int64_t row;         // cache row stride (elements)
+    float* out;          // [M][n_q * HD]
+    uint32_t* cnt;       // [M][n_kv] arrival counters, zero between launches
 };
+
+// Partials are stored and reloaded with agent-scope (device-coherent)
+// accesses: they bypass the per-XCD L2, so the workgroup that merges them
+// sees every other XCD's stores once those have completed.
+__device__ __forceinline__ void st_dev(float* p, float v) {
+    __hip_atomic_store((__attribute__((address_space(1))) float*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+    return __hip_atomic_load((const __attribute__((address_space(1))) float*)p, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Fold the S split states of one (row, query head) for dimension d in split
+// order (so the result does not depend on which workgroup merges): running
+// (M, L, O), rescaled between batches of up to kCB splits that are loaded
+// before any is used (indices past S repeat split S - 1, in bounds, with
+// weight 0), one memory latency per batch instead of one per split.
+template <int PART>
+__device__ __forceinline__ float fold_splits(const float* ph, int S, int d) {
+    float M = -__builtin_inff(), L = 0.0f, O = 0.0f;
+    constexpr int kCB = 16;
+    for (int s0 = 0; s0 < S; s0 += kCB) {
+        float ms[kCB], ls[kCB], os[kCB];
+#pragma unroll
+        for (int j = 0; j < kCB; ++j) {
+            const float* ps = ph + min(s0 + j, S - 1) * PART;
+            ms[j] = ld_dev(ps);
+            ls[j] = ld_dev(ps + 1);
+            os[j] = ld_dev(ps + 4 + d);
+        }
+        float Mb = M;
+#pragma unroll
+        for (int j = 0; j < kCB; ++j) Mb = s0 + j < S ? fmaxf(Mb, ms[j]) : Mb;
+        if (Mb == -__builtin_inff()) continue;
+        const float r = M == -__builtin_inff() ? 0.0f : exp_fast(M - Mb);
+        L *= r;
+        O *= r;
+#pragma unroll
+        for (int j = 0; j < kCB; ++j) {
+            const float w = s0 + j < S ? exp_fast(ms[j] - Mb) : 0.0f;
+            L += ls[j] * w;
+            O += os[j] * w;
+        }
+        M = Mb;
+    }
+    return L > 0.0f ? O / L : 0.0f;
+}
 
 template <bool F16>
 __device__ __forceinline__ void load8(const void* base, int64_t off, f32x4& a, f32x4& b) {
@@ -309,70 +361,45 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
         }
         float* dst = a.part + ((static_cast<int64_t>(m) * n_q + kvh * G + h) * S + sp) * Geo::PART;
         if (d4 == 0) {
-            dst[0] = M;
-            dst[1] = L;
+            st_dev(dst, M);
+            st_dev(dst + 1, L);
         }
-        *reinterpret_cast<f32x4*>(dst + 4 + d4 * 4) = O;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) st_dev(dst + 4 + d4 * 4 + e, O[e]);
     }
-}
-
-// Workgroup (query head, row): fold the splits in order, out = o / l.
-template <int HD>
-__global__ __launch_bounds__(HD) void k_attn2_combine(const float* __restrict__ part, float* __restrict__ out,
-                                                      int S, int n_q) {
-    constexpr int PART = AttnGeom<HD>::PART;
-    const int h = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
-    const float* ph = part + (static_cast<int64_t>(m) * n_q + h) * S * PART;
-    float M = -__builtin_inff(), L = 0.0f, O = 0.0f;
-    // Batches of up to kCB splits load before any is used (indices past S
-    // repeat split S - 1, in bounds, with weight 0): one memory latency per
-    // batch instead of one per split.  Running (M, L, O) rescales between
-    // batches, in split order.
-    constexpr int kCB = 16;
-    for (int s0 = 0; s0 < S; s0 += kCB) {
-        float ms[kCB], ls[kCB], os[kCB];
-#pragma unroll
-        for (int j = 0; j < kCB; ++j) {
-            const float* ps = ph + min(s0 + j, S - 1) * PART;
-            ms[j] = ps[0];
-            ls[j] = ps[1];
-            os[j] = ps[4 + d];
-        }
-        float Mb = M;
-#pragma unroll
-        for (int j = 0; j < kCB; ++j) Mb = s0 + j < S ? fmaxf(Mb, ms[j]) : Mb;
-        if (Mb == -__builtin_inff()) continue;
-        const float r = M == -__builtin_inff() ? 0.0f : exp_fast(M - Mb);
-        L *= r;
-        O *= r;
-#pragma unroll
-        for (int j = 0; j < kCB; ++j) {
-            const float w = s0 + j < S ? exp_fast(ms[j] - Mb) : 0.0f;
-            L += ls[j] * w;
-            O += os[j] * w;
-        }
-        M = Mb;
+    // Every thread's partial stores have completed, then one arrival per
+    // workgroup; the last of the S splits of (row, kv head) merges them and
+    // resets the counter for the next launch.
+    wait_vmcnt<0>();
+    __syncthreads();
+    __shared__ uint32_t arrival;
+    uint32_t* const cnt = a.cnt + static_cast<int64_t>(m) * a.n_kv + kvh;
+    if (tid == 0) arrival = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrival != static_cast<uint32_t>(S - 1)) return;
+    for (int t = tid; t < G * HD; t += kAT) {
+        const int h = t / HD, d = t % HD;
+        const float* ph = a.part + (static_cast<int64_t>(m) * n_q + kvh * G + h) * S * Geo::PART;
+        a.out[(static_cast<int64_t>(m) * n_q + kvh * G + h) * HD + d] = fold_splits<Geo::PART>(ph, S, d);
     }
-    out[(static_cast<int64_t>(m) * n_q + h) * HD + d] = L > 0.0f ? O / L : 0.0f;
+    if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int HD, int G, bool F16>
-hipError_t run_attn(const AttnArgs& a, int S, int M, float* out, hipStream_t s) {
+hipError_t run_attn(const AttnArgs& a, int S, int M, hipStream_t s) {
     hipLaunchKernelGGL((k_attn2_partial<HD, G, F16>), dim3(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(S),
                                                              static_cast<unsigned>(M)),
                        dim3(kAT), 0, s, a);
-    hipLaunchKernelGGL(k_attn2_combine<HD>, dim3(static_cast<unsigned>(a.n_kv * G), static_cast<unsigned>(M)),
-                       dim3(HD), 0, s, a.part, out, S, a.n_kv * G);
     return hipGetLastError();
 }
 
 template <int HD, bool F16>
-hipError_t attn_g(const AttnArgs& a, int G, int S, int M, float* out, hipStream_t s) {
+hipError_t attn_g(const AttnArgs& a, int G, int S, int M, hipStream_t s) {
     switch (G) {
-        case 1: return run_attn<HD, 1, F16>(a, S, M, out, s);
-        case 2: return run_attn<HD, 2, F16>(a, S, M, out, s);
-        case 3: return run_attn<HD, 3, F16>(a, S, M, out, s);
-        case 4: return run_attn<HD, 4, F16>(a, S, M, out, s);
+        case 1: return run_attn<HD, 1, F16>(a, S, M, s);
+        case 2: return run_attn<HD, 2, F16>(a, S, M, s);
+        case 3: return run_attn<HD, 3, F16>(a, S, M, s);
+        case 4: return run_attn<HD, 4, F16>(a, S, M, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -455,7 +482,8 @@ size_t attention2_workspace(int n_q, int head_dim, int splits, int m) {
     return static_cast<size_t>(m) * n_q * splits * (4 + head_dim) * sizeof(float);
 }
 
-hipError_t launch_attention2(const Attn2& p, float* part, hipStream_t s) {
+hipError_t launch_attention2(const Attn2& p, float* part, uint32_t* counters, hipStream_t s) {
+    if (!counters) return hipErrorInvalidValue;
     AttnArgs a;
     a.q = p.q;
     a.kc = p.k_cache;
@@ -467,14 +495,16 @@ hipError_t launch_attention2(const Attn2& p, float* part, hipStream_t s) {
     a.n_kv = p.n_kv;
     a.scale = p.scale;
     a.row = static_cast<int64_t>(p.n_kv) * p.head_dim;
+    a.out = p.out;
+    a.cnt = counters;
     const int G = p.n_q / p.n_kv;
     switch (p.head_dim) {
-        case 64: return p.f16 ? attn_g<64, true>(a, G, p.splits, p.m, p.out, s)
-                              : attn_g<64, false>(a, G, p.splits, p.m, p.out, s);
-        case 128: return p.f16 ? attn_g<128, true>(a, G, p.splits, p.m, p.out, s)
-                               : attn_g<128, false>(a, G, p.splits, p.m, p.out, s);
-        case 256: return p.f16 ? attn_g<256, true>(a, G, p.splits, p.m, p.out, s)
-                               : attn_g<256, false>(a, G, p.splits, p.m, p.out, s);
+        case 64: return p.f16 ? attn_g<64, true>(a, G, p.splits, p.m, s)
+                              : attn_g<64, false>(a, G, p.splits, p.m, s);
+        case 128: return p.f16 ? attn_g<128, true>(a, G, p.splits, p.m, s)
+                               : attn_g<128, false>(a, G, p.splits, p.m, s);
+        case 256: return p.f16 ? attn_g<256, true>(a, G, p.splits, p.m, s)
+                               : attn_g<256, false>(a, G, p.splits, p.m, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -56,10 +56,19 @@ enum Epi { kEpiNone = 0, kEpiRope = 1, kEpiAdd = 2 };
 
 struct Rope {
     const float* inv_freq = nullptr;  // [head_dim / 2], device
+    const int32_t* pos_dev = nullptr;  // position in device memory (else pos)
+    int64_t cache_row = 0;             // with pos_dev: jobs in cache_jobs store at y + position * cache_row
     int pos = 0;
     int head_dim = 0;
     int jobs = 0;
     int half = 0;  // half-split pairing: rows of rotated jobs tiled interleaved
+    int cache_jobs = 0;
+
+    __device__ __forceinline__ int position() const { return pos_dev ? pos_dev[0] : pos; }
+    // Where output set j (a job, or kRopeCacheBf16Bit for the BF16 rows) starts.
+    __device__ __forceinline__ float* dest(float* y, int j) const {
+        return pos_dev && ((cache_jobs >> j) & 1) ? y + static_cast<int64_t>(pos_dev[0]) * cache_row : y;
+    }
 };
 
 // Job-table fields read into scalar registers through readfirstlane, and
@@ -305,7 +314,8 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     const int row = row0 + ln.n;
     const bool keep = row < n_job;  // false for tile slots past the last tile
     const Four<uint64_t> ys = {sreg(jobs.y[0]), sreg(jobs.y[1]), sreg(jobs.y[2]), sreg(jobs.y[3])};
-    float* const yj = reinterpret_cast<float*>(ys[job]);
+    float* yj = reinterpret_cast<float*>(ys[job]);
+    if constexpr (EPI == kEpiRope) yj = rope.dest(yj, job);
     // Where the row is stored: with the half-split pairing the rows of a
     // rotated job were tiled interleaved (row 2j of a head holds element j,
     // row 2j + 1 element j + head_dim / 2), and go back to their places here.
@@ -324,7 +334,7 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
             const float other = __shfl_xor(val, 1, kWave);
             if ((rope.jobs >> job) & 1) {  // wave-uniform
                 const int j = row % rope.head_dim;
-                const float ang = static_cast<float>(rope.pos) * rope.inv_freq[j >> 1];
+                const float ang = static_cast<float>(rope.position()) * rope.inv_freq[j >> 1];
                 const float c = cosf(ang), sn = sinf(ang);
                 val = (j & 1) ? other * sn + val * c : val * c - other * sn;
             }
@@ -388,8 +398,9 @@ __global__ __launch_bounds__(bf16_gemv::kThreads) void k_gemv_q4k_bf16(
         q4k_tiles<4, XPQ, true, J34, XOP, EPI>(blk, X, K, split, bf16_gemv::kThreads, w0, w1, n0, n1, tile1, jobs,
                                                lds, aux, eps, rope);
     else
-        bf16_gemv::rows<8, XPB, false, bf16_gemv::kThreads, XOP>(blk - q4k_wgs, (nb_rows + 3) / 4, wb, X, yb,
-                                                                 nb_rows, K, nullptr, lds, aux, eps);
+        bf16_gemv::rows<8, XPB, false, bf16_gemv::kThreads, XOP>(
+            blk - q4k_wgs, (nb_rows + 3) / 4, wb, X, EPI == kEpiRope ? rope.dest(yb, kRopeCacheBf16Bit) : yb, nb_rows, K, nullptr,
+            lds, aux, eps);
 }
 
 // The x operation, its second vector and eps (XOp).
@@ -500,7 +511,8 @@ size_t q4k_m1_lds_bytes(int64_t k) { return mfma_gemv_lds_bytes(k, kMaxThreads /
 
 hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* const* y, const int64_t* n,
                               const float* x, const float* aux, float eps, int64_t k, hipStream_t s,
-                              const float* inv_freq, int pos, int head_dim, int rope_jobs, bool add) {
+                              const float* inv_freq, int pos, int head_dim, int rope_jobs, bool add,
+                              const RopeCache& cache) {
     if (count < 1 || count > kMaxJobs || (aux == nullptr && xop != kXNone)) return hipErrorInvalidValue;
     Jobs jobs{};
     jobs.count = count;
@@ -528,6 +540,9 @@ hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* 
         xa.rope.head_dim = head_dim;
         xa.rope.jobs = rope_jobs & 0xff;
         xa.rope.half = (rope_jobs >> 8) & 1;
+        xa.rope.pos_dev = cache.pos;
+        xa.rope.cache_row = cache.row;
+        xa.rope.cache_jobs = cache.jobs;
         switch (xop) {
             case kXRmsNorm: return dispatch<true, kXRmsNorm, kEpiRope>(jobs, x, k, s, xa);
             case kXRmsNorm1: return dispatch<true, kXRmsNorm1, kEpiRope>(jobs, x, k, s, xa);
@@ -618,7 +633,8 @@ size_t q4k_bf16_fused_lds_bytes(int64_t k) {
 hipError_t launch_gemv_q4k_bf16_fused(int count, const void* const* w, float* const* y, const int64_t* n,
                                       const uint16_t* wb, float* yb, int64_t nb_rows, const float* x,
                                       int64_t k, hipStream_t s, int xop, const float* aux, float eps,
-                                      const float* inv_freq, int pos, int head_dim, int rope_jobs) {
+                                      const float* inv_freq, int pos, int head_dim, int rope_jobs,
+                                      const RopeCache& cache) {
     if (count < 1 || count > kMaxJobs || k > 8192) return hipErrorInvalidValue;
     Jobs jobs{};
     jobs.count = count;
@@ -659,6 +675,9 @@ hipError_t launch_gemv_q4k_bf16_fused(int count, const void* const* w, float* co
         xa.rope.head_dim = head_dim;
         xa.rope.jobs = rope_jobs & 0xff;
         xa.rope.half = (rope_jobs >> 8) & 1;
+        xa.rope.pos_dev = cache.pos;
+        xa.rope.cache_row = cache.row;
+        xa.rope.cache_jobs = cache.jobs;
         switch (xop) {
             case kXRmsNorm: return fused_xp<kXRmsNorm, kEpiRope>(jobs, ks, q4k_wgs, wb, yb, nb_rows, x, xa, k, lds, s);
             case kXRmsNorm1:

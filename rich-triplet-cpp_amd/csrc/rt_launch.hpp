@@ -72,10 +72,22 @@ hipError_t launch_gemv_bf16_xop(int xop, const uint16_t* w, const float* x, cons
 // rope_jobs != 0: interleaved RoPE (position pos, inv_freq [head_dim / 2])
 // on the outputs of the jobs in that bit mask; only with an RMSNorm xop.
 // add: y += the product (the residual add); with xop 0 (none) or 3 (SwiGLU).
+// cache.pos != null (RoPE launches only): the position is read from device
+// memory at run time instead of pos, and the outputs of the jobs in
+// cache.jobs (bit kRopeCacheBf16: the BF16 rows of the fused launch below)
+// are stored at y + position * cache.row -- the KV-cache row of the token,
+// so a captured graph serves every position.
+struct RopeCache {
+    const int32_t* pos = nullptr;
+    int64_t row = 0;
+    int jobs = 0;
+};
+constexpr int kRopeCacheBf16Bit = 4;
+constexpr int kRopeCacheBf16 = 1 << kRopeCacheBf16Bit;
 hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* const* y, const int64_t* n,
                               const float* x, const float* aux, float eps, int64_t k, hipStream_t s,
                               const float* inv_freq = nullptr, int pos = 0, int head_dim = 0, int rope_jobs = 0,
-                              bool add = false);
+                              bool add = false, const RopeCache& cache = {});
 hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* const* y,
                                       const int64_t* n, const float* x, int64_t k, hipStream_t s,
                                       bool tiled);
@@ -94,7 +106,7 @@ hipError_t launch_gemv_q4k_bf16_fused(int count, const void* const* w, float* co
                                       const uint16_t* wb, float* yb, int64_t nb_rows, const float* x,
                                       int64_t k, hipStream_t s, int xop = 0, const float* aux = nullptr,
                                       float eps = 0.0f, const float* inv_freq = nullptr, int pos = 0,
-                                      int head_dim = 0, int rope_jobs = 0);
+                                      int head_dim = 0, int rope_jobs = 0, const RopeCache& cache = {});
 
 hipError_t launch_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
                             int m, uint64_t* argmax_key, hipStream_t s);
@@ -194,7 +206,9 @@ struct Attn2 {
 };
 int attention2_splits(int n_kv, int m, int64_t max_len);
 size_t attention2_workspace(int n_q, int head_dim, int splits, int m);
-hipError_t launch_attention2(const Attn2& p, float* part, hipStream_t s);
+// part: attention2_workspace bytes; counters: m * n_kv zeroed words (each
+// launch leaves them zero).
+hipError_t launch_attention2(const Attn2& p, float* part, uint32_t* counters, hipStream_t s);
 // out = gelu_tanh(gate) * up (the Gemma 3 MLP activation); silu(gate) * up
 // (the Llama one); a + b.
 hipError_t launch_gelu_mul(const float* gate, const float* up, float* out, int64_t n, hipStream_t s);
