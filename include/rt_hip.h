@@ -277,9 +277,15 @@ int rt_hip_attention_decode_noalloc(const float* q, const float* k_cache, const 
  * RT_HIP_E_SHAPE); t = 0 is a no-op.  Buffers 16-byte aligned; out must not
  * overlap q, k or v.  Products and sums in f32 (matrix cores, online softmax
  * over tiles of 32 keys): results match the reference to f32 rounding and
- * are deterministic.  Allocates nothing. */
+ * are deterministic.  With more 128-query blocks (n_heads * ceil(t / 128))
+ * than two per CU, the work is divided evenly over two workgroups per CU and
+ * the blocks cut between two of them keep their partial states in the
+ * library workspace (see above): rt_hip_flux_attention_workspace_bytes gives
+ * the need for a shape (0 when none, -1 for invalid sizes), to reserve before
+ * a graph capture. */
 int rt_hip_flux_attention(const float* q, const float* k, const float* v, float* out, int64_t t, int32_t n_heads,
                           int32_t head_dim, rt_hip_stream stream);
+int64_t rt_hip_flux_attention_workspace_bytes(int64_t t, int32_t n_heads, int32_t head_dim);
 
 /* The same two operations for the BF16-widened projections of a Q4_K_M
  * model (src/transformer4_load.cpp:141-143): q/k (tiled Q4_K) and a BF16 v

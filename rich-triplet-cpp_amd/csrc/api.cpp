@@ -521,7 +521,8 @@ int rt_hip_flux_attention(const float* q, const float* k, const float* v, float*
     if (head_dim < 8 || head_dim > 128 || head_dim % 8 != 0)
         return fail(RT_HIP_E_SHAPE, std::string(fn) + ": head_dim must be a multiple of 8 in [8, 128]");
     const int64_t row_bytes = static_cast<int64_t>(n_heads) * head_dim * 4;
-    if (t > 0x7fffffffLL || row_bytes > (int64_t{1} << 40) / (t > 0 ? t : 1))
+    // a 32-key tile of a head is addressed with 32-bit offsets below 2^31
+    if (t > 0x7fffffffLL || row_bytes > (int64_t{1} << 26) || row_bytes > (int64_t{1} << 40) / (t > 0 ? t : 1))
         return fail(RT_HIP_E_SHAPE, std::string(fn) + ": t * n_heads * head_dim out of range");
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
         return fail(RT_HIP_E_ALIGN, std::string(fn) + ": buffers must be 16-byte aligned");
@@ -533,8 +534,24 @@ int rt_hip_flux_attention(const float* q, const float* k, const float* v, float*
     if (!state_for_current(&e)) return hip_fail(e, fn);
     // the scale of flux.cpp:290 and metal_flux.mm:264, in f32
     const float scale = 1.0f / std::sqrt(static_cast<float>(head_dim));
-    return check_stream_launch(
-        launch_flux_attention(q, k, v, out, t, n_heads, head_dim, scale, static_cast<hipStream_t>(stream)), fn);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    float* part = nullptr;
+    uint32_t* counters = nullptr;
+    if (const size_t need = flux_attention_workspace(t, n_heads, head_dim)) {
+        part = static_cast<float*>(workspace(need, s, &e));
+        if (!part) return hip_fail(e, fn);
+        counters = arrival_counters(s, &e);
+        if (!counters) return hip_fail(e, fn);
+    }
+    return check_stream_launch(launch_flux_attention(q, k, v, out, t, n_heads, head_dim, scale, part, counters, s),
+                               fn);
+}
+
+int64_t rt_hip_flux_attention_workspace_bytes(int64_t t, int32_t n_heads, int32_t head_dim) {
+    if (t < 0 || n_heads < 1 || head_dim < 8 || head_dim > 128 || head_dim % 8 != 0) return -1;
+    hipError_t e;
+    if (!state_for_current(&e)) return -1;
+    return static_cast<int64_t>(flux_attention_workspace(t, n_heads, head_dim));
 }
 
 int rt_hip_gemv_q4k_tiled_swiglu(const void* tiled, const float* gate, const float* up, float* y, int64_t n,

@@ -48,8 +48,13 @@ hipError_t launch_gemv_q4k_mfma(const void* w, const float* x, float* y, int64_t
 // tiled layout (q4k_mfma.hpp) rather than reference row-major blocks.
 // FLUX attention (flux_attention.hip): q, k, v, out [t][n_heads * head_dim]
 // f32, head_dim a multiple of 8 in [8, 128], no mask, 16-byte aligned.
+// With more query blocks than workgroup slots the work is split evenly over
+// the slots: part (flux_attention_workspace bytes) holds the states of the
+// blocks cut in two, and counters (kArrivalCounters) their arrivals; both
+// null otherwise.
+size_t flux_attention_workspace(int64_t t, int n_heads, int head_dim);
 hipError_t launch_flux_attention(const float* q, const float* k, const float* v, float* out, int64_t t, int n_heads,
-                                 int head_dim, float scale, hipStream_t s);
+                                 int head_dim, float scale, float* part, uint32_t* counters, hipStream_t s);
 
 // Decode attention (attention.hip): head_dim 128, n_q / n_kv in {1, 2, 3, 4};
 // `part` holds attention_decode_workspace(...) bytes.

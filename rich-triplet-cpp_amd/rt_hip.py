@@ -77,6 +77,7 @@ _SIZE_SIGNATURES = {
     "rt_hip_gemm_workspace_bytes": [_i32, _i32, _i64, _i64, _i64],
     "rt_hip_gemv_workspace_bytes": [_i32, _i64, _i64, _i32],
     "rt_hip_attention_workspace_bytes": [_i32, _i32, _i64],
+    "rt_hip_flux_attention_workspace_bytes": [_i64, _i32, _i32],
     "rt_hip_q4mat_bytes": [_i64, _i64],
     "rt_hip_q4mat_scales_offset": [_i64, _i64],
 }

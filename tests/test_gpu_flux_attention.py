@@ -10,7 +10,12 @@ oracle's restatement of flux.cpp:287-321.
 * Closed forms bit for bit: one key gives v; a key that dominates every
   other by more than 104 in score gives its v; and q = 0 gives the mean of v
   (to f32 rounding).
-* Deterministic (two runs agree bit for bit); argument errors.
+* Shapes with more 128-query blocks than workgroup slots (two per CU),
+  where the blocks cut between two workgroups merge two partial states:
+  every row against the oracle, a dominant key still gives exactly its v,
+  and two runs agree bit for bit.
+* Deterministic (two runs agree bit for bit); argument errors; the
+  workspace query.
 """
 import numpy as np
 import pytest
@@ -108,3 +113,49 @@ def test_flux_attention_errors(rt):
     assert lib.status(name, None, p(x), p(x), p(o), 64, 2, 128, None) == 1   # null
     assert lib.status(name, p(x), p(x), p(x), p(o), 0, 2, 128, None) == 0    # t = 0: nothing
     torch.cuda.synchronize()
+
+
+def slots():
+    import torch
+    return 2 * torch.cuda.get_device_properties(0).multi_processor_count
+
+
+@pytest.mark.parametrize("t,h,d", [(512, 130, 8), (300, 260, 16)])
+def test_flux_attention_split_blocks_every_row(rt, orc, t, h, d):
+    assert h * ((t + 127) // 128) > slots()  # the split path
+    say(f"[flux attention split] t={t} heads={h} head_dim={d}")
+    rng = np.random.default_rng(t + h + d)
+    q, k, v = rand(rng, t, h, d)
+    got = run(rt, q, k, v, h, d)
+    want = orc.flux_attention(q, k, v, h, d)
+    err = normwise_err(got, want)
+    say(f"[flux attention split] normwise {err:.2e}")
+    assert err <= FLUX_ATTN_TOL
+    # per head as well: a wrong merge of one block would hide in the whole
+    for hh in range(0, h, 7):
+        sl = slice(hh * d, (hh + 1) * d)
+        assert normwise_err(got[:, sl], want[:, sl]) <= FLUX_ATTN_TOL, hh
+
+
+def test_flux_attention_split_blocks_closed_form_and_determinism(rt, orc):
+    t, h, d = 600, 120, 8
+    assert h * ((t + 127) // 128) > slots()
+    rng = np.random.default_rng(5)
+    q, k, v = rand(rng, t, h, d, 0.05)
+    # key 333 dominates query row 100 in every head by more than 104 in score
+    for hh in range(h):
+        sl = slice(hh * d, (hh + 1) * d)
+        k[333, sl] = q[100, sl] * np.float32(200.0 * np.sqrt(d) / np.sum(np.square(q[100, sl])))
+    a = run(rt, q, k, v, h, d)
+    b = run(rt, q, k, v, h, d)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(a[100].view(np.uint32), v[333].view(np.uint32))
+
+
+def test_flux_attention_workspace_bytes(rt):
+    lib = rt.library().lib
+    f = lib.rt_hip_flux_attention_workspace_bytes
+    assert f(4352, 24, 128) == slots() * 2 * (128 * 128 + 256) * 4
+    assert f(1000, 2, 128) == 0
+    assert f(512, 130, 8) == slots() * 2 * (128 * 32 + 256) * 4
+    assert f(10, 1, 12) == -1
