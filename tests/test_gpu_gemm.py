@@ -98,3 +98,21 @@ def test_gemm_flux_shape_properties(rt):
     c = rt.gemm(rt.Q4K, a, blocks, n, k)
     err = ((c - ref).abs().max() / ref.abs().max()).item()
     assert err <= 1e-5 * 4  # f32 torch reference itself rounds differently
+
+
+@pytest.mark.parametrize("m,n,k", [(2304, 6400, 1024), (2304, 6400, 12288)])
+def test_gemm_large_tile_partial_round(rt, m, n, k):
+    """225 tiles of 256 x 256 (fewer than the CUs), short and long K, N not a
+    multiple of the tile: equals the f32 product of the same bf16 operands
+    (tolerance (i)), and two runs agree bit for bit."""
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(m + k)
+    a = torch.randn((m, k), generator=g, device="cuda").bfloat16()
+    wb = (torch.randn((n, k), generator=g, device="cuda") * 0.02).bfloat16()
+    c1 = rt.gemm(rt.BF16, a, wb.view(torch.int16), n, k)
+    c2 = rt.gemm(rt.BF16, a, wb.view(torch.int16), n, k)
+    ref = a.float() @ wb.float().t().contiguous()
+    err = ((c1 - ref).abs().max() / ref.abs().max()).item()
+    say(f"[gemm large tile] {m}x{n}x{k} normwise {err:.2e}")
+    assert err <= 4e-5
+    assert torch.equal(c1.view(torch.int32), c2.view(torch.int32))
