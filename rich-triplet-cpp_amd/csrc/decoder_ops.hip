@@ -63,20 +63,48 @@ __global__ __launch_bounds__(256) void k_embed(const void* __restrict__ table, c
 // g = gamma or 1 + gamma (TensorNode::rms_norm / rms_norm_gemma3,
 // tensor_node.cpp:320-344, 383-387; rms_norm_gemma3, decode_gemma3.msl:7-53).
 // ADD: out = resid + that (metal_decode.mm:468-469, 479-481).  out may be resid.
-template <bool ADD>
+// D % 4 == 0 and D <= 1024 V: each thread loads its V groups of 4 (x, gamma,
+// resid) at once, before the reduction, so the row costs one memory latency
+// instead of one per group.
+template <bool ADD, int V>
 __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* __restrict__ x, const float* __restrict__ gamma,
                                                       const float* resid, float* out, int D, float eps,
                                                       int gemma) {
     __shared__ float red[4];
     const int64_t base = static_cast<int64_t>(blockIdx.x) * D;
+    const int n4 = D >> 2, tid = threadIdx.x;
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(x + base);
+    const f32x4* g4 = reinterpret_cast<const f32x4*>(gamma);
+    const f32x4* r4 = reinterpret_cast<const f32x4*>(resid + (ADD ? base : 0));
+    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 xv[V], gv[V], rv[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        const int i = tid + 256 * v;
+        xv[v] = i < n4 ? x4[i] : z;
+        gv[v] = i < n4 ? g4[i] : z;
+        if constexpr (ADD) rv[v] = i < n4 ? r4[i] : z;
+    }
     float sq = 0.0f;
-    for (int i = threadIdx.x; i < D; i += 256) sq = __builtin_fmaf(x[base + i], x[base + i], sq);
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sq = __builtin_fmaf(xv[v][e], xv[v][e], sq);
     sq = block_sum<256>(sq, red);
     const float rms_inv = 1.0f / sqrtf(sq * (1.0f / static_cast<float>(D)) + eps);
-    for (int i = threadIdx.x; i < D; i += 256) {
-        const float g = gemma ? 1.0f + gamma[i] : gamma[i];
-        const float v = (x[base + i] * rms_inv) * g;
-        out[base + i] = ADD ? resid[base + i] + v : v;
+    f32x4* o4 = reinterpret_cast<f32x4*>(out + base);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        const int i = tid + 256 * v;
+        if (i >= n4) break;
+        f32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float g = gemma ? 1.0f + gv[v][e] : gv[v][e];
+            const float t = (xv[v][e] * rms_inv) * g;
+            o[e] = ADD ? rv[v][e] + t : t;
+        }
+        o4[i] = o;
     }
 }
 
@@ -221,40 +249,54 @@ __device__ __forceinline__ float ld_dev(const float* p) {
                              __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Fold the S split states of one (row, query head) for dimension d in split
+// Fold the S split states of P (row, query head, dimension d) pairs in split
 // order (so the result does not depend on which workgroup merges): running
-// (M, L, O), rescaled between batches of up to kCB splits that are loaded
-// before any is used (indices past S repeat split S - 1, in bounds, with
-// weight 0), one memory latency per batch instead of one per split.
-template <int PART>
-__device__ __forceinline__ float fold_splits(const float* ph, int S, int d) {
-    float M = -__builtin_inff(), L = 0.0f, O = 0.0f;
+// (M, L, O), rescaled between batches of up to kCB splits whose loads, for
+// all P pairs, are issued before any is used (indices past S repeat split
+// S - 1, in bounds, with weight 0): one memory latency per batch instead of
+// one per split and pair.
+template <int PART, int P>
+__device__ __forceinline__ void fold_splits(const float* const (&ph)[P], const int (&d)[P], int S, float (&res)[P]) {
+    float M[P], L[P], O[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        M[p] = -__builtin_inff();
+        L[p] = 0.0f;
+        O[p] = 0.0f;
+    }
     constexpr int kCB = 16;
     for (int s0 = 0; s0 < S; s0 += kCB) {
-        float ms[kCB], ls[kCB], os[kCB];
+        // every load of the batch, for all of this thread's P pairs, first
+        float ms[P][kCB], ls[P][kCB], os[P][kCB];
 #pragma unroll
-        for (int j = 0; j < kCB; ++j) {
-            const float* ps = ph + min(s0 + j, S - 1) * PART;
-            ms[j] = ld_dev(ps);
-            ls[j] = ld_dev(ps + 1);
-            os[j] = ld_dev(ps + 4 + d);
+        for (int p = 0; p < P; ++p)
+#pragma unroll
+            for (int j = 0; j < kCB; ++j) {
+                const float* ps = ph[p] + min(s0 + j, S - 1) * PART;
+                ms[p][j] = ld_dev(ps);
+                ls[p][j] = ld_dev(ps + 1);
+                os[p][j] = ld_dev(ps + 4 + d[p]);
+            }
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            float Mb = M[p];
+#pragma unroll
+            for (int j = 0; j < kCB; ++j) Mb = s0 + j < S ? fmaxf(Mb, ms[p][j]) : Mb;
+            if (Mb == -__builtin_inff()) continue;
+            const float r = M[p] == -__builtin_inff() ? 0.0f : exp_fast(M[p] - Mb);
+            L[p] *= r;
+            O[p] *= r;
+#pragma unroll
+            for (int j = 0; j < kCB; ++j) {
+                const float w = s0 + j < S ? exp_fast(ms[p][j] - Mb) : 0.0f;
+                L[p] += ls[p][j] * w;
+                O[p] += os[p][j] * w;
+            }
+            M[p] = Mb;
         }
-        float Mb = M;
-#pragma unroll
-        for (int j = 0; j < kCB; ++j) Mb = s0 + j < S ? fmaxf(Mb, ms[j]) : Mb;
-        if (Mb == -__builtin_inff()) continue;
-        const float r = M == -__builtin_inff() ? 0.0f : exp_fast(M - Mb);
-        L *= r;
-        O *= r;
-#pragma unroll
-        for (int j = 0; j < kCB; ++j) {
-            const float w = s0 + j < S ? exp_fast(ms[j] - Mb) : 0.0f;
-            L += ls[j] * w;
-            O += os[j] * w;
-        }
-        M = Mb;
     }
-    return L > 0.0f ? O / L : 0.0f;
+#pragma unroll
+    for (int p = 0; p < P; ++p) res[p] = L[p] > 0.0f ? O[p] / L[p] : 0.0f;
 }
 
 template <bool F16>
@@ -377,10 +419,23 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
     if (tid == 0) arrival = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (arrival != static_cast<uint32_t>(S - 1)) return;
-    for (int t = tid; t < G * HD; t += kAT) {
-        const int h = t / HD, d = t % HD;
-        const float* ph = a.part + (static_cast<int64_t>(m) * n_q + kvh * G + h) * S * Geo::PART;
-        a.out[(static_cast<int64_t>(m) * n_q + kvh * G + h) * HD + d] = fold_splits<Geo::PART>(ph, S, d);
+    // this thread's (query head, dim) pairs t = tid, tid + kAT, ..., all
+    // merged together
+    constexpr int P = (G * HD + kAT - 1) / kAT;
+    const float* ph[P];
+    int dd[P];
+    float res[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int t = tid + kAT * p < G * HD ? tid + kAT * p : tid;  // past the pairs: a repeat, not stored
+        dd[p] = t % HD;
+        ph[p] = a.part + (static_cast<int64_t>(m) * n_q + kvh * G + t / HD) * S * Geo::PART;
+    }
+    fold_splits<Geo::PART, P>(ph, dd, S, res);
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int t = tid + kAT * p;
+        if (t < G * HD) a.out[(static_cast<int64_t>(m) * n_q + kvh * G + t / HD) * HD + t % HD] = res[p];
     }
     if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -430,15 +485,24 @@ hipError_t launch_embed(const void* table, bool bf16, const int32_t* tokens, flo
     return hipGetLastError();
 }
 
-hipError_t launch_rmsnorm_rows(const float* x, const float* gamma, const float* resid, float* out, int64_t d,
-                               int rows, float eps, bool gemma, hipStream_t s) {
+template <int V>
+hipError_t rmsnorm_v(const float* x, const float* gamma, const float* resid, float* out, int64_t d, int rows,
+                     float eps, bool gemma, hipStream_t s) {
     if (resid)
-        hipLaunchKernelGGL(k_rmsnorm_rows<true>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, x, gamma,
+        hipLaunchKernelGGL((k_rmsnorm_rows<true, V>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, x, gamma,
                            resid, out, static_cast<int>(d), eps, gemma ? 1 : 0);
     else
-        hipLaunchKernelGGL(k_rmsnorm_rows<false>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, x, gamma,
+        hipLaunchKernelGGL((k_rmsnorm_rows<false, V>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, s, x, gamma,
                            resid, out, static_cast<int>(d), eps, gemma ? 1 : 0);
     return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_rows(const float* x, const float* gamma, const float* resid, float* out, int64_t d,
+                               int rows, float eps, bool gemma, hipStream_t s) {
+    if (d % 4 != 0 || d > 16384) return hipErrorInvalidValue;
+    if (d <= 4096) return rmsnorm_v<4>(x, gamma, resid, out, d, rows, eps, gemma, s);
+    if (d <= 8192) return rmsnorm_v<8>(x, gamma, resid, out, d, rows, eps, gemma, s);
+    return rmsnorm_v<16>(x, gamma, resid, out, d, rows, eps, gemma, s);
 }
 
 hipError_t launch_qk_prep(const QkPrep& p, hipStream_t s) {

@@ -399,8 +399,8 @@ __global__ __launch_bounds__(bf16_gemv::kThreads) void k_gemv_q4k_bf16(
                                                lds, aux, eps, rope);
     else
         bf16_gemv::rows<8, XPB, false, bf16_gemv::kThreads, XOP>(
-            blk - q4k_wgs, (nb_rows + 3) / 4, wb, X, EPI == kEpiRope ? rope.dest(yb, kRopeCacheBf16Bit) : yb, nb_rows, K, nullptr,
-            lds, aux, eps);
+            blk - q4k_wgs, (nb_rows + 3) / 4, wb, X, EPI == kEpiRope ? rope.dest(yb, kRopeCacheBf16Bit) : yb,
+            nb_rows, K, nullptr, lds, aux, eps);
 }
 
 // The x operation, its second vector and eps (XOp).
