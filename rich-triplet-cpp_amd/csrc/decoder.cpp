@@ -267,8 +267,22 @@ int layer_step1(rt_hip_decoder* d, int li, hipStream_t s) {
         return rt_hip_gemv_bf16_swiglu_residual(static_cast<const uint16_t*>(L.down.data), d->gate, d->up, d->hidden,
                                                 H, F, s);
     }
-    rc = chk(launch_gelu_mul(d->gate, d->up, d->act, F, s), "decoder: gelu");
-    if (!rc) rc = gemv1(L.down, d->act, d->down, s);
+    // gelu_tanh(gate) * up applied while down stages its input (xop 4);
+    // a BF16 down wider than the fused launch's 8192 takes the separate pass
+    constexpr int kXopGelu = 4;
+    if (L.down.q4k()) {
+        const void* w[1] = {L.down.tiled};
+        float* y[1] = {d->down};
+        const int64_t n[1] = {L.down.n};
+        rc = chk(launch_gemv_q4k_xop(kXopGelu, 1, w, y, n, d->gate, d->up, 0.0f, F, s), "decoder: gelu + down");
+    } else if (F <= 8192) {
+        rc = chk(launch_gemv_bf16_xop(kXopGelu, static_cast<const uint16_t*>(L.down.data), d->gate, d->up, 0.0f,
+                                      d->down, L.down.n, F, s),
+                 "decoder: gelu + down");
+    } else {
+        rc = chk(launch_gelu_mul(d->gate, d->up, d->act, F, s), "decoder: gelu");
+        if (!rc) rc = gemv1(L.down, d->act, d->down, s);
+    }
     if (!rc)
         rc = chk(launch_rmsnorm_rows(d->down, L.post_ffn_norm, d->hidden2, d->hidden, H, 1, c.norm_eps, true, s),
                  "decoder: post-FFN norm");

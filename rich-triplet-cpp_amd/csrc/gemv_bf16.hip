@@ -129,6 +129,7 @@ hipError_t launch_gemv_bf16_xop(int xop, const uint16_t* w, const float* x, cons
         case kXRmsNorm: return run_xop<kXRmsNorm, false>(w, x, aux, eps, y, n, k, s);
         case kXRmsNorm1: return run_xop<kXRmsNorm1, false>(w, x, aux, eps, y, n, k, s);
         case kXSwiGlu: return run_xop<kXSwiGlu, false>(w, x, aux, eps, y, n, k, s);
+        case kXGelu: return run_xop<kXGelu, false>(w, x, aux, eps, y, n, k, s);
         default: return hipErrorInvalidValue;
     }
 }

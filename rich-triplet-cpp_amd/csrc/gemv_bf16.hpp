@@ -32,12 +32,14 @@ namespace rt_hip {
 //   kXRmsNorm  RMSNorm(x) * gamma            (tensor_node.cpp:320-344, 383);
 //   kXRmsNorm1 RMSNorm(x) * (1 + gamma)      (the Gemma 3 form, :387);
 //   kXSwiGlu   silu(gate) * up, x = gate     (tensor_node.cpp:391-402,
-//              transformer5.cpp:186-190).
+//              transformer5.cpp:186-190);
+//   kXGelu     gelu_tanh(gate) * up, x = gate (the Gemma 3 MLP gating,
+//              decode_gemma3.msl:128-158).
 // `aux` is gamma or up.  RMSNorm(x) * g = rms_inv * (x * g) with one scalar
 // rms_inv per vector, so kernels stage x * g and scale the finished dot
 // products by rms_inv (equal in exact arithmetic); the sum of squares is
 // reduced per wave and across waves through LDS at the staging barrier.
-enum XOp { kXNone = 0, kXRmsNorm = 1, kXRmsNorm1 = 2, kXSwiGlu = 3 };
+enum XOp { kXNone = 0, kXRmsNorm = 1, kXRmsNorm1 = 2, kXSwiGlu = 3, kXGelu = 4 };
 
 // silu(g) * u in the reference's order, the sigmoid from the hardware exp2
 // and reciprocal (about 1 ulp each; exp overflows to inf for g < -88 and
@@ -45,6 +47,18 @@ enum XOp { kXNone = 0, kXRmsNorm = 1, kXRmsNorm1 = 2, kXSwiGlu = 3 };
 __device__ __forceinline__ float swiglu1(float g, float u) {
     const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
     return (g * sig) * u;
+}
+
+// gelu_tanh(g) * u as the Metal kernel forms it (decode_gemma3.msl:128-145):
+// inner = 0.7978845608 (g + 0.044715 g^3), clamped to [-10, 10], then
+// 0.5 g (1 + tanh(inner)), times up.  tanh(a) = 1 - 2 / (e^(2a) + 1) from
+// the hardware exp2 and reciprocal (about 1 ulp each; |2a| <= 20 keeps e^(2a)
+// finite), rather than the library tanhf (~20 VALU per value).
+__device__ __forceinline__ float gelu1(float g, float u) {
+    float inner = 0.7978845608f * (g + 0.044715f * (g * g * g));
+    inner = fminf(fmaxf(inner, -10.0f), 10.0f);
+    const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(inner * 2.88539008177792682f) + 1.0f);
+    return (0.5f * g * (1.0f + t)) * u;
 }
 
 namespace bf16_gemv {
@@ -162,6 +176,9 @@ __device__ __forceinline__ void rows(int blk, int nblk, const uint16_t* __restri
         } else if constexpr (XOP == kXSwiGlu) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = swiglu1(v[e], a[e]);
+        } else if constexpr (XOP == kXGelu) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = gelu1(v[e], a[e]);
         }
         return v;
     };

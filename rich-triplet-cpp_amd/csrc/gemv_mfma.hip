@@ -265,6 +265,11 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
         for (int i = 0; i < XP; ++i)
 #pragma unroll
             for (int e = 0; e < 4; ++e) xv[i][e] = swiglu1(xv[i][e], av[i][e]);
+    } else if constexpr (XOP == kXGelu) {
+#pragma unroll
+        for (int i = 0; i < XP; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[i][e] = gelu1(xv[i][e], av[i][e]);
     }
     // Every lane converts its values (past the end: a dummy that is not
     // stored; the 8-lane reductions need the whole group).  No branch may
@@ -560,6 +565,7 @@ hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* 
         case kXRmsNorm: return dispatch<true, kXRmsNorm>(jobs, x, k, s, xa);
         case kXRmsNorm1: return dispatch<true, kXRmsNorm1>(jobs, x, k, s, xa);
         case kXSwiGlu: return dispatch<true, kXSwiGlu>(jobs, x, k, s, xa);
+        case kXGelu: return dispatch<true, kXGelu>(jobs, x, k, s, xa);
         default: return hipErrorInvalidValue;
     }
 }

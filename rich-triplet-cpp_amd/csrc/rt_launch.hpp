@@ -72,8 +72,8 @@ hipError_t launch_attention_decode(const float* q, const float* kc, const float*
 hipError_t launch_gemv_bf16_xop(int xop, const uint16_t* w, const float* x, const float* aux, float eps, float* y,
                                 int64_t n, int64_t k, hipStream_t s, bool add = false);
 // Tiled Q4_K GEMVs sharing x, with a layer operation applied to x while it
-// is staged: xop 1 RMSNorm * gamma, 2 RMSNorm * (1 + gamma), 3 silu(x) * aux
-// (aux = gamma or up; eps for the norms).
+// is staged: xop 1 RMSNorm * gamma, 2 RMSNorm * (1 + gamma), 3 silu(x) * aux,
+// 4 gelu_tanh(x) * aux (aux = gamma or up; eps for the norms).
 // rope_jobs != 0: interleaved RoPE (position pos, inv_freq [head_dim / 2])
 // on the outputs of the jobs in that bit mask; only with an RMSNorm xop.
 // add: y += the product (the residual add); with xop 0 (none) or 3 (SwiGLU).
