@@ -355,27 +355,42 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
 #pragma unroll
         for (int u = 0; u < kAU; ++u) {
             const int p = pb + u * NG;
+            const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+            ka[u] = kb[u] = va[u] = vb[u] = z;
             if (p < p1) {
                 const int64_t off = static_cast<int64_t>(p) * a.row + static_cast<int64_t>(kvh) * HD + sub * 8;
                 load8<F16>(a.kc, off, ka[u], kb[u]);
                 load8<F16>(a.vc, off, va[u], vb[u]);
             }
         }
+        // The round's kAU scores do not depend on each other: all of them
+        // first (their cross-lane sums overlap), then one running-maximum
+        // update and one rescale per round instead of one per position.
 #pragma unroll
-        for (int u = 0; u < kAU; ++u) {
-            if (pb + u * NG >= p1) break;  // uniform per position group
+        for (int h = 0; h < G; ++h) {
+            float sc[kAU];
+            float mn = mx[h];
 #pragma unroll
-            for (int h = 0; h < G; ++h) {
+            for (int u = 0; u < kAU; ++u) {
                 float dd = (qa[h][0] * ka[u][0] + qa[h][1] * ka[u][1]) + (qa[h][2] * ka[u][2] + qa[h][3] * ka[u][3]);
                 dd += (qb[h][0] * kb[u][0] + qb[h][1] * kb[u][1]) + (qb[h][2] * kb[u][2] + qb[h][3] * kb[u][3]);
-                const float sc = segment_sum<LP>(dd) * a.scale;
-                const float mn = fmaxf(mx[h], sc);
-                const float al = exp_fast(mx[h] - mn), be = exp_fast(sc - mn);
-                l[h] = l[h] * al + be;
-                oa[h] = oa[h] * al + va[u] * be;
-                ob[h] = ob[h] * al + vb[u] * be;
-                mx[h] = mn;
+                const float v = segment_sum<LP>(dd) * a.scale;
+                sc[u] = pb + u * NG < p1 ? v : -__builtin_inff();  // uniform per position group
+                mn = fmaxf(mn, sc[u]);
             }
+            if (mn == -__builtin_inff()) continue;  // no position of this group yet
+            const float al = exp_fast(mx[h] - mn);  // 0 while mx is -inf
+            l[h] *= al;
+            oa[h] *= al;
+            ob[h] *= al;
+#pragma unroll
+            for (int u = 0; u < kAU; ++u) {
+                const float be = exp_fast(sc[u] - mn);  // 0 for positions past the range
+                l[h] += be;
+                oa[h] += va[u] * be;
+                ob[h] += vb[u] * be;
+            }
+            mx[h] = mn;
         }
     }
 #pragma unroll
@@ -431,7 +446,9 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
         dd[p] = t % HD;
         ph[p] = a.part + (static_cast<int64_t>(m) * n_q + kvh * G + t / HD) * S * Geo::PART;
     }
-    fold_splits<Geo::PART, P>(ph, dd, S, res);
+    // splits past the range (chunk * busy >= len) hold empty states: skip them
+    const int busy = min(S, (len + chunk - 1) / chunk);
+    fold_splits<Geo::PART, P>(ph, dd, busy, res);
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         const int t = tid + kAT * p;
@@ -547,7 +564,7 @@ size_t attention2_workspace(int n_q, int head_dim, int splits, int m) {
 }
 
 hipError_t launch_attention2(const Attn2& p, float* part, uint32_t* counters, hipStream_t s) {
-    if (!counters) return hipErrorInvalidValue;
+    if (!counters || p.splits < 1) return hipErrorInvalidValue;
     AttnArgs a;
     a.q = p.q;
     a.kc = p.k_cache;
