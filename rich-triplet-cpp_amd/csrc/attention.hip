@@ -84,6 +84,8 @@ __global__ __launch_bounds__(kT) void k_attn_partial(const float* __restrict__ q
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
             const int p = pb + u * kGroups;
+            const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+            ka[u] = kb[u] = va[u] = vb[u] = z;
             if (p < p1) {
                 const float* kp = kc + p * row + kvh * kHd + sub * 8;
                 const float* vp = vc + p * row + kvh * kHd + sub * 8;
@@ -93,21 +95,34 @@ __global__ __launch_bounds__(kT) void k_attn_partial(const float* __restrict__ q
                 vb[u] = *reinterpret_cast<const f32x4*>(vp + 4);
             }
         }
+        // The batch's kU scores do not depend on each other: all of them
+        // first (their cross-lane sums overlap), then one running-maximum
+        // update and one rescale per batch instead of one per position.
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            if (pb + u * kGroups >= p1) break;  // uniform per group
+        for (int h = 0; h < G; ++h) {
+            float sc[kU];
+            float mn = m[h];
 #pragma unroll
-            for (int h = 0; h < G; ++h) {
+            for (int u = 0; u < kU; ++u) {
                 float d = (qa[h][0] * ka[u][0] + qa[h][1] * ka[u][1]) + (qa[h][2] * ka[u][2] + qa[h][3] * ka[u][3]);
                 d += (qb[h][0] * kb[u][0] + qb[h][1] * kb[u][1]) + (qb[h][2] * kb[u][2] + qb[h][3] * kb[u][3]);
-                const float sc = row16_sum(d) * scale;
-                const float mn = fmaxf(m[h], sc);
-                const float a = exp_fast(m[h] - mn), b = exp_fast(sc - mn);
-                l[h] = l[h] * a + b;
-                oa[h] = oa[h] * a + va[u] * b;
-                ob[h] = ob[h] * a + vb[u] * b;
-                m[h] = mn;
+                const float v = row16_sum(d) * scale;
+                sc[u] = pb + u * kGroups < p1 ? v : -__builtin_inff();  // uniform per group
+                mn = fmaxf(mn, sc[u]);
             }
+            if (mn == -__builtin_inff()) continue;  // no position of this group yet
+            const float a = exp_fast(m[h] - mn);    // 0 while m is -inf
+            l[h] *= a;
+            oa[h] *= a;
+            ob[h] *= a;
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                const float b = exp_fast(sc[u] - mn);  // 0 for positions past the range
+                l[h] += b;
+                oa[h] += va[u] * b;
+                ob[h] += vb[u] * b;
+            }
+            m[h] = mn;
         }
     }
     // Merge the 16 group states: every group writes, then thread (h, d4)
