@@ -159,6 +159,28 @@ int rt_hip_gemv_q4k_tiled(const void* tiled, const float* x, float* y, int64_t n
 int rt_hip_gemv_q4k_tiled_multi(int32_t count, const void* const* tiled, float* const* y,
                                 const int64_t* n, const float* x, int64_t k, rt_hip_stream stream);
 
+/* ---- Q8 activations (the reference's aarch64 GEMV path) -------------------
+ * rt_hip_q4k_quantize_activation_q8: a [k] f32 -> q8 [ceil(k/32) * 32] int8
+ * (zero-padded), scales and sums [ceil(k/32)] f32, bit for bit as
+ * Q4KMat::quantize_activation_q8 (src/quant_q4k.cpp:525-562; struct
+ * Q8Activation, include/rt/quant.hpp:108-117): per 32 values scale =
+ * absmax / 127, q = clamp(round(a / scale), -128, 127), sum in order.
+ * Any k >= 1; a, scales, sums 4-byte aligned; no output may overlap a.
+ * rt_hip_gemv_q4k_q8 / rt_hip_gemv_q4k_tiled_q8: M == 1 y = W x with x
+ * quantized as above inside the launch, then per row the integer chunk dots
+ * and the f32 combination of dot_row_q8 (src/quant_q4k.cpp:425-478), chunks
+ * summed in order: bit-identical to the reference's arithmetic (its build
+ * does not contract, CMakeLists.txt:17-47).
+ * Replace: Q4KMat::gemv_mt's aarch64 branch (src/quant_q4k.cpp:573-576,
+ * 590-591), which trades ~0.4% accuracy for integer dot products
+ * (include/rt/quant.hpp:160-170).  k % 256 == 0, k <= 16384; row-major
+ * blocks or the tiled layout. */
+int rt_hip_q4k_quantize_activation_q8(const float* a, int64_t k, int8_t* q8, float* scales, float* sums,
+                                      rt_hip_stream stream);
+int rt_hip_gemv_q4k_q8(const void* blocks, const float* x, float* y, int64_t n, int64_t k, rt_hip_stream stream);
+int rt_hip_gemv_q4k_tiled_q8(const void* tiled, const float* x, float* y, int64_t n, int64_t k,
+                             rt_hip_stream stream);
+
 /* A layer's q/k/v when v is BF16 (the Q6_K-widened v of a Q4_K_M model,
  * src/transformer4_load.cpp:141-143): up to four tiled-Q4_K GEMVs and one
  * BF16 GEMV w_bf16 [n_bf16, k] that all read x, in one launch.

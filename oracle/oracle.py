@@ -60,6 +60,8 @@ class Oracle:
                              C.c_int, _sz, _sz)
         self._q8act = _bind(L, "orc_q4k_quantize_activation_q8", None, _f32p, _sz, _i8p,
                             _f32p, _f32p)
+        self._q8dot = _bind(L, "orc_q4k_dot_row_q8", C.c_float, _u8p, _sz, _sz, _i8p, _f32p, _f32p)
+        self._q8gemv = _bind(L, "orc_q4k_gemv_q8", None, _u8p, _sz, _sz, _f32p, _f32p)
         self._bf16_mm = _bind(L, "orc_bf16_matmul_t", None, _u16p, _sz, _sz, _f32p, _sz,
                               _f32p, C.c_int, _sz, _sz)
         self._q4mat_quant = _bind(L, "orc_q4mat_quantize", None, _f32p, _sz, _u8p, _f32p)
@@ -251,6 +253,19 @@ class Oracle:
         su = np.zeros(nb, np.float32)
         self._q8act(a, a.size, q8, sc, su)
         return q8, sc, su
+
+    def q4k_dot_row_q8(self, blocks, cols, row, q8, scales, sums) -> float:
+        """dot_row_q8 (quant_q4k.cpp:425-478) on a quantized activation."""
+        return float(self._q8dot(np.ascontiguousarray(blocks, np.uint8), cols, row,
+                                 np.ascontiguousarray(q8, np.int8), np.ascontiguousarray(scales, np.float32),
+                                 np.ascontiguousarray(sums, np.float32)))
+
+    def q4k_gemv_q8(self, blocks, rows, cols, a) -> np.ndarray:
+        """gemv_mt's aarch64 branch (quant_q4k.cpp:564-600): Q8 activation, dot_row_q8."""
+        y = np.zeros(rows, np.float32)
+        self._q8gemv(np.ascontiguousarray(blocks, np.uint8), rows, cols,
+                     np.ascontiguousarray(a, np.float32).reshape(-1)[:cols].copy(), y)
+        return y
 
     # BF16 -- mat.cpp
     def bf16_matmul_t(self, w, a, n_threads=None, r0=0, r1=None) -> np.ndarray:

@@ -399,6 +399,58 @@ void orc_q4k_quantize_activation_q8(const float* a, size_t k, int8_t* q8, float*
     }
 }
 
+/* dot_row_q8 (src/quant_q4k.cpp:425-478, the aarch64 SDOT branch): per
+ * 64-value chunk of a super-block, the exact integer dots of the low nibbles
+ * with q8[64c .. 64c+32) and of the high nibbles with q8[64c+32 .. 64c+64)
+ * (vdotq_s32 lanes summed: an exact int32), then
+ *     total += d*sv1*scale_lo*idot_lo - dmin*mv1*sum_lo
+ *            + d*sv2*scale_hi*idot_hi - dmin*mv2*sum_hi
+ * left to right, each operation rounded (the reference builds with
+ * -ffp-contract=off, CMakeLists.txt:17-47).  The NEON intrinsics do not
+ * compile here; the integer dot is written as the plain sum it computes. */
+float orc_q4k_dot_row_q8(const uint8_t* blocks, size_t cols, size_t row, const int8_t* q8,
+                         const float* scales, const float* sums) {
+    const size_t nb = cols / Q4K_SUPERBLOCK;
+    float total = 0.0f;
+    for (size_t b = 0; b < nb; ++b) {
+        const uint8_t* bp = blocks + (row * nb + b) * Q4K_BLOCK_BYTES;
+        const float d = orc_f16_to_f32(rd16(bp)), dmin = orc_f16_to_f32(rd16(bp + 2));
+        const uint8_t* sc = bp + 4;
+        const uint8_t* qs = bp + 16;
+        const size_t a_base = b * Q4K_SUPERBLOCK;
+        for (size_t c = 0; c < 4; ++c) {
+            float sv1, mv1, sv2, mv2;
+            orc_q4k_scale_min(sc, 2 * c, &sv1, &mv1);
+            orc_q4k_scale_min(sc, 2 * c + 1, &sv2, &mv2);
+            const uint8_t* q = qs + c * 32;
+            const size_t lo = a_base + c * 64, hi = lo + 32;
+            int32_t idot_lo = 0, idot_hi = 0;
+            for (size_t l = 0; l < 32; ++l) {
+                idot_lo += (int32_t)(q[l] & 0x0f) * (int32_t)q8[lo + l];
+                idot_hi += (int32_t)(q[l] >> 4) * (int32_t)q8[hi + l];
+            }
+            total += d * sv1 * scales[lo / 32] * (float)idot_lo - dmin * mv1 * sums[lo / 32] +
+                     d * sv2 * scales[hi / 32] * (float)idot_hi - dmin * mv2 * sums[hi / 32];
+        }
+    }
+    return total;
+}
+
+/* gemv_mt's aarch64 branch (src/quant_q4k.cpp:564-600): the activation is
+ * quantized once (quantize_activation_q8), then every row takes dot_row_q8.
+ * Rows are independent, so one thread computes them all here. */
+void orc_q4k_gemv_q8(const uint8_t* blocks, size_t rows, size_t cols, const float* a, float* y) {
+    const size_t nb32 = div_ceil(cols, 32);
+    int8_t* q8 = (int8_t*)calloc(nb32 * 32, 1);
+    float* sc = (float*)calloc(nb32, sizeof(float));
+    float* su = (float*)calloc(nb32, sizeof(float));
+    orc_q4k_quantize_activation_q8(a, cols, q8, sc, su);
+    for (size_t j = 0; j < rows; ++j) y[j] = orc_q4k_dot_row_q8(blocks, cols, j, q8, sc, su);
+    free(q8);
+    free(sc);
+    free(su);
+}
+
 /* ------------------------------------------------------------------------ */
 /* BF16: src/mat.cpp:304-414                                                 */
 /* ------------------------------------------------------------------------ */

@@ -81,6 +81,16 @@ void orc_q4k_matmul_t(const uint8_t* blocks, size_t rows, size_t cols, const flo
 /* src/quant_q4k.cpp:525-562 (portable part of the aarch64 activation path) */
 void orc_q4k_quantize_activation_q8(const float* a, size_t k, int8_t* q8, float* scales,
                                     float* sums);
+/* src/quant_q4k.cpp:425-478 (dot_row_q8, aarch64): integer chunk dots, then
+ * the f32 combination left to right.  Pinned (tests/test_oracle_q8.py) by the
+ * integer dots recomputed in int64, activations that Q8 represents exactly
+ * (the result then equals the f64 dequantized dot to f32 rounding), the
+ * quantization error bound on random activations, one-hot and constant
+ * blocks in closed form, and a planted dropped term. */
+float orc_q4k_dot_row_q8(const uint8_t* blocks, size_t cols, size_t row, const int8_t* q8,
+                         const float* scales, const float* sums);
+/* src/quant_q4k.cpp:564-600 (aarch64 branch): quantize once, dot_row_q8 per row */
+void orc_q4k_gemv_q8(const uint8_t* blocks, size_t rows, size_t cols, const float* a, float* y);
 
 /* src/mat.cpp:304-316 (x86 branch) */
 float orc_bf16_dot_row(const uint16_t* w, size_t cols, size_t row, const float* a);

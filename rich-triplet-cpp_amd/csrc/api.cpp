@@ -376,7 +376,7 @@ int rt_hip_gemv_q4k_tiled_multi(int32_t count, const void* const* tiled, float* 
 }
 
 namespace {
-int gemv_xop(const char* fn, int xop, int32_t count, const void* const* tiled, float* const* y, const int64_t* n,
+static int gemv_xop(const char* fn, int xop, int32_t count, const void* const* tiled, float* const* y, const int64_t* n,
              const float* x, const float* aux, float eps, int64_t k, rt_hip_stream stream,
              const float* inv_freq = nullptr, int pos = 0, int head_dim = 0, int rope_jobs = 0, bool add = false) {
     if (count < 1 || count > RT_HIP_MULTI_MAX || !tiled || !y || !n)
@@ -461,7 +461,7 @@ int rt_hip_gemv_bf16_swiglu_residual(const uint16_t* w, const float* gate, const
 }
 
 namespace {
-int attention_args(const char* fn, const float* q, const float* k_cache, const float* v_cache, const float* out,
+static int attention_args(const char* fn, const float* q, const float* k_cache, const float* v_cache, const float* out,
                    int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int64_t seq_len) {
     if (!q || !k_cache || !v_cache || !out) return fail(RT_HIP_E_ARG, std::string(fn) + ": null pointer");
     if (head_dim != 128) return fail(RT_HIP_E_UNSUPPORTED, std::string(fn) + ": head_dim must be 128");
@@ -658,6 +658,43 @@ int rt_hip_gemv_q4k_tiled_bf16(int32_t count, const void* const* tiled, float* c
 int rt_hip_gemv_q4k_tiled(const void* tiled, const float* x, float* y, int64_t n, int64_t k,
                           rt_hip_stream stream) {
     return rt_hip_gemv_q4k_tiled_multi(1, &tiled, &y, &n, x, k, stream);
+}
+
+int rt_hip_q4k_quantize_activation_q8(const float* a, int64_t k, int8_t* q8, float* scales, float* sums,
+                                      rt_hip_stream stream) {
+    const char* fn = "rt_hip_q4k_quantize_activation_q8";
+    if (!a || !q8 || !scales || !sums) return fail(RT_HIP_E_ARG, std::string(fn) + ": null pointer");
+    if (k <= 0 || k > 0x7fffffffLL) return fail(RT_HIP_E_ARG, std::string(fn) + ": k must be in [1, 2^31)");
+    if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(sums)) &
+        3u)
+        return fail(RT_HIP_E_ALIGN, std::string(fn) + ": a, scales and sums must be 4-byte aligned");
+    const int64_t nq = (k + 31) / 32;
+    if (overlaps(q8, nq * 32, a, k * 4) || overlaps(scales, nq * 4, a, k * 4) || overlaps(sums, nq * 4, a, k * 4) ||
+        overlaps(q8, nq * 32, scales, nq * 4) || overlaps(q8, nq * 32, sums, nq * 4) ||
+        overlaps(scales, nq * 4, sums, nq * 4))
+        return fail(RT_HIP_E_ARG, std::string(fn) + ": outputs overlap each other or a");
+    return check_stream_launch(launch_quantize_q8(a, k, q8, scales, sums, static_cast<hipStream_t>(stream)), fn);
+}
+
+namespace {
+static int gemv_q8(const char* fn, bool tiled, const void* w, const float* x, float* y, int64_t n, int64_t k,
+            rt_hip_stream stream) {
+    int rc = gemv_args(fn, w, x, y, n, k, 1, 256);
+    if (rc) return rc;
+    if (k > 16384) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 16384");
+    hipError_t e;
+    if (!state_for_current(&e)) return hip_fail(e, fn);
+    return check_stream_launch(launch_gemv_q4k_q8(w, tiled, x, y, n, k, static_cast<hipStream_t>(stream)), fn);
+}
+}  // namespace
+
+int rt_hip_gemv_q4k_q8(const void* blocks, const float* x, float* y, int64_t n, int64_t k, rt_hip_stream stream) {
+    return gemv_q8("rt_hip_gemv_q4k_q8", false, blocks, x, y, n, k, stream);
+}
+
+int rt_hip_gemv_q4k_tiled_q8(const void* tiled, const float* x, float* y, int64_t n, int64_t k,
+                             rt_hip_stream stream) {
+    return gemv_q8("rt_hip_gemv_q4k_tiled_q8", true, tiled, x, y, n, k, stream);
 }
 
 }  // extern "C"

@@ -328,7 +328,7 @@ int rt_hip_gguf_linear_shape(const rt_hip_gguf* f, int64_t idx, int64_t* rows, i
 }
 
 namespace {
-const Meta* meta_at(const rt_hip_gguf* f, const char* key, int64_t index) {
+static const Meta* meta_at(const rt_hip_gguf* f, const char* key, int64_t index) {
     if (!f || !key) return nullptr;
     auto it = f->meta.find(key);
     if (it == f->meta.end()) return nullptr;

@@ -160,6 +160,13 @@ hipError_t launch_dequant_q4k_cvt(const void* w, uint16_t* wout, int64_t n, int6
 hipError_t launch_quantize_q4k(const float* w, void* blocks, int64_t n, int64_t k,
                                hipStream_t s);
 
+// Q8 activations (gemv_q8.hip): quantize_activation_q8 for any k (q8 padded
+// with zeros to whole 32-value blocks), and the M = 1 Q4_K x Q8 GEMV on
+// row-major or tiled blocks (k % 256 == 0, k <= 16384).
+hipError_t launch_quantize_q8(const float* a, int64_t k, int8_t* q8, float* scales, float* sums, hipStream_t s);
+hipError_t launch_gemv_q4k_q8(const void* w, bool tiled, const float* x, float* y, int64_t n, int64_t k,
+                              hipStream_t s);
+
 // Q4Mat (q4mat.hip): one buffer of packed nibbles then f32 scales at
 // q4mat_scales_offset; K % 32 == 0.  The M <= 8 GEMV stages x [M][K] in LDS
 // (q4mat_gemv_lds_bytes).  launch_dequant_4bit: Q4Mat or GGUF Q4_0 -> bf16

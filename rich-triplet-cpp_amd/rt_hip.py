@@ -33,6 +33,9 @@ _SIGNATURES = {
     "rt_hip_q4k_tile_rope_half": [_vp, _vp, _i64, _i64, _i32, _vp],
     "rt_hip_gemv_q4k_tiled": [_vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_multi": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _i64, _vp],
+    "rt_hip_q4k_quantize_activation_q8": [_vp, _i64, _vp, _vp, _vp, _vp],
+    "rt_hip_gemv_q4k_q8": [_vp, _vp, _vp, _i64, _i64, _vp],
+    "rt_hip_gemv_q4k_tiled_q8": [_vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_gemv_q4_0": [_vp, _vp, _vp, _i64, _i64, _i32, _vp],
     "rt_hip_argmax": [_vp, _i64, _i64, _vp, _vp, _vp],
     "rt_hip_gemv_bf16_argmax": [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp],
@@ -265,6 +268,30 @@ def gemv_q4k_tiled(tiled, x, n: int, k: int, y=None, stream=None):
         y = torch.empty((1, n), dtype=torch.float32, device=x.device)
     _dev_check(tiled, x, y)
     library().call("rt_hip_gemv_q4k_tiled", _ptr(tiled), _ptr(x), _ptr(y), n, k, _stream(stream))
+    return y
+
+
+def quantize_activation_q8(a, stream=None):
+    """Q4KMat::quantize_activation_q8 (quant_q4k.cpp:525-562): (q8, scales, sums)."""
+    torch = _torch()
+    k = a.numel()
+    nq = (k + 31) // 32
+    q8 = torch.empty(nq * 32, dtype=torch.int8, device=a.device)
+    sc = torch.empty(nq, dtype=torch.float32, device=a.device)
+    su = torch.empty(nq, dtype=torch.float32, device=a.device)
+    _dev_check(a)
+    library().call("rt_hip_q4k_quantize_activation_q8", _ptr(a), k, _ptr(q8), _ptr(sc), _ptr(su), _stream(stream))
+    return q8, sc, su
+
+
+def gemv_q4k_q8(w, x, n: int, k: int, tiled: bool = False, y=None, stream=None):
+    """gemv_mt's aarch64 branch (quant_q4k.cpp:564-600): Q8 activation, dot_row_q8 per row."""
+    torch = _torch()
+    if y is None:
+        y = torch.empty((1, n), dtype=torch.float32, device=x.device)
+    _dev_check(w, x, y)
+    library().call("rt_hip_gemv_q4k_tiled_q8" if tiled else "rt_hip_gemv_q4k_q8", _ptr(w), _ptr(x), _ptr(y), n, k,
+                   _stream(stream))
     return y
 
 
