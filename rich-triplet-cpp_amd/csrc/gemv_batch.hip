@@ -107,25 +107,6 @@ __host__ __device__ inline size_t batch_lds_bytes(int steps, int q) {
     return static_cast<size_t>(steps) * q * (F::kLimb + F::kCst) + kZeroBytes;
 }
 
-// bf16 limbs of four activations (one f32x4): three 8-byte bf16 quads.  An
-// infinite x keeps its infinity in h and zero low limbs.
-__device__ __forceinline__ void bf16_limbs4(const f32x4 v, u32x2& h, u32x2& m, u32x2& l) {
-    uint32_t hb[4], mb[4], lb[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float x = v[e];
-        hb[e] = f32_to_bf16_rne(x);
-        const float hf = __uint_as_float(hb[e] << 16);
-        const float r1 = __builtin_isinf(hf) ? 0.0f : x - hf;
-        mb[e] = f32_to_bf16_rne(r1);
-        const float r2 = r1 - __uint_as_float(mb[e] << 16);
-        lb[e] = f32_to_bf16_rne(r2);
-    }
-    h = u32x2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
-    m = u32x2{mb[0] | (mb[1] << 16), mb[2] | (mb[3] << 16)};
-    l = u32x2{lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
-}
-
 // Sum and max over the aligned quad of lanes (every lane gets the same bits).
 __device__ __forceinline__ float quad_sum(float v) {
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1, 0xf, 0xf, false));

@@ -147,24 +147,6 @@ __device__ __forceinline__ bf16x8 widen(const Slot& s, float d, uint32_t gsh) {
     return __builtin_bit_cast(bf16x8, w);
 }
 
-// bf16 limbs of 4 activations (as in the batched GEMV): h + m + l == x.
-__device__ __forceinline__ void limbs4(const f32x4 v, u32x2& h, u32x2& m, u32x2& l) {
-    uint32_t hb[4], mb[4], lb[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float x = v[e];
-        hb[e] = f32_to_bf16_rne(x);
-        const float hf = __uint_as_float(hb[e] << 16);
-        const float r1 = __builtin_isinf(hf) ? 0.0f : x - hf;
-        mb[e] = f32_to_bf16_rne(r1);
-        const float r2 = r1 - __uint_as_float(mb[e] << 16);
-        lb[e] = f32_to_bf16_rne(r2);
-    }
-    h = u32x2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
-    m = u32x2{mb[0] | (mb[1] << 16), mb[2] | (mb[3] << 16)};
-    l = u32x2{lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
-}
-
 // Workgroup of T threads: KS <= 4 runs 4 waves, TPW = 4 / KS tiles each
 // split over KS waves by blocks; larger KS runs one tile on KS waves.  LDS:
 // x limbs [K/32 steps][3][32] bf16, a zero line, then the KS partial rows.
@@ -215,8 +197,8 @@ __global__ __launch_bounds__(T) void k_gemv_q6k(const uint8_t* __restrict__ W, c
     for (int i = 0; i < XP; ++i) {
         const int u = tid + nthr * i;
         u32x2 ha, ma, la, hb, mb, lb;
-        limbs4(xa[i], ha, ma, la);
-        limbs4(xb[i], hb, mb, lb);
+        bf16_limbs4(xa[i], ha, ma, la);
+        bf16_limbs4(xb[i], hb, mb, lb);
         if (u < units) {
             u32x4* dst = reinterpret_cast<u32x4*>(lds + (u >> 2) * kStepBytes + (u & 3) * 16);
             dst[0] = u32x4{ha[0], ha[1], hb[0], hb[1]};

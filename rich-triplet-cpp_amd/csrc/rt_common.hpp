@@ -102,6 +102,26 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
     return (static_cast<uint64_t>(u) << 32) | (0xffffffffu - idx);
 }
 
+// bf16 limbs of four activations (one f32x4): three 8-byte bf16 quads with
+// h + m + l == x exactly for every finite x (each residual is exact in f32);
+// an infinite x keeps its infinity in h and zero low limbs.  Each limb is one
+// v_cvt_pk_bf16_f32 per pair (bf16_pair): the same bits as f32_to_bf16_rne at
+// a fifth of the VALU.
+__device__ __forceinline__ void bf16_limbs4(const f32x4 v, u32x2& h, u32x2& m, u32x2& l) {
+    const uint32_t h01 = bf16_pair(v[0], v[1]), h23 = bf16_pair(v[2], v[3]);
+    const float hf[4] = {__uint_as_float(h01 << 16), __uint_as_float(h01 & 0xffff0000u), __uint_as_float(h23 << 16),
+                         __uint_as_float(h23 & 0xffff0000u)};
+    float r1[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r1[e] = __builtin_isinf(hf[e]) ? 0.0f : v[e] - hf[e];
+    const uint32_t m01 = bf16_pair(r1[0], r1[1]), m23 = bf16_pair(r1[2], r1[3]);
+    const float r2[4] = {r1[0] - __uint_as_float(m01 << 16), r1[1] - __uint_as_float(m01 & 0xffff0000u),
+                         r1[2] - __uint_as_float(m23 << 16), r1[3] - __uint_as_float(m23 & 0xffff0000u)};
+    h = u32x2{h01, h23};
+    m = u32x2{m01, m23};
+    l = u32x2{bf16_pair(r2[0], r2[1]), bf16_pair(r2[2], r2[3])};
+}
+
 // f32 -> bf16 round-to-nearest-even with NaN quieting (bf16.hpp:50-60).
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float v) {
     const uint32_t bits = __float_as_uint(v);
