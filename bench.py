@@ -722,6 +722,134 @@ def bench_single_gemv(args, rt, torch, fmt, n, k, label, workload, copies_bytes=
                 roof, cpu)
 
 
+def bench_path_gemv(args, rt, torch, kind: str):
+    """The GEMV paths beside the headline, each measured like configs 1-2b
+    (one product per launch, rotating through weight copies that exceed the
+    256 MB MALL, HIP events over graph replays) with the reference's CPU
+    path for the same product timed beside it:
+      q8_gemv     Q4_K x Q8 activations (the reference's aarch64 gemv_mt,
+                  dot_row_q8), 8192 x 3072 tiled;
+      q6k_gemv    native GGUF Q6_K, the Llama-3.2-3B down 3072 x 8192 tiled;
+      q4mat_gemv  Q4Mat (Linear2::quantize's storage), 4096 x 4096;
+      batch_gemv  Q4_K 8192 x 3072 at M = 8 (speculative verify)."""
+    import numpy as np
+    g = torch.Generator(device="cuda").manual_seed(0)
+    m = 1
+    if kind == "q8_gemv":
+        n, k = 8192, 3072
+        wbytes = n * k // 256 * 144
+    elif kind == "q6k_gemv":
+        n, k = 3072, 8192
+        wbytes = n * k // 256 * 210
+    elif kind == "q4mat_gemv":
+        n, k = 4096, 4096
+        wbytes = rt.q4mat_bytes(n, k)
+    elif kind == "batch_gemv":
+        n, k, m = 8192, 3072, 8
+        wbytes = n * k // 256 * 144
+    else:
+        raise ValueError(kind)
+    copies = max(2, (768 << 20) // wbytes)
+    ws, host = [], None
+    for i in range(copies):
+        if kind == "q6k_gemv":
+            b = torch.randint(0, 256, (n * (k // 256), 210), dtype=torch.uint8, device="cuda", generator=g)
+            b[:, 208] = 0x00
+            b[:, 209] = 0x20  # d = 2^-7 (f16 0x2000): finite, typical magnitude
+            b = b.reshape(-1)
+            if i == 0:
+                host = rt.dequant_q6k_bf16(b, n, k).cpu().numpy().view(np.uint16)
+            ws.append(rt.q6k_tile(b, n, k))
+        elif kind == "q4mat_gemv":
+            # synthetic Q4Mat storage: random nibbles (-8..7), scales of the
+            # magnitude absmax / 7 gives N(0, 0.02) weights
+            packed = torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8, device="cuda",
+                                   generator=g).cpu().numpy()
+            scales = (0.006 + 0.004 * torch.rand((n * k // 32,), generator=g, device="cuda")).cpu().numpy()
+            if i == 0:
+                host = (packed, scales)
+            ws.append(rt.q4mat_upload(packed, scales, n, k))
+        else:
+            w = torch.randn((n, k), generator=g, device="cuda") * 0.02
+            blocks = rt.quantize_q4k(w)
+            del w
+            if i == 0:
+                host = blocks.cpu().numpy()
+            ws.append(rt.q4k_tile(blocks, n, k) if kind == "q8_gemv" else blocks)
+    x = torch.randn((m, k), generator=g, device="cuda")
+    y = torch.empty((m, n), device="cuda")
+
+    def run():
+        for w in ws:
+            if kind == "q8_gemv":
+                rt.gemv_q4k_q8(w, x, n, k, tiled=True, y=y)
+            elif kind == "q6k_gemv":
+                rt.gemv_q6k_tiled(w, x, n, k, y=y)
+            elif kind == "q4mat_gemv":
+                rt.gemv(rt.Q4MAT, w, x, n, k, y=y)
+            else:
+                rt.gemv(rt.Q4K, w, x, n, k, y=y)
+
+    ms, _ = time_graph(torch, run, args.warmup, args.steps)
+    us = ms * 1e3 / copies
+    nbytes = wbytes + 4 * m * k + 4 * m * n
+    gbs = nbytes / (us * 1e-6) / 1e9
+    roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "us_per_launch": round(us, 3),
+            "bytes_per_launch": nbytes}
+    cpu = None
+    if not args.no_cpu_baseline:
+        ckind, cref, threads, orc = _cpu_handles()
+        xh = x.cpu().numpy()
+        if kind == "q8_gemv":
+            # dot_row_q8 is NEON-only: the oracle's restatement, one thread.
+            ckind, threads = "port", 1
+            med, reps = _cpu_timed(lambda: orc.q4k_gemv_q8(host, n, k, xh), 10.0)
+            desc = ("the oracle's restatement of gemv_mt's aarch64 branch (quantize_activation_q8, then "
+                    "dot_row_q8 per row; the reference's NEON code does not build on x86), one thread")
+        elif kind == "q6k_gemv":
+            if ckind == "reference":
+                h = cref.bf16_new(host, n, k)
+                out = np.empty((1, n), np.float32)
+                med, reps = _cpu_timed(lambda: cref.bf16_handle_matmul_t(h, xh, 1, out), 10.0)
+                cref.bf16_delete(h)
+            else:
+                med, reps = _cpu_timed(lambda: orc.bf16_matmul_t(host, xh), 10.0)
+            desc = (f"the reference's path for a Q6_K weight: widened to BF16 at load (not timed), then "
+                    f"MatBf16 gemv_mt with threads = min(hw={threads}, N/128); GB/s over the Q6_K bytes")
+        elif kind == "q4mat_gemv":
+            packed, scales = host
+            fn = cref.q4mat_matmul_t if ckind == "reference" else orc.q4mat_matmul_t
+            med, reps = _cpu_timed(lambda: fn(packed, scales, n, k, xh), 10.0)
+            threads = 1
+            desc = "Q4Mat::matmul_q4_t (single-threaded, quant_q4.cpp:92-114)"
+        else:
+            rows = 256
+            bh = host.reshape(n, -1)[:rows].reshape(-1)
+            fn = cref.q4k_matmul_t if ckind == "reference" else orc.q4k_matmul_t
+            med_rows, reps = _cpu_timed(lambda: fn(bh, rows, k, xh), 10.0)
+            med = med_rows * n / rows
+            threads = 1
+            desc = (f"Q4KMat::matmul_q4k_t's M > 1 loop (single-threaded, quant_q4k.cpp:611-623) on the first "
+                    f"{rows} output rows, extrapolated linearly to all {n} rows")
+        cpu = {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": ckind,
+               "sample": f"the whole product, median of {reps} reps ({med * 1e3:.2f} ms each); {desc}",
+               "us_per_launch": round(med * 1e6, 1)}
+    label = {"q8_gemv": "Q4_K x Q8-activation GEMV 8192x3072 (aarch64 gemv_mt semantics)",
+             "q6k_gemv": "native Q6_K GEMV 3072x8192 (Llama-3.2-3B down)",
+             "q4mat_gemv": "Q4Mat GEMV 4096x4096",
+             "batch_gemv": "batched Q4_K GEMV 8192x3072, M=8"}[kind]
+    dtype = {"q8_gemv": "q4_k weights, int8 activations (per-32 absmax/127 scale), i32 dots, f32 combine",
+             "q6k_gemv": "q6_k weights widened in registers to the reference's bf16 values, f32 activations "
+                         "(3 exact bf16 limbs)",
+             "q4mat_gemv": "q4mat weights (signed nibbles, f32 scale per 32), f32 activations",
+             "batch_gemv": "q4_k weights, f32 activations (3 exact int8 limbs per value)"}[kind]
+    return line(args, f"{label} achieved HBM GB/s", round(gbs, 1), "GB/s", ms / copies, True, dtype,
+                {"workload": kind, "n": n, "k": k, "m": m, "bytes_per_launch": nbytes,
+                 "weight_copies": int(copies), "us_per_launch": round(us, 3),
+                 "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}, roof, cpu)
+
+
 def bench_gemm(args, rt, torch, shapes, label, a_bf16, workload):
     """BASELINE configs 4 and 5: Q4_K GEMMs (dequantize once per call, bf16
     MFMA, f32 accumulate), one graph of the config's GEMMs per step.  The
@@ -845,7 +973,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="llama_decode",
                     choices=["llama_decode", "q4k_gemv", "q4_0_gemv", "bf16_lm_head", "prefill",
-                             "flux", "flux_attention", "layer_ops", "decode_layers", "engine_llama3b", "engine_gemma3_4b"])
+                             "flux", "flux_attention", "layer_ops", "decode_layers", "engine_llama3b", "engine_gemma3_4b",
+                             "q8_gemv", "q6k_gemv", "q4mat_gemv", "batch_gemv"])
     ap.add_argument("--mix", default="q4km", choices=["q4km", "q4k"])
     ap.add_argument("--context", type=int, default=1024,
                     help="cached positions for --workload decode_layers")
@@ -907,6 +1036,8 @@ def main() -> int:
         out = bench_decode_layers(args, rt, torch)
     elif args.workload.startswith("engine_"):
         out = bench_engine(args, rt, torch, args.workload[len("engine_"):])
+    elif args.workload in ("q8_gemv", "q6k_gemv", "q4mat_gemv", "batch_gemv"):
+        out = bench_path_gemv(args, rt, torch, args.workload)
     elif args.workload == "flux":
         out = bench_gemm(args, rt, torch, [(4608, 9216, 3072), (4608, 12288, 3072), (4608, 3072, 12288)],
                          "config 5 FLUX linears M=4608 (QKV, MLP-in, MLP-out)", True,
