@@ -88,6 +88,7 @@ struct rt_hip_decoder {
     uint32_t* attn_cnt = nullptr;  // attention arrival counters, [max rows][n_kv], zero between launches
     int32_t* dstate = nullptr;  // [0] position of row 0, [1..8] tokens
     int32_t* hstate = nullptr;  // pinned host mirror
+    float* logits_stage = nullptr;  // pinned host staging for the logits readback, [max rows][vocab]
     uint64_t* argmax_keys = nullptr;
     int64_t* argmax_idx = nullptr;
     hipStream_t stream = nullptr;  // used when the caller passes the legacy stream (not capturable)
@@ -375,17 +376,39 @@ int record_step(rt_hip_decoder* d, int m, hipStream_t s) {
             const void* w[1] = {d->lm_head.tiled};
             float* y[1] = {d->logits};
             const int64_t n[1] = {V};
-            return rt_hip_gemv_q4k_tiled_rmsnorm_multi(1, w, y, n, d->hidden, d->out_norm, c.norm_eps,
-                                                       d->gemma ? 1 : 0, H, s);
+            rc = rt_hip_gemv_q4k_tiled_rmsnorm_multi(1, w, y, n, d->hidden, d->out_norm, c.norm_eps,
+                                                     d->gemma ? 1 : 0, H, s);
+        } else {
+            rc = chk(launch_gemv_bf16_xop(d->gemma ? 2 : 1, static_cast<const uint16_t*>(d->lm_head.data), d->hidden,
+                                          d->out_norm, c.norm_eps, d->logits, V, H, s),
+                     "decoder: lm_head");
         }
-        return chk(launch_gemv_bf16_xop(d->gemma ? 2 : 1, static_cast<const uint16_t*>(d->lm_head.data), d->hidden,
-                                        d->out_norm, c.norm_eps, d->logits, V, H, s),
-                   "decoder: lm_head");
+        // The argmax of the logits (transformer5.cpp:382-391) rides in the
+        // same graph: three small launches on the GPU instead of a separate
+        // host call per token.
+        if (!rc) rc = chk(launch_argmax_init(d->argmax_keys, 1, s), "decoder: argmax");
+        if (!rc) rc = chk(launch_argmax_scan(d->logits, 1, V, d->argmax_keys, s), "decoder: argmax");
+        if (!rc) rc = chk(launch_argmax_finalize(d->argmax_keys, 1, d->argmax_idx, nullptr, s), "decoder: argmax");
+        return rc;
     }
     rc = chk(launch_rmsnorm_rows(d->hidden, d->out_norm, nullptr, d->normed, H, m, c.norm_eps, d->gemma, s),
              "decoder: final norm");
     if (!rc) rc = gemvm(d->lm_head, d->normed, d->logits, m, s);
     return rc;
+}
+
+// Queues the copy of `elems` logits to the caller's host buffer.  A pinned
+// (page-locked) destination takes the copy directly; pageable memory would
+// make the runtime stage the copy itself at a fraction of the bandwidth, so
+// it goes through the decoder's pinned staging buffer and *staged is set: the
+// caller copies from there after the stream has synchronised.
+hipError_t logits_readback(rt_hip_decoder* d, float* dst, int64_t elems, hipStream_t s, float** staged) {
+    hipPointerAttribute_t attr{};
+    const bool pinned = hipPointerGetAttributes(&attr, dst) == hipSuccess && attr.type == hipMemoryTypeHost;
+    (void)hipGetLastError();  // an unregistered pointer may leave an error behind: clear it
+    *staged = pinned ? nullptr : d->logits_stage;
+    return hipMemcpyAsync(pinned ? dst : d->logits_stage, d->logits, static_cast<size_t>(elems) * 4,
+                          hipMemcpyDeviceToHost, s);
 }
 
 bool complete(const rt_hip_decoder* d, std::string* what) {
@@ -510,6 +533,9 @@ int rt_hip_decoder_create(const rt_hip_decoder_config* cfg, rt_hip_decoder** out
         (e = dev_alloc_t(d, &d->argmax_idx, 16)) != hipSuccess)
         return cleanup(e);
     if ((e = hipHostMalloc(reinterpret_cast<void**>(&d->hstate), 16 * sizeof(int32_t))) != hipSuccess)
+        return cleanup(e);
+    if ((e = hipHostMalloc(reinterpret_cast<void**>(&d->logits_stage), static_cast<size_t>(R) * c.vocab * 4)) !=
+        hipSuccess)
         return cleanup(e);
     if ((e = hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking)) != hipSuccess) return cleanup(e);
     // attention partials for the largest split count of any batch size
@@ -674,15 +700,12 @@ int rt_hip_decoder_step(rt_hip_decoder* d, int32_t token, int32_t pos, float* lo
     const hipStream_t s = stream ? static_cast<hipStream_t>(stream) : d->stream;
     int rc = run_step(d, &token, 1, pos, s);
     if (rc) return rc;
-    if (argmax_host) {
-        rc = rt_hip_argmax(d->logits, 1, d->lm_head.n, d->argmax_idx, nullptr, s);
-        if (rc) return rc;
-    }
     hipError_t e = hipSuccess;
-    if (logits_host)
-        e = hipMemcpyAsync(logits_host, d->logits, d->lm_head.n * 4, hipMemcpyDeviceToHost, s);
+    float* staged = nullptr;
+    if (logits_host) e = logits_readback(d, logits_host, d->lm_head.n, s, &staged);
     if (e == hipSuccess && argmax_host) e = hipMemcpyAsync(argmax_host, d->argmax_idx, 8, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e == hipSuccess && staged) std::memcpy(logits_host, staged, static_cast<size_t>(d->lm_head.n) * 4);
     return e == hipSuccess ? RT_HIP_OK : hip_fail(e, "rt_hip_decoder_step");
 }
 
@@ -696,10 +719,11 @@ int rt_hip_decoder_step_batch(rt_hip_decoder* d, const int32_t* tokens, int32_t 
     int rc = run_step(d, tokens, count, start_pos, s);
     if (rc) return rc;
     hipError_t e = hipSuccess;
-    if (logits_host)
-        e = hipMemcpyAsync(logits_host, d->logits, static_cast<size_t>(count) * d->lm_head.n * 4,
-                           hipMemcpyDeviceToHost, s);
+    float* staged = nullptr;
+    const int64_t elems = static_cast<int64_t>(count) * d->lm_head.n;
+    if (logits_host) e = logits_readback(d, logits_host, elems, s, &staged);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e == hipSuccess && staged) std::memcpy(logits_host, staged, static_cast<size_t>(elems) * 4);
     return e == hipSuccess ? RT_HIP_OK : hip_fail(e, fn);
 }
 
@@ -714,6 +738,7 @@ int rt_hip_decoder_destroy(rt_hip_decoder* d) {
     for (auto& g : d->graphs) rt_hip_graph_destroy(g);
     for (void* p : d->allocations) (void)hipFree(p);
     if (d->hstate) (void)hipHostFree(d->hstate);
+    if (d->logits_stage) (void)hipHostFree(d->logits_stage);
     if (d->stream) (void)hipStreamDestroy(d->stream);
     delete d;
     return RT_HIP_OK;
