@@ -182,20 +182,15 @@ __global__ __launch_bounds__(256) void k_gemm(const void* __restrict__ Ap,
 }
 
 // ---------------------------------------------------------------------------
-// Pipelined kernel (K % 256 == 0): bf16 A, Q4_K or bf16 W.
+// Pipelined kernel (K % 256 == 0): bf16 A and W.
 //
 // LDS tiles are 128 rows x 64 bf16 (128 B per row, unpadded) with the 16-byte
 // chunk c of row r stored at chunk slot c ^ (r & 7), so the MFMA fragment
 // reads (16 rows x one chunk) are conflict-free and whole tiles can be
 // written by direct-to-LDS buffer loads (1 KB per wave instruction: 8 rows).
-//  * A (and a bf16 W) stream through a ring of kStages LDS tiles, copied by
+//  * A and W stream through a ring of kStages LDS tiles each, copied by
 //    buffer loads straight into LDS kStages-1 steps ahead; rows past M (N)
 //    read as zeros through the buffer range check.
-//  * A Q4_K W goes through a ring of kRing register slots (header + 16 qs
-//    bytes per thread and step), kRing steps ahead, and is dequantized into
-//    one of two LDS tiles one step ahead of its use: w = (d*sv)*q - dmin*mv
-//    exact in f32, then round-to-nearest-even bf16 (v_cvt_pk_bf16_f32), as
-//    the reference's flux_dequant_q4k (shaders/flux.msl:69-81).
 //  * One barrier per 64-wide K step.  Tiles are assigned XCD by XCD (a
 //    workgroup's XCD is its id mod 8), each XCD getting a contiguous range
 //    of a grouped tile order (8 M-tiles per N column), so the tiles resident
@@ -203,7 +198,6 @@ __global__ __launch_bounds__(256) void k_gemm(const void* __restrict__ Ap,
 constexpr int kPThreads = 256;
 constexpr int kStages = 4;
 constexpr int kTile = 128 * 128;    // bytes of one 128 x 64 bf16 tile
-constexpr int kRawStage = 8192;     // raw Q4_K bytes of one step: headers 4 KB, qs 4 KB
 constexpr int kGroupM = 8;
 
 __device__ __forceinline__ uint32_t swz(int r, int c) {
@@ -286,15 +280,14 @@ __device__ __forceinline__ void store_tile_staged(const f32x4 (&acc)[NI][4], flo
     }
 }
 
-template <bool W_Q4K>
 __global__ __launch_bounds__(kPThreads) void k_gemm_pipe(const uint16_t* __restrict__ A,
-                                                         const void* __restrict__ Wp,
-                                                         const float* __restrict__ bias,
-                                                         float* __restrict__ Cp, int M, int N, int K,
-                                                         int mt, int ldk, int64_t c_split) {
+                                                        const uint16_t* __restrict__ Wp,
+                                                        const float* __restrict__ bias,
+                                                        float* __restrict__ Cp, int M, int N, int K,
+                                                        int mt, int ldk, int64_t c_split) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     uint8_t* const sA = lds;                        // [kStages][kTile]
-    uint8_t* const sW = lds + kStages * kTile;      // bf16: [kStages][kTile]; Q4_K: [2][kTile] + raw ring
+    uint8_t* const sW = lds + kStages * kTile;      // [kStages][kTile]
 
     // XCD-contiguous tile id, then grouped order: consecutive ids walk
     // kGroupM M-tiles of one N column before the next column, so the tiles
@@ -312,8 +305,8 @@ __global__ __launch_bounds__(kPThreads) void k_gemm_pipe(const uint16_t* __restr
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
     // Split-K slice blockIdx.y: columns [k0, k0 + K) of rows of ldk
-    // elements, into C + blockIdx.y * c_split (the Q4_K path and unsplit
-    // calls have one slice: k0 = 0, ldk = K).
+    // elements, into C + blockIdx.y * c_split (unsplit calls have one slice:
+    // k0 = 0, ldk = K).
     const int k0 = static_cast<int>(blockIdx.y) * K;
     float* const C = Cp + static_cast<int64_t>(blockIdx.y) * c_split;
     const int S = K >> 6;
@@ -339,61 +332,8 @@ __global__ __launch_bounds__(kPThreads) void k_gemm_pipe(const uint16_t* __restr
                 rs, (__attribute__((address_space(3))) void*)(dst + (4 * wave + i) * 1024), 16,
                 static_cast<int>(coff[i]), 0, 0, 0);
     };
-    const uint8_t* const Wb16 = static_cast<const uint8_t*>(Wp) + static_cast<int64_t>(n0) * rowA + 2 * k0;
+    const uint8_t* const Wb16 = reinterpret_cast<const uint8_t*>(Wp) + static_cast<int64_t>(n0) * rowA + 2 * k0;
     const int64_t Wleft16 = static_cast<int64_t>(N - n0) * rowA - 2 * k0;
-
-    // Q4_K: the raw bytes of a step (per tile row: the super-block header
-    // and the step's 32-byte qs chunk) are copied straight into a raw ring
-    // of kStages LDS stages (kRawStage bytes each): wave w copies rows
-    // 32w .. 32w+31, one instruction for their headers (lanes 0-31; lanes
-    // 32-63 read past the resource and load nothing) and one for their qs
-    // (lane l: row 32w + l/2, half l%2).  Dequantized one step ahead by
-    // thread (row sr, half sh) into one of two bf16 LDS tiles.
-    const int nb = K >> 8;
-    const int64_t rbq = static_cast<int64_t>(nb) * kQ4kBlockBytes;
-    const uint8_t* const Wq = static_cast<const uint8_t*>(Wp) + static_cast<int64_t>(n0) * rbq;
-    const int64_t Wleftq = static_cast<int64_t>(N - n0) * rbq;
-    const uint32_t hoff = lane < 32 ? static_cast<uint32_t>((32 * wave + lane) * rbq) : 0x7fffffffu;
-    const uint32_t qoff = static_cast<uint32_t>((32 * wave + (lane >> 1)) * rbq) + 16u + 16u * (lane & 1);
-    auto copy_q4k = [&](uint8_t* raw, int step) {
-        const int b = step >> 2, c = step & 3;
-        const int64_t o = static_cast<int64_t>(b) * kQ4kBlockBytes;
-        const BufRsrc rs = make_rsrc(Wq + o, step < S ? Wleftq - o : 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rs, (__attribute__((address_space(3))) void*)(raw + wave * 1024), 16, static_cast<int>(hoff), 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rs, (__attribute__((address_space(3))) void*)(raw + 4096 + wave * 1024), 16,
-            static_cast<int>(qoff + 32u * static_cast<uint32_t>(c)), 0, 0, 0);
-    };
-    // Values k0 + 16 sh .. +15 (low nibbles, sub-block 2c) and k0 + 32 + 16 sh
-    // .. +15 (high nibbles, sub-block 2c + 1) of row sr: chunks 2 sh, 2 sh + 1,
-    // 4 + 2 sh, 5 + 2 sh of the tile row.
-    const int sr = tid >> 1, sh = tid & 1;
-    auto dequant = [&](const uint8_t* raw, uint8_t* dst, int step) {
-        const int c = step & 3;
-        const u32x4 h = *reinterpret_cast<const u32x4*>(raw + (sr >> 5) * 1024 + (sr & 31) * 16);
-        const u32x4 qv = *reinterpret_cast<const u32x4*>(raw + 4096 + sr * 32 + sh * 16);
-        const float d = f16_bits_to_f32(h[0] & 0xffffu), dm = f16_bits_to_f32(h[0] >> 16);
-        uint32_t sv1, mv1, sv2, mv2;
-        decode_scale_min(make_scale_sel(2 * c), h[1], h[2], h[3], sv1, mv1);
-        decode_scale_min(make_scale_sel(2 * c + 1), h[1], h[2], h[3], sv2, mv2);
-        const float s1 = d * static_cast<float>(sv1), n1 = dm * static_cast<float>(mv1);
-        const float s2 = d * static_cast<float>(sv2), n2 = dm * static_cast<float>(mv2);
-        u32x4 lo[2], hi[2];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t wl = qv[j] & 0x0f0f0f0fu, wh = (qv[j] >> 4) & 0x0f0f0f0fu;
-            lo[j >> 1][2 * (j & 1)] = pk_bf16(s1 * ubyte_f32(wl, 0) - n1, s1 * ubyte_f32(wl, 1) - n1);
-            lo[j >> 1][2 * (j & 1) + 1] = pk_bf16(s1 * ubyte_f32(wl, 2) - n1, s1 * ubyte_f32(wl, 3) - n1);
-            hi[j >> 1][2 * (j & 1)] = pk_bf16(s2 * ubyte_f32(wh, 0) - n2, s2 * ubyte_f32(wh, 1) - n2);
-            hi[j >> 1][2 * (j & 1) + 1] = pk_bf16(s2 * ubyte_f32(wh, 2) - n2, s2 * ubyte_f32(wh, 3) - n2);
-        }
-        *reinterpret_cast<u32x4*>(dst + swz(sr, 2 * sh)) = lo[0];
-        *reinterpret_cast<u32x4*>(dst + swz(sr, 2 * sh + 1)) = lo[1];
-        *reinterpret_cast<u32x4*>(dst + swz(sr, 4 + 2 * sh)) = hi[0];
-        *reinterpret_cast<u32x4*>(dst + swz(sr, 5 + 2 * sh)) = hi[1];
-    };
-    uint8_t* const sRaw = sW + 2 * kTile;  // Q4_K: [kStages][kRawStage]
 
     f32x4 acc[4][4];
 #pragma unroll
@@ -419,50 +359,30 @@ __global__ __launch_bounds__(kPThreads) void k_gemm_pipe(const uint16_t* __restr
         }
     };
 
-    // Prologue: copies of steps 0 .. kStages-2; step 0's W dequantized.
+    // Prologue: copies of steps 0 .. kStages-2.
 #pragma unroll
     for (int j = 0; j < kStages - 1; ++j) {
-        if constexpr (W_Q4K) {
-            copy_q4k(sRaw + j * kRawStage, j);
-            copy_tile(sA + j * kTile, Ab, Aleft, j);
-        } else {
-            copy_tile(sA + j * kTile, Ab, Aleft, j);
-            copy_tile(sW + j * kTile, Wb16, Wleft16, j);
-        }
+        copy_tile(sA + j * kTile, Ab, Aleft, j);
+        copy_tile(sW + j * kTile, Wb16, Wleft16, j);
     }
     wait_vm<0>();
     lds_sync();
-    if constexpr (W_Q4K) {
-        dequant(sRaw, sW, 0);
-        lds_sync();
-    }
 
-    // Step s: copy step t = s+kStages-1 (Q4_K: raw W, then A; bf16: A, then
-    // W); (Q4_K) dequantize step s+1 into the other bf16 W tile; MFMAs of
-    // step s; wait for this wave's copies that step s+1 needs, then the
-    // barrier.  Copies are ordered and counted by vmcnt: after the last one
-    // step s+1 needs (Q4_K: raw W of step s+2, for its dequant; bf16: W of
-    // s+1) this wave has issued 10 (Q4_K: A(s+2), raw(s+3), A(s+3)) or 16
-    // (bf16: A, W of s+2 and s+3) more.  kStages == 4 and S % 4 == 0: the
-    // unrolled round keeps every ring index a compile-time constant.
+    // Step s: copy step t = s+kStages-1 (A, then W); MFMAs of step s; wait
+    // for this wave's copies that step s+1 needs, then the barrier.  Copies
+    // are ordered and counted by vmcnt: after W of step s+1 this wave has
+    // issued 16 more (A, W of s+2 and s+3).  kStages == 4 and S % 4 == 0:
+    // the unrolled round keeps every ring index a compile-time constant.
     static_assert(kStages == 4, "the unrolled round assumes a 4-stage ring");
     for (int s0 = 0; s0 < S; s0 += 4) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int s = s0 + j;
             const int t = (j + kStages - 1) % kStages;
-            if constexpr (W_Q4K) {
-                copy_q4k(sRaw + t * kRawStage, s + kStages - 1);
-                copy_tile(sA + t * kTile, Ab, Aleft, s + kStages - 1);
-                dequant(sRaw + ((j + 1) % kStages) * kRawStage, sW + ((j + 1) & 1) * kTile, s + 1);
-                mfma_step(sA + j * kTile, sW + (j & 1) * kTile);
-                wait_vm<10>();
-            } else {
-                copy_tile(sA + t * kTile, Ab, Aleft, s + kStages - 1);
-                copy_tile(sW + t * kTile, Wb16, Wleft16, s + kStages - 1);
-                mfma_step(sA + j * kTile, sW + j * kTile);
-                wait_vm<16>();
-            }
+            copy_tile(sA + t * kTile, Ab, Aleft, s + kStages - 1);
+            copy_tile(sW + t * kTile, Wb16, Wleft16, s + kStages - 1);
+            mfma_step(sA + j * kTile, sW + j * kTile);
+            wait_vm<16>();
             lds_sync();
         }
     }
@@ -474,6 +394,190 @@ __global__ __launch_bounds__(kPThreads) void k_gemm_pipe(const uint16_t* __restr
     __syncthreads();
     store_tile_staged<4>(acc, reinterpret_cast<float*>(lds + wave * kEpiWaveBytes), C, M, N, m0 + wm, n0 + wn, bias,
                          lane);
+}
+
+// Q4_K W over several M tiles, warp-specialized (128 x 128 tiles, 8 waves).
+//  * Waves 0-3 compute: the four 64 x 64 MFMA tiles of k_gemm_pipe with the
+//    same fragment reads and MFMA order, so the result is bit-identical to
+//    dequantizing W and converting A once and running k_gemm_pipe.
+//  * Waves 4-7 produce: every K step's W tile is dequantized straight from
+//    the Q4_K bytes in HBM (w = (d*sv)*q - dmin*mv, exact in f32, then
+//    round-to-nearest-even bf16, as the reference's flux_dequant_q4k,
+//    shaders/flux.msl:69-81) and its A tile converted from f32 (RNE) or
+//    copied as bf16, into a two-stage LDS ring.  Their global loads run
+//    kWsAhead steps ahead in registers.  Thread p of the producers owns row
+//    p / 2 of both tiles, half p % 2 of the step's 64 values.
+//  * One barrier per step: in round j the compute waves read stage j % 2
+//    while the producers fill stage (j + 1) % 2 with step j + 1.
+//  * Rows past M or N and steps past the slice read zeros (buffer range);
+//    split-K slices start on super-block boundaries.
+// Replaces the dequantize-into-HBM pre-pass for several M tiles: no weight
+// copy, no extra launch; the dequantization of a W tile repeats per M tile,
+// in waves of its own beside the MFMA waves.
+constexpr int kWsThreads = 512;
+constexpr int kWsAhead = 3;  // steps loaded ahead; kWsAhead + 1 register slots
+constexpr size_t kWsLds = 4 * kEpiWaveBytes > 4 * kTile ? 4 * kEpiWaveBytes : 4 * kTile;
+
+template <bool A_F32>
+__global__ __launch_bounds__(kWsThreads) void k_gemm_ws(const void* __restrict__ Ap, const uint8_t* __restrict__ Wq,
+                                                        const float* __restrict__ bias, float* __restrict__ Cp,
+                                                        int M, int N, int K, int mt, int ldk, int64_t c_split) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    uint8_t* const stA = lds;              // [2][kTile]
+    uint8_t* const stW = lds + 2 * kTile;  // [2][kTile]
+
+    const int G = static_cast<int>(gridDim.x), bid = static_cast<int>(blockIdx.x);
+    const int xcd = bid & 7, idx = bid >> 3, q8 = G >> 3, r8 = G & 7;
+    const int tile = xcd < r8 ? xcd * (q8 + 1) + idx : r8 * (q8 + 1) + (xcd - r8) * q8 + idx;
+    const int nt = G / mt;
+    const int group = tile / (kGroupM * nt), first_m = group * kGroupM;
+    const int gm = min(mt - first_m, kGroupM);
+    const int m0 = (first_m + (tile % (kGroupM * nt)) % gm) * 128;
+    const int n0 = ((tile % (kGroupM * nt)) / gm) * 128;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int k0 = static_cast<int>(blockIdx.y) * K;  // split-K slice: columns [k0, k0 + K) of rows of ldk
+    float* const C = Cp + static_cast<int64_t>(blockIdx.y) * c_split;
+    const int S = K >> 6;
+
+    if (wave < 4) {
+        const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+        const int fr = lane & 15, fc = lane >> 4;
+        f32x4 acc[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        lds_sync();  // round -1: the producers fill stage 0
+        for (int s0 = 0; s0 < S; s0 += 2) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const uint8_t* ta = stA + u * kTile;
+                const uint8_t* tw = stW + u * kTile;
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    bf16x8 af[4], bf[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        af[i] = *reinterpret_cast<const bf16x8*>(ta + swz(wm + 16 * i + fr, 4 * ks + fc));
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        bf[j] = *reinterpret_cast<const bf16x8*>(tw + swz(wn + 16 * j + fr, 4 * ks + fc));
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                }
+                lds_sync();
+            }
+        }
+        // After the last round's barrier no wave touches the ring again.
+        store_tile_staged<4>(acc, reinterpret_cast<float*>(lds + wave * kEpiWaveBytes), C, M, N, m0 + wm, n0 + wn,
+                             bias, lane);
+        return;
+    }
+
+    // ---- producers ----
+    // W: thread p dequantizes row p / 2, half p % 2 of the step (the two
+    // lanes of a row read its 32 contiguous qs bytes).  A: load i of thread p
+    // is row 16 i + p / 16, values 4 (p % 16) .. +3 of the step (f32; bf16:
+    // 8 rows per load, 8 values) -- whole 256-byte row pieces per 16 lanes.
+    const int p = tid - 4 * kWave;
+    const int r = p >> 1, h = p & 1;
+    const int nbk = ldk >> 8;
+    const uint32_t rbq = static_cast<uint32_t>(nbk * kQ4kBlockBytes);
+    const uint8_t* const wbase = Wq + static_cast<int64_t>(n0) * rbq + static_cast<int64_t>(k0 >> 8) * kQ4kBlockBytes;
+    const BufRsrc rw = make_rsrc(wbase, static_cast<int64_t>(N - n0) * rbq - static_cast<int64_t>(k0 >> 8) * kQ4kBlockBytes);
+    constexpr int kAEl = A_F32 ? 4 : 2;
+    const int64_t arow = static_cast<int64_t>(ldk) * kAEl;
+    const uint8_t* const abase = static_cast<const uint8_t*>(Ap) + static_cast<int64_t>(m0) * arow +
+                                 static_cast<int64_t>(k0) * kAEl;
+    const BufRsrc ra = make_rsrc(abase, static_cast<int64_t>(M - m0) * arow - static_cast<int64_t>(k0) * kAEl);
+    const uint32_t wro = static_cast<uint32_t>(r) * rbq;
+    constexpr int kAL = A_F32 ? 8 : 4;     // 16-byte A loads per thread and step
+    constexpr int kRowsPerLoad = 256 / (A_F32 ? 16 : 8);  // rows one load instruction of all producers covers
+    const int alane = A_F32 ? (p & 15) : (p & 7);          // 16-byte piece of the row's step
+    const int arow0 = A_F32 ? (p >> 4) : (p >> 3);
+    const uint32_t aro = static_cast<uint32_t>(static_cast<int64_t>(arow0) * arow) + static_cast<uint32_t>(alane) * 16u;
+    const uint32_t a_load_stride = static_cast<uint32_t>(static_cast<int64_t>(kRowsPerLoad) * arow);
+    struct Slot {
+        u32x4 hdr, qs;
+        u32x4 a[kAL];
+    };
+    Slot slot[kWsAhead + 1];
+    // Steps past the slice load nothing (an offset past the resource reads
+    // zeros).
+    auto issue = [&](Slot& sl, int t) {
+        const uint32_t bo = wro + static_cast<uint32_t>(t >> 2) * kQ4kBlockBytes;
+        sl.hdr = ld16(rw, t < S ? bo : 0xfffffff0u);
+        sl.qs = ld16(rw, t < S ? bo + 16u + 32u * static_cast<uint32_t>(t & 3) + 16u * static_cast<uint32_t>(h)
+                               : 0xfffffff0u);
+        const uint32_t ao = aro + static_cast<uint32_t>(t) * 64u * kAEl;
+#pragma unroll
+        for (int i = 0; i < kAL; ++i)
+            sl.a[i] = ld16(ra, t < S ? ao + a_load_stride * static_cast<uint32_t>(i) : 0xfffffff0u);
+    };
+    auto produce = [&](const Slot& sl, int t, int stage) {
+        const int c = t & 3;
+        uint8_t* const tw = stW + stage * kTile;
+        uint8_t* const ta = stA + stage * kTile;
+        const float d = f16_bits_to_f32(sl.hdr[0] & 0xffffu), dm = f16_bits_to_f32(sl.hdr[0] >> 16);
+        uint32_t sv1, mv1, sv2, mv2;
+        decode_scale_min(make_scale_sel(2 * c), sl.hdr[1], sl.hdr[2], sl.hdr[3], sv1, mv1);
+        decode_scale_min(make_scale_sel(2 * c + 1), sl.hdr[1], sl.hdr[2], sl.hdr[3], sv2, mv2);
+        const float s1 = d * static_cast<float>(sv1), n1 = dm * static_cast<float>(mv1);
+        const float s2 = d * static_cast<float>(sv2), n2 = dm * static_cast<float>(mv2);
+        u32x4 lo[2], hi[2];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t wl = sl.qs[j] & 0x0f0f0f0fu, wh = (sl.qs[j] >> 4) & 0x0f0f0f0fu;
+            lo[j >> 1][2 * (j & 1)] = pk_bf16(s1 * ubyte_f32(wl, 0) - n1, s1 * ubyte_f32(wl, 1) - n1);
+            lo[j >> 1][2 * (j & 1) + 1] = pk_bf16(s1 * ubyte_f32(wl, 2) - n1, s1 * ubyte_f32(wl, 3) - n1);
+            hi[j >> 1][2 * (j & 1)] = pk_bf16(s2 * ubyte_f32(wh, 0) - n2, s2 * ubyte_f32(wh, 1) - n2);
+            hi[j >> 1][2 * (j & 1) + 1] = pk_bf16(s2 * ubyte_f32(wh, 2) - n2, s2 * ubyte_f32(wh, 3) - n2);
+        }
+        *reinterpret_cast<u32x4*>(tw + swz(r, 2 * h)) = lo[0];
+        *reinterpret_cast<u32x4*>(tw + swz(r, 2 * h + 1)) = lo[1];
+        *reinterpret_cast<u32x4*>(tw + swz(r, 4 + 2 * h)) = hi[0];
+        *reinterpret_cast<u32x4*>(tw + swz(r, 5 + 2 * h)) = hi[1];
+#pragma unroll
+        for (int i = 0; i < kAL; ++i) {
+            const int ar = arow0 + kRowsPerLoad * i;
+            if constexpr (A_F32) {
+                // 4 values -> 8 bytes: half (alane % 2) of 16-byte chunk alane / 2
+                const f32x4 x = __builtin_bit_cast(f32x4, sl.a[i]);
+                *reinterpret_cast<u32x2*>(ta + swz(ar, alane >> 1) + 8 * (alane & 1)) =
+                    u32x2{bf16_pair(x[0], x[1]), bf16_pair(x[2], x[3])};
+            } else {
+                *reinterpret_cast<u32x4*>(ta + swz(ar, alane)) = sl.a[i];
+            }
+        }
+    };
+    constexpr int kL = 2 + kAL;  // loads per step (vmcnt)
+    static_assert(kWsAhead == 3 && kWsAhead * kL < 64, "the unrolled round assumes four slots");
+#pragma unroll
+    for (int t = 0; t <= kWsAhead; ++t) {
+        issue(slot[t], t);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    wait_vm<kWsAhead * kL>();
+    produce(slot[0], 0, 0);
+    lds_sync();  // round -1
+    // Round j (S % 4 == 0): refill slot j % 4 (step j freed it) with step
+    // j + 4, wait for step j + 1 (three steps' loads may still run),
+    // produce it into stage (j + 1) % 2.
+    for (int s0 = 0; s0 < S; s0 += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            issue(slot[u], s0 + u + kWsAhead + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vm<kWsAhead * kL>();
+            produce(slot[(u + 1) & 3], s0 + u + 1, (u + 1) & 1);
+            lds_sync();
+        }
+    }
 }
 
 // Large-tile bf16 GEMM (both operands bf16 in HBM): C = A * W^T (+ bias).
@@ -666,10 +770,10 @@ namespace {
 
 // How one GEMM call runs (shared by the launcher and the workspace query).
 struct GemmPlan {
-    bool pipe = false;       // pipelined bf16-MFMA kernels (k % 256 == 0, Q4_K or BF16 W)
-    bool fused_q4k = false;  // one M tile: Q4_K dequantized into LDS inside the GEMM
-    bool big = false;        // 256 x 256 kernel
-    int splits = 1;          // split-K slices of the 128 x 128 kernel
+    bool pipe = false;  // pipelined MFMA kernels (k % 256 == 0, Q4_K or BF16 W)
+    bool big = false;   // 256 x 256 bf16 kernel
+    bool ws = false;    // Q4_K W dequantized inside the GEMM by producer waves (k_gemm_ws)
+    int splits = 1;     // split-K slices of the 128 x 128 kernels
     int64_t mt = 0, nt = 0, mt2 = 0, nt2 = 0;
     size_t a_bytes = 0, w_bytes = 0, p_bytes = 0;
 };
@@ -678,31 +782,36 @@ GemmPlan plan_gemm(int w_fmt, bool a_bf16, int64_t m, int64_t n, int64_t k) {
     GemmPlan p;
     p.pipe = k % 256 == 0 && (w_fmt == RT_HIP_Q4K || w_fmt == RT_HIP_BF16);
     if (!p.pipe) return p;
-    // Pipelined kernel on bf16 A (f32 A converted once into the workspace).
-    // A Q4_K weight used by more than one M tile is dequantized once into the
-    // workspace (bf16, round-to-nearest-even of the exact f32 value, as the
-    // fused path and the reference's flux_dequant_q4k) instead of once per M
-    // tile inside the GEMM.
+    // A Q4_K weight is dequantized (bf16, round-to-nearest-even of the exact
+    // f32 value, as the reference's flux_dequant_q4k) either inside the GEMM
+    // by producer waves, once per 128-row M tile, or once per call into the
+    // workspace ahead of the bf16 kernels.  Measured on the Llama-3.2-3B
+    // shapes: inside wins up to two M tiles (32 rows: 19 against 47 us for
+    // gate, 33 against 113 us for down; 256 rows: 36 against 42 us), the
+    // workspace from three on (512 rows: 50 against 52 us).  f32 A is
+    // converted to bf16 inside k_gemm_ws, else once into the workspace.
     p.mt = (m + 127) / 128;
     p.nt = (n + 127) / 128;
-    p.fused_q4k = w_fmt == RT_HIP_Q4K && p.mt <= tune_param("GEMM_FUSED_MT", 1);
     const int64_t cus = device_info().cus;
     p.mt2 = (m + 255) / 256;
     p.nt2 = (n + 255) / 256;
-    p.big = !p.fused_q4k && 4 * p.mt2 * p.nt2 >= 3 * cus && tune_param("GEMM_BIG", 1);
-    // Split-K for the 128 x 128 bf16 kernel when its tiles leave at least
-    // half the CUs idle: up to 4 slices of K, each a multiple of 64, summed
-    // afterwards in a fixed order (deterministic).
-    if (!p.fused_q4k && !p.big && 2 * p.mt * p.nt <= cus && n % 4 == 0) {
+    p.big = 4 * p.mt2 * p.nt2 >= 3 * cus && tune_param("GEMM_BIG", 1);
+    p.ws = w_fmt == RT_HIP_Q4K && !p.big && p.mt <= tune_param("GEMM_WS_MT", 2);
+    // Split-K for the 128 x 128 kernels when their tiles leave at least half
+    // the CUs idle: up to 4 slices of K (8 for k_gemm_ws), summed afterwards
+    // in a fixed order (deterministic).  Slices are multiples of 64 values
+    // (256 for k_gemm_ws, whose slices start on super-blocks).
+    if (!p.big && 2 * p.mt * p.nt <= cus && n % 4 == 0) {
+        const int cap = p.ws ? 8 : 4, unit = p.ws ? 256 : 64;
         int splits = static_cast<int>(cus / (p.mt * p.nt));
-        splits = splits > 4 ? 4 : splits;
-        while (splits > 1 && k % (64 * splits) != 0) --splits;
+        splits = splits > cap ? cap : splits;
+        while (splits > 1 && k % (unit * splits) != 0) --splits;
         const int forced = tune_param("GEMM_SPLITK", 0);
-        if (forced >= 1 && forced <= 4 && k % (64 * forced) == 0) splits = forced;
+        if (forced >= 1 && forced <= cap && k % (unit * forced) == 0) splits = forced;
         p.splits = splits;
     }
-    p.a_bytes = a_bf16 ? 0 : static_cast<size_t>(m * k) * 2;
-    p.w_bytes = (w_fmt == RT_HIP_Q4K && !p.fused_q4k) ? static_cast<size_t>(n * k) * 2 : 0;
+    p.a_bytes = a_bf16 || p.ws ? 0 : static_cast<size_t>(m * k) * 2;
+    p.w_bytes = w_fmt == RT_HIP_Q4K && !p.ws ? static_cast<size_t>(n * k) * 2 : 0;
     p.p_bytes = p.splits > 1 ? static_cast<size_t>(p.splits) * m * n * 4 : 0;
     return p;
 }
@@ -720,7 +829,7 @@ hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, con
     const GemmPlan P = plan_gemm(w_fmt, a_bf16, m, n, k);
     if (P.pipe) {
         const int64_t mt = P.mt, nt = P.nt, mt2 = P.mt2, nt2 = P.nt2;
-        const bool fused_q4k = P.fused_q4k, big = P.big;
+        const bool big = P.big;
         const int splits = P.splits;
         const size_t a_bytes = P.a_bytes, w_bytes = P.w_bytes, p_bytes = P.p_bytes;
         uint8_t* ws = nullptr;
@@ -728,6 +837,29 @@ hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, con
             hipError_t e;
             ws = static_cast<uint8_t*>(workspace(a_bytes + w_bytes + p_bytes, s, &e));
             if (!ws) return e;
+        }
+        if (P.ws) {
+            // Both roles of k_gemm_ws run the same number of barriers only if
+            // each slice is whole super-blocks (S % 4 == 0).
+            if ((k / splits) % 256 != 0) return hipErrorInvalidValue;
+            const int im = static_cast<int>(m), in = static_cast<int>(n), ik = static_cast<int>(k);
+            const dim3 g(static_cast<unsigned>(mt * nt), static_cast<unsigned>(splits)), b(kWsThreads);
+            const auto* wq = static_cast<const uint8_t*>(w);
+            float* out = splits > 1 ? reinterpret_cast<float*>(ws) : c;
+            const float* bs = splits > 1 ? nullptr : bias;
+            const int64_t cs = splits > 1 ? m * n : 0;
+            if (a_bf16)
+                hipLaunchKernelGGL((k_gemm_ws<false>), g, b, kWsLds, s, a, wq, bs, out, im, in, ik / splits,
+                                   static_cast<int>(mt), ik, cs);
+            else
+                hipLaunchKernelGGL((k_gemm_ws<true>), g, b, kWsLds, s, a, wq, bs, out, im, in, ik / splits,
+                                   static_cast<int>(mt), ik, cs);
+            if (splits > 1) {
+                const int64_t mn = m * n;
+                hipLaunchKernelGGL(k_splitk_sum, dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0, s,
+                                   reinterpret_cast<const float*>(ws), splits, bias, c, mn, n);
+            }
+            return hipGetLastError();
         }
         const uint16_t* a16 = static_cast<const uint16_t*>(a);
         if (!a_bf16 && w_bytes) {
@@ -749,7 +881,6 @@ hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, con
             if (e != hipSuccess) return e;
             w = ws + a_bytes;
         }
-        const bool q4k = fused_q4k;
         // Large outputs: the 256 x 256 kernel when its tiles cover at least
         // three quarters of the CUs (k % 64 == 0 always holds here).
         if (big) {
@@ -761,21 +892,18 @@ hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, con
                                in, ik, imt);
             return hipGetLastError();
         }
-        const size_t lds = q4k ? static_cast<size_t>(kStages + 2) * kTile + kStages * kRawStage
-                               : static_cast<size_t>(2 * kStages) * kTile;
+        const size_t lds = static_cast<size_t>(2 * kStages) * kTile;
         const int im = static_cast<int>(m), in = static_cast<int>(n), ik = static_cast<int>(k);
         const dim3 g(static_cast<unsigned>(mt * nt)), b(kPThreads);
-        if (q4k) {
-            hipLaunchKernelGGL((k_gemm_pipe<true>), g, b, lds, s, a16, w, bias, c, im, in, ik,
-                               static_cast<int>(mt), ik, int64_t{0});
-        } else if (splits == 1) {
-            hipLaunchKernelGGL((k_gemm_pipe<false>), g, b, lds, s, a16, w, bias, c, im, in, ik,
-                               static_cast<int>(mt), ik, int64_t{0});
+        const uint16_t* w16 = static_cast<const uint16_t*>(w);
+        if (splits == 1) {
+            hipLaunchKernelGGL(k_gemm_pipe, g, b, lds, s, a16, w16, bias, c, im, in, ik, static_cast<int>(mt), ik,
+                               int64_t{0});
         } else {
             float* parts = reinterpret_cast<float*>(ws + a_bytes + w_bytes);
             const int64_t mn = m * n;
-            hipLaunchKernelGGL((k_gemm_pipe<false>), dim3(g.x, static_cast<unsigned>(splits)), b, lds, s, a16, w,
-                               nullptr, parts, im, in, ik / splits, static_cast<int>(mt), ik, mn);
+            hipLaunchKernelGGL(k_gemm_pipe, dim3(g.x, static_cast<unsigned>(splits)), b, lds, s, a16, w16, nullptr,
+                               parts, im, in, ik / splits, static_cast<int>(mt), ik, mn);
             hipLaunchKernelGGL(k_splitk_sum, dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0, s,
                                parts, splits, bias, c, mn, n);
         }

@@ -24,6 +24,8 @@ CASES = [
     (513, 260, 1024, False),
     (9, 64, 256, False),
     (4100, 4000, 512, True),   # enough 256 x 256 tiles for the large-tile kernel, ragged edges
+    (32, 3072, 8192, False),   # one M tile: W dequantized by producer waves, K split 8 ways
+    (96, 3072, 3072, True),    # K split 6 ways, bf16 A
 ]
 
 
@@ -116,3 +118,29 @@ def test_gemm_large_tile_partial_round(rt, m, n, k):
     say(f"[gemm large tile] {m}x{n}x{k} normwise {err:.2e}")
     assert err <= 4e-5
     assert torch.equal(c1.view(torch.int32), c2.view(torch.int32))
+
+
+@pytest.mark.parametrize("m,n,k,a_bf16", [(256, 8192, 3072, False), (200, 1000, 1024, True),
+                                         (160, 3072, 8192, False), (512, 3072, 8192, False)])
+def test_gemm_q4k_bit_identical_to_bf16_path(rt, m, n, k, a_bf16):
+    """Up to two 128-row M tiles, a Q4_K weight is dequantized inside the
+    GEMM by producer waves (w = (d*sv)*q - dmin*mv, RNE bf16) beside the
+    MFMA waves; from three on, once into the workspace.  Either way, with
+    the same K split, every output equals, bit for bit, the bf16 GEMM on the
+    dequantized weight (the same MFMA order), bias included: gate and down
+    shapes at 160, 200 and 256 rows (the in-GEMM path, K split 2 and 4,
+    ragged M and N, bf16 A) and config 4's down (the workspace path)."""
+    import torch
+    say(f"[gemm q4k vs bf16 path] M={m} N={n} K={k} a_bf16={a_bf16}")
+    g = torch.Generator(device="cuda").manual_seed(m + n + k)
+    blocks = rt.quantize_q4k(torch.randn((n, k), generator=g, device="cuda") * 0.02)
+    wbf = rt.dequant_q4k(blocks, n, k, bf16=True)
+    a = torch.randn((m, k), generator=g, device="cuda")
+    if a_bf16:
+        a = a.bfloat16()
+    bias = torch.randn(n, generator=g, device="cuda")
+    c1 = rt.gemm(rt.Q4K, a, blocks, n, k, bias=bias)
+    c2 = rt.gemm(rt.BF16, a, wbf, n, k, bias=bias)
+    assert torch.equal(c1.view(torch.int32), c2.view(torch.int32))
+    c3 = rt.gemm(rt.Q4K, a, blocks, n, k, bias=bias)
+    assert torch.equal(c1.view(torch.int32), c3.view(torch.int32))
