@@ -418,10 +418,11 @@ constexpr int kWsThreads = 512;
 constexpr int kWsAhead = 3;  // steps loaded ahead; kWsAhead + 1 register slots
 constexpr size_t kWsLds = 4 * kEpiWaveBytes > 4 * kTile ? 4 * kEpiWaveBytes : 4 * kTile;
 
-template <bool A_F32>
+template <int WF, bool A_F32>
 __global__ __launch_bounds__(kWsThreads) void k_gemm_ws(const void* __restrict__ Ap, const uint8_t* __restrict__ Wq,
                                                         const float* __restrict__ bias, float* __restrict__ Cp,
-                                                        int M, int N, int K, int mt, int ldk, int64_t c_split) {
+                                                        int M, int N, int K, int mt, int ldk, int64_t c_split,
+                                                        int64_t sc_off) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     uint8_t* const stA = lds;              // [2][kTile]
     uint8_t* const stW = lds + 2 * kTile;  // [2][kTile]
@@ -480,68 +481,155 @@ __global__ __launch_bounds__(kWsThreads) void k_gemm_ws(const void* __restrict__
     }
 
     // ---- producers ----
-    // W: thread p dequantizes row p / 2, half p % 2 of the step (the two
-    // lanes of a row read its 32 contiguous qs bytes).  A: load i of thread p
-    // is row 16 i + p / 16, values 4 (p % 16) .. +3 of the step (f32; bf16:
-    // 8 rows per load, 8 values) -- whole 256-byte row pieces per 16 lanes.
+    // W: thread p decodes row p / 2, half p % 2 of the step.  A: load i of
+    // thread p is row 16 i + p / 16, values 4 (p % 16) .. +3 of the step
+    // (f32; bf16: 8 rows per load, 8 values) -- whole 256-byte row pieces per
+    // 16 lanes.
     const int p = tid - 4 * kWave;
     const int r = p >> 1, h = p & 1;
-    const int nbk = ldk >> 8;
-    const uint32_t rbq = static_cast<uint32_t>(nbk * kQ4kBlockBytes);
-    const uint8_t* const wbase = Wq + static_cast<int64_t>(n0) * rbq + static_cast<int64_t>(k0 >> 8) * kQ4kBlockBytes;
-    const BufRsrc rw = make_rsrc(wbase, static_cast<int64_t>(N - n0) * rbq - static_cast<int64_t>(k0 >> 8) * kQ4kBlockBytes);
+    // W bytes per row and at the slice's first column, and this thread's
+    // row offset, by format:
+    //   Q4_K  144-byte super-blocks of 256 values;
+    //   Q4Mat packed nibbles (two values per byte), then f32 scales per 32
+    //         flat values at sc_off;
+    //   Q4_0  18-byte GGUF blocks of 32 values (rows of K % 256 == 0 values
+    //         start 16-byte aligned; block 2t + h starts 0 or 2 mod 4).
+    const int64_t wrow = WF == RT_HIP_Q4K ? static_cast<int64_t>(ldk >> 8) * kQ4kBlockBytes
+                       : WF == RT_HIP_Q4MAT ? static_cast<int64_t>(ldk >> 1)
+                                            : static_cast<int64_t>(ldk >> 5) * kQ40BlockBytes;
+    const int64_t wk0 = WF == RT_HIP_Q4K ? static_cast<int64_t>(k0 >> 8) * kQ4kBlockBytes
+                      : WF == RT_HIP_Q4MAT ? static_cast<int64_t>(k0 >> 1)
+                                           : static_cast<int64_t>(k0 >> 5) * kQ40BlockBytes;
+    const uint8_t* const wbase = Wq + static_cast<int64_t>(n0) * wrow + wk0;
+    const BufRsrc rw = make_rsrc(wbase, static_cast<int64_t>(N - n0) * wrow - wk0);
+    // Q4Mat scales: one f32 per 32 values, rows of ldk / 32
+    const int64_t srow = static_cast<int64_t>(ldk >> 5) * 4;
+    const uint8_t* const sbase = Wq + sc_off + static_cast<int64_t>(n0) * srow + static_cast<int64_t>(k0 >> 5) * 4;
+    const BufRsrc rs = make_rsrc(sbase, WF == RT_HIP_Q4MAT ? static_cast<int64_t>(N - n0) * srow - (k0 >> 5) * 4 : 0);
     constexpr int kAEl = A_F32 ? 4 : 2;
     const int64_t arow = static_cast<int64_t>(ldk) * kAEl;
     const uint8_t* const abase = static_cast<const uint8_t*>(Ap) + static_cast<int64_t>(m0) * arow +
                                  static_cast<int64_t>(k0) * kAEl;
     const BufRsrc ra = make_rsrc(abase, static_cast<int64_t>(M - m0) * arow - static_cast<int64_t>(k0) * kAEl);
-    const uint32_t wro = static_cast<uint32_t>(r) * rbq;
+    const uint32_t wro = static_cast<uint32_t>(static_cast<int64_t>(r) * wrow);
+    const uint32_t sro = static_cast<uint32_t>(static_cast<int64_t>(r) * srow);
     constexpr int kAL = A_F32 ? 8 : 4;     // 16-byte A loads per thread and step
     constexpr int kRowsPerLoad = 256 / (A_F32 ? 16 : 8);  // rows one load instruction of all producers covers
     const int alane = A_F32 ? (p & 15) : (p & 7);          // 16-byte piece of the row's step
     const int arow0 = A_F32 ? (p >> 4) : (p >> 3);
     const uint32_t aro = static_cast<uint32_t>(static_cast<int64_t>(arow0) * arow) + static_cast<uint32_t>(alane) * 16u;
     const uint32_t a_load_stride = static_cast<uint32_t>(static_cast<int64_t>(kRowsPerLoad) * arow);
+    // W registers of a step: Q4_K header and qs; Q4Mat packed bytes and the
+    // scale (w1[0]); Q4_0 the five dwords covering the block.
     struct Slot {
-        u32x4 hdr, qs;
+        u32x4 w0;
+        uint32_t w1[4];
         u32x4 a[kAL];
     };
     Slot slot[kWsAhead + 1];
     // Steps past the slice load nothing (an offset past the resource reads
     // zeros).
     auto issue = [&](Slot& sl, int t) {
-        const uint32_t bo = wro + static_cast<uint32_t>(t >> 2) * kQ4kBlockBytes;
-        sl.hdr = ld16(rw, t < S ? bo : 0xfffffff0u);
-        sl.qs = ld16(rw, t < S ? bo + 16u + 32u * static_cast<uint32_t>(t & 3) + 16u * static_cast<uint32_t>(h)
-                               : 0xfffffff0u);
+        const bool in = t < S;
+        if constexpr (WF == RT_HIP_Q4K) {
+            const uint32_t bo = wro + static_cast<uint32_t>(t >> 2) * kQ4kBlockBytes;
+            sl.w0 = ld16(rw, in ? bo : 0xfffffff0u);
+            const u32x4 q = ld16(rw, in ? bo + 16u + 32u * static_cast<uint32_t>(t & 3) + 16u * static_cast<uint32_t>(h)
+                                        : 0xfffffff0u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sl.w1[e] = q[e];
+        } else if constexpr (WF == RT_HIP_Q4MAT) {
+            const uint32_t v = static_cast<uint32_t>(64 * t + 32 * h);  // first value of the thread's 32
+            sl.w0 = ld16(rw, in ? wro + v / 2u : 0xfffffff0u);
+            sl.w1[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(in ? sro + (v / 32u) * 4u : 0xfffffff0u),
+                                                            0, 0);
+        } else {
+            const uint32_t bo = wro + static_cast<uint32_t>(2 * t + h) * kQ40BlockBytes;
+            const uint32_t al = bo & ~3u;
+            sl.w0 = ld16(rw, in ? al : 0xfffffff0u);
+            sl.w1[0] = __builtin_amdgcn_raw_buffer_load_b32(rw, static_cast<int>(in ? al + 16u : 0xfffffff0u), 0, 0);
+            sl.w1[1] = bo & 2u;  // the block's offset in its first dword (not a load)
+        }
         const uint32_t ao = aro + static_cast<uint32_t>(t) * 64u * kAEl;
 #pragma unroll
         for (int i = 0; i < kAL; ++i)
-            sl.a[i] = ld16(ra, t < S ? ao + a_load_stride * static_cast<uint32_t>(i) : 0xfffffff0u);
+            sl.a[i] = ld16(ra, in ? ao + a_load_stride * static_cast<uint32_t>(i) : 0xfffffff0u);
     };
     auto produce = [&](const Slot& sl, int t, int stage) {
-        const int c = t & 3;
         uint8_t* const tw = stW + stage * kTile;
         uint8_t* const ta = stA + stage * kTile;
-        const float d = f16_bits_to_f32(sl.hdr[0] & 0xffffu), dm = f16_bits_to_f32(sl.hdr[0] >> 16);
-        uint32_t sv1, mv1, sv2, mv2;
-        decode_scale_min(make_scale_sel(2 * c), sl.hdr[1], sl.hdr[2], sl.hdr[3], sv1, mv1);
-        decode_scale_min(make_scale_sel(2 * c + 1), sl.hdr[1], sl.hdr[2], sl.hdr[3], sv2, mv2);
-        const float s1 = d * static_cast<float>(sv1), n1 = dm * static_cast<float>(mv1);
-        const float s2 = d * static_cast<float>(sv2), n2 = dm * static_cast<float>(mv2);
-        u32x4 lo[2], hi[2];
+        if constexpr (WF == RT_HIP_Q4K) {
+            // values 16 h .. +15 (low nibbles, sub-block 2c) and 32 + 16 h ..
+            // +15 (high nibbles, sub-block 2c + 1): chunks 2h, 2h + 1, 4 + 2h,
+            // 5 + 2h of the tile row
+            const int c = t & 3;
+            const float d = f16_bits_to_f32(sl.w0[0] & 0xffffu), dm = f16_bits_to_f32(sl.w0[0] >> 16);
+            uint32_t sv1, mv1, sv2, mv2;
+            decode_scale_min(make_scale_sel(2 * c), sl.w0[1], sl.w0[2], sl.w0[3], sv1, mv1);
+            decode_scale_min(make_scale_sel(2 * c + 1), sl.w0[1], sl.w0[2], sl.w0[3], sv2, mv2);
+            const float s1 = d * static_cast<float>(sv1), n1 = dm * static_cast<float>(mv1);
+            const float s2 = d * static_cast<float>(sv2), n2 = dm * static_cast<float>(mv2);
+            u32x4 lo[2], hi[2];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t wl = sl.qs[j] & 0x0f0f0f0fu, wh = (sl.qs[j] >> 4) & 0x0f0f0f0fu;
-            lo[j >> 1][2 * (j & 1)] = pk_bf16(s1 * ubyte_f32(wl, 0) - n1, s1 * ubyte_f32(wl, 1) - n1);
-            lo[j >> 1][2 * (j & 1) + 1] = pk_bf16(s1 * ubyte_f32(wl, 2) - n1, s1 * ubyte_f32(wl, 3) - n1);
-            hi[j >> 1][2 * (j & 1)] = pk_bf16(s2 * ubyte_f32(wh, 0) - n2, s2 * ubyte_f32(wh, 1) - n2);
-            hi[j >> 1][2 * (j & 1) + 1] = pk_bf16(s2 * ubyte_f32(wh, 2) - n2, s2 * ubyte_f32(wh, 3) - n2);
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t wl = sl.w1[j] & 0x0f0f0f0fu, wh = (sl.w1[j] >> 4) & 0x0f0f0f0fu;
+                lo[j >> 1][2 * (j & 1)] = pk_bf16(s1 * ubyte_f32(wl, 0) - n1, s1 * ubyte_f32(wl, 1) - n1);
+                lo[j >> 1][2 * (j & 1) + 1] = pk_bf16(s1 * ubyte_f32(wl, 2) - n1, s1 * ubyte_f32(wl, 3) - n1);
+                hi[j >> 1][2 * (j & 1)] = pk_bf16(s2 * ubyte_f32(wh, 0) - n2, s2 * ubyte_f32(wh, 1) - n2);
+                hi[j >> 1][2 * (j & 1) + 1] = pk_bf16(s2 * ubyte_f32(wh, 2) - n2, s2 * ubyte_f32(wh, 3) - n2);
+            }
+            *reinterpret_cast<u32x4*>(tw + swz(r, 2 * h)) = lo[0];
+            *reinterpret_cast<u32x4*>(tw + swz(r, 2 * h + 1)) = lo[1];
+            *reinterpret_cast<u32x4*>(tw + swz(r, 4 + 2 * h)) = hi[0];
+            *reinterpret_cast<u32x4*>(tw + swz(r, 5 + 2 * h)) = hi[1];
+        } else if constexpr (WF == RT_HIP_Q4MAT) {
+            // values 32 h .. +31 in order (chunks 4h .. 4h + 3): byte i of the
+            // packed load holds values 2i (low nibble) and 2i + 1 (high),
+            // signed 4-bit, times the group's scale (quant_q4.cpp:56-90)
+            const float sc = __uint_as_float(sl.w1[0]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t q = sl.w0[c];
+                u32x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    // (the builtin's result is unsigned: the sign extension
+                    // survives only through int)
+                    const int nl = static_cast<int>(__builtin_amdgcn_sbfe(static_cast<int>(q), 8 * e, 4));
+                    const int nh = static_cast<int>(__builtin_amdgcn_sbfe(static_cast<int>(q), 8 * e + 4, 4));
+                    const float lo = static_cast<float>(nl) * sc;
+                    const float hi = static_cast<float>(nh) * sc;
+                    v[e] = pk_bf16(lo, hi);
+                }
+                *reinterpret_cast<u32x4*>(tw + swz(r, 4 * h + c)) = v;
+            }
+        } else {
+            // GGUF Q4_0 block (gguf.cpp:495-529): d, then qs[16]; value j is
+            // (qs[j] & 15) - 8, value 16 + j is (qs[j] >> 4) - 8, times d
+            const bool odd = sl.w1[1] != 0;  // block at byte 2 of its first dword
+            const uint32_t d0 = sl.w0[0], d1 = sl.w0[1], d2 = sl.w0[2], d3 = sl.w0[3], d4 = sl.w1[0];
+            const float d = f16_bits_to_f32(odd ? d0 >> 16 : d0 & 0xffffu);
+            // qs as four dwords: bytes 2..17 of the block
+            const uint32_t qs[4] = {odd ? d1 : __builtin_amdgcn_alignbyte(d1, d0, 2),
+                                    odd ? d2 : __builtin_amdgcn_alignbyte(d2, d1, 2),
+                                    odd ? d3 : __builtin_amdgcn_alignbyte(d3, d2, 2),
+                                    odd ? d4 : __builtin_amdgcn_alignbyte(d4, d3, 2)};
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {  // chunks 4h + c (low nibbles), 4h + 2 + c (high)
+                u32x4 lo, hi;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t q = qs[2 * c + (e >> 1)];
+                    const int s0 = 16 * (e & 1);
+                    lo[e] = pk_bf16(static_cast<float>(static_cast<int>(__builtin_amdgcn_ubfe(q, s0, 4)) - 8) * d,
+                                    static_cast<float>(static_cast<int>(__builtin_amdgcn_ubfe(q, s0 + 8, 4)) - 8) * d);
+                    hi[e] = pk_bf16(static_cast<float>(static_cast<int>(__builtin_amdgcn_ubfe(q, s0 + 4, 4)) - 8) * d,
+                                    static_cast<float>(static_cast<int>(__builtin_amdgcn_ubfe(q, s0 + 12, 4)) - 8) * d);
+                }
+                *reinterpret_cast<u32x4*>(tw + swz(r, 4 * h + c)) = lo;
+                *reinterpret_cast<u32x4*>(tw + swz(r, 4 * h + 2 + c)) = hi;
+            }
         }
-        *reinterpret_cast<u32x4*>(tw + swz(r, 2 * h)) = lo[0];
-        *reinterpret_cast<u32x4*>(tw + swz(r, 2 * h + 1)) = lo[1];
-        *reinterpret_cast<u32x4*>(tw + swz(r, 4 + 2 * h)) = hi[0];
-        *reinterpret_cast<u32x4*>(tw + swz(r, 5 + 2 * h)) = hi[1];
 #pragma unroll
         for (int i = 0; i < kAL; ++i) {
             const int ar = arow0 + kRowsPerLoad * i;
@@ -780,12 +868,14 @@ struct GemmPlan {
 
 GemmPlan plan_gemm(int w_fmt, bool a_bf16, int64_t m, int64_t n, int64_t k) {
     GemmPlan p;
-    p.pipe = k % 256 == 0 && (w_fmt == RT_HIP_Q4K || w_fmt == RT_HIP_BF16);
+    const bool four_bit = w_fmt == RT_HIP_Q4MAT || w_fmt == RT_HIP_Q4_0;
+    p.pipe = k % 256 == 0 && (w_fmt == RT_HIP_Q4K || w_fmt == RT_HIP_BF16 || four_bit);
     if (!p.pipe) return p;
     // A Q4_K weight is dequantized (bf16, round-to-nearest-even of the exact
     // f32 value, as the reference's flux_dequant_q4k) either inside the GEMM
     // by producer waves, once per 128-row M tile, or once per call into the
-    // workspace ahead of the bf16 kernels.  Measured on the Llama-3.2-3B
+    // workspace ahead of the bf16 kernels; Q4Mat and GGUF Q4_0 weights the
+    // same way (their workspace route runs in the ABI layer).  Measured on the Llama-3.2-3B
     // shapes: inside wins up to two M tiles (32 rows: 19 against 47 us for
     // gate, 33 against 113 us for down; 256 rows: 36 against 42 us), the
     // workspace from three on (512 rows: 50 against 52 us).  f32 A is
@@ -796,7 +886,11 @@ GemmPlan plan_gemm(int w_fmt, bool a_bf16, int64_t m, int64_t n, int64_t k) {
     p.mt2 = (m + 255) / 256;
     p.nt2 = (n + 255) / 256;
     p.big = 4 * p.mt2 * p.nt2 >= 3 * cus && tune_param("GEMM_BIG", 1);
-    p.ws = w_fmt == RT_HIP_Q4K && !p.big && p.mt <= tune_param("GEMM_WS_MT", 2);
+    p.ws = w_fmt != RT_HIP_BF16 && !p.big && p.mt <= tune_param("GEMM_WS_MT", 2);
+    if (four_bit && !p.ws) {
+        p.pipe = false;  // Q4Mat / Q4_0 beyond two M tiles: the caller dequantizes into the workspace
+        return p;
+    }
     // Split-K for the 128 x 128 kernels when their tiles leave at least half
     // the CUs idle: up to 4 slices of K (8 for k_gemm_ws), summed afterwards
     // in a fixed order (deterministic).  Slices are multiples of 64 values
@@ -817,6 +911,11 @@ GemmPlan plan_gemm(int w_fmt, bool a_bf16, int64_t m, int64_t n, int64_t k) {
 }
 
 }  // namespace
+
+bool gemm_dequant_in_kernel(int w_fmt, int64_t m, int64_t n, int64_t k) {
+    const GemmPlan p = plan_gemm(w_fmt, false, m, n, k);
+    return p.pipe && p.ws;
+}
 
 size_t gemm_workspace_bytes(int w_fmt, bool a_bf16, int64_t m, int64_t n, int64_t k) {
     const GemmPlan p = plan_gemm(w_fmt, a_bf16, m, n, k);
@@ -848,12 +947,17 @@ hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, con
             float* out = splits > 1 ? reinterpret_cast<float*>(ws) : c;
             const float* bs = splits > 1 ? nullptr : bias;
             const int64_t cs = splits > 1 ? m * n : 0;
-            if (a_bf16)
-                hipLaunchKernelGGL((k_gemm_ws<false>), g, b, kWsLds, s, a, wq, bs, out, im, in, ik / splits,
-                                   static_cast<int>(mt), ik, cs);
+            const int64_t so = w_fmt == RT_HIP_Q4MAT ? static_cast<int64_t>(q4mat_scales_offset(n, k)) : 0;
+            const int imt = static_cast<int>(mt), iks = ik / splits;
+            auto go = [&](auto kernel) {
+                hipLaunchKernelGGL(kernel, g, b, kWsLds, s, a, wq, bs, out, im, in, iks, imt, ik, cs, so);
+            };
+            if (w_fmt == RT_HIP_Q4K)
+                a_bf16 ? go(k_gemm_ws<RT_HIP_Q4K, false>) : go(k_gemm_ws<RT_HIP_Q4K, true>);
+            else if (w_fmt == RT_HIP_Q4MAT)
+                a_bf16 ? go(k_gemm_ws<RT_HIP_Q4MAT, false>) : go(k_gemm_ws<RT_HIP_Q4MAT, true>);
             else
-                hipLaunchKernelGGL((k_gemm_ws<true>), g, b, kWsLds, s, a, wq, bs, out, im, in, ik / splits,
-                                   static_cast<int>(mt), ik, cs);
+                a_bf16 ? go(k_gemm_ws<RT_HIP_Q4_0, false>) : go(k_gemm_ws<RT_HIP_Q4_0, true>);
             if (splits > 1) {
                 const int64_t mn = m * n;
                 hipLaunchKernelGGL(k_splitk_sum, dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0, s,

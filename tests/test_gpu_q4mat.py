@@ -4,10 +4,12 @@
   restatement (quant_q4.cpp:67-74), and its bf16 form is the RNE of that.
 * Q4Mat GEMV (M <= 8) against the oracle's Q4Mat::matmul_q4_t restatement
   (quant_q4.cpp:92-114): normwise 1e-5.
-* GEMM for Q4Mat and GGUF Q4_0 at M > 8 (dequantized once to bf16, then the
-  bf16 GEMM): (i) normwise 1e-5 against the f32 product of the same
+* GEMM for Q4Mat and GGUF Q4_0 at M > 8 (decoded to bf16 inside the GEMM
+  up to two 128-row M tiles, else once into the workspace, then the bf16
+  MFMA kernels): (i) normwise 1e-5 against the f32 product of the same
   bf16-rounded operands, (ii) relative RMS within GEMM_TOL_VS_F32_RMS against
-  the reference's f32 loop.
+  the reference's f32 loop; and bit-identical to the bf16 GEMM on the
+  dequantized weight where both split K alike.
 * rt_hip_linear_forward over every storage Linear2::fused_linear holds
   (nn2.cpp:143-203: Q4Mat, Q4_K, BF16, and GGUF Q4_0) at M in {1, 8, 64, 512},
   with a bias (qlinear.cpp:42-53).
@@ -82,7 +84,8 @@ def test_q4mat_gemv_one_hot_is_exact(rt, orc):
 
 @pytest.mark.parametrize("fmt_name,m,n,k", [("q4mat", 64, 1024, 1024), ("q4mat", 512, 4096, 4096),
                                             ("q4_0", 64, 512, 2048), ("q4_0", 512, 4096, 4096),
-                                            ("q4mat", 300, 1000, 3072)])
+                                            ("q4mat", 300, 1000, 3072), ("q4mat", 16, 4096, 4096),
+                                            ("q4_0", 32, 3072, 8192), ("q4_0", 200, 1000, 1024)])
 def test_4bit_gemm(rt, orc, fmt_name, m, n, k):
     say(f"[4-bit gemm] {fmt_name} M={m} N={n} K={k}")
     rng = np.random.default_rng(m + n + k)
@@ -140,3 +143,32 @@ def test_linear_forward_every_format(rt, orc, m):
                 assert normwise_err(y[r], want[r]) <= tol_gemv, (fmt, r)
         else:
             assert rel_rms(y[rows], want) <= GEMM_TOL_VS_F32_RMS, fmt
+
+
+@pytest.mark.parametrize("fmt_name", ["q4mat", "q4_0"])
+@pytest.mark.parametrize("m,n,k,a_bf16", [(200, 1000, 1024, False), (160, 3072, 8192, True)])
+def test_4bit_gemm_in_kernel_decode_bit_identical(rt, orc, fmt_name, m, n, k, a_bf16):
+    """Up to two M tiles the 4-bit weight is decoded inside the GEMM (signed
+    nibble x f32 scale, or (q - 8) x d, then RNE bf16); with the same K split
+    every output equals, bit for bit, the bf16 GEMM on the dequantized
+    weight.  Every Q4Mat nibble value (-8 included) appears."""
+    import torch
+    say(f"[4-bit gemm in-kernel] {fmt_name} M={m} N={n} K={k} a_bf16={a_bf16}")
+    rng = np.random.default_rng(m * 3 + n + k)
+    w32 = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    if fmt_name == "q4mat":
+        packed, scales = orc.q4mat_quantize(w32)
+        packed[: 256] = np.arange(256, dtype=np.uint8)
+        dw = rt.q4mat_upload(packed, scales, n, k)
+        fmt = rt.Q4MAT
+    else:
+        dw = to_dev(orc.q4_0_quantize(w32))
+        fmt = rt.Q4_0
+    wbf = rt.dequant(fmt, dw, n, k, bf16=True)
+    a = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).cuda()
+    if a_bf16:
+        a = a.bfloat16()
+    bias = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).cuda()
+    c1 = rt.gemm(fmt, a, dw, n, k, bias=bias)
+    c2 = rt.gemm(rt.BF16, a, wbf, n, k, bias=bias)
+    assert torch.equal(c1.view(torch.int32), c2.view(torch.int32))
