@@ -273,7 +273,8 @@ int rt_hip_reserve_workspace(int64_t bytes) {
 
 int64_t rt_hip_gemm_workspace_bytes(int32_t format, int32_t a_dtype, int64_t m, int64_t n, int64_t k) {
     if (m <= 0 || n <= 0 || k <= 0 || (a_dtype != RT_HIP_F32 && a_dtype != RT_HIP_BF16)) return -1;
-    if ((format == RT_HIP_Q4_0 || format == RT_HIP_Q4MAT) && gemm_dequant_in_kernel(format, m, n, k))
+    if ((format == RT_HIP_Q4_0 || format == RT_HIP_Q4MAT) &&
+        gemm_dequant_in_kernel(format, a_dtype == RT_HIP_BF16, m, n, k))
         return static_cast<int64_t>(gemm_workspace_bytes(format, a_dtype == RT_HIP_BF16, m, n, k));
     if (format == RT_HIP_Q4_0 || format == RT_HIP_Q4MAT)
         return static_cast<int64_t>((gemm_workspace_bytes(RT_HIP_BF16, a_dtype == RT_HIP_BF16, m, n, k) + 255) /
@@ -919,7 +920,7 @@ int rt_hip_gemm(int32_t format, const void* a, int32_t a_dtype, const void* w, c
     if (!aligned16(a) || !aligned16(w) || !aligned16(c))
         return fail(RT_HIP_E_ALIGN, std::string(fn) + ": a, w, c must be 16-byte aligned");
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (gemm_dequant_in_kernel(format, m, n, k))  // small M: decoded inside the GEMM
+    if (gemm_dequant_in_kernel(format, a_dtype == RT_HIP_BF16, m, n, k))  // decoded inside the GEMM
         return check_stream_launch(launch_gemm(format, a, a_dtype == RT_HIP_BF16, w, bias, c, m, n, k, s), fn);
     const size_t own = (gemm_workspace_bytes(RT_HIP_BF16, a_dtype == RT_HIP_BF16, m, n, k) + 255) / 256 * 256;
     hipError_t e;

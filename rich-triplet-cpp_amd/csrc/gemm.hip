@@ -875,18 +875,27 @@ GemmPlan plan_gemm(int w_fmt, bool a_bf16, int64_t m, int64_t n, int64_t k) {
     // f32 value, as the reference's flux_dequant_q4k) either inside the GEMM
     // by producer waves, once per 128-row M tile, or once per call into the
     // workspace ahead of the bf16 kernels; Q4Mat and GGUF Q4_0 weights the
-    // same way (their workspace route runs in the ABI layer).  Measured on the Llama-3.2-3B
-    // shapes: inside wins up to two M tiles (32 rows: 19 against 47 us for
-    // gate, 33 against 113 us for down; 256 rows: 36 against 42 us), the
-    // workspace from three on (512 rows: 50 against 52 us).  f32 A is
-    // converted to bf16 inside k_gemm_ws, else once into the workspace.
+    // same way (their workspace route runs in the ABI layer).
     p.mt = (m + 127) / 128;
     p.nt = (n + 127) / 128;
     const int64_t cus = device_info().cus;
     p.mt2 = (m + 255) / 256;
     p.nt2 = (n + 255) / 256;
     p.big = 4 * p.mt2 * p.nt2 >= 3 * cus && tune_param("GEMM_BIG", 1);
-    p.ws = w_fmt != RT_HIP_BF16 && !p.big && p.mt <= tune_param("GEMM_WS_MT", 2);
+    // Measured (Q4_K, Llama-3.2-3B and 4096-square shapes): inside wins up
+    // to two M tiles (32 rows: 19 against 47 us for gate 8192 x 3072, 33
+    // against 113 us for down 3072 x 8192; 256 rows: 36 against 42 us); up
+    // to eight tiles when N >= 2K (gate, 768 rows: 68.5 against 76.1 us with
+    // f32 A, 62.7 against 72.6 with bf16 A); up to four when N >= K with a
+    // bf16 A (3072 x 3072, 384 rows: 26.7 against 28.2 us).  It loses for
+    // square shapes beyond four tiles (4096 x 4096, 768 rows: 61 against
+    // 53 us) and for the down shape beyond two (60 against 57 us at 512).
+    // Up to two M tiles an f32 A is converted to bf16 inside k_gemm_ws;
+    // beyond that once into the workspace first (read as f32 by every N
+    // tile, its traffic made the in-GEMM route lose).
+    const bool wide = p.mt <= 8 && (n >= 2 * k || (a_bf16 && n >= k && p.mt <= 4));
+    p.ws = w_fmt != RT_HIP_BF16 && !p.big &&
+           (p.mt <= tune_param("GEMM_WS_MT", 2) || (wide && tune_param("GEMM_WS_WIDE", 1)));
     if (four_bit && !p.ws) {
         p.pipe = false;  // Q4Mat / Q4_0 beyond two M tiles: the caller dequantizes into the workspace
         return p;
@@ -904,7 +913,7 @@ GemmPlan plan_gemm(int w_fmt, bool a_bf16, int64_t m, int64_t n, int64_t k) {
         if (forced >= 1 && forced <= cap && k % (unit * forced) == 0) splits = forced;
         p.splits = splits;
     }
-    p.a_bytes = a_bf16 || p.ws ? 0 : static_cast<size_t>(m * k) * 2;
+    p.a_bytes = a_bf16 || (p.ws && p.mt <= 2) ? 0 : static_cast<size_t>(m * k) * 2;
     p.w_bytes = w_fmt == RT_HIP_Q4K && !p.ws ? static_cast<size_t>(n * k) * 2 : 0;
     p.p_bytes = p.splits > 1 ? static_cast<size_t>(p.splits) * m * n * 4 : 0;
     return p;
@@ -912,8 +921,8 @@ GemmPlan plan_gemm(int w_fmt, bool a_bf16, int64_t m, int64_t n, int64_t k) {
 
 }  // namespace
 
-bool gemm_dequant_in_kernel(int w_fmt, int64_t m, int64_t n, int64_t k) {
-    const GemmPlan p = plan_gemm(w_fmt, false, m, n, k);
+bool gemm_dequant_in_kernel(int w_fmt, bool a_bf16, int64_t m, int64_t n, int64_t k) {
+    const GemmPlan p = plan_gemm(w_fmt, a_bf16, m, n, k);
     return p.pipe && p.ws;
 }
 
@@ -944,24 +953,34 @@ hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, con
             const int im = static_cast<int>(m), in = static_cast<int>(n), ik = static_cast<int>(k);
             const dim3 g(static_cast<unsigned>(mt * nt), static_cast<unsigned>(splits)), b(kWsThreads);
             const auto* wq = static_cast<const uint8_t*>(w);
-            float* out = splits > 1 ? reinterpret_cast<float*>(ws) : c;
+            bool abf = a_bf16;
+            const void* ain = a;
+            if (a_bytes) {  // f32 A over more than two M tiles: once to bf16 first
+                uint16_t* ab = reinterpret_cast<uint16_t*>(ws);
+                const int64_t n8 = m * k / 8;
+                hipLaunchKernelGGL(k_f32_to_bf16, dim3(static_cast<unsigned>((n8 + 255) / 256)), dim3(256), 0, s,
+                                   static_cast<const float*>(a), ab, n8);
+                ain = ab;
+                abf = true;
+            }
+            float* out = splits > 1 ? reinterpret_cast<float*>(ws + a_bytes) : c;
             const float* bs = splits > 1 ? nullptr : bias;
             const int64_t cs = splits > 1 ? m * n : 0;
             const int64_t so = w_fmt == RT_HIP_Q4MAT ? static_cast<int64_t>(q4mat_scales_offset(n, k)) : 0;
             const int imt = static_cast<int>(mt), iks = ik / splits;
             auto go = [&](auto kernel) {
-                hipLaunchKernelGGL(kernel, g, b, kWsLds, s, a, wq, bs, out, im, in, iks, imt, ik, cs, so);
+                hipLaunchKernelGGL(kernel, g, b, kWsLds, s, ain, wq, bs, out, im, in, iks, imt, ik, cs, so);
             };
             if (w_fmt == RT_HIP_Q4K)
-                a_bf16 ? go(k_gemm_ws<RT_HIP_Q4K, false>) : go(k_gemm_ws<RT_HIP_Q4K, true>);
+                abf ? go(k_gemm_ws<RT_HIP_Q4K, false>) : go(k_gemm_ws<RT_HIP_Q4K, true>);
             else if (w_fmt == RT_HIP_Q4MAT)
-                a_bf16 ? go(k_gemm_ws<RT_HIP_Q4MAT, false>) : go(k_gemm_ws<RT_HIP_Q4MAT, true>);
+                abf ? go(k_gemm_ws<RT_HIP_Q4MAT, false>) : go(k_gemm_ws<RT_HIP_Q4MAT, true>);
             else
-                a_bf16 ? go(k_gemm_ws<RT_HIP_Q4_0, false>) : go(k_gemm_ws<RT_HIP_Q4_0, true>);
+                abf ? go(k_gemm_ws<RT_HIP_Q4_0, false>) : go(k_gemm_ws<RT_HIP_Q4_0, true>);
             if (splits > 1) {
                 const int64_t mn = m * n;
                 hipLaunchKernelGGL(k_splitk_sum, dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0, s,
-                                   reinterpret_cast<const float*>(ws), splits, bias, c, mn, n);
+                                   reinterpret_cast<const float*>(ws + a_bytes), splits, bias, c, mn, n);
             }
             return hipGetLastError();
         }

@@ -230,8 +230,9 @@ hipError_t launch_add(const float* a, const float* b, float* out, int64_t n, hip
 hipError_t launch_gemm(int w_fmt, const void* a, bool a_bf16, const void* w, const float* bias,
                        float* c, int64_t m, int64_t n, int64_t k, hipStream_t s);
 // Whether launch_gemm dequantizes this 4-bit weight inside the GEMM (small
-// M); otherwise a Q4Mat / Q4_0 caller dequantizes into the workspace first.
-bool gemm_dequant_in_kernel(int w_fmt, int64_t m, int64_t n, int64_t k);
+// M, or wide N); otherwise a Q4Mat / Q4_0 caller dequantizes into the
+// workspace first.
+bool gemm_dequant_in_kernel(int w_fmt, bool a_bf16, int64_t m, int64_t n, int64_t k);
 // Workspace bytes one launch_gemm call needs.
 size_t gemm_workspace_bytes(int w_fmt, bool a_bf16, int64_t m, int64_t n, int64_t k);
 hipError_t launch_add_bias(float* y, const float* bias, int64_t m, int64_t n, hipStream_t s);

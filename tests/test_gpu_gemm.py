@@ -121,15 +121,20 @@ def test_gemm_large_tile_partial_round(rt, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k,a_bf16", [(256, 8192, 3072, False), (200, 1000, 1024, True),
-                                         (160, 3072, 8192, False), (512, 3072, 8192, False)])
+                                         (160, 3072, 8192, False), (512, 3072, 8192, False),
+                                         (512, 8192, 3072, False), (1000, 4096, 4096, False),
+                                         (700, 2048, 1024, False), (384, 3072, 3072, True)])
 def test_gemm_q4k_bit_identical_to_bf16_path(rt, m, n, k, a_bf16):
-    """Up to two 128-row M tiles, a Q4_K weight is dequantized inside the
-    GEMM by producer waves (w = (d*sv)*q - dmin*mv, RNE bf16) beside the
-    MFMA waves; from three on, once into the workspace.  Either way, with
-    the same K split, every output equals, bit for bit, the bf16 GEMM on the
-    dequantized weight (the same MFMA order), bias included: gate and down
-    shapes at 160, 200 and 256 rows (the in-GEMM path, K split 2 and 4,
-    ragged M and N, bf16 A) and config 4's down (the workspace path)."""
+    """Up to two 128-row M tiles (eight when N >= K), a Q4_K weight is
+    dequantized inside the GEMM by producer waves (w = (d*sv)*q - dmin*mv,
+    RNE bf16) beside the MFMA waves; otherwise once into the workspace.
+    Either way, with the same K split, every output equals, bit for bit, the
+    bf16 GEMM on the dequantized weight (the same MFMA order), bias
+    included: gate and down shapes at 160, 200 and 256 rows (the in-GEMM
+    path, K split 2 and 4, ragged M and N, bf16 A), config 4's down (the
+    workspace path), gate and N = 2K shapes at 512 and 700 rows (in-GEMM
+    with A converted to bf16 first, K split 2 at 700), a square one at 1000
+    rows (workspace) and at 384 rows with bf16 A (in-GEMM, K split 3)."""
     import torch
     say(f"[gemm q4k vs bf16 path] M={m} N={n} K={k} a_bf16={a_bf16}")
     g = torch.Generator(device="cuda").manual_seed(m + n + k)

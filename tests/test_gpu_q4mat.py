@@ -146,9 +146,13 @@ def test_linear_forward_every_format(rt, orc, m):
 
 
 @pytest.mark.parametrize("fmt_name", ["q4mat", "q4_0"])
-@pytest.mark.parametrize("m,n,k,a_bf16", [(200, 1000, 1024, False), (160, 3072, 8192, True)])
+@pytest.mark.parametrize("m,n,k,a_bf16", [(200, 1000, 1024, False), (160, 3072, 8192, True),
+                                         (600, 8192, 3072, False), (512, 4096, 4096, True),
+                                         (384, 2048, 1024, False)])
 def test_4bit_gemm_in_kernel_decode_bit_identical(rt, orc, fmt_name, m, n, k, a_bf16):
-    """Up to two M tiles the 4-bit weight is decoded inside the GEMM (signed
+    """Up to two M tiles (eight when N >= 2K, four when N >= K with bf16 A;
+    beyond two an f32 A is converted to bf16 first) the 4-bit weight is
+    decoded inside the GEMM (signed
     nibble x f32 scale, or (q - 8) x d, then RNE bf16); with the same K split
     every output equals, bit for bit, the bf16 GEMM on the dequantized
     weight.  Every Q4Mat nibble value (-8 included) appears."""
