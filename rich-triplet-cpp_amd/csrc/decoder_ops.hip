@@ -255,8 +255,9 @@ __device__ __forceinline__ float ld_dev(const float* p) {
 // all P pairs, are issued before any is used (indices past S repeat split
 // S - 1, in bounds, with weight 0): one memory latency per batch instead of
 // one per split and pair.
-template <int PART, int P>
+template <int PART, int P, bool COH>
 __device__ __forceinline__ void fold_splits(const float* const (&ph)[P], const int (&d)[P], int S, float (&res)[P]) {
+    auto ld = [](const float* p) { return COH ? ld_dev(p) : *p; };
     float M[P], L[P], O[P];
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -273,9 +274,9 @@ __device__ __forceinline__ void fold_splits(const float* const (&ph)[P], const i
 #pragma unroll
             for (int j = 0; j < kCB; ++j) {
                 const float* ps = ph[p] + min(s0 + j, S - 1) * PART;
-                ms[p][j] = ld_dev(ps);
-                ls[p][j] = ld_dev(ps + 1);
-                os[p][j] = ld_dev(ps + 4 + d[p]);
+                ms[p][j] = ld(ps);
+                ls[p][j] = ld(ps + 1);
+                os[p][j] = ld(ps + 4 + d[p]);
             }
 #pragma unroll
         for (int p = 0; p < P; ++p) {
@@ -321,7 +322,36 @@ __device__ __forceinline__ void attn_range(const AttnArgs& a, int m, int& k0, in
     k0 = a.window > 0 && k1 > a.window ? k1 - a.window : 0;
 }
 
-template <int HD, int G, bool F16>
+// Sum over aligned groups of L lanes (8, 16 or 32), every lane of a group
+// ending with the same bits: DPP within a 16-lane row (lane ^ 1, lane ^ 2,
+// the half-row mirror, the row mirror), one cross-row shuffle for 32.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(L == 8 || L == 16 || L == 32, "8, 16 or 32 lanes");
+    v += dpp_f<0xb1>(v);
+    v += dpp_f<0x4e>(v);
+    v += dpp_f<0x141>(v);
+    if constexpr (L >= 16) v += dpp_f<0x140>(v);
+    if constexpr (L == 32) v += __shfl_xor(v, 16, kWave);
+    return v;
+}
+
+// Positions per split: whole rounds of BATCH.
+template <int BATCH>
+__device__ __forceinline__ int attn_chunk(int len, int S) {
+    const int chunk = (len + S - 1) / S;
+    return (chunk + BATCH - 1) / BATCH * BATCH;
+}
+
+// MERGE: the last split of a (row, kv head) to arrive merges in this launch
+// (partials stored device-coherent); otherwise partials are plain stores
+// and k_attn2_combine merges them in a second launch.
+template <int HD, int G, bool F16, bool MERGE>
 __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
     using Geo = AttnGeom<HD>;
     constexpr int LP = Geo::LP, NG = Geo::NG;
@@ -331,13 +361,7 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
     const int n_q = a.n_kv * G;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = wave * Geo::GPW + lane / LP, sub = lane % LP;
-    int k0, k1;
-    attn_range(a, m, k0, k1);
-    const int len = k1 - k0;
-    int chunk = (len + S - 1) / S;
-    chunk = (chunk + Geo::BATCH - 1) / Geo::BATCH * Geo::BATCH;
-    const int p0 = k0 + sp * chunk, p1 = min(k1, p0 + chunk);
-
+    // q first: its loads do not wait for the device-side position
     f32x4 qa[G], qb[G], oa[G], ob[G];
     float mx[G], l[G];
 #pragma unroll
@@ -350,6 +374,11 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
         mx[h] = -__builtin_inff();
         l[h] = 0.0f;
     }
+    int k0, k1;
+    attn_range(a, m, k0, k1);
+    const int len = k1 - k0;
+    const int chunk = attn_chunk<Geo::BATCH>(len, S);
+    const int p0 = k0 + sp * chunk, p1 = min(k1, p0 + chunk);
     for (int pb = p0 + grp; pb < p1; pb += NG * kAU) {
         f32x4 ka[kAU], kb[kAU], va[kAU], vb[kAU];
 #pragma unroll
@@ -374,7 +403,7 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
             for (int u = 0; u < kAU; ++u) {
                 float dd = (qa[h][0] * ka[u][0] + qa[h][1] * ka[u][1]) + (qa[h][2] * ka[u][2] + qa[h][3] * ka[u][3]);
                 dd += (qb[h][0] * kb[u][0] + qb[h][1] * kb[u][1]) + (qb[h][2] * kb[u][2] + qb[h][3] * kb[u][3]);
-                const float v = segment_sum<LP>(dd) * a.scale;
+                const float v = group_sum<LP>(dd) * a.scale;
                 sc[u] = pb + u * NG < p1 ? v : -__builtin_inff();  // uniform per position group
                 mn = fmaxf(mn, sc[u]);
             }
@@ -417,13 +446,22 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
             }
         }
         float* dst = a.part + ((static_cast<int64_t>(m) * n_q + kvh * G + h) * S + sp) * Geo::PART;
-        if (d4 == 0) {
-            st_dev(dst, M);
-            st_dev(dst + 1, L);
-        }
+        if constexpr (MERGE) {
+            if (d4 == 0) {
+                st_dev(dst, M);
+                st_dev(dst + 1, L);
+            }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) st_dev(dst + 4 + d4 * 4 + e, O[e]);
+            for (int e = 0; e < 4; ++e) st_dev(dst + 4 + d4 * 4 + e, O[e]);
+        } else {
+            if (d4 == 0) {
+                dst[0] = M;
+                dst[1] = L;
+            }
+            *reinterpret_cast<f32x4*>(dst + 4 + d4 * 4) = O;  // PART = 4 + HD: 16-byte aligned
+        }
     }
+    if constexpr (!MERGE) return;
     // Every thread's partial stores have completed, then one arrival per
     // workgroup; the last of the S splits of (row, kv head) merges them and
     // resets the counter for the next launch.
@@ -448,7 +486,7 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
     }
     // splits past the range (chunk * busy >= len) hold empty states: skip them
     const int busy = min(S, (len + chunk - 1) / chunk);
-    fold_splits<Geo::PART, P>(ph, dd, busy, res);
+    fold_splits<Geo::PART, P, true>(ph, dd, busy, res);
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         const int t = tid + kAT * p;
@@ -457,11 +495,43 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
     if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Second launch of the two-launch form: workgroup (query head, row), one
+// thread per dimension, folds the busy splits' plain-stored partials in
+// split order (the same fold as the in-launch merge, so the same bits).
+template <int HD>
+__global__ __launch_bounds__(HD) void k_attn2_combine(const AttnArgs a, int S) {
+    using Geo = AttnGeom<HD>;
+    const int h = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
+    const int n_q = gridDim.x;
+    int k0, k1;
+    attn_range(a, m, k0, k1);
+    const int len = k1 - k0;
+    const int chunk = attn_chunk<Geo::BATCH>(len, S);
+    const int busy = min(S, (len + chunk - 1) / chunk);
+    const float* ph[1] = {a.part + (static_cast<int64_t>(m) * n_q + h) * S * Geo::PART};
+    const int dd[1] = {d};
+    float res[1];
+    fold_splits<Geo::PART, 1, false>(ph, dd, busy, res);
+    a.out[(static_cast<int64_t>(m) * n_q + h) * HD + d] = res[0];
+}
+
 template <int HD, int G, bool F16>
 hipError_t run_attn(const AttnArgs& a, int S, int M, hipStream_t s) {
-    hipLaunchKernelGGL((k_attn2_partial<HD, G, F16>), dim3(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(S),
-                                                             static_cast<unsigned>(M)),
-                       dim3(kAT), 0, s, a);
+    const dim3 grid(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(S), static_cast<unsigned>(M));
+    // Two launches by default.  Measured at 1024 cached positions: the
+    // Llama-3.2-3B engine token 1162 us against 1201 us with the merge in
+    // the last-arriving workgroup (Gemma-3-4B shapes 1989 against 1982 us);
+    // 28 layers of attention alone 289 against 322 us.  The in-launch
+    // merge's device-coherent partial stores, arrival atomic and coherent
+    // reloads are three memory round trips in series, more than a kernel
+    // boundary costs.
+    if (tune_param("ATTN_MERGE_IN_LAUNCH", 0)) {
+        hipLaunchKernelGGL((k_attn2_partial<HD, G, F16, true>), grid, dim3(kAT), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((k_attn2_partial<HD, G, F16, false>), grid, dim3(kAT), 0, s, a);
+        hipLaunchKernelGGL(k_attn2_combine<HD>, dim3(static_cast<unsigned>(a.n_kv * G), static_cast<unsigned>(M)),
+                           dim3(HD), 0, s, a, S);
+    }
     return hipGetLastError();
 }
 
