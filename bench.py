@@ -30,6 +30,9 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 F32_PEAK_TFLOPS = 157.3
 WIDENED_LAYERS = {0, 1, 2, 5, 8, 11, 14, 17, 20, 23, 24, 25, 26, 27}
+# --mix q4km_q6k: the widened layers' down projection kept as native Q6_K
+# (rt_hip_gemv_q6k_tiled) instead of its BF16-widened copy
+Q6K_NATIVE = "q6k"
 HIDDEN, KV, FFN, VOCAB, LAYERS = 3072, 1024, 8192, 128256, 28
 # HBM bytes per launch of the dominant kernel (fused gate+up, tiled layout),
 # measured with rocprofv3 FETCH_SIZE / WRITE_SIZE and scaled by a 1 GiB device
@@ -58,6 +61,8 @@ def q4k_bytes(n, k):
 
 
 def weight_bytes(fmt, n, k, rt):
+    if fmt == Q6K_NATIVE:
+        return n * (k // 256) * 210
     if fmt == rt.Q4K:
         return q4k_bytes(n, k)
     if fmt == rt.Q4_0:
@@ -96,6 +101,13 @@ class DecodeModel:
         dev = "cuda"
 
         def make(n, k, fmt):
+            if fmt == Q6K_NATIVE:
+                # synthetic Q6_K blocks (random quants and scales, d = 2^-7),
+                # tiled once at load as the native GEMV reads them
+                b = torch.randint(0, 256, (n * (k // 256), 210), dtype=torch.uint8, device=dev, generator=g)
+                b[:, 208] = 0x00
+                b[:, 209] = 0x20
+                return rt.q6k_tile(b.reshape(-1), n, k)
             w = torch.randn((n, k), generator=g, device=dev) * 0.02
             if fmt == rt.Q4K:
                 out = rt.quantize_q4k(w)
@@ -105,7 +117,7 @@ class DecodeModel:
             return out
 
         for layer in range(LAYERS):
-            wide = mix == "q4km" and layer in WIDENED_LAYERS
+            wide = mix in ("q4km", "q4km_q6k") and layer in WIDENED_LAYERS
             x_attn = torch.randn((1, HIDDEN), generator=g, device=dev)
             x_o = torch.randn((1, HIDDEN), generator=g, device=dev)
             x_mlp = torch.randn((1, HIDDEN), generator=g, device=dev)
@@ -116,7 +128,8 @@ class DecodeModel:
                      ("o", HIDDEN, HIDDEN, rt.Q4K, x_o),
                      ("gate", FFN, HIDDEN, rt.Q4K, x_mlp),
                      ("up", FFN, HIDDEN, rt.Q4K, x_mlp),
-                     ("down", HIDDEN, FFN, rt.BF16 if wide else rt.Q4K, x_down)]
+                     ("down", HIDDEN, FFN, (Q6K_NATIVE if mix == "q4km_q6k" else rt.BF16) if wide else rt.Q4K,
+                      x_down)]
             for name, n, k, fmt, x in specs:
                 w = make(n, k, fmt)
                 y = torch.empty((1, n), device=dev)
@@ -145,7 +158,9 @@ class DecodeModel:
 
     def one(self, gv):
         name, fmt, w, x, y, n, k = gv
-        if fmt == self.rt.Q4K and self.layout == "tiled":
+        if fmt == Q6K_NATIVE:
+            self.rt.gemv_q6k_tiled(w, x, n, k, y=y)
+        elif fmt == self.rt.Q4K and self.layout == "tiled":
             self.rt.gemv_q4k_tiled(self.tiled[name], x, n, k, y=y)
         else:
             self.rt.gemv(fmt, w, x, n, k, y=y)
@@ -322,7 +337,9 @@ def bench_decode(args, rt, torch):
                         else DOMINANT_TRAFFIC_BYTES.get(args.layout)), "kernel": dom["kernel"],
             "us_per_launch": round(dom["us_per_launch"], 3),
             "bytes_per_launch": dom["bytes_per_launch"]}
-    cpu = None if args.no_cpu_baseline else cpu_baseline(rt, torch, model)
+    # the native-Q6_K variant has the headline's CPU path (the reference
+    # widens Q6_K to BF16 at load): its baseline is the q4km line's
+    cpu = None if args.no_cpu_baseline or args.mix == "q4km_q6k" else cpu_baseline(rt, torch, model)
     if cpu:
         log(f"[bench] cpu baseline: {cpu}")
     return {
@@ -332,7 +349,9 @@ def bench_decode(args, rt, torch):
         "scaling": "weak", "vs_baseline": None, "dtype": "q4_k/bf16 weights, f32 activations",
         "data": "synthetic: random N(0,0.02) weights quantized on GPU, N(0,1) inputs",
         "config": {"workload": "llama-3.2-3b decode step, all 28 layers' GEMVs + lm_head, batch 1",
-                   "weights": "Q4_K_M mix" if args.mix == "q4km" else "pure Q4_K",
+                   "weights": {"q4km": "Q4_K_M mix",
+                               "q4km_q6k": "Q4_K_M mix, Q6_K down projections kept native (not widened)",
+                               "q4k": "pure Q4_K"}[args.mix],
                    "gemvs_per_token": len(model.gemvs), "bytes_per_token": nbytes,
                    "us_per_token": round(us, 2), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
                    "launches_per_token": len(model.plan),
@@ -981,7 +1000,7 @@ def main() -> int:
                     choices=["llama_decode", "q4k_gemv", "q4_0_gemv", "bf16_lm_head", "prefill",
                              "flux", "flux_attention", "layer_ops", "decode_layers", "engine_llama3b", "engine_gemma3_4b",
                              "q8_gemv", "q6k_gemv", "q4mat_gemv", "batch_gemv"])
-    ap.add_argument("--mix", default="q4km", choices=["q4km", "q4k"])
+    ap.add_argument("--mix", default="q4km", choices=["q4km", "q4k", "q4km_q6k"])
     ap.add_argument("--context", type=int, default=1024,
                     help="cached positions for --workload decode_layers")
     ap.add_argument("--no-cpu-baseline", action="store_true")
