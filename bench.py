@@ -90,6 +90,15 @@ def q4_0_blocks(torch, w):
 
 # --------------------------------------------------------------- config 3 --
 
+def q6k_tiled_synthetic(rt, torch, g, n, k):
+    """Synthetic Q6_K blocks (random quants and scales, d = 2^-7), tiled once
+    at load as the native GEMV reads them."""
+    b = torch.randint(0, 256, (n * (k // 256), 210), dtype=torch.uint8, device="cuda", generator=g)
+    b[:, 208] = 0x00
+    b[:, 209] = 0x20
+    return rt.q6k_tile(b.reshape(-1), n, k)
+
+
 class DecodeModel:
     """Synthetic Llama-3.2-3B linear weights and per-GEMV inputs on the GPU."""
 
@@ -102,12 +111,7 @@ class DecodeModel:
 
         def make(n, k, fmt):
             if fmt == Q6K_NATIVE:
-                # synthetic Q6_K blocks (random quants and scales, d = 2^-7),
-                # tiled once at load as the native GEMV reads them
-                b = torch.randint(0, 256, (n * (k // 256), 210), dtype=torch.uint8, device=dev, generator=g)
-                b[:, 208] = 0x00
-                b[:, 209] = 0x20
-                return rt.q6k_tile(b.reshape(-1), n, k)
+                return q6k_tiled_synthetic(rt, torch, g, n, k)
             w = torch.randn((n, k), generator=g, device=dev) * 0.02
             if fmt == rt.Q4K:
                 out = rt.quantize_q4k(w)
@@ -386,11 +390,13 @@ def bench_layer_ops(args, rt, torch):
 
     layers = []
     for layer in range(LAYERS):
-        wide = args.mix == "q4km" and layer in WIDENED_LAYERS
-        L = {"wide": wide, "qk": [tiled(HIDDEN, HIDDEN), tiled(KV, HIDDEN)],
+        wide = args.mix in ("q4km", "q4km_q6k") and layer in WIDENED_LAYERS
+        q6 = wide and args.mix == "q4km_q6k"
+        L = {"wide": wide, "q6": q6, "qk": [tiled(HIDDEN, HIDDEN), tiled(KV, HIDDEN)],
              "v": bf16(KV, HIDDEN) if wide else tiled(KV, HIDDEN), "o": tiled(HIDDEN, HIDDEN),
              "gu": [tiled(FFN, HIDDEN), tiled(FFN, HIDDEN)],
-             "down": bf16(HIDDEN, FFN) if wide else tiled(HIDDEN, FFN),
+             "down": (q6k_tiled_synthetic(rt, torch, g, HIDDEN, FFN) if q6 else bf16(HIDDEN, FFN)) if wide
+             else tiled(HIDDEN, FFN),
              "x": torch.randn((1, HIDDEN), generator=g, device=dev),
              "x_o": torch.randn((1, HIDDEN), generator=g, device=dev),
              "g1": 1.0 + 0.1 * torch.randn((HIDDEN,), generator=g, device=dev),
@@ -416,7 +422,10 @@ def bench_layer_ops(args, rt, torch):
                                                 HIDDEN, ys=L["y_qkv"])
             rt.gemv_q4k_tiled(L["o"], L["x_o"], HIDDEN, HIDDEN, y=L["y_o"])
             rt.gemv_q4k_tiled_rmsnorm_multi(L["gu"], L["x"], L["g2"], eps, [FFN, FFN], HIDDEN, ys=L["y_gu"])
-            if L["wide"]:
+            if L["q6"]:  # the native Q6_K down with its residual add (y_d is the residual here)
+                rt.gemv_swiglu_residual(None, L["down"], L["y_gu"][0], L["y_gu"][1], L["y_d"], HIDDEN, FFN,
+                                        q6k=True)
+            elif L["wide"]:
                 rt.gemv_bf16_swiglu(L["down"], L["y_gu"][0], L["y_gu"][1], HIDDEN, FFN, y=L["y_d"])
             else:
                 rt.gemv_q4k_tiled_swiglu(L["down"], L["y_gu"][0], L["y_gu"][1], HIDDEN, FFN, y=L["y_d"])
@@ -434,7 +443,9 @@ def bench_layer_ops(args, rt, torch):
             xn = F.rms_norm(L["x"], (HIDDEN,), L["g2"], eps)
             rt.gemv_q4k_tiled_multi(L["gu"], xn, [FFN, FFN], HIDDEN, ys=L["y_gu"])
             act = F.silu(L["y_gu"][0]) * L["y_gu"][1]
-            if L["wide"]:
+            if L["q6"]:
+                rt.gemv_q6k_tiled(L["down"], act, HIDDEN, FFN, y=L["y_d"])
+            elif L["wide"]:
                 rt.gemv(rt.BF16, L["down"], act, HIDDEN, FFN, y=L["y_d"])
             else:
                 rt.gemv_q4k_tiled(L["down"], act, HIDDEN, FFN, y=L["y_d"])
@@ -448,7 +459,9 @@ def bench_layer_ops(args, rt, torch):
     return {"metric": "Llama-3.2-3B linear work + RMSNorm/SwiGLU per token, fused into the GEMVs",
             "value": round(ms_f * 1e3, 2), "unit": "us/token", "higher_is_better": False,
             "separate_us_per_token": round(ms_s * 1e3, 2), "steps": args.steps, "warmup": args.warmup,
-            "weights": "Q4_K_M mix" if args.mix == "q4km" else "pure Q4_K",
+            "weights": {"q4km": "Q4_K_M mix",
+                        "q4km_q6k": "Q4_K_M mix, Q6_K down projections kept native (fused SwiGLU + residual add)",
+                        "q4k": "pure Q4_K"}[args.mix],
             "launches_per_token_fused": 4 * LAYERS + 1,
             "separate": "the same GEMVs with torch's rms_norm, silu and mul kernels between them",
             "data": "synthetic"}

@@ -373,12 +373,21 @@ int rt_hip_gemv_q4_0(const void* blocks, const float* x, float* y, int64_t n, in
  *   bytes (0.82 byte per weight instead of 2) and widening each weight to the
  *   same bf16 value in registers; equals rt_hip_gemv_bf16 on the widened
  *   weights to f32 rounding.  Replace: the BF16 GEMV of a Q6_K-widened v or
- *   down (MatBf16::matmul_by_t, src/mat.cpp:318-414). */
+ *   down (MatBf16::matmul_by_t, src/mat.cpp:318-414).
+ * rt_hip_gemv_q6k_tiled_swiglu_residual: resid += W . (silu(gate) * up),
+ *   the same product on the Q6_K bytes with the MLP's gating applied while x
+ *   is staged and the rows added to resid in the store: the Q6_K counterpart
+ *   of rt_hip_gemv_bf16_swiglu_residual.  Replace: LlamaMlp::forward's down
+ *   projection of silu(gate) * up (src/transformer5.cpp:186-190) and the
+ *   residual add after it (:205-212), for a Q6_K down widened at load.
+ *   resid [n] is read and written; it must not overlap gate or up. */
 int rt_hip_dequant_q6k_bf16(const void* blocks, uint16_t* out, int64_t n, int64_t k, rt_hip_stream stream);
 int64_t rt_hip_q6k_tiled_bytes(int64_t n, int64_t k);
 int rt_hip_q6k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, rt_hip_stream stream);
 int rt_hip_gemv_q6k_tiled(const void* tiled, const float* x, float* y, int64_t n, int64_t k,
                           rt_hip_stream stream);
+int rt_hip_gemv_q6k_tiled_swiglu_residual(const void* tiled, const float* gate, const float* up, float* resid,
+                                          int64_t n, int64_t k, rt_hip_stream stream);
 
 /* ---- GGUF files: reading and uploading weights ------------------------------
  * Replace: GgufFile::open, find_tensor, read_tensor_bytes and the metadata

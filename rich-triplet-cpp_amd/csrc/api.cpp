@@ -795,6 +795,21 @@ int rt_hip_gemv_q6k_tiled(const void* tiled, const float* x, float* y, int64_t n
     return check_stream_launch(launch_gemv_q6k(tiled, x, y, n, k, static_cast<hipStream_t>(stream)), fn);
 }
 
+int rt_hip_gemv_q6k_tiled_swiglu_residual(const void* tiled, const float* gate, const float* up, float* resid,
+                                          int64_t n, int64_t k, rt_hip_stream stream) {
+    const char* fn = "rt_hip_gemv_q6k_tiled_swiglu_residual";
+    int rc = gemv_args(fn, tiled, gate, resid, n, k, 1, 256);
+    if (rc) return rc;
+    if (!up) return fail(RT_HIP_E_ARG, std::string(fn) + ": null up");
+    if (!aligned16(up)) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": up must be 16-byte aligned");
+    if (overlaps(resid, n * 4, gate, k * 4) || overlaps(resid, n * 4, up, k * 4))
+        return fail(RT_HIP_E_ARG, std::string(fn) + ": resid overlaps gate or up");
+    if (k > 8192) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 8192");
+    hipError_t e;
+    if (!state_for_current(&e)) return hip_fail(e, fn);
+    return check_stream_launch(launch_gemv_q6k(tiled, gate, resid, n, k, static_cast<hipStream_t>(stream), up), fn);
+}
+
 int rt_hip_argmax(const float* logits, int64_t rows, int64_t cols, int64_t* idx, float* val,
                   rt_hip_stream stream) {
     if (!logits || !idx) return fail(RT_HIP_E_ARG, "rt_hip_argmax: null pointer");

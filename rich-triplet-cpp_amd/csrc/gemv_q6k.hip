@@ -37,6 +37,7 @@
 // limbs (h + m + l == x exactly), the other rows zero.  Products are exact,
 // so C accumulates the whole K-range with no per-step epilogue; lane (n, 0)
 // ends with the three limb dots of row n.
+#include "gemv_bf16.hpp"
 #include "rt_common.hpp"
 #include "rt_launch.hpp"
 
@@ -150,9 +151,13 @@ __device__ __forceinline__ bf16x8 widen(const Slot& s, float d, uint32_t gsh) {
 // Workgroup of T threads: KS <= 4 runs 4 waves, TPW = 4 / KS tiles each
 // split over KS waves by blocks; larger KS runs one tile on KS waves.  LDS:
 // x limbs [K/32 steps][3][32] bf16, a zero line, then the KS partial rows.
-template <int D, int XP, int T>
+// SWIGLU: x = silu(X) * UP while it is staged (swiglu1, the BF16 GEMV's
+// form), and the finished rows are added to Y (the residual add of the MLP's
+// down projection) instead of stored.
+template <int D, int XP, int T, bool SWIGLU>
 __global__ __launch_bounds__(T) void k_gemv_q6k(const uint8_t* __restrict__ W, const float* __restrict__ X,
-                                               float* __restrict__ Y, int N, int K, int KS) {
+                                               const float* __restrict__ UP, float* __restrict__ Y, int N, int K,
+                                               int KS) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -170,13 +175,18 @@ __global__ __launch_bounds__(T) void k_gemv_q6k(const uint8_t* __restrict__ W, c
 
     // x first: unit u = (step, g) is the 8 values 8u .. 8u + 7.
     const int units = K >> 3;
-    f32x4 xa[XP], xb[XP];
+    f32x4 xa[XP], xb[XP], ua[XP], ub[XP];
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
         const int u = tid + nthr * i;
         const f32x4* src = reinterpret_cast<const f32x4*>(X) + 2 * (u < units ? u : 0);
         xa[i] = src[0];
         xb[i] = src[1];
+        if constexpr (SWIGLU) {
+            const f32x4* up = reinterpret_cast<const f32x4*>(UP) + 2 * (u < units ? u : 0);
+            ua[i] = up[0];
+            ub[i] = up[1];
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -196,6 +206,13 @@ __global__ __launch_bounds__(T) void k_gemv_q6k(const uint8_t* __restrict__ W, c
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
         const int u = tid + nthr * i;
+        if constexpr (SWIGLU) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                xa[i][e] = swiglu1(xa[i][e], ua[i][e]);
+                xb[i][e] = swiglu1(xb[i][e], ub[i][e]);
+            }
+        }
         u32x2 ha, ma, la, hb, mb, lb;
         bf16_limbs4(xa[i], ha, ma, la);
         bf16_limbs4(xb[i], hb, mb, lb);
@@ -253,7 +270,7 @@ __global__ __launch_bounds__(T) void k_gemv_q6k(const uint8_t* __restrict__ W, c
     float v = (C[0] + C[1]) + C[2];
     const int row = tile * 16 + n;
     if (KS == 1) {
-        if (lane < 16 && row < N) Y[row] = v;
+        if (lane < 16 && row < N) Y[row] = SWIGLU ? Y[row] + v : v;
     } else {
         float* red = reinterpret_cast<float*>(lds + zoff + 16);  // [tpw][KS][16], tpw * KS <= 16
         float* rp = red + tslot * KS * 16;
@@ -262,30 +279,36 @@ __global__ __launch_bounds__(T) void k_gemv_q6k(const uint8_t* __restrict__ W, c
         if (ks == 0 && lane < 16 && row < N) {
             float sum = rp[lane];
             for (int q = 1; q < KS; ++q) sum += rp[q * 16 + lane];
-            Y[row] = sum;
+            Y[row] = SWIGLU ? Y[row] + sum : sum;
         }
     }
 }
 
 template <int D, int XP, int T>
-hipError_t run(const void* w, const float* x, float* y, int64_t n, int64_t k, int ks, hipStream_t s) {
+hipError_t run(const void* w, const float* x, const float* up, float* y, int64_t n, int64_t k, int ks,
+               hipStream_t s) {
     const int64_t tiles = (n + 15) / 16;
     const int waves = ks <= 4 ? 4 : ks;
     const int tpw = waves / ks;
     const int64_t wgs = (tiles + tpw - 1) / tpw;
-    hipLaunchKernelGGL((k_gemv_q6k<D, XP, T>), dim3(static_cast<unsigned>(wgs)), dim3(static_cast<unsigned>(waves * kWave)),
-                       q6k_gemv_lds_bytes(k), s, static_cast<const uint8_t*>(w), x, y, static_cast<int>(n),
-                       static_cast<int>(k), ks);
+    const dim3 g(static_cast<unsigned>(wgs)), b(static_cast<unsigned>(waves * kWave));
+    const auto* wb = static_cast<const uint8_t*>(w);
+    const int in = static_cast<int>(n), ik = static_cast<int>(k);
+    if (up)
+        hipLaunchKernelGGL((k_gemv_q6k<D, XP, T, true>), g, b, q6k_gemv_lds_bytes(k), s, wb, x, up, y, in, ik, ks);
+    else
+        hipLaunchKernelGGL((k_gemv_q6k<D, XP, T, false>), g, b, q6k_gemv_lds_bytes(k), s, wb, x, up, y, in, ik, ks);
     return hipGetLastError();
 }
 
 template <int D, int T>
-hipError_t run_xp(const void* w, const float* x, float* y, int64_t n, int64_t k, int ks, hipStream_t s) {
+hipError_t run_xp(const void* w, const float* x, const float* up, float* y, int64_t n, int64_t k, int ks,
+                  hipStream_t s) {
     const int waves = ks <= 4 ? 4 : ks;
     const int64_t per = (k / 8 + waves * kWave - 1) / (waves * kWave);  // 8-value units of x per thread
-    if (per <= 1) return run<D, 1, T>(w, x, y, n, k, ks, s);
-    if (per <= 2) return run<D, 2, T>(w, x, y, n, k, ks, s);
-    return run<D, 4, T>(w, x, y, n, k, ks, s);
+    if (per <= 1) return run<D, 1, T>(w, x, up, y, n, k, ks, s);
+    if (per <= 2) return run<D, 2, T>(w, x, up, y, n, k, ks, s);
+    return run<D, 4, T>(w, x, up, y, n, k, ks, s);
 }
 
 }  // namespace
@@ -317,7 +340,8 @@ hipError_t launch_q6k_to_bf16(const void* blocks, uint16_t* dst, int64_t n, int6
 // four VALU per weight), so it wants more waves than the streaming GEMVs:
 // splits above 4 run one tile on KS waves with a two-slot ring (<= 128 VGPRs,
 // four waves per SIMD).
-hipError_t launch_gemv_q6k(const void* tiled, const float* x, float* y, int64_t n, int64_t k, hipStream_t s) {
+hipError_t launch_gemv_q6k(const void* tiled, const float* x, float* y, int64_t n, int64_t k, hipStream_t s,
+                           const float* up) {
     if (k % 256 != 0 || k > kMaxK) return hipErrorInvalidValue;
     const int64_t nb = k / 256, tiles = (n + 15) / 16, cus = device_info().cus;
     static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16};
@@ -333,8 +357,8 @@ hipError_t launch_gemv_q6k(const void* tiled, const float* x, float* y, int64_t 
     if (const int forced = tune_param("Q6K_KS", 0))
         for (int c : kSplits)
             if (c == forced && nb % c == 0 && c != 3) ks = c;
-    if (ks <= 4) return run_xp<4, kThreads>(tiled, x, y, n, k, ks, s);
-    return run_xp<2, kMaxThreads>(tiled, x, y, n, k, ks, s);
+    if (ks <= 4) return run_xp<4, kThreads>(tiled, x, up, y, n, k, ks, s);
+    return run_xp<2, kMaxThreads>(tiled, x, up, y, n, k, ks, s);
 }
 
 }  // namespace rt_hip

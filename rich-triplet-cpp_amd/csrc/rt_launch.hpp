@@ -139,7 +139,10 @@ size_t q6k_gemv_lds_bytes(int64_t k);
 int64_t q6k_tiled_bytes(int64_t n, int64_t k);
 hipError_t launch_q6k_tile(const void* blocks, void* tiled, int64_t n, int64_t k, hipStream_t s);
 hipError_t launch_q6k_to_bf16(const void* blocks, uint16_t* dst, int64_t n, int64_t k, hipStream_t s);
-hipError_t launch_gemv_q6k(const void* tiled, const float* x, float* y, int64_t n, int64_t k, hipStream_t s);
+// With `up`: y += W . (silu(x) * up) (the MLP's down projection and its
+// residual add).
+hipError_t launch_gemv_q6k(const void* tiled, const float* x, float* y, int64_t n, int64_t k, hipStream_t s,
+                           const float* up = nullptr);
 
 // The fused BF16 GEMV + argmax writes one partial key per workgroup
 // (bf16_argmax_partials(n, k) of them); launch_argmax_reduce folds them.

@@ -56,6 +56,7 @@ _SIGNATURES = {
     "rt_hip_gemv_q4k_tiled_residual": [_vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_swiglu_residual": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_gemv_bf16_swiglu_residual": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
+    "rt_hip_gemv_q6k_tiled_swiglu_residual": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_rmsnorm_rope": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp,
                                            C.c_float, _i32, _vp, _i32, _i32, _i32, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_bf16_rmsnorm": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp, _i64,
@@ -369,10 +370,12 @@ def gemv_q4k_tiled_residual(w, x, resid, n: int, k: int, stream=None):
     return resid
 
 
-def gemv_swiglu_residual(fmt: int, w, gate, up, resid, n: int, k: int, stream=None):
-    """resid += W . (silu(gate) * up), W tiled Q4_K (fmt Q4K) or BF16 bits."""
+def gemv_swiglu_residual(fmt: int, w, gate, up, resid, n: int, k: int, stream=None, q6k: bool = False):
+    """resid += W . (silu(gate) * up), W tiled Q4_K (fmt Q4K), BF16 bits, or
+    a tiled Q6_K copy (q6k=True)."""
     _dev_check(w, gate, up, resid)
-    name = "rt_hip_gemv_q4k_tiled_swiglu_residual" if fmt == Q4K else "rt_hip_gemv_bf16_swiglu_residual"
+    name = ("rt_hip_gemv_q6k_tiled_swiglu_residual" if q6k else
+            "rt_hip_gemv_q4k_tiled_swiglu_residual" if fmt == Q4K else "rt_hip_gemv_bf16_swiglu_residual")
     library().call(name, _ptr(w), _ptr(gate), _ptr(up), _ptr(resid), n, k, _stream(stream))
     return resid
 

@@ -69,6 +69,41 @@ def test_q6k_gemv_matches_widened_bf16(rt, orc, n, k, note):
     assert normwise_err(y, y_bf16) <= GEMV_TOL
 
 
+@pytest.mark.parametrize("n,k", [(3072, 8192), (1000, 2304), (16, 256)])
+def test_q6k_swiglu_residual(rt, orc, n, k):
+    """resid += W . (silu(gate) * up) on the Q6_K bytes (the down projection
+    and residual add of transformer5.cpp:186-190, 205-212) against the
+    oracle's composition (swiglu, then the BF16 product on the widened
+    weights, plus resid) at the GEMV bar, and against this library's BF16
+    swiglu-residual on the widened copy.  K splits 8 (3072 x 8192), 1
+    (16 x 256, a single tile) and 9 blocks unsplit (1000 x 2304)."""
+    say(f"[q6k swiglu residual] N={n} K={k}")
+    rng = np.random.default_rng(3 * n + k)
+    blocks = random_q6k(rng, n, k)
+    w = widened(orc, blocks, n, k)
+    gate = (rng.standard_normal(k) * 2).astype(np.float32)
+    up = rng.standard_normal(k).astype(np.float32)
+    r0 = rng.standard_normal(n).astype(np.float32)
+    want = r0 + orc.bf16_matmul_t(w, orc.swiglu(gate, up).reshape(1, k)).reshape(-1)
+    tiled = rt.q6k_tile(to_dev(blocks), n, k)
+    resid = to_dev(r0)
+    rt.gemv_swiglu_residual(None, tiled, to_dev(gate), to_dev(up), resid, n, k, q6k=True)
+    got = from_dev(resid)
+    assert normwise_err(got, want) <= GEMV_TOL, normwise_err(got, want)
+    rb = to_dev(r0)
+    rt.gemv_swiglu_residual(rt.BF16, to_dev(w.view(np.int16)), to_dev(gate), to_dev(up), rb, n, k)
+    assert normwise_err(got, from_dev(rb)) <= GEMV_TOL
+    # gate = 0 makes silu(gate) * up zero: resid comes back unchanged, bit for bit
+    rz = to_dev(r0)
+    rt.gemv_swiglu_residual(None, tiled, to_dev(np.zeros(k, np.float32)), to_dev(up), rz, n, k, q6k=True)
+    assert np.array_equal(from_dev(rz).view(np.uint32), r0.view(np.uint32))
+    # an aliased residual is refused
+    lib = rt.library()
+    g = to_dev(gate)
+    assert lib.status("rt_hip_gemv_q6k_tiled_swiglu_residual", tiled.data_ptr(), g.data_ptr(), g.data_ptr(),
+                      g.data_ptr(), n, k, None) != 0
+
+
 def test_q6k_gemv_one_hot_is_exact(rt, orc):
     """x = e_c gives y = W[:, c], the widened bf16 weight exactly (a -0
     weight gives +0, as the reference's sum that starts from 0.0f does)."""
