@@ -563,6 +563,9 @@ def bench_engine(args, rt, torch, model: str):
     cfg = dict(ENGINE_MODELS[model])
     ctx = args.context
     cfg["max_seq"] = ctx + args.warmup + args.steps + 1
+    q6_down = args.mix == "q4km_q6k" and cfg["arch"] != 1
+    if q6_down:
+        cfg["max_batch"] = 0  # a Q6_K down is single-token only
     dec = rt.Decoder(**cfg)
     g = torch.Generator(device="cuda").manual_seed(0)
     H, F, nq, nkv, d, V, L = (cfg[k] for k in ("hidden", "ffn", "n_heads", "n_kv_heads", "head_dim", "vocab",
@@ -587,8 +590,15 @@ def bench_engine(args, rt, torch, model: str):
                                       ("v", rt.T_V, nkv * d, H, wide), ("o", rt.T_O, H, nq * d, False),
                                       ("gate", rt.T_GATE, F, H, False), ("up", rt.T_UP, F, H, False),
                                       ("down", rt.T_DOWN, H, F, wide)]:
-            arr = bf(n, k) if use_bf else q4(n, k)
-            dec.set(li, t, rt.BF16 if use_bf else rt.Q4K, arr)
+            if use_bf and q6_down and name == "down":
+                # GGUF Q6_K bytes kept native: random quants and scales, d = 2^-14
+                arr = torch.randint(0, 256, (n * (k // 256), 210), dtype=torch.uint8, generator=g,
+                                    device="cuda").cpu().numpy()
+                arr[:, 208], arr[:, 209] = 0x00, 0x04
+                dec.set(li, t, rt.Q6K, arr)
+            else:
+                arr = bf(n, k) if use_bf else q4(n, k)
+                dec.set(li, t, rt.BF16 if use_bf else rt.Q4K, arr)
             wbytes += arr.nbytes
         dec.set(li, rt.T_ATTN_NORM, rt.F32, norm(H))
         dec.set(li, rt.T_FFN_NORM, rt.F32, norm(H))
@@ -626,7 +636,8 @@ def bench_engine(args, rt, torch, model: str):
     dec.close()
     return line(args, f"decode engine whole-token latency, {model}", round(us, 2), "us/token", wall * 1e3, False,
                 "q4_k/bf16 weights, f32 activations, " + ("f16" if cfg["kv_f16"] else "f32") + " KV cache",
-                {"workload": f"decode engine (rt_hip_decoder_step), {model}, context {ctx}",
+                {"workload": f"decode engine (rt_hip_decoder_step), {model}, context {ctx}"
+                             + (", Q6_K down projections kept native" if q6_down else ""),
                  "gemv_weight_bytes_per_token": wbytes, "weight_gbs": round(gbs, 1),
                  "includes": "embedding, all layers (norms, q/k/v, RoPE, KV append, attention, o, MLP), final "
                              "norm, lm_head, argmax, the position upload and the host synchronisation"},

@@ -64,7 +64,8 @@ typedef enum {
     RT_HIP_BF16 = 1,
     RT_HIP_Q4K = 2,
     RT_HIP_Q4_0 = 3,
-    RT_HIP_Q4MAT = 4
+    RT_HIP_Q4MAT = 4,
+    RT_HIP_Q6K = 5   /* GGUF Q6_K blocks: the decode engine's Llama down projection (rt_hip_decoder_set_tensor) */
 } rt_hip_format;
 
 /* Largest activation batch the GEMV kernels take; the reference's

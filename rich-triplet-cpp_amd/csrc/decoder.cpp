@@ -15,7 +15,8 @@
 // transformer5.cpp:152-212 (RMSNorm, q/k/v, RoPE, attention, o + residual,
 // RMSNorm, gate/up, SwiGLU, down + residual).  Projection weights are Q4_K or
 // BF16, as the Metal engine's upload_linear_detect_type (metal_decode.mm:
-// 157-176) allows.
+// 157-176) allows; a Llama down projection may also keep its GGUF Q6_K bytes
+// (the reference widens them to BF16 at load).
 //
 // Single-token step: the library's fused launches where the formats allow
 // (RMSNorm inside the q/k/v and gate/up GEMVs' activation staging; the Llama
@@ -102,6 +103,7 @@ int64_t format_bytes(int32_t f, int64_t n, int64_t k) {
     if (f == RT_HIP_Q4K) return k % 256 ? -1 : n * (k / 256) * 144;
     if (f == RT_HIP_BF16) return n * k * 2;
     if (f == RT_HIP_F32) return n * k * 4;
+    if (f == RT_HIP_Q6K) return k % 256 ? -1 : n * (k / 256) * 210;
     return -1;
 }
 
@@ -265,6 +267,8 @@ int layer_step1(rt_hip_decoder* d, int li, hipStream_t s) {
     if (!d->gemma) {
         if (L.down.q4k())
             return rt_hip_gemv_q4k_tiled_swiglu_residual(L.down.tiled, d->gate, d->up, d->hidden, H, F, s);
+        if (L.down.format == RT_HIP_Q6K)
+            return rt_hip_gemv_q6k_tiled_swiglu_residual(L.down.tiled, d->gate, d->up, d->hidden, H, F, s);
         return rt_hip_gemv_bf16_swiglu_residual(static_cast<const uint16_t*>(L.down.data), d->gate, d->up, d->hidden,
                                                 H, F, s);
     }
@@ -620,10 +624,16 @@ int rt_hip_decoder_set_tensor(rt_hip_decoder* d, int32_t layer, int32_t tensor, 
         return upload(reinterpret_cast<void**>(dst), n * 4);
     };
     auto proj = [&](Proj& p, int64_t n, int64_t k) -> int {
-        if (format != RT_HIP_Q4K && format != RT_HIP_BF16)
-            return fail(RT_HIP_E_UNSUPPORTED, std::string(fn) + ": projections are Q4_K or BF16");
+        // A Q6_K down projection stays in its GGUF bytes (tiled once here)
+        // instead of the reference's load-time widening: Llama's SwiGLU down
+        // + residual, single-token steps only (no batched Q6_K GEMV).
+        const bool q6_ok = tensor == RT_HIP_T_DOWN && !d->gemma && c.max_batch <= 1;
+        if (format != RT_HIP_Q4K && format != RT_HIP_BF16 && !(format == RT_HIP_Q6K && q6_ok))
+            return fail(RT_HIP_E_UNSUPPORTED, std::string(fn) + ": projections are Q4_K or BF16 (Q6_K: a Llama "
+                                                                "down projection with max_batch <= 1)");
         const int64_t need = format_bytes(format, n, k);
-        if (need < 0) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": Q4_K needs k % 256 == 0");
+        if (need < 0) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": Q4_K and Q6_K need k % 256 == 0");
+        if (format == RT_HIP_Q6K && k > 8192) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": Q6_K k above 8192");
         if (p.set() && p.format != format) {  // format change: fresh buffers
             p.data = nullptr;
             p.tiled = nullptr;
@@ -632,12 +642,14 @@ int rt_hip_decoder_set_tensor(rt_hip_decoder* d, int32_t layer, int32_t tensor, 
         p.n = n;
         p.k = k;
         int rc = upload(&p.data, need);
-        if (rc || format != RT_HIP_Q4K) return rc;
+        if (rc || (format != RT_HIP_Q4K && format != RT_HIP_Q6K)) return rc;
+        const bool q6 = format == RT_HIP_Q6K;
         if (!p.tiled) {
-            hipError_t er = dev_alloc(d, &p.tiled, static_cast<size_t>(rt_hip_q4k_tiled_bytes(n, k)));
+            const int64_t tb = q6 ? rt_hip_q6k_tiled_bytes(n, k) : rt_hip_q4k_tiled_bytes(n, k);
+            hipError_t er = dev_alloc(d, &p.tiled, static_cast<size_t>(tb));
             if (er != hipSuccess) return hip_fail(er, fn);
         }
-        rc = rt_hip_q4k_tile(p.data, p.tiled, n, k, nullptr);
+        rc = q6 ? rt_hip_q6k_tile(p.data, p.tiled, n, k, nullptr) : rt_hip_q4k_tile(p.data, p.tiled, n, k, nullptr);
         if (!rc) rc = chk(hipDeviceSynchronize(), fn);
         return rc;
     };

@@ -18,7 +18,7 @@ ROOT = os.path.dirname(HERE)
 LIB_PATH = os.environ.get("RT_HIP_LIB_PATH", os.path.join(HERE, "lib", "librt_hip.so"))
 HEADER_PATH = os.path.join(ROOT, "include", "rt_hip.h")
 
-F32, BF16, Q4K, Q4_0, Q4MAT = 0, 1, 2, 3, 4
+F32, BF16, Q4K, Q4_0, Q4MAT, Q6K = 0, 1, 2, 3, 4, 5
 GEMV_MAX_M = 8
 
 _vp, _i64, _i32 = C.c_void_p, C.c_int64, C.c_int32

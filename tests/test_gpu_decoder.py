@@ -32,7 +32,7 @@ STEP_TOL = 1e-5
 class Model:
     """Weights on the host and the oracle's decode step."""
 
-    def __init__(self, orc, arch, rng, **cfg):
+    def __init__(self, orc, arch, rng, q6k_down=False, **cfg):
         self.orc, self.arch, self.cfg = orc, arch, cfg
         self.gemma = arch == "gemma3"
         H, F, nq, nkv, d, V = (cfg[k] for k in ("hidden", "ffn", "n_heads", "n_kv_heads", "head_dim", "vocab"))
@@ -40,6 +40,13 @@ class Model:
         self.w = {}
 
         def proj(name, n, k, bf16):
+            if bf16 == "q6k":  # GGUF Q6_K bytes; the oracle multiplies their bf16 widening
+                from test_gpu_q6k import random_q6k
+                self.w[name] = random_q6k(rng, n, k)
+                self.fmt[name] = "q6k"
+                self.wide_q6k = getattr(self, "wide_q6k", {})
+                self.wide_q6k[name] = orc.f32_to_bf16_n(orc.q6k_decode(self.w[name], n * k)).reshape(n, k)
+                return
             w32 = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
             if bf16:
                 self.w[name] = orc.f32_to_bf16_n(w32).reshape(n, k)
@@ -61,7 +68,7 @@ class Model:
             proj(f"{li}.o", H, nq * d, False)
             proj(f"{li}.gate", F, H, False)
             proj(f"{li}.up", F, H, False)
-            proj(f"{li}.down", H, F, wide)
+            proj(f"{li}.down", H, F, "q6k" if wide and q6k_down else wide)
             for nm in ("attn_norm", "ffn_norm") + (("post_attn_norm", "post_ffn_norm") if self.gemma else ()):
                 norm(f"{li}.{nm}", H)
             if self.gemma:
@@ -79,7 +86,7 @@ class Model:
         c = dict(self.cfg)
         c["arch"] = rt.ARCH_GEMMA3 if self.gemma else rt.ARCH_LLAMA
         dec = rt.Decoder(**c)
-        F = {"q4k": rt.Q4K, "bf16": rt.BF16}
+        F = {"q4k": rt.Q4K, "bf16": rt.BF16, "q6k": rt.Q6K}
         T = {"q": rt.T_Q, "k": rt.T_K, "v": rt.T_V, "o": rt.T_O, "gate": rt.T_GATE, "up": rt.T_UP,
              "down": rt.T_DOWN, "attn_norm": rt.T_ATTN_NORM, "ffn_norm": rt.T_FFN_NORM,
              "post_attn_norm": rt.T_POST_ATTN_NORM, "post_ffn_norm": rt.T_POST_FFN_NORM,
@@ -99,6 +106,8 @@ class Model:
     def mm(self, name, x, n, k):
         if self.fmt[name] == "q4k":
             return self.orc.q4k_matmul_t(self.w[name], n, k, x.reshape(1, k)).reshape(-1)
+        if self.fmt[name] == "q6k":
+            return self.orc.bf16_matmul_t(self.wide_q6k[name], x.reshape(1, k)).reshape(-1)
         return self.orc.bf16_matmul_t(self.w[name], x.reshape(1, k)).reshape(-1)
 
     def step(self, token, pos):
@@ -203,6 +212,32 @@ def test_decoder_batch_matches_single_steps(rt, orc, arch, cfg):
         assert e <= STEP_TOL, (i, e)
     a.close()
     b.close()
+
+
+def test_decoder_q6k_down_matches_oracle(rt, orc):
+    """A Llama down projection kept as GGUF Q6_K (layer 0; the reference
+    widens it to BF16 at load) through rt_hip_gemv_q6k_tiled_swiglu_residual
+    inside the token's graph: logits against the oracle's step on the widened
+    weights, token by token.  Batch graphs take no Q6_K down: refused."""
+    cfg = dict(LLAMA, max_batch=0)
+    say("[decoder q6k down] llama, 6 tokens")
+    m = Model(orc, "llama", np.random.default_rng(77), q6k_down=True, **cfg)
+    assert m.fmt["0.down"] == "q6k" and m.fmt["1.down"] == "q4k"
+    dec = m.load(rt)
+    try:
+        for pos, tok in enumerate([5, 17, 999, 0, 42, 7]):
+            got = dec.step(tok, pos)
+            want = m.step(tok, pos)
+            err = normwise_err(got, want)
+            assert err <= STEP_TOL, (pos, err)
+    finally:
+        dec.close()
+    bad = rt.Decoder(**dict(LLAMA, arch=rt.ARCH_LLAMA))  # max_batch 4
+    try:
+        with pytest.raises(RuntimeError):
+            bad.set(0, rt.T_DOWN, rt.Q6K, m.w["0.down"])
+    finally:
+        bad.close()
 
 
 def test_decoder_rejects_bad_use(rt, orc):
