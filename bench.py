@@ -1015,6 +1015,125 @@ def bench_flux_attention(args, rt, torch):
                 roof, cpu, data="synthetic: N(0,1) q, k, v")
 
 
+# ------------------------------------------------- launch-ceiling calibration --
+
+def token_launch_bytes(mix: str):
+    """Algorithmic bytes of each launch of the headline token, in order: per
+    layer q/k/v (one launch; a BF16-widened v included), o, gate+up, down,
+    then the lm_head -- the byte counts DecodeModel.launches() reads."""
+    def q4(n, k):
+        return n * (k // 256) * 144
+
+    out = []
+    for layer in range(LAYERS):
+        wide = mix in ("q4km", "q4km_q6k") and layer in WIDENED_LAYERS
+        v = KV * HIDDEN * 2 if wide else q4(KV, HIDDEN)
+        if wide and mix == "q4km_q6k":
+            down = HIDDEN * (FFN // 256) * 210
+        else:
+            down = HIDDEN * FFN * 2 if wide else q4(HIDDEN, FFN)
+        out.append(("qkv_bf16v" if wide else "qkv",
+                    q4(HIDDEN, HIDDEN) + q4(KV, HIDDEN) + v + 4 * HIDDEN + 4 * (HIDDEN + 2 * KV),
+                    4 * (HIDDEN + 2 * KV)))
+        out.append(("o", q4(HIDDEN, HIDDEN) + 8 * HIDDEN, 4 * HIDDEN))
+        out.append(("gate_up", 2 * q4(FFN, HIDDEN) + 4 * HIDDEN + 8 * FFN, 8 * FFN))
+        out.append(("down_bf16" if wide else "down", down + 4 * FFN + 4 * HIDDEN, 4 * HIDDEN))
+    out.append(("lm_head", q4(VOCAB, HIDDEN) + 4 * HIDDEN + 4 * VOCAB, 4 * VOCAB))
+    return out
+
+
+def bench_ceiling(args, rt, torch):
+    """What the headline's launch structure allows with no GEMV arithmetic at
+    all.  The token's 113 launches keep their order, their byte counts and
+    their dependencies (one stream, one hipGraph), but each launch is a plain
+    streaming read of its bytes from a buffer of its own
+    (rt_hip_probe_read), so nothing is reused across launches and the whole
+    token (2.38 GB) exceeds the 256 MB MALL.  Read shapes: several workgroup
+    counts; per-launch figures: a graph of the token's launches of one kind
+    alone.  Also N dependent empty launches in one graph (the fixed cost of a
+    launch) and one read of all the token's bytes in a single launch (the
+    bandwidth the device gives with no launch boundaries)."""
+    plan = token_launch_bytes(args.mix)
+    align = 4096
+    offs, total = [], 0
+    for _, b, _ in plan:
+        offs.append(total)
+        total += (b + align - 1) // align * align
+    buf = torch.randint(-2**31, 2**31 - 1, (total // 4,), dtype=torch.int32, device="cuda")
+    sink = torch.zeros(max(65536, VOCAB), dtype=torch.int32, device="cuda")
+    nbytes = sum(b for _, b, _ in plan)
+    log(f"[bench] ceiling: {len(plan)} launches, {nbytes / 1e9:.3f} GB/token ({args.mix})")
+
+    def reads(sel, wgs, write=True):
+        # each launch reads its bytes, then writes its output rows (a GEMV's
+        # y); write=False: reads alone
+        def run():
+            for i in sel:
+                b = plan[i][1] // 16 * 16
+                rt.probe_read(buf[offs[i] // 4:], b, wgs(b), sink, plan[i][2] if write else 0)
+        return run
+
+    read_shapes = {"256 workgroups": lambda b: 256, "512 workgroups": lambda b: 512,
+                   "1024 workgroups": lambda b: 1024, "2048 workgroups": lambda b: 2048,
+                   "one workgroup per 16 KB": lambda b: max(256, min(65536, b // 16384)),
+                   "one workgroup per 64 KB": lambda b: max(256, min(65536, b // 65536))}
+    shapes = {}
+    for name, wgs in read_shapes.items():
+        ms, _ = time_graph(torch, reads(range(len(plan)), wgs), args.warmup, args.steps)
+        shapes[name] = round(ms * 1e3, 2)
+        log(f"[bench] token as plain reads, {name}: {ms * 1e3:.1f} us/token "
+            f"({nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
+    best_name = min(shapes, key=shapes.get)
+    best_us = shapes[best_name]
+    ms, _ = time_graph(torch, reads(range(len(plan)), read_shapes[best_name], write=False), args.warmup, args.steps)
+    reads_only_us = round(ms * 1e3, 2)
+    log(f"[bench] token as plain reads with no output writes ({best_name}): {reads_only_us} us/token")
+    # per kind: the token's launches of one kind alone, back to back, best shape per kind
+    per_kind = {}
+    for kind in dict.fromkeys(k for k, _, _ in plan):
+        sel = [i for i, (k, _, _) in enumerate(plan) if k == kind]
+        best = None
+        for name, fn in read_shapes.items():
+            ms, _ = time_graph(torch, reads(sel, fn), args.warmup, args.steps)
+            us = ms * 1e3 / len(sel)
+            if best is None or us < best[0]:
+                best = (us, name)
+        b = plan[sel[0]][1]
+        per_kind[kind] = {"bytes": b, "launches": len(sel), "us_per_launch": round(best[0], 3),
+                          "gbs": round(b / (best[0] * 1e-6) / 1e9, 1), "shape": best[1]}
+        log(f"[bench] {kind}: {b / 1e6:.2f} MB per launch, {best[0]:.2f} us ({best[1]})")
+    # fixed cost of a dependent launch
+    empty = {}
+    for wg, th in [(1, 64), (256, 256), (1024, 256)]:
+        def run(wg=wg, th=th):
+            for _ in range(len(plan)):
+                rt.probe_empty(wg, th)
+        ms, _ = time_graph(torch, run, args.warmup, args.steps)
+        empty[f"{wg}x{th}"] = round(ms * 1e3 / len(plan), 3)
+        log(f"[bench] empty launch {wg}x{th}: {ms * 1e3 / len(plan):.3f} us per dependent launch")
+    # the whole token's bytes in one read
+    one = {}
+    for wg in (1024, 4096, 16384):
+        ms, _ = time_graph(torch, lambda wg=wg: rt.probe_read(buf, total, wg, sink, 0), args.warmup, args.steps)
+        one[str(wg)] = round(ms * 1e3, 2)
+    one_us = min(one.values())
+    log(f"[bench] all {total / 1e9:.3f} GB in one launch: {one_us:.1f} us "
+        f"({total / (one_us * 1e-6) / 1e9:.0f} GB/s)")
+    gbs = nbytes / (best_us * 1e-6) / 1e9
+    return line(args, "decode-step launch ceiling: us/token of the headline's 113 launches as plain reads",
+                best_us, "us/token", best_us / 1e3, False, "u8 (reads only)",
+                {"workload": "the headline token's launch sequence (Llama-3.2-3B, " + args.mix +
+                             "), each launch a plain read of its byte count, one hipGraph",
+                 "launches_per_token": len(plan), "bytes_per_token": nbytes,
+                 "gbs": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+                 "best_shape": best_name, "us_per_token_by_shape": shapes,
+                 "us_per_token_reads_only": reads_only_us, "per_kind": per_kind,
+                 "empty_launch_us": empty,
+                 "one_launch_read": {"bytes": total, "us_by_workgroups": one,
+                                     "gbs": round(total / (one_us * 1e-6) / 1e9, 1)}},
+                None, None, data="synthetic: random bytes, read only")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[1])
     ap.add_argument("--gpus", type=int, default=1)
@@ -1023,7 +1142,7 @@ def main() -> int:
     ap.add_argument("--workload", default="llama_decode",
                     choices=["llama_decode", "q4k_gemv", "q4_0_gemv", "bf16_lm_head", "prefill",
                              "flux", "flux_attention", "layer_ops", "decode_layers", "engine_llama3b", "engine_gemma3_4b",
-                             "q8_gemv", "q6k_gemv", "q4mat_gemv", "batch_gemv"])
+                             "q8_gemv", "q6k_gemv", "q4mat_gemv", "batch_gemv", "ceiling"])
     ap.add_argument("--mix", default="q4km", choices=["q4km", "q4k", "q4km_q6k"])
     ap.add_argument("--context", type=int, default=1024,
                     help="cached positions for --workload decode_layers")
@@ -1087,6 +1206,8 @@ def main() -> int:
         out = bench_engine(args, rt, torch, args.workload[len("engine_"):])
     elif args.workload in ("q8_gemv", "q6k_gemv", "q4mat_gemv", "batch_gemv"):
         out = bench_path_gemv(args, rt, torch, args.workload)
+    elif args.workload == "ceiling":
+        out = bench_ceiling(args, rt, torch)
     elif args.workload == "flux":
         out = bench_gemm(args, rt, torch, [(4608, 9216, 3072), (4608, 12288, 3072), (4608, 3072, 12288)],
                          "config 5 FLUX linears M=4608 (QKV, MLP-in, MLP-out)", True,

@@ -636,6 +636,20 @@ int rt_hip_decoder_destroy(rt_hip_decoder* dec);
 int rt_hip_linear_forward(int32_t format, const void* w, const float* bias, const float* x,
                           float* y, int64_t m, int64_t n, int64_t k, rt_hip_stream stream);
 
+/* ---- launch-ceiling calibration --------------------------------------------
+ * No counterpart in the reference: two kernels that do none of the path's
+ * arithmetic, so that a graph of the decode step's launch sequence built
+ * from them measures what the launch structure itself allows on the device.
+ * rt_hip_probe_read streams `bytes` (a multiple of 16) of `buf` with 16-byte
+ * loads over about `workgroups` workgroups of 256 threads, then writes
+ * `out_bytes` (a multiple of 4) of `out` from what it read, as a GEMV stores
+ * its rows; with out_bytes 0 it writes nothing (out then needs one u32 per
+ * workgroup, named only so the loads stay live).
+ * rt_hip_probe_empty launches an empty kernel of the given shape. */
+int rt_hip_probe_read(const void* buf, int64_t bytes, int32_t workgroups, uint32_t* out, int64_t out_bytes,
+                      rt_hip_stream stream);
+int rt_hip_probe_empty(int32_t workgroups, int32_t threads, rt_hip_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -113,12 +113,31 @@ hipError_t dev_alloc(rt_hip_decoder* d, void** p, size_t bytes) {
     return e;
 }
 
+// Frees one of the decoder's allocations (no captured graph may still use it).
+void dev_free(rt_hip_decoder* d, void** p) {
+    if (!*p) return;
+    for (auto it = d->allocations.begin(); it != d->allocations.end(); ++it)
+        if (*it == *p) {
+            d->allocations.erase(it);
+            break;
+        }
+    (void)hipFree(*p);
+    *p = nullptr;
+}
+
 template <typename T>
 hipError_t dev_alloc_t(rt_hip_decoder* d, T** p, size_t count) {
     void* v = nullptr;
     hipError_t e = dev_alloc(d, &v, count * sizeof(T));
     *p = static_cast<T*>(v);
     return e;
+}
+
+// A window of max_seq positions or more covers every position a step can
+// reach (pos < max_seq), so it is no window: 0.  The attention's split count
+// and its partials buffer then both follow max_seq.
+int clamp_window(const rt_hip_decoder_config& c) {
+    return c.sliding_window >= c.max_seq ? 0 : c.sliding_window;
 }
 
 bool is_global_layer(const rt_hip_decoder_config& c, int i) {
@@ -140,6 +159,20 @@ int gemvm(const Proj& p, const float* x, float* y, int m, hipStream_t s) {
     if (m == 1) return gemv1(p, x, y, s);
     if (p.q4k()) return rt_hip_gemv_q4k(p.data, x, y, p.n, p.k, m, s);
     return rt_hip_gemv_bf16(static_cast<const uint16_t*>(p.data), x, y, p.n, p.k, m, s);
+}
+
+// Split count of a layer's attention for m rows: the window bounds the
+// positions a row reads, else the cache length.  The partials buffer was
+// sized at create for the cache length, and create clamps every window to
+// below max_seq, so the count never needs more; the check keeps a future
+// change from writing past the buffer.
+int attn_splits(const rt_hip_decoder* d, const Layer& L, int m, int* splits) {
+    const auto& c = d->cfg;
+    const int S = attention2_splits(c.n_kv_heads, m, L.window > 0 ? L.window : c.max_seq);
+    if (attention2_workspace(c.n_heads, c.head_dim, S, m) > d->part_bytes)
+        return fail(RT_HIP_E_SHAPE, "decoder: attention partials exceed the buffer sized at create");
+    *splits = S;
+    return RT_HIP_OK;
 }
 
 // ---- one layer, single token ------------------------------------------------
@@ -229,7 +262,8 @@ int layer_step1(rt_hip_decoder* d, int li, hipStream_t s) {
     a.n_kv = nkv;
     a.head_dim = hd;
     a.m = 1;
-    a.splits = attention2_splits(nkv, 1, L.window > 0 ? L.window : c.max_seq);
+    rc = attn_splits(d, L, 1, &a.splits);
+    if (rc) return rc;
     a.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt(static_cast<float>(hd));
     a.f16 = c.kv_f16 != 0;
     rc = chk(launch_attention2(a, d->part, d->attn_cnt, s), "decoder: attention");
@@ -338,7 +372,8 @@ int layer_stepm(rt_hip_decoder* d, int li, int m, hipStream_t s) {
     a.n_kv = nkv;
     a.head_dim = hd;
     a.m = m;
-    a.splits = attention2_splits(nkv, m, L.window > 0 ? L.window : c.max_seq);
+    rc = attn_splits(d, L, m, &a.splits);
+    if (rc) return rc;
     a.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt(static_cast<float>(hd));
     a.f16 = c.kv_f16 != 0;
     rc = chk(launch_attention2(a, d->part, d->attn_cnt, s), "decoder: attention");
@@ -503,6 +538,7 @@ int rt_hip_decoder_create(const rt_hip_decoder_config* cfg, rt_hip_decoder** out
     if (c.max_batch < 0 || c.max_batch > RT_HIP_GEMV_MAX_M)
         return fail(RT_HIP_E_SHAPE, std::string(fn) + ": max_batch must be in [0, 8]");
     if (!(c.norm_eps >= 0.0f)) return fail(RT_HIP_E_ARG, std::string(fn) + ": norm_eps must be >= 0");
+    if (c.sliding_window < 0) return fail(RT_HIP_E_ARG, std::string(fn) + ": sliding_window must be >= 0");
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, fn);
@@ -573,7 +609,7 @@ int rt_hip_decoder_create(const rt_hip_decoder_config* cfg, rt_hip_decoder** out
             const bool global = is_global_layer(c, i);
             const float theta = global ? c.rope_theta : c.rope_theta_local;
             L.freq_scale = global ? c.rope_freq_scale : c.rope_freq_scale_local;
-            L.window = global ? 0 : c.sliding_window;
+            L.window = global ? 0 : clamp_window(c);
             for (int j = 0; j < hd / 2; ++j)
                 tab[j] = std::pow(theta, 2.0f * static_cast<float>(j) / static_cast<float>(hd));
         } else {
@@ -582,7 +618,7 @@ int rt_hip_decoder_create(const rt_hip_decoder_config* cfg, rt_hip_decoder** out
                 tab[j] = cfg->llama_inv_freq
                              ? cfg->llama_inv_freq[j]
                              : 1.0f / std::pow(c.rope_theta, 2.0f * static_cast<float>(j) / static_cast<float>(hd));
-            L.window = c.sliding_window;
+            L.window = clamp_window(c);
         }
         if ((e = dev_alloc_t(d, &L.rope_tab, hd / 2)) != hipSuccess) return cleanup(e);
         if ((e = hipMemcpy(L.rope_tab, tab.data(), tab.size() * 4, hipMemcpyHostToDevice)) != hipSuccess)
@@ -634,9 +670,16 @@ int rt_hip_decoder_set_tensor(rt_hip_decoder* d, int32_t layer, int32_t tensor, 
         const int64_t need = format_bytes(format, n, k);
         if (need < 0) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": Q4_K and Q6_K need k % 256 == 0");
         if (format == RT_HIP_Q6K && k > 8192) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": Q6_K k above 8192");
-        if (p.set() && p.format != format) {  // format change: fresh buffers
-            p.data = nullptr;
-            p.tiled = nullptr;
+        // Every check comes before the tensor changes, so a rejected call
+        // leaves the previous weight in place.
+        if (bytes != need)
+            return fail(RT_HIP_E_SHAPE, std::string(fn) + ": " + std::to_string(bytes) + " bytes given, " +
+                                            std::to_string(need) + " expected");
+        if (p.set() && p.format != format) {
+            // Format change: the old buffers are freed (the graphs that read
+            // them were destroyed above, and steps are synchronous).
+            dev_free(d, &p.data);
+            dev_free(d, &p.tiled);
         }
         p.format = format;
         p.n = n;
@@ -656,9 +699,13 @@ int rt_hip_decoder_set_tensor(rt_hip_decoder* d, int32_t layer, int32_t tensor, 
     if (tensor == RT_HIP_T_EMBED) {
         if (format != RT_HIP_BF16 && format != RT_HIP_F32)
             return fail(RT_HIP_E_UNSUPPORTED, std::string(fn) + ": the embedding is BF16 or F32");
-        if (d->embed && d->embed_format != format) d->embed = nullptr;
+        const int64_t need = format_bytes(format, c.vocab, H);
+        if (bytes != need)
+            return fail(RT_HIP_E_SHAPE, std::string(fn) + ": " + std::to_string(bytes) + " bytes given, " +
+                                            std::to_string(need) + " expected");
+        if (d->embed && d->embed_format != format) dev_free(d, &d->embed);
         d->embed_format = format;
-        return upload(&d->embed, format_bytes(format, c.vocab, H));
+        return upload(&d->embed, need);
     }
     if (tensor == RT_HIP_T_OUTPUT_NORM) return norm(&d->out_norm, H);
     if (tensor == RT_HIP_T_LM_HEAD) return proj(d->lm_head, c.vocab, H);

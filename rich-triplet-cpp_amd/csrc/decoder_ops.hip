@@ -469,9 +469,13 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
     __syncthreads();
     __shared__ uint32_t arrival;
     uint32_t* const cnt = a.cnt + static_cast<int64_t>(m) * a.n_kv + kvh;
-    if (tid == 0) arrival = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // acq_rel at agent scope: the release orders this split's partial
+    // stores before the arrival, the acquire the last arriver's loads of the
+    // other splits' partials after it.
+    if (tid == 0) arrival = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (arrival != static_cast<uint32_t>(S - 1)) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     // this thread's (query head, dim) pairs t = tid, tid + kAT, ..., all
     // merged together
     constexpr int P = (G * HD + kAT - 1) / kAT;

@@ -272,9 +272,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             }
             wait_vmcnt<0>();
             __syncthreads();
-            if (tid == 0) arrival = __hip_atomic_fetch_add(cnt + bnd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // acq_rel at agent scope: the release orders this piece's state
+            // stores before the arrival, and the acquire orders the merging
+            // piece's loads of the other state after it.
+            if (tid == 0) arrival = __hip_atomic_fetch_add(cnt + bnd, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
             __syncthreads();
             if (arrival == 0) continue;  // the other piece merges
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
             // Merge: m = max, each side scaled by exp(m_side - m).  Two terms,
             // so the result does not depend on which piece merges.
             const float* other = part + (static_cast<int64_t>(bnd) * 2 + (1 - piece)) * piece_floats<DP>();

@@ -338,9 +338,11 @@ __global__ __launch_bounds__(kThreads) void k_gemv_batch(const uint8_t* __restri
     lds_barrier();
     uint32_t* const flag = reinterpret_cast<uint32_t*>(lds);
     if (tid == 0)
-        *flag = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     lds_barrier();
     if (*flag != static_cast<uint32_t>(nslices - 1)) return;
+    // the last arriver's loads of the other slices come after their release
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
         if (!keep[q]) continue;

@@ -45,6 +45,8 @@ _SIGNATURES = {
     "rt_hip_gemm_q4k": [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "rt_hip_gemm_bf16": [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "rt_hip_linear_forward": [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "rt_hip_probe_read": [_vp, _i64, _i32, _vp, _i64, _vp],
+    "rt_hip_probe_empty": [_i32, _i32, _vp],
     "rt_hip_gemv_q4k_tiled_bf16": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp, _i64,
                                    _vp, _i64, _vp],
     "rt_hip_gemv_q4k_tiled_rmsnorm_multi": [_i32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_i64), _vp, _vp,
@@ -640,6 +642,17 @@ def linear_forward(fmt: int, w, x, n: int, k: int, bias=None, y=None, stream=Non
     library().call("rt_hip_linear_forward", fmt, _ptr(w), _ptr(bias), _ptr(x), _ptr(y), m, n, k,
                    _stream(stream))
     return y
+
+
+def probe_read(buf, nbytes: int, workgroups: int, out, out_bytes: int = 0, stream=None) -> None:
+    """rt_hip_probe_read: a plain streaming read of nbytes of buf, then
+    out_bytes of out written (calibration)."""
+    library().call("rt_hip_probe_read", _ptr(buf), nbytes, workgroups, _ptr(out), out_bytes, _stream(stream))
+
+
+def probe_empty(workgroups: int = 1, threads: int = 64, stream=None) -> None:
+    """rt_hip_probe_empty: an empty kernel launch (calibration)."""
+    library().call("rt_hip_probe_empty", workgroups, threads, _stream(stream))
 
 
 # ---------------------------------------------------------------- decoder --

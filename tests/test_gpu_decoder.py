@@ -258,3 +258,155 @@ def test_decoder_rejects_bad_use(rt, orc):
         dec.set(0, rt.T_EMBED, rt.BF16, np.zeros(10, np.uint16))  # model tensor with a layer
     dec.close()
     del C
+
+
+# ---- the attention the engine benchmarks: real head geometry, long caches ----
+# attention2_splits and the split fold (decoder_ops.hip) only take more than
+# one split once the cache is longer than one 64-position chunk per split;
+# the toy models above never get there.  These cases keep hidden, ffn and
+# vocab small but use the Llama-3.2-3B attention geometry (24 query heads
+# over 8 KV heads, head_dim 128: k_attn2_partial<128, 3>) and the Gemma 3
+# local/global geometry (8 over 4, head_dim 256, f16 cache) with caches
+# pre-filled through rt_hip_decoder_set_kv, so several splits are busy and,
+# where the cache is shorter than max_seq, some are idle.
+
+def split_rule(n_kv, m, max_len, cus):
+    """attention2_splits (decoder_ops.hip): enough (kv head, split) work-
+    groups for every CU, at least 64 positions per split."""
+    want = -(-cus // (n_kv * m))
+    by_len = -(-max_len // 64)
+    return max(1, min(want, by_len))
+
+
+def busy_rule(length, S, head_dim):
+    """Splits holding positions: chunks of ceil(len / S) positions rounded up
+    to whole rounds of the partial kernel (64 positions at head_dim 128, 32 at
+    256: 16 or 8 position groups x 4 loaded ahead)."""
+    batch = 64 if head_dim <= 128 else 32
+    chunk = -(-(-(-length // S)) // batch) * batch
+    return min(S, -(-length // chunk))
+
+
+def cu_count():
+    import torch
+    return torch.cuda.get_device_properties(0).multi_processor_count
+
+
+def prefill(m, dec, rng, rows):
+    """Random N(0,1) K/V rows 0..rows-1 in every layer, in the engine (set_kv)
+    and the oracle's cache (f16-rounded when the cache is f16, as set_kv's
+    conversion rounds them)."""
+    c = m.cfg
+    width = c["n_kv_heads"] * c["head_dim"]
+    for li in range(c["n_layers"]):
+        k = rng.standard_normal((rows, width)).astype(np.float32)
+        v = rng.standard_normal((rows, width)).astype(np.float32)
+        dec.set_kv(li, k, v, rows)
+        if c.get("kv_f16"):
+            k = m.orc.f32_to_f16_rne_n(k.reshape(-1)).view(np.float16).astype(np.float32).reshape(rows, width)
+            v = m.orc.f32_to_f16_rne_n(v.reshape(-1)).view(np.float16).astype(np.float32).reshape(rows, width)
+        m.kc[li][:rows] = k
+        m.vc[li][:rows] = v
+
+
+LLAMA_3B_ATTN = dict(LLAMA, n_heads=24, n_kv_heads=8, head_dim=128, ffn=512, max_seq=2048, max_batch=0)
+GEMMA_4B_ATTN = dict(GEMMA, n_heads=8, n_kv_heads=4, head_dim=256, ffn=512, max_seq=512, sliding_window=200,
+                     max_batch=0)
+
+
+@pytest.mark.parametrize("arch,cfg,rows", [
+    # S = 32 splits, 16 busy at 1001 positions
+    ("llama3b", LLAMA_3B_ATTN, 1000),
+    # S = 32, 2 busy
+    ("llama3b", LLAMA_3B_ATTN, 100),
+    # the bench's cache: S = 16, all busy
+    ("llama3b", dict(LLAMA_3B_ATTN, max_seq=1024), 1000),
+    # local layer: window 200 > one chunk, S = 4 (3 busy); global: S = 8 (5 busy)
+    ("gemma3_4b", GEMMA_4B_ATTN, 150),
+    # local: the window slides past position 0 (all 4 busy); global 7 of 8
+    ("gemma3_4b", GEMMA_4B_ATTN, 400),
+])
+def test_decoder_long_cache_matches_oracle(rt, orc, arch, cfg, rows):
+    gemma = arch.startswith("gemma")
+    rng = np.random.default_rng(rows + len(arch))
+    m = Model(orc, "gemma3" if gemma else "llama", rng, **cfg)
+    dec = m.load(rt)
+    cus = cu_count()
+    try:
+        prefill(m, dec, rng, rows)
+        n_kv, hd = cfg["n_kv_heads"], cfg["head_dim"]
+        windows = [cfg["sliding_window"] if gemma and li % cfg["global_every"] != cfg["global_every"] - 1 else 0
+                   for li in range(cfg["n_layers"])]
+        worst = 0.0
+        for i, tok in enumerate(rng.integers(0, cfg["vocab"], 4)):
+            pos = rows + i
+            for li, win in enumerate(windows):
+                S = split_rule(n_kv, 1, win if win else cfg["max_seq"], cus)
+                length = min(pos + 1, win) if win else pos + 1
+                busy = busy_rule(length, S, hd)
+                say(f"[decoder {arch}] pos={pos} layer {li}: window {win}, S={S} splits, {busy} busy")
+                assert S > 1 and busy >= 1
+            got, idx = dec.step(int(tok), pos, argmax=True)
+            want = m.step(int(tok), pos)
+            e = normwise_err(got, want)
+            worst = max(worst, e)
+            assert e <= STEP_TOL, (pos, e)
+            assert idx == orc.argmax_first(got), pos
+        say(f"[decoder {arch}] {rows} cached positions: worst step normwise error {worst:.2e}")
+        if arch == "llama3b" and rows == 1000 and cfg["max_seq"] == 2048:
+            # the case meant to hold idle splits does
+            S = split_rule(n_kv, 1, cfg["max_seq"], cus)
+            assert busy_rule(rows + 1, S, hd) < S
+    finally:
+        dec.close()
+
+
+def test_decoder_long_cache_batch_matches_single(rt, orc):
+    """A batch step of 4 tokens after 1000 cached positions at the
+    Llama-3.2-3B attention geometry (S = 8 splits for 4 rows) gives the
+    single-token steps' logits."""
+    cfg = dict(LLAMA_3B_ATTN, max_seq=1024, max_batch=4)
+    rng = np.random.default_rng(31)
+    m = Model(orc, "llama", rng, **cfg)
+    a, b = m.load(rt), m.load(rt)
+    try:
+        state = np.random.default_rng(5)
+        prefill(m, a, state, 1000)
+        state = np.random.default_rng(5)
+        prefill(m, b, state, 1000)
+        tokens = rng.integers(0, cfg["vocab"], 4)
+        S = split_rule(cfg["n_kv_heads"], 4, cfg["max_seq"], cu_count())
+        say(f"[decoder llama3b batch] 4 tokens at position 1000, S={S}")
+        assert S > 1
+        single = []
+        for i, tok in enumerate(tokens):
+            single.append(a.step(int(tok), 1000 + i))
+            want = m.step(int(tok), 1000 + i)
+            assert normwise_err(single[-1], want) <= STEP_TOL, i
+        batch = b.step_batch(tokens, 1000)
+        for i in range(4):
+            e = normwise_err(batch[i], single[i])
+            assert e <= STEP_TOL, (i, e)
+    finally:
+        a.close()
+        b.close()
+
+
+def test_decoder_window_beyond_cache_matches_oracle(rt, orc):
+    """A sliding window longer than the cache (1024 > max_seq 512) covers every
+    position a step reaches: the engine treats it as no window, so its split
+    count (and the partials it stores) follow max_seq, never the window."""
+    cfg = dict(GEMMA_4B_ATTN, sliding_window=1024, max_batch=0)
+    rng = np.random.default_rng(1024)
+    m = Model(orc, "gemma3", rng, **cfg)
+    dec = m.load(rt)
+    try:
+        prefill(m, dec, rng, 300)
+        for i, tok in enumerate([3, 999, 0]):
+            say(f"[decoder gemma3 window 1024 > max_seq 512] pos={300 + i}")
+            got = dec.step(tok, 300 + i)
+            want = m.step(tok, 300 + i)
+            e = normwise_err(got, want)
+            assert e <= STEP_TOL, (i, e)
+    finally:
+        dec.close()
