@@ -34,11 +34,29 @@ WIDENED_LAYERS = {0, 1, 2, 5, 8, 11, 14, 17, 20, 23, 24, 25, 26, 27}
 # (rt_hip_gemv_q6k_tiled) instead of its BF16-widened copy
 Q6K_NATIVE = "q6k"
 HIDDEN, KV, FFN, VOCAB, LAYERS = 3072, 1024, 8192, 128256, 28
-# HBM bytes per launch of the dominant kernel (fused gate+up, tiled layout),
-# measured with rocprofv3 FETCH_SIZE / WRITE_SIZE and scaled by a 1 GiB device
-# copy: profiles/decode_kernels_hbm_traffic.md (command there).  The
-# row-major layout has no measured figure.
-DOMINANT_TRAFFIC_BYTES = {"tiled": 28655556}
+# HBM bytes per launch of the dominant kernel (fused gate+up, tiled layout)
+# come from the committed counter profile of this build (rocprofv3
+# FETCH_SIZE / WRITE_SIZE scaled by a 1 GiB device copy; the command is in
+# the file): the table row marked "(dominant)".
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_kernels_hbm_traffic.md")
+
+
+def dominant_traffic_bytes(layout: str):
+    """The '(dominant)' row's scaled HBM bytes in TRAFFIC_PROFILE (tiled
+    layout only; the row-major layout has no measured figure)."""
+    if layout != "tiled" or not os.path.exists(TRAFFIC_PROFILE):
+        return None
+    col = None
+    with open(TRAFFIC_PROFILE) as f:
+        for row in f:
+            if not row.startswith("|"):
+                continue
+            cells = [c.strip() for c in row.strip().strip("|").split("|")]
+            if col is None and "HBM bytes (scaled)" in cells:
+                col = cells.index("HBM bytes (scaled)")
+            elif col is not None and "(dominant)" in row:
+                return int(cells[col].replace(",", ""))
+    return None
 
 
 def log(*a):
@@ -264,15 +282,15 @@ def dominant_kernel_roofline(rt, torch, model, reps: int = 5):
 
 def cpu_baseline(rt, torch, model, budget_s: float = 12.0):
     """The reference's own CPU GEMVs (oracle/_ref: Q4KMat::matmul_q4k_t ->
-    gemv_mt, MatBf16::matmul_by_t -> gemv_mt, x86 scalar dot_row) on a
-    bounded sample of the same decode step: layers 0 (mixed, with BF16 v and
-    down) and 3 (all Q4_K) plus the lm_head, repeated until ~budget_s."""
+    gemv_mt, MatBf16::matmul_by_t -> gemv_mt, x86 scalar dot_row) over the
+    whole decode step: all 197 GEMVs of the token, in order, timed in full
+    (median of at least 5 reps after one warm-up, more until ~budget_s)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     from oracle import Oracle, Reference, reference_available  # noqa: PLC0415
 
     kind = "reference" if reference_available() else "port"
-    sample = [gv for gv in model.gemvs if gv[0].startswith(("L0.", "L3.")) or gv[0] == "lm_head"]
+    sample = list(model.gemvs)
     host = []
     for name, fmt, w, x, y, n, k in sample:
         wh = w.cpu().numpy()
@@ -304,7 +322,7 @@ def cpu_baseline(rt, torch, model, budget_s: float = 12.0):
     once()  # warm-up
     times = []
     t_end = time.perf_counter() + budget_s
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 50):
         t0 = time.perf_counter()
         once()
         times.append(time.perf_counter() - t0)
@@ -314,11 +332,10 @@ def cpu_baseline(rt, torch, model, budget_s: float = 12.0):
     med = sorted(times)[len(times) // 2]
     gbs = nbytes / med / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": (f"layers 0 (Q4_K + BF16 v/down) and 3 (Q4_K) + lm_head of the same "
-                       f"decode step: {len(host)} GEMVs, {nbytes / 1e6:.1f} MB, median of "
-                       f"{len(times)} reps ({med * 1e3:.1f} ms each); x86 scalar dot_row, "
-                       f"gemv_mt threads = min(hw={threads}, N/128)"),
-            "us_per_token_extrapolated": round(model.bytes_per_token() / (gbs * 1e9) * 1e6, 1)}
+            "sample": (f"the whole decode step, timed in full: all {len(host)} GEMVs, "
+                       f"{nbytes / 1e6:.1f} MB, median of {len(times)} reps ({med * 1e3:.1f} ms per token); "
+                       f"x86 scalar dot_row, gemv_mt threads = min(hw={threads}, N/128)"),
+            "us_per_token": round(med * 1e6, 1)}
 
 
 def bench_decode(args, rt, torch):
@@ -338,7 +355,7 @@ def bench_decode(args, rt, torch):
     roof = {"bound": "hbm", "achieved": round(dom["achieved_gbs"], 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(dom["achieved_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": (args.traffic_bytes if args.traffic_bytes is not None
-                        else DOMINANT_TRAFFIC_BYTES.get(args.layout)), "kernel": dom["kernel"],
+                        else dominant_traffic_bytes(args.layout)), "kernel": dom["kernel"],
             "us_per_launch": round(dom["us_per_launch"], 3),
             "bytes_per_launch": dom["bytes_per_launch"]}
     # the native-Q6_K variant has the headline's CPU path (the reference
@@ -1020,7 +1037,9 @@ def bench_flux_attention(args, rt, torch):
 def token_launch_bytes(mix: str):
     """Algorithmic bytes of each launch of the headline token, in order: per
     layer q/k/v (one launch; a BF16-widened v included), o, gate+up, down,
-    then the lm_head -- the byte counts DecodeModel.launches() reads."""
+    then the lm_head -- the byte counts DecodeModel.launches() reads, with
+    the activation counted once per GEMV as DecodeModel.bytes_per_token
+    counts it -- and the bytes each launch writes."""
     def q4(n, k):
         return n * (k // 256) * 144
 
@@ -1033,10 +1052,10 @@ def token_launch_bytes(mix: str):
         else:
             down = HIDDEN * FFN * 2 if wide else q4(HIDDEN, FFN)
         out.append(("qkv_bf16v" if wide else "qkv",
-                    q4(HIDDEN, HIDDEN) + q4(KV, HIDDEN) + v + 4 * HIDDEN + 4 * (HIDDEN + 2 * KV),
+                    q4(HIDDEN, HIDDEN) + q4(KV, HIDDEN) + v + 3 * 4 * HIDDEN + 4 * (HIDDEN + 2 * KV),
                     4 * (HIDDEN + 2 * KV)))
         out.append(("o", q4(HIDDEN, HIDDEN) + 8 * HIDDEN, 4 * HIDDEN))
-        out.append(("gate_up", 2 * q4(FFN, HIDDEN) + 4 * HIDDEN + 8 * FFN, 8 * FFN))
+        out.append(("gate_up", 2 * q4(FFN, HIDDEN) + 2 * 4 * HIDDEN + 8 * FFN, 8 * FFN))
         out.append(("down_bf16" if wide else "down", down + 4 * FFN + 4 * HIDDEN, 4 * HIDDEN))
     out.append(("lm_head", q4(VOCAB, HIDDEN) + 4 * HIDDEN + 4 * VOCAB, 4 * VOCAB))
     return out

@@ -218,7 +218,8 @@ int rt_hip_gemv_q4k_tiled_bf16(int32_t count, const void* const* tiled, float* c
  * to f32 rounding: the sum of squares is reduced in a tree, not in sequence,
  * and the scalar rms_inv multiplies the finished dot product rather than
  * each activation (equal in exact arithmetic).
- * k % 256 == 0, k <= 8192. */
+ * k % 256 == 0; any k whose staged activation (3.5 bytes per value) fits one
+ * workgroup's LDS (160 KB on gfx950: k up to about 45 000). */
 int rt_hip_gemv_q4k_tiled_rmsnorm_multi(int32_t count, const void* const* tiled, float* const* y,
                                         const int64_t* n, const float* x, const float* gamma, float eps,
                                         int32_t gemma3, int64_t k, rt_hip_stream stream);
@@ -343,8 +344,9 @@ int rt_hip_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int
  * (src/quant_q4.cpp:92-156) and metal_matmul_q4_t (metal_ops.hpp:54-55,
  * src/metal_ops.mm:117-161, 578-619).  w = s(nibble) * scale, summed in f32
  * (factorized: agreement to f32 rounding, normwise 1e-5).  K % 32 == 0 and
- * K <= 15872 (x and its group sums are staged in 64 KB of LDS; larger M is
- * split into launches that fit).
+ * K up to what one workgroup's LDS holds for one row of x and its group
+ * sums (4.125 bytes per value: K up to about 39 700 in gfx950's 160 KB);
+ * larger M is split into launches that fit.
  * rt_hip_q4mat_bytes / _scales_offset: the buffer size and where the
  * scales start (-1 for invalid n, k). */
 int64_t rt_hip_q4mat_bytes(int64_t n, int64_t k);

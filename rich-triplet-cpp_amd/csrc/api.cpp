@@ -112,7 +112,7 @@ int gemv_batched(const char* fn, int fmt, const float* x, float* y, int64_t n, i
     hipError_t e;
     DeviceState* st = state_for_current(&e);
     if (!st) return hip_fail(e, fn);
-    const size_t cap = st->info.lds_per_block < 65536 ? st->info.lds_per_block : 65536;
+    const size_t cap = lds_cap();
     int mb = m;
     while (mb > 1 && gemv_lds_bytes(fmt, mb, k) > cap) --mb;
     if (gemv_lds_bytes(fmt, mb, k) > cap)
@@ -134,6 +134,11 @@ const DeviceInfo& device_info() {
     DeviceState* st = state_for_current(&e);
     static DeviceInfo fallback;
     return st ? st->info : fallback;
+}
+
+size_t lds_cap() {
+    const size_t b = device_info().lds_per_block;
+    return b >= 65536 ? b : 65536;
 }
 
 int tune_param(const char* name, int fallback) {
@@ -310,6 +315,16 @@ int rt_hip_gemv_q4k(const void* blocks, const float* x, float* y, int64_t n, int
     if (m > 1 && tune_param("GEMV_BATCH_MFMA", 1))
         return check_stream_launch(launch_gemv_batch(RT_HIP_Q4K, blocks, x, y, n, k, m, static_cast<hipStream_t>(stream)),
                                    "rt_hip_gemv_q4k");
+    if (m == 1) {
+        // the int8-MFMA kernel stages 3.5 bytes per value (the VALU kernel's
+        // bound below is 4.25)
+        hipError_t e;
+        if (!state_for_current(&e)) return hip_fail(e, "rt_hip_gemv_q4k");
+        if (q4k_m1_lds_bytes(k) > lds_cap())
+            return fail(RT_HIP_E_SHAPE, "rt_hip_gemv_q4k: k too large for the LDS");
+        return check_stream_launch(launch_gemv_q4k_mfma(blocks, x, y, n, k, static_cast<hipStream_t>(stream)),
+                                   "rt_hip_gemv_q4k");
+    }
     return gemv_batched("rt_hip_gemv_q4k", RT_HIP_Q4K, x, y, n, k, m,
                         [&](const float* xx, float* yy, int mm) {
                             return launch_gemv_q4k(blocks, xx, yy, n, k, mm,
@@ -325,8 +340,8 @@ int rt_hip_gemv_q4k_multi(int32_t count, const void* const* blocks, float* const
         int rc = gemv_args("rt_hip_gemv_q4k_multi", blocks[j], x, y[j], n[j], k, 1, 256);
         if (rc) return rc;
     }
-    if (q4k_m1_lds_bytes(k) > 65536)
-        return fail(RT_HIP_E_SHAPE, "rt_hip_gemv_q4k_multi: k too large");
+    if (q4k_m1_lds_bytes(k) > lds_cap())
+        return fail(RT_HIP_E_SHAPE, "rt_hip_gemv_q4k_multi: k too large for the LDS");
     return check_stream_launch(launch_gemv_q4k_mfma_multi(count, blocks, y, n, x, k,
                                                           static_cast<hipStream_t>(stream), false),
                                "rt_hip_gemv_q4k_multi");
@@ -371,8 +386,8 @@ int rt_hip_gemv_q4k_tiled_multi(int32_t count, const void* const* tiled, float* 
         int rc = gemv_args("rt_hip_gemv_q4k_tiled_multi", tiled[j], x, y[j], n[j], k, 1, 256);
         if (rc) return rc;
     }
-    if (q4k_m1_lds_bytes(k) > 65536)
-        return fail(RT_HIP_E_SHAPE, "rt_hip_gemv_q4k_tiled_multi: k too large");
+    if (q4k_m1_lds_bytes(k) > lds_cap())
+        return fail(RT_HIP_E_SHAPE, "rt_hip_gemv_q4k_tiled_multi: k too large for the LDS");
     return check_stream_launch(launch_gemv_q4k_mfma_multi(count, tiled, y, n, x, k,
                                                           static_cast<hipStream_t>(stream), true),
                                "rt_hip_gemv_q4k_tiled_multi");
@@ -391,7 +406,7 @@ static int gemv_xop(const char* fn, int xop, int32_t count, const void* const* t
     if (xop != 0 && !aux) return fail(RT_HIP_E_ARG, std::string(fn) + ": null gamma / up");
     if (xop != 0 && !aligned16(aux))
         return fail(RT_HIP_E_ALIGN, std::string(fn) + ": gamma / up must be 16-byte aligned");
-    if (k > 8192 || q4k_m1_lds_bytes(k) > 65536) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 8192");
+    if (q4k_m1_lds_bytes(k) > lds_cap()) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k too large for the LDS");
     // Every workgroup reads all of x (and gamma / up) while others already
     // store rows of y, so no output may overlap an input.
     for (int32_t j = 0; j < count; ++j) {
@@ -456,7 +471,7 @@ int rt_hip_gemv_bf16_swiglu_residual(const uint16_t* w, const float* gate, const
     if (!aligned16(up)) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": up must be 16-byte aligned");
     if (overlaps(resid, n * 4, gate, k * 4) || overlaps(resid, n * 4, up, k * 4))
         return fail(RT_HIP_E_ARG, std::string(fn) + ": resid overlaps gate or up");
-    if (k > 8192) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 8192");
+    if (bf16_m1_lds_bytes(k) > lds_cap()) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k too large for the LDS");
     hipError_t e;
     if (!state_for_current(&e)) return hip_fail(e, fn);
     return check_stream_launch(
@@ -630,7 +645,7 @@ int rt_hip_gemv_bf16_swiglu(const uint16_t* w, const float* gate, const float* u
     if (!up) return fail(RT_HIP_E_ARG, std::string(fn) + ": null up");
     if (!aligned16(up)) return fail(RT_HIP_E_ALIGN, std::string(fn) + ": up must be 16-byte aligned");
     if (overlaps(y, n * 4, up, k * 4)) return fail(RT_HIP_E_ARG, std::string(fn) + ": y overlaps up");
-    if (k > 8192) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 8192");
+    if (bf16_m1_lds_bytes(k) > lds_cap()) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k too large for the LDS");
     hipError_t e;
     if (!state_for_current(&e)) return hip_fail(e, fn);
     return check_stream_launch(launch_gemv_bf16_xop(3, w, gate, up, 0.0f, y, n, k, static_cast<hipStream_t>(stream)),
@@ -733,11 +748,11 @@ int rt_hip_gemv_q4mat(const void* w, const float* x, float* y, int64_t n, int64_
     const char* fn = "rt_hip_gemv_q4mat";
     int rc = gemv_args(fn, w, x, y, n, k, m, 32);
     if (rc) return rc;
-    if (q4mat_gemv_lds_bytes(1, k) > 65536) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k above 15872");
+    if (q4mat_gemv_lds_bytes(1, k) > lds_cap()) return fail(RT_HIP_E_SHAPE, std::string(fn) + ": k too large for the LDS");
     hipError_t e;
     if (!state_for_current(&e)) return hip_fail(e, fn);
     int mb = m;
-    while (mb > 1 && q4mat_gemv_lds_bytes(mb, k) > 65536) --mb;
+    while (mb > 1 && q4mat_gemv_lds_bytes(mb, k) > lds_cap()) --mb;
     for (int32_t m0 = 0; m0 < m; m0 += mb) {
         const int32_t mm = (m - m0) < mb ? (m - m0) : mb;
         e = launch_gemv_q4mat(w, x + static_cast<size_t>(m0) * k, y + static_cast<size_t>(m0) * n, n, k, mm,
@@ -834,7 +849,7 @@ int rt_hip_gemv_bf16_argmax(const uint16_t* w, const float* x, float* y, int64_t
     if (rc) return rc;
     if (!idx) return fail(RT_HIP_E_ARG, "rt_hip_gemv_bf16_argmax: null idx");
     hipError_t e;
-    if (bf16_m1_lds_bytes(k) > 65536) return fail(RT_HIP_E_SHAPE, "rt_hip_gemv_bf16_argmax: k too large");
+    if (bf16_m1_lds_bytes(k) > lds_cap()) return fail(RT_HIP_E_SHAPE, "rt_hip_gemv_bf16_argmax: k too large for the LDS");
     const int64_t parts = bf16_argmax_partials(n, k);
     uint64_t* key = static_cast<uint64_t*>(workspace(static_cast<size_t>(parts) * 8, static_cast<hipStream_t>(stream), &e));
     if (!key) return check_stream_launch(e, "rt_hip_gemv_bf16_argmax: workspace");

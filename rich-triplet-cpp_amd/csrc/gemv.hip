@@ -545,7 +545,7 @@ size_t gemv_lds_bytes(int fmt, int m, int64_t k) {
 hipError_t launch_gemv_q4k(const void* w, const float* x, float* y, int64_t n, int64_t k, int m,
                            hipStream_t s) {
     // M == 1 (decode) runs on int8 MFMA; small batches on the VALU kernel.
-    if (m == 1 && q4k_m1_lds_bytes(k) <= 65536) return launch_gemv_q4k_mfma(w, x, y, n, k, s);
+    if (m == 1 && q4k_m1_lds_bytes(k) <= lds_cap()) return launch_gemv_q4k_mfma(w, x, y, n, k, s);
     // Q4_K pieces per row = 8 * K/256, so L >= 8 always.
     return dispatch<Q4kFmt, 8, false>(w, x, y, n, k, m, nullptr, s, RT_HIP_Q4K);
 }
@@ -553,14 +553,14 @@ hipError_t launch_gemv_q4k(const void* w, const float* x, float* y, int64_t n, i
 hipError_t launch_gemv_bf16(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
                             int m, uint64_t* key, hipStream_t s) {
     // M == 1 (decode, and the fused-argmax lm_head) has its own kernel.
-    if (m == 1 && bf16_m1_lds_bytes(k) <= 65536) return launch_gemv_bf16_m1(w, x, y, n, k, key, s);
+    if (m == 1 && bf16_m1_lds_bytes(k) <= lds_cap()) return launch_gemv_bf16_m1(w, x, y, n, k, key, s);
     return dispatch<Bf16Fmt, 1, true>(w, x, y, n, k, m, key, s, RT_HIP_BF16);
 }
 
 hipError_t launch_gemv_q4_0(const void* w, const float* x, float* y, int64_t n, int64_t k, int m,
                             hipStream_t s) {
     // M == 1 (decode): whole blocks per lane, rows streamed (gemv_q40.hip).
-    if (m == 1 && q40_m1_lds_bytes(k) <= 65536 && n <= 64ll * 0x7fffffff / 4)
+    if (m == 1 && q40_m1_lds_bytes(k) <= lds_cap() && n <= 64ll * 0x7fffffff / 4)
         return launch_gemv_q4_0_m1(w, x, y, n, k, s);
     return dispatch<Q40Fmt, 1, false>(w, x, y, n, k, m, nullptr, s, RT_HIP_Q4_0);
 }

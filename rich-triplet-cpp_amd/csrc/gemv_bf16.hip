@@ -63,6 +63,15 @@ hipError_t run(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k
     const int ik = static_cast<int>(k), in = static_cast<int>(n);
     const int64_t per = (k / 4 + T - 1) / T;
     const dim3 g(static_cast<unsigned>(wgs)), b(T);
+    if (tune_param("BF16_RING", 8) == 16) {
+        if (per <= 2)
+            hipLaunchKernelGGL((k_gemv_bf16<16, 2, ARGMAX, T>), g, b, lds, s, w, x, y, in, ik, key);
+        else if (per <= 4)
+            hipLaunchKernelGGL((k_gemv_bf16<16, 4, ARGMAX, T>), g, b, lds, s, w, x, y, in, ik, key);
+        else
+            hipLaunchKernelGGL((k_gemv_bf16<16, 8, ARGMAX, T>), g, b, lds, s, w, x, y, in, ik, key);
+        return hipGetLastError();
+    }
     if (per <= 2)
         hipLaunchKernelGGL((k_gemv_bf16<8, 2, ARGMAX, T>), g, b, lds, s, w, x, y, in, ik, key);
     else if (per <= 4)

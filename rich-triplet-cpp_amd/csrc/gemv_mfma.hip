@@ -107,6 +107,99 @@ __host__ __device__ inline size_t norm_offset(int K, int waves) {
     return lds_bytes(K) + static_cast<size_t>(waves) * 16 * sizeof(float);
 }
 
+// The part of x past a staging batch held in registers (K beyond what XP
+// f32x4 per thread cover, up to the LDS bound): f32x4 f = first, first +
+// step, ..., loaded, transformed by the x operation and written as limbs;
+// returns the sum of squares of the raw values (the RMSNorm partial).
+// first and step are multiples of 64 plus the lane, and K / 4 is a multiple
+// of 64, so every wave runs whole iterations (the 8-lane limb reductions
+// need the whole group).
+template <int XOP>
+__device__ __forceinline__ float stage_rest(const float* __restrict__ X, const float* __restrict__ aux, int K,
+                                            int first, int step, uint8_t* lds) {
+    const int nx = K >> 2;
+    const f32x4* const X4 = reinterpret_cast<const f32x4*>(X);
+    const f32x4* const A4 = reinterpret_cast<const f32x4*>(aux);
+    float sq = 0.0f;
+    for (int f = first; f < nx; f += step) {
+        f32x4 v = X4[f];
+        if constexpr (XOP == kXRmsNorm || XOP == kXRmsNorm1) {
+            const f32x4 a = A4[f];
+            sq += (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] *= XOP == kXRmsNorm1 ? 1.0f + a[e] : a[e];
+        } else if constexpr (XOP == kXSwiGlu) {
+            const f32x4 a = A4[f];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = swiglu1(v[e], a[e]);
+        } else if constexpr (XOP == kXGelu) {
+            const f32x4 a = A4[f];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = gelu1(v[e], a[e]);
+        }
+        limbs_of(v, lds, K, f, true);
+    }
+    return sq;
+}
+
+// x staged by the converter waves of a warp-specialized workgroup (CW > 0
+// below): thread c of the cthreads converter threads loads x[4f .. 4f+3] for
+// f = c + cthreads * i (XP of them), applies the x operation, writes the
+// limb planes and, for RMSNorm, its wave's partial sum of squares into
+// slot `nslot` of the norm partials.  The weight waves of the workgroup
+// issue their loads meanwhile; nothing here waits for them.
+template <int XP, int XOP>
+__device__ __forceinline__ void convert_x(const float* __restrict__ X, const float* __restrict__ aux, int K, int c,
+                                          int cthreads, int lane, int nslot, float* norm_part, uint8_t* lds) {
+    const int nx = K >> 2;
+    const f32x4* const X4 = reinterpret_cast<const f32x4*>(X);
+    f32x4 xv[XP], av[XP];
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+        const int f = c + cthreads * i;
+        xv[i] = X4[f < nx ? f : 0];
+    }
+    if constexpr (XOP != kXNone) {
+        const f32x4* const A4 = reinterpret_cast<const f32x4*>(aux);
+#pragma unroll
+        for (int i = 0; i < XP; ++i) {
+            const int f = c + cthreads * i;
+            av[i] = A4[f < nx ? f : 0];
+        }
+    }
+    [[maybe_unused]] const float rest_sq = stage_rest<XOP>(X, aux, K, c + cthreads * XP, cthreads, lds);
+    if constexpr (XOP == kXRmsNorm || XOP == kXRmsNorm1) {
+        float sq = rest_sq;
+#pragma unroll
+        for (int i = 0; i < XP; ++i) {
+            const f32x4 v = c + cthreads * i < nx ? xv[i] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            sq += (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+        }
+        sq = bf16_gemv::wave_sum(sq, lane);
+        if (lane == 0) norm_part[nslot] = sq;
+#pragma unroll
+        for (int i = 0; i < XP; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[i][e] *= XOP == kXRmsNorm1 ? 1.0f + av[i][e] : av[i][e];
+    } else if constexpr (XOP == kXSwiGlu) {
+#pragma unroll
+        for (int i = 0; i < XP; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[i][e] = swiglu1(xv[i][e], av[i][e]);
+    } else if constexpr (XOP == kXGelu) {
+#pragma unroll
+        for (int i = 0; i < XP; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[i][e] = gelu1(xv[i][e], av[i][e]);
+    }
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+        const int f = c + cthreads * i;
+        limbs_of(xv[i], lds, K, f, f < nx);
+    }
+    if (c < 4) reinterpret_cast<u32x4*>(lds + 3 * static_cast<size_t>(K))[c] = u32x4{0u, 0u, 0u, 0u};
+}
+
 // KS waves split a tile's super-blocks; a workgroup of blockDim.x / 64 waves
 // holds TPW = waves / KS tiles.
 // The arguments every wave needs before its first load come first, as
@@ -116,12 +209,29 @@ __host__ __device__ inline size_t norm_offset(int K, int waves) {
 // output pointer) come from the table.
 // The body of workgroup `blk` (the kernel below, and the Q4_K workgroups of
 // the fused q/k/v launch); `lds` holds mfma_gemv_lds_bytes(K, waves).
-template <int D, int XP, bool TILED, bool J34, int XOP = kXNone, int EPI = kEpiNone>
+//
+// CW > 0 (warp-specialized): the workgroup is KS * TPW weight waves and CW
+// converter waves after them (nthreads counts both).  The converter waves
+// stage x (XP f32x4 per converter thread) and leave at the staging barrier;
+// the weight waves issue their ring at once and load no x, so nothing of x
+// sits ahead of the weights in their in-order load counters.
+template <int D, int XP, bool TILED, bool J34, int XOP = kXNone, int EPI = kEpiNone, int CW = 0>
 __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, int K, uint32_t split, int nthreads,
                                           const uint8_t* w0, const uint8_t* w1, int n0, int n1, int tile1,
                                           const Jobs& jobs, uint8_t* lds, const float* __restrict__ aux = nullptr,
                                           float eps = 0.0f, const Rope& rope = Rope{}) {
     const int count = static_cast<int>(split >> 29);
+    const int wwaves = (nthreads >> 6) - CW;  // weight waves
+    if constexpr (CW > 0) {
+        const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+        if (w >= wwaves) {
+            float* const np = reinterpret_cast<float*>(lds + norm_offset(K, wwaves));
+            convert_x<XP, XOP>(X, aux, K, static_cast<int>(threadIdx.x) - wwaves * kWave, CW * kWave,
+                               static_cast<int>(threadIdx.x) & 63, w - wwaves, np, lds);
+            lds_barrier();
+            return;
+        }
+    }
     // nthreads == blockDim.x, passed as a preloaded argument: blockDim
     // itself is a kernel-argument load that the first x loads would wait for.
     const int KS = static_cast<int>(split & 15u), TPW = static_cast<int>((split >> 4) & 15u);
@@ -144,18 +254,21 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     // keeps these loads ahead of the weight prologue; vmcnt counts them in
     // order, so waiting for them is partial.
     const f32x4* const X4 = reinterpret_cast<const f32x4*>(X);
-    f32x4 xv[XP], av[XP];
-#pragma unroll
-    for (int i = 0; i < XP; ++i) {
-        const int f = tid + nthreads * i;
-        xv[i] = X4[f < nx ? f : 0];
-    }
-    if constexpr (XOP != kXNone) {
-        const f32x4* const A4 = reinterpret_cast<const f32x4*>(aux);
+    constexpr int XPW = CW > 0 ? 1 : XP;  // the weight waves of a specialized workgroup load no x
+    f32x4 xv[XPW], av[XPW];
+    if constexpr (CW == 0) {
 #pragma unroll
         for (int i = 0; i < XP; ++i) {
             const int f = tid + nthreads * i;
-            av[i] = A4[f < nx ? f : 0];
+            xv[i] = X4[f < nx ? f : 0];
+        }
+        if constexpr (XOP != kXNone) {
+            const f32x4* const A4 = reinterpret_cast<const f32x4*>(aux);
+#pragma unroll
+            for (int i = 0; i < XP; ++i) {
+                const int f = tid + nthreads * i;
+                av[i] = A4[f < nx ? f : 0];
+            }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -234,7 +347,11 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
 
     // The x loads are older than the 3*D prologue loads: wait for them
     // alone (XP * nthreads >= K/4, checked by the host), then convert.
+    if constexpr (CW == 0) {
     wait_vmcnt<3 * D>();
+    // x past the register batch (K above XP * nthreads * 4): loaded after
+    // the weight prologue, so its waits are full ones; large K only.
+    [[maybe_unused]] const float rest_sq = stage_rest<XOP>(X, aux, K, tid + nthreads * XP, nthreads, lds);
     if constexpr (XOP == kXRmsNorm || XOP == kXRmsNorm1) {
         // RMSNorm(x) * g = rms_inv * (x * g) with one scalar rms_inv per
         // launch, so the staged activation is x * g and rms_inv multiplies
@@ -242,7 +359,7 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
         // of squares then needs no barrier of its own.  Per thread, then
         // over the wave (DPP and permlane); each wave's partial goes to LDS
         // before the limb barrier below and is summed after it.
-        float sq = 0.0f;
+        float sq = rest_sq;
 #pragma unroll
         for (int i = 0; i < XP; ++i) {
             const f32x4 v = tid + nthreads * i < nx ? xv[i] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -281,14 +398,16 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
         limbs_of(xv[i], lds, K, f, f < nx);
     }
     if (tid < 4) reinterpret_cast<u32x4*>(lds + 3 * static_cast<size_t>(K))[tid] = u32x4{0u, 0u, 0u, 0u};
+    }
     lds_barrier();
     // rms_inv = 1 / sqrt(sum(x^2) * (1/K) + eps), as the reference forms it
     // (the sum itself is reduced in a tree).
     float out_scale = 1.0f;
     if constexpr (XOP == kXRmsNorm || XOP == kXRmsNorm1) {
-        const float* part = reinterpret_cast<const float*>(lds + norm_offset(K, nthreads >> 6));
+        const int parts = CW > 0 ? CW : (nthreads >> 6);
+        const float* part = reinterpret_cast<const float*>(lds + norm_offset(K, CW > 0 ? wwaves : (nthreads >> 6)));
         float tot = 0.0f;
-        for (int w = 0; w < (nthreads >> 6); ++w) tot += part[w];
+        for (int w = 0; w < parts; ++w) tot += part[w];
         out_scale = 1.0f / __builtin_sqrtf(tot * (1.0f / static_cast<float>(K)) + eps);
     }
 
@@ -364,25 +483,25 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     }
 }
 
-template <int D, int XP, bool TILED, bool J34>
-__global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_mfma(
+template <int D, int XP, bool TILED, bool J34, int CW>
+__global__ __launch_bounds__(CW > 0 ? 1024 : kMaxThreads) void k_gemv_q4k_mfma(
     const float* __restrict__ X, int K, uint32_t split, int nthreads, const uint8_t* w0, const uint8_t* w1,
     int n0, int n1, int tile1, const Jobs jobs) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    q4k_tiles<D, XP, TILED, J34>(static_cast<int>(blockIdx.x), X, K, split, nthreads, w0, w1, n0, n1, tile1, jobs,
-                                 lds);
+    q4k_tiles<D, XP, TILED, J34, kXNone, kEpiNone, CW>(static_cast<int>(blockIdx.x), X, K, split, nthreads, w0, w1,
+                                                       n0, n1, tile1, jobs, lds);
 }
 
 // The same with a layer operation applied to x while it is staged (XOp).
 // Pointers first, then the 32-bit arguments: no padding, so all fourteen
 // leading dwords (aux, gamma or up, included) are preloaded.
-template <int XP, bool J34, int XOP, int EPI>
-__global__ __launch_bounds__(kMaxThreads) void k_gemv_q4k_xop(
+template <int XP, bool J34, int XOP, int EPI, int CW>
+__global__ __launch_bounds__(CW > 0 ? 1024 : kMaxThreads) void k_gemv_q4k_xop(
     const float* __restrict__ X, const float* __restrict__ aux, const uint8_t* w0, const uint8_t* w1, int K,
     uint32_t split, int nthreads, int n0, int n1, int tile1, const Jobs jobs, float eps, const Rope rope) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    q4k_tiles<4, XP, true, J34, XOP, EPI>(static_cast<int>(blockIdx.x), X, K, split, nthreads, w0, w1, n0, n1,
-                                           tile1, jobs, lds, aux, eps, rope);
+    q4k_tiles<4, XP, true, J34, XOP, EPI, CW>(static_cast<int>(blockIdx.x), X, K, split, nthreads, w0, w1, n0, n1,
+                                               tile1, jobs, lds, aux, eps, rope);
 }
 
 // A layer's q/k/v when v is BF16 (Q6_K widened): the first q4k_wgs
@@ -415,47 +534,51 @@ struct XArgs {
     Rope rope;
 };
 
-template <int D, int XP, bool TILED, bool J34, int XOP, int EPI>
+// `waves` weight waves plus CW converter waves per workgroup.
+template <int D, int XP, bool TILED, bool J34, int XOP, int EPI, int CW>
 hipError_t run(const Jobs& jobs, const float* x, const XArgs& xa, int64_t k, int ks, int waves, hipStream_t s) {
     const int tpw = waves / ks;
     const int64_t wgs = (static_cast<int64_t>(jobs.total) + tpw - 1) / tpw;
-    const size_t lds = mfma_gemv_lds_bytes(k, waves);
+    const int all = waves + CW;
+    const size_t lds = mfma_gemv_lds_bytes(k, all);
     const uint32_t split = pack_split(ks, tpw, static_cast<int>((k / 256 + ks - 1) / ks), jobs.count);
-    const dim3 g(static_cast<unsigned>(wgs)), b(static_cast<unsigned>(waves * kWave));
+    const dim3 g(static_cast<unsigned>(wgs)), b(static_cast<unsigned>(all * kWave));
     if constexpr (XOP == kXNone && EPI == kEpiNone) {
-        hipLaunchKernelGGL((k_gemv_q4k_mfma<D, XP, TILED, J34>), g, b, lds, s, x, static_cast<int>(k), split,
-                           waves * kWave, jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], jobs);
+        hipLaunchKernelGGL((k_gemv_q4k_mfma<D, XP, TILED, J34, CW>), g, b, lds, s, x, static_cast<int>(k), split,
+                           all * kWave, jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], jobs);
     } else {
         static_assert(D == 4 && TILED, "x operations and RoPE run on the tiled layout, ring depth 4");
-        hipLaunchKernelGGL((k_gemv_q4k_xop<XP, J34, XOP, EPI>), g, b, lds, s, x, xa.aux, jobs.w[0], jobs.w[1],
-                           static_cast<int>(k), split, waves * kWave, jobs.n[0], jobs.n[1], jobs.tile0[1], jobs,
+        hipLaunchKernelGGL((k_gemv_q4k_xop<XP, J34, XOP, EPI, CW>), g, b, lds, s, x, xa.aux, jobs.w[0], jobs.w[1],
+                           static_cast<int>(k), split, all * kWave, jobs.n[0], jobs.n[1], jobs.tile0[1], jobs,
                            xa.eps, xa.rope);
     }
     return hipGetLastError();
 }
 
 // x prefetch depth: enough f32x4 per thread for all of x (up to K = 8192 at
-// 256 threads) before the weight prologue.
-template <int D, bool TILED, int XOP, int EPI>
+// 256 threads) before the weight prologue; with CW converter waves, per
+// converter thread.
+template <int D, bool TILED, int XOP, int EPI, int CW = 0>
 hipError_t run_xp(const Jobs& jobs, const float* x, const XArgs& xa, int64_t k, int ks, int waves,
                   hipStream_t s) {
-    const int64_t per = (k / 4 + waves * kWave - 1) / (waves * kWave);
-    // The host keeps K within the staging bound: 16 float4 per thread, 8
-    // with an x operation (its second vector doubles the registers).
+    const int xthreads = (CW > 0 ? CW : waves) * kWave;
+    const int64_t per = (k / 4 + xthreads - 1) / xthreads;
+    // At most 16 float4 per thread in registers, 8 with an x operation (its
+    // second vector doubles the registers); the rest of a longer x is
+    // staged by a loop after them.
     constexpr bool kPlain = XOP == kXNone && EPI == kEpiNone;
-    if (per > (kPlain ? 16 : 8)) return hipErrorInvalidValue;
     if (jobs.count > 2) {
-        if (per <= 2) return run<D, 2, TILED, true, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
-        if (per <= 3) return run<D, 3, TILED, true, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
-        if (per <= 4) return run<D, 4, TILED, true, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
-        if (per <= 8 || !kPlain) return run<D, 8, TILED, true, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
-        if constexpr (kPlain) return run<D, 16, TILED, true, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
+        if (per <= 2) return run<D, 2, TILED, true, XOP, EPI, CW>(jobs, x, xa, k, ks, waves, s);
+        if (per <= 3) return run<D, 3, TILED, true, XOP, EPI, CW>(jobs, x, xa, k, ks, waves, s);
+        if (per <= 4) return run<D, 4, TILED, true, XOP, EPI, CW>(jobs, x, xa, k, ks, waves, s);
+        if (per <= 8 || !kPlain) return run<D, 8, TILED, true, XOP, EPI, CW>(jobs, x, xa, k, ks, waves, s);
+        if constexpr (kPlain) return run<D, 16, TILED, true, XOP, EPI, CW>(jobs, x, xa, k, ks, waves, s);
     }
-    if (per <= 2) return run<D, 2, TILED, false, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
-    if (per <= 3) return run<D, 3, TILED, false, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
-    if (per <= 4) return run<D, 4, TILED, false, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
-    if (per <= 8 || !kPlain) return run<D, 8, TILED, false, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
-    if constexpr (kPlain) return run<D, 16, TILED, false, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
+    if (per <= 2) return run<D, 2, TILED, false, XOP, EPI, CW>(jobs, x, xa, k, ks, waves, s);
+    if (per <= 3) return run<D, 3, TILED, false, XOP, EPI, CW>(jobs, x, xa, k, ks, waves, s);
+    if (per <= 4) return run<D, 4, TILED, false, XOP, EPI, CW>(jobs, x, xa, k, ks, waves, s);
+    if (per <= 8 || !kPlain) return run<D, 8, TILED, false, XOP, EPI, CW>(jobs, x, xa, k, ks, waves, s);
+    if constexpr (kPlain) return run<D, 16, TILED, false, XOP, EPI, CW>(jobs, x, xa, k, ks, waves, s);
     return hipErrorInvalidValue;
 }
 
@@ -495,6 +618,15 @@ hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s, 
     int waves = ks <= 4 ? (4 / ks) * ks : ks;
     if (const int tpw = tune_param("Q4K_TPW", 0)) waves = ks * tpw;
     if (waves % ks != 0 || waves > kMaxThreads / kWave) return hipErrorInvalidValue;
+    // Converter waves (tiled layout): measured per launch shape on the
+    // headline token, 8 of them beside the weight waves take o 3072 x 3072
+    // from 3.85 to 3.62-3.67 us, the q/k/v launch from 4.86 to 4.57-4.60 and
+    // gate+up from 7.29-7.33 to 7.18-7.26, but the K = 8192 down projection
+    // from 5.90 to 6.66-6.73 and the lm_head (31 rounds of workgroups) from
+    // 37.4 to 43.9: so one round of workgroups and K <= 4096 only.
+    const int64_t wgs_now = (tiles + waves / ks - 1) / (waves / ks);
+    const int cw = tune_param("Q4K_CONV", TILED && wgs_now <= cus && k <= 4096 && waves + 8 <= 16 ? 8 : 0);
+    if (TILED && cw == 8 && waves + 8 <= 16) return run_xp<4, TILED, XOP, EPI, 8>(jobs, x, xa, k, ks, waves, s);
     if constexpr (XOP != kXNone || EPI != kEpiNone) {
         return run_xp<4, TILED, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
     } else {

@@ -15,9 +15,12 @@ namespace rt_hip {
 struct DeviceInfo {
     int ordinal = -1;
     int cus = 256;
-    size_t lds_per_block = 65536;
+    size_t lds_per_block = 65536;  // the device's, read at first use
 };
 const DeviceInfo& device_info();
+// LDS one workgroup may allocate on the current device (160 KB on gfx950):
+// the bound of every kernel that stages its activation in LDS.
+size_t lds_cap();
 
 // Records `msg` as the calling thread's last error (rt_hip_last_error) and
 // returns `code` (host code outside api.cpp).
@@ -68,7 +71,7 @@ hipError_t attention_scratch_setup(int dev, void** out);
 hipError_t launch_attention_decode(const float* q, const float* kc, const float* vc, float* out, float* part,
                                    int64_t n_q, int64_t n_kv, int64_t seq_len, float scale, hipStream_t s);
 // M = 1 BF16 GEMV with a layer operation applied to x while it is staged
-// (xop as below), k <= 8192.
+// (xop as below); LDS: bf16_m1_lds_bytes(k).
 hipError_t launch_gemv_bf16_xop(int xop, const uint16_t* w, const float* x, const float* aux, float eps, float* y,
                                 int64_t n, int64_t k, hipStream_t s, bool add = false);
 // Tiled Q4_K GEMVs sharing x, with a layer operation applied to x while it
@@ -97,7 +100,7 @@ hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* co
                                       const int64_t* n, const float* x, int64_t k, hipStream_t s,
                                       bool tiled);
 // LDS of the M = 1 Q4_K GEMV for `waves` waves per workgroup, and its
-// worst case over the splits it picks (the callers' K bound: <= 64 KB).
+// worst case over the splits it picks (the callers' K bound: <= lds_cap()).
 size_t mfma_gemv_lds_bytes(int64_t k, int waves);
 size_t q4k_m1_lds_bytes(int64_t k);
 // head_dim > 0: interleave each head's rows (2j <- j, 2j + 1 <- j + head_dim / 2).

@@ -72,7 +72,7 @@ def test_layer_ops_reject_bad_arguments(rt):
     import ctypes as C
     lib = rt.library()
     t = to_dev(np.zeros(2304, np.uint8))
-    x = to_dev(np.zeros(16384, np.float32))
+    x = to_dev(np.zeros(65536, np.float32))
     y = to_dev(np.zeros(16, np.float32))
     wp = (C.c_void_p * 1)(t.data_ptr())
     yp = (C.c_void_p * 1)(y.data_ptr())
@@ -81,8 +81,10 @@ def test_layer_ops_reject_bad_arguments(rt):
                       C.c_float(1e-5), 0, 256, None) == E_ARG
     assert lib.status("rt_hip_gemv_q4k_tiled_rmsnorm_multi", 1, wp, yp, npp, x.data_ptr(), x.data_ptr(),
                       C.c_float(-1.0), 0, 256, None) == E_ARG
+    # K whose staged limbs (3.5 bytes per value) exceed one workgroup's LDS:
+    # refused before any launch
     assert lib.status("rt_hip_gemv_q4k_tiled_swiglu", t.data_ptr(), x.data_ptr(), x.data_ptr(), y.data_ptr(),
-                      16, 16384, None) == E_SHAPE
+                      16, 65536, None) == E_SHAPE
     assert lib.status("rt_hip_gemv_q4k_tiled_swiglu", t.data_ptr(), x.data_ptr(), None, y.data_ptr(),
                       16, 256, None) == E_ARG
 
