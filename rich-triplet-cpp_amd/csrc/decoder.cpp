@@ -91,6 +91,7 @@ struct rt_hip_decoder {
     int32_t* hstate = nullptr;  // pinned host mirror
     float* logits_stage = nullptr;  // pinned host staging for the logits readback, [max rows][vocab]
     uint64_t* argmax_keys = nullptr;
+    uint64_t* argmax_part = nullptr;  // per-workgroup keys of the Q4_K lm_head (zeroed at create)
     int64_t* argmax_idx = nullptr;
     hipStream_t stream = nullptr;  // used when the caller passes the legacy stream (not capturable)
     rt_hip_graph* graphs[RT_HIP_GEMV_MAX_M + 1] = {};
@@ -412,19 +413,27 @@ int record_step(rt_hip_decoder* d, int m, hipStream_t s) {
     if (m == 1) {
         // final norm inside the lm_head GEMV's staging
         if (d->lm_head.q4k()) {
+            // the argmax of the logits (transformer5.cpp:382-391) rides in
+            // the GEMV's epilogue, one key per workgroup, and one launch
+            // folds them
             const void* w[1] = {d->lm_head.tiled};
             float* y[1] = {d->logits};
             const int64_t n[1] = {V};
-            rc = rt_hip_gemv_q4k_tiled_rmsnorm_multi(1, w, y, n, d->hidden, d->out_norm, c.norm_eps,
-                                                     d->gemma ? 1 : 0, H, s);
+            rc = chk(launch_gemv_q4k_xop(d->gemma ? 2 : 1, 1, w, y, n, d->hidden, d->out_norm, c.norm_eps, H, s,
+                                         nullptr, 0, 0, 0, false, RopeCache{}, d->argmax_part),
+                     "decoder: lm_head + argmax");
+            if (!rc)
+                rc = chk(launch_argmax_reduce(d->argmax_part, q4k_argmax_partials(V), d->argmax_idx, nullptr, s),
+                         "decoder: argmax");
+            return rc;
         } else {
             rc = chk(launch_gemv_bf16_xop(d->gemma ? 2 : 1, static_cast<const uint16_t*>(d->lm_head.data), d->hidden,
                                           d->out_norm, c.norm_eps, d->logits, V, H, s),
                      "decoder: lm_head");
         }
-        // The argmax of the logits (transformer5.cpp:382-391) rides in the
-        // same graph: three small launches on the GPU instead of a separate
-        // host call per token.
+        // The argmax of the BF16 logits (transformer5.cpp:382-391) rides in
+        // the same graph: three small launches on the GPU instead of a
+        // separate host call per token.
         if (!rc) rc = chk(launch_argmax_init(d->argmax_keys, 1, s), "decoder: argmax");
         if (!rc) rc = chk(launch_argmax_scan(d->logits, 1, V, d->argmax_keys, s), "decoder: argmax");
         if (!rc) rc = chk(launch_argmax_finalize(d->argmax_keys, 1, d->argmax_idx, nullptr, s), "decoder: argmax");
@@ -570,6 +579,8 @@ int rt_hip_decoder_create(const rt_hip_decoder_config* cfg, rt_hip_decoder** out
         (e = dev_alloc_t(d, &d->logits, static_cast<size_t>(R) * c.vocab)) != hipSuccess ||
         (e = dev_alloc_t(d, &d->dstate, 16)) != hipSuccess ||
         (e = dev_alloc_t(d, &d->argmax_keys, 64)) != hipSuccess ||
+        (e = dev_alloc_t(d, &d->argmax_part, static_cast<size_t>(q4k_argmax_partials(c.vocab)))) != hipSuccess ||
+        (e = hipMemset(d->argmax_part, 0, static_cast<size_t>(q4k_argmax_partials(c.vocab)) * 8)) != hipSuccess ||
         (e = dev_alloc_t(d, &d->argmax_idx, 16)) != hipSuccess)
         return cleanup(e);
     if ((e = hipHostMalloc(reinterpret_cast<void**>(&d->hstate), 16 * sizeof(int32_t))) != hipSuccess)

@@ -502,6 +502,9 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
 // Second launch of the two-launch form: workgroup (query head, row), one
 // thread per dimension, folds the busy splits' plain-stored partials in
 // split order (the same fold as the in-launch merge, so the same bits).
+// Folding every split instead (idle ones hold M = -inf and weigh 0), with no
+// read of the position, measured 5.88 against 3.96 us per launch on the
+// Llama-3.2-3B engine at 1024 positions.
 template <int HD>
 __global__ __launch_bounds__(HD) void k_attn2_combine(const AttnArgs a, int S) {
     using Geo = AttnGeom<HD>;
@@ -625,6 +628,10 @@ hipError_t launch_qk_prep(const QkPrep& p, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Enough (kv head, split, row) workgroups for every CU, at least 64
+// positions per split.  Measured on the Llama-3.2-3B engine at 1024
+// positions: 17 splits 6.44 us per partial launch, 32 splits of 32 positions
+// (2 loaded ahead per group) 6.88 us.
 int attention2_splits(int n_kv, int m, int64_t max_len) {
     const int64_t cus = device_info().cus;
     int64_t want = (cus + n_kv * m - 1) / (n_kv * m);

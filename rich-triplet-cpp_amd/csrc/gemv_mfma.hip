@@ -52,7 +52,11 @@ struct Jobs {
 // (RoPE, below), or add it to what y holds (the residual add of
 // LlamaBlock::forward_cached, transformer5.cpp:205-212: x = x + attn(...),
 // x = x + mlp(...)).
-enum Epi { kEpiNone = 0, kEpiRope = 1, kEpiAdd = 2 };
+// kEpiArgmax: store the row and fold it into its tile's greedy-argmax key
+// (the first index of the strict maximum, NaN never chosen:
+// transformer5.cpp:382-391), one key per 16-row tile in Rope::keys; a
+// second launch folds those (launch_argmax_reduce).
+enum Epi { kEpiNone = 0, kEpiRope = 1, kEpiAdd = 2, kEpiArgmax = 3 };
 
 struct Rope {
     const float* inv_freq = nullptr;  // [head_dim / 2], device
@@ -63,6 +67,7 @@ struct Rope {
     int jobs = 0;
     int half = 0;  // half-split pairing: rows of rotated jobs tiled interleaved
     int cache_jobs = 0;
+    uint64_t* keys = nullptr;  // kEpiArgmax: one key per tile
 
     __device__ __forceinline__ int position() const { return pos_dev ? pos_dev[0] : pos; }
     // Where output set j (a job, or kRopeCacheBf16Bit for the BF16 rows) starts.
@@ -106,6 +111,13 @@ __host__ __device__ inline uint32_t pack_split(int ks, int tpw, int bpw, int cou
 __host__ __device__ inline size_t norm_offset(int K, int waves) {
     return lds_bytes(K) + static_cast<size_t>(waves) * 16 * sizeof(float);
 }
+
+// Whether an instantiation can see x longer than its register batch: only
+// the widest batch (16 f32x4 per thread, 8 with an x operation), which the
+// host picks when nothing narrower covers K.  The narrower ones carry no
+// loop (its registers and code cost the short launches measurably).
+template <int XP, int XOP>
+constexpr bool kHasRest = XP >= (XOP == kXNone ? 16 : 8);
 
 // The part of x past a staging batch held in registers (K beyond what XP
 // f32x4 per thread cover, up to the LDS bound): f32x4 f = first, first +
@@ -167,7 +179,8 @@ __device__ __forceinline__ void convert_x(const float* __restrict__ X, const flo
             av[i] = A4[f < nx ? f : 0];
         }
     }
-    [[maybe_unused]] const float rest_sq = stage_rest<XOP>(X, aux, K, c + cthreads * XP, cthreads, lds);
+    float rest_sq = 0.0f;
+    if constexpr (kHasRest<XP, XOP>) rest_sq = stage_rest<XOP>(X, aux, K, c + cthreads * XP, cthreads, lds);
     if constexpr (XOP == kXRmsNorm || XOP == kXRmsNorm1) {
         float sq = rest_sq;
 #pragma unroll
@@ -225,9 +238,9 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     if constexpr (CW > 0) {
         const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
         if (w >= wwaves) {
+            const int c = static_cast<int>(threadIdx.x) - wwaves * kWave;
             float* const np = reinterpret_cast<float*>(lds + norm_offset(K, wwaves));
-            convert_x<XP, XOP>(X, aux, K, static_cast<int>(threadIdx.x) - wwaves * kWave, CW * kWave,
-                               static_cast<int>(threadIdx.x) & 63, w - wwaves, np, lds);
+            convert_x<XP, XOP>(X, aux, K, c, CW * kWave, static_cast<int>(threadIdx.x) & 63, w - wwaves, np, lds);
             lds_barrier();
             return;
         }
@@ -351,7 +364,8 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     wait_vmcnt<3 * D>();
     // x past the register batch (K above XP * nthreads * 4): loaded after
     // the weight prologue, so its waits are full ones; large K only.
-    [[maybe_unused]] const float rest_sq = stage_rest<XOP>(X, aux, K, tid + nthreads * XP, nthreads, lds);
+    float rest_sq = 0.0f;
+    if constexpr (kHasRest<XP, XOP>) rest_sq = stage_rest<XOP>(X, aux, K, tid + nthreads * XP, nthreads, lds);
     if constexpr (XOP == kXRmsNorm || XOP == kXRmsNorm1) {
         // RMSNorm(x) * g = rms_inv * (x * g) with one scalar rms_inv per
         // launch, so the staged activation is x * g and rms_inv multiplies
@@ -465,9 +479,15 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
         }
         return val;
     };
+    uint64_t key = 0;  // kEpiArgmax: this lane's row (0: none)
+    auto keep_key = [&](float out) {
+        if constexpr (EPI == kEpiArgmax)
+            if (lane < 16 && keep && out == out) key = argmax_key(out, static_cast<uint32_t>(row));
+    };
     if (KS == 1) {
         const float out = finish(v);
         if (lane < 16 && keep) yj[drow] = EPI == kEpiAdd ? yj[drow] + out : out;
+        keep_key(out);
     } else {
         float* red = reinterpret_cast<float*>(lds + lds_bytes(K));  // [TPW][KS][16]
         float* rp = red + tslot * KS * 16;
@@ -479,6 +499,19 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
             for (int q = 1; q < KS; ++q) s += rp[q * 16 + (lane & 15)];
             const float out = finish(s);
             if (lane < 16 && keep) yj[drow] = EPI == kEpiAdd ? yj[drow] + out : out;
+            keep_key(out);
+        }
+    }
+    if constexpr (EPI == kEpiArgmax) {
+        // One wave finishes each tile (KS == 1: every wave; else the ks == 0
+        // one): its largest key goes to the tile's slot, with no barrier.
+        if (KS == 1 || ks == 0) {
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                const uint64_t o = __shfl_xor(key, off, kWave);
+                key = o > key ? o : key;
+            }
+            if (lane == 0 && t < jobs.total) rope.keys[t] = key;
         }
     }
 }
@@ -649,7 +682,7 @@ size_t q4k_m1_lds_bytes(int64_t k) { return mfma_gemv_lds_bytes(k, kMaxThreads /
 hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* const* y, const int64_t* n,
                               const float* x, const float* aux, float eps, int64_t k, hipStream_t s,
                               const float* inv_freq, int pos, int head_dim, int rope_jobs, bool add,
-                              const RopeCache& cache) {
+                              const RopeCache& cache, uint64_t* argmax_keys) {
     if (count < 1 || count > kMaxJobs || (aux == nullptr && xop != kXNone)) return hipErrorInvalidValue;
     Jobs jobs{};
     jobs.count = count;
@@ -671,6 +704,16 @@ hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* 
     XArgs xa;
     xa.aux = aux;
     xa.eps = eps;
+    if (argmax_keys) {
+        // the lm_head: the final norm while staging, the argmax after the rows
+        if (rope_jobs || add) return hipErrorInvalidValue;
+        xa.rope.keys = argmax_keys;
+        switch (xop) {
+            case kXRmsNorm: return dispatch<true, kXRmsNorm, kEpiArgmax>(jobs, x, k, s, xa);
+            case kXRmsNorm1: return dispatch<true, kXRmsNorm1, kEpiArgmax>(jobs, x, k, s, xa);
+            default: return hipErrorInvalidValue;
+        }
+    }
     if (rope_jobs) {
         xa.rope.inv_freq = inv_freq;
         xa.rope.pos = pos;

@@ -92,10 +92,16 @@ struct RopeCache {
 };
 constexpr int kRopeCacheBf16Bit = 4;
 constexpr int kRopeCacheBf16 = 1 << kRopeCacheBf16Bit;
+// argmax_keys (RMSNorm xops only, no RoPE or add, one job): every 16-row
+// tile also stores its greedy-argmax key there (q4k_argmax_partials(n)
+// slots); launch_argmax_reduce(keys, q4k_argmax_partials(n)) then gives the
+// index.
 hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* const* y, const int64_t* n,
                               const float* x, const float* aux, float eps, int64_t k, hipStream_t s,
                               const float* inv_freq = nullptr, int pos = 0, int head_dim = 0, int rope_jobs = 0,
-                              bool add = false, const RopeCache& cache = {});
+                              bool add = false, const RopeCache& cache = {}, uint64_t* argmax_keys = nullptr);
+// Argmax key slots of a one-job Q4_K GEMV of n rows: its tiles.
+inline int64_t q4k_argmax_partials(int64_t n) { return (n + 15) / 16; }
 hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* const* y,
                                       const int64_t* n, const float* x, int64_t k, hipStream_t s,
                                       bool tiled);

@@ -353,8 +353,8 @@ def test_decoder_long_cache_matches_oracle(rt, orc, arch, cfg, rows):
             assert e <= STEP_TOL, (pos, e)
             assert idx == orc.argmax_first(got), pos
         say(f"[decoder {arch}] {rows} cached positions: worst step normwise error {worst:.2e}")
-        if arch == "llama3b" and rows == 1000 and cfg["max_seq"] == 2048:
-            # the case meant to hold idle splits does
+        if arch == "llama3b" and cfg["max_seq"] == 2048:
+            # the cases meant to hold idle splits do
             S = split_rule(n_kv, 1, cfg["max_seq"], cus)
             assert busy_rule(rows + 1, S, hd) < S
     finally:
