@@ -33,6 +33,24 @@ def rel_rms(y, ref) -> float:
     return float(np.sqrt(np.mean((y - ref) ** 2)) / max(np.sqrt(np.mean(ref ** 2)), 1e-30))
 
 
+def same_operand_err(c, a, wd, n_cols=64, seed=0):
+    """Normwise error of a bf16-MFMA GEMM output c [M, N] (device) against
+    the float64 product of the same bf16-rounded operands on n_cols sampled
+    output columns: a [M, K] (device f32 or bf16; rounded to bf16 RNE as the
+    GEMM rounds it) and wd [N, K] (device bf16 or f32 holding bf16 values).
+    float64 makes the reference's own rounding negligible, so the bar is the
+    stated GEMM_TOL_SAME_OPERANDS."""
+    import torch
+    n = wd.shape[0]
+    cols = np.sort(np.random.default_rng(seed).choice(n, min(n_cols, n), replace=False))
+    idx = torch.from_numpy(cols).to(wd.device)
+    ah = a.bfloat16().float().cpu().numpy().astype(np.float64)
+    wh = wd.index_select(0, idx).float().cpu().numpy().astype(np.float64)
+    ref = ah @ wh.T
+    got = c.index_select(1, idx).cpu().numpy().astype(np.float64)
+    return float(np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
 def to_dev(arr):
     import torch
     return torch.from_numpy(np.ascontiguousarray(arr)).cuda()
