@@ -278,18 +278,23 @@ __device__ __forceinline__ void fold_splits(const float* const (&ph)[P], const i
                 ls[p][j] = ld(ps + 1);
                 os[p][j] = ld(ps + 4 + d[p]);
             }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             float Mb = M[p];
 #pragma unroll
             for (int j = 0; j < kCB; ++j) Mb = s0 + j < S ? fmaxf(Mb, ms[p][j]) : Mb;
-            if (Mb == -__builtin_inff()) continue;
+            // No state yet (Mb = -inf, so M = -inf, L = O = 0): every weight
+            // is 0 and nothing changes.  Selects, not a branch: behind a
+            // branch the compiler issues the O loads only once the M loads
+            // have arrived, two memory latencies instead of one.
+            const bool any = Mb != -__builtin_inff();
             const float r = M[p] == -__builtin_inff() ? 0.0f : exp_fast(M[p] - Mb);
             L[p] *= r;
             O[p] *= r;
 #pragma unroll
             for (int j = 0; j < kCB; ++j) {
-                const float w = s0 + j < S ? exp_fast(ms[p][j] - Mb) : 0.0f;
+                const float w = s0 + j < S && any ? exp_fast(ms[p][j] - Mb) : 0.0f;
                 L[p] += ls[p][j] * w;
                 O[p] += os[p][j] * w;
             }

@@ -164,6 +164,11 @@ __device__ __forceinline__ void rows(int blk, int nblk, const uint16_t* __restri
         ir = __builtin_amdgcn_readfirstlane(wrap ? ir + 1 : ir);
         __builtin_amdgcn_sched_barrier(0);
     }
+    // ADD: the values the rows add to, loaded behind the prologue so that
+    // their latency passes while the weights stream.
+    float y_old = 0.0f;
+    if constexpr (ADD) y_old = lane < R ? Yg[gw + lane * NW] : 0.0f;
+    __builtin_amdgcn_sched_barrier(0);
 
     // Stage x (zeros past K, up to the whole last piece), with the x
     // operation applied.
@@ -263,7 +268,7 @@ __device__ __forceinline__ void rows(int blk, int nblk, const uint16_t* __restri
 
     if (lane < R) {
         const float out = kNorm ? res * out_scale : res;
-        Yg[gw + lane * NW] = ADD ? Yg[gw + lane * NW] + out : out;
+        Yg[gw + lane * NW] = ADD ? y_old + out : out;
     }
     if constexpr (ARGMAX) {
         // the wave's best key (0: no row) into slot `wave` of the caller's

@@ -69,10 +69,17 @@ struct Rope {
     int cache_jobs = 0;
     uint64_t* keys = nullptr;  // kEpiArgmax: one key per tile
 
-    __device__ __forceinline__ int position() const { return pos_dev ? pos_dev[0] : pos; }
+    // A scalar load: the position does not change during a launch.  (As a
+    // vector load, uniform, its value would go through readfirstlane, which
+    // waits for every load in flight, the weight ring's too.)
+    __device__ __forceinline__ int position() const {
+        return pos_dev ? ((const __attribute__((address_space(4))) int32_t*)pos_dev)[0] : pos;
+    }
     // Where output set j (a job, or kRopeCacheBf16Bit for the BF16 rows) starts.
-    __device__ __forceinline__ float* dest(float* y, int j) const {
-        return pos_dev && ((cache_jobs >> j) & 1) ? y + static_cast<int64_t>(pos_dev[0]) * cache_row : y;
+    __device__ __forceinline__ float* dest(float* y, int j) const { return dest_at(y, j, position()); }
+    // The same with the position already read (p == position()).
+    __device__ __forceinline__ float* dest_at(float* y, int j, int p) const {
+        return pos_dev && ((cache_jobs >> j) & 1) ? y + static_cast<int64_t>(p) * cache_row : y;
     }
 };
 
@@ -358,10 +365,33 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
         __builtin_amdgcn_sched_barrier(0);
     }
 
+    // The epilogue's own operands, loaded right behind the prologue so that
+    // their latency passes while the weights stream rather than after the
+    // last product: the value a row adds to (kEpiAdd), the position and the
+    // row's rotation frequency (kEpiRope).  Lanes past 16 and tile slots past
+    // the last tile read a row of the job that exists, unused.
+    const int row = row0 + ln.n;
+    const Four<uint64_t> ys = {sreg(jobs.y[0]), sreg(jobs.y[1]), sreg(jobs.y[2]), sreg(jobs.y[3])};
+    float* yj = reinterpret_cast<float*>(ys[job]);
+    // Global (not flat) loads: a flat load also counts in lgkmcnt, and the
+    // staging barrier's LDS wait would then wait for it.
+    using GF = const __attribute__((address_space(1))) float;
+    float y_old = 0.0f;
+    if constexpr (EPI == kEpiAdd) y_old = ((GF*)yj)[min(row, n_job - 1)];
+    int rpos = 0;
+    float rfreq = 0.0f;
+    if constexpr (EPI == kEpiRope) {
+        rpos = rope.position();
+        if ((rope.jobs >> job) & 1)  // wave-uniform
+            rfreq = ((GF*)rope.inv_freq)[(row % rope.head_dim) >> 1];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
     // The x loads are older than the 3*D prologue loads: wait for them
     // alone (XP * nthreads >= K/4, checked by the host), then convert.
+    // (The residual load above is younger still: this wait leaves it.)
     if constexpr (CW == 0) {
-    wait_vmcnt<3 * D>();
+    wait_vmcnt<3 * D + (EPI == kEpiAdd ? 1 : 0)>();
     // x past the register batch (K above XP * nthreads * 4): loaded after
     // the weight prologue, so its waits are full ones; large K only.
     float rest_sq = 0.0f;
@@ -449,11 +479,8 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     float v = acc;
     v += __shfl_xor(v, 16, kWave);
     v += __shfl_xor(v, 32, kWave);
-    const int row = row0 + ln.n;
     const bool keep = row < n_job;  // false for tile slots past the last tile
-    const Four<uint64_t> ys = {sreg(jobs.y[0]), sreg(jobs.y[1]), sreg(jobs.y[2]), sreg(jobs.y[3])};
-    float* yj = reinterpret_cast<float*>(ys[job]);
-    if constexpr (EPI == kEpiRope) yj = rope.dest(yj, job);
+    if constexpr (EPI == kEpiRope) yj = rope.dest_at(yj, job, rpos);
     // Where the row is stored: with the half-split pairing the rows of a
     // rotated job were tiled interleaved (row 2j of a head holds element j,
     // row 2j + 1 element j + head_dim / 2), and go back to their places here.
@@ -472,7 +499,7 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
             const float other = __shfl_xor(val, 1, kWave);
             if ((rope.jobs >> job) & 1) {  // wave-uniform
                 const int j = row % rope.head_dim;
-                const float ang = static_cast<float>(rope.position()) * rope.inv_freq[j >> 1];
+                const float ang = static_cast<float>(rpos) * rfreq;
                 const float c = cosf(ang), sn = sinf(ang);
                 val = (j & 1) ? other * sn + val * c : val * c - other * sn;
             }
@@ -486,7 +513,7 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     };
     if (KS == 1) {
         const float out = finish(v);
-        if (lane < 16 && keep) yj[drow] = EPI == kEpiAdd ? yj[drow] + out : out;
+        if (lane < 16 && keep) yj[drow] = EPI == kEpiAdd ? y_old + out : out;
         keep_key(out);
     } else {
         float* red = reinterpret_cast<float*>(lds + lds_bytes(K));  // [TPW][KS][16]
@@ -498,7 +525,7 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
 #pragma unroll
             for (int q = 1; q < KS; ++q) s += rp[q * 16 + (lane & 15)];
             const float out = finish(s);
-            if (lane < 16 && keep) yj[drow] = EPI == kEpiAdd ? yj[drow] + out : out;
+            if (lane < 16 && keep) yj[drow] = EPI == kEpiAdd ? y_old + out : out;
             keep_key(out);
         }
     }
@@ -628,9 +655,14 @@ hipError_t run_xp(const Jobs& jobs, const float* x, const XArgs& xa, int64_t k, 
 // KS = 1 use KS = 4 (the lm_head: 38.0 us against 40.9 us at KS = 2).
 // KS = 1, 2, 4 run 4 waves per workgroup (4/KS tiles); other splits one
 // tile per workgroup of KS waves.
-template <bool TILED, int XOP = kXNone, int EPI = kEpiNone>
-hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s, const XArgs& xa = XArgs{}) {
-    const int64_t tiles = jobs.total;
+struct Shape {
+    int ks = 1;     // waves per tile
+    int waves = 4;  // weight waves per workgroup
+    int cw = 0;     // converter waves per workgroup
+};
+
+template <bool TILED>
+bool shape_for(int64_t tiles, int64_t k, Shape& sh) {
     const int64_t nb = k / 256;
     const int64_t cus = device_info().cus;
     static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12};
@@ -650,7 +682,7 @@ hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s, 
     // exactly KS waves (one tile) otherwise
     int waves = ks <= 4 ? (4 / ks) * ks : ks;
     if (const int tpw = tune_param("Q4K_TPW", 0)) waves = ks * tpw;
-    if (waves % ks != 0 || waves > kMaxThreads / kWave) return hipErrorInvalidValue;
+    if (waves % ks != 0 || waves > kMaxThreads / kWave) return false;
     // Converter waves (tiled layout): measured per launch shape on the
     // headline token, 8 of them beside the weight waves take o 3072 x 3072
     // from 3.85 to 3.62-3.67 us, the q/k/v launch from 4.86 to 4.57-4.60 and
@@ -658,8 +690,20 @@ hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s, 
     // from 5.90 to 6.66-6.73 and the lm_head (31 rounds of workgroups) from
     // 37.4 to 43.9: so one round of workgroups and K <= 4096 only.
     const int64_t wgs_now = (tiles + waves / ks - 1) / (waves / ks);
-    const int cw = tune_param("Q4K_CONV", TILED && wgs_now <= cus && k <= 4096 && waves + 8 <= 16 ? 8 : 0);
-    if (TILED && cw == 8 && waves + 8 <= 16) return run_xp<4, TILED, XOP, EPI, 8>(jobs, x, xa, k, ks, waves, s);
+    int cw = tune_param("Q4K_CONV", TILED && wgs_now <= cus && k <= 4096 && waves + 8 <= 16 ? 8 : 0);
+    if (!(TILED && cw == 8 && waves + 8 <= 16)) cw = 0;
+    sh.ks = ks;
+    sh.waves = waves;
+    sh.cw = cw;
+    return true;
+}
+
+template <bool TILED, int XOP = kXNone, int EPI = kEpiNone>
+hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s, const XArgs& xa = XArgs{}) {
+    Shape sh;
+    if (!shape_for<TILED>(jobs.total, k, sh)) return hipErrorInvalidValue;
+    const int ks = sh.ks, waves = sh.waves;
+    if (sh.cw == 8) return run_xp<4, TILED, XOP, EPI, 8>(jobs, x, xa, k, ks, waves, s);
     if constexpr (XOP != kXNone || EPI != kEpiNone) {
         return run_xp<4, TILED, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
     } else {
