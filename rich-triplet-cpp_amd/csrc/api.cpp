@@ -145,16 +145,17 @@ int tune_param(const char* name, int fallback) {
 #ifdef RT_HIP_TUNING
     // Sweep builds only (make TUNING=1): RT_HIP_<name> overrides a launch
     // shape.  The library as shipped always runs the measured defaults.
+    // The environment is read once per name; an unset name keeps every
+    // call's own default (which differs between launch shapes).
     static std::mutex mu;
-    static std::vector<std::pair<std::string, int>> cache;
+    static std::vector<std::pair<std::string, std::pair<bool, int>>> cache;
     std::lock_guard<std::mutex> lk(mu);
     for (const auto& kv : cache)
-        if (kv.first == name) return kv.second;
-    int v = fallback;
+        if (kv.first == name) return kv.second.first ? kv.second.second : fallback;
     const std::string env = std::string("RT_HIP_") + name;
-    if (const char* s = std::getenv(env.c_str())) v = std::atoi(s);
-    cache.emplace_back(name, v);
-    return v;
+    const char* s = std::getenv(env.c_str());
+    cache.emplace_back(name, std::make_pair(s != nullptr, s ? std::atoi(s) : 0));
+    return s ? std::atoi(s) : fallback;
 #else
     (void)name;
     return fallback;
