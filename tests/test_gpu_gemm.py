@@ -120,6 +120,26 @@ def test_gemm_large_tile_partial_round(rt, m, n, k):
     assert torch.equal(c1.view(torch.int32), c2.view(torch.int32))
 
 
+@pytest.mark.parametrize("m,n,k", [(3000, 5000, 1024), (4100, 4000, 512), (4608, 3072, 2048)])
+def test_gemm_large_tile_bias(rt, m, n, k):
+    """The large-tile kernel with a bias: 240 tiles (ragged M and N), 272
+    tiles (a second round of 16) and 216 tiles (the FLUX MLP-out tile grid):
+    the output equals the float64 product of the same bf16 operands plus the
+    bias (tolerance (i)), and a second run agrees bit for bit."""
+    import torch
+    say(f"[gemm large tile + bias] {m}x{n}x{k}")
+    g = torch.Generator(device="cuda").manual_seed(m + n + k)
+    a = torch.randn((m, k), generator=g, device="cuda").bfloat16()
+    wb = (torch.randn((n, k), generator=g, device="cuda") * 0.02).bfloat16()
+    bias = torch.randn(n, generator=g, device="cuda")
+    c1 = rt.gemm(rt.BF16, a, wb.view(torch.int16), n, k, bias=bias)
+    c2 = rt.gemm(rt.BF16, a, wb.view(torch.int16), n, k, bias=bias)
+    err = same_operand_err(c1 - bias, a, wb, seed=n)
+    say(f"[gemm large tile + bias] {m}x{n}x{k} same-operand normwise {err:.2e} (float64, 64 columns)")
+    assert err <= GEMM_TOL_SAME_OPERANDS
+    assert torch.equal(c1.view(torch.int32), c2.view(torch.int32))
+
+
 @pytest.mark.parametrize("m,n,k,a_bf16", [(256, 8192, 3072, False), (200, 1000, 1024, True),
                                          (160, 3072, 8192, False), (512, 3072, 8192, False),
                                          (512, 8192, 3072, False), (1000, 4096, 4096, False),
