@@ -251,11 +251,11 @@ __device__ __forceinline__ float ld_dev(const float* p) {
 
 // Fold the S split states of P (row, query head, dimension d) pairs in split
 // order (so the result does not depend on which workgroup merges): running
-// (M, L, O), rescaled between batches of up to CB splits whose loads, for
+// (M, L, O), rescaled between batches of up to kCB splits whose loads, for
 // all P pairs, are issued before any is used (indices past S repeat split
 // S - 1, in bounds, with weight 0): one memory latency per batch instead of
 // one per split and pair.
-template <int PART, int P, bool COH, int CB = 16>
+template <int PART, int P, bool COH>
 __device__ __forceinline__ void fold_splits(const float* const (&ph)[P], const int (&d)[P], int S, float (&res)[P]) {
     auto ld = [](const float* p) { return COH ? ld_dev(p) : *p; };
     float M[P], L[P], O[P];
@@ -265,7 +265,7 @@ __device__ __forceinline__ void fold_splits(const float* const (&ph)[P], const i
         L[p] = 0.0f;
         O[p] = 0.0f;
     }
-    constexpr int kCB = CB;
+    constexpr int kCB = 16;
     for (int s0 = 0; s0 < S; s0 += kCB) {
         // every load of the batch, for all of this thread's P pairs, first
         float ms[P][kCB], ls[P][kCB], os[P][kCB];
@@ -505,29 +505,19 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
 }
 
 // Second launch of the two-launch form: workgroup (query head, row), one
-// thread per dimension, folds the plain-stored partials in split order.
-// POS: only the busy splits (their count from the position); otherwise all
-// S, with no read of the position, so the loads issue at once (idle splits
-// hold M = -inf, L = O = 0 and change nothing: the same values).  CB: splits
-// per batch of loads (a batch is one memory latency).  The launch below
-// runs the position-free form.
-template <int HD, int CB, bool POS>
+// thread per dimension, folds the plain-stored partials of all S splits in
+// split order, with no read of the position, so its loads issue at once (a
+// split past the cached range holds M = -inf, L = O = 0 and changes
+// nothing).
+template <int HD>
 __global__ __launch_bounds__(HD) void k_attn2_combine(const AttnArgs a, int S) {
     using Geo = AttnGeom<HD>;
     const int h = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
     const int n_q = gridDim.x;
-    int busy = S;
-    if constexpr (POS) {
-        int k0, k1;
-        attn_range(a, m, k0, k1);
-        const int len = k1 - k0;
-        const int chunk = attn_chunk<Geo::BATCH>(len, S);
-        busy = min(S, (len + chunk - 1) / chunk);
-    }
     const float* ph[1] = {a.part + (static_cast<int64_t>(m) * n_q + h) * S * Geo::PART};
     const int dd[1] = {d};
     float res[1];
-    fold_splits<Geo::PART, 1, false, CB>(ph, dd, busy, res);
+    fold_splits<Geo::PART, 1, false>(ph, dd, S, res);
     a.out[(static_cast<int64_t>(m) * n_q + h) * HD + d] = res[0];
 }
 
@@ -545,13 +535,12 @@ hipError_t run_attn(const AttnArgs& a, int S, int M, hipStream_t s) {
         hipLaunchKernelGGL((k_attn2_partial<HD, G, F16, true>), grid, dim3(kAT), 0, s, a);
     } else {
         hipLaunchKernelGGL((k_attn2_partial<HD, G, F16, false>), grid, dim3(kAT), 0, s, a);
-        // The merge folds all S splits with no read of the position.
         // Measured (engine tokens, Llama-3.2-3B / Gemma-3-4B shapes, 1024
         // positions, 17 splits): 1120 / 1951 us against 1125-1130 / 1949-1963
         // folding only the busy splits after reading the position; batches
         // of 32 splits (one latency for all 17) 1137-1150 / 2002-2044.
-        hipLaunchKernelGGL((k_attn2_combine<HD, 16, false>), dim3(static_cast<unsigned>(a.n_kv * G),
-                           static_cast<unsigned>(M)), dim3(HD), 0, s, a, S);
+        hipLaunchKernelGGL(k_attn2_combine<HD>, dim3(static_cast<unsigned>(a.n_kv * G), static_cast<unsigned>(M)),
+                           dim3(HD), 0, s, a, S);
     }
     return hipGetLastError();
 }

@@ -681,6 +681,15 @@ bool shape_for(int64_t tiles, int64_t k, Shape& sh) {
     // a whole number of tiles per workgroup: 4 waves for KS = 1, 2, 4;
     // exactly KS waves (one tile) otherwise
     int waves = ks <= 4 ? (4 / ks) * ks : ks;
+    // More tiles than one round of those workgroups holds, but no more than
+    // 8 per CU: one round at KS = 1 with one weight wave per tile (and the
+    // converter waves beside them).  Gemma-3-4B's gate+up, 1280 tiles at
+    // K = 2560: 256 workgroups of 5 tiles instead of 640 of 2.
+    if (TILED && (tiles + waves / ks - 1) / (waves / ks) > cus && (tiles + cus - 1) / cus <= 8 && k <= 4096 &&
+        tune_param("Q4K_ONE_ROUND", 1)) {
+        ks = 1;
+        waves = static_cast<int>((tiles + cus - 1) / cus);
+    }
     if (const int tpw = tune_param("Q4K_TPW", 0)) waves = ks * tpw;
     if (waves % ks != 0 || waves > kMaxThreads / kWave) return false;
     // Converter waves (tiled layout): measured per launch shape on the
