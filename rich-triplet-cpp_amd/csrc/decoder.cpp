@@ -176,6 +176,29 @@ int attn_splits(const rt_hip_decoder* d, const Layer& L, int m, int* splits) {
     return RT_HIP_OK;
 }
 
+// Gemma 3's post-attention and post-FFN norms with their residual adds
+// (metal_decode.mm:467-480) run inside the next launch that reads their
+// result: gate/up, and the next layer's q/k/v, stage
+// x = a + RMSNorm(b) * (1 + g2) and normalize it in one pass, one workgroup
+// storing x for the residual add after (launch_gemv_q4k_postnorm).  Only
+// where that launch is all Q4_K on a shape with converter waves; otherwise
+// the separate norm launch runs.
+bool postnorm_into_qkv(const rt_hip_decoder* d, int li) {
+    if (!d->gemma || li < 1 || li >= d->cfg.n_layers) return false;
+    const Layer& L = d->layers[li];
+    if (!(L.q.q4k() && L.k.q4k() && L.v.q4k())) return false;
+    const int64_t n[3] = {L.q.n, L.k.n, L.v.n};
+    return q4k_postnorm_fits(3, n, d->cfg.hidden);
+}
+
+bool postnorm_into_gate_up(const rt_hip_decoder* d, int li) {
+    if (!d->gemma) return false;
+    const Layer& L = d->layers[li];
+    if (!(L.gate.q4k() && L.up.q4k())) return false;
+    const int64_t n[2] = {L.gate.n, L.up.n};
+    return q4k_postnorm_fits(2, n, d->cfg.hidden);
+}
+
 // ---- one layer, single token ------------------------------------------------
 int layer_step1(rt_hip_decoder* d, int li, hipStream_t s) {
     const auto& c = d->cfg;
@@ -208,6 +231,15 @@ int layer_step1(rt_hip_decoder* d, int li, hipStream_t s) {
                                                 RopeCache{d->dstate, kvd, 0x2 | kRopeCacheBf16}),
                      "decoder: q/k/v + RoPE + KV append");
         }
+    } else if (postnorm_into_qkv(d, li)) {
+        // the previous layer's post-FFN norm and residual add, then this
+        // layer's attention norm
+        const void* w[3] = {L.q.tiled, L.k.tiled, L.v.tiled};
+        float* y[3] = {d->q, d->k, d->v};
+        const int64_t n[3] = {L.q.n, L.k.n, L.v.n};
+        rc = chk(launch_gemv_q4k_postnorm(3, w, y, n, d->hidden2, d->down, d->layers[li - 1].post_ffn_norm,
+                                          L.attn_norm, c.norm_eps, H, d->hidden, s),
+                 "decoder: post-FFN norm + q/k/v");
     } else if (L.q.q4k() && L.k.q4k() && L.v.q4k()) {
         const void* w[3] = {L.q.tiled, L.k.tiled, L.v.tiled};
         float* y[3] = {d->q, d->k, d->v};
@@ -279,14 +311,21 @@ int layer_step1(rt_hip_decoder* d, int li, hipStream_t s) {
         }
     } else {
         rc = gemv1(L.o, d->attn, d->o, s);
-        if (!rc)
+        if (!rc && !postnorm_into_gate_up(d, li))
             rc = chk(launch_rmsnorm_rows(d->o, L.post_attn_norm, d->hidden, d->hidden2, H, 1, c.norm_eps, true, s),
                      "decoder: post-attention norm");
     }
     if (rc) return rc;
     // gate/up on RMSNorm of the residual stream
     float* h = d->gemma ? d->hidden2 : d->hidden;
-    if (L.gate.q4k() && L.up.q4k()) {
+    if (postnorm_into_gate_up(d, li)) {
+        const void* w[2] = {L.gate.tiled, L.up.tiled};
+        float* y[2] = {d->gate, d->up};
+        const int64_t n[2] = {L.gate.n, L.up.n};
+        rc = chk(launch_gemv_q4k_postnorm(2, w, y, n, d->hidden, d->o, L.post_attn_norm, L.ffn_norm, c.norm_eps, H,
+                                          d->hidden2, s),
+                 "decoder: post-attention norm + gate/up");
+    } else if (L.gate.q4k() && L.up.q4k()) {
         const void* w[2] = {L.gate.tiled, L.up.tiled};
         float* y[2] = {d->gate, d->up};
         const int64_t n[2] = {L.gate.n, L.up.n};
@@ -323,7 +362,7 @@ int layer_step1(rt_hip_decoder* d, int li, hipStream_t s) {
         rc = chk(launch_gelu_mul(d->gate, d->up, d->act, F, s), "decoder: gelu");
         if (!rc) rc = gemv1(L.down, d->act, d->down, s);
     }
-    if (!rc)
+    if (!rc && !postnorm_into_qkv(d, li + 1))
         rc = chk(launch_rmsnorm_rows(d->down, L.post_ffn_norm, d->hidden2, d->hidden, H, 1, c.norm_eps, true, s),
                  "decoder: post-FFN norm");
     return rc;

@@ -34,12 +34,16 @@ namespace rt_hip {
 //   kXSwiGlu   silu(gate) * up, x = gate     (tensor_node.cpp:391-402,
 //              transformer5.cpp:186-190);
 //   kXGelu     gelu_tanh(gate) * up, x = gate (the Gemma 3 MLP gating,
-//              decode_gemma3.msl:128-158).
+//              decode_gemma3.msl:128-158);
+//   kXPostNorm1 the Gemma 3 residual step, then kXRmsNorm1 of its result:
+//              x = a + RMSNorm(b) * (1 + g2) (the post-attention / post-FFN
+//              norm and residual add, metal_decode.mm:467-480), x also
+//              stored for the next residual add (Q4_K GEMV only).
 // `aux` is gamma or up.  RMSNorm(x) * g = rms_inv * (x * g) with one scalar
 // rms_inv per vector, so kernels stage x * g and scale the finished dot
 // products by rms_inv (equal in exact arithmetic); the sum of squares is
 // reduced per wave and across waves through LDS at the staging barrier.
-enum XOp { kXNone = 0, kXRmsNorm = 1, kXRmsNorm1 = 2, kXSwiGlu = 3, kXGelu = 4 };
+enum XOp { kXNone = 0, kXRmsNorm = 1, kXRmsNorm1 = 2, kXSwiGlu = 3, kXGelu = 4, kXPostNorm1 = 5 };
 
 // silu(g) * u in the reference's order, the sigmoid from the hardware exp2
 // and reciprocal (about 1 ulp each; exp overflows to inf for g < -88 and

@@ -123,8 +123,25 @@ __host__ __device__ inline size_t norm_offset(int K, int waves) {
 // the widest batch (16 f32x4 per thread, 8 with an x operation), which the
 // host picks when nothing narrower covers K.  The narrower ones carry no
 // loop (its registers and code cost the short launches measurably).
+// kXPostNorm1 needs all of b before any x exists, so it never has a rest:
+// the host runs it only where the batch covers K.
 template <int XP, int XOP>
-constexpr bool kHasRest = XP >= (XOP == kXNone ? 16 : 8);
+constexpr bool kHasRest = XP >= (XOP == kXNone ? 16 : 8) && XOP != kXPostNorm1;
+
+// kXPostNorm1's operands: x = X + RMSNorm(b) * (1 + g2), stored to out.
+// Its own kernel takes them (k_gemv_q4k_postnorm), so the other x-op
+// kernels' arguments do not grow.
+struct PostNorm {
+    const float* b = nullptr;
+    const float* g2 = nullptr;
+    float* out = nullptr;
+};
+
+// x operations that end in an RMSNorm, and those whose gamma applies as 1 + g
+template <int XOP>
+constexpr bool kNormOp = XOP == kXRmsNorm || XOP == kXRmsNorm1 || XOP == kXPostNorm1;
+template <int XOP>
+constexpr bool kOnePlus = XOP == kXRmsNorm1 || XOP == kXPostNorm1;
 
 // The part of x past a staging batch held in registers (K beyond what XP
 // f32x4 per thread cover, up to the LDS bound): f32x4 f = first, first +
@@ -167,12 +184,20 @@ __device__ __forceinline__ float stage_rest(const float* __restrict__ X, const f
 // limb planes and, for RMSNorm, its wave's partial sum of squares into
 // slot `nslot` of the norm partials.  The weight waves of the workgroup
 // issue their loads meanwhile; nothing here waits for them.
+// kXPostNorm1 (cthreads * XP * 4 >= K, checked by the host): X is the
+// residual a, and x = a + (b * rms_inv(b)) * (1 + g2) is formed first, in
+// the separate norm's order (k_rmsnorm_rows); the sum of squares of b goes
+// through one more barrier (the weight waves take part in it), its wave
+// partials in the K-split rows' LDS, which are not used before the staging
+// barrier.  `store_x` (one workgroup) stores x to pn.out.
 template <int XP, int XOP>
 __device__ __forceinline__ void convert_x(const float* __restrict__ X, const float* __restrict__ aux, int K, int c,
-                                          int cthreads, int lane, int nslot, float* norm_part, uint8_t* lds) {
+                                          int cthreads, int lane, int nslot, float* norm_part, uint8_t* lds,
+                                          float eps, const PostNorm& pn, bool store_x) {
     const int nx = K >> 2;
     const f32x4* const X4 = reinterpret_cast<const f32x4*>(X);
-    f32x4 xv[XP], av[XP];
+    constexpr int XPN = XOP == kXPostNorm1 ? XP : 1;
+    f32x4 xv[XP], av[XP], bv[XPN], gv[XPN];
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
         const int f = c + cthreads * i;
@@ -186,9 +211,44 @@ __device__ __forceinline__ void convert_x(const float* __restrict__ X, const flo
             av[i] = A4[f < nx ? f : 0];
         }
     }
+    if constexpr (XOP == kXPostNorm1) {
+        const f32x4* const B4 = reinterpret_cast<const f32x4*>(pn.b);
+        const f32x4* const G4 = reinterpret_cast<const f32x4*>(pn.g2);
+#pragma unroll
+        for (int i = 0; i < XP; ++i) {
+            const int f = c + cthreads * i;
+            bv[i] = B4[f < nx ? f : 0];
+            gv[i] = G4[f < nx ? f : 0];
+        }
+        float sb = 0.0f;
+#pragma unroll
+        for (int i = 0; i < XP; ++i) {
+            const f32x4 v = c + cthreads * i < nx ? bv[i] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            sb += (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+        }
+        sb = bf16_gemv::wave_sum(sb, lane);
+        float* const bpart = reinterpret_cast<float*>(lds + lds_bytes(K));
+        if (lane == 0) bpart[nslot] = sb;
+        lds_barrier();
+        float tb = 0.0f;
+        for (int w = 0; w < (cthreads >> 6); ++w) tb += bpart[w];
+        const float rb = 1.0f / __builtin_sqrtf(tb * (1.0f / static_cast<float>(K)) + eps);
+#pragma unroll
+        for (int i = 0; i < XP; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[i][e] = xv[i][e] + (bv[i][e] * rb) * (1.0f + gv[i][e]);
+        if (store_x) {
+            f32x4* const O4 = reinterpret_cast<f32x4*>(pn.out);
+#pragma unroll
+            for (int i = 0; i < XP; ++i) {
+                const int f = c + cthreads * i;
+                if (f < nx) O4[f] = xv[i];
+            }
+        }
+    }
     float rest_sq = 0.0f;
     if constexpr (kHasRest<XP, XOP>) rest_sq = stage_rest<XOP>(X, aux, K, c + cthreads * XP, cthreads, lds);
-    if constexpr (XOP == kXRmsNorm || XOP == kXRmsNorm1) {
+    if constexpr (kNormOp<XOP>) {
         float sq = rest_sq;
 #pragma unroll
         for (int i = 0; i < XP; ++i) {
@@ -200,7 +260,7 @@ __device__ __forceinline__ void convert_x(const float* __restrict__ X, const flo
 #pragma unroll
         for (int i = 0; i < XP; ++i)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) xv[i][e] *= XOP == kXRmsNorm1 ? 1.0f + av[i][e] : av[i][e];
+            for (int e = 0; e < 4; ++e) xv[i][e] *= kOnePlus<XOP> ? 1.0f + av[i][e] : av[i][e];
     } else if constexpr (XOP == kXSwiGlu) {
 #pragma unroll
         for (int i = 0; i < XP; ++i)
@@ -239,7 +299,9 @@ template <int D, int XP, bool TILED, bool J34, int XOP = kXNone, int EPI = kEpiN
 __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, int K, uint32_t split, int nthreads,
                                           const uint8_t* w0, const uint8_t* w1, int n0, int n1, int tile1,
                                           const Jobs& jobs, uint8_t* lds, const float* __restrict__ aux = nullptr,
-                                          float eps = 0.0f, const Rope& rope = Rope{}) {
+                                          float eps = 0.0f, const Rope& rope = Rope{},
+                                          const PostNorm& pn = PostNorm{}) {
+    static_assert(XOP != kXPostNorm1 || CW > 0, "the post-norm residual step runs in converter waves");
     const int count = static_cast<int>(split >> 29);
     const int wwaves = (nthreads >> 6) - CW;  // weight waves
     if constexpr (CW > 0) {
@@ -247,7 +309,8 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
         if (w >= wwaves) {
             const int c = static_cast<int>(threadIdx.x) - wwaves * kWave;
             float* const np = reinterpret_cast<float*>(lds + norm_offset(K, wwaves));
-            convert_x<XP, XOP>(X, aux, K, c, CW * kWave, static_cast<int>(threadIdx.x) & 63, w - wwaves, np, lds);
+            convert_x<XP, XOP>(X, aux, K, c, CW * kWave, static_cast<int>(threadIdx.x) & 63, w - wwaves, np, lds,
+                               eps, pn, blk == 0);
             lds_barrier();
             return;
         }
@@ -443,11 +506,13 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     }
     if (tid < 4) reinterpret_cast<u32x4*>(lds + 3 * static_cast<size_t>(K))[tid] = u32x4{0u, 0u, 0u, 0u};
     }
+    // the converter waves' first barrier (their sum of squares of b)
+    if constexpr (XOP == kXPostNorm1) __builtin_amdgcn_s_barrier();
     lds_barrier();
     // rms_inv = 1 / sqrt(sum(x^2) * (1/K) + eps), as the reference forms it
     // (the sum itself is reduced in a tree).
     float out_scale = 1.0f;
-    if constexpr (XOP == kXRmsNorm || XOP == kXRmsNorm1) {
+    if constexpr (kNormOp<XOP>) {
         const int parts = CW > 0 ? CW : (nthreads >> 6);
         const float* part = reinterpret_cast<const float*>(lds + norm_offset(K, CW > 0 ? wwaves : (nthreads >> 6)));
         float tot = 0.0f;
@@ -494,7 +559,7 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     // The row's final value, computed by every lane of the storing wave (the
     // RoPE partner exchange needs the whole wave).
     auto finish = [&](float val) {
-        if constexpr (XOP == kXRmsNorm || XOP == kXRmsNorm1) val *= out_scale;
+        if constexpr (kNormOp<XOP>) val *= out_scale;
         if constexpr (EPI == kEpiRope) {
             const float other = __shfl_xor(val, 1, kWave);
             if ((rope.jobs >> job) & 1) {  // wave-uniform
@@ -564,6 +629,16 @@ __global__ __launch_bounds__(CW > 0 ? 1024 : kMaxThreads) void k_gemv_q4k_xop(
                                                tile1, jobs, lds, aux, eps, rope);
 }
 
+// kXPostNorm1 (one shape: converter waves, two f32x4 per converter thread).
+template <bool J34>
+__global__ __launch_bounds__(1024) void k_gemv_q4k_postnorm(
+    const float* __restrict__ X, const float* __restrict__ aux, const uint8_t* w0, const uint8_t* w1, int K,
+    uint32_t split, int nthreads, int n0, int n1, int tile1, const Jobs jobs, float eps, const PostNorm pn) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    q4k_tiles<4, 2, true, J34, kXPostNorm1, kEpiNone, 8>(static_cast<int>(blockIdx.x), X, K, split, nthreads, w0,
+                                                         w1, n0, n1, tile1, jobs, lds, aux, eps, Rope{}, pn);
+}
+
 // A layer's q/k/v when v is BF16 (Q6_K widened): the first q4k_wgs
 // workgroups run the tiled Q4_K GEMVs, the rest the BF16 rows, all on the
 // same x.  One launch instead of two dependent ones; each workgroup's work is
@@ -592,6 +667,7 @@ struct XArgs {
     const float* aux = nullptr;
     float eps = 0.0f;
     Rope rope;
+    PostNorm pn;
 };
 
 // `waves` weight waves plus CW converter waves per workgroup.
@@ -606,6 +682,11 @@ hipError_t run(const Jobs& jobs, const float* x, const XArgs& xa, int64_t k, int
     if constexpr (XOP == kXNone && EPI == kEpiNone) {
         hipLaunchKernelGGL((k_gemv_q4k_mfma<D, XP, TILED, J34, CW>), g, b, lds, s, x, static_cast<int>(k), split,
                            all * kWave, jobs.w[0], jobs.w[1], jobs.n[0], jobs.n[1], jobs.tile0[1], jobs);
+    } else if constexpr (XOP == kXPostNorm1) {
+        static_assert(D == 4 && XP == 2 && TILED && EPI == kEpiNone && CW == 8, "the post-norm kernel's one shape");
+        hipLaunchKernelGGL((k_gemv_q4k_postnorm<J34>), g, b, lds, s, x, xa.aux, jobs.w[0], jobs.w[1],
+                           static_cast<int>(k), split, all * kWave, jobs.n[0], jobs.n[1], jobs.tile0[1], jobs, xa.eps,
+                           xa.pn);
     } else {
         static_assert(D == 4 && TILED, "x operations and RoPE run on the tiled layout, ring depth 4");
         hipLaunchKernelGGL((k_gemv_q4k_xop<XP, J34, XOP, EPI, CW>), g, b, lds, s, x, xa.aux, jobs.w[0], jobs.w[1],
@@ -712,13 +793,21 @@ hipError_t dispatch(const Jobs& jobs, const float* x, int64_t k, hipStream_t s, 
     Shape sh;
     if (!shape_for<TILED>(jobs.total, k, sh)) return hipErrorInvalidValue;
     const int ks = sh.ks, waves = sh.waves;
-    if (sh.cw == 8) return run_xp<4, TILED, XOP, EPI, 8>(jobs, x, xa, k, ks, waves, s);
-    if constexpr (XOP != kXNone || EPI != kEpiNone) {
-        return run_xp<4, TILED, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
+    if constexpr (XOP == kXPostNorm1) {
+        // converter waves only (K <= 4096), two f32x4 per converter thread
+        // covering K
+        if (sh.cw != 8 || k > 2 * 4 * 8 * kWave) return hipErrorNotSupported;
+        return jobs.count > 2 ? run<4, 2, TILED, true, XOP, EPI, 8>(jobs, x, xa, k, ks, waves, s)
+                              : run<4, 2, TILED, false, XOP, EPI, 8>(jobs, x, xa, k, ks, waves, s);
     } else {
-        const int d = tune_param("Q4K_RING", 4);
-        return d == 8 ? run_xp<8, TILED, XOP, EPI>(jobs, x, xa, k, ks, waves, s)
-                      : run_xp<4, TILED, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
+        if (sh.cw == 8) return run_xp<4, TILED, XOP, EPI, 8>(jobs, x, xa, k, ks, waves, s);
+        if constexpr (XOP != kXNone || EPI != kEpiNone) {
+            return run_xp<4, TILED, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
+        } else {
+            const int d = tune_param("Q4K_RING", 4);
+            return d == 8 ? run_xp<8, TILED, XOP, EPI>(jobs, x, xa, k, ks, waves, s)
+                          : run_xp<4, TILED, XOP, EPI>(jobs, x, xa, k, ks, waves, s);
+        }
     }
 }
 
@@ -732,11 +821,11 @@ size_t mfma_gemv_lds_bytes(int64_t k, int waves) {
 
 size_t q4k_m1_lds_bytes(int64_t k) { return mfma_gemv_lds_bytes(k, kMaxThreads / kWave); }
 
-hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* const* y, const int64_t* n,
-                              const float* x, const float* aux, float eps, int64_t k, hipStream_t s,
-                              const float* inv_freq, int pos, int head_dim, int rope_jobs, bool add,
-                              const RopeCache& cache, uint64_t* argmax_keys) {
-    if (count < 1 || count > kMaxJobs || (aux == nullptr && xop != kXNone)) return hipErrorInvalidValue;
+namespace {
+
+// The job table of `count` (1..4) products; unused entries repeat job 0
+// with no tiles.
+Jobs make_jobs(int count, const void* const* w, float* const* y, const int64_t* n) {
     Jobs jobs{};
     jobs.count = count;
     int64_t tiles = 0;
@@ -754,6 +843,17 @@ hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* 
         jobs.tile0[j] = static_cast<int>(tiles);
     }
     jobs.total = static_cast<int>(tiles);
+    return jobs;
+}
+
+}  // namespace
+
+hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* const* y, const int64_t* n,
+                              const float* x, const float* aux, float eps, int64_t k, hipStream_t s,
+                              const float* inv_freq, int pos, int head_dim, int rope_jobs, bool add,
+                              const RopeCache& cache, uint64_t* argmax_keys) {
+    if (count < 1 || count > kMaxJobs || (aux == nullptr && xop != kXNone)) return hipErrorInvalidValue;
+    const Jobs jobs = make_jobs(count, w, y, n);
     XArgs xa;
     xa.aux = aux;
     xa.eps = eps;
@@ -798,27 +898,34 @@ hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* 
     }
 }
 
+bool q4k_postnorm_fits(int count, const int64_t* n, int64_t k) {
+    if (count < 1 || count > kMaxJobs || k % 256 != 0) return false;
+    int64_t tiles = 0;
+    for (int j = 0; j < count; ++j) tiles += (n[j] + 15) / 16;
+    Shape sh;
+    return shape_for<true>(tiles, k, sh) && sh.cw == 8 && k <= 2 * 4 * 8 * kWave;
+}
+
+hipError_t launch_gemv_q4k_postnorm(int count, const void* const* w, float* const* y, const int64_t* n,
+                                    const float* a, const float* b, const float* g2, const float* gamma, float eps,
+                                    int64_t k, float* x_out, hipStream_t s) {
+    if (count < 1 || count > kMaxJobs || !a || !b || !g2 || !gamma || !x_out) return hipErrorInvalidValue;
+    if (!q4k_postnorm_fits(count, n, k)) return hipErrorNotSupported;
+    const Jobs jobs = make_jobs(count, w, y, n);
+    XArgs xa;
+    xa.aux = gamma;
+    xa.eps = eps;
+    xa.pn.b = b;
+    xa.pn.g2 = g2;
+    xa.pn.out = x_out;
+    return dispatch<true, kXPostNorm1>(jobs, a, k, s, xa);
+}
+
 hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* const* y,
                                       const int64_t* n, const float* x, int64_t k, hipStream_t s,
                                       bool tiled) {
     if (count < 1 || count > kMaxJobs) return hipErrorInvalidValue;
-    Jobs jobs{};
-    jobs.count = count;
-    int64_t tiles = 0;
-    for (int j = 0; j < count; ++j) {
-        jobs.w[j] = static_cast<const uint8_t*>(w[j]);
-        jobs.y[j] = y[j];
-        jobs.n[j] = static_cast<int>(n[j]);
-        jobs.tile0[j] = static_cast<int>(tiles);
-        tiles += (n[j] + 15) / 16;
-    }
-    for (int j = count; j < kMaxJobs; ++j) {
-        jobs.w[j] = jobs.w[0];
-        jobs.y[j] = jobs.y[0];
-        jobs.n[j] = jobs.n[0];
-        jobs.tile0[j] = static_cast<int>(tiles);
-    }
-    jobs.total = static_cast<int>(tiles);
+    const Jobs jobs = make_jobs(count, w, y, n);
     return tiled ? dispatch<true>(jobs, x, k, s) : dispatch<false>(jobs, x, k, s);
 }
 
@@ -870,35 +977,19 @@ hipError_t launch_gemv_q4k_bf16_fused(int count, const void* const* w, float* co
                                       const float* inv_freq, int pos, int head_dim, int rope_jobs,
                                       const RopeCache& cache) {
     if (count < 1 || count > kMaxJobs || k > 8192) return hipErrorInvalidValue;
-    Jobs jobs{};
-    jobs.count = count;
-    int64_t tiles = 0;
-    for (int j = 0; j < count; ++j) {
-        jobs.w[j] = static_cast<const uint8_t*>(w[j]);
-        jobs.y[j] = y[j];
-        jobs.n[j] = static_cast<int>(n[j]);
-        jobs.tile0[j] = static_cast<int>(tiles);
-        tiles += (n[j] + 15) / 16;
-    }
-    for (int j = count; j < kMaxJobs; ++j) {
-        jobs.w[j] = jobs.w[0];
-        jobs.y[j] = jobs.y[0];
-        jobs.n[j] = jobs.n[0];
-        jobs.tile0[j] = static_cast<int>(tiles);
-    }
-    jobs.total = static_cast<int>(tiles);
+    const Jobs jobs = make_jobs(count, w, y, n);
     // Four waves per workgroup on both sides, so the Q4_K split is 4, 2 or 1
     // waves per tile: the largest that divides the super-blocks, leaves two
     // per wave and keeps the Q4_K part to one workgroup per CU.
     const int64_t nb = k / 256, cus = device_info().cus;
     int ks = 1;
     for (int c : {4, 2})
-        if (nb % c == 0 && 2 * c <= nb && (tiles + (4 / c) - 1) / (4 / c) <= cus) {
+        if (nb % c == 0 && 2 * c <= nb && (jobs.total + (4 / c) - 1) / (4 / c) <= cus) {
             ks = c;
             break;
         }
     const int tpw = 4 / ks;
-    const int q4k_wgs = static_cast<int>((tiles + tpw - 1) / tpw);
+    const int q4k_wgs = (jobs.total + tpw - 1) / tpw;
     const size_t lds = q4k_bf16_fused_lds_bytes(k);
     XArgs xa;
     xa.aux = aux;

@@ -102,6 +102,16 @@ hipError_t launch_gemv_q4k_xop(int xop, int count, const void* const* w, float* 
                               bool add = false, const RopeCache& cache = {}, uint64_t* argmax_keys = nullptr);
 // Argmax key slots of a one-job Q4_K GEMV of n rows: its tiles.
 inline int64_t q4k_argmax_partials(int64_t n) { return (n + 15) / 16; }
+// Up to four tiled-Q4_K GEMVs on RMSNorm(x) * (1 + gamma) where
+// x = a + RMSNorm(b) * (1 + g2) (the Gemma 3 post-norm residual step of the
+// previous sub-layer, folded into this launch's staging); x is also stored
+// to x_out (k floats).  Runs only on the launch shapes with converter
+// waves (q4k_postnorm_fits); hipErrorNotSupported otherwise, nothing
+// launched.
+bool q4k_postnorm_fits(int count, const int64_t* n, int64_t k);
+hipError_t launch_gemv_q4k_postnorm(int count, const void* const* w, float* const* y, const int64_t* n,
+                                    const float* a, const float* b, const float* g2, const float* gamma, float eps,
+                                    int64_t k, float* x_out, hipStream_t s);
 hipError_t launch_gemv_q4k_mfma_multi(int count, const void* const* w, float* const* y,
                                       const int64_t* n, const float* x, int64_t k, hipStream_t s,
                                       bool tiled);
