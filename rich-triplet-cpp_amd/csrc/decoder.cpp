@@ -169,7 +169,7 @@ int gemvm(const Proj& p, const float* x, float* y, int m, hipStream_t s) {
 // change from writing past the buffer.
 int attn_splits(const rt_hip_decoder* d, const Layer& L, int m, int* splits) {
     const auto& c = d->cfg;
-    const int S = attention2_splits(c.n_kv_heads, m, L.window > 0 ? L.window : c.max_seq);
+    const int S = attention2_splits(c.n_kv_heads, m, L.window > 0 ? L.window : c.max_seq, c.head_dim);
     if (attention2_workspace(c.n_heads, c.head_dim, S, m) > d->part_bytes)
         return fail(RT_HIP_E_SHAPE, "decoder: attention partials exceed the buffer sized at create");
     *splits = S;
@@ -631,7 +631,7 @@ int rt_hip_decoder_create(const rt_hip_decoder_config* cfg, rt_hip_decoder** out
     // attention partials for the largest split count of any batch size
     size_t pb = 0;
     for (int m = 1; m <= R; ++m) {
-        const int S = attention2_splits(c.n_kv_heads, m, c.max_seq);
+        const int S = attention2_splits(c.n_kv_heads, m, c.max_seq, hd);
         const size_t b = attention2_workspace(c.n_heads, hd, S, m);
         pb = b > pb ? b : pb;
     }

@@ -223,6 +223,12 @@ struct AttnGeom {
     static constexpr int PART = 4 + HD;          // floats per partial state
 };
 
+// AttnGeom<hd>::BATCH for the host (head_dim 64, 128 or 256).
+constexpr int attn_round_positions(int hd) { return (kAT / kWave) * (kWave / (hd / 8)) * kAU; }
+static_assert(attn_round_positions(64) == AttnGeom<64>::BATCH && attn_round_positions(128) == AttnGeom<128>::BATCH &&
+                  attn_round_positions(256) == AttnGeom<256>::BATCH,
+              "host and kernel agree on the positions per round");
+
 struct AttnArgs {
     const float* q;      // [M][n_q * HD]
     const void* kc;
@@ -631,14 +637,18 @@ hipError_t launch_qk_prep(const QkPrep& p, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Enough (kv head, split, row) workgroups for every CU, at least 64
-// positions per split.  Measured on the Llama-3.2-3B engine at 1024
-// positions: 17 splits 6.44 us per partial launch, 32 splits of 32 positions
-// (2 loaded ahead per group) 6.88 us.
-int attention2_splits(int n_kv, int m, int64_t max_len) {
+// Enough (kv head, split, row) workgroups for every CU, at least one round
+// of the partial kernel's positions per split (64 at head_dim 128, 32 at
+// 256): each workgroup then loads its positions in one round, one memory
+// latency.  Measured at 1024 positions: Llama-3.2-3B engine, 17 splits 6.44
+// us per partial launch, 32 splits of 32 positions (2 loaded ahead per
+// group) 6.88 us; Gemma-3-4B engine (head_dim 256) 1889-1903 us/token at 64
+// positions per split (two rounds), 1796-1799 at 32, 1847 at 16.
+int attention2_splits(int n_kv, int m, int64_t max_len, int head_dim) {
     const int64_t cus = device_info().cus;
     int64_t want = (cus + n_kv * m - 1) / (n_kv * m);
-    const int64_t by_len = (max_len + 63) / 64;
+    const int64_t per = tune_param("ATTN_SPLIT_POS", attn_round_positions(head_dim));
+    const int64_t by_len = (max_len + per - 1) / per;
     want = want < by_len ? want : by_len;
     return static_cast<int>(want < 1 ? 1 : want);
 }

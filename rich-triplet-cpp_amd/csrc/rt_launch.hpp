@@ -238,7 +238,7 @@ struct Attn2 {
     float scale = 1.0f;
     bool f16 = false;
 };
-int attention2_splits(int n_kv, int m, int64_t max_len);
+int attention2_splits(int n_kv, int m, int64_t max_len, int head_dim);
 size_t attention2_workspace(int n_q, int head_dim, int splits, int m);
 // part: attention2_workspace bytes; counters: m * n_kv zeroed words (each
 // launch leaves them zero).

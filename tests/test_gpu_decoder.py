@@ -270,11 +270,12 @@ def test_decoder_rejects_bad_use(rt, orc):
 # pre-filled through rt_hip_decoder_set_kv, so several splits are busy and,
 # where the cache is shorter than max_seq, some are idle.
 
-def split_rule(n_kv, m, max_len, cus):
+def split_rule(n_kv, m, max_len, cus, head_dim):
     """attention2_splits (decoder_ops.hip): enough (kv head, split) work-
-    groups for every CU, at least 64 positions per split."""
+    groups for every CU, at least one round of the partial kernel's positions
+    per split (64 at head_dim 128, 32 at 256)."""
     want = -(-cus // (n_kv * m))
-    by_len = -(-max_len // 64)
+    by_len = -(-max_len // (64 if head_dim <= 128 else 32))
     return max(1, min(want, by_len))
 
 
@@ -321,9 +322,9 @@ GEMMA_4B_ATTN = dict(GEMMA, n_heads=8, n_kv_heads=4, head_dim=256, ffn=512, max_
     ("llama3b", LLAMA_3B_ATTN, 100),
     # the bench's cache: S = 16, all busy
     ("llama3b", dict(LLAMA_3B_ATTN, max_seq=1024), 1000),
-    # local layer: window 200 > one chunk, S = 4 (3 busy); global: S = 8 (5 busy)
+    # local layer: window 200 > one chunk, S = 7 (5 busy); global: S = 16 (5 busy)
     ("gemma3_4b", GEMMA_4B_ATTN, 150),
-    # local: the window slides past position 0 (all 4 busy); global 7 of 8
+    # local: the window slides past position 0 (all 7 busy); global 13 of 16
     ("gemma3_4b", GEMMA_4B_ATTN, 400),
 ])
 def test_decoder_long_cache_matches_oracle(rt, orc, arch, cfg, rows):
@@ -341,7 +342,7 @@ def test_decoder_long_cache_matches_oracle(rt, orc, arch, cfg, rows):
         for i, tok in enumerate(rng.integers(0, cfg["vocab"], 4)):
             pos = rows + i
             for li, win in enumerate(windows):
-                S = split_rule(n_kv, 1, win if win else cfg["max_seq"], cus)
+                S = split_rule(n_kv, 1, win if win else cfg["max_seq"], cus, hd)
                 length = min(pos + 1, win) if win else pos + 1
                 busy = busy_rule(length, S, hd)
                 say(f"[decoder {arch}] pos={pos} layer {li}: window {win}, S={S} splits, {busy} busy")
@@ -355,7 +356,7 @@ def test_decoder_long_cache_matches_oracle(rt, orc, arch, cfg, rows):
         say(f"[decoder {arch}] {rows} cached positions: worst step normwise error {worst:.2e}")
         if arch == "llama3b" and cfg["max_seq"] == 2048:
             # the cases meant to hold idle splits do
-            S = split_rule(n_kv, 1, cfg["max_seq"], cus)
+            S = split_rule(n_kv, 1, cfg["max_seq"], cus, hd)
             assert busy_rule(rows + 1, S, hd) < S
     finally:
         dec.close()
@@ -375,7 +376,7 @@ def test_decoder_long_cache_batch_matches_single(rt, orc):
         state = np.random.default_rng(5)
         prefill(m, b, state, 1000)
         tokens = rng.integers(0, cfg["vocab"], 4)
-        S = split_rule(cfg["n_kv_heads"], 4, cfg["max_seq"], cu_count())
+        S = split_rule(cfg["n_kv_heads"], 4, cfg["max_seq"], cu_count(), cfg["head_dim"])
         say(f"[decoder llama3b batch] 4 tokens at position 1000, S={S}")
         assert S > 1
         single = []
