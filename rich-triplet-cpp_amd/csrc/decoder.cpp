@@ -259,9 +259,9 @@ int layer_step1(rt_hip_decoder* d, int li, hipStream_t s) {
         if (!rc) rc = gemv1(L.v, d->normed, d->v, s);
     }
     if (rc) return rc;
-    // per-head norms, RoPE, KV append
+    // per-head norms, RoPE, KV append: inside the attention launch
+    QkPrep p;
     if (!fused_kv) {
-        QkPrep p;
         p.q = d->q;
         p.k = d->k;
         p.v = d->v;
@@ -281,11 +281,10 @@ int layer_step1(rt_hip_decoder* d, int li, hipStream_t s) {
         p.half_split = d->gemma || c.rope_half;
         p.pow_angle = d->gemma;
         p.f16 = c.kv_f16 != 0;
-        rc = chk(launch_qk_prep(p, s), "decoder: q/k prep");
-        if (rc) return rc;
     }
     Attn2 a;
-    a.q = d->q_rot;
+    a.q = fused_kv ? d->q_rot : d->q;
+    a.prep = fused_kv ? nullptr : &p;
     a.k_cache = L.kc;
     a.v_cache = L.vc;
     a.out = d->attn;

@@ -311,16 +311,18 @@ __device__ __forceinline__ void fold_splits(const float* const (&ph)[P], const i
     for (int p = 0; p < P; ++p) res[p] = L[p] > 0.0f ? O[p] / L[p] : 0.0f;
 }
 
+// Eight f16 values (their bits in w) widened to f32.
+__device__ __forceinline__ void widen8(const u32x4 w, f32x4& a, f32x4& b) {
+    auto h2 = [](uint32_t u) { return f32x2{f16_bits_to_f32(u & 0xffffu), f16_bits_to_f32(u >> 16)}; };
+    const f32x2 p0 = h2(w[0]), p1 = h2(w[1]), p2 = h2(w[2]), p3 = h2(w[3]);
+    a = f32x4{p0[0], p0[1], p1[0], p1[1]};
+    b = f32x4{p2[0], p2[1], p3[0], p3[1]};
+}
+
 template <bool F16>
 __device__ __forceinline__ void load8(const void* base, int64_t off, f32x4& a, f32x4& b) {
     if constexpr (F16) {
-        const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const _Float16*>(base) + off);
-        auto h2 = [](uint32_t u) {
-            return f32x2{f16_bits_to_f32(u & 0xffffu), f16_bits_to_f32(u >> 16)};
-        };
-        const f32x2 p0 = h2(w[0]), p1 = h2(w[1]), p2 = h2(w[2]), p3 = h2(w[3]);
-        a = f32x4{p0[0], p0[1], p1[0], p1[1]};
-        b = f32x4{p2[0], p2[1], p3[0], p3[1]};
+        widen8(*reinterpret_cast<const u32x4*>(static_cast<const _Float16*>(base) + off), a, b);
     } else {
         const float* p = static_cast<const float*>(base) + off;
         a = *reinterpret_cast<const f32x4*>(p);
@@ -359,11 +361,68 @@ __device__ __forceinline__ int attn_chunk(int len, int S) {
     return (chunk + BATCH - 1) / BATCH * BATCH;
 }
 
+// k_qk_prep's operations on one head held as 8 values per lane (dims
+// 8 sub .. 8 sub + 7) by the LP lanes of a position group: the optional
+// per-head RMSNorm, x * rms_inv * (1 + g) with rms_inv = 1 / sqrt(sum(x^2) /
+// d + eps), then RoPE with cs / sn the cosine and sine of each dim's pair
+// angle.  Half-split pairs (j, j + d/2) meet across lanes sub and
+// sub ^ (LP / 2); interleaved pairs (2i, 2i + 1) sit in one lane.
+template <int HD>
+__device__ __forceinline__ void prep_head(f32x4& xa, f32x4& xb, bool norm, const float (&g)[8],
+                                          const float (&cs)[8], const float (&sn)[8], bool half, float eps,
+                                          int sub) {
+    constexpr int LP = HD / 8;
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        x[e] = xa[e];
+        x[e + 4] = xb[e];
+    }
+    if (norm) {  // uniform
+        float sq = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sq += x[e] * x[e];
+        sq = group_sum<LP>(sq);
+        const float rms_inv = 1.0f / sqrtf(sq / static_cast<float>(HD) + eps);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = x[e] * rms_inv * (1.0f + g[e]);
+    }
+    if (half) {  // uniform
+        const bool lower = sub < LP / 2;
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = __shfl_xor(x[e], LP / 2, kWave);
+        // the pair's lower dim: x0 * c - x1 * s; its upper dim: x0 * s + x1 * c
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = lower ? x[e] * cs[e] - y[e] * sn[e] : y[e] * sn[e] + x[e] * cs[e];
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const float x0 = x[e], x1 = x[e + 1];
+            x[e] = x0 * cs[e] - x1 * sn[e];
+            x[e + 1] = x0 * sn[e] + x1 * cs[e];
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        xa[e] = x[e];
+        xb[e] = x[e + 4];
+    }
+}
+
 // MERGE: the last split of a (row, kv head) to arrive merges in this launch
 // (partials stored device-coherent); otherwise partials are plain stores
 // and k_attn2_combine merges them in a second launch.
-template <int HD, int G, bool F16, bool MERGE>
-__global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
+// PREP (one row, device position): k_qk_prep's work is done here.  Every
+// workgroup normalizes and rotates its query heads from the raw q, and the
+// new token's key and value from the raw k and v (rounded as the cache
+// stores them); the position group that meets the new position uses those
+// instead of the cache row, and the workgroup whose split holds it appends
+// them to the cache for the next tokens.  No other workgroup reads that row,
+// so the separate launch before the attention is gone.
+template <int HD, int G, bool F16, bool MERGE, bool PREP>
+__device__ __forceinline__ void attn2_partial(const AttnArgs& a, const PrepArgs& pp) {
+    static_assert(!(PREP && MERGE), "the fused prep runs in the two-launch form");
     using Geo = AttnGeom<HD>;
     constexpr int LP = Geo::LP, NG = Geo::NG;
     __shared__ float sm[NG][G][2];
@@ -375,9 +434,10 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
     // q first: its loads do not wait for the device-side position
     f32x4 qa[G], qb[G], oa[G], ob[G];
     float mx[G], l[G];
+    const float* const qsrc = PREP ? pp.q : a.q;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        const float* qp = a.q + static_cast<int64_t>(m) * n_q * HD + (static_cast<int64_t>(kvh) * G + h) * HD + sub * 8;
+        const float* qp = qsrc + static_cast<int64_t>(m) * n_q * HD + (static_cast<int64_t>(kvh) * G + h) * HD + sub * 8;
         qa[h] = *reinterpret_cast<const f32x4*>(qp);
         qb[h] = *reinterpret_cast<const f32x4*>(qp + 4);
         oa[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -385,24 +445,83 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
         mx[h] = -__builtin_inff();
         l[h] = 0.0f;
     }
+    // PREP: the new token's raw key and value, the norm gammas and, for
+    // thread t < d/2, pair t's rotation-table entry, also before the position
+    // (Unconditional loads: behind a branch each would be waited for on its
+    // own; an absent gamma reads the raw k instead, unused.)
+    f32x4 kna, knb, vna, vnb;
+    float qg[8], kg[8], tv = 1.0f;
+    if constexpr (PREP) {
+        const int64_t o = static_cast<int64_t>(kvh) * HD + sub * 8;
+        kna = *reinterpret_cast<const f32x4*>(pp.k + o);
+        knb = *reinterpret_cast<const f32x4*>(pp.k + o + 4);
+        vna = *reinterpret_cast<const f32x4*>(pp.v + o);
+        vnb = *reinterpret_cast<const f32x4*>(pp.v + o + 4);
+        const float* const qgp = (pp.qg ? pp.qg : pp.k) + sub * 8;
+        const float* const kgp = (pp.kg ? pp.kg : pp.k) + sub * 8;
+        const f32x4 qg0 = *reinterpret_cast<const f32x4*>(qgp), qg1 = *reinterpret_cast<const f32x4*>(qgp + 4);
+        const f32x4 kg0 = *reinterpret_cast<const f32x4*>(kgp), kg1 = *reinterpret_cast<const f32x4*>(kgp + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            qg[e] = qg0[e];
+            qg[e + 4] = qg1[e];
+            kg[e] = kg0[e];
+            kg[e + 4] = kg1[e];
+        }
+        tv = pp.tab[tid < HD / 2 ? tid : 0];
+    }
     int k0, k1;
     attn_range(a, m, k0, k1);
     const int len = k1 - k0;
     const int chunk = attn_chunk<Geo::BATCH>(len, S);
     const int p0 = k0 + sp * chunk, p1 = min(k1, p0 + chunk);
-    for (int pb = p0 + grp; pb < p1; pb += NG * kAU) {
-        f32x4 ka[kAU], kb[kAU], va[kAU], vb[kAU];
+    const int pcur = k1 - 1;  // PREP: the new token's position (row 0)
+
+    // One round: the K and V of positions pb, pb + NG, ... (kAU of them)
+    // issued, then their scores and the running state.  Every load is
+    // issued with no branch around it (a position past the range reads row
+    // k0, which exists, and `land` replaces it with zeros): loads behind
+    // branches leave the compiler unsure how many are in flight, so a later
+    // wait for an older load becomes a wait for all of them.  An f16
+    // cache's bits are loaded into ka / va as they are and widened in
+    // `land`, after the round's loads are all issued.
+    auto issue = [&](int pb, f32x4 (&ka)[kAU], f32x4 (&kb)[kAU], f32x4 (&va)[kAU], f32x4 (&vb)[kAU]) {
 #pragma unroll
         for (int u = 0; u < kAU; ++u) {
             const int p = pb + u * NG;
-            const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-            ka[u] = kb[u] = va[u] = vb[u] = z;
-            if (p < p1) {
-                const int64_t off = static_cast<int64_t>(p) * a.row + static_cast<int64_t>(kvh) * HD + sub * 8;
-                load8<F16>(a.kc, off, ka[u], kb[u]);
-                load8<F16>(a.vc, off, va[u], vb[u]);
+            const int64_t off =
+                static_cast<int64_t>(p < p1 ? p : k0) * a.row + static_cast<int64_t>(kvh) * HD + sub * 8;
+            if constexpr (F16) {
+                ka[u] = __builtin_bit_cast(f32x4,
+                                           *reinterpret_cast<const u32x4*>(static_cast<const _Float16*>(a.kc) + off));
+                va[u] = __builtin_bit_cast(f32x4,
+                                           *reinterpret_cast<const u32x4*>(static_cast<const _Float16*>(a.vc) + off));
+            } else {
+                load8<false>(a.kc, off, ka[u], kb[u]);
+                load8<false>(a.vc, off, va[u], vb[u]);
             }
         }
+        // every load of the round before any use (else the compiler
+        // interleaves the first products and waits between the loads)
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto land = [&](int pb, f32x4 (&ka)[kAU], f32x4 (&kb)[kAU], f32x4 (&va)[kAU], f32x4 (&vb)[kAU]) {
+        const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int u = 0; u < kAU; ++u) {
+            if constexpr (F16) {
+                widen8(__builtin_bit_cast(u32x4, ka[u]), ka[u], kb[u]);
+                widen8(__builtin_bit_cast(u32x4, va[u]), va[u], vb[u]);
+            }
+            const bool in = pb + u * NG < p1;  // uniform per position group
+            ka[u] = in ? ka[u] : z;
+            kb[u] = in ? kb[u] : z;
+            va[u] = in ? va[u] : z;
+            vb[u] = in ? vb[u] : z;
+        }
+    };
+    auto consume = [&](int pb, const f32x4 (&ka)[kAU], const f32x4 (&kb)[kAU], const f32x4 (&va)[kAU],
+                       const f32x4 (&vb)[kAU]) {
         // The round's kAU scores do not depend on each other: all of them
         // first (their cross-lane sums overlap), then one running-maximum
         // update and one rescale per round instead of one per position.
@@ -432,6 +551,97 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
             }
             mx[h] = mn;
         }
+    };
+
+    // PREP: the new position's key and value are this launch's own, not the
+    // cache row (in whichever round of its split the position falls)
+    auto own_row = [&](int pb, f32x4 (&ka)[kAU], f32x4 (&kb)[kAU], f32x4 (&va)[kAU], f32x4 (&vb)[kAU]) {
+#pragma unroll
+        for (int u = 0; u < kAU; ++u) {
+            if (pb + u * NG == pcur) {  // uniform per position group
+                ka[u] = kna;
+                kb[u] = knb;
+                va[u] = vna;
+                vb[u] = vnb;
+            }
+        }
+    };
+
+    int pb = p0 + grp;
+    if constexpr (PREP) {
+        // The first round by every group (one past the range loads nothing
+        // and scores -inf), its loads in flight while the new token is
+        // prepared: the workgroup's threads share the d/2 rotation angles
+        // of k_qk_prep (pos * tab[i], or (pos * freq_scale) / tab[i])
+        // through LDS, one cosine and sine each.
+        f32x4 ka[kAU], kb[kAU], va[kAU], vb[kAU];
+        issue(pb, ka, kb, va, vb);
+        __shared__ float tcs[HD / 2], tsn[HD / 2];
+        if (tid < HD / 2) {
+            const float ang = pp.mode == 0 ? static_cast<float>(pcur) * tv
+                                           : (static_cast<float>(pcur) * pp.freq_scale) / tv;
+            tcs[tid] = cosf(ang);
+            tsn[tid] = sinf(ang);
+        }
+        __syncthreads();
+        float cs[8], sn[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            // the pair of dim j: j mod d/2 (half-split) or j / 2
+            const int i = pp.half ? (sub * 8 + e) % (HD / 2) : (sub * 8 + e) >> 1;
+            cs[e] = tcs[i];
+            sn[e] = tsn[i];
+        }
+#pragma unroll
+        for (int h = 0; h < G; ++h) prep_head<HD>(qa[h], qb[h], pp.qg != nullptr, qg, cs, sn, pp.half, pp.eps, sub);
+        prep_head<HD>(kna, knb, pp.kg != nullptr, kg, cs, sn, pp.half, pp.eps, sub);
+        const int64_t o = static_cast<int64_t>(pcur) * pp.cache_row + static_cast<int64_t>(kvh) * HD + sub * 8;
+        const bool store = grp == 0 && pcur >= p0 && pcur < p1;  // one group of one workgroup per kv head
+        if constexpr (F16) {
+            // the cache's rounding (RNE), kept for this launch's own use
+            _Float16 hk[8], hv[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                hk[e] = static_cast<_Float16>(kna[e]);
+                hk[e + 4] = static_cast<_Float16>(knb[e]);
+                hv[e] = static_cast<_Float16>(vna[e]);
+                hv[e + 4] = static_cast<_Float16>(vnb[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                kna[e] = static_cast<float>(hk[e]);
+                knb[e] = static_cast<float>(hk[e + 4]);
+                vna[e] = static_cast<float>(hv[e]);
+                vnb[e] = static_cast<float>(hv[e + 4]);
+            }
+            if (store) {
+                _Float16* kc = static_cast<_Float16*>(pp.kc) + o;
+                _Float16* vc = static_cast<_Float16*>(pp.vc) + o;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    kc[e] = hk[e];
+                    vc[e] = hv[e];
+                }
+            }
+        } else if (store) {
+            float* kc = static_cast<float*>(pp.kc) + o;
+            float* vc = static_cast<float*>(pp.vc) + o;
+            *reinterpret_cast<f32x4*>(kc) = kna;
+            *reinterpret_cast<f32x4*>(kc + 4) = knb;
+            *reinterpret_cast<f32x4*>(vc) = vna;
+            *reinterpret_cast<f32x4*>(vc + 4) = vnb;
+        }
+        land(pb, ka, kb, va, vb);
+        own_row(pb, ka, kb, va, vb);
+        consume(pb, ka, kb, va, vb);
+        pb += NG * kAU;
+    }
+    for (; pb < p1; pb += NG * kAU) {
+        f32x4 ka[kAU], kb[kAU], va[kAU], vb[kAU];
+        issue(pb, ka, kb, va, vb);
+        land(pb, ka, kb, va, vb);
+        if constexpr (PREP) own_row(pb, ka, kb, va, vb);
+        consume(pb, ka, kb, va, vb);
     }
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -510,6 +720,16 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
     if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+template <int HD, int G, bool F16, bool MERGE>
+__global__ __launch_bounds__(kAT) void k_attn2_partial(const AttnArgs a) {
+    attn2_partial<HD, G, F16, MERGE, false>(a, PrepArgs{});
+}
+
+template <int HD, int G, bool F16>
+__global__ __launch_bounds__(kAT) void k_attn2_partial_prep(const AttnArgs a, const PrepArgs p) {
+    attn2_partial<HD, G, F16, false, true>(a, p);
+}
+
 // Second launch of the two-launch form: workgroup (query head, row), one
 // thread per dimension, folds the plain-stored partials of all S splits in
 // split order, with no read of the position, so its loads issue at once (a
@@ -528,8 +748,14 @@ __global__ __launch_bounds__(HD) void k_attn2_combine(const AttnArgs a, int S) {
 }
 
 template <int HD, int G, bool F16>
-hipError_t run_attn(const AttnArgs& a, int S, int M, hipStream_t s) {
+hipError_t run_attn(const AttnArgs& a, int S, int M, hipStream_t s, const PrepArgs* prep) {
     const dim3 grid(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(S), static_cast<unsigned>(M));
+    if (prep) {
+        hipLaunchKernelGGL((k_attn2_partial_prep<HD, G, F16>), grid, dim3(kAT), 0, s, a, *prep);
+        hipLaunchKernelGGL(k_attn2_combine<HD>, dim3(static_cast<unsigned>(a.n_kv * G), static_cast<unsigned>(M)),
+                           dim3(HD), 0, s, a, S);
+        return hipGetLastError();
+    }
     // Two launches by default.  Measured at 1024 cached positions: the
     // Llama-3.2-3B engine token 1162 us against 1201 us with the merge in
     // the last-arriving workgroup (Gemma-3-4B shapes 1989 against 1982 us);
@@ -552,12 +778,12 @@ hipError_t run_attn(const AttnArgs& a, int S, int M, hipStream_t s) {
 }
 
 template <int HD, bool F16>
-hipError_t attn_g(const AttnArgs& a, int G, int S, int M, hipStream_t s) {
+hipError_t attn_g(const AttnArgs& a, int G, int S, int M, hipStream_t s, const PrepArgs* prep) {
     switch (G) {
-        case 1: return run_attn<HD, 1, F16>(a, S, M, s);
-        case 2: return run_attn<HD, 2, F16>(a, S, M, s);
-        case 3: return run_attn<HD, 3, F16>(a, S, M, s);
-        case 4: return run_attn<HD, 4, F16>(a, S, M, s);
+        case 1: return run_attn<HD, 1, F16>(a, S, M, s, prep);
+        case 2: return run_attn<HD, 2, F16>(a, S, M, s, prep);
+        case 3: return run_attn<HD, 3, F16>(a, S, M, s, prep);
+        case 4: return run_attn<HD, 4, F16>(a, S, M, s, prep);
         default: return hipErrorInvalidValue;
     }
 }
@@ -608,8 +834,7 @@ hipError_t launch_rmsnorm_rows(const float* x, const float* gamma, const float* 
     return rmsnorm_v<16>(x, gamma, resid, out, d, rows, eps, gemma, s);
 }
 
-hipError_t launch_qk_prep(const QkPrep& p, hipStream_t s) {
-    if (p.head_dim < 2 || p.head_dim > 256 || p.head_dim % 2) return hipErrorInvalidValue;
+static PrepArgs prep_args(const QkPrep& p) {
     PrepArgs a;
     a.q = p.q;
     a.k = p.k;
@@ -632,6 +857,12 @@ hipError_t launch_qk_prep(const QkPrep& p, hipStream_t s) {
     a.q_stride = static_cast<int64_t>(p.n_q) * p.head_dim;
     a.kv_stride = static_cast<int64_t>(p.n_kv) * p.head_dim;
     a.cache_row = static_cast<int64_t>(p.n_kv) * p.head_dim;
+    return a;
+}
+
+hipError_t launch_qk_prep(const QkPrep& p, hipStream_t s) {
+    if (p.head_dim < 2 || p.head_dim > 256 || p.head_dim % 2) return hipErrorInvalidValue;
+    const PrepArgs a = prep_args(p);
     hipLaunchKernelGGL(k_qk_prep, dim3(static_cast<unsigned>(p.n_q + 2 * p.n_kv), static_cast<unsigned>(p.m)),
                        dim3(128), 0, s, a);
     return hipGetLastError();
@@ -673,13 +904,24 @@ hipError_t launch_attention2(const Attn2& p, float* part, uint32_t* counters, hi
     a.out = p.out;
     a.cnt = counters;
     const int G = p.n_q / p.n_kv;
+    PrepArgs pa{};
+    if (p.prep) {
+        // the fused form: one row at a device position, the same geometry
+        const QkPrep& q = *p.prep;
+        if (p.m != 1 || q.m != 1 || !p.pos || q.pos != p.pos || q.n_q != p.n_q || q.n_kv != p.n_kv ||
+            q.head_dim != p.head_dim || q.f16 != p.f16 || !q.rope_tab || q.k_cache != p.k_cache ||
+            q.v_cache != p.v_cache)
+            return hipErrorInvalidValue;
+        pa = prep_args(q);
+    }
+    const PrepArgs* pp = p.prep ? &pa : nullptr;
     switch (p.head_dim) {
-        case 64: return p.f16 ? attn_g<64, true>(a, G, p.splits, p.m, s)
-                              : attn_g<64, false>(a, G, p.splits, p.m, s);
-        case 128: return p.f16 ? attn_g<128, true>(a, G, p.splits, p.m, s)
-                               : attn_g<128, false>(a, G, p.splits, p.m, s);
-        case 256: return p.f16 ? attn_g<256, true>(a, G, p.splits, p.m, s)
-                               : attn_g<256, false>(a, G, p.splits, p.m, s);
+        case 64: return p.f16 ? attn_g<64, true>(a, G, p.splits, p.m, s, pp)
+                              : attn_g<64, false>(a, G, p.splits, p.m, s, pp);
+        case 128: return p.f16 ? attn_g<128, true>(a, G, p.splits, p.m, s, pp)
+                               : attn_g<128, false>(a, G, p.splits, p.m, s, pp);
+        case 256: return p.f16 ? attn_g<256, true>(a, G, p.splits, p.m, s, pp)
+                               : attn_g<256, false>(a, G, p.splits, p.m, s, pp);
         default: return hipErrorInvalidValue;
     }
 }

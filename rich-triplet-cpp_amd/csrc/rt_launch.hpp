@@ -237,6 +237,10 @@ struct Attn2 {
     int n_q = 0, n_kv = 0, head_dim = 0, m = 1, splits = 1;
     float scale = 1.0f;
     bool f16 = false;
+    // m = 1 with pos: the q/k preparation of launch_qk_prep (same operands,
+    // same caches) runs inside the attention launch; q is then its raw q,
+    // and q_out is not written.
+    const QkPrep* prep = nullptr;
 };
 int attention2_splits(int n_kv, int m, int64_t max_len, int head_dim);
 size_t attention2_workspace(int n_q, int head_dim, int splits, int m);

@@ -326,6 +326,12 @@ GEMMA_4B_ATTN = dict(GEMMA, n_heads=8, n_kv_heads=4, head_dim=256, ffn=512, max_
     ("gemma3_4b", GEMMA_4B_ATTN, 150),
     # local: the window slides past position 0 (all 7 busy); global 13 of 16
     ("gemma3_4b", GEMMA_4B_ATTN, 400),
+    # splits of two rounds (S capped by the CUs), the new position in the
+    # second round of the last busy split: global layer S = 64, 48 busy;
+    # the half-split Llama form (q/k prepared inside the attention launch):
+    # S = 32, 24 busy
+    ("gemma3_4b", dict(GEMMA_4B_ATTN, max_seq=4096), 3050),
+    ("llama3b_half", dict(LLAMA_3B_ATTN, max_seq=4096, rope_half=1), 3050),
 ])
 def test_decoder_long_cache_matches_oracle(rt, orc, arch, cfg, rows):
     gemma = arch.startswith("gemma")
