@@ -261,18 +261,21 @@ __device__ __forceinline__ float ld_dev(const float* p) {
 // all P pairs, are issued before any is used (indices past S repeat split
 // S - 1, in bounds, with weight 0): one memory latency per batch instead of
 // one per split and pair.
+constexpr int kCB = 16;  // splits per batch of loads
+
+// The running (M, L, O) of splits [s_begin, s_end) (none: -inf, 0, 0).
 template <int PART, int P, bool COH>
-__device__ __forceinline__ void fold_splits(const float* const (&ph)[P], const int (&d)[P], int S, float (&res)[P]) {
+__device__ __forceinline__ void fold_state(const float* const (&ph)[P], const int (&d)[P], int s_begin, int s_end,
+                                           float (&M)[P], float (&L)[P], float (&O)[P]) {
     auto ld = [](const float* p) { return COH ? ld_dev(p) : *p; };
-    float M[P], L[P], O[P];
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         M[p] = -__builtin_inff();
         L[p] = 0.0f;
         O[p] = 0.0f;
     }
-    constexpr int kCB = 16;
-    for (int s0 = 0; s0 < S; s0 += kCB) {
+    const int S = s_end;
+    for (int s0 = s_begin; s0 < S; s0 += kCB) {
         // every load of the batch, for all of this thread's P pairs, first
         float ms[P][kCB], ls[P][kCB], os[P][kCB];
 #pragma unroll
@@ -307,6 +310,12 @@ __device__ __forceinline__ void fold_splits(const float* const (&ph)[P], const i
             M[p] = Mb;
         }
     }
+}
+
+template <int PART, int P, bool COH>
+__device__ __forceinline__ void fold_splits(const float* const (&ph)[P], const int (&d)[P], int S, float (&res)[P]) {
+    float M[P], L[P], O[P];
+    fold_state<PART, P, COH>(ph, d, 0, S, M, L, O);
 #pragma unroll
     for (int p = 0; p < P; ++p) res[p] = L[p] > 0.0f ? O[p] / L[p] : 0.0f;
 }
@@ -731,20 +740,64 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial_prep(const AttnArgs a, co
 }
 
 // Second launch of the two-launch form: workgroup (query head, row), one
-// thread per dimension, folds the plain-stored partials of all S splits in
-// split order, with no read of the position, so its loads issue at once (a
-// split past the cached range holds M = -inf, L = O = 0 and changes
-// nothing).
-template <int HD>
-__global__ __launch_bounds__(HD) void k_attn2_combine(const AttnArgs a, int S) {
+// thread per dimension and part.  Part r folds the plain-stored partials of
+// its contiguous share of the S splits in split order, with no read of the
+// position, so its loads issue at once (a split past the cached range holds
+// M = -inf, L = O = 0 and changes nothing); with R parts of at most kCB
+// splits that is one memory latency.  Part 0 then folds the R states in
+// order: the result is the same for every run.
+template <int HD, int R>
+__global__ __launch_bounds__(HD * R) void k_attn2_combine(const AttnArgs a, int S) {
     using Geo = AttnGeom<HD>;
-    const int h = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
+    const int h = blockIdx.x, m = blockIdx.y, d = static_cast<int>(threadIdx.x) % HD;
+    const int r = static_cast<int>(threadIdx.x) / HD;
     const int n_q = gridDim.x;
     const float* ph[1] = {a.part + (static_cast<int64_t>(m) * n_q + h) * S * Geo::PART};
     const int dd[1] = {d};
-    float res[1];
-    fold_splits<Geo::PART, 1, false>(ph, dd, S, res);
-    a.out[(static_cast<int64_t>(m) * n_q + h) * HD + d] = res[0];
+    float* const out = a.out + (static_cast<int64_t>(m) * n_q + h) * HD + d;
+    if constexpr (R == 1) {
+        float res[1];
+        fold_splits<Geo::PART, 1, false>(ph, dd, S, res);
+        *out = res[0];
+    } else {
+        float M[1], L[1], O[1];
+        fold_state<Geo::PART, 1, false>(ph, dd, (S * r) / R, (S * (r + 1)) / R, M, L, O);
+        __shared__ float sm[R], sl[R], so[R][HD];
+        if (d == 0) {
+            sm[r] = M[0];
+            sl[r] = L[0];
+        }
+        so[r][d] = O[0];
+        __syncthreads();
+        if (r != 0) return;
+        float mx = sm[0];
+#pragma unroll
+        for (int q = 1; q < R; ++q) mx = fmaxf(mx, sm[q]);
+        float lt = 0.0f, ot = 0.0f;
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+            const float w = sm[q] == -__builtin_inff() ? 0.0f : exp_fast(sm[q] - mx);
+            lt += sl[q] * w;
+            ot += so[q][d] * w;
+        }
+        *out = lt > 0.0f ? ot / lt : 0.0f;
+    }
+}
+
+// The combine launch: two parts when that makes one batch of loads each.
+// Measured (engine tokens at 1024 positions): Llama-3.2-3B, 17 splits,
+// 1120-1123 us with two parts against 1129-1136 with one and 1136-1142 with
+// four; Gemma-3-4B, 33 splits, 1649-1659 with one part against 1663-1669
+// with two and 1687-1689 with four (the wider workgroup and its LDS fold
+// cost more than the third batch's latency there).
+template <int HD>
+void launch_combine(const AttnArgs& a, int n_q, int S, int M, hipStream_t s) {
+    const int parts = tune_param("ATTN_COMBINE_PARTS", S > kCB && S <= 2 * kCB ? 2 : 1);
+    const dim3 g(static_cast<unsigned>(n_q), static_cast<unsigned>(M));
+    if (parts >= 2)
+        hipLaunchKernelGGL((k_attn2_combine<HD, 2>), g, dim3(HD * 2), 0, s, a, S);
+    else
+        hipLaunchKernelGGL((k_attn2_combine<HD, 1>), g, dim3(HD), 0, s, a, S);
 }
 
 template <int HD, int G, bool F16>
@@ -752,8 +805,7 @@ hipError_t run_attn(const AttnArgs& a, int S, int M, hipStream_t s, const PrepAr
     const dim3 grid(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(S), static_cast<unsigned>(M));
     if (prep) {
         hipLaunchKernelGGL((k_attn2_partial_prep<HD, G, F16>), grid, dim3(kAT), 0, s, a, *prep);
-        hipLaunchKernelGGL(k_attn2_combine<HD>, dim3(static_cast<unsigned>(a.n_kv * G), static_cast<unsigned>(M)),
-                           dim3(HD), 0, s, a, S);
+        launch_combine<HD>(a, a.n_kv * G, S, M, s);
         return hipGetLastError();
     }
     // Two launches by default.  Measured at 1024 cached positions: the
@@ -771,8 +823,7 @@ hipError_t run_attn(const AttnArgs& a, int S, int M, hipStream_t s, const PrepAr
         // positions, 17 splits): 1120 / 1951 us against 1125-1130 / 1949-1963
         // folding only the busy splits after reading the position; batches
         // of 32 splits (one latency for all 17) 1137-1150 / 2002-2044.
-        hipLaunchKernelGGL(k_attn2_combine<HD>, dim3(static_cast<unsigned>(a.n_kv * G), static_cast<unsigned>(M)),
-                           dim3(HD), 0, s, a, S);
+        launch_combine<HD>(a, a.n_kv * G, S, M, s);
     }
     return hipGetLastError();
 }
