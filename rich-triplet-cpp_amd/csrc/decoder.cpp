@@ -26,6 +26,7 @@
 // row-major weights.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -90,8 +91,7 @@ struct rt_hip_decoder {
     int32_t* dstate = nullptr;  // [0] position of row 0, [1..8] tokens
     int32_t* hstate = nullptr;  // pinned host mirror
     float* logits_stage = nullptr;  // pinned host staging for the logits readback, [max rows][vocab]
-    uint64_t* argmax_keys = nullptr;
-    uint64_t* argmax_part = nullptr;  // per-workgroup keys of the Q4_K lm_head (zeroed at create)
+    uint64_t* argmax_part = nullptr;  // per-workgroup keys of the lm_head (zeroed at create)
     int64_t* argmax_idx = nullptr;
     hipStream_t stream = nullptr;  // used when the caller passes the legacy stream (not capturable)
     rt_hip_graph* graphs[RT_HIP_GEMV_MAX_M + 1] = {};
@@ -464,17 +464,14 @@ int record_step(rt_hip_decoder* d, int m, hipStream_t s) {
                 rc = chk(launch_argmax_reduce(d->argmax_part, q4k_argmax_partials(V), d->argmax_idx, nullptr, s),
                          "decoder: argmax");
             return rc;
-        } else {
-            rc = chk(launch_gemv_bf16_xop(d->gemma ? 2 : 1, static_cast<const uint16_t*>(d->lm_head.data), d->hidden,
-                                          d->out_norm, c.norm_eps, d->logits, V, H, s),
-                     "decoder: lm_head");
         }
-        // The argmax of the BF16 logits (transformer5.cpp:382-391) rides in
-        // the same graph: three small launches on the GPU instead of a
-        // separate host call per token.
-        if (!rc) rc = chk(launch_argmax_init(d->argmax_keys, 1, s), "decoder: argmax");
-        if (!rc) rc = chk(launch_argmax_scan(d->logits, 1, V, d->argmax_keys, s), "decoder: argmax");
-        if (!rc) rc = chk(launch_argmax_finalize(d->argmax_keys, 1, d->argmax_idx, nullptr, s), "decoder: argmax");
+        // BF16 (the tied embedding): the same, one key per workgroup
+        rc = chk(launch_gemv_bf16_xop_argmax(d->gemma ? 2 : 1, static_cast<const uint16_t*>(d->lm_head.data),
+                                             d->hidden, d->out_norm, c.norm_eps, d->logits, V, H, d->argmax_part, s),
+                 "decoder: lm_head + argmax");
+        if (!rc)
+            rc = chk(launch_argmax_reduce(d->argmax_part, bf16_xop_argmax_partials(V, H), d->argmax_idx, nullptr, s),
+                     "decoder: argmax");
         return rc;
     }
     rc = chk(launch_rmsnorm_rows(d->hidden, d->out_norm, nullptr, d->normed, H, m, c.norm_eps, d->gemma, s),
@@ -598,6 +595,9 @@ int rt_hip_decoder_create(const rt_hip_decoder_config* cfg, rt_hip_decoder** out
     d->rows = c.max_batch > 1 ? c.max_batch : 1;
     d->layers.resize(c.n_layers);
     const int R = d->rows, H = c.hidden, F = c.ffn, hd = c.head_dim;
+    // per-workgroup argmax keys of the lm_head, Q4_K or BF16
+    const size_t argmax_slots = static_cast<size_t>(
+        std::max(q4k_argmax_partials(c.vocab), bf16_xop_argmax_partials(c.vocab, c.hidden)));
     const int64_t qd = static_cast<int64_t>(c.n_heads) * hd, kvd = static_cast<int64_t>(c.n_kv_heads) * hd;
     const size_t kv_elem = c.kv_f16 ? 2 : 4;
     auto cleanup = [&](hipError_t err) {
@@ -616,9 +616,8 @@ int rt_hip_decoder_create(const rt_hip_decoder_config* cfg, rt_hip_decoder** out
         (e = dev_alloc_t(d, &d->act, static_cast<size_t>(R) * F)) != hipSuccess ||
         (e = dev_alloc_t(d, &d->logits, static_cast<size_t>(R) * c.vocab)) != hipSuccess ||
         (e = dev_alloc_t(d, &d->dstate, 16)) != hipSuccess ||
-        (e = dev_alloc_t(d, &d->argmax_keys, 64)) != hipSuccess ||
-        (e = dev_alloc_t(d, &d->argmax_part, static_cast<size_t>(q4k_argmax_partials(c.vocab)))) != hipSuccess ||
-        (e = hipMemset(d->argmax_part, 0, static_cast<size_t>(q4k_argmax_partials(c.vocab)) * 8)) != hipSuccess ||
+        (e = dev_alloc_t(d, &d->argmax_part, argmax_slots)) != hipSuccess ||
+        (e = hipMemset(d->argmax_part, 0, argmax_slots * 8)) != hipSuccess ||
         (e = dev_alloc_t(d, &d->argmax_idx, 16)) != hipSuccess)
         return cleanup(e);
     if ((e = hipHostMalloc(reinterpret_cast<void**>(&d->hstate), 16 * sizeof(int32_t))) != hipSuccess)

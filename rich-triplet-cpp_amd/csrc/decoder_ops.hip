@@ -784,15 +784,16 @@ __global__ __launch_bounds__(HD * R) void k_attn2_combine(const AttnArgs a, int 
     }
 }
 
-// The combine launch: two parts when that makes one batch of loads each.
-// Measured (engine tokens at 1024 positions): Llama-3.2-3B, 17 splits,
-// 1120-1123 us with two parts against 1129-1136 with one and 1136-1142 with
-// four; Gemma-3-4B, 33 splits, 1649-1659 with one part against 1663-1669
-// with two and 1687-1689 with four (the wider workgroup and its LDS fold
-// cost more than the third batch's latency there).
+// The combine launch: two parts when that makes one batch of loads each and
+// the workgroup stays at 256 threads (head_dim <= 128).  Measured (engine
+// tokens at 1024 positions): Llama-3.2-3B, 17 splits, 1120-1123 us with two
+// parts against 1129-1136 with one and 1136-1142 with four; Gemma-3-4B
+// (head_dim 256), 32 and 33 splits, 1649-1659 with one part against
+// 1663-1669 with two and 1687-1689 with four (the wider workgroup and its
+// LDS fold cost more than the last batch's latency there).
 template <int HD>
 void launch_combine(const AttnArgs& a, int n_q, int S, int M, hipStream_t s) {
-    const int parts = tune_param("ATTN_COMBINE_PARTS", S > kCB && S <= 2 * kCB ? 2 : 1);
+    const int parts = tune_param("ATTN_COMBINE_PARTS", S > kCB && S <= 2 * kCB && HD <= 128 ? 2 : 1);
     const dim3 g(static_cast<unsigned>(n_q), static_cast<unsigned>(M));
     if (parts >= 2)
         hipLaunchKernelGGL((k_attn2_combine<HD, 2>), g, dim3(HD * 2), 0, s, a, S);

@@ -33,14 +33,27 @@ __global__ __launch_bounds__(T) void k_gemv_bf16(const uint16_t* __restrict__ W,
     }
 }
 
-// The same with a layer operation applied to x while it is staged (XOp).
-template <int D, int XP, int T, int XOP, bool ADD>
+// The same with a layer operation applied to x while it is staged (XOp);
+// ARGMAX as above (the key of each row as stored, after the norm's scale).
+template <int D, int XP, int T, int XOP, bool ADD, bool ARGMAX = false>
 __global__ __launch_bounds__(T) void k_gemv_bf16_xop(const uint16_t* __restrict__ W, const float* __restrict__ X,
                                                     const float* __restrict__ aux, float* __restrict__ Y, int N,
-                                                    int K, float eps) {
+                                                    int K, float eps, uint64_t* __restrict__ key = nullptr) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    rows<D, XP, false, T, XOP, ADD>(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), W, X, Y, N, K,
-                                    nullptr, lds, aux, eps);
+    if constexpr (ARGMAX) {
+        __shared__ uint64_t wbest[T / kWave];
+        rows<D, XP, true, T, XOP, ADD>(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), W, X, Y, N, K,
+                                       wbest, lds, aux, eps);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint64_t b = wbest[0];
+            for (int w = 1; w < T / kWave; ++w) b = wbest[w] > b ? wbest[w] : b;
+            key[blockIdx.x] = b;
+        }
+    } else {
+        rows<D, XP, false, T, XOP, ADD>(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), W, X, Y, N, K,
+                                        nullptr, lds, aux, eps);
+    }
 }
 
 // T threads per workgroup, each wave looping over its rows; x is prefetched into registers before the
@@ -110,26 +123,43 @@ hipError_t launch_gemv_bf16_m1(const uint16_t* w, const float* x, float* y, int6
 
 namespace {
 // The default launch shape of run() (8 waves), with an x operation.
-template <int XOP, bool ADD>
-hipError_t run_xop(const uint16_t* w, const float* x, const float* aux, float eps, float* y, int64_t n, int64_t k,
-                   hipStream_t s) {
-    constexpr int T = 512;
-    const int64_t waves = T / kWave, pieces = (k + kPiece - 1) / kPiece;
+constexpr int kXopThreads = 512;
+int64_t xop_workgroups(int64_t n, int64_t k) {
+    const int64_t waves = kXopThreads / kWave, pieces = (k + kPiece - 1) / kPiece;
     const int64_t rpw = pieces <= 3 ? 4 : (pieces >= 12 ? 2 : 1);
-    const int64_t wgs = (n + waves * rpw - 1) / (waves * rpw);
+    return (n + waves * rpw - 1) / (waves * rpw);
+}
+
+template <int XOP, bool ADD, bool ARGMAX = false>
+hipError_t run_xop(const uint16_t* w, const float* x, const float* aux, float eps, float* y, int64_t n, int64_t k,
+                   hipStream_t s, uint64_t* key = nullptr) {
+    constexpr int T = kXopThreads;
+    const int64_t wgs = xop_workgroups(n, k);
     const int64_t per = (k / 4 + T - 1) / T;
     const dim3 g(static_cast<unsigned>(wgs)), b(T);
     const size_t lds = bf16_m1_lds_bytes(k);
     const int ik = static_cast<int>(k), in = static_cast<int>(n);
     if (per <= 2)
-        hipLaunchKernelGGL((k_gemv_bf16_xop<8, 2, T, XOP, ADD>), g, b, lds, s, w, x, aux, y, in, ik, eps);
+        hipLaunchKernelGGL((k_gemv_bf16_xop<8, 2, T, XOP, ADD, ARGMAX>), g, b, lds, s, w, x, aux, y, in, ik, eps, key);
     else if (per <= 4)
-        hipLaunchKernelGGL((k_gemv_bf16_xop<8, 4, T, XOP, ADD>), g, b, lds, s, w, x, aux, y, in, ik, eps);
+        hipLaunchKernelGGL((k_gemv_bf16_xop<8, 4, T, XOP, ADD, ARGMAX>), g, b, lds, s, w, x, aux, y, in, ik, eps, key);
     else
-        hipLaunchKernelGGL((k_gemv_bf16_xop<8, 8, T, XOP, ADD>), g, b, lds, s, w, x, aux, y, in, ik, eps);
+        hipLaunchKernelGGL((k_gemv_bf16_xop<8, 8, T, XOP, ADD, ARGMAX>), g, b, lds, s, w, x, aux, y, in, ik, eps, key);
     return hipGetLastError();
 }
 }  // namespace
+
+int64_t bf16_xop_argmax_partials(int64_t n, int64_t k) { return xop_workgroups(n, k); }
+
+hipError_t launch_gemv_bf16_xop_argmax(int xop, const uint16_t* w, const float* x, const float* gamma, float eps,
+                                       float* y, int64_t n, int64_t k, uint64_t* keys, hipStream_t s) {
+    if (!keys) return hipErrorInvalidValue;
+    switch (xop) {
+        case kXRmsNorm: return run_xop<kXRmsNorm, false, true>(w, x, gamma, eps, y, n, k, s, keys);
+        case kXRmsNorm1: return run_xop<kXRmsNorm1, false, true>(w, x, gamma, eps, y, n, k, s, keys);
+        default: return hipErrorInvalidValue;
+    }
+}
 
 hipError_t launch_gemv_bf16_xop(int xop, const uint16_t* w, const float* x, const float* aux, float eps, float* y,
                                 int64_t n, int64_t k, hipStream_t s, bool add) {

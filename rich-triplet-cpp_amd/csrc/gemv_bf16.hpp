@@ -119,7 +119,7 @@ __device__ __forceinline__ void rows(int blk, int nblk, const uint16_t* __restri
                                      const float* __restrict__ X, float* __restrict__ Y, int N, int K,
                                      uint64_t* __restrict__ key, uint8_t* lds,
                                      const float* __restrict__ aux = nullptr, float eps = 0.0f) {
-    static_assert(XOP == kXNone || !ARGMAX, "x operations run without the argmax epilogue");
+    static_assert(!(ADD && ARGMAX), "the argmax epilogue keys stored rows, not added ones");
     constexpr bool kNorm = XOP == kXRmsNorm || XOP == kXRmsNorm1;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -238,8 +238,10 @@ __device__ __forceinline__ void rows(int blk, int nblk, const uint16_t* __restri
             const float v = wave_sum(acc, lane);                                                            \
             res = lane == cr ? v : res;                                                                     \
             if constexpr (ARGMAX) {                                                                         \
-                if (v == v) {                                                                               \
-                    const uint64_t kk = argmax_key(v, static_cast<uint32_t>(gw + cr * NW));                 \
+                /* the key of the value stored (scaled by the norm's rms_inv, the same product) */          \
+                const float fv = kNorm ? v * out_scale : v;                                                 \
+                if (fv == fv) {                                                                             \
+                    const uint64_t kk = argmax_key(fv, static_cast<uint32_t>(gw + cr * NW));                \
                     best = kk > best ? kk : best;                                                           \
                 }                                                                                           \
             }                                                                                               \

@@ -166,6 +166,12 @@ hipError_t launch_gemv_q6k(const void* tiled, const float* x, float* y, int64_t 
 // The fused BF16 GEMV + argmax writes one partial key per workgroup
 // (bf16_argmax_partials(n, k) of them); launch_argmax_reduce folds them.
 int64_t bf16_argmax_partials(int64_t n, int64_t k);
+// The BF16 GEMV with an RMSNorm xop (1 or 2, gamma) and the argmax epilogue:
+// each workgroup's best key (of the rows as stored) into keys
+// (bf16_xop_argmax_partials(n, k) of them); launch_argmax_reduce folds them.
+int64_t bf16_xop_argmax_partials(int64_t n, int64_t k);
+hipError_t launch_gemv_bf16_xop_argmax(int xop, const uint16_t* w, const float* x, const float* gamma, float eps,
+                                       float* y, int64_t n, int64_t k, uint64_t* keys, hipStream_t s);
 hipError_t launch_argmax_reduce(const uint64_t* part, int64_t count, int64_t* idx, float* val, hipStream_t s);
 hipError_t launch_argmax_init(uint64_t* keys, int64_t rows, hipStream_t s);
 hipError_t launch_argmax_scan(const float* v, int64_t rows, int64_t cols, uint64_t* keys,
