@@ -71,21 +71,26 @@ __global__ void k_argmax_finalize(const uint64_t* keys, int64_t rows, int64_t* i
 }
 
 // Largest of `count` partial keys (0 = empty) -> idx[0], val[0]; one
-// workgroup, order-independent.
+// workgroup, order-independent.  U loads in flight per thread before any is
+// compared (the launcher picks U so that one round covers the keys: 8016
+// for the Q4_K lm_head of 128256 rows, 32768 for a BF16 one of 262144).
+// Indices past the end repeat the thread's first key, which changes no
+// maximum: loads behind a branch would each be waited for on their own.
+template <int U>
 __global__ __launch_bounds__(1024) void k_argmax_reduce(const uint64_t* __restrict__ part, int64_t count,
                                                         int64_t* idx, float* val) {
     __shared__ uint64_t wbest[1024 / kWave];
     uint64_t best = kInitKey;
-    // eight loads in flight per thread before any is compared
-    for (int64_t i0 = threadIdx.x; i0 < count; i0 += 8 * 1024) {
-        uint64_t v[8];
+    const int64_t first = threadIdx.x < count ? threadIdx.x : 0;
+    for (int64_t i0 = threadIdx.x; i0 < count; i0 += U * 1024) {
+        uint64_t v[U];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < U; ++u) {
             const int64_t i = i0 + u * 1024;
-            v[u] = i < count ? part[i] : 0;
+            v[u] = part[i < count ? i : first];
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) best = v[u] > best ? v[u] : best;
+        for (int u = 0; u < U; ++u) best = v[u] > best ? v[u] : best;
     }
 #pragma unroll
     for (int off = kWave / 2; off >= 1; off >>= 1) {
@@ -107,7 +112,12 @@ __global__ __launch_bounds__(1024) void k_argmax_reduce(const uint64_t* __restri
 }  // namespace
 
 hipError_t launch_argmax_reduce(const uint64_t* part, int64_t count, int64_t* idx, float* val, hipStream_t s) {
-    hipLaunchKernelGGL(k_argmax_reduce, dim3(1), dim3(1024), 0, s, part, count, idx, val);
+    if (count <= 8 * 1024)
+        hipLaunchKernelGGL(k_argmax_reduce<8>, dim3(1), dim3(1024), 0, s, part, count, idx, val);
+    else if (count <= 16 * 1024)
+        hipLaunchKernelGGL(k_argmax_reduce<16>, dim3(1), dim3(1024), 0, s, part, count, idx, val);
+    else
+        hipLaunchKernelGGL(k_argmax_reduce<32>, dim3(1), dim3(1024), 0, s, part, count, idx, val);
     return hipGetLastError();
 }
 
