@@ -56,22 +56,38 @@ __global__ __launch_bounds__(T) void k_gemv_bf16_xop(const uint16_t* __restrict_
     }
 }
 
-// T threads per workgroup, each wave looping over its rows; x is prefetched into registers before the
-// weight prologue when XP * T covers K / 4 (else the rest is copied after).
-// Rows per wave (at most 64: the row sums stay in lanes), measured: 4 for
-// short rows (<= 3 pieces: one row alone leaves the ring part empty), 2 for
-// long ones (x is staged by half as many workgroups), else 1.
-int64_t bf16_workgroups(int64_t n, int64_t k, int T) {
-    const int64_t waves = T / kWave, pieces = (k + kPiece - 1) / kPiece;
-    int64_t rpw = tune_param("BF16_ROWS_PER_WAVE", pieces <= 3 ? 4 : (pieces >= 12 ? 2 : 1));
-    rpw = rpw < 1 ? 1 : (rpw > 64 ? 64 : rpw);
-    return (n + waves * rpw - 1) / (waves * rpw);
+// Launch shape: waves per workgroup (T / 64), each wave looping over its
+// rows; x is prefetched into registers before the weight prologue when
+// XP * T covers K / 4 (else the rest is copied after).  Rows per wave (at
+// most 64: the row sums stay in lanes), measured: 4 for short rows (<= 3
+// pieces: one row alone leaves the ring part empty), 2 for long ones (x is
+// staged by half as many workgroups), else 1, with 8 waves.  Long rows
+// whose 16-row workgroups would leave CUs idle take 12 waves of one row
+// each where that is one round: the K = 8192 BF16 down projection of
+// 3072 rows in 256 workgroups instead of 192, the headline step 697-699
+// against 702-704 us (4 waves of 3 rows, also 256 workgroups, 699-700).
+struct Bf16Shape {
+    int waves;
+    int64_t rpw;
+};
+Bf16Shape bf16_shape(int64_t n, int64_t k) {
+    const int64_t pieces = (k + kPiece - 1) / kPiece, cus = device_info().cus;
+    Bf16Shape sh{8, pieces <= 3 ? 4 : (pieces >= 12 ? 2 : 1)};
+    if (pieces >= 12 && (n + 15) / 16 < cus && (n + 11) / 12 <= cus) sh = Bf16Shape{12, 1};
+    sh.waves = tune_param("BF16_WAVES", sh.waves);
+    if (sh.waves != 4 && sh.waves != 12 && sh.waves != 16) sh.waves = 8;
+    const int64_t r = tune_param("BF16_ROWS_PER_WAVE", static_cast<int>(sh.rpw));
+    sh.rpw = r < 1 ? 1 : (r > 64 ? 64 : r);
+    return sh;
+}
+int64_t bf16_workgroups(int64_t n, const Bf16Shape& sh) {
+    return (n + sh.waves * sh.rpw - 1) / (sh.waves * sh.rpw);
 }
 
 template <bool ARGMAX, int T>
 hipError_t run(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k, uint64_t* key,
-               hipStream_t s) {
-    const int64_t wgs = bf16_workgroups(n, k, T);
+               hipStream_t s, const Bf16Shape& sh) {
+    const int64_t wgs = bf16_workgroups(n, sh);
     const size_t lds = bf16_m1_lds_bytes(k);
     const int ik = static_cast<int>(k), in = static_cast<int>(n);
     const int64_t per = (k / 4 + T - 1) / T;
@@ -97,24 +113,19 @@ hipError_t run(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k
 template <bool ARGMAX>
 hipError_t run_rows(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k, uint64_t* key,
                     hipStream_t s) {
-    // One row per wave at a time, ring of 8 pieces; RT_HIP_BF16_WAVES (waves
-    // per workgroup) overrides the measured default.
-    const int waves = tune_param("BF16_WAVES", 8);
-    if (waves == 4) return run<ARGMAX, 256>(w, x, y, n, k, key, s);
-    if (waves == 12) return run<ARGMAX, 768>(w, x, y, n, k, key, s);
-    if (waves == 16) return run<ARGMAX, 1024>(w, x, y, n, k, key, s);
-    return run<ARGMAX, 512>(w, x, y, n, k, key, s);
+    // One row per wave at a time, ring of 8 pieces.
+    const Bf16Shape sh = bf16_shape(n, k);
+    if (sh.waves == 4) return run<ARGMAX, 256>(w, x, y, n, k, key, s, sh);
+    if (sh.waves == 12) return run<ARGMAX, 768>(w, x, y, n, k, key, s, sh);
+    if (sh.waves == 16) return run<ARGMAX, 1024>(w, x, y, n, k, key, s, sh);
+    return run<ARGMAX, 512>(w, x, y, n, k, key, s, sh);
 }
 
 }  // namespace
 
 size_t bf16_m1_lds_bytes(int64_t k) { return bf16_gemv::lds_bytes(k); }
 
-int64_t bf16_argmax_partials(int64_t n, int64_t k) {
-    const int waves = tune_param("BF16_WAVES", 8);
-    const int T = waves == 4 ? 256 : (waves == 12 ? 768 : (waves == 16 ? 1024 : 512));
-    return bf16_workgroups(n, k, T);
-}
+int64_t bf16_argmax_partials(int64_t n, int64_t k) { return bf16_workgroups(n, bf16_shape(n, k)); }
 
 hipError_t launch_gemv_bf16_m1(const uint16_t* w, const float* x, float* y, int64_t n, int64_t k,
                                uint64_t* key, hipStream_t s) {
@@ -122,19 +133,17 @@ hipError_t launch_gemv_bf16_m1(const uint16_t* w, const float* x, float* y, int6
 }
 
 namespace {
-// The default launch shape of run() (8 waves), with an x operation.
-constexpr int kXopThreads = 512;
-int64_t xop_workgroups(int64_t n, int64_t k) {
-    const int64_t waves = kXopThreads / kWave, pieces = (k + kPiece - 1) / kPiece;
-    const int64_t rpw = pieces <= 3 ? 4 : (pieces >= 12 ? 2 : 1);
-    return (n + waves * rpw - 1) / (waves * rpw);
+// run()'s launch shape with an x operation: 8 or 12 waves (bf16_shape).
+Bf16Shape xop_shape(int64_t n, int64_t k) {
+    Bf16Shape sh = bf16_shape(n, k);
+    if (sh.waves != 12) sh.waves = 8;
+    return sh;
 }
 
-template <int XOP, bool ADD, bool ARGMAX = false>
-hipError_t run_xop(const uint16_t* w, const float* x, const float* aux, float eps, float* y, int64_t n, int64_t k,
-                   hipStream_t s, uint64_t* key = nullptr) {
-    constexpr int T = kXopThreads;
-    const int64_t wgs = xop_workgroups(n, k);
+template <int XOP, bool ADD, bool ARGMAX, int T>
+hipError_t run_xop_t(const uint16_t* w, const float* x, const float* aux, float eps, float* y, int64_t n, int64_t k,
+                     hipStream_t s, uint64_t* key, const Bf16Shape& sh) {
+    const int64_t wgs = bf16_workgroups(n, sh);
     const int64_t per = (k / 4 + T - 1) / T;
     const dim3 g(static_cast<unsigned>(wgs)), b(T);
     const size_t lds = bf16_m1_lds_bytes(k);
@@ -147,9 +156,17 @@ hipError_t run_xop(const uint16_t* w, const float* x, const float* aux, float ep
         hipLaunchKernelGGL((k_gemv_bf16_xop<8, 8, T, XOP, ADD, ARGMAX>), g, b, lds, s, w, x, aux, y, in, ik, eps, key);
     return hipGetLastError();
 }
+
+template <int XOP, bool ADD, bool ARGMAX = false>
+hipError_t run_xop(const uint16_t* w, const float* x, const float* aux, float eps, float* y, int64_t n, int64_t k,
+                   hipStream_t s, uint64_t* key = nullptr) {
+    const Bf16Shape sh = xop_shape(n, k);
+    return sh.waves == 12 ? run_xop_t<XOP, ADD, ARGMAX, 768>(w, x, aux, eps, y, n, k, s, key, sh)
+                          : run_xop_t<XOP, ADD, ARGMAX, 512>(w, x, aux, eps, y, n, k, s, key, sh);
+}
 }  // namespace
 
-int64_t bf16_xop_argmax_partials(int64_t n, int64_t k) { return xop_workgroups(n, k); }
+int64_t bf16_xop_argmax_partials(int64_t n, int64_t k) { return bf16_workgroups(n, xop_shape(n, k)); }
 
 hipError_t launch_gemv_bf16_xop_argmax(int xop, const uint16_t* w, const float* x, const float* gamma, float eps,
                                        float* y, int64_t n, int64_t k, uint64_t* keys, hipStream_t s) {
