@@ -133,11 +133,12 @@ hipError_t launch_gemv_bf16_m1(const uint16_t* w, const float* x, float* y, int6
 }
 
 namespace {
-// run()'s launch shape with an x operation: 8 or 12 waves (bf16_shape).
+// run()'s default launch shape (8 waves) with an x operation.  The 12-wave
+// shape of long rows measured slower here: the Llama-3.2-3B engine's BF16
+// SwiGLU + down + residual 1124.6-1124.9 against 1116.0-1117.3 us/token.
 Bf16Shape xop_shape(int64_t n, int64_t k) {
-    Bf16Shape sh = bf16_shape(n, k);
-    if (sh.waves != 12) sh.waves = 8;
-    return sh;
+    const int64_t pieces = (k + kPiece - 1) / kPiece;
+    return Bf16Shape{8, pieces <= 3 ? 4 : (pieces >= 12 ? 2 : 1)};
 }
 
 template <int XOP, bool ADD, bool ARGMAX, int T>
@@ -160,9 +161,7 @@ hipError_t run_xop_t(const uint16_t* w, const float* x, const float* aux, float 
 template <int XOP, bool ADD, bool ARGMAX = false>
 hipError_t run_xop(const uint16_t* w, const float* x, const float* aux, float eps, float* y, int64_t n, int64_t k,
                    hipStream_t s, uint64_t* key = nullptr) {
-    const Bf16Shape sh = xop_shape(n, k);
-    return sh.waves == 12 ? run_xop_t<XOP, ADD, ARGMAX, 768>(w, x, aux, eps, y, n, k, s, key, sh)
-                          : run_xop_t<XOP, ADD, ARGMAX, 512>(w, x, aux, eps, y, n, k, s, key, sh);
+    return run_xop_t<XOP, ADD, ARGMAX, 512>(w, x, aux, eps, y, n, k, s, key, xop_shape(n, k));
 }
 }  // namespace
 
