@@ -32,7 +32,7 @@ STEP_TOL = 1e-5
 class Model:
     """Weights on the host and the oracle's decode step."""
 
-    def __init__(self, orc, arch, rng, q6k_down=False, **cfg):
+    def __init__(self, orc, arch, rng, q6k_down=False, wide_layers=None, **cfg):
         self.orc, self.arch, self.cfg = orc, arch, cfg
         self.gemma = arch == "gemma3"
         H, F, nq, nkv, d, V = (cfg[k] for k in ("hidden", "ffn", "n_heads", "n_kv_heads", "head_dim", "vocab"))
@@ -61,7 +61,7 @@ class Model:
             self.w[name] = (base + 0.1 * rng.standard_normal(n)).astype(np.float32)
 
         for li in range(cfg["n_layers"]):
-            wide = li == 0 and not self.gemma
+            wide = li in wide_layers if wide_layers is not None else (li == 0 and not self.gemma)
             proj(f"{li}.q", nq * d, H, False)
             proj(f"{li}.k", nkv * d, H, False)
             proj(f"{li}.v", nkv * d, H, wide)
@@ -187,6 +187,29 @@ def test_decoder_steps_match_oracle(rt, orc, arch, cfg):
         assert idx == orc.argmax_first(got) and idx == orc.argmax_first(want), pos
     say(f"[decoder {arch}] worst step normwise error {worst:.2e}")
     dec.close()
+
+
+def test_decoder_gemma_mixed_formats_match_oracle(rt, orc):
+    """Gemma 3 with BF16 v and down in the middle layer (a Q4_K_M-style mix):
+    that layer's q/k/v launch cannot take the previous layer's post-FFN norm
+    (the separate norm runs there), the next layer's can (after a BF16 GELU
+    down), and every gate/up launch takes its post-attention norm."""
+    cfg = dict(GEMMA, n_layers=3)
+    rng = np.random.default_rng(23)
+    m = Model(orc, "gemma3", rng, wide_layers={1}, **cfg)
+    dec = m.load(rt)
+    try:
+        worst = 0.0
+        for pos, tok in enumerate(rng.integers(0, cfg["vocab"], 8)):
+            got, idx = dec.step(int(tok), pos, argmax=True)
+            want = m.step(int(tok), pos)
+            e = normwise_err(got, want)
+            worst = max(worst, e)
+            assert e <= STEP_TOL, (pos, e)
+            assert idx == orc.argmax_first(got), pos
+        say(f"[decoder gemma3 mixed] worst step normwise error {worst:.2e}")
+    finally:
+        dec.close()
 
 
 @pytest.mark.parametrize("arch,cfg", [("llama", LLAMA), ("gemma3", GEMMA)])
