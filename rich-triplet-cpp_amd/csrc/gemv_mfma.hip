@@ -726,14 +726,20 @@ hipError_t run_xp(const Jobs& jobs, const float* x, const XArgs& xa, int64_t k, 
 // K-split per tile.  One round of workgroups (at most one per CU) is what
 // matters for the short outputs of a decode step: a launch whose last few
 // CUs get a second workgroup takes twice as long.  Among the splits of
-// {1, 2, 3, 4, 6, 8, 12} that divide the super-block count, leave every
+// {1, 2, 3, 4, 6, 8, 10, 12} that divide the super-block count, leave every
 // wave at least two super-blocks and fit one workgroup per CU, the one with
 // the fewest rounds of x conversion per SIMD (every wave converts its share
-// of x before it uses any weight: waves per SIMD x f32x4 per thread), and
-// among those the largest (more loads in flight).  Measured: o 3072 x 3072
-// 3.84 us at KS = 4 (3 rounds) against 4.41 us at KS = 6 (4 rounds); down
-// 3072 x 8192 best at KS = 8.  Outputs too long for one round even at
-// KS = 1 use KS = 4 (the lm_head: 38.0 us against 40.9 us at KS = 2).
+// of x before it uses any weight: waves per SIMD x f32x4 per thread, the
+// latter as the register batch the launch instantiates, 2, 3, 4 or 8, and
+// past 8 counted twice, since the rest is converted after the weight
+// prologue with full waits), and among those the largest (more loads in
+// flight).  Measured: o 3072 x 3072 3.84 us at KS = 4 (3 rounds) against
+// 4.41 us at KS = 6 (4 rounds); down 3072 x 8192 best at KS = 8; the
+// Gemma-3-4B down 2560 x 10240 (GELU gating) at KS = 10 (4 f32x4 per
+// thread, 12 rounds) rather than 8 (5, batched as 8: 16 rounds), engine
+// token 1609-1613 against 1633-1641 us (KS = 4: 1672-1678, 5: 1669).
+// Outputs too long for one round even at KS = 1 use KS = 4 (the lm_head:
+// 38.0 us against 40.9 us at KS = 2).
 // KS = 1, 2, 4 run 4 waves per workgroup (4/KS tiles); other splits one
 // tile per workgroup of KS waves.
 struct Shape {
@@ -746,12 +752,13 @@ template <bool TILED>
 bool shape_for(int64_t tiles, int64_t k, Shape& sh) {
     const int64_t nb = k / 256;
     const int64_t cus = device_info().cus;
-    static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12};
+    static const int kSplits[] = {1, 2, 3, 4, 6, 8, 10, 12};
     auto waves_for = [](int c) { return c <= 4 ? (4 / c) * c : c; };
     auto wgs_for = [&](int c) { return (tiles + waves_for(c) / c - 1) / (waves_for(c) / c); };
     auto rounds = [&](int c) {
         const int64_t w = waves_for(c), per = (k / 4 + 64 * w - 1) / (64 * w);
-        return (w + 3) / 4 * per;
+        const int64_t batch = per <= 2 ? 2 : (per <= 4 ? per : (per <= 8 ? 8 : 2 * per - 8));
+        return (w + 3) / 4 * batch;
     };
     auto usable = [&](int c) { return nb % c == 0 && (c == 1 || 2 * c <= nb); };
     int ks = 1;

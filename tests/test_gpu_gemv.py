@@ -32,6 +32,7 @@ Q4K_CASES = [
     (3072, 3072, 2, "llama q/o, M=2"),
     (7, 512, 3, "tiny N"),
     (1, 12288, 1, "single row, K=12288"),
+    (2560, 10240, 1, "gemma-3-4b down: K split 10 ways"),
 ]
 
 

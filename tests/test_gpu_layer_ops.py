@@ -52,7 +52,8 @@ def test_rmsnorm_zero_activation_gives_zero(rt, orc):
     assert not np.any(from_dev(y))
 
 
-@pytest.mark.parametrize("n,k,note", [(3072, 8192, "llama down"), (100, 512, "ragged N"), (16, 256, "one block")])
+@pytest.mark.parametrize("n,k,note", [(3072, 8192, "llama down"), (2560, 10240, "gemma-3-4b down shape, K split 10"),
+                                      (100, 512, "ragged N"), (16, 256, "one block")])
 def test_swiglu_fused_gemv(rt, orc, n, k, note):
     say(f"[swiglu gemv] N={n} K={k} ({note})")
     rng = np.random.default_rng(n + 3 * k)
