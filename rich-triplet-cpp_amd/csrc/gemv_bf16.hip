@@ -66,13 +66,22 @@ __global__ __launch_bounds__(T) void k_gemv_bf16_xop(const uint16_t* __restrict_
 // each where that is one round: the K = 8192 BF16 down projection of
 // 3072 rows in 256 workgroups instead of 192, the headline step 697-699
 // against 702-704 us (4 waves of 3 rows, also 256 workgroups, 699-700).
+// Outputs of more than 16 rounds of workgroups (the lm_heads) double the
+// rows per wave up to 8, so each workgroup stages x for more rows: config
+// 2b (262144 x 1152) 5214-5281 GB/s at 8 rows against 4880-4946 at 4 on
+// one box (5104 at 16).
 struct Bf16Shape {
     int waves;
     int64_t rpw;
 };
+int64_t amortized_rows(int64_t n, int waves, int64_t rpw) {
+    const int64_t cus = device_info().cus;
+    while (rpw < 8 && (n + waves * rpw - 1) / (waves * rpw) > 16 * cus) rpw *= 2;
+    return rpw;
+}
 Bf16Shape bf16_shape(int64_t n, int64_t k) {
     const int64_t pieces = (k + kPiece - 1) / kPiece, cus = device_info().cus;
-    Bf16Shape sh{8, pieces <= 3 ? 4 : (pieces >= 12 ? 2 : 1)};
+    Bf16Shape sh{8, amortized_rows(n, 8, pieces <= 3 ? 4 : (pieces >= 12 ? 2 : 1))};
     if (pieces >= 12 && (n + 15) / 16 < cus && (n + 11) / 12 <= cus) sh = Bf16Shape{12, 1};
     sh.waves = tune_param("BF16_WAVES", sh.waves);
     if (sh.waves != 4 && sh.waves != 12 && sh.waves != 16) sh.waves = 8;
@@ -136,9 +145,13 @@ namespace {
 // run()'s default launch shape (8 waves) with an x operation.  The 12-wave
 // shape of long rows measured slower here: the Llama-3.2-3B engine's BF16
 // SwiGLU + down + residual 1124.6-1124.9 against 1116.0-1117.3 us/token.
+// Nor do more rows per wave pay for the Gemma-3-4B lm_head (262144 x 2560
+// with the final norm): engine token 1623-1627 us at 8 rows against
+// 1608-1612 at 1, on one box.
 Bf16Shape xop_shape(int64_t n, int64_t k) {
     const int64_t pieces = (k + kPiece - 1) / kPiece;
-    return Bf16Shape{8, pieces <= 3 ? 4 : (pieces >= 12 ? 2 : 1)};
+    const int r = tune_param("BF16_XOP_ROWS_PER_WAVE", pieces <= 3 ? 4 : (pieces >= 12 ? 2 : 1));
+    return Bf16Shape{8, r < 1 ? 1 : (r > 64 ? 64 : r)};
 }
 
 template <int XOP, bool ADD, bool ARGMAX, int T>
