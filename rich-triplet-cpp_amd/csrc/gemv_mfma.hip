@@ -764,11 +764,16 @@ bool shape_for(int64_t tiles, int64_t k, Shape& sh) {
     int ks = 1;
     for (int c : kSplits)
         if (usable(c) && wgs_for(c) <= cus && rounds(c) <= rounds(ks)) ks = c;
-    if (wgs_for(1) > cus) ks = usable(4) ? 4 : (usable(2) ? 2 : 1);
+    // (Swept on the headline step's lm_head, 8016 tiles: KS 4 with one tile
+    // per workgroup 701-702 us against 703-705 for KS 4 x 2 tiles, 2 x 2,
+    // 2 x 4, 1 x 4 and 1 x 8.)
+    const bool many = wgs_for(1) > cus;
+    if (many) ks = tune_param("Q4K_MANY_KS", usable(4) ? 4 : (usable(2) ? 2 : 1));
     if (const int forced = tune_param("Q4K_KS", 0)) ks = (nb % forced == 0 && forced <= 12) ? forced : ks;
     // a whole number of tiles per workgroup: 4 waves for KS = 1, 2, 4;
     // exactly KS waves (one tile) otherwise
     int waves = ks <= 4 ? (4 / ks) * ks : ks;
+    if (many) waves = ks * tune_param("Q4K_MANY_TPW", waves / ks);
     // More tiles than one round of those workgroups holds, but no more than
     // 8 per CU: one round at KS = 1 with one weight wave per tile (and the
     // converter waves beside them).  Gemma-3-4B's gate+up, 1280 tiles at
