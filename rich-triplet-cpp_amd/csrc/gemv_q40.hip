@@ -27,7 +27,6 @@
 namespace rt_hip {
 namespace {
 
-constexpr int kT = 256;  // 4 waves
 constexpr int kBlockBytes = 18;
 
 template <int CTRL>
@@ -39,7 +38,7 @@ struct Slot {
     uint32_t w0, w1, w2, w3, w4;
 };
 
-template <int D, int XP>
+template <int D, int XP, int kT>
 __global__ __launch_bounds__(kT) void k_gemv_q40(const uint8_t* __restrict__ W, const float* __restrict__ X,
                                                  float* __restrict__ Y, int N, int K) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -184,21 +183,33 @@ hipError_t launch_gemv_q4_0_m1(const void* w, const float* x, float* y, int64_t 
     // Rows per wave: four 64-block runs per wave, at most 64 rows (row sums
     // stay in lanes).  Measured at 4096 x 4096 (two runs per row): 2 rows
     // per wave 5.65 us, 4 rows (a full ring of 8) 5.92 us, 1 row 6.26 us --
-    // more waves per CU hide more latency than a fuller ring.
+    // more waves per CU hide more latency than a fuller ring.  8 waves per
+    // workgroup where that is one round of workgroups (x staged once per CU
+    // instead of twice): 5.51-5.53 us against 5.69-5.76 with 4 (1 row per
+    // wave at 8: 6.13; 4 rows: 7.04).
     const int64_t runs = (k / 32 + 63) / 64;
     int64_t rpw = tune_param("Q40_ROWS_PER_WAVE", static_cast<int>((4 + runs - 1) / runs));
     rpw = rpw < 1 ? 1 : (rpw > 64 ? 64 : rpw);
-    const int64_t waves = kT / kWave;
+    const int T = tune_param("Q40_THREADS", (n + 8 * rpw - 1) / (8 * rpw) <= device_info().cus ? 512 : 256) == 512
+                      ? 512
+                      : 256;
+    const int64_t waves = T / kWave;
     const int64_t wgs = (n + waves * rpw - 1) / (waves * rpw);
-    const int64_t per = (k / 4 + kT - 1) / kT;
+    const int64_t per = (k / 4 + T - 1) / T;
     const size_t lds = q40_m1_lds_bytes(k);
-    const dim3 g(static_cast<unsigned>(wgs)), b(kT);
+    const dim3 g(static_cast<unsigned>(wgs)), b(T);
     const auto* wb = static_cast<const uint8_t*>(w);
     const int in = static_cast<int>(n), ik = static_cast<int>(k);
-    if (per <= 4)
-        hipLaunchKernelGGL((k_gemv_q40<8, 4>), g, b, lds, s, wb, x, y, in, ik);
-    else
-        hipLaunchKernelGGL((k_gemv_q40<8, 8>), g, b, lds, s, wb, x, y, in, ik);
+    if (T == 512) {
+        if (per <= 4)
+            hipLaunchKernelGGL((k_gemv_q40<8, 4, 512>), g, b, lds, s, wb, x, y, in, ik);
+        else
+            hipLaunchKernelGGL((k_gemv_q40<8, 8, 512>), g, b, lds, s, wb, x, y, in, ik);
+    } else if (per <= 4) {
+        hipLaunchKernelGGL((k_gemv_q40<8, 4, 256>), g, b, lds, s, wb, x, y, in, ik);
+    } else {
+        hipLaunchKernelGGL((k_gemv_q40<8, 8, 256>), g, b, lds, s, wb, x, y, in, ik);
+    }
     return hipGetLastError();
 }
 
