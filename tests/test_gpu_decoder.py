@@ -32,12 +32,14 @@ STEP_TOL = 1e-5
 class Model:
     """Weights on the host and the oracle's decode step."""
 
-    def __init__(self, orc, arch, rng, q6k_down=False, wide_layers=None, **cfg):
+    def __init__(self, orc, arch, rng, q6k_down=False, wide_layers=None, randn=None, **cfg):
         self.orc, self.arch, self.cfg = orc, arch, cfg
         self.gemma = arch == "gemma3"
         H, F, nq, nkv, d, V = (cfg[k] for k in ("hidden", "ffn", "n_heads", "n_kv_heads", "head_dim", "vocab"))
         self.fmt = {}
         self.w = {}
+        # N(0, 1) draws (float32 arrays of `shape`): numpy's by default
+        randn = randn or (lambda shape: rng.standard_normal(shape))
 
         def proj(name, n, k, bf16):
             if bf16 == "q6k":  # GGUF Q6_K bytes; the oracle multiplies their bf16 widening
@@ -47,7 +49,7 @@ class Model:
                 self.wide_q6k = getattr(self, "wide_q6k", {})
                 self.wide_q6k[name] = orc.f32_to_bf16_n(orc.q6k_decode(self.w[name], n * k)).reshape(n, k)
                 return
-            w32 = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+            w32 = (randn((n, k)) * 0.02).astype(np.float32)
             if bf16:
                 self.w[name] = orc.f32_to_bf16_n(w32).reshape(n, k)
                 self.fmt[name] = "bf16"
@@ -58,7 +60,7 @@ class Model:
         def norm(name, n):
             # Gemma 3 norms apply 1 + gamma, Llama's gamma itself
             base = 0.0 if self.gemma else 1.0
-            self.w[name] = (base + 0.1 * rng.standard_normal(n)).astype(np.float32)
+            self.w[name] = (base + 0.1 * randn((n,))).astype(np.float32)
 
         for li in range(cfg["n_layers"]):
             wide = li in wide_layers if wide_layers is not None else (li == 0 and not self.gemma)
@@ -74,7 +76,7 @@ class Model:
             if self.gemma:
                 norm(f"{li}.q_norm", d)
                 norm(f"{li}.k_norm", d)
-        self.w["embed"] = orc.f32_to_bf16_n((rng.standard_normal((V, H)) * 0.5).astype(np.float32)).reshape(V, H)
+        self.w["embed"] = orc.f32_to_bf16_n((randn((V, H)) * 0.5).astype(np.float32)).reshape(V, H)
         norm("out_norm", H)
         proj("lm_head", V, H, self.gemma)
         self.kc = [np.zeros((cfg["max_seq"], nkv * d), np.float32) for _ in range(cfg["n_layers"])]
@@ -387,6 +389,50 @@ def test_decoder_long_cache_matches_oracle(rt, orc, arch, cfg, rows):
             # the cases meant to hold idle splits do
             S = split_rule(n_kv, 1, cfg["max_seq"], cus, hd)
             assert busy_rule(rows + 1, S, hd) < S
+    finally:
+        dec.close()
+
+
+# The benchmarked models' layer dimensions (hidden, ffn, heads), two layers
+# and a 32768-token vocabulary (the weights drawn on the GPU for speed).
+LLAMA_3B_FULL = dict(LLAMA, hidden=3072, n_heads=24, n_kv_heads=8, head_dim=128, ffn=8192, vocab=32768,
+                     max_seq=1024, max_batch=0)
+GEMMA_4B_FULL = dict(GEMMA, hidden=2560, n_heads=8, n_kv_heads=4, head_dim=256, ffn=10240, vocab=32768,
+                     max_seq=1024, sliding_window=512, max_batch=0, embed_scale=float(np.sqrt(np.float32(2560))))
+
+
+@pytest.mark.parametrize("arch,cfg", [("llama3b", LLAMA_3B_FULL), ("gemma3_4b", GEMMA_4B_FULL)])
+def test_decoder_full_dimensions_match_oracle(rt, orc, arch, cfg):
+    """The engine at Llama-3.2-3B / Gemma-3-4B layer dimensions, 600 cached
+    positions, four steps against the oracle.  Llama: layer 0 in the
+    Q4_K_M-style mix (BF16 v in the fused q/k/v + RoPE + KV append launch,
+    BF16 SwiGLU down), layer 1 all Q4_K.  Gemma: a local layer whose window
+    has slid past position 0 and a global one, the post-norms folded into
+    gate/up and into layer 1's q/k/v at K = 2560, the GELU down split 10
+    ways at K = 10240, the BF16 lm_head's argmax epilogue."""
+    import torch
+    say(f"[decoder {arch} full dimensions]")
+    g = torch.Generator(device="cuda").manual_seed(11 + len(arch))
+
+    def randn(shape):
+        return torch.randn(shape, generator=g, device="cuda").cpu().numpy()
+
+    rng = np.random.default_rng(11 + len(arch))
+    gemma = arch.startswith("gemma")
+    m = Model(orc, "gemma3" if gemma else "llama", rng, randn=randn, **cfg)
+    dec = m.load(rt)
+    try:
+        prefill(m, dec, rng, 600)
+        worst = 0.0
+        for i, tok in enumerate(rng.integers(0, cfg["vocab"], 4)):
+            pos = 600 + i
+            got, idx = dec.step(int(tok), pos, argmax=True)
+            want = m.step(int(tok), pos)
+            e = normwise_err(got, want)
+            worst = max(worst, e)
+            assert e <= STEP_TOL, (pos, e)
+            assert idx == orc.argmax_first(got), pos
+        say(f"[decoder {arch} full dimensions] worst step normwise error {worst:.2e}")
     finally:
         dec.close()
 
