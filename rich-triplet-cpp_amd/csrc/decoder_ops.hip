@@ -578,9 +578,9 @@ __device__ __forceinline__ void attn2_partial(const AttnArgs& a, const PrepArgs&
 
     int pb = p0 + grp;
     if constexpr (PREP) {
-        // The first round by every group (one past the range loads nothing
-        // and scores -inf), its loads in flight while the new token is
-        // prepared: the workgroup's threads share the d/2 rotation angles
+        // The first round by every group (one past the range reads row k0,
+        // replaced by zeros, and scores -inf), its loads in flight while the
+        // new token is prepared: the workgroup's threads share the d/2 rotation angles
         // of k_qk_prep (pos * tab[i], or (pos * freq_scale) / tab[i])
         // through LDS, one cosine and sine each.
         f32x4 ka[kAU], kb[kAU], va[kAU], vb[kAU];
