@@ -264,7 +264,7 @@ __device__ __forceinline__ float ld_dev(const float* p) {
 constexpr int kCB = 16;  // splits per batch of loads
 
 // The running (M, L, O) of splits [s_begin, s_end) (none: -inf, 0, 0).
-template <int PART, int P, bool COH>
+template <int PART, int P, bool COH, int CB = kCB>
 __device__ __forceinline__ void fold_state(const float* const (&ph)[P], const int (&d)[P], int s_begin, int s_end,
                                            float (&M)[P], float (&L)[P], float (&O)[P]) {
     auto ld = [](const float* p) { return COH ? ld_dev(p) : *p; };
@@ -275,13 +275,13 @@ __device__ __forceinline__ void fold_state(const float* const (&ph)[P], const in
         O[p] = 0.0f;
     }
     const int S = s_end;
-    for (int s0 = s_begin; s0 < S; s0 += kCB) {
+    for (int s0 = s_begin; s0 < S; s0 += CB) {
         // every load of the batch, for all of this thread's P pairs, first
-        float ms[P][kCB], ls[P][kCB], os[P][kCB];
+        float ms[P][CB], ls[P][CB], os[P][CB];
 #pragma unroll
         for (int p = 0; p < P; ++p)
 #pragma unroll
-            for (int j = 0; j < kCB; ++j) {
+            for (int j = 0; j < CB; ++j) {
                 const float* ps = ph[p] + min(s0 + j, S - 1) * PART;
                 ms[p][j] = ld(ps);
                 ls[p][j] = ld(ps + 1);
@@ -292,7 +292,7 @@ __device__ __forceinline__ void fold_state(const float* const (&ph)[P], const in
         for (int p = 0; p < P; ++p) {
             float Mb = M[p];
 #pragma unroll
-            for (int j = 0; j < kCB; ++j) Mb = s0 + j < S ? fmaxf(Mb, ms[p][j]) : Mb;
+            for (int j = 0; j < CB; ++j) Mb = s0 + j < S ? fmaxf(Mb, ms[p][j]) : Mb;
             // No state yet (Mb = -inf, so M = -inf, L = O = 0): every weight
             // is 0 and nothing changes.  Selects, not a branch: behind a
             // branch the compiler issues the O loads only once the M loads
@@ -302,7 +302,7 @@ __device__ __forceinline__ void fold_state(const float* const (&ph)[P], const in
             L[p] *= r;
             O[p] *= r;
 #pragma unroll
-            for (int j = 0; j < kCB; ++j) {
+            for (int j = 0; j < CB; ++j) {
                 const float w = s0 + j < S && any ? exp_fast(ms[p][j] - Mb) : 0.0f;
                 L[p] += ls[p][j] * w;
                 O[p] += os[p][j] * w;
@@ -312,10 +312,10 @@ __device__ __forceinline__ void fold_state(const float* const (&ph)[P], const in
     }
 }
 
-template <int PART, int P, bool COH>
+template <int PART, int P, bool COH, int CB = kCB>
 __device__ __forceinline__ void fold_splits(const float* const (&ph)[P], const int (&d)[P], int S, float (&res)[P]) {
     float M[P], L[P], O[P];
-    fold_state<PART, P, COH>(ph, d, 0, S, M, L, O);
+    fold_state<PART, P, COH, CB>(ph, d, 0, S, M, L, O);
 #pragma unroll
     for (int p = 0; p < P; ++p) res[p] = L[p] > 0.0f ? O[p] / L[p] : 0.0f;
 }
@@ -746,7 +746,7 @@ __global__ __launch_bounds__(kAT) void k_attn2_partial_prep(const AttnArgs a, co
 // M = -inf, L = O = 0 and changes nothing); with R parts of at most kCB
 // splits that is one memory latency.  Part 0 then folds the R states in
 // order: the result is the same for every run.
-template <int HD, int R>
+template <int HD, int R, int CB = kCB>
 __global__ __launch_bounds__(HD * R) void k_attn2_combine(const AttnArgs a, int S) {
     using Geo = AttnGeom<HD>;
     const int h = blockIdx.x, m = blockIdx.y, d = static_cast<int>(threadIdx.x) % HD;
@@ -757,7 +757,7 @@ __global__ __launch_bounds__(HD * R) void k_attn2_combine(const AttnArgs a, int 
     float* const out = a.out + (static_cast<int64_t>(m) * n_q + h) * HD + d;
     if constexpr (R == 1) {
         float res[1];
-        fold_splits<Geo::PART, 1, false>(ph, dd, S, res);
+        fold_splits<Geo::PART, 1, false, CB>(ph, dd, S, res);
         *out = res[0];
     } else {
         float M[1], L[1], O[1];
@@ -787,16 +787,24 @@ __global__ __launch_bounds__(HD * R) void k_attn2_combine(const AttnArgs a, int 
 // The combine launch: two parts when that makes one batch of loads each and
 // the workgroup stays at 256 threads (head_dim <= 128).  Measured (engine
 // tokens at 1024 positions): Llama-3.2-3B, 17 splits, 1120-1123 us with two
-// parts against 1129-1136 with one and 1136-1142 with four; Gemma-3-4B
-// (head_dim 256), 32 and 33 splits, 1649-1659 with one part against
-// 1663-1669 with two and 1687-1689 with four (the wider workgroup and its
-// LDS fold cost more than the last batch's latency there).
+// parts against 1129-1136 with one and 1136-1142 with four (one part in one
+// batch of 20: the same as two parts, 1115-1119 against 1114-1115 on one
+// box); Gemma-3-4B (head_dim 256), 32 and 33 splits, 1649-1659 with one
+// part against 1663-1669 with two and 1687-1689 with four (the wider
+// workgroup and its LDS fold cost more than the last batch's latency
+// there), batches of 16 1606-1632 against 1618-1634 for 20 and 1654-1660
+// for 24.
 template <int HD>
 void launch_combine(const AttnArgs& a, int n_q, int S, int M, hipStream_t s) {
     const int parts = tune_param("ATTN_COMBINE_PARTS", S > kCB && S <= 2 * kCB && HD <= 128 ? 2 : 1);
     const dim3 g(static_cast<unsigned>(n_q), static_cast<unsigned>(M));
+    const int cb = tune_param("ATTN_COMBINE_BATCH", kCB);  // sweeps: 16, 20 or 24
     if (parts >= 2)
         hipLaunchKernelGGL((k_attn2_combine<HD, 2>), g, dim3(HD * 2), 0, s, a, S);
+    else if (cb == 20)
+        hipLaunchKernelGGL((k_attn2_combine<HD, 1, 20>), g, dim3(HD), 0, s, a, S);
+    else if (cb == 24)
+        hipLaunchKernelGGL((k_attn2_combine<HD, 1, 24>), g, dim3(HD), 0, s, a, S);
     else
         hipLaunchKernelGGL((k_attn2_combine<HD, 1>), g, dim3(HD), 0, s, a, S);
 }
