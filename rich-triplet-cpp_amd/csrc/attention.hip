@@ -80,20 +80,31 @@ __global__ __launch_bounds__(kT) void k_attn_partial(const float* __restrict__ q
     // the DPP reductions stay inside the group.  kU positions per group are
     // loaded before any is used, so each batch costs one memory latency.
     for (int pb = p0 + grp; pb < p1; pb += kGroups * kU) {
+        // Every load issued with no branch around it (a position past the
+        // split reads row p0, which exists, and is replaced by zeros once
+        // the batch's loads are all issued): behind branches the compiler
+        // cannot count the loads in flight and waits for all of them.
         f32x4 ka[kU], kb[kU], va[kU], vb[kU];
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
             const int p = pb + u * kGroups;
+            const int pr = p < p1 ? p : p0;
+            const float* kp = kc + pr * row + kvh * kHd + sub * 8;
+            const float* vp = vc + pr * row + kvh * kHd + sub * 8;
+            ka[u] = *reinterpret_cast<const f32x4*>(kp);
+            kb[u] = *reinterpret_cast<const f32x4*>(kp + 4);
+            va[u] = *reinterpret_cast<const f32x4*>(vp);
+            vb[u] = *reinterpret_cast<const f32x4*>(vp + 4);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
             const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-            ka[u] = kb[u] = va[u] = vb[u] = z;
-            if (p < p1) {
-                const float* kp = kc + p * row + kvh * kHd + sub * 8;
-                const float* vp = vc + p * row + kvh * kHd + sub * 8;
-                ka[u] = *reinterpret_cast<const f32x4*>(kp);
-                kb[u] = *reinterpret_cast<const f32x4*>(kp + 4);
-                va[u] = *reinterpret_cast<const f32x4*>(vp);
-                vb[u] = *reinterpret_cast<const f32x4*>(vp + 4);
-            }
+            const bool in = pb + u * kGroups < p1;  // uniform per group
+            ka[u] = in ? ka[u] : z;
+            kb[u] = in ? kb[u] : z;
+            va[u] = in ? va[u] : z;
+            vb[u] = in ? vb[u] : z;
         }
         // The batch's kU scores do not depend on each other: all of them
         // first (their cross-lane sums overlap), then one running-maximum
