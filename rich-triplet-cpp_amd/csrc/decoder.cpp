@@ -294,6 +294,7 @@ int layer_step1(rt_hip_decoder* d, int li, hipStream_t s) {
     a.n_kv = nkv;
     a.head_dim = hd;
     a.m = 1;
+    a.cache_rows = c.max_seq;
     rc = attn_splits(d, L, 1, &a.splits);
     if (rc) return rc;
     a.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt(static_cast<float>(hd));
@@ -411,6 +412,7 @@ int layer_stepm(rt_hip_decoder* d, int li, int m, hipStream_t s) {
     a.n_kv = nkv;
     a.head_dim = hd;
     a.m = m;
+    a.cache_rows = c.max_seq;
     rc = attn_splits(d, L, m, &a.splits);
     if (rc) return rc;
     a.scale = c.attn_scale > 0.0f ? c.attn_scale : 1.0f / std::sqrt(static_cast<float>(hd));

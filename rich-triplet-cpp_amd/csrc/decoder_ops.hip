@@ -242,6 +242,11 @@ struct AttnArgs {
     int64_t row;         // cache row stride (elements)
     float* out;          // [M][n_q * HD]
     uint32_t* cnt;       // [M][n_kv] arrival counters, zero between launches
+    // > 0: the cache's row count, when no row ever has a window and S
+    // splits of one round cover it (so split s starts at s * BATCH whatever
+    // the position): the first round's loads are then issued before the
+    // position is read, rows clamped below this count.  0: after it.
+    int early_rows;
 };
 
 // Partials are stored and reloaded with agent-scope (device-coherent)
@@ -479,12 +484,21 @@ __device__ __forceinline__ void attn2_partial(const AttnArgs& a, const PrepArgs&
         }
         tv = pp.tab[tid < HD / 2 ? tid : 0];
     }
-    int k0, k1;
-    attn_range(a, m, k0, k1);
-    const int len = k1 - k0;
-    const int chunk = attn_chunk<Geo::BATCH>(len, S);
-    const int p0 = k0 + sp * chunk, p1 = min(k1, p0 + chunk);
-    const int pcur = k1 - 1;  // PREP: the new token's position (row 0)
+    // The range [k0, k1) of row m and this split's share [p0, p1) of it
+    // (pcur: PREP's new position), once the position has been read.
+    int k0 = 0, k1 = 0, len = 0, chunk = 0, p0 = 0, p1 = 0, pcur = 0;
+    auto set_range = [&]() {
+        attn_range(a, m, k0, k1);
+        len = k1 - k0;
+        chunk = attn_chunk<Geo::BATCH>(len, S);
+        p0 = k0 + sp * chunk;
+        p1 = min(k1, p0 + chunk);
+        pcur = k1 - 1;
+    };
+    // early_rows > 0: split sp's first round is positions sp * BATCH + [0,
+    // BATCH) for every position (no window, chunk = BATCH), so its loads go
+    // out before the position's own load has returned.
+    const bool early = a.early_rows > 0;  // uniform
 
     // One round: the K and V of positions pb, pb + NG, ... (kAU of them)
     // issued, then their scores and the running state.  Every load is
@@ -493,13 +507,15 @@ __device__ __forceinline__ void attn2_partial(const AttnArgs& a, const PrepArgs&
     // branches leave the compiler unsure how many are in flight, so a later
     // wait for an older load becomes a wait for all of them.  An f16
     // cache's bits are loaded into ka / va as they are and widened in
-    // `land`, after the round's loads are all issued.
-    auto issue = [&](int pb, f32x4 (&ka)[kAU], f32x4 (&kb)[kAU], f32x4 (&va)[kAU], f32x4 (&vb)[kAU]) {
+    // `land`, after the round's loads are all issued.  Issued before the
+    // range is known (`before`), a row is clamped to the cache instead.
+    auto issue = [&](int pb, f32x4 (&ka)[kAU], f32x4 (&kb)[kAU], f32x4 (&va)[kAU], f32x4 (&vb)[kAU],
+                     bool before = false) {
 #pragma unroll
         for (int u = 0; u < kAU; ++u) {
             const int p = pb + u * NG;
-            const int64_t off =
-                static_cast<int64_t>(p < p1 ? p : k0) * a.row + static_cast<int64_t>(kvh) * HD + sub * 8;
+            const int r = before ? min(p, a.early_rows - 1) : (p < p1 ? p : k0);
+            const int64_t off = static_cast<int64_t>(r) * a.row + static_cast<int64_t>(kvh) * HD + sub * 8;
             if constexpr (F16) {
                 ka[u] = __builtin_bit_cast(f32x4,
                                            *reinterpret_cast<const u32x4*>(static_cast<const _Float16*>(a.kc) + off));
@@ -546,14 +562,18 @@ __device__ __forceinline__ void attn2_partial(const AttnArgs& a, const PrepArgs&
                 sc[u] = pb + u * NG < p1 ? v : -__builtin_inff();  // uniform per position group
                 mn = fmaxf(mn, sc[u]);
             }
-            if (mn == -__builtin_inff()) continue;  // no position of this group yet
-            const float al = exp_fast(mx[h] - mn);  // 0 while mx is -inf
+            // No position of this group yet (mn = -inf, so mx = -inf and l, o
+            // are 0): a finite reference makes every weight 0 and changes
+            // nothing.  A select, not a branch, so the G heads' chains
+            // interleave.
+            const float mref = mn == -__builtin_inff() ? 0.0f : mn;
+            const float al = exp_fast(mx[h] - mref);  // 0 while mx is -inf
             l[h] *= al;
             oa[h] *= al;
             ob[h] *= al;
 #pragma unroll
             for (int u = 0; u < kAU; ++u) {
-                const float be = exp_fast(sc[u] - mn);  // 0 for positions past the range
+                const float be = exp_fast(sc[u] - mref);  // 0 for positions past the range
                 l[h] += be;
                 oa[h] += va[u] * be;
                 ob[h] += vb[u] * be;
@@ -576,72 +596,78 @@ __device__ __forceinline__ void attn2_partial(const AttnArgs& a, const PrepArgs&
         }
     };
 
-    int pb = p0 + grp;
-    if constexpr (PREP) {
-        // The first round by every group (one past the range reads row k0,
-        // replaced by zeros, and scores -inf), its loads in flight while the
-        // new token is prepared: the workgroup's threads share the d/2 rotation angles
-        // of k_qk_prep (pos * tab[i], or (pos * freq_scale) / tab[i])
-        // through LDS, one cosine and sine each.
+    // The first round by every group, with no branch around its loads (a
+    // group with no position left reads row k0, replaced by zeros, and
+    // scores -inf).  With `early` its loads go out before the position is
+    // read.  PREP: the loads are in flight while the new token is
+    // prepared: the workgroup's threads share the d/2 rotation angles of
+    // k_qk_prep (pos * tab[i], or (pos * freq_scale) / tab[i]) through LDS,
+    // one cosine and sine each.
+    if (!early) set_range();  // uniform; a scalar load, so no vector wait is lost
+    int pb = (early ? sp * Geo::BATCH : p0) + grp;
+    {
         f32x4 ka[kAU], kb[kAU], va[kAU], vb[kAU];
-        issue(pb, ka, kb, va, vb);
-        __shared__ float tcs[HD / 2], tsn[HD / 2];
-        if (tid < HD / 2) {
-            const float ang = pp.mode == 0 ? static_cast<float>(pcur) * tv
-                                           : (static_cast<float>(pcur) * pp.freq_scale) / tv;
-            tcs[tid] = cosf(ang);
-            tsn[tid] = sinf(ang);
-        }
-        __syncthreads();
-        float cs[8], sn[8];
+        issue(pb, ka, kb, va, vb, early);
+        if (early) set_range();
+        if constexpr (PREP) {
+            __shared__ float tcs[HD / 2], tsn[HD / 2];
+            if (tid < HD / 2) {
+                const float ang = pp.mode == 0 ? static_cast<float>(pcur) * tv
+                                               : (static_cast<float>(pcur) * pp.freq_scale) / tv;
+                tcs[tid] = cosf(ang);
+                tsn[tid] = sinf(ang);
+            }
+            __syncthreads();
+            float cs[8], sn[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            // the pair of dim j: j mod d/2 (half-split) or j / 2
-            const int i = pp.half ? (sub * 8 + e) % (HD / 2) : (sub * 8 + e) >> 1;
-            cs[e] = tcs[i];
-            sn[e] = tsn[i];
-        }
-#pragma unroll
-        for (int h = 0; h < G; ++h) prep_head<HD>(qa[h], qb[h], pp.qg != nullptr, qg, cs, sn, pp.half, pp.eps, sub);
-        prep_head<HD>(kna, knb, pp.kg != nullptr, kg, cs, sn, pp.half, pp.eps, sub);
-        const int64_t o = static_cast<int64_t>(pcur) * pp.cache_row + static_cast<int64_t>(kvh) * HD + sub * 8;
-        const bool store = grp == 0 && pcur >= p0 && pcur < p1;  // one group of one workgroup per kv head
-        if constexpr (F16) {
-            // the cache's rounding (RNE), kept for this launch's own use
-            _Float16 hk[8], hv[8];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                hk[e] = static_cast<_Float16>(kna[e]);
-                hk[e + 4] = static_cast<_Float16>(knb[e]);
-                hv[e] = static_cast<_Float16>(vna[e]);
-                hv[e + 4] = static_cast<_Float16>(vnb[e]);
+            for (int e = 0; e < 8; ++e) {
+                // the pair of dim j: j mod d/2 (half-split) or j / 2
+                const int i = pp.half ? (sub * 8 + e) % (HD / 2) : (sub * 8 + e) >> 1;
+                cs[e] = tcs[i];
+                sn[e] = tsn[i];
             }
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                kna[e] = static_cast<float>(hk[e]);
-                knb[e] = static_cast<float>(hk[e + 4]);
-                vna[e] = static_cast<float>(hv[e]);
-                vnb[e] = static_cast<float>(hv[e + 4]);
-            }
-            if (store) {
-                _Float16* kc = static_cast<_Float16*>(pp.kc) + o;
-                _Float16* vc = static_cast<_Float16*>(pp.vc) + o;
+            for (int h = 0; h < G; ++h) prep_head<HD>(qa[h], qb[h], pp.qg != nullptr, qg, cs, sn, pp.half, pp.eps, sub);
+            prep_head<HD>(kna, knb, pp.kg != nullptr, kg, cs, sn, pp.half, pp.eps, sub);
+            const int64_t o = static_cast<int64_t>(pcur) * pp.cache_row + static_cast<int64_t>(kvh) * HD + sub * 8;
+            const bool store = grp == 0 && pcur >= p0 && pcur < p1;  // one group of one workgroup per kv head
+            if constexpr (F16) {
+                // the cache's rounding (RNE), kept for this launch's own use
+                _Float16 hk[8], hv[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    kc[e] = hk[e];
-                    vc[e] = hv[e];
+                for (int e = 0; e < 4; ++e) {
+                    hk[e] = static_cast<_Float16>(kna[e]);
+                    hk[e + 4] = static_cast<_Float16>(knb[e]);
+                    hv[e] = static_cast<_Float16>(vna[e]);
+                    hv[e + 4] = static_cast<_Float16>(vnb[e]);
                 }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    kna[e] = static_cast<float>(hk[e]);
+                    knb[e] = static_cast<float>(hk[e + 4]);
+                    vna[e] = static_cast<float>(hv[e]);
+                    vnb[e] = static_cast<float>(hv[e + 4]);
+                }
+                if (store) {
+                    _Float16* kc = static_cast<_Float16*>(pp.kc) + o;
+                    _Float16* vc = static_cast<_Float16*>(pp.vc) + o;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        kc[e] = hk[e];
+                        vc[e] = hv[e];
+                    }
+                }
+            } else if (store) {
+                float* kc = static_cast<float*>(pp.kc) + o;
+                float* vc = static_cast<float*>(pp.vc) + o;
+                *reinterpret_cast<f32x4*>(kc) = kna;
+                *reinterpret_cast<f32x4*>(kc + 4) = knb;
+                *reinterpret_cast<f32x4*>(vc) = vna;
+                *reinterpret_cast<f32x4*>(vc + 4) = vnb;
             }
-        } else if (store) {
-            float* kc = static_cast<float*>(pp.kc) + o;
-            float* vc = static_cast<float*>(pp.vc) + o;
-            *reinterpret_cast<f32x4*>(kc) = kna;
-            *reinterpret_cast<f32x4*>(kc + 4) = knb;
-            *reinterpret_cast<f32x4*>(vc) = vna;
-            *reinterpret_cast<f32x4*>(vc + 4) = vnb;
         }
         land(pb, ka, kb, va, vb);
-        own_row(pb, ka, kb, va, vb);
+        if constexpr (PREP) own_row(pb, ka, kb, va, vb);
         consume(pb, ka, kb, va, vb);
         pb += NG * kAU;
     }
@@ -963,6 +989,10 @@ hipError_t launch_attention2(const Attn2& p, float* part, uint32_t* counters, hi
     a.row = static_cast<int64_t>(p.n_kv) * p.head_dim;
     a.out = p.out;
     a.cnt = counters;
+    const int64_t round = attn_round_positions(p.head_dim);
+    a.early_rows = p.cache_rows > 0 && p.window == 0 && static_cast<int64_t>(p.splits) * round >= p.cache_rows
+                       ? p.cache_rows
+                       : 0;
     const int G = p.n_q / p.n_kv;
     PrepArgs pa{};
     if (p.prep) {

@@ -241,6 +241,10 @@ struct Attn2 {
     const int32_t* pos = nullptr;
     int k_end = 0, window = 0;
     int n_q = 0, n_kv = 0, head_dim = 0, m = 1, splits = 1;
+    // rows the caches hold (0: not stated); with no window and splits of one
+    // round covering them, the first round's loads leave before the
+    // position is read
+    int cache_rows = 0;
     float scale = 1.0f;
     bool f16 = false;
     // m = 1 with pos: the q/k preparation of launch_qk_prep (same operands,
