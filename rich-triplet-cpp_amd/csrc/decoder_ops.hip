@@ -269,6 +269,12 @@ __device__ __forceinline__ float ld_dev(const float* p) {
 constexpr int kCB = 16;  // splits per batch of loads
 
 // The running (M, L, O) of splits [s_begin, s_end) (none: -inf, 0, 0).
+// Plain-stored partials (!COH) are read after the launch that wrote them, so
+// a split's (M, L) pair, the same for the whole wave when ph and s_begin are,
+// is one scalar load through the constant address space: the wave's vector
+// loads are then only the O values (a third of them), which the memory
+// pipeline takes in fewer issue slots.
+typedef const __attribute__((address_space(4))) f32x2 ConstF2;
 template <int PART, int P, bool COH, int CB = kCB>
 __device__ __forceinline__ void fold_state(const float* const (&ph)[P], const int (&d)[P], int s_begin, int s_end,
                                            float (&M)[P], float (&L)[P], float (&O)[P]) {
@@ -288,8 +294,14 @@ __device__ __forceinline__ void fold_state(const float* const (&ph)[P], const in
 #pragma unroll
             for (int j = 0; j < CB; ++j) {
                 const float* ps = ph[p] + min(s0 + j, S - 1) * PART;
-                ms[p][j] = ld(ps);
-                ls[p][j] = ld(ps + 1);
+                if constexpr (COH) {
+                    ms[p][j] = ld(ps);
+                    ls[p][j] = ld(ps + 1);
+                } else {
+                    const f32x2 ml = *((ConstF2*)(ps));  // PART even: 8-byte aligned
+                    ms[p][j] = ml[0];
+                    ls[p][j] = ml[1];
+                }
                 os[p][j] = ld(ps + 4 + d[p]);
             }
         __builtin_amdgcn_sched_barrier(0);
@@ -776,7 +788,9 @@ template <int HD, int R, int CB = kCB>
 __global__ __launch_bounds__(HD * R) void k_attn2_combine(const AttnArgs a, int S) {
     using Geo = AttnGeom<HD>;
     const int h = blockIdx.x, m = blockIdx.y, d = static_cast<int>(threadIdx.x) % HD;
-    const int r = static_cast<int>(threadIdx.x) / HD;
+    // the part: the same for a whole wave (HD >= 64), said so to the compiler
+    // so that the (M, L) loads are scalar
+    const int r = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / HD);
     const int n_q = gridDim.x;
     const float* ph[1] = {a.part + (static_cast<int64_t>(m) * n_q + h) * S * Geo::PART};
     const int dd[1] = {d};
@@ -810,29 +824,25 @@ __global__ __launch_bounds__(HD * R) void k_attn2_combine(const AttnArgs a, int 
     }
 }
 
-// The combine launch: two parts when that makes one batch of loads each and
-// the workgroup stays at 256 threads (head_dim <= 128).  Measured (engine
-// tokens at 1024 positions): Llama-3.2-3B, 17 splits, 1120-1123 us with two
-// parts against 1129-1136 with one and 1136-1142 with four (one part in one
-// batch of 20: the same as two parts, 1115-1119 against 1114-1115 on one
-// box); Gemma-3-4B (head_dim 256), 32 and 33 splits, 1649-1659 with one
-// part against 1663-1669 with two and 1687-1689 with four (the wider
-// workgroup and its LDS fold cost more than the last batch's latency
-// there), batches of 16 1606-1632 against 1618-1634 for 20 and 1654-1660
-// for 24.
+// The combine launch: ceil(S / kCB) parts (at most 4), so each part is one
+// batch of loads.  Measured (engine tokens at 1024 positions, vector loads
+// for every value): Llama-3.2-3B, 17 splits, 1120-1123 us with two parts
+// against 1129-1136 with one and 1136-1142 with four; Gemma-3-4B (head_dim
+// 256, 32 and 34 splits) one part 1649-1659 against 1663-1669 with two.
+// With the (M, L) pairs as scalar loads, timed alone in a hipGraph: 17
+// splits at head_dim 128 in two parts 2.47 against 2.66 us, 33 splits at
+// head_dim 256 in two parts 3.60 against 4.00 for one part with vector loads.
 template <int HD>
 void launch_combine(const AttnArgs& a, int n_q, int S, int M, hipStream_t s) {
-    const int parts = tune_param("ATTN_COMBINE_PARTS", S > kCB && S <= 2 * kCB && HD <= 128 ? 2 : 1);
+    int parts = tune_param("ATTN_COMBINE_PARTS", (S + kCB - 1) / kCB);
+    parts = parts < 1 ? 1 : (parts > 4 ? 4 : parts);
     const dim3 g(static_cast<unsigned>(n_q), static_cast<unsigned>(M));
-    const int cb = tune_param("ATTN_COMBINE_BATCH", kCB);  // sweeps: 16, 20 or 24
-    if (parts >= 2)
-        hipLaunchKernelGGL((k_attn2_combine<HD, 2>), g, dim3(HD * 2), 0, s, a, S);
-    else if (cb == 20)
-        hipLaunchKernelGGL((k_attn2_combine<HD, 1, 20>), g, dim3(HD), 0, s, a, S);
-    else if (cb == 24)
-        hipLaunchKernelGGL((k_attn2_combine<HD, 1, 24>), g, dim3(HD), 0, s, a, S);
-    else
-        hipLaunchKernelGGL((k_attn2_combine<HD, 1>), g, dim3(HD), 0, s, a, S);
+    switch (parts) {
+        case 1: hipLaunchKernelGGL((k_attn2_combine<HD, 1>), g, dim3(HD), 0, s, a, S); break;
+        case 2: hipLaunchKernelGGL((k_attn2_combine<HD, 2>), g, dim3(HD * 2), 0, s, a, S); break;
+        case 3: hipLaunchKernelGGL((k_attn2_combine<HD, 3>), g, dim3(HD * 3), 0, s, a, S); break;
+        default: hipLaunchKernelGGL((k_attn2_combine<HD, 4>), g, dim3(HD * 4), 0, s, a, S); break;
+    }
 }
 
 template <int HD, int G, bool F16>
