@@ -1180,7 +1180,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; the path's multi-GPU sharding is "
-              "described in DESIGN.md and not run. Use --gpus 1.", file=sys.stderr)
+              "a design that is not run here. Use --gpus 1.", file=sys.stderr)
         return 2
 
     import torch

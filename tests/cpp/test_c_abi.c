@@ -1,6 +1,6 @@
 /* A C translation unit that includes include/rt_hip.h, links librt_hip.so and
- * calls it the way a C or C++ caller of the reference path would (the
- * reference-side binding in INTEGRATION.md).  "cpu": argument checking and
+ * calls it the way a C or C++ caller of the reference path would (through
+ * the declarations a reference-side binding uses).  "cpu": argument checking and
  * size queries, no device needed.  "gpu": the host drop-in with its weight
  * cache, a weight handle, and a captured graph, each checked against the
  * CPU oracle (oracle/liboracle.so: the restatement of the reference's
