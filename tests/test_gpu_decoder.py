@@ -357,6 +357,14 @@ GEMMA_4B_ATTN = dict(GEMMA, n_heads=8, n_kv_heads=4, head_dim=256, ffn=512, max_
     # S = 32, 24 busy
     ("gemma3_4b", dict(GEMMA_4B_ATTN, max_seq=4096), 3050),
     ("llama3b_half", dict(LLAMA_3B_ATTN, max_seq=4096, rope_half=1), 3050),
+    # caches that are not whole rounds long: with no window and S splits of
+    # one round covering the cache, every split's loads leave before the
+    # position is read, and the last split's rows past the cache (1000..1023,
+    # 500..511) are clamped to its last row before being masked: S = 16
+    # (Llama), global S = 16 (Gemma; its local layers read the position
+    # first)
+    ("llama3b", dict(LLAMA_3B_ATTN, max_seq=1000), 990),
+    ("gemma3_4b", dict(GEMMA_4B_ATTN, max_seq=500), 480),
 ])
 def test_decoder_long_cache_matches_oracle(rt, orc, arch, cfg, rows):
     gemma = arch.startswith("gemma")
