@@ -31,13 +31,17 @@ constexpr int kMaxJobs = 4;
 
 // Job table passed by value: job j owns tiles [tile0[j], tile0[j + 1]), the
 // last one up to `total`; unused entries hold `total`.
+// y last: the output pointers are read after the weight prologue, and next
+// to the weight pointers of jobs 2 and 3 (read before it, by the waves of
+// those jobs only) the compiler merged both into one scalar load issued
+// ahead of the job lookup, which every wave then waited for.
 struct Jobs {
     const uint8_t* w[kMaxJobs];
-    float* y[kMaxJobs];
     int n[kMaxJobs];
     int tile0[kMaxJobs];
     int total;
     int count;
+    float* y[kMaxJobs];
 };
 
 // Rotary position embedding on the outputs of the jobs in `jobs` (a bit
@@ -377,14 +381,26 @@ __device__ __forceinline__ void q4k_tiles(int blk, const float* __restrict__ X, 
     if (J34 && count > 2) {
         // jobs 2 and 3 (a layer's k/v after q): from the table.  A separate
         // instantiation, so that launches of one or two jobs never wait for
-        // a table load before their first weight load.
-        const int t2 = sreg(jobs.tile0[2]), t3 = sreg(jobs.tile0[3]);
-        if (t >= t2) {
+        // a table load before their first weight load.  Job 2 starts after
+        // the tiles of jobs 0 and 1, which follow from the preloaded row
+        // counts, so the waves of jobs 0 and 1 read no table at all; the
+        // others read all they may need from it unconditionally, one batch
+        // of scalar loads and one latency.  (Looked up one field after
+        // another, the job-2 start, then the chosen job's row count and
+        // weights behind a branch, every wave waited for two or three scalar
+        // loads in series before its weight prologue.  Headline token on one
+        // box 698.2-700.9 against 699.9-702.3 us: the v tiles still wait for
+        // one.)
+        const int t2 = tile1 + ((n1 + 15) >> 4);
+        if (t >= t2) {  // wave-uniform
+            const int t3 = sreg(jobs.tile0[3]);
+            const int n2 = sreg(jobs.n[2]), n3 = sreg(jobs.n[3]);
+            const uint64_t w2 = sreg(jobs.w[2]), w3 = sreg(jobs.w[3]);
             const bool j3 = count > 3 && t >= t3;
             job = j3 ? 3 : 2;
             tile_base = j3 ? t3 : t2;
-            n_job = j3 ? sreg(jobs.n[3]) : sreg(jobs.n[2]);
-            wj = reinterpret_cast<const uint8_t*>(j3 ? sreg(jobs.w[3]) : sreg(jobs.w[2]));
+            n_job = j3 ? n3 : n2;
+            wj = reinterpret_cast<const uint8_t*>(j3 ? w3 : w2);
         }
     }
     const int row0 = 16 * (t - tile_base);
