@@ -387,53 +387,78 @@ __device__ __forceinline__ int attn_chunk(int len, int S) {
     return (chunk + BATCH - 1) / BATCH * BATCH;
 }
 
-// k_qk_prep's operations on one head held as 8 values per lane (dims
+// k_qk_prep's operations on NH heads held as 8 values per lane each (dims
 // 8 sub .. 8 sub + 7) by the LP lanes of a position group: the optional
-// per-head RMSNorm, x * rms_inv * (1 + g) with rms_inv = 1 / sqrt(sum(x^2) /
-// d + eps), then RoPE with cs / sn the cosine and sine of each dim's pair
-// angle.  Half-split pairs (j, j + d/2) meet across lanes sub and
-// sub ^ (LP / 2); interleaved pairs (2i, 2i + 1) sit in one lane.
-template <int HD>
-__device__ __forceinline__ void prep_head(f32x4& xa, f32x4& xb, bool norm, const float (&g)[8],
-                                          const float (&cs)[8], const float (&sn)[8], bool half, float eps,
-                                          int sub) {
+// per-head RMSNorm (norm[h]), x * rms_inv * (1 + g) with rms_inv = 1 /
+// sqrt(sum(x^2) / d + eps), then RoPE with cs / sn the cosine and sine of
+// each dim's pair angle.  Half-split pairs (j, j + d/2) meet across lanes
+// sub and sub ^ (LP / 2); interleaved pairs (2i, 2i + 1) sit in one lane.
+// All heads go through each step together, with one uniform branch per
+// step rather than per head, so their sums, exchanges and products
+// overlap instead of running head after head.
+template <int HD, int NH>
+__device__ __forceinline__ void prep_heads(f32x4 (&xa)[NH], f32x4 (&xb)[NH], const bool (&norm)[NH],
+                                           const float* const (&g)[NH], const float (&cs)[8],
+                                           const float (&sn)[8], bool half, float eps, int sub) {
     constexpr int LP = HD / 8;
-    float x[8];
+    float x[NH][8];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        x[e] = xa[e];
-        x[e + 4] = xb[e];
-    }
-    if (norm) {  // uniform
-        float sq = 0.0f;
+    for (int h = 0; h < NH; ++h)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sq += x[e] * x[e];
-        sq = group_sum<LP>(sq);
-        const float rms_inv = 1.0f / sqrtf(sq / static_cast<float>(HD) + eps);
+        for (int e = 0; e < 4; ++e) {
+            x[h][e] = xa[h][e];
+            x[h][e + 4] = xb[h][e];
+        }
+    bool any = false;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = x[e] * rms_inv * (1.0f + g[e]);
+    for (int h = 0; h < NH; ++h) any = any || norm[h];
+    if (any) {  // uniform
+        float sq[NH];
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            sq[h] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sq[h] += x[h][e] * x[h][e];
+        }
+#pragma unroll
+        for (int h = 0; h < NH; ++h) sq[h] = group_sum<LP>(sq[h]);
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            const float rms_inv = 1.0f / sqrtf(sq[h] / static_cast<float>(HD) + eps);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[h][e] = norm[h] ? x[h][e] * rms_inv * (1.0f + g[h][e]) : x[h][e];
+        }
     }
     if (half) {  // uniform
         const bool lower = sub < LP / 2;
-        float y[8];
+        float y[NH][8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] = __shfl_xor(x[e], LP / 2, kWave);
+        for (int h = 0; h < NH; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) y[h][e] = __shfl_xor(x[h][e], LP / 2, kWave);
         // the pair's lower dim: x0 * c - x1 * s; its upper dim: x0 * s + x1 * c
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = lower ? x[e] * cs[e] - y[e] * sn[e] : y[e] * sn[e] + x[e] * cs[e];
+        for (int h = 0; h < NH; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                x[h][e] = lower ? x[h][e] * cs[e] - y[h][e] * sn[e] : y[h][e] * sn[e] + x[h][e] * cs[e];
     } else {
 #pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-            const float x0 = x[e], x1 = x[e + 1];
-            x[e] = x0 * cs[e] - x1 * sn[e];
-            x[e + 1] = x0 * sn[e] + x1 * cs[e];
-        }
+        for (int h = 0; h < NH; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const float x0 = x[h][e], x1 = x[h][e + 1];
+                x[h][e] = x0 * cs[e] - x1 * sn[e];
+                x[h][e + 1] = x0 * sn[e] + x1 * cs[e];
+            }
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        xa[e] = x[e];
-        xb[e] = x[e + 4];
-    }
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            xa[h][e] = x[h][e];
+            xb[h][e] = x[h][e + 4];
+        }
 }
 
 // MERGE: the last split of a (row, kv head) to arrive merges in this launch
@@ -638,9 +663,29 @@ __device__ __forceinline__ void attn2_partial(const AttnArgs& a, const PrepArgs&
                 cs[e] = tcs[i];
                 sn[e] = tsn[i];
             }
+            // the G query heads and the new key, together
+            f32x4 ha[G + 1], hb[G + 1];
+            bool hn[G + 1];
+            const float* hg[G + 1];
 #pragma unroll
-            for (int h = 0; h < G; ++h) prep_head<HD>(qa[h], qb[h], pp.qg != nullptr, qg, cs, sn, pp.half, pp.eps, sub);
-            prep_head<HD>(kna, knb, pp.kg != nullptr, kg, cs, sn, pp.half, pp.eps, sub);
+            for (int h = 0; h < G; ++h) {
+                ha[h] = qa[h];
+                hb[h] = qb[h];
+                hn[h] = pp.qg != nullptr;
+                hg[h] = qg;
+            }
+            ha[G] = kna;
+            hb[G] = knb;
+            hn[G] = pp.kg != nullptr;
+            hg[G] = kg;
+            prep_heads<HD, G + 1>(ha, hb, hn, hg, cs, sn, pp.half, pp.eps, sub);
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                qa[h] = ha[h];
+                qb[h] = hb[h];
+            }
+            kna = ha[G];
+            knb = hb[G];
             const int64_t o = static_cast<int64_t>(pcur) * pp.cache_row + static_cast<int64_t>(kvh) * HD + sub * 8;
             const bool store = grp == 0 && pcur >= p0 && pcur < p1;  // one group of one workgroup per kv head
             if constexpr (F16) {
